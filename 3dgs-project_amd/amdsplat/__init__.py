@@ -1,0 +1,9 @@
+"""amdsplat: MI355X-native (gfx950) differentiable Gaussian-splat rasterizer.
+
+`rasterize(means, scales, quats, opacities, sh, viewmat, K, W, H) -> (image, alpha, aux)` runs
+the 3D path through hand-written HIP kernels behind a C ABI (include/amdsplat.h). The 2D
+drop-in surfaces live in the sibling packages `gs2d` and `splat2d`.
+"""
+from .rasterize import Camera, backward_pass, forward_pass, rasterize
+
+__all__ = ["Camera", "rasterize", "forward_pass", "backward_pass"]

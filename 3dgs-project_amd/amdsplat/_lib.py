@@ -1,0 +1,146 @@
+"""ctypes binding of the C ABI in include/amdsplat.h (libamdsplat.so, built for gfx950).
+
+The library is the only compute path: if it is missing or a call fails, the functions here
+raise; nothing falls back to a CPU implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libamdsplat.so"
+
+c_float_p = C.c_void_p  # device pointers are passed as integers
+_vp = C.c_void_p
+_i64 = C.c_int64
+_i32 = C.c_int
+_sz = C.c_size_t
+
+
+class GsCamera(C.Structure):
+    _fields_ = [
+        ("viewmat", C.c_float * 16),
+        ("fx", C.c_float),
+        ("fy", C.c_float),
+        ("cx", C.c_float),
+        ("cy", C.c_float),
+        ("width", C.c_int32),
+        ("height", C.c_int32),
+        ("near_plane", C.c_float),
+        ("far_plane", C.c_float),
+    ]
+
+
+class AmdSplatError(RuntimeError):
+    pass
+
+
+_SIGS = {
+    "gs_last_error": (C.c_char_p, []),
+    "gs_version": (_i32, []),
+    "gs_splat_record_floats": (_i32, []),
+    "gs_grad2d_floats": (_i32, []),
+    "gs_scan_workspace_size": (_sz, [_i64]),
+    "gs_scan_u32": (_i32, [_vp, _vp, _i64, _vp, _sz, _vp]),
+    "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp]),
+    "gs_bin_workspace_size": (_sz, [_i64, _i32]),
+    "gs_bin_fill_3d": (_i32, [_vp, _vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
+    "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                               _vp, _vp]),
+    "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp,
+                                 _vp, _vp, _vp, _vp, _vp, _vp]),
+    # 2D rule sets
+    "gs2d_pack": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "gs2d_blend_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp,
+                              _vp, _vp, _vp]),
+    "gs2d_blend_bwd_bucket": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, C.POINTER(C.c_float),
+                                     _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs2d_blend_bwd_pixel": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp,
+                                    _vp, _vp, _vp]),
+    "gs2d_bin_count_rect": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
+    "gs2d_bin_fill_rect": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+}
+
+_lib = None
+_missing: set[str] = set()
+
+
+def lib() -> C.CDLL:
+    """Loads libamdsplat.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise AmdSplatError(
+                f"{LIB_PATH} not found: build it with `python 3dgs-project_amd/build.py` "
+                "(or __graft_entry__.build())")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            try:
+                fn = getattr(L, name)
+            except AttributeError:
+                _missing.add(name)
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols() -> set[str]:
+    lib()
+    return set(_SIGS) - _missing
+
+
+def call(name: str, *args) -> None:
+    L = lib()
+    if name in _missing:
+        raise AmdSplatError(f"{name} is not exported by {LIB_PATH}")
+    rc = getattr(L, name)(*args)
+    if rc != 0:
+        msg = L.gs_last_error().decode(errors="replace")
+        raise AmdSplatError(f"{name} failed (code {rc}): {msg}")
+
+
+def size_call(name: str, *args) -> int:
+    return int(getattr(lib(), name)(*args))
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None or empty tensors)."""
+    if t is None or t.numel() == 0:
+        return None
+    return t.data_ptr()
+
+
+def stream_handle(device=None) -> int | None:
+    import torch
+
+    s = torch.cuda.current_stream(device)
+    return s.cuda_stream or None
+
+
+def float3(v) -> C.Array:
+    arr = (C.c_float * 3)(*[float(x) for x in v])
+    return arr
+
+
+def make_camera(viewmat, fx: float, fy: float, cx: float, cy: float, width: int, height: int,
+                near: float, far: float) -> GsCamera:
+    cam = GsCamera()
+    flat = [float(x) for x in viewmat.reshape(-1).tolist()] if hasattr(viewmat, "reshape") else \
+        [float(x) for row in viewmat for x in row]
+    if len(flat) != 16:
+        raise ValueError("viewmat must be 4x4")
+    for i, v in enumerate(flat):
+        cam.viewmat[i] = v
+    cam.fx, cam.fy, cam.cx, cam.cy = float(fx), float(fy), float(cx), float(cy)
+    cam.width, cam.height = int(width), int(height)
+    cam.near_plane, cam.far_plane = float(near), float(far)
+    return cam
+
+
+def env_debug() -> bool:
+    return os.environ.get("AMDSPLAT_DEBUG", "0") == "1"

@@ -1,0 +1,277 @@
+"""3D Gaussian-splat rasterizer: `rasterize(means, scales, quats, opacities, sh, viewmat, K, W, H)`.
+
+Host side of the MI355X path. Every stage is a C-ABI call into libamdsplat.so on the current
+torch stream; this module only allocates the buffers (PyTorch owns all device memory) and
+wires the stages:
+
+    preprocess -> scan(tiles touched) -> [read M] -> emit keys + radix sort + ranges + buckets
+    -> bucket->tile table -> forward blend                       (forward)
+    bucketed blend backward -> preprocess backward                (backward)
+
+The operator surface follows the reference's 3D call sites: gsplat's
+`rasterization(means, quats, scales, opac, colors, viewmats, K, W, H) -> (img, alpha, meta)`
+(cluster/build_env.sbatch:47-55) and Faster-GS's raw-parameter convention for
+`_C.forward` / `_C.backward` (phase1/tests/test_parity.py:59-98: log-scales, unnormalised
+quaternions, opacity logits, SH coefficients).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr
+
+TILE = 16
+BUCKET = 32
+REC_FLOATS = 16
+GRAD2D_FLOATS = 12
+
+
+def _u8(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+@dataclass
+class Camera:
+    """Pinhole camera: row-major world-to-camera `viewmat` (4x4, OpenCV axes) and intrinsics."""
+
+    viewmat: torch.Tensor
+    fx: float
+    fy: float
+    cx: float
+    cy: float
+    width: int
+    height: int
+    near: float = 0.01
+    far: float = 100.0
+
+    @staticmethod
+    def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0) -> "Camera":
+        K = torch.as_tensor(K, dtype=torch.float64).cpu()
+        vm = torch.as_tensor(viewmat, dtype=torch.float32).detach().cpu().reshape(4, 4)
+        return Camera(vm, float(K[0, 0]), float(K[1, 1]), float(K[0, 2]), float(K[1, 2]), int(width),
+                      int(height), float(near), float(far))
+
+    @property
+    def tiles_x(self) -> int:
+        return (self.width + TILE - 1) // TILE
+
+    @property
+    def tiles_y(self) -> int:
+        return (self.height + TILE - 1) // TILE
+
+    @property
+    def n_tiles(self) -> int:
+        return self.tiles_x * self.tiles_y
+
+    def c_struct(self) -> _lib.GsCamera:
+        return _lib.make_camera(self.viewmat.detach().cpu().float(), self.fx, self.fy, self.cx, self.cy,
+                                self.width, self.height, self.near, self.far)
+
+
+@dataclass
+class ForwardState:
+    """Device buffers of one forward pass (kept for the backward)."""
+
+    cam: Camera
+    n: int
+    sh_coeffs: int
+    sh_degree: int
+    rec: torch.Tensor            # [n, 16] splat records
+    touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
+    offsets: torch.Tensor        # [n + 1] int32
+    m: int                       # instances
+    keys: torch.Tensor           # [m] int64 sorted keys
+    point_list: torch.Tensor     # [m] int32
+    ranges: torch.Tensor         # [T, 2] int32
+    bucket_offsets: torch.Tensor  # [T + 1] int32
+    n_buckets_max: int
+    bucket_to_tile: torch.Tensor  # [n_buckets_max] int32
+    image: torch.Tensor          # [3, H, W]
+    final_T: torch.Tensor        # [H, W]
+    n_contrib: torch.Tensor      # [H, W] int32
+    tile_max: torch.Tensor       # [T] int32
+    ckpt: torch.Tensor           # [n_buckets_max, 256, 4]
+    bg: tuple = (0.0, 0.0, 0.0)
+    timings: dict = field(default_factory=dict)
+
+    @property
+    def n_buckets(self) -> int:
+        return int(self.bucket_offsets[-1].item())
+
+
+class StageTimer:
+    """Records torch.cuda events on the current stream between stages (no-op if disabled)."""
+
+    def __init__(self, enabled: bool):
+        self.enabled = enabled
+        self.marks: list[tuple[str, torch.cuda.Event]] = []
+
+    def mark(self, name: str) -> None:
+        if self.enabled:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.marks.append((name, e))
+
+    def result(self, sync: bool = True) -> dict:
+        """Per-stage milliseconds; with sync=False the caller must have synchronised."""
+        if not self.enabled or len(self.marks) < 2:
+            return {}
+        if sync:
+            torch.cuda.synchronize()
+        out = {}
+        for (_, a), (name, b) in zip(self.marks[:-1], self.marks[1:]):
+            out[name] = out.get(name, 0.0) + a.elapsed_time(b)
+        return out
+
+
+def _check_inputs(means, log_scales, quats, opacity_logits, sh):
+    n = means.shape[0]
+    dev = means.device
+    if dev.type != "cuda":
+        raise ValueError("amdsplat.rasterize runs on the GPU: inputs must be CUDA tensors")
+    for name, t, shape in (("means", means, (n, 3)), ("scales", log_scales, (n, 3)), ("quats", quats, (n, 4)),
+                           ("opacities", opacity_logits, (n,))):
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+        if t.dtype != torch.float32 or t.device != dev:
+            raise ValueError(f"{name} must be float32 on {dev}")
+    if sh.dim() != 3 or sh.shape[0] != n or sh.shape[2] != 3 or sh.shape[1] not in (1, 4, 9, 16):
+        raise ValueError(f"sh must have shape [N, K, 3] with K in (1, 4, 9, 16), got {tuple(sh.shape)}")
+    if sh.dtype != torch.float32 or sh.device != dev:
+        raise ValueError(f"sh must be float32 on {dev}")
+
+
+def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_degree: int | None = None,
+                 bg=(0.0, 0.0, 0.0), timing: bool = False) -> ForwardState:
+    """Runs the forward stages; inputs are contiguous float32 CUDA tensors (raw parameters)."""
+    means, log_scales, quats = means.contiguous(), log_scales.contiguous(), quats.contiguous()
+    opacity_logits, sh = opacity_logits.contiguous(), sh.contiguous()
+    _check_inputs(means, log_scales, quats, opacity_logits, sh)
+    n = means.shape[0]
+    dev = means.device
+    K = sh.shape[1]
+    if sh_degree is None:
+        sh_degree = int(round(math.sqrt(K))) - 1
+    T = cam.n_tiles
+    H, W = cam.height, cam.width
+    ccam = cam.c_struct()
+    st = _lib.stream_handle(dev)
+    tm = timing if isinstance(timing, StageTimer) else StageTimer(bool(timing))
+    tm.mark("start")
+
+    rec = torch.empty(n, REC_FLOATS, dtype=torch.float32, device=dev)
+    touched = torch.empty(n, dtype=torch.int32, device=dev)
+    call("gs_preprocess_fwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh), n, K,
+         sh_degree, ccam, ptr(rec), ptr(touched), st)
+    tm.mark("preprocess")
+    offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    ws = _u8(_lib.size_call("gs_scan_workspace_size", n), dev)
+    call("gs_scan_u32", ptr(touched), ptr(offsets), n, ptr(ws), ws.numel(), st)
+    tm.mark("scan")
+    m = int(offsets[n].item()) if n > 0 else 0  # host readback: instance count
+    keys = torch.empty(m, dtype=torch.int64, device=dev)
+    point_list = torch.empty(m, dtype=torch.int32, device=dev)
+    ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
+    bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
+    ws = _u8(_lib.size_call("gs_bin_workspace_size", m, T), dev)
+    call("gs_bin_fill_3d", ptr(rec), ptr(touched), ptr(offsets), n, ccam, m, ptr(keys), ptr(point_list),
+         ptr(ranges), ptr(bucket_offsets), ptr(ws), ws.numel(), st)
+    tm.mark("binning")
+    nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
+    bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
+    call("gs_bucket_fill", ptr(bucket_offsets), T, ptr(bucket_to_tile), nb_max, st)
+    image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
+    final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
+    n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
+    tile_max = torch.empty(T, dtype=torch.int32, device=dev)
+    ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
+    tm.mark("buckets")
+    call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
+         ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), st)
+    tm.mark("blend_fwd")
+    return ForwardState(cam, n, K, sh_degree, rec, touched, offsets, m, keys, point_list, ranges, bucket_offsets,
+                        nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, tuple(bg),
+                        {} if isinstance(timing, StageTimer) else tm.result())
+
+
+def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
+                  grad_alpha=None, timing: bool = False):
+    """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings)."""
+    dev = means.device
+    n = fs.n
+    cam = fs.cam
+    st = _lib.stream_handle(dev)
+    grad_image = grad_image.contiguous().float()
+    if grad_alpha is not None:
+        grad_alpha = grad_alpha.contiguous().float()
+    tm = timing if isinstance(timing, StageTimer) else StageTimer(bool(timing))
+    tm.mark("start")
+    grad2d = torch.empty(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+    call("gs_blend_bwd_3d", ptr(fs.rec), ptr(fs.ranges), ptr(fs.point_list), ptr(fs.bucket_offsets),
+         ptr(fs.bucket_to_tile), fs.n_buckets_max, n, cam.width, cam.height, ptr(fs.image), ptr(grad_image),
+         ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(grad2d), st)
+    tm.mark("blend_bwd")
+    g_means = torch.empty(n, 3, dtype=torch.float32, device=dev)
+    g_ls = torch.empty(n, 3, dtype=torch.float32, device=dev)
+    g_q = torch.empty(n, 4, dtype=torch.float32, device=dev)
+    g_op = torch.empty(n, dtype=torch.float32, device=dev)
+    g_sh = torch.empty(n, fs.sh_coeffs, 3, dtype=torch.float32, device=dev)
+    call("gs_preprocess_bwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh), n,
+         fs.sh_coeffs, fs.sh_degree, cam.c_struct(), ptr(fs.rec), ptr(fs.touched), ptr(grad2d), ptr(g_means),
+         ptr(g_ls), ptr(g_q), ptr(g_op), ptr(g_sh), st)
+    tm.mark("preprocess_bwd")
+    return g_means, g_ls, g_q, g_op, g_sh, grad2d, {} if isinstance(timing, StageTimer) else tm.result()
+
+
+class _Rasterize3D(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg):
+        fs = forward_pass(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg)
+        ctx.fs = fs
+        ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh)
+        alpha = 1.0 - fs.final_T
+        ctx.mark_non_differentiable(fs.touched)
+        return fs.image, alpha, fs.touched
+
+    @staticmethod
+    def backward(ctx, grad_image, grad_alpha, _grad_touched):
+        means, log_scales, quats, opacity_logits, sh = ctx.saved_tensors
+        fs = ctx.fs
+        if grad_image is None:
+            grad_image = torch.zeros_like(fs.image)
+        gm, gls, gq, gop, gsh, grad2d, _ = backward_pass(fs, means.contiguous(), log_scales.contiguous(),
+                                                         quats.contiguous(), opacity_logits.contiguous(),
+                                                         sh.contiguous(), grad_image, grad_alpha)
+        ctx.grad2d = grad2d
+        return gm, gls, gq, gop, gsh, None, None, None
+
+
+def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None, near: float = 0.01,
+              far: float = 100.0, sh_degree: int | None = None, activated: bool = False):
+    """Renders one view. Returns (image [3, H, W], alpha [H, W], aux).
+
+    Parameters follow Faster-GS's raw convention unless `activated=True`:
+      means [N,3]; scales [N,3] log-scales (activated: positive scales); quats [N,4] (w, x, y, z),
+      any norm; opacities [N] or [N,1] logits (activated: opacities in (0,1)); sh [N,K,3] SH
+      coefficients, K in {1,4,9,16}; viewmat [4,4] world-to-camera (OpenCV axes); K [3,3] intrinsics.
+    aux: {"tiles_touched": [N] int32 (> 0 = visible; the visibility mask for a sparse optimizer),
+          "n_visible", "n_instances", "n_buckets"}.
+    Gradients flow to means, scales, quats, opacities and sh.
+    """
+    if opacities.dim() == 2:
+        opacities = opacities.reshape(-1)
+    if activated:
+        scales = torch.log(scales)
+        opacities = torch.logit(opacities)
+    cam = Camera.from_K(viewmat, K, W, H, near, far)
+    if bg is None:
+        bg = (0.0, 0.0, 0.0)
+    bg = tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
+    image, alpha, touched = _Rasterize3D.apply(means, scales, quats, opacities, sh, cam, sh_degree, bg)
+    aux = {"tiles_touched": touched}
+    aux["n_visible"] = lambda: int((touched > 0).sum().item())
+    return image, alpha, aux

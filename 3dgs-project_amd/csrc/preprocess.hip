@@ -1,0 +1,521 @@
+// 3D preprocess, forward and backward.
+//
+// One thread per Gaussian, 256-thread workgroups. A wavefront's 64 Gaussians own one
+// contiguous block of the [n, K, 3] SH tensor (64 * 3K floats); the wavefront moves that
+// block through LDS with 16-byte loads/stores (rows padded to an odd stride, so a lane's
+// row reads are bank-conflict free), instead of each lane streaming its own 3K floats 12K
+// bytes apart. Same idea as the reference's coalesced SH access
+// (phase2/sh_coalesce.patch:20-170, upstream/upstream_main_kernels.patch:26-76).
+#include <stdarg.h>
+
+#include "gs_host.h"
+#include "gs_sh.h"
+
+namespace gs {
+
+struct Geom {
+  bool vis;
+  float vx, vy, vz, iz, tx, ty, txc, tyc;
+  float o;
+  float qw, qx, qy, qz, qinv;  // normalised quaternion and 1/|q|
+  float R[9];                  // rotation of the Gaussian
+  float s[3];                  // scales
+  float M[9];                  // R diag(s)
+  float S[6];                  // 3D covariance (00 01 02 11 12 22)
+  float T[6];                  // J W, 2x3
+  float a, b, c;               // 2D covariance incl. dilation
+  float det, A, B, C;          // conic
+  float mx, my;                // mean2d
+};
+
+// The forward geometry of one Gaussian. The operation order is part of the rule set: the
+// CPU oracle evaluates the same sequence.
+__device__ __forceinline__ void compute_geom(const float* __restrict__ means,
+                                             const float* __restrict__ log_scales,
+                                             const float4* __restrict__ quats,
+                                             const float* __restrict__ opacity_logits,
+                                             int64_t i, const CamK& cam, Geom& g) {
+  const float px = means[3 * i], py = means[3 * i + 1], pz = means[3 * i + 2];
+  g.vx = fmaf(cam.r[0], px, fmaf(cam.r[1], py, fmaf(cam.r[2], pz, cam.t[0])));
+  g.vy = fmaf(cam.r[3], px, fmaf(cam.r[4], py, fmaf(cam.r[5], pz, cam.t[1])));
+  g.vz = fmaf(cam.r[6], px, fmaf(cam.r[7], py, fmaf(cam.r[8], pz, cam.t[2])));
+  bool vis = (g.vz > cam.znear) && (g.vz < cam.zfar);
+  g.o = sigmoid(opacity_logits[i]);
+  vis = vis && (g.o >= kAlphaMin);
+
+  const float4 q = quats[i];
+  const float n2 = fmaf(q.x, q.x, fmaf(q.y, q.y, fmaf(q.z, q.z, q.w * q.w)));
+  vis = vis && (n2 > 0.0f);
+  g.qinv = 1.0f / sqrtf(n2);
+  const float w = q.x * g.qinv, x = q.y * g.qinv, y = q.z * g.qinv, z = q.w * g.qinv;
+  g.qw = w;
+  g.qx = x;
+  g.qy = y;
+  g.qz = z;
+  const float xx = x * x, yy = y * y, zz = z * z;
+  const float xy = x * y, xz = x * z, yz = y * z;
+  const float wx = w * x, wy = w * y, wz = w * z;
+  float t;
+  t = yy + zz; t = t + t; g.R[0] = 1.0f - t;
+  t = xy - wz; g.R[1] = t + t;
+  t = xz + wy; g.R[2] = t + t;
+  t = xy + wz; g.R[3] = t + t;
+  t = xx + zz; t = t + t; g.R[4] = 1.0f - t;
+  t = yz - wx; g.R[5] = t + t;
+  t = xz - wy; g.R[6] = t + t;
+  t = yz + wx; g.R[7] = t + t;
+  t = xx + yy; t = t + t; g.R[8] = 1.0f - t;
+
+  for (int k = 0; k < 3; ++k) g.s[k] = exp_any(log_scales[3 * i + k]);
+  for (int r = 0; r < 3; ++r)
+    for (int k = 0; k < 3; ++k) g.M[3 * r + k] = g.R[3 * r + k] * g.s[k];
+  const float* M = g.M;
+  g.S[0] = fmaf(M[0], M[0], fmaf(M[1], M[1], M[2] * M[2]));
+  g.S[1] = fmaf(M[0], M[3], fmaf(M[1], M[4], M[2] * M[5]));
+  g.S[2] = fmaf(M[0], M[6], fmaf(M[1], M[7], M[2] * M[8]));
+  g.S[3] = fmaf(M[3], M[3], fmaf(M[4], M[4], M[5] * M[5]));
+  g.S[4] = fmaf(M[3], M[6], fmaf(M[4], M[7], M[5] * M[8]));
+  g.S[5] = fmaf(M[6], M[6], fmaf(M[7], M[7], M[8] * M[8]));
+
+  g.iz = 1.0f / g.vz;
+  g.tx = g.vx * g.iz;
+  g.ty = g.vy * g.iz;
+  g.txc = fminf(fmaxf(g.tx, cam.lim_x_lo), cam.lim_x_hi);
+  g.tyc = fminf(fmaxf(g.ty, cam.lim_y_lo), cam.lim_y_hi);
+  const float j00 = cam.fx * g.iz, j11 = cam.fy * g.iz;
+  const float j02 = -(j00 * g.txc), j12 = -(j11 * g.tyc);
+  for (int k = 0; k < 3; ++k) {
+    g.T[k] = fmaf(j00, cam.r[k], j02 * cam.r[6 + k]);
+    g.T[3 + k] = fmaf(j11, cam.r[3 + k], j12 * cam.r[6 + k]);
+  }
+  const float* S = g.S;
+  const float* T = g.T;
+  // U = T S (2x3), S symmetric with rows (S0 S1 S2), (S1 S3 S4), (S2 S4 S5)
+  const float u00 = fmaf(T[0], S[0], fmaf(T[1], S[1], T[2] * S[2]));
+  const float u01 = fmaf(T[0], S[1], fmaf(T[1], S[3], T[2] * S[4]));
+  const float u02 = fmaf(T[0], S[2], fmaf(T[1], S[4], T[2] * S[5]));
+  const float u10 = fmaf(T[3], S[0], fmaf(T[4], S[1], T[5] * S[2]));
+  const float u11 = fmaf(T[3], S[1], fmaf(T[4], S[3], T[5] * S[4]));
+  const float u12 = fmaf(T[3], S[2], fmaf(T[4], S[4], T[5] * S[5]));
+  g.a = fmaf(u00, T[0], fmaf(u01, T[1], u02 * T[2])) + kDilation;
+  g.b = fmaf(u00, T[3], fmaf(u01, T[4], u02 * T[5]));
+  g.c = fmaf(u10, T[3], fmaf(u11, T[4], u12 * T[5])) + kDilation;
+  g.det = fmaf(g.a, g.c, -(g.b * g.b));
+  vis = vis && (g.det > 0.0f);
+  const float idet = 1.0f / g.det;
+  g.A = g.c * idet;
+  g.B = -g.b * idet;
+  g.C = g.a * idet;
+  g.mx = fmaf(cam.fx, g.tx, cam.cx);
+  g.my = fmaf(cam.fy, g.ty, cam.cy);
+  g.vis = vis;
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void preprocess_fwd_kernel(
+    const float* __restrict__ means, const float* __restrict__ log_scales,
+    const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
+    const float* __restrict__ sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
+    uint32_t* __restrict__ tiles_touched) {
+  constexpr int R = 3 * K;      // floats per Gaussian row
+  constexpr int RP = R | 1;     // padded LDS row
+  __shared__ float s_sh[4][64 * RP];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
+  if (wave_first >= n) return;  // whole wavefront
+  const int64_t i = wave_first + lane;
+  const bool valid = i < n;
+
+  Geom g;
+  g.vis = false;
+  int4 bnd = make_int4(0, -1, 0, -1);
+  float thr = 0.0f;
+  if (valid) {
+    compute_geom(means, log_scales, quats, opacity_logits, i, cam, g);
+    if (g.vis) {
+      thr = log_pos(255.0f * g.o);
+      const float t2 = thr + thr;
+      const float ex = sqrtf(t2 * g.a), ey = sqrtf(t2 * g.c);
+      float xf0 = ceilf((g.mx - ex) - 0.5f), xf1 = floorf((g.mx + ex) - 0.5f);
+      float yf0 = ceilf((g.my - ey) - 0.5f), yf1 = floorf((g.my + ey) - 0.5f);
+      bool ok = (thr > 0.0f) && __builtin_isfinite(xf0) && __builtin_isfinite(xf1) &&
+                __builtin_isfinite(yf0) && __builtin_isfinite(yf1);
+      xf0 = fmaxf(xf0, 0.0f);
+      yf0 = fmaxf(yf0, 0.0f);
+      xf1 = fminf(xf1, static_cast<float>(cam.width - 1));
+      yf1 = fminf(yf1, static_cast<float>(cam.height - 1));
+      ok = ok && (xf0 <= xf1) && (yf0 <= yf1);
+      if (ok) {
+        bnd = make_int4(static_cast<int>(xf0), static_cast<int>(xf1), static_cast<int>(yf0),
+                        static_cast<int>(yf1));
+      }
+      g.vis = ok;
+    }
+  }
+  uint32_t count = 0;
+  float4 ra, rb;
+  if (g.vis) {
+    ra = make_float4(g.mx, g.my, g.A, g.B);
+    rb = make_float4(g.C, g.o, g.vz, thr);
+    count = static_cast<uint32_t>(
+        for_each_touched_tile(ra, rb, bnd, cam.tiles_x, [](int, int) {}));
+    g.vis = count > 0;
+  }
+
+  // Colour: stage the wavefront's SH rows through LDS (wave-uniform branch).
+  const uint64_t vmask = __ballot(g.vis ? 1 : 0);
+  float col[3] = {0.0f, 0.0f, 0.0f};
+  uint32_t mask = 0;
+  if (vmask != 0) {
+    float* srow = s_sh[wave];
+    const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
+    const int total = rows * R;
+    const float* src = sh + wave_first * R;
+    if (aligned16(src)) {
+      const int n4 = total / 4;
+      for (int f4 = lane; f4 < n4; f4 += 64) {
+        const float4 v = reinterpret_cast<const float4*>(src)[f4];
+        const int f = 4 * f4;
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = (f + e) / R, colm = (f + e) - row * R;
+          srow[row * RP + colm] = vv[e];
+        }
+      }
+      for (int f = 4 * n4 + lane; f < total; f += 64) {
+        const int row = f / R, colm = f - row * R;
+        srow[row * RP + colm] = src[f];
+      }
+    } else {
+      for (int f = lane; f < total; f += 64) {
+        const int row = f / R, colm = f - row * R;
+        srow[row * RP + colm] = src[f];
+      }
+    }
+    wave_sync();
+    if (g.vis) {
+      const float dx = means[3 * i] - cam.campos[0];
+      const float dy = means[3 * i + 1] - cam.campos[1];
+      const float dz = means[3 * i + 2] - cam.campos[2];
+      const float len = sqrtf(fmaf(dx, dx, fmaf(dy, dy, dz * dz)));
+      const float il = 1.0f / len;
+      float basis[16];
+      sh_basis(dx * il, dy * il, dz * il, active, basis);
+      const float* row = srow + lane * RP;
+#pragma unroll
+      for (int ch = 0; ch < 3; ++ch) {
+        float acc = basis[0] * row[ch];
+        for (int k = 1; k < active; ++k) acc = fmaf(basis[k], row[3 * k + ch], acc);
+        acc = acc + 0.5f;
+        if (acc < 0.0f) mask |= (1u << ch);
+        col[ch] = fmaxf(acc, 0.0f);
+      }
+    }
+  }
+  if (valid) {
+    tiles_touched[i] = g.vis ? count : 0u;
+    if (g.vis) {
+      SplatRec r;
+      r.a = ra;
+      r.b = rb;
+      r.c = make_float4(col[0], col[1], col[2], __uint_as_float(mask));
+      r.d = bnd;
+      rec[i] = r;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
+    const float* __restrict__ means, const float* __restrict__ log_scales,
+    const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
+    const float* __restrict__ sh, int64_t n, int active, CamK cam,
+    const SplatRec* __restrict__ rec, const uint32_t* __restrict__ tiles_touched,
+    const float* __restrict__ grad2d, float* __restrict__ g_means,
+    float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
+    float* __restrict__ g_opacity, float* __restrict__ g_sh) {
+  constexpr int R = 3 * K;
+  constexpr int RP = R | 1;
+  __shared__ float s_sh[4][64 * RP];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
+  if (wave_first >= n) return;
+  const int64_t i = wave_first + lane;
+  const bool valid = i < n;
+  const bool vis = valid && tiles_touched[i] != 0u;
+  const uint64_t vmask = __ballot(vis ? 1 : 0);
+  float* srow = s_sh[wave];
+  const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
+  const int total = rows * R;
+
+  float gm[3] = {0.0f, 0.0f, 0.0f};  // dL/dmean (world)
+  float gcol[3] = {0.0f, 0.0f, 0.0f};
+  float gdl[3] = {0.0f, 0.0f, 0.0f};  // dL/dlog_scale
+  float4 gq = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float gop = 0.0f;
+
+  if (vmask != 0) {
+    // stage SH coefficients (needed for the view-direction gradient)
+    const float* src = sh + wave_first * R;
+    for (int f = lane; f < total; f += 64) {
+      const int row = f / R, colm = f - row * R;
+      srow[row * RP + colm] = src[f];
+    }
+  }
+  wave_sync();
+
+  if (vis) {
+    const float* g2 = grad2d + i * kGrad2D;
+    const SplatRec r = rec[i];
+    const uint32_t mask = __float_as_uint(r.c.w);
+    for (int ch = 0; ch < 3; ++ch) gcol[ch] = (mask & (1u << ch)) ? 0.0f : g2[6 + ch];
+
+    // ---- SH colour: coefficient gradients (into LDS row) and view-direction gradient ----
+    const float dxw = means[3 * i] - cam.campos[0];
+    const float dyw = means[3 * i + 1] - cam.campos[1];
+    const float dzw = means[3 * i + 2] - cam.campos[2];
+    const float len = sqrtf(fmaf(dxw, dxw, fmaf(dyw, dyw, dzw * dzw)));
+    const float il = 1.0f / len;
+    const float dx = dxw * il, dy = dyw * il, dz = dzw * il;
+    float basis[16];
+    sh_basis(dx, dy, dz, active, basis);
+    float* row = srow + lane * RP;
+    float gb[16];
+    for (int k = 0; k < K; ++k) {
+      if (k < active) {
+        gb[k] = row[3 * k] * gcol[0] + row[3 * k + 1] * gcol[1] + row[3 * k + 2] * gcol[2];
+      } else {
+        gb[k] = 0.0f;
+      }
+    }
+    float gdx, gdy, gdz;
+    sh_basis_grad(dx, dy, dz, active, gb, gdx, gdy, gdz);
+    // d dir / d v = (I - d d^T) / |v|
+    const float dd = dx * gdx + dy * gdy + dz * gdz;
+    gm[0] = (gdx - dx * dd) * il;
+    gm[1] = (gdy - dy * dd) * il;
+    gm[2] = (gdz - dz * dd) * il;
+    // overwrite the row with coefficient gradients (after its values were read above)
+    for (int k = 0; k < K; ++k) {
+      const float bk = k < active ? basis[k] : 0.0f;
+      row[3 * k] = bk * gcol[0];
+      row[3 * k + 1] = bk * gcol[1];
+      row[3 * k + 2] = bk * gcol[2];
+    }
+
+    // ---- geometry ----
+    Geom g;
+    compute_geom(means, log_scales, quats, opacity_logits, i, cam, g);
+    gop = g2[5] * g.o * (1.0f - g.o);
+
+    // mean2d = (fx vx/vz + cx, fy vy/vz + cy)
+    float gvx = g2[0] * cam.fx * g.iz;
+    float gvy = g2[1] * cam.fy * g.iz;
+    float gvz = -(g2[0] * cam.fx * g.tx + g2[1] * cam.fy * g.ty) * g.iz;
+
+    // conic (A, B, C) = (c, -b, a) / det  ->  2D covariance (a, b, c)
+    const float gA = g2[2], gB = g2[3], gC = g2[4];
+    const float a = g.a, b = g.b, c = g.c;
+    const float id2 = 1.0f / (g.det * g.det);
+    const float ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
+    const float gbb = (2.0f * b * c * gA - (a * c + b * b) * gB + 2.0f * a * b * gC) * id2;
+    const float gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
+    // cov2d = T S T^T (+ dilation); Gc = [[ga, gbb/2], [gbb/2, gc]]
+    const float Gc00 = ga, Gc01 = 0.5f * gbb, Gc11 = gc;
+    const float* T = g.T;
+    const float* S = g.S;
+    // dL/dS = T^T Gc T (symmetric, 3x3)
+    float GT[6];  // Gc T (2x3)
+    for (int k = 0; k < 3; ++k) {
+      GT[k] = Gc00 * T[k] + Gc01 * T[3 + k];
+      GT[3 + k] = Gc01 * T[k] + Gc11 * T[3 + k];
+    }
+    float dS[9];
+    for (int r0 = 0; r0 < 3; ++r0)
+      for (int c0 = 0; c0 < 3; ++c0) dS[3 * r0 + c0] = T[r0] * GT[c0] + T[3 + r0] * GT[3 + c0];
+    // dL/dT = 2 Gc T S
+    const float Sf[9] = {S[0], S[1], S[2], S[1], S[3], S[4], S[2], S[4], S[5]};
+    float dT[6];
+    for (int r0 = 0; r0 < 2; ++r0)
+      for (int c0 = 0; c0 < 3; ++c0) {
+        float acc = 0.0f;
+        for (int k = 0; k < 3; ++k) acc += GT[3 * r0 + k] * Sf[3 * k + c0];
+        dT[3 * r0 + c0] = 2.0f * acc;
+      }
+    // T = J W with J = [[j00, 0, j02], [0, j11, j12]]
+    float gj00 = 0.0f, gj02 = 0.0f, gj11 = 0.0f, gj12 = 0.0f;
+    for (int k = 0; k < 3; ++k) {
+      gj00 += dT[k] * cam.r[k];
+      gj02 += dT[k] * cam.r[6 + k];
+      gj11 += dT[3 + k] * cam.r[3 + k];
+      gj12 += dT[3 + k] * cam.r[6 + k];
+    }
+    const float iz = g.iz, iz2 = iz * iz;
+    // j00 = fx/vz, j02 = -fx txc/vz (txc = clamp(vx/vz)), same for y
+    gvz += -cam.fx * iz2 * gj00 - cam.fy * iz2 * gj11;
+    gvz += cam.fx * g.txc * iz2 * gj02 + cam.fy * g.tyc * iz2 * gj12;
+    if (g.tx >= cam.lim_x_lo && g.tx <= cam.lim_x_hi) {
+      gvx += -cam.fx * iz2 * gj02;
+      gvz += cam.fx * g.vx * iz2 * iz * gj02;
+    }
+    if (g.ty >= cam.lim_y_lo && g.ty <= cam.lim_y_hi) {
+      gvy += -cam.fy * iz2 * gj12;
+      gvz += cam.fy * g.vy * iz2 * iz * gj12;
+    }
+    // v = W p + t
+    gm[0] += cam.r[0] * gvx + cam.r[3] * gvy + cam.r[6] * gvz;
+    gm[1] += cam.r[1] * gvx + cam.r[4] * gvy + cam.r[7] * gvz;
+    gm[2] += cam.r[2] * gvx + cam.r[5] * gvy + cam.r[8] * gvz;
+
+    // S = M M^T, M = R diag(s): dL/dM = 2 dS M
+    float dM[9];
+    for (int r0 = 0; r0 < 3; ++r0)
+      for (int c0 = 0; c0 < 3; ++c0) {
+        float acc = 0.0f;
+        for (int k = 0; k < 3; ++k) acc += dS[3 * r0 + k] * g.M[3 * k + c0];
+        dM[3 * r0 + c0] = 2.0f * acc;
+      }
+    float dR[9];
+    for (int k = 0; k < 3; ++k) {
+      float ds = 0.0f;
+      for (int r0 = 0; r0 < 3; ++r0) {
+        ds += dM[3 * r0 + k] * g.R[3 * r0 + k];
+        dR[3 * r0 + k] = dM[3 * r0 + k] * g.s[k];
+      }
+      gdl[k] = ds * g.s[k];
+    }
+    // rotation matrix of the normalised quaternion (w, x, y, z)
+    const float w = g.qw, x = g.qx, y = g.qy, z = g.qz;
+    const float gw = 2.0f * (-z * dR[1] + y * dR[2] + z * dR[3] - x * dR[5] - y * dR[6] + x * dR[7]);
+    const float gx = 2.0f * (y * dR[1] + z * dR[2] + y * dR[3] - 2.0f * x * dR[4] - w * dR[5] +
+                             z * dR[6] + w * dR[7] - 2.0f * x * dR[8]);
+    const float gy = 2.0f * (-2.0f * y * dR[0] + x * dR[1] + w * dR[2] + x * dR[3] + z * dR[5] -
+                             w * dR[6] + z * dR[7] - 2.0f * y * dR[8]);
+    const float gz = 2.0f * (-2.0f * z * dR[0] - w * dR[1] + x * dR[2] + w * dR[3] -
+                             2.0f * z * dR[4] + y * dR[5] + x * dR[6] + y * dR[7]);
+    const float qd = w * gw + x * gx + y * gy + z * gz;
+    gq = make_float4((gw - w * qd) * g.qinv, (gx - x * qd) * g.qinv, (gy - y * qd) * g.qinv,
+                     (gz - z * qd) * g.qinv);
+  } else if (valid && vmask != 0) {
+    float* row = srow + lane * RP;
+    for (int k = 0; k < R; ++k) row[k] = 0.0f;
+  }
+  wave_sync();
+
+  // SH gradients: whole wavefront writes its contiguous block
+  float* dst = g_sh + wave_first * R;
+  if (vmask != 0) {
+    for (int f = lane; f < total; f += 64) {
+      const int row = f / R, colm = f - row * R;
+      dst[f] = srow[row * RP + colm];
+    }
+  } else {
+    for (int f = lane; f < total; f += 64) dst[f] = 0.0f;
+  }
+  if (valid) {
+    g_means[3 * i] = gm[0];
+    g_means[3 * i + 1] = gm[1];
+    g_means[3 * i + 2] = gm[2];
+    g_log_scales[3 * i] = gdl[0];
+    g_log_scales[3 * i + 1] = gdl[1];
+    g_log_scales[3 * i + 2] = gdl[2];
+    g_quats[i] = gq;
+    g_opacity[i] = gop;
+  }
+}
+
+}  // namespace gs
+
+using namespace gs;
+
+template <int K>
+static void launch_pre_fwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
+                           const float* quats, const float* op, const float* sh, int64_t n,
+                           int active, const CamK& cam, float* rec, uint32_t* touched) {
+  hipLaunchKernelGGL(preprocess_fwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
+                     reinterpret_cast<SplatRec*>(rec), touched);
+}
+
+template <int K>
+static void launch_pre_bwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
+                           const float* quats, const float* op, const float* sh, int64_t n,
+                           int active, const CamK& cam, const float* rec, const uint32_t* touched,
+                           const float* g2, float* gm, float* gls, float* gq, float* gop,
+                           float* gsh) {
+  hipLaunchKernelGGL(preprocess_bwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
+                     reinterpret_cast<const SplatRec*>(rec), touched, g2, gm, gls,
+                     reinterpret_cast<float4*>(gq), gop, gsh);
+}
+
+static int check_sh(int sh_coeffs, int sh_degree) {
+  GS_REQUIRE(sh_coeffs == 1 || sh_coeffs == 4 || sh_coeffs == 9 || sh_coeffs == 16, GS_ERR_ARG,
+             "sh_coeffs must be 1, 4, 9 or 16 (got %d)", sh_coeffs);
+  GS_REQUIRE(sh_degree >= 0 && (sh_degree + 1) * (sh_degree + 1) <= sh_coeffs, GS_ERR_ARG,
+             "sh_degree %d needs more than %d coefficients", sh_degree, sh_coeffs);
+  return GS_OK;
+}
+
+extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, const float* quats,
+                                 const float* opacity_logits, const float* sh, int64_t n,
+                                 int sh_coeffs, int sh_degree, const gs_camera* cam,
+                                 float* splat_rec, uint32_t* tiles_touched, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
+  if (int e = check_cam(cam)) return e;
+  if (int e = check_sh(sh_coeffs, sh_degree)) return e;
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means && log_scales && quats && opacity_logits && sh && splat_rec && tiles_touched,
+             GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(aligned(quats, 16) && aligned(splat_rec, 16), GS_ERR_ALIGN,
+             "quats and splat_rec must be 16-byte aligned");
+  const CamK k = make_cam(*cam);
+  const int active = (sh_degree + 1) * (sh_degree + 1);
+  const int64_t blocks = (n + 255) / 256;
+  hipStream_t st = as_stream(stream);
+  switch (sh_coeffs) {
+    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
+    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
+    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
+    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
+  }
+  return check_launch("preprocess_fwd");
+}
+
+extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, const float* quats,
+                                 const float* opacity_logits, const float* sh, int64_t n,
+                                 int sh_coeffs, int sh_degree, const gs_camera* cam,
+                                 const float* splat_rec, const uint32_t* tiles_touched,
+                                 const float* grad2d, float* grad_means, float* grad_log_scales,
+                                 float* grad_quats, float* grad_opacity_logits, float* grad_sh,
+                                 void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
+  if (int e = check_cam(cam)) return e;
+  if (int e = check_sh(sh_coeffs, sh_degree)) return e;
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means && log_scales && quats && opacity_logits && sh && splat_rec && tiles_touched &&
+                 grad2d && grad_means && grad_log_scales && grad_quats && grad_opacity_logits &&
+                 grad_sh,
+             GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(aligned(quats, 16) && aligned(splat_rec, 16) && aligned(grad_quats, 16), GS_ERR_ALIGN,
+             "quats, splat_rec and grad_quats must be 16-byte aligned");
+  const CamK k = make_cam(*cam);
+  const int active = (sh_degree + 1) * (sh_degree + 1);
+  const int64_t blocks = (n + 255) / 256;
+  hipStream_t st = as_stream(stream);
+  switch (sh_coeffs) {
+    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
+    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
+    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
+    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
+  }
+  return check_launch("preprocess_bwd");
+}

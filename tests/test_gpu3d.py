@@ -1,0 +1,247 @@
+"""GPU parity of the 3D path: HIP kernels (through the C ABI) against the CPU oracle and the
+float64 autograd reference, on identical seeded inputs.
+
+Bar (north star): tile assignment, sorted keys and per-tile ranges bit-exact; forward image
+and alpha within 1e-5 max abs; gradients within 1e-4 relative L2 (atomic order differs).
+Scenes follow phase1/tests/test_parity.py:43-84 (camera-space scenes with partial tiles,
+heavy overlap, small splats) plus the empty case of :143-153.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dense3d as D
+import oracle as O
+from amdsplat import rasterize as R
+from amdsplat import scenes
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 1e-5
+GRAD_TOL = 1e-4
+BG = (0.2, 0.5, 0.8)
+
+SCENES = {
+    # name: (n, W, H, scale range, opacity range, depth range)
+    "tiny": (1_000, 160, 120, (0.01, 0.1), (0.05, 0.95), (2.0, 8.0)),
+    "partial_tiles": (20_000, 333, 250, (0.005, 0.08), (0.05, 0.95), (2.0, 8.0)),
+    "heavy_overlap": (8_000, 200, 152, (0.05, 0.4), (0.3, 0.99), (2.0, 8.0)),
+    "small_splats": (30_000, 321, 217, (0.0005, 0.006), (0.02, 0.99), (2.0, 8.0)),
+}
+
+
+def make(name, seed=0, sh_coeffs=16):
+    n, W, H, sc, op, dp = SCENES[name]
+    return scenes.small_scene(n, W, H, seed=seed, sh_coeffs=sh_coeffs, scale=sc, opacity=op, depth=dp)
+
+
+def gpu_forward(scene, sh_degree, bg=BG):
+    cam = scene.cameras[0]
+    p = [t.cuda().contiguous() for t in scene.params()]
+    fs = R.forward_pass(*p, cam, sh_degree=sh_degree, bg=bg)
+    torch.cuda.synchronize()
+    return p, fs
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def read_ckpt_mask(n_contrib, boff, tile_max, W, H):
+    """(bucket, pixel) pairs the backward reads: bucket start < n_contrib of that pixel."""
+    tiles_x = (W + 15) // 16
+    sel = []
+    for tile in range(len(tile_max)):
+        tx, ty = tile % tiles_x, tile // tiles_x
+        for b in range(int(boff[tile]), int(boff[tile + 1])):
+            bstart = (b - int(boff[tile])) * 32
+            if bstart >= int(tile_max[tile]):
+                break
+            for t in range(256):
+                px, py = tx * 16 + t % 16, ty * 16 + t // 16
+                if px < W and py < H and n_contrib[py, px] > bstart:
+                    sel.append((b, t))
+    return np.array(sel, dtype=np.int64).reshape(-1, 2)
+
+
+@pytest.mark.parametrize("name", list(SCENES))
+def test_forward_matches_oracle(name):
+    sc = make(name)
+    cam = sc.cameras[0]
+    deg = 3
+    p, fs = gpu_forward(sc, deg)
+    ref = O.render(*[t.numpy() for t in sc.params()], cam, deg, bg=BG)
+    vis = ref["touched"] > 0
+    assert (np_(fs.touched).astype(np.uint32) == ref["touched"]).all(), "tiles touched differ"
+    assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref["rec"][vis].view(np.uint32)), "splat records differ"
+    assert fs.m == len(ref["keys"])
+    assert np.array_equal(np_(fs.keys).view(np.uint64), ref["keys"]), "sorted keys differ"
+    assert np.array_equal(np_(fs.point_list).view(np.uint32), ref["point_list"]), "point list differs"
+    assert np.array_equal(np_(fs.ranges).view(np.uint32), ref["ranges"]), "tile ranges differ"
+    assert np.array_equal(np_(fs.bucket_offsets).view(np.uint32), ref["bucket_offsets"]), "bucket offsets differ"
+    assert np.array_equal(np_(fs.n_contrib), ref["n_contrib"]), "n_contrib differs"
+    assert np.array_equal(np_(fs.tile_max).view(np.uint32), ref["tile_max"]), "tile max differs"
+    img, fT = np_(fs.image), np_(fs.final_T)
+    assert np.abs(img - ref["image"]).max() <= FWD_TOL
+    assert np.abs(fT - ref["final_T"]).max() <= FWD_TOL
+    sel = read_ckpt_mask(ref["n_contrib"], ref["bucket_offsets"], ref["tile_max"], cam.width, cam.height)
+    ck = np_(fs.ckpt)
+    assert np.abs(ck[sel[:, 0], sel[:, 1]] - ref["ckpt"][sel[:, 0], sel[:, 1]]).max() <= FWD_TOL
+    b2t = np_(fs.bucket_to_tile).view(np.uint32)[: int(ref["bucket_offsets"][-1])]
+    expect = np.repeat(np.arange(len(ref["tile_max"]), dtype=np.uint32), np.diff(ref["bucket_offsets"]))
+    assert np.array_equal(b2t, expect)
+
+
+@pytest.mark.parametrize("name", ["tiny", "partial_tiles", "heavy_overlap"])
+def test_gradients_match_float64_autograd(name):
+    sc = make(name, seed=1)
+    cam = sc.cameras[0]
+    deg = 3
+    p, fs = gpu_forward(sc, deg)
+    g = torch.Generator().manual_seed(7)
+    gi = torch.randn(3, cam.height, cam.width, generator=g, dtype=torch.float64)
+    ga = torch.randn(cam.height, cam.width, generator=g, dtype=torch.float64)
+    grads = R.backward_pass(fs, *p, gi.float().cuda(), ga.float().cuda())
+    torch.cuda.synchronize()
+    ref = O.render(*[t.numpy() for t in sc.params()], cam, deg, bg=BG)
+    mask = O.contrib_mask(ref["rec"], ref["point_list"], ref["ranges"], cam.width, cam.height, ref["n_contrib"])
+    P = [t.double().requires_grad_(True) for t in sc.params()]
+    pre = D.preprocess64(*P, cam, deg)
+    img, fT = D.blend64(pre["mean2d"], pre["conic"], pre["opacity"], pre["color"], ref["point_list"],
+                        ref["ranges"], mask, cam.width, cam.height, BG)
+    assert np.abs(img.detach().numpy() - np_(fs.image)).max() <= FWD_TOL
+    ((img * gi).sum() + ((1 - fT) * ga).sum()).backward()
+    for gname, a, b in zip(("means", "log_scales", "quats", "opacity_logits", "sh"), grads[:5], P):
+        e = D.rel_err(np_(a), b.grad)
+        assert e < GRAD_TOL, f"{name}/{gname}: rel err {e:.2e}"
+
+
+def test_grad2d_matches_oracle_replay():
+    sc = make("partial_tiles", seed=2)
+    cam = sc.cameras[0]
+    p, fs = gpu_forward(sc, 3)
+    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(3))
+    g2 = R.backward_pass(fs, *p, gi.cuda())[5]
+    ref = O.render(*[t.numpy() for t in sc.params()], cam, 3, bg=BG)
+    o2 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
+                     ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"],
+                     sc.n)
+    g2 = np_(g2)
+    for k, name in enumerate(["mx", "my", "A", "B", "C", "opacity", "r", "g", "b", "|mx|", "|my|"]):
+        e = D.rel_err(g2[:, k], o2[:, k])
+        assert e < 1e-5, f"grad2d {name}: {e:.2e}"
+
+
+@pytest.mark.parametrize("sh_coeffs,deg", [(1, 0), (4, 1), (9, 2), (16, 3), (16, 1)])
+def test_sh_degrees(sh_coeffs, deg):
+    sc = make("tiny", seed=4, sh_coeffs=sh_coeffs)
+    cam = sc.cameras[0]
+    p, fs = gpu_forward(sc, deg)
+    ref = O.render(*[t.numpy() for t in sc.params()], cam, deg, bg=BG)
+    vis = ref["touched"] > 0
+    assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref["rec"][vis].view(np.uint32))
+    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(5))
+    gsh = np_(R.backward_pass(fs, *p, gi.cuda())[4])
+    active = (deg + 1) ** 2
+    assert np.all(gsh[:, active:, :] == 0.0), "coefficients above the active degree must get zero gradient"
+    assert np.all(gsh[~vis] == 0.0)
+
+
+def test_misaligned_sh_pointer():
+    """SH tensor whose data pointer is 4 bytes off a 16-byte boundary (upstream/tests/test_sh_load_equiv.py:58-63)."""
+    sc = make("tiny", seed=6)
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    buf = torch.empty(p[4].numel() + 1, device="cuda")
+    sh_mis = buf[1:].view_as(p[4])
+    sh_mis.copy_(p[4])
+    assert sh_mis.data_ptr() % 16 != 0
+    fs_a = R.forward_pass(*p, cam, sh_degree=3, bg=BG)
+    fs_b = R.forward_pass(*p[:4], sh_mis, cam, sh_degree=3, bg=BG)
+    assert torch.equal(fs_a.image, fs_b.image)
+
+
+def test_empty_scene_behind_camera():
+    sc = make("tiny", seed=3)
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    p[0] = p[0] * torch.tensor([1.0, 1.0, -1.0], device="cuda")  # all behind the camera
+    fs = R.forward_pass(*p, cam, sh_degree=3, bg=BG)
+    torch.cuda.synchronize()
+    assert fs.m == 0 and fs.n_buckets == 0
+    assert torch.allclose(fs.image, torch.tensor(BG, device="cuda")[:, None, None].expand_as(fs.image))
+    grads = R.backward_pass(fs, *p, torch.ones_like(fs.image))
+    for g in grads[:5]:
+        assert float(g.abs().sum()) == 0.0
+
+
+def test_deterministic_and_back_to_back():
+    """Integer outputs identical across 10 unsynchronised calls; gradients within atomic-order noise."""
+    sc = make("partial_tiles", seed=8)
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    gi = torch.randn(3, cam.height, cam.width, device="cuda")
+    outs = []
+    for _ in range(10):
+        fs = R.forward_pass(*p, cam, sh_degree=3, bg=BG)
+        outs.append((fs, R.backward_pass(fs, *p, gi)))
+    torch.cuda.synchronize()
+    fs0, g0 = outs[0]
+    for fs, g in outs[1:]:
+        assert torch.equal(fs.point_list, fs0.point_list) and torch.equal(fs.ranges, fs0.ranges)
+        assert torch.equal(fs.image, fs0.image) and torch.equal(fs.n_contrib, fs0.n_contrib)
+        for a, b in zip(g[:5], g0[:5]):
+            assert D.rel_err(np_(a), np_(b)) < 1e-6
+
+
+def test_autograd_function_surface():
+    """rasterize(means, scales, quats, opacities, sh, viewmat, K, W, H) -> (image, alpha, aux)."""
+    sc = make("tiny", seed=9)
+    cam = sc.cameras[0]
+    K = torch.tensor([[cam.fx, 0, cam.cx], [0, cam.fy, cam.cy], [0, 0, 1]])
+    leaves = [t.cuda().requires_grad_(True) for t in sc.params()]
+    img, alpha, aux = R.rasterize(*leaves, cam.viewmat, K, cam.width, cam.height, bg=BG, near=cam.near, far=cam.far)
+    assert img.shape == (3, cam.height, cam.width) and alpha.shape == (cam.height, cam.width)
+    (img.sum() + alpha.sum()).backward()
+    assert all(t.grad is not None and torch.isfinite(t.grad).all() for t in leaves)
+    # activated parameters give the same image
+    img2, _, _ = R.rasterize(leaves[0].detach(), leaves[1].detach().exp(), leaves[2].detach(),
+                             torch.sigmoid(leaves[3].detach()), leaves[4].detach(), cam.viewmat, K, cam.width,
+                             cam.height, bg=BG, near=cam.near, far=cam.far, activated=True)
+    assert (img2 - img.detach()).abs().max() < 1e-5
+    assert aux["tiles_touched"].shape == (sc.n,)
+
+
+def test_full_size_1m_sampled_tiles():
+    """1M-Gaussian SH3 1297x840 view: size-independent properties on the whole frame, and
+    oracle parity on every preprocess record plus a sample of tiles."""
+    sc = scenes.sh3_1m()
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    fs = R.forward_pass(*p, cam, sh_degree=3)
+    torch.cuda.synchronize()
+    keys = np_(fs.keys).view(np.uint64)
+    assert np.all(keys[1:] >= keys[:-1]), "keys not sorted"
+    rng = np_(fs.ranges).astype(np.int64)
+    assert int((rng[:, 1] - rng[:, 0]).sum()) == fs.m
+    assert torch.isfinite(fs.image).all()
+    ref_rec, ref_touched = O.preprocess_fwd(*[t.numpy() for t in sc.params()], cam, 3)
+    assert np.array_equal(np_(fs.touched).astype(np.uint32), ref_touched)
+    vis = ref_touched > 0
+    assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref_rec[vis].view(np.uint32))
+    # sampled tiles: rebuild their lists on the CPU from the GPU's records, blend, compare
+    T = cam.n_tiles
+    sample = np.random.default_rng(0).choice(T, size=64, replace=False)
+    keep = np.zeros(T, bool)
+    keep[sample] = True
+    ranges = np_(fs.ranges).view(np.uint32).copy()
+    ranges[~keep] = 0
+    pl = np_(fs.point_list).view(np.uint32)
+    boff = np_(fs.bucket_offsets).view(np.uint32)
+    img, fT, nc, tmax, _ = O.blend_fwd(ref_rec, pl, ranges, boff, cam.width, cam.height, with_ckpt=False)
+    tiles_x = cam.tiles_x
+    for t in sample:
+        tx, ty = t % tiles_x, t // tiles_x
+        ys, xs = slice(ty * 16, min(ty * 16 + 16, cam.height)), slice(tx * 16, min(tx * 16 + 16, cam.width))
+        assert np.abs(np_(fs.image)[:, ys, xs] - img[:, ys, xs]).max() <= FWD_TOL
+        assert np.array_equal(np_(fs.n_contrib)[ys, xs], nc[ys, xs])
