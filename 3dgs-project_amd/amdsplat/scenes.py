@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .rasterize import Camera
+from .raster3d import Camera
 
 SH_C0 = 0.28209479177387814
 

@@ -250,17 +250,22 @@ __global__ void bucket_count_kernel(const uint32_t* __restrict__ ranges, int n_t
   counts[t] = (len + kBucket - 1) / kBucket;
 }
 
+// One thread per bucket slot: binary search of the tile whose bucket range holds b.
 __global__ void bucket_fill_kernel(const uint32_t* __restrict__ boff, int n_tiles,
                                    uint32_t* __restrict__ b2t, int64_t n_max) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t > n_tiles) return;
-  if (t == n_tiles) {
-    // tail: mark unused slots
-    for (int64_t b = boff[n_tiles]; b < n_max; ++b) b2t[b] = 0xffffffffu;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= n_max) return;
+  if (b >= static_cast<int64_t>(boff[n_tiles])) {
+    b2t[b] = 0xffffffffu;
     return;
   }
-  const uint32_t b1 = boff[t + 1];
-  for (uint32_t b = boff[t]; b < b1 && b < n_max; ++b) b2t[b] = static_cast<uint32_t>(t);
+  int lo = 0, hi = n_tiles - 1;  // largest t with boff[t] <= b
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (static_cast<int64_t>(boff[mid]) <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  b2t[b] = static_cast<uint32_t>(lo);
 }
 
 }  // namespace gs
@@ -380,7 +385,8 @@ extern "C" int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint3
   GS_REQUIRE(n_tiles > 0 && n_buckets_max >= 0 && bucket_offsets, GS_ERR_ARG,
              "invalid bucket_fill arguments");
   GS_REQUIRE(n_buckets_max == 0 || bucket_to_tile, GS_ERR_ARG, "null bucket_to_tile");
-  hipLaunchKernelGGL(bucket_fill_kernel, dim3(grid_for(n_tiles + 1, 256)), dim3(256), 0,
+  if (n_buckets_max == 0) return GS_OK;
+  hipLaunchKernelGGL(bucket_fill_kernel, dim3(grid_for(n_buckets_max, 256)), dim3(256), 0,
                      as_stream(stream), bucket_offsets, n_tiles, bucket_to_tile, n_buckets_max);
   return check_launch("bucket_fill");
 }

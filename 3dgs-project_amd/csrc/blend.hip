@@ -264,9 +264,9 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
                                float* ckpt, void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARG, "image size must be positive");
-  GS_REQUIRE(splat_rec && ranges && point_list && bucket_offsets && image && final_T && n_contrib &&
-                 tile_max && ckpt,
-             GS_ERR_ARG, "null pointer argument");
+  // splat_rec, point_list and ckpt may be NULL when the scene has no instances
+  GS_REQUIRE(ranges && bucket_offsets && image && final_T && n_contrib && tile_max, GS_ERR_ARG,
+             "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16) && aligned(ranges, 8), GS_ERR_ALIGN,
              "splat_rec/ckpt must be 16-byte and ranges 8-byte aligned");
   const int tiles_x = (width + kTile - 1) / kTile, tiles_y = (height + kTile - 1) / kTile;
@@ -292,9 +292,11 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
   GS_REQUIRE(grad2d || n == 0, GS_ERR_ARG, "null grad2d");
   hipStream_t st = as_stream(stream);
   fill_zero_f32(grad2d, n * kGrad2D, st);
-  if (n_buckets_max == 0 || n == 0) return check_launch("blend_bwd_3d");
-  GS_REQUIRE(splat_rec && ranges && point_list && bucket_offsets && bucket_to_tile && image &&
-                 grad_image && n_contrib && tile_max && ckpt && (final_T || !grad_alpha),
+  if (int e = check_launch("blend_bwd_3d (zero fill)")) return e;
+  if (n_buckets_max == 0 || n == 0) return GS_OK;
+  // splat_rec, point_list and ckpt may be NULL when there are no instances (no bucket reads them)
+  GS_REQUIRE(ranges && bucket_offsets && bucket_to_tile && image && grad_image && n_contrib &&
+                 tile_max && (final_T || !grad_alpha),
              GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16) && aligned(ranges, 8), GS_ERR_ALIGN,
              "splat_rec/ckpt must be 16-byte and ranges 8-byte aligned");

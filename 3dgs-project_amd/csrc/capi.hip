@@ -15,12 +15,24 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
-void clear_error() { g_last_error[0] = 0; }
+// An error left pending by earlier, unrelated HIP calls is taken off the error slot on entry
+// (so it is not blamed on this call) and reported alongside any failure of this call.
+static thread_local hipError_t g_stale = hipSuccess;
+
+void clear_error() {
+  g_last_error[0] = 0;
+  g_stale = hipGetLastError();
+}
 
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    set_error("%s: %s", what, hipGetErrorString(e));
+    if (g_stale != hipSuccess) {
+      set_error("%s: %s (an earlier HIP call had left: %s)", what, hipGetErrorString(e),
+                hipGetErrorString(g_stale));
+    } else {
+      set_error("%s: %s", what, hipGetErrorString(e));
+    }
     return GS_ERR_LAUNCH;
   }
   return GS_OK;

@@ -1,7 +1,6 @@
-// Camera description shared by the 3D kernels and the exact ellipse / tile-rectangle test
-// used both to count a Gaussian's tiles in the preprocess and to emit its instances in the
-// binning. Both callers go through ellipse_hits_rect(), so the count and the emitted keys
-// always agree.
+// Camera description shared by the 3D kernels, and the ellipse / tile test used both to count
+// a Gaussian's tiles in the preprocess and to emit its instances in the binning. Both callers
+// go through band_columns(), so the count and the emitted keys always agree.
 #pragma once
 
 #include "gs_common.h"
@@ -21,68 +20,91 @@ struct CamK {
   int tiles_x, tiles_y;
 };
 
-// 1/2 (A dx^2 + 2 B dx dy + C dy^2) with a fixed operation order.
-__device__ __forceinline__ float half_quad(float A, float B, float C, float dx, float dy) {
-  float u = C * dy;
-  u = u * dy;
-  float v = B * dx;
-  v = v + v;
-  u = fmaf(v, dy, u);
-  const float w = A * dx;
-  u = fmaf(w, dx, u);
-  return 0.5f * u;
+// Tile assignment. A tile row is a horizontal band of pixel-centre rows [Y0, Y1] (the
+// tile's rows clipped to the splat's pixel bounds). The alpha >= 1/255 ellipse
+// 1/2 d^T Q d <= thr (d = p - mean) meets the band in a convex set whose x-extent [xl, xr] has
+// a closed form; the splat touches the tiles that own a pixel column c (inside its bounds)
+// with c + 0.5 in [xl, xr]. Cost is O(tile rows) per splat instead of O(tiles).
+struct BandSetup {
+  float mx, my, A, B, det, tA, vmax, vr;
+  bool ok;
+};
+
+__device__ __forceinline__ BandSetup band_setup(const float4 a, const float4 b) {
+  BandSetup s;
+  s.mx = a.x;
+  s.my = a.y;
+  s.A = a.z;
+  s.B = a.w;
+  const float C = b.x, thr = b.w;
+  const float t2 = thr + thr;
+  s.det = fmaf(s.A, C, -(s.B * s.B));
+  s.ok = s.det > 0.0f;
+  s.tA = t2 * s.A;
+  s.vmax = sqrtf(s.tA / s.det);  // half height of the ellipse
+  // the rightmost point of the ellipse is (ur, vr) relative to the mean
+  const float ur = sqrtf((t2 * C) / s.det);
+  s.vr = -((s.B / C) * ur);
+  return s;
 }
 
-// Does the ellipse 1/2 d^T Q d <= thr (d = mean - p) reach any point p of the axis-aligned
-// rectangle [X0, X1] x [Y0, Y1]? Exact for a convex quadratic: if the mean lies outside, the
-// minimum over the rectangle is attained on an edge facing the mean, and on an edge the
-// 1D minimiser is the clamped stationary point.
-__device__ __forceinline__ bool ellipse_hits_rect(float mx, float my, float A, float B, float C,
-                                                  float thr, float X0, float X1, float Y0,
-                                                  float Y1) {
-  const bool out_x = (mx < X0) || (mx > X1);
-  const bool out_y = (my < Y0) || (my > Y1);
-  if (!out_x && !out_y) return true;
-  float best = 3.0e38f;
-  if (out_x) {
-    const float xe = (mx < X0) ? X0 : X1;
-    const float dx = mx - xe;
-    const float k = B / C;
-    const float ys = fminf(fmaxf(fmaf(k, dx, my), Y0), Y1);
-    const float dy = my - ys;
-    best = fminf(best, half_quad(A, B, C, dx, dy));
-  }
-  if (out_y) {
-    const float ye = (my < Y0) ? Y0 : Y1;
-    const float dy = my - ye;
-    const float k = B / A;
-    const float xs = fminf(fmaxf(fmaf(k, dy, mx), X0), X1);
-    const float dx = mx - xs;
-    best = fminf(best, half_quad(A, B, C, dx, dy));
-  }
-  return best <= thr;
+// Pixel columns [c0, c1] (clipped to [bx0, bx1]) of the ellipse within the row band.
+__device__ __forceinline__ bool band_columns(const BandSetup& s, float Y0, float Y1, int bx0, int bx1,
+                                             int& c0, int& c1) {
+  if (!s.ok) return false;
+  const float v0 = fmaxf(Y0 - s.my, -s.vmax);
+  const float v1 = fminf(Y1 - s.my, s.vmax);
+  if (!(v0 <= v1)) return false;
+  // the x-extent of a row v is concave in v: its max / min over the band sit at the clamped
+  // rows of the rightmost / leftmost points
+  const float vc = fminf(fmaxf(s.vr, v0), v1);
+  const float dr = fmaxf(fmaf(-s.det, vc * vc, s.tA), 0.0f);
+  const float br = s.B * vc;
+  const float xr = s.mx + (sqrtf(dr) - br) / s.A;
+  const float vl = fminf(fmaxf(-s.vr, v0), v1);
+  const float dl = fmaxf(fmaf(-s.det, vl * vl, s.tA), 0.0f);
+  const float bl = s.B * vl;
+  const float xl = s.mx + (-bl - sqrtf(dl)) / s.A;
+  const float f0 = fmaxf(ceilf(xl - 0.5f), static_cast<float>(bx0));
+  const float f1 = fminf(floorf(xr - 0.5f), static_cast<float>(bx1));
+  if (!(f0 <= f1)) return false;
+  c0 = static_cast<int>(f0);
+  c1 = static_cast<int>(f1);
+  return true;
 }
 
-// Visits every tile whose pixels (restricted to the splat's pixel bounds) the ellipse
-// reaches, in row-major tile order. Returns the number of such tiles.
+// Visits the touched tiles in row-major order; returns their number.
 template <typename F>
 __device__ __forceinline__ int for_each_touched_tile(const float4 a, const float4 b, const int4 d,
                                                      int tiles_x, F&& visit) {
-  const float mx = a.x, my = a.y, A = a.z, B = a.w, C = b.x, thr = b.w;
-  const int tx0 = d.x / kTile, tx1 = d.y / kTile;
+  const BandSetup s = band_setup(a, b);
   const int ty0 = d.z / kTile, ty1 = d.w / kTile;
   int count = 0;
   for (int ty = ty0; ty <= ty1; ++ty) {
     const int py0 = max(ty * kTile, d.z), py1 = min(ty * kTile + kTile - 1, d.w);
-    const float Y0 = static_cast<float>(py0) + 0.5f, Y1 = static_cast<float>(py1) + 0.5f;
-    for (int tx = tx0; tx <= tx1; ++tx) {
-      const int px0 = max(tx * kTile, d.x), px1 = min(tx * kTile + kTile - 1, d.y);
-      const float X0 = static_cast<float>(px0) + 0.5f, X1 = static_cast<float>(px1) + 0.5f;
-      if (ellipse_hits_rect(mx, my, A, B, C, thr, X0, X1, Y0, Y1)) {
-        visit(ty * tiles_x + tx, count);
-        ++count;
-      }
+    int c0, c1;
+    if (!band_columns(s, static_cast<float>(py0) + 0.5f, static_cast<float>(py1) + 0.5f, d.x, d.y,
+                      c0, c1))
+      continue;
+    for (int tx = c0 / kTile; tx <= c1 / kTile; ++tx) {
+      visit(ty * tiles_x + tx, count);
+      ++count;
     }
+  }
+  return count;
+}
+
+// Number of touched tiles (same rule, without enumerating them).
+__device__ __forceinline__ int count_touched_tiles(const float4 a, const float4 b, const int4 d) {
+  const BandSetup s = band_setup(a, b);
+  const int ty0 = d.z / kTile, ty1 = d.w / kTile;
+  int count = 0;
+  for (int ty = ty0; ty <= ty1; ++ty) {
+    const int py0 = max(ty * kTile, d.z), py1 = min(ty * kTile + kTile - 1, d.w);
+    int c0, c1;
+    if (band_columns(s, static_cast<float>(py0) + 0.5f, static_cast<float>(py1) + 0.5f, d.x, d.y, c0,
+                     c1))
+      count += c1 / kTile - c0 / kTile + 1;
   }
   return count;
 }

@@ -158,8 +158,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   if (g.vis) {
     ra = make_float4(g.mx, g.my, g.A, g.B);
     rb = make_float4(g.C, g.o, g.vz, thr);
-    count = static_cast<uint32_t>(
-        for_each_touched_tile(ra, rb, bnd, cam.tiles_x, [](int, int) {}));
+    count = static_cast<uint32_t>(count_touched_tiles(ra, rb, bnd));
     g.vis = count > 0;
   }
 

@@ -109,7 +109,7 @@ def main():
         sys.exit(2)
     import torch
 
-    from amdsplat import rasterize as R
+    from amdsplat import raster3d as R
     from amdsplat import scenes
 
     make = {"sh3_1m": scenes.sh3_1m, "sh3_3m": scenes.sh3_3m, "sh_rgb_100k": scenes.sh_rgb_100k}[args.workload]

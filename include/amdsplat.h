@@ -107,7 +107,8 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
  *   image [3,H,W] = C + T_final * bg; final_T [H,W]; n_contrib [H,W] = 1 + list position of
  *   the last splat blended into the pixel (0 if none); tile_max [T] = max n_contrib of the
  *   tile; ckpt [n_buckets, 256, 4] = (C.r, C.g, C.b, T) at the start of every 32-entry
- *   bucket. bg is host memory (3 floats) or NULL for black.
+ *   bucket. bg is host memory (3 floats) or NULL for black. splat_rec, point_list and ckpt
+ *   may be NULL when there are no instances (every tile range empty).
  * ------------------------------------------------------------------------------------- */
 int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, int width, int height, const float* bg,

@@ -21,8 +21,8 @@
  *   - colour clamped at 0 with a gradient mask        phase1/fastergs_macro.patch:105-107
  *   - exp2-folded conic                               upstream/upstream_main_kernels.patch:9-13
  *   - SH basis and its backward                       phase2/sh_coalesce.patch:80-170
- *   - tile assignment: exact ellipse / rectangle test (the role of create_instances_cu,
- *     phase2/ellipse_cull.patch:66-68) against the alpha >= 1/255 ellipse; depth-sorted
+ *   - tile assignment: exact ellipse test per tile row against the alpha >= 1/255 ellipse (the
+ *     role of create_instances_cu, phase2/ellipse_cull.patch:66-68); depth-sorted
  *     per-tile lists with ties in Gaussian-index order (phase2/tests/test_readback_equiv.py:57-59)
  *   - EWA projection with a 0.3 px^2 dilation and the 1.3x frustum clamp of the Jacobian
  *     (the published 3DGS preprocess; not pinned by any in-tree file).
@@ -304,59 +304,52 @@ static void geom(const float* means, const float* ls, const float* quats, const 
   g->vis = vis;
 }
 
-static float half_quad(float A, float B, float C, float dx, float dy) {
-  float u = C * dy;
-  u = u * dy;
-  float v = B * dx;
-  v = v + v;
-  u = fmaf(v, dy, u);
-  float w = A * dx;
-  u = fmaf(w, dx, u);
-  return 0.5f * u;
-}
-
-int or_ellipse_hits_rect(float mx, float my, float A, float B, float C, float thr, float X0, float X1,
-                         float Y0, float Y1) {
-  int out_x = (mx < X0) || (mx > X1);
-  int out_y = (my < Y0) || (my > Y1);
-  if (!out_x && !out_y) return 1;
-  float best = 3.0e38f;
-  if (out_x) {
-    float xe = (mx < X0) ? X0 : X1;
-    float dx = mx - xe;
-    float k = B / C;
-    float ys = fminf(fmaxf(fmaf(k, dx, my), Y0), Y1);
-    float dy = my - ys;
-    best = fminf(best, half_quad(A, B, C, dx, dy));
-  }
-  if (out_y) {
-    float ye = (my < Y0) ? Y0 : Y1;
-    float dy = my - ye;
-    float k = B / A;
-    float xs = fminf(fmaxf(fmaf(k, dy, mx), X0), X1);
-    float dx = mx - xs;
-    best = fminf(best, half_quad(A, B, C, dx, dy));
-  }
-  return best <= thr;
+/* Tile assignment (row-band rule): for each tile row, the pixel-centre band [Y0, Y1] (tile
+ * rows clipped to the pixel bounds) meets the ellipse 1/2 d^T Q d <= thr in a convex set with
+ * x-extent [xl, xr]; the splat touches the tiles owning a column c of its bounds with
+ * c + 0.5 in [xl, xr]. Outputs the column range; returns 0 if the band misses. */
+int or_band_columns(float mx, float my, float A, float B, float C, float thr, float Y0, float Y1,
+                    int bx0, int bx1, int* c0, int* c1) {
+  float t2 = thr + thr;
+  float det = fmaf(A, C, -(B * B));
+  if (!(det > 0.0f)) return 0;
+  float tA = t2 * A;
+  float vmax = sqrtf(tA / det);
+  float ur = sqrtf((t2 * C) / det);
+  float vr = -((B / C) * ur);
+  float v0 = fmaxf(Y0 - my, -vmax);
+  float v1 = fminf(Y1 - my, vmax);
+  if (!(v0 <= v1)) return 0;
+  float vc = fminf(fmaxf(vr, v0), v1);
+  float dr = fmaxf(fmaf(-det, vc * vc, tA), 0.0f);
+  float br = B * vc;
+  float xr = mx + (sqrtf(dr) - br) / A;
+  float vl = fminf(fmaxf(-vr, v0), v1);
+  float dl = fmaxf(fmaf(-det, vl * vl, tA), 0.0f);
+  float bl = B * vl;
+  float xl = mx + (-bl - sqrtf(dl)) / A;
+  float f0 = fmaxf(ceilf(xl - 0.5f), (float)bx0);
+  float f1 = fminf(floorf(xr - 0.5f), (float)bx1);
+  if (!(f0 <= f1)) return 0;
+  *c0 = (int)f0;
+  *c1 = (int)f1;
+  return 1;
 }
 
 /* record layout: a = (mx, my, A, B), b = (C, o, depth, thr), c = (r, g, b, mask), d = (x0, x1, y0, y1) */
 static int touched_tiles(const float* rec, int tiles_x, uint32_t* tiles_out) {
   const int32_t* d = (const int32_t*)(rec + 12);
-  float mx = rec[0], my = rec[1], A = rec[2], B = rec[3], C = rec[4], thr = rec[7];
   int cnt = 0;
   for (int ty = d[2] / TILE; ty <= d[3] / TILE; ++ty) {
     int py0 = ty * TILE > d[2] ? ty * TILE : d[2];
     int py1 = ty * TILE + TILE - 1 < d[3] ? ty * TILE + TILE - 1 : d[3];
-    float Y0 = (float)py0 + 0.5f, Y1 = (float)py1 + 0.5f;
-    for (int tx = d[0] / TILE; tx <= d[1] / TILE; ++tx) {
-      int px0 = tx * TILE > d[0] ? tx * TILE : d[0];
-      int px1 = tx * TILE + TILE - 1 < d[1] ? tx * TILE + TILE - 1 : d[1];
-      float X0 = (float)px0 + 0.5f, X1 = (float)px1 + 0.5f;
-      if (or_ellipse_hits_rect(mx, my, A, B, C, thr, X0, X1, Y0, Y1)) {
-        if (tiles_out) tiles_out[cnt] = (uint32_t)(ty * tiles_x + tx);
-        ++cnt;
-      }
+    int c0, c1;
+    if (!or_band_columns(rec[0], rec[1], rec[2], rec[3], rec[4], rec[7], (float)py0 + 0.5f,
+                         (float)py1 + 0.5f, d[0], d[1], &c0, &c1))
+      continue;
+    for (int tx = c0 / TILE; tx <= c1 / TILE; ++tx) {
+      if (tiles_out) tiles_out[cnt] = (uint32_t)(ty * tiles_x + tx);
+      ++cnt;
     }
   }
   return cnt;

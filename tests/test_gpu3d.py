@@ -12,7 +12,7 @@ import torch
 
 import dense3d as D
 import oracle as O
-from amdsplat import rasterize as R
+from amdsplat import raster3d as R
 from amdsplat import scenes
 
 pytestmark = pytest.mark.gpu
@@ -176,7 +176,8 @@ def test_empty_scene_behind_camera():
 
 
 def test_deterministic_and_back_to_back():
-    """Integer outputs identical across 10 unsynchronised calls; gradients within atomic-order noise."""
+    """Integer outputs identical across 10 unsynchronised calls; gradients within the noise of
+    float atomics arriving in a different order (phase1/tests/test_parity.py:131-140)."""
     sc = make("partial_tiles", seed=8)
     cam = sc.cameras[0]
     p = [t.cuda().contiguous() for t in sc.params()]
@@ -191,7 +192,7 @@ def test_deterministic_and_back_to_back():
         assert torch.equal(fs.point_list, fs0.point_list) and torch.equal(fs.ranges, fs0.ranges)
         assert torch.equal(fs.image, fs0.image) and torch.equal(fs.n_contrib, fs0.n_contrib)
         for a, b in zip(g[:5], g0[:5]):
-            assert D.rel_err(np_(a), np_(b)) < 1e-6
+            assert D.rel_err(np_(a), np_(b)) < 1e-5
 
 
 def test_autograd_function_surface():
