@@ -44,8 +44,10 @@ _SIGS = {
     "gs_scan_workspace_size": (_sz, [_i64]),
     "gs_scan_u32": (_i32, [_vp, _vp, _i64, _vp, _sz, _vp]),
     "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp]),
-    "gs_bin_workspace_size": (_sz, [_i64, _i32]),
-    "gs_bin_fill_3d": (_i32, [_vp, _vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32]),
+    "gs_bin_fill_3d": (_i32, [_vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_rect_counts": (_i32, [_vp, _i64, _vp, _vp]),
+    "gs_bin_fill_rect": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -60,8 +62,6 @@ _SIGS = {
                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs2d_blend_bwd_pixel": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp,
                                     _vp, _vp, _vp]),
-    "gs2d_bin_count_rect": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
-    "gs2d_bin_fill_rect": (_i32, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
 }
 
 _lib = None

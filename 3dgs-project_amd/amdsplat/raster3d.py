@@ -84,7 +84,7 @@ class ForwardState:
     touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
     offsets: torch.Tensor        # [n + 1] int32
     m: int                       # instances
-    keys: torch.Tensor           # [m] int64 sorted keys
+    keys: torch.Tensor           # [m] int64 sorted keys (empty unless keep_keys)
     point_list: torch.Tensor     # [m] int32
     ranges: torch.Tensor         # [T, 2] int32
     bucket_offsets: torch.Tensor  # [T + 1] int32
@@ -146,7 +146,7 @@ def _check_inputs(means, log_scales, quats, opacity_logits, sh):
 
 
 def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_degree: int | None = None,
-                 bg=(0.0, 0.0, 0.0), timing: bool = False) -> ForwardState:
+                 bg=(0.0, 0.0, 0.0), timing: bool = False, keep_keys: bool = False) -> ForwardState:
     """Runs the forward stages; inputs are contiguous float32 CUDA tensors (raw parameters)."""
     means, log_scales, quats = means.contiguous(), log_scales.contiguous(), quats.contiguous()
     opacity_logits, sh = opacity_logits.contiguous(), sh.contiguous()
@@ -173,12 +173,12 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     call("gs_scan_u32", ptr(touched), ptr(offsets), n, ptr(ws), ws.numel(), st)
     tm.mark("scan")
     m = int(offsets[n].item()) if n > 0 else 0  # host readback: instance count
-    keys = torch.empty(m, dtype=torch.int64, device=dev)
+    keys = torch.empty(m if keep_keys else 0, dtype=torch.int64, device=dev)
     point_list = torch.empty(m, dtype=torch.int32, device=dev)
     ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
     bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
-    ws = _u8(_lib.size_call("gs_bin_workspace_size", m, T), dev)
-    call("gs_bin_fill_3d", ptr(rec), ptr(touched), ptr(offsets), n, ccam, m, ptr(keys), ptr(point_list),
+    ws = _u8(_lib.size_call("gs_bin_workspace_size", n, m, T), dev)
+    call("gs_bin_fill_3d", ptr(rec), ptr(touched), n, ccam, m, ptr(keys) if keep_keys else None, ptr(point_list),
          ptr(ranges), ptr(bucket_offsets), ptr(ws), ws.numel(), st)
     tm.mark("binning")
     nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)

@@ -1,11 +1,14 @@
-// Tile binning: exclusive scan, instance (key, value) emission, stable LSD radix sort of the
-// 64-bit keys (tile << 32 | orderable depth), per-tile ranges and 32-entry buckets.
+// Tile binning: exclusive scan, per-tile instance lists in (tile, depth, Gaussian index)
+// order, per-tile ranges and 32-entry buckets.
 //
-// The radix sort is reduce-then-scan per 8-bit digit: a histogram kernel, a device-wide
-// exclusive scan of the digit-major histogram table, and a scatter kernel that ranks keys
-// stably inside its block (wavefront match over the 8 digit bits with ballots, then a
-// per-digit prefix over the block's four wavefronts). No kernel waits on another
-// workgroup, so there is no forward-progress requirement.
+// The order is that of a stable sort of 64-bit keys (tile << 32 | orderable depth) over
+// instances emitted in Gaussian-index order, obtained in two levels: a stable 32-bit sort of
+// the Gaussians by depth (N keys), emission of the instances in that order, and a stable sort
+// of the instances by tile (M keys, ceil(log2 T) bits). Each sort is LSD radix with 8-bit
+// digits, reduce-then-scan per digit: a histogram kernel, a device-wide exclusive scan of the
+// digit-major histogram table, and a scatter kernel that ranks keys stably inside its
+// workgroup. No kernel waits on another workgroup, so there is no forward-progress
+// requirement.
 #include "gs_host.h"
 
 namespace gs {
@@ -13,10 +16,6 @@ namespace gs {
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanThreads * kScanItems;  // 2048 values per workgroup
-
-constexpr int kSortThreads = 256;
-constexpr int kSortRounds = 16;
-constexpr int kSortTile = kSortThreads * kSortRounds;  // 4096 keys per workgroup
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
   return (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -123,104 +122,7 @@ static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hip
 }
 
 // ---------------------------------------------------------------------------------------
-// Instances
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void emit_instances_kernel(
-    const SplatRec* __restrict__ rec, const uint32_t* __restrict__ touched,
-    const uint32_t* __restrict__ offsets, int64_t n, int tiles_x, uint64_t* __restrict__ keys,
-    uint32_t* __restrict__ vals) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n || touched[i] == 0u) return;
-  const SplatRec r = rec[i];
-  const uint64_t dkey = float_order_key(r.b.z);
-  const uint32_t off = offsets[i];
-  for_each_touched_tile(r.a, r.b, r.d, tiles_x, [&](int tile, int k) {
-    keys[off + k] = (static_cast<uint64_t>(tile) << 32) | dkey;
-    vals[off + k] = static_cast<uint32_t>(i);
-  });
-}
-
-// ---------------------------------------------------------------------------------------
-// Radix sort
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint64_t* __restrict__ keys,
-                                                                  int64_t m, int shift,
-                                                                  uint32_t* __restrict__ hist,
-                                                                  int n_blocks) {
-  __shared__ uint32_t s_h[256];
-  s_h[threadIdx.x] = 0;
-  __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
-#pragma unroll 4
-  for (int r = 0; r < kSortRounds; ++r) {
-    const int64_t idx = base + r * kSortThreads + threadIdx.x;
-    if (idx < m) {
-      const uint32_t d = static_cast<uint32_t>(keys[idx] >> shift) & 255u;
-      atomicAdd(&s_h[d], 1u);
-    }
-  }
-  __syncthreads();
-  hist[static_cast<int64_t>(threadIdx.x) * n_blocks + blockIdx.x] = s_h[threadIdx.x];
-}
-
-__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
-    const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
-    uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t m, int shift,
-    const uint32_t* __restrict__ offs, int n_blocks) {
-  __shared__ uint32_t s_base[256];
-  __shared__ uint32_t s_cnt[4][256];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  s_base[tid] = offs[static_cast<int64_t>(tid) * n_blocks + blockIdx.x];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
-  const uint64_t lt = lanemask_lt(lane);
-  for (int r = 0; r < kSortRounds; ++r) {
-    const int64_t idx = base + r * kSortThreads + tid;
-    const bool valid = idx < m;
-    uint64_t key = 0;
-    uint32_t val = 0;
-    uint32_t d = 0;
-    if (valid) {
-      key = kin[idx];
-      val = vin[idx];
-      d = static_cast<uint32_t>(key >> shift) & 255u;
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) s_cnt[w][tid] = 0;
-    uint64_t peers = __ballot(valid ? 1 : 0);
-#pragma unroll
-    for (int bit = 0; bit < 8; ++bit) {
-      const bool set = (d >> bit) & 1u;
-      const uint64_t bm = __ballot(set ? 1 : 0);
-      peers &= set ? bm : ~bm;
-    }
-    const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt));
-    const uint32_t cnt = static_cast<uint32_t>(__popcll(peers));
-    __syncthreads();  // s_cnt cleared, s_base final from the previous round
-    if (valid && rank == 0) s_cnt[wave][d] = cnt;
-    __syncthreads();
-    {
-      const uint32_t c0 = s_cnt[0][tid], c1 = s_cnt[1][tid], c2 = s_cnt[2][tid], c3 = s_cnt[3][tid];
-      const uint32_t run = s_base[tid];
-      s_cnt[0][tid] = run;
-      s_cnt[1][tid] = run + c0;
-      s_cnt[2][tid] = run + c0 + c1;
-      s_cnt[3][tid] = run + c0 + c1 + c2;
-      s_base[tid] = run + c0 + c1 + c2 + c3;
-    }
-    __syncthreads();
-    if (valid) {
-      const uint32_t pos = s_cnt[wave][d] + rank;
-      kout[pos] = key;
-      vout[pos] = val;
-    }
-    __syncthreads();  // s_cnt is cleared at the top of the next round
-  }
-}
-
-// ---------------------------------------------------------------------------------------
-// Ranges and buckets
+// Small kernels
 // ---------------------------------------------------------------------------------------
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -232,14 +134,220 @@ __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
   if (i < n) p[i] = v;
 }
 
-__global__ void ranges_kernel(const uint64_t* __restrict__ keys, int64_t m,
-                              uint32_t* __restrict__ ranges) {
+// ---------------------------------------------------------------------------------------
+// Stable LSD radix sort of (uint32 key, uint32 value) pairs, 8-bit digits.
+//
+// Each workgroup owns a contiguous chunk of kChunk pairs; inside it, wavefront w owns the
+// contiguous sub-chunk [w * kSub, (w + 1) * kSub), read in kRounds coalesced rounds (once to
+// count, once to scatter). Keys with equal digits are matched with eight ballots; the
+// lowest lane of each match group updates that wavefront's digit counter in LDS. Order
+// inside a digit is therefore (workgroup, wavefront, round, lane) = input order: stable.
+// ---------------------------------------------------------------------------------------
+constexpr int kSortWaves = 8;
+constexpr int kSortThreads = kSortWaves * kWave;  // 512
+constexpr int kRounds = 16;
+constexpr int kSub = kRounds * kWave;             // 1024 pairs per wavefront
+constexpr int kChunk = kSortWaves * kSub;         // 8192 pairs per workgroup
+
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
+  uint64_t peers = __ballot(valid ? 1 : 0);
+#pragma unroll
+  for (int bit = 0; bit < 8; ++bit) {
+    const bool set = (d >> bit) & 1u;
+    const uint64_t bm = __ballot(set ? 1 : 0);
+    peers &= set ? bm : ~bm;
+  }
+  return valid ? peers : 0ull;
+}
+
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys,
+                                                                  int64_t m, int shift,
+                                                                  uint32_t* __restrict__ hist,
+                                                                  int n_blocks) {
+  __shared__ uint32_t s_h[256];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (threadIdx.x < 256) s_h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + wave * kSub;
+  const uint64_t lt = lanemask_lt(lane);
+  for (int r = 0; r < kRounds; ++r) {
+    const int64_t idx = base + r * kWave + lane;
+    const bool valid = idx < m;
+    const uint32_t d = valid ? (keys[idx] >> shift) & 255u : 0u;
+    const uint64_t peers = match_digit(d, valid);
+    if (valid && (peers & lt) == 0ull) atomicAdd(&s_h[d], static_cast<uint32_t>(__popcll(peers)));
+  }
+  __syncthreads();
+  if (threadIdx.x < 256) hist[static_cast<int64_t>(threadIdx.x) * n_blocks + blockIdx.x] = s_h[threadIdx.x];
+}
+
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
+    uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t m, int shift,
+    const uint32_t* __restrict__ offs, int n_blocks) {
+  __shared__ uint32_t s_cnt[kSortWaves][256];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int k = threadIdx.x; k < kSortWaves * 256; k += kSortThreads) (&s_cnt[0][0])[k] = 0;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + wave * kSub;
+  const uint64_t lt = lanemask_lt(lane);
+  __syncthreads();
+  // per-wavefront digit counts
+  for (int r = 0; r < kRounds; ++r) {
+    const int64_t idx = base + r * kWave + lane;
+    const bool valid = idx < m;
+    const uint32_t d = valid ? (kin[idx] >> shift) & 255u : 0u;
+    const uint64_t peers = match_digit(d, valid);
+    if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
+    wave_sync();
+  }
+  __syncthreads();
+  // per-wavefront starting positions: global digit offset of this workgroup + earlier wavefronts
+  if (threadIdx.x < 256) {
+    const int d = threadIdx.x;
+    uint32_t run = offs[static_cast<int64_t>(d) * n_blocks + blockIdx.x];
+    for (int w = 0; w < kSortWaves; ++w) {
+      const uint32_t c = s_cnt[w][d];
+      s_cnt[w][d] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  // scatter (the chunk was just read, so these loads hit the cache)
+  for (int r = 0; r < kRounds; ++r) {
+    const int64_t idx = base + r * kWave + lane;
+    const bool valid = idx < m;
+    uint32_t key = 0, val = 0;
+    if (valid) {
+      key = kin[idx];
+      val = vin[idx];
+    }
+    const uint32_t d = (key >> shift) & 255u;
+    const uint64_t peers = match_digit(d, valid);
+    uint32_t pos = 0;
+    if (valid) pos = s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt));
+    wave_sync();
+    if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
+    if (valid) {
+      kout[pos] = key;
+      vout[pos] = val;
+    }
+    wave_sync();
+  }
+}
+
+static size_t sort_ws(int64_t m) {
+  const int64_t nb = (m + kChunk - 1) / kChunk;
+  const int64_t hist = 256 * (nb > 0 ? nb : 1);
+  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up((hist + 1) * 4) + scan_ws(hist);
+}
+
+// Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
+static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, uint32_t* v_out, int64_t m,
+                       int bits, char* ws, hipStream_t st) {
+  if (m <= 0) return;
+  const int64_t nb = (m + kChunk - 1) / kChunk;
+  const int64_t hist_n = 256 * nb;
+  uint32_t* k_alt = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up(m * 4);
+  uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up(m * 4);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up(hist_n * 4);
+  uint32_t* hist_scan = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up((hist_n + 1) * 4);
+  const int passes = bits <= 0 ? 0 : (bits + 7) / 8;
+  if (passes == 0) {
+    hipMemcpyAsync(k_out, k, m * 4, hipMemcpyDeviceToDevice, st);
+    hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
+    return;
+  }
+  // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
+  // the last pass lands in (k_out, v_out) and no pass works in place
+  const uint32_t* src_k = k;
+  const uint32_t* src_v = v;
+  for (int p = 0; p < passes; ++p) {
+    const bool to_out = ((passes - 1 - p) % 2) == 0;
+    uint32_t* dst_k = to_out ? k_out : k_alt;
+    uint32_t* dst_v = to_out ? v_out : v_alt;
+    hipLaunchKernelGGL(radix_hist_kernel, dim3(static_cast<unsigned>(nb)), dim3(kSortThreads), 0, st,
+                       src_k, m, 8 * p, hist, static_cast<int>(nb));
+    scan_rec(hist, hist_scan, hist_n, ws, st);
+    hipLaunchKernelGGL(radix_scatter_kernel, dim3(static_cast<unsigned>(nb)), dim3(kSortThreads), 0,
+                       st, src_k, src_v, dst_k, dst_v, m, 8 * p, hist_scan, static_cast<int>(nb));
+    src_k = dst_k;
+    src_v = dst_v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Two-level binning: (1) stable sort of the Gaussians by depth key (culled ones last);
+// (2) emission of (tile, Gaussian) instances in that order; (3) stable sort by tile.
+// The result equals a stable sort of (tile << 32 | depth key) over instances emitted in
+// Gaussian-index order.
+// ---------------------------------------------------------------------------------------
+__global__ void depth_keys_kernel(const SplatRec* __restrict__ rec, const float* __restrict__ depth,
+                                  const uint32_t* __restrict__ counts, int64_t n,
+                                  uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint32_t k = 0xffffffffu;
+  if (counts[i] != 0u) k = rec ? float_order_key(rec[i].b.z) : (depth ? float_order_key(depth[i]) : 0u);
+  keys[i] = k;
+  vals[i] = static_cast<uint32_t>(i);
+}
+
+__global__ void gather_counts_kernel(const uint32_t* __restrict__ order, const uint32_t* __restrict__ counts,
+                                     int64_t n, uint32_t* __restrict__ out) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j < n) out[j] = counts[order[j]];
+}
+
+// 3D: tiles from the row-band rule; 2D: every tile of the rectangle [x0, x1) x [y0, y1).
+template <bool kRect>
+__global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ rec,
+                                                   const int4* __restrict__ rects,
+                                                   const uint32_t* __restrict__ order,
+                                                   const uint32_t* __restrict__ offs, int64_t n,
+                                                   int tiles_x, uint32_t* __restrict__ tkeys,
+                                                   uint32_t* __restrict__ vals) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (j >= n) return;
+  const uint32_t off = offs[j];
+  if (offs[j + 1] == off) return;
+  const uint32_t g = order[j];
+  if constexpr (kRect) {
+    const int4 r = rects[g];
+    uint32_t k = off;
+    for (int ty = r.y; ty < r.w; ++ty)
+      for (int tx = r.x; tx < r.z; ++tx) {
+        tkeys[k] = static_cast<uint32_t>(ty * tiles_x + tx);
+        vals[k] = g;
+        ++k;
+      }
+  } else {
+    const SplatRec r = rec[g];
+    for_each_touched_tile(r.a, r.b, r.d, tiles_x, [&](int tile, int k) {
+      tkeys[off + k] = static_cast<uint32_t>(tile);
+      vals[off + k] = g;
+    });
+  }
+}
+
+__global__ void ranges_kernel(const uint32_t* __restrict__ tkeys, int64_t m, uint32_t* __restrict__ ranges) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= m) return;
-  const uint32_t t = static_cast<uint32_t>(keys[p] >> 32);
-  if (p == 0 || static_cast<uint32_t>(keys[p - 1] >> 32) != t) ranges[2 * t] = static_cast<uint32_t>(p);
-  if (p == m - 1 || static_cast<uint32_t>(keys[p + 1] >> 32) != t)
-    ranges[2 * t + 1] = static_cast<uint32_t>(p + 1);
+  const uint32_t t = tkeys[p];
+  if (p == 0 || tkeys[p - 1] != t) ranges[2 * t] = static_cast<uint32_t>(p);
+  if (p == m - 1 || tkeys[p + 1] != t) ranges[2 * t + 1] = static_cast<uint32_t>(p + 1);
+}
+
+// Full 64-bit keys of the sorted instances (tile << 32 | depth key), for callers that want them.
+__global__ void full_keys_kernel(const uint32_t* __restrict__ tkeys, const uint32_t* __restrict__ vals,
+                                 const uint32_t* __restrict__ dkey_of, int64_t m, uint64_t* __restrict__ out) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p < m) out[p] = (static_cast<uint64_t>(tkeys[p]) << 32) | dkey_of[vals[p]];
 }
 
 __global__ void bucket_count_kernel(const uint32_t* __restrict__ ranges, int n_tiles,
@@ -268,13 +376,88 @@ __global__ void bucket_fill_kernel(const uint32_t* __restrict__ boff, int n_tile
   b2t[b] = static_cast<uint32_t>(lo);
 }
 
-}  // namespace gs
-
-using namespace gs;
+__global__ void rect_counts_kernel(const int4* __restrict__ rects, int64_t n, uint32_t* __restrict__ counts) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 r = rects[i];
+  const int w = r.z - r.x, h = r.w - r.y;
+  counts[i] = (w > 0 && h > 0) ? static_cast<uint32_t>(w * h) : 0u;
+}
 
 static inline unsigned grid_for(int64_t n, int threads) {
   return static_cast<unsigned>((n + threads - 1) / threads);
 }
+
+static int bits_for(int64_t n_values) {
+  int b = 0;
+  while ((int64_t(1) << b) < n_values) ++b;
+  return b;
+}
+
+static size_t bin_ws(int64_t n, int64_t m, int n_tiles) {
+  size_t s = align_up(n * 4) * 6;           // depth keys (in/sorted), identity, order, counts, key copy
+  s += align_up((n + 1) * 4);
+  s += align_up(m * 4) * 2;                 // emitted tile keys and values
+  s += align_up(m * 4);                     // sorted tile keys
+  s += std::max(sort_ws(n), sort_ws(m));    // sort scratch (reused)
+  s += scan_ws(n + 1);
+  s += align_up(static_cast<size_t>(n_tiles) * 4) + scan_ws(n_tiles);
+  return s;
+}
+
+// Shared driver of the 3D and rectangle binnings.
+static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, const uint32_t* counts,
+                    int64_t n, int tiles_x, int n_tiles, int64_t m, uint64_t* sorted_keys,
+                    uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets, char* ws,
+                    hipStream_t st) {
+  uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* dsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* iota = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* order = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* scounts = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* dkey_of = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* soffs = reinterpret_cast<uint32_t*>(ws); ws += align_up((n + 1) * 4);
+  uint32_t* tkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
+  uint32_t* tvals = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
+  uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
+  char* sort_scratch = ws; ws += std::max(sort_ws(n), sort_ws(m));
+  char* scan_scratch = ws; ws += scan_ws(n + 1);
+  uint32_t* bcount = reinterpret_cast<uint32_t*>(ws); ws += align_up(static_cast<size_t>(n_tiles) * 4);
+  char* tile_scratch = ws;
+
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * int64_t(n_tiles), 256)), dim3(256), 0, st,
+                     ranges, 2 * int64_t(n_tiles), 0u);
+  if (m > 0) {
+    const bool by_depth = rec != nullptr || depth != nullptr;
+    hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, counts,
+                       n, dkeys, by_depth ? iota : order);
+    if (sorted_keys) hipMemcpyAsync(dkey_of, dkeys, n * 4, hipMemcpyDeviceToDevice, st);
+    if (by_depth) radix_sort(dkeys, iota, dsorted, order, n, 32, sort_scratch, st);
+    hipLaunchKernelGGL(gather_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, counts, n,
+                       scounts);
+    scan_rec(scounts, soffs, n, scan_scratch, st);
+    if (rects) {
+      hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, rects, order,
+                         soffs, n, tiles_x, tkeys, tvals);
+    } else {
+      hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, rects, order,
+                         soffs, n, tiles_x, tkeys, tvals);
+    }
+    radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
+    hipLaunchKernelGGL(ranges_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, ranges);
+    if (sorted_keys)
+      hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
+                         dkey_of, m, sorted_keys);
+  }
+  hipLaunchKernelGGL(bucket_count_kernel, dim3(grid_for(n_tiles, 256)), dim3(256), 0, st, ranges,
+                     n_tiles, bcount);
+  scan_rec(bcount, bucket_offsets, n_tiles, tile_scratch, st);
+  return GS_OK;
+}
+
+}  // namespace gs
+
+using namespace gs;
 
 extern "C" size_t gs_scan_workspace_size(int64_t n) { return scan_ws(n < 0 ? 0 : n); }
 
@@ -294,29 +477,15 @@ extern "C" int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* w
   return check_launch("scan");
 }
 
-static int tile_bits(int n_tiles) {
-  int b = 0;
-  while ((1 << b) < n_tiles) ++b;
-  return b;
+extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles) {
+  if (n < 0 || m < 0 || n_tiles <= 0) return 0;
+  return bin_ws(n, m, n_tiles);
 }
 
-static int sort_passes(int n_tiles) { return (32 + tile_bits(n_tiles) + 7) / 8; }
-
-extern "C" size_t gs_bin_workspace_size(int64_t m, int n_tiles) {
-  if (m < 0 || n_tiles <= 0) return 0;
-  const int64_t nb = (m + kSortTile - 1) / kSortTile;
-  const int64_t hist = 256 * (nb > 0 ? nb : 1);
-  size_t s = align_up(m * 8) + align_up(m * 4);  // ping-pong keys and values
-  s += align_up(hist * 4) + align_up((hist + 1) * 4) + scan_ws(hist);
-  s += align_up(static_cast<size_t>(n_tiles) * 4) + scan_ws(n_tiles);
-  return s;
-}
-
-extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched,
-                              const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
-                              uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
-                              uint32_t* bucket_offsets, void* workspace, size_t workspace_bytes,
-                              void* stream) {
+extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, int64_t n,
+                              const gs_camera* cam, int64_t m, uint64_t* sorted_keys,
+                              uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (int e = check_cam(cam)) return e;
   GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32), GS_ERR_ARG, "invalid sizes n=%lld m=%lld",
@@ -324,59 +493,44 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touc
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const CamK k = make_cam(*cam);
   const int n_tiles = k.tiles_x * k.tiles_y;
-  const size_t need = gs_bin_workspace_size(m, n_tiles);
+  const size_t need = bin_ws(n, m, n_tiles);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
-  GS_REQUIRE(m == 0 || (splat_rec && tiles_touched && offsets && sorted_keys && point_list),
-             GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(m == 0 || (splat_rec && tiles_touched && point_list), GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
-  hipStream_t st = as_stream(stream);
-  char* ws = static_cast<char*>(workspace);
-  uint64_t* k_alt = reinterpret_cast<uint64_t*>(ws);
-  ws += align_up(m * 8);
-  uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(m * 4);
-  const int64_t nb = (m + kSortTile - 1) / kSortTile;
-  const int64_t hist_n = 256 * (nb > 0 ? nb : 1);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(hist_n * 4);
-  uint32_t* hist_scan = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up((hist_n + 1) * 4);
-  char* hist_ws = ws;
-  ws += scan_ws(hist_n);
-  uint32_t* bcount = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(static_cast<size_t>(n_tiles) * 4);
-  char* tile_ws = ws;
-
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * int64_t(n_tiles), 256)), dim3(256), 0, st,
-                     ranges, 2 * int64_t(n_tiles), 0u);
-  if (m > 0) {
-    const int passes = sort_passes(n_tiles);
-    // emit into the buffer that ends up holding the result after `passes` ping-pongs
-    uint64_t* k0 = (passes % 2 == 0) ? sorted_keys : k_alt;
-    uint32_t* v0 = (passes % 2 == 0) ? point_list : v_alt;
-    uint64_t* k1 = (passes % 2 == 0) ? k_alt : sorted_keys;
-    uint32_t* v1 = (passes % 2 == 0) ? v_alt : point_list;
-    hipLaunchKernelGGL(emit_instances_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st,
-                       reinterpret_cast<const SplatRec*>(splat_rec), tiles_touched, offsets, n,
-                       k.tiles_x, k0, v0);
-    for (int p = 0; p < passes; ++p) {
-      const int shift = 8 * p;
-      hipLaunchKernelGGL(radix_hist_kernel, dim3(static_cast<unsigned>(nb)), dim3(kSortThreads), 0,
-                         st, k0, m, shift, hist, static_cast<int>(nb));
-      scan_rec(hist, hist_scan, hist_n, hist_ws, st);
-      hipLaunchKernelGGL(radix_scatter_kernel, dim3(static_cast<unsigned>(nb)), dim3(kSortThreads),
-                         0, st, k0, v0, k1, v1, m, shift, hist_scan, static_cast<int>(nb));
-      std::swap(k0, k1);
-      std::swap(v0, v1);
-    }
-    hipLaunchKernelGGL(ranges_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, sorted_keys, m,
-                       ranges);
-  }
-  hipLaunchKernelGGL(bucket_count_kernel, dim3(grid_for(n_tiles, 256)), dim3(256), 0, st, ranges,
-                     n_tiles, bcount);
-  scan_rec(bcount, bucket_offsets, n_tiles, tile_ws, st);
+  bin_fill(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, tiles_touched, n, k.tiles_x,
+           n_tiles, m, sorted_keys, point_list, ranges, bucket_offsets, static_cast<char*>(workspace),
+           as_stream(stream));
   return check_launch("bin_fill_3d");
+}
+
+extern "C" int gs_rect_counts(const int32_t* rects, int64_t n, uint32_t* counts, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0 && (n == 0 || (rects && counts)), GS_ERR_ARG, "invalid rect_counts arguments");
+  GS_REQUIRE(aligned(rects, 16), GS_ERR_ALIGN, "rects must be 16-byte aligned");
+  if (n == 0) return GS_OK;
+  hipLaunchKernelGGL(rect_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const int4*>(rects), n, counts);
+  return check_launch("rect_counts");
+}
+
+extern "C" int gs_bin_fill_rect(const int32_t* rects, const float* depth, const uint32_t* counts,
+                                int64_t n, int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
+                                uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32) && tiles_x > 0 && tiles_y > 0, GS_ERR_ARG,
+             "invalid sizes");
+  GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
+  const int n_tiles = tiles_x * tiles_y;
+  const size_t need = bin_ws(n, m, n_tiles);
+  GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
+             "binning workspace too small: need %zu bytes", need);
+  GS_REQUIRE(m == 0 || (rects && counts && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(aligned(rects, 16), GS_ERR_ALIGN, "rects must be 16-byte aligned");
+  bin_fill(nullptr, reinterpret_cast<const int4*>(rects), depth, counts, n, tiles_x, n_tiles, m,
+           sorted_keys, point_list, ranges, bucket_offsets, static_cast<char*>(workspace), as_stream(stream));
+  return check_launch("bin_fill_rect");
 }
 
 extern "C" int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket_to_tile,

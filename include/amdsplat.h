@@ -80,22 +80,35 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
 
 /* ---------------------------------------------------------------------------------------
  * 3D binning (replaces create_instances_cu, the two cub Onesweep sorts,
- * extract_instance_ranges_cu and extract_bucket_counts; §3C of the call stack in
+ * extract_instance_ranges_cu and extract_bucket_counts; the call sequence is visible in
  * results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:10-31).
- * offsets = exclusive scan of tiles_touched (n + 1 values), m = offsets[n].
- * Emits key (tile << 32 | orderable depth bits) and value (Gaussian index) per instance
- * in Gaussian-index order, sorts them with a stable LSD radix sort, and writes
+ * m = sum of tiles_touched (the caller reads it, e.g. from gs_scan_u32's out[n]).
+ * Produces the stable order of instances by (tile, depth, Gaussian index) -- the order of a
+ * stable sort of 64-bit keys (tile << 32 | orderable depth bits) over instances emitted in
+ * Gaussian-index order -- with two stable LSD radix sorts: the Gaussians by depth, then the
+ * instances (emitted in depth order) by tile. Writes
  *   point_list [m]        Gaussian index per instance, tile-major, front to back
- *   sorted_keys [m]       the sorted 64-bit keys
+ *   sorted_keys [m]       the 64-bit keys in that order (may be NULL: not needed downstream)
  *   ranges [T,2]          [start, end) of each tile in point_list
  *   bucket_offsets [T+1]  exclusive scan of ceil(len/32); bucket_offsets[T] = number of buckets
- * Workspace from gs_bin_workspace_size(m, T).
+ * Workspace from gs_bin_workspace_size(n, m, T).
  * ------------------------------------------------------------------------------------- */
-size_t gs_bin_workspace_size(int64_t m, int n_tiles);
-int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, const uint32_t* offsets,
-                   int64_t n, const gs_camera* cam, int64_t m, uint64_t* sorted_keys,
-                   uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
-                   void* workspace, size_t workspace_bytes, void* stream);
+size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles);
+int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, int64_t n,
+                   const gs_camera* cam, int64_t m, uint64_t* sorted_keys, uint32_t* point_list,
+                   uint32_t* ranges, uint32_t* bucket_offsets, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Rectangle binning for the 2D operators (replaces toy2d/gs2d/binning.py:34-88, whose
+ * per-tile lists are ordered by a stable depth rank, and phase0/splat2d/ops.py:206-255, whose
+ * lists are in index order). rects [n,4] int32 = (tx0, ty0, tx1, ty1) tile rectangle, max
+ * exclusive, 16-byte aligned; depth [n] (NULL = index order). counts from gs_rect_counts.
+ * Outputs as gs_bin_fill_3d; the depth key is the orderable image of the float depth. */
+int gs_rect_counts(const int32_t* rects, int64_t n, uint32_t* counts, void* stream);
+int gs_bin_fill_rect(const int32_t* rects, const float* depth, const uint32_t* counts, int64_t n,
+                     int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
+                     uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* bucket_to_tile[b] = tile of bucket b, for b < bucket_offsets[n_tiles] (read on device);
  * entries up to n_buckets_max are written, unused ones with 0xffffffff. */

@@ -38,7 +38,7 @@ def make(name, seed=0, sh_coeffs=16):
 def gpu_forward(scene, sh_degree, bg=BG):
     cam = scene.cameras[0]
     p = [t.cuda().contiguous() for t in scene.params()]
-    fs = R.forward_pass(*p, cam, sh_degree=sh_degree, bg=bg)
+    fs = R.forward_pass(*p, cam, sh_degree=sh_degree, bg=bg, keep_keys=True)
     torch.cuda.synchronize()
     return p, fs
 
@@ -219,7 +219,7 @@ def test_full_size_1m_sampled_tiles():
     sc = scenes.sh3_1m()
     cam = sc.cameras[0]
     p = [t.cuda().contiguous() for t in sc.params()]
-    fs = R.forward_pass(*p, cam, sh_degree=3)
+    fs = R.forward_pass(*p, cam, sh_degree=3, keep_keys=True)
     torch.cuda.synchronize()
     keys = np_(fs.keys).view(np.uint64)
     assert np.all(keys[1:] >= keys[:-1]), "keys not sorted"
@@ -246,3 +246,18 @@ def test_full_size_1m_sampled_tiles():
         ys, xs = slice(ty * 16, min(ty * 16 + 16, cam.height)), slice(tx * 16, min(tx * 16 + 16, cam.width))
         assert np.abs(np_(fs.image)[:, ys, xs] - img[:, ys, xs]).max() <= FWD_TOL
         assert np.array_equal(np_(fs.n_contrib)[ys, xs], nc[ys, xs])
+
+
+def test_equal_depths_keep_index_order():
+    """All Gaussians at one depth: every tile list must be in Gaussian-index order (ties of the
+    depth sort stay in input order, phase2/tests/test_readback_equiv.py:57-59)."""
+    sc = make("partial_tiles", seed=11)
+    sc.means[:, 2] = 4.0
+    cam = sc.cameras[0]
+    p, fs = gpu_forward(sc, 3)
+    ref = O.render(*[t.numpy() for t in sc.params()], cam, 3, bg=BG)
+    pl = np_(fs.point_list).view(np.uint32)
+    assert np.array_equal(pl, ref["point_list"])
+    rng = np_(fs.ranges)
+    for s, e in rng:
+        assert np.all(np.diff(pl[s:e].astype(np.int64)) > 0)
