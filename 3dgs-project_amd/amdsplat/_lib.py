@@ -46,7 +46,7 @@ _SIGS = {
     "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp]),
     "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32]),
     "gs_bin_fill_3d": (_i32, [_vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "gs_rect_counts": (_i32, [_vp, _i64, _vp, _vp]),
+    "gs_rect_counts": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
     "gs_bin_fill_rect": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),

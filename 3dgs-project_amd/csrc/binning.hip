@@ -259,8 +259,8 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
   ws += align_up((hist_n + 1) * 4);
   const int passes = bits <= 0 ? 0 : (bits + 7) / 8;
   if (passes == 0) {
-    hipMemcpyAsync(k_out, k, m * 4, hipMemcpyDeviceToDevice, st);
-    hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
+    (void)hipMemcpyAsync(k_out, k, m * 4, hipMemcpyDeviceToDevice, st);
+    (void)hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
     return;
   }
   // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
@@ -304,33 +304,47 @@ __global__ void gather_counts_kernel(const uint32_t* __restrict__ order, const u
   if (j < n) out[j] = counts[order[j]];
 }
 
+// Tile rectangle (tx0, ty0, tx1, ty1), max exclusive, clipped to the tile grid.
+__device__ __forceinline__ int4 clamp_rect(int4 r, int tiles_x, int tiles_y) {
+  r.x = max(r.x, 0);
+  r.y = max(r.y, 0);
+  r.z = min(r.z, tiles_x);
+  r.w = min(r.w, tiles_y);
+  return r;
+}
+
 // 3D: tiles from the row-band rule; 2D: every tile of the rectangle [x0, x1) x [y0, y1).
 template <bool kRect>
 __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ rec,
                                                    const int4* __restrict__ rects,
                                                    const uint32_t* __restrict__ order,
                                                    const uint32_t* __restrict__ offs, int64_t n,
-                                                   int tiles_x, uint32_t* __restrict__ tkeys,
+                                                   int tiles_x, int tiles_y, uint32_t* __restrict__ tkeys,
                                                    uint32_t* __restrict__ vals) {
   const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (j >= n) return;
   const uint32_t off = offs[j];
-  if (offs[j + 1] == off) return;
+  const uint32_t cap = offs[j + 1] - off;  // never write past this Gaussian's slots
+  if (cap == 0) return;
   const uint32_t g = order[j];
   if constexpr (kRect) {
-    const int4 r = rects[g];
-    uint32_t k = off;
+    const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
+    uint32_t k = 0;
     for (int ty = r.y; ty < r.w; ++ty)
       for (int tx = r.x; tx < r.z; ++tx) {
-        tkeys[k] = static_cast<uint32_t>(ty * tiles_x + tx);
-        vals[k] = g;
+        if (k < cap) {
+          tkeys[off + k] = static_cast<uint32_t>(ty * tiles_x + tx);
+          vals[off + k] = g;
+        }
         ++k;
       }
   } else {
     const SplatRec r = rec[g];
     for_each_touched_tile(r.a, r.b, r.d, tiles_x, [&](int tile, int k) {
-      tkeys[off + k] = static_cast<uint32_t>(tile);
-      vals[off + k] = g;
+      if (static_cast<uint32_t>(k) < cap) {
+        tkeys[off + k] = static_cast<uint32_t>(tile);
+        vals[off + k] = g;
+      }
     });
   }
 }
@@ -376,10 +390,11 @@ __global__ void bucket_fill_kernel(const uint32_t* __restrict__ boff, int n_tile
   b2t[b] = static_cast<uint32_t>(lo);
 }
 
-__global__ void rect_counts_kernel(const int4* __restrict__ rects, int64_t n, uint32_t* __restrict__ counts) {
+__global__ void rect_counts_kernel(const int4* __restrict__ rects, int64_t n, int tiles_x, int tiles_y,
+                                   uint32_t* __restrict__ counts) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const int4 r = rects[i];
+  const int4 r = clamp_rect(rects[i], tiles_x, tiles_y);
   const int w = r.z - r.x, h = r.w - r.y;
   counts[i] = (w > 0 && h > 0) ? static_cast<uint32_t>(w * h) : 0u;
 }
@@ -431,17 +446,17 @@ static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, 
     const bool by_depth = rec != nullptr || depth != nullptr;
     hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, counts,
                        n, dkeys, by_depth ? iota : order);
-    if (sorted_keys) hipMemcpyAsync(dkey_of, dkeys, n * 4, hipMemcpyDeviceToDevice, st);
+    if (sorted_keys) (void)hipMemcpyAsync(dkey_of, dkeys, n * 4, hipMemcpyDeviceToDevice, st);
     if (by_depth) radix_sort(dkeys, iota, dsorted, order, n, 32, sort_scratch, st);
     hipLaunchKernelGGL(gather_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, counts, n,
                        scounts);
     scan_rec(scounts, soffs, n, scan_scratch, st);
     if (rects) {
       hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, rects, order,
-                         soffs, n, tiles_x, tkeys, tvals);
+                         soffs, n, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     } else {
       hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, rects, order,
-                         soffs, n, tiles_x, tkeys, tvals);
+                         soffs, n, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     }
     radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
     hipLaunchKernelGGL(ranges_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, ranges);
@@ -504,13 +519,15 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touc
   return check_launch("bin_fill_3d");
 }
 
-extern "C" int gs_rect_counts(const int32_t* rects, int64_t n, uint32_t* counts, void* stream) {
+extern "C" int gs_rect_counts(const int32_t* rects, int64_t n, int tiles_x, int tiles_y, uint32_t* counts,
+                              void* stream) {
   clear_error();
-  GS_REQUIRE(n >= 0 && (n == 0 || (rects && counts)), GS_ERR_ARG, "invalid rect_counts arguments");
+  GS_REQUIRE(n >= 0 && (n == 0 || (rects && counts)) && tiles_x > 0 && tiles_y > 0, GS_ERR_ARG,
+             "invalid rect_counts arguments");
   GS_REQUIRE(aligned(rects, 16), GS_ERR_ALIGN, "rects must be 16-byte aligned");
   if (n == 0) return GS_OK;
   hipLaunchKernelGGL(rect_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream),
-                     reinterpret_cast<const int4*>(rects), n, counts);
+                     reinterpret_cast<const int4*>(rects), n, tiles_x, tiles_y, counts);
   return check_launch("rect_counts");
 }
 

@@ -104,7 +104,8 @@ int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, int64_
  * lists are in index order). rects [n,4] int32 = (tx0, ty0, tx1, ty1) tile rectangle, max
  * exclusive, 16-byte aligned; depth [n] (NULL = index order). counts from gs_rect_counts.
  * Outputs as gs_bin_fill_3d; the depth key is the orderable image of the float depth. */
-int gs_rect_counts(const int32_t* rects, int64_t n, uint32_t* counts, void* stream);
+int gs_rect_counts(const int32_t* rects, int64_t n, int tiles_x, int tiles_y, uint32_t* counts,
+                   void* stream);
 int gs_bin_fill_rect(const int32_t* rects, const float* depth, const uint32_t* counts, int64_t n,
                      int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
                      uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,

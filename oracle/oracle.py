@@ -163,3 +163,15 @@ def contrib_mask(rec, point_list, ranges, width, height, n_contrib):
                           _p(np.ascontiguousarray(point_list, np.uint32)), C.c_int(width), C.c_int(height),
                           _p(np.ascontiguousarray(n_contrib, np.int32)), _p(mask))
     return mask[:m]
+
+
+def sh_basis(dirs, n):
+    """Real SH basis values [len(dirs), n] of unit directions (float32 oracle routine)."""
+    d = f32(dirs).reshape(-1, 3)
+    out = np.zeros((d.shape[0], 16), np.float32)
+    fn = lib().or_sh_basis
+    buf = (C.c_float * 16)()
+    for i, (x, y, z) in enumerate(d):
+        fn(C.c_float(x), C.c_float(y), C.c_float(z), C.c_int(n), buf)
+        out[i, :n] = np.frombuffer(buf, np.float32, n)
+    return out[:, :n]

@@ -1,0 +1,399 @@
+"""CPU checks that pin the 3D oracle (no GPU): the C restatement against closed forms,
+quadrature identities, a float64 autograd restatement and brute force on tiny inputs, plus
+the C ABI library's exported symbols.
+
+Each check is chosen so that a plausible slip in the oracle (a dropped term, a wrong sign
+or index, a transposed operand) fails it:
+  - elementary functions against float64 math at a dense grid of points;
+  - the SH basis against orthonormality on the sphere (constants, polynomial forms) and
+    against the unit-sphere forms of the reference's SH backward
+    (phase2/sh_coalesce.patch:102-149, signs and band layout);
+  - the projection against closed forms (on-axis isotropic Gaussian, off-axis mean);
+  - the hand-derived backwards (blend replay, preprocess chain rule) against float64
+    autograd of dense3d, whose forward is itself checked against the oracle;
+  - the tiled forward against a brute-force dense render over all Gaussians (binning
+    completeness + blend rules), and the binning against its invariants
+    (toy2d/tests/test_cpu.py:10-21: complete lists, depth order, bucket count).
+"""
+import math
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import dense3d as D
+import oracle as O
+from amdsplat import scenes
+
+ROOT = Path(__file__).resolve().parent.parent
+BG = (0.2, 0.5, 0.8)
+
+
+def small(n=400, W=96, H=72, seed=0, **kw):
+    return scenes.small_scene(n, W, H, seed=seed, **kw)
+
+
+def np_params(sc):
+    return [t.numpy() for t in sc.params()]
+
+
+# ---------------------------------------------------------------------------------------
+# C ABI library
+# ---------------------------------------------------------------------------------------
+def header_functions():
+    text = (ROOT / "include" / "amdsplat.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gs\w*)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import ctypes
+
+    from amdsplat import _lib
+
+    L = ctypes.CDLL(str(_lib.LIB_PATH))
+    names = header_functions()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"declared in include/amdsplat.h but not exported: {missing}"
+    # every declared entry point has a ctypes signature in the binding
+    assert not [n for n in names if n not in _lib._SIGS]
+
+
+# ---------------------------------------------------------------------------------------
+# Elementary functions
+# ---------------------------------------------------------------------------------------
+def test_exp2_polynomial_within_one_ulp():
+    xs = np.linspace(-64.0, 0.0, 20001, dtype=np.float32)
+    got = np.array([O.exp2_neg(float(x)) for x in xs], np.float64)
+    ref = np.exp2(xs.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert np.max(np.abs(got - ref) / ulp) <= 1.0
+    assert O.exp2_neg(0.0) == 1.0 and O.exp2_neg(-1.0) == 0.5
+
+
+def test_log_and_sigmoid_accuracy():
+    xs = np.exp(np.linspace(-20, 20, 4001)).astype(np.float32)
+    got = np.array([O.log_pos(float(x)) for x in xs], np.float64)
+    ref = np.log(xs.astype(np.float64))
+    assert np.max(np.abs(got - ref) / np.maximum(1.0, np.abs(ref))) < 4e-7
+    zs = np.linspace(-30, 30, 2001, dtype=np.float32)
+    got = np.array([O.sigmoid(float(z)) for z in zs], np.float64)
+    ref = 1.0 / (1.0 + np.exp(-zs.astype(np.float64)))
+    # exp(z) is evaluated as 2^(z log2 e): the rounding of the product costs ~|z| 2^-24 relative
+    assert np.max(np.abs(got - ref) / ref / np.maximum(1.0, np.abs(zs))) < 1e-7
+
+
+# ---------------------------------------------------------------------------------------
+# Spherical harmonics
+# ---------------------------------------------------------------------------------------
+def sphere_quadrature(n_theta=12, n_phi=24):
+    """Gauss-Legendre in cos(theta) x uniform phi: exact for polynomials of degree < 2*n_theta."""
+    zt, wt = np.polynomial.legendre.leggauss(n_theta)
+    phi = 2 * np.pi * np.arange(n_phi) / n_phi
+    Z, P = np.meshgrid(zt, phi, indexing="ij")
+    r = np.sqrt(1 - Z * Z)
+    dirs = np.stack([r * np.cos(P), r * np.sin(P), Z], -1).reshape(-1, 3)
+    w = (wt[:, None] * np.full(n_phi, 2 * np.pi / n_phi)[None, :]).reshape(-1)
+    return dirs, w
+
+
+def test_sh_basis_is_orthonormal():
+    dirs, w = sphere_quadrature()
+    B = O.sh_basis(dirs, 16).astype(np.float64)
+    gram = (B * w[:, None]).T @ B
+    assert np.abs(gram - np.eye(16)).max() < 2e-6
+
+
+def test_sh_basis_matches_reference_unit_sphere_forms():
+    """phase2/sh_coalesce.patch:105-149 writes bands 2-3 in forms reduced with x^2+y^2+z^2=1
+    (e.g. C2b zz - C2c, y (C3d - C3e zz)); the constants follow from the normalisation."""
+    K = D.sh_norm_constant
+    c1 = K(1, 0)
+    rng = np.random.default_rng(0)
+    d = rng.standard_normal((500, 3))
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    x, y, z = d.T
+    xx, yy, zz = x * x, y * y, z * z
+    # constant names of the reference: C2a = 6 K22, C2b = 1.5 K20, C2c = 0.5 K20, C2d = 3 K22,
+    # C3a = 15 K33, C3b = 45 K33, C3c = 30 K32, C3d = 1.5 K31, C3e = 7.5 K31, C3f = 2.5 K30,
+    # C3g = 1.5 K30, C3h = 15 K32 (associated-Legendre factors times the normalisation)
+    ref = np.stack([
+        np.full_like(x, K(0, 0)), -c1 * y, c1 * z, -c1 * x,
+        6 * K(2, 2) * x * y, -3 * K(2, 1) * y * z, 1.5 * K(2, 0) * zz - 0.5 * K(2, 0),
+        -3 * K(2, 1) * x * z, 3 * K(2, 2) * (xx - yy),
+        y * (15 * K(3, 3) * yy - 45 * K(3, 3) * xx),
+        30 * K(3, 2) * x * y * z,
+        y * (1.5 * K(3, 1) - 7.5 * K(3, 1) * zz),
+        z * (2.5 * K(3, 0) * zz - 1.5 * K(3, 0)),
+        x * (1.5 * K(3, 1) - 7.5 * K(3, 1) * zz),
+        15 * K(3, 2) * z * (xx - yy),
+        x * (45 * K(3, 3) * yy - 15 * K(3, 3) * xx),
+    ], -1)
+    got = O.sh_basis(d, 16).astype(np.float64)
+    assert np.abs(got - ref).max() < 3e-6
+
+
+# ---------------------------------------------------------------------------------------
+# Projection
+# ---------------------------------------------------------------------------------------
+def one_gaussian(p, log_s, q=(1.0, 0.0, 0.0, 0.0), logit=2.0, sh0=(0.3, -0.2, 0.1)):
+    means = np.array([p], np.float32)
+    ls = np.full((1, 3), log_s, np.float32)
+    quats = np.array([q], np.float32)
+    op = np.array([logit], np.float32)
+    sh = np.zeros((1, 16, 3), np.float32)
+    sh[0, 0] = sh0
+    return means, ls, quats, op, sh
+
+
+def test_preprocess_on_axis_isotropic_closed_form():
+    cam = scenes.Camera(torch.eye(4), 500.0, 500.0, 64.3, 47.8, 128, 96, 0.2, 100.0)
+    z, s = 4.0, 0.05
+    rec, touched = O.preprocess_fwd(*one_gaussian((0.0, 0.0, z), math.log(s)), cam, 0)
+    assert touched[0] > 0
+    r = rec[0]
+    assert r[0] == np.float32(64.3) and r[1] == np.float32(47.8)  # mean2d = principal point
+    a = (500.0 * s / z) ** 2 + 0.3  # cov2d = (f s / z)^2 I + dilation
+    np.testing.assert_allclose(r[2], 1.0 / a, rtol=2e-6)
+    assert abs(r[3]) < 1e-9
+    np.testing.assert_allclose(r[4], 1.0 / a, rtol=2e-6)
+    np.testing.assert_allclose(r[5], 1.0 / (1.0 + math.exp(-2.0)), rtol=1e-6)
+    assert r[6] == np.float32(z)
+    np.testing.assert_allclose(r[7], math.log(255.0 / (1.0 + math.exp(-2.0))), rtol=1e-6)
+    # SH degree 0: colour = C0 sh0 + 0.5, clamped at 0 with the mask bit set
+    np.testing.assert_allclose(r[8:11], np.maximum(D.SH0 * np.array([0.3, -0.2, 0.1]) + 0.5, 0), rtol=1e-6)
+    # the pixel bounds are the alpha >= 1/255 extent: sqrt(2 ln(255 o) a)
+    ext = math.sqrt(2 * r[7] * a)
+    b = r[12:16].view(np.int32)
+    assert b[0] == math.ceil(64.3 - ext - 0.5) and b[1] == math.floor(64.3 + ext - 0.5)
+
+
+def test_preprocess_off_axis_mean_and_rotation_invariance():
+    cam = scenes.Camera(torch.eye(4), 400.0, 300.0, 50.0, 40.0, 100, 80, 0.2, 100.0)
+    p = (0.3, -0.2, 5.0)
+    q = np.array([0.3, -0.5, 0.7, 0.1])
+    r1, _ = O.preprocess_fwd(*one_gaussian(p, math.log(0.02), tuple(q)), cam, 3)
+    np.testing.assert_allclose(r1[0, :2], [400.0 * 0.3 / 5.0 + 50.0, 300.0 * -0.2 / 5.0 + 40.0], rtol=1e-6)
+    # an isotropic Gaussian's covariance does not depend on its rotation, nor on |q|
+    r2, _ = O.preprocess_fwd(*one_gaussian(p, math.log(0.02), tuple(3.7 * q)), cam, 3)
+    r3, _ = O.preprocess_fwd(*one_gaussian(p, math.log(0.02)), cam, 3)
+    np.testing.assert_allclose(r1[0, 2:5], r3[0, 2:5], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(r1[0, 2:5], r2[0, 2:5], rtol=1e-5, atol=1e-6)
+
+
+def test_preprocess_culls_behind_and_far():
+    cam = scenes.Camera(torch.eye(4), 400.0, 400.0, 50.0, 40.0, 100, 80, 0.2, 10.0)
+    for z in (-1.0, 0.1, 12.0):
+        _, touched = O.preprocess_fwd(*one_gaussian((0.0, 0.0, z), math.log(0.05)), cam, 0)
+        assert touched[0] == 0
+
+
+def test_preprocess_matches_float64_restatement():
+    sc = small(seed=3)
+    cam = sc.cameras[0]
+    rec, touched = O.preprocess_fwd(*np_params(sc), cam, 3)
+    vis = touched > 0
+    assert vis.sum() > 50
+    P = [t.double() for t in sc.params()]
+    pre = D.preprocess64(*P, cam, 3)
+    np.testing.assert_allclose(rec[vis, 0:2], pre["mean2d"][vis].numpy(), rtol=1e-5, atol=1e-4)
+    conic = pre["conic"][vis].numpy()
+    scale = np.abs(conic).max(1, keepdims=True)
+    assert np.abs(rec[vis, 2:5] - conic).max() / 1 <= 1e-4 * scale.max()
+    np.testing.assert_allclose(rec[vis, 8:11], pre["color"][vis].numpy(), atol=2e-6)
+
+
+# ---------------------------------------------------------------------------------------
+# Binning
+# ---------------------------------------------------------------------------------------
+def band_touch_f64(r, tx, ty, tiles_x, margin):
+    """Whether the alpha >= 1/255 ellipse of record r reaches a pixel centre column of tile
+    (tx, ty) at some y of the tile's rows (both clipped to r's pixel bounds), in float64.
+    Returns True / False, or None within `margin` px of the boundary."""
+    mx, my, A, B, C, thr = (float(v) for v in (r[0], r[1], r[2], r[3], r[4], r[7]))
+    x0, x1, y0, y1 = (int(v) for v in r[12:16].view(np.int32))
+    cx0, cx1 = max(tx * 16, x0), min(tx * 16 + 15, x1)
+    Y0, Y1 = max(ty * 16, y0) + 0.5, min(ty * 16 + 15, y1) + 0.5
+    if cx0 > cx1 or Y0 > Y1:
+        return False
+    best = -np.inf
+    for c in range(cx0, cx1 + 1):
+        u = c + 0.5 - mx
+        # max over y in [Y0, Y1] of thr - 0.5 (A u^2 + 2 B u v + C v^2), v = y - my
+        v_star = np.clip(-B * u / C, Y0 - my, Y1 - my)
+        val = thr - 0.5 * (A * u * u + 2 * B * u * v_star + C * v_star * v_star)
+        best = max(best, val)
+    if abs(best) < margin:
+        return None
+    return best >= 0
+
+
+def test_binning_lists_complete_sorted_and_bucketed():
+    sc = small(n=600, seed=5)
+    cam = sc.cameras[0]
+    rec, touched = O.preprocess_fwd(*np_params(sc), cam, 3)
+    keys, pl, ranges, boff = O.bin_instances(rec, touched, cam)
+    tiles_x, T = cam.tiles_x, cam.n_tiles
+    assert int((ranges[:, 1] - ranges[:, 0]).sum()) == len(pl) == int(touched.sum())
+    assert np.all(keys[1:] >= keys[:-1])
+    assert np.array_equal(np.diff(boff), (ranges[:, 1] - ranges[:, 0] + 31) // 32)
+    depth = rec[:, 6]
+    undecided = 0
+    for t in range(T):
+        s, e = ranges[t]
+        lst = pl[s:e].astype(np.int64)
+        assert np.all(keys[s:e] >> np.uint64(32) == t)
+        # front to back, ties in index order
+        dl = depth[lst]
+        assert np.all((dl[1:] > dl[:-1]) | ((dl[1:] == dl[:-1]) & (lst[1:] > lst[:-1])))
+        members = set(lst.tolist())
+        tx, ty = t % tiles_x, t // tiles_x
+        for g in np.nonzero(touched)[0]:
+            want = band_touch_f64(rec[g], tx, ty, tiles_x, 1e-3)
+            if want is None:
+                undecided += 1
+                continue
+            assert want == (g in members), f"tile {t}, Gaussian {g}: expected {want}"
+    assert undecided < 20
+
+
+def test_binning_counts_match_emitted_tiles():
+    sc = small(n=300, seed=6, scale=(0.02, 0.3))
+    cam = sc.cameras[0]
+    rec, touched = O.preprocess_fwd(*np_params(sc), cam, 3)
+    keys, pl, ranges, boff = O.bin_instances(rec, touched, cam)
+    per_g = np.bincount(pl, minlength=sc.n)
+    assert np.array_equal(per_g, touched.astype(np.int64))
+
+
+# ---------------------------------------------------------------------------------------
+# Blending
+# ---------------------------------------------------------------------------------------
+def brute_force_render(rec, touched, W, H, bg):
+    """All visible Gaussians at every pixel, depth order (ties by index), float64, with the
+    forward's rules (G = exp(min(power, 0)), alpha = o G >= 1/255, stop once T < 1e-4)."""
+    vis = np.nonzero(touched)[0]
+    order = vis[np.lexsort((vis, rec[vis, 6]))]
+    ys, xs = np.mgrid[0:H, 0:W]
+    px, py = xs.reshape(-1) + 0.5, ys.reshape(-1) + 0.5
+    T = np.ones(px.shape)
+    C = np.zeros((px.size, 3))
+    done = np.zeros(px.shape, bool)
+    for g in order:
+        r = rec[g].astype(np.float64)
+        b = rec[g, 12:16].view(np.int32)
+        dx, dy = r[0] - px, r[1] - py
+        power = np.minimum(-0.5 * (r[2] * dx * dx + 2 * r[3] * dx * dy + r[4] * dy * dy), 0.0)
+        alpha = r[5] * np.exp(power)
+        inb = (xs.reshape(-1) >= b[0]) & (xs.reshape(-1) <= b[1]) & (ys.reshape(-1) >= b[2]) & (ys.reshape(-1) <= b[3])
+        ok = inb & (alpha >= 1 / 255) & ~done
+        a = np.where(ok, alpha, 0.0)
+        C += (a * T)[:, None] * r[8:11][None, :]
+        T = T * (1 - a)
+        done |= T < 1e-4
+    img = C + T[:, None] * np.asarray(bg)[None, :]
+    return img.T.reshape(3, H, W), T.reshape(H, W)
+
+
+def test_tiled_forward_equals_brute_force_over_all_gaussians():
+    sc = small(n=500, seed=7)
+    cam = sc.cameras[0]
+    ref = O.render(*np_params(sc), cam, 3, bg=BG)
+    img, fT = brute_force_render(ref["rec"], ref["touched"], cam.width, cam.height, BG)
+    diff = np.abs(ref["image"] - img).max(0)
+    # decisions at the alpha / T thresholds may differ between float32 and float64 on a
+    # handful of pixels; everywhere else the images agree to float32 rounding
+    assert (diff > 1e-5).mean() < 2e-3
+    assert np.median(diff) < 1e-6
+
+
+def test_termination_rule_and_checkpoints():
+    sc = small(n=800, seed=8, opacity=(0.6, 0.99), scale=(0.05, 0.3))
+    cam = sc.cameras[0]
+    ref = O.render(*np_params(sc), cam, 3, bg=BG)
+    fT, nc = ref["final_T"], ref["n_contrib"]
+    assert (fT < 1e-4).any(), "scene must reach early termination"
+    # a terminated pixel stops right after the splat that took T below 1e-4
+    assert np.all(fT[fT < 1e-4] > 0)
+    # checkpoints: T is non-increasing over a pixel's buckets and starts at 1
+    ck = ref["ckpt"]
+    boff = ref["bucket_offsets"]
+    for tile in range(len(boff) - 1):
+        b0, b1 = int(boff[tile]), int(boff[tile + 1])
+        if b1 > b0:
+            assert np.all(ck[b0, :, 3] == 1.0)
+            assert np.all(np.diff(ck[b0:b1, :, 3], axis=0) <= 0)
+
+
+def test_blend_forward_matches_dense_float64():
+    sc = small(n=400, seed=9)
+    cam = sc.cameras[0]
+    ref = O.render(*np_params(sc), cam, 3, bg=BG)
+    mask = O.contrib_mask(ref["rec"], ref["point_list"], ref["ranges"], cam.width, cam.height, ref["n_contrib"])
+    P = [t.double() for t in sc.params()]
+    pre = D.preprocess64(*P, cam, 3)
+    img, fT = D.blend64(pre["mean2d"], pre["conic"], pre["opacity"], pre["color"], ref["point_list"],
+                        ref["ranges"], mask, cam.width, cam.height, BG)
+    assert np.abs(img.numpy() - ref["image"]).max() <= 1e-5
+    assert np.abs(fT.numpy() - ref["final_T"]).max() <= 1e-5
+
+
+def test_blend_backward_replay_matches_autograd():
+    sc = small(n=400, seed=10)
+    cam = sc.cameras[0]
+    ref = O.render(*np_params(sc), cam, 3, bg=BG)
+    mask = O.contrib_mask(ref["rec"], ref["point_list"], ref["ranges"], cam.width, cam.height, ref["n_contrib"])
+    rec = ref["rec"].astype(np.float64)
+    m2 = torch.tensor(rec[:, 0:2], requires_grad=True)
+    con = torch.tensor(rec[:, 2:5], requires_grad=True)
+    op = torch.tensor(rec[:, 5], requires_grad=True)
+    col = torch.tensor(rec[:, 8:11], requires_grad=True)
+    img, fT = D.blend64(m2, con, op, col, ref["point_list"], ref["ranges"], mask, cam.width, cam.height, BG)
+    g = torch.Generator().manual_seed(1)
+    gi = torch.randn(3, cam.height, cam.width, generator=g, dtype=torch.float64)
+    ga = torch.randn(cam.height, cam.width, generator=g, dtype=torch.float64)
+    ((img * gi).sum() + ((1 - fT) * ga).sum()).backward()
+    g2 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
+                     ref["image"], gi.float().numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"],
+                     ref["ckpt"], sc.n, grad_alpha=ga.float().numpy())
+    vis = ref["touched"] > 0
+    for cols, t in (((0, 1), m2.grad), ((2, 3, 4), con.grad), ((5,), op.grad[:, None]), ((6, 7, 8), col.grad)):
+        a = g2[vis][:, list(cols)]
+        b = t.numpy()[vis]
+        assert D.rel_err(a, b) < 2e-5, (cols, D.rel_err(a, b))
+
+
+def test_preprocess_backward_matches_autograd():
+    sc = small(n=300, seed=11)
+    cam = sc.cameras[0]
+    rec, touched = O.preprocess_fwd(*np_params(sc), cam, 3)
+    vis = touched > 0
+    rng = np.random.default_rng(2)
+    g2 = rng.standard_normal((sc.n, 12)).astype(np.float32)
+    g2[:, 9:] = 0
+    gm, gls, gq, gop, gsh = O.preprocess_bwd(*np_params(sc), cam, 3, rec, touched, g2)
+    P = [t.double().requires_grad_(True) for t in sc.params()]
+    pre = D.preprocess64(*P, cam, 3)
+    g2t = torch.tensor(g2, dtype=torch.float64) * torch.tensor(vis, dtype=torch.float64)[:, None]
+    # clamped colour channels carry no gradient: preprocess64 clamps with torch.clamp as well
+    loss = ((pre["mean2d"] * g2t[:, 0:2]).sum() + (pre["conic"] * g2t[:, 2:5]).sum()
+            + (pre["opacity"] * g2t[:, 5]).sum() + (pre["color"] * g2t[:, 6:9]).sum())
+    loss.backward()
+    for name, a, t in (("means", gm, P[0]), ("log_scales", gls, P[1]), ("quats", gq, P[2]),
+                       ("opacity", gop, P[3]), ("sh", gsh, P[4])):
+        e = D.rel_err(a[vis], t.grad.numpy()[vis])
+        assert e < 1e-4, f"{name}: {e:.2e}"
+        assert np.all(a[~vis] == 0)
+
+
+def test_degree0_rest_gradients_are_zero():
+    sc = small(n=200, seed=12)
+    cam = sc.cameras[0]
+    rec, touched = O.preprocess_fwd(*np_params(sc), cam, 0)
+    g2 = np.ones((sc.n, 12), np.float32)
+    gsh = O.preprocess_bwd(*np_params(sc), cam, 0, rec, touched, g2)[4]
+    assert np.all(gsh[:, 1:, :] == 0)
+    assert np.any(gsh[:, 0, :] != 0)
