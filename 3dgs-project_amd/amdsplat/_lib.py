@@ -47,7 +47,8 @@ _SIGS = {
     "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32]),
     "gs_bin_fill_3d": (_i32, [_vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "gs_rect_counts": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
-    "gs_bin_fill_rect": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "gs_bin_fill_rect": (_i32, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -55,13 +56,15 @@ _SIGS = {
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp]),
     # 2D rule sets
-    "gs2d_pack": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
-    "gs2d_blend_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp,
-                              _vp, _vp, _vp]),
-    "gs2d_blend_bwd_bucket": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, C.POINTER(C.c_float),
-                                     _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "gs2d_blend_bwd_pixel": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp,
-                                    _vp, _vp, _vp]),
+    "gs2d_rects_toy": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "gs2d_rects_phase0": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "gs2d_pack": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "gs2d_blend_fwd": (_i32, [_i32, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, C.POINTER(C.c_double), _vp, _vp, _vp,
+                              _vp, _vp, _vp, _vp, _vp]),
+    "gs2d_blend_bwd_bucket": (_i32, [_i32, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _vp, _vp]),
+    "gs2d_blend_bwd_pixel": (_i32, [_i32, _i32, _vp, _vp, _i32, _vp, _i64, _i32, _i32, C.POINTER(C.c_double), _vp,
+                                    _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

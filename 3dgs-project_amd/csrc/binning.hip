@@ -287,15 +287,34 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
 // The result equals a stable sort of (tile << 32 | depth key) over instances emitted in
 // Gaussian-index order.
 // ---------------------------------------------------------------------------------------
+// Depth sort keys. 3D: the view depth of the record, culled Gaussians last. 2D: the caller's
+// depth (float32, or float64 split into a high and a low 32-bit key), every Gaussian kept,
+// so the resulting order is the stable argsort of the depths.
 __global__ void depth_keys_kernel(const SplatRec* __restrict__ rec, const float* __restrict__ depth,
-                                  const uint32_t* __restrict__ counts, int64_t n,
-                                  uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+                                  const double* __restrict__ depth64, const uint32_t* __restrict__ counts,
+                                  int64_t n, uint32_t* __restrict__ keys, uint32_t* __restrict__ keys_hi,
+                                  uint32_t* __restrict__ vals) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  uint32_t k = 0xffffffffu;
-  if (counts[i] != 0u) k = rec ? float_order_key(rec[i].b.z) : (depth ? float_order_key(depth[i]) : 0u);
+  uint32_t k = 0u;
+  if (rec) {
+    k = counts[i] != 0u ? float_order_key(rec[i].b.z) : 0xffffffffu;
+  } else if (depth) {
+    k = float_order_key(depth[i]);
+  } else if (depth64) {
+    const uint64_t u = static_cast<uint64_t>(__double_as_longlong(depth64[i] + 0.0));
+    const uint64_t o = (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+    k = static_cast<uint32_t>(o);
+    keys_hi[i] = static_cast<uint32_t>(o >> 32);
+  }
   keys[i] = k;
   vals[i] = static_cast<uint32_t>(i);
+}
+
+__global__ void gather_u32_kernel(const uint32_t* __restrict__ src, const uint32_t* __restrict__ idx, int64_t n,
+                                  uint32_t* __restrict__ out) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j < n) out[j] = src[idx[j]];
 }
 
 __global__ void gather_counts_kernel(const uint32_t* __restrict__ order, const uint32_t* __restrict__ counts,
@@ -349,12 +368,30 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
   }
 }
 
-__global__ void ranges_kernel(const uint32_t* __restrict__ tkeys, int64_t m, uint32_t* __restrict__ ranges) {
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (p >= m) return;
-  const uint32_t t = tkeys[p];
-  if (p == 0 || tkeys[p - 1] != t) ranges[2 * t] = static_cast<uint32_t>(p);
-  if (p == m - 1 || tkeys[p + 1] != t) ranges[2 * t + 1] = static_cast<uint32_t>(p + 1);
+// Per-tile [start, end) of the sorted instances by binary search of the sorted tile keys;
+// empty tiles get an empty range at their CSR position. Optionally the CSR offsets [T + 1].
+__device__ __forceinline__ uint32_t lower_bound_u32(const uint32_t* __restrict__ a, int64_t m, uint32_t v) {
+  int64_t lo = 0, hi = m;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (a[mid] < v) lo = mid + 1;
+    else hi = mid;
+  }
+  return static_cast<uint32_t>(lo);
+}
+
+__global__ void tile_ranges_kernel(const uint32_t* __restrict__ tkeys, int64_t m, int n_tiles,
+                                   uint32_t* __restrict__ ranges, uint32_t* __restrict__ offsets) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_tiles) return;
+  const uint32_t s = m > 0 ? lower_bound_u32(tkeys, m, static_cast<uint32_t>(t)) : 0u;
+  const uint32_t e = m > 0 ? lower_bound_u32(tkeys, m, static_cast<uint32_t>(t) + 1u) : 0u;
+  ranges[2 * t] = s;
+  ranges[2 * t + 1] = e;
+  if (offsets) {
+    offsets[t] = s;
+    if (t == n_tiles - 1) offsets[n_tiles] = e;
+  }
 }
 
 // Full 64-bit keys of the sorted instances (tile << 32 | depth key), for callers that want them.
@@ -421,10 +458,10 @@ static size_t bin_ws(int64_t n, int64_t m, int n_tiles) {
 }
 
 // Shared driver of the 3D and rectangle binnings.
-static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, const uint32_t* counts,
-                    int64_t n, int tiles_x, int n_tiles, int64_t m, uint64_t* sorted_keys,
-                    uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets, char* ws,
-                    hipStream_t st) {
+static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, const double* depth64,
+                    const uint32_t* counts, int64_t n, int tiles_x, int n_tiles, int64_t m,
+                    uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
+                    uint32_t* bucket_offsets, uint32_t* order_out, char* ws, hipStream_t st) {
   uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
   uint32_t* dsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
   uint32_t* iota = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
@@ -440,14 +477,24 @@ static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, 
   uint32_t* bcount = reinterpret_cast<uint32_t*>(ws); ws += align_up(static_cast<size_t>(n_tiles) * 4);
   char* tile_scratch = ws;
 
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(2 * int64_t(n_tiles), 256)), dim3(256), 0, st,
-                     ranges, 2 * int64_t(n_tiles), 0u);
+  const bool by_depth = rec != nullptr || depth != nullptr || depth64 != nullptr;
+  if (n > 0 && (m > 0 || order_out)) {
+    // a float64 depth sorts by its low key half first, then stably by the high half (kept in
+    // scounts, gathered into dkey_of in the order of the first sort)
+    uint32_t* khi = dkey_of;
+    hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, depth64,
+                       counts, n, dkeys, depth64 ? scounts : nullptr, by_depth ? iota : order);
+    if (sorted_keys && m > 0 && !depth64) (void)hipMemcpyAsync(dkey_of, dkeys, n * 4, hipMemcpyDeviceToDevice, st);
+    if (depth64) {
+      radix_sort(dkeys, iota, dsorted, soffs, n, 32, sort_scratch, st);
+      hipLaunchKernelGGL(gather_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, scounts, soffs, n, khi);
+      radix_sort(khi, soffs, dsorted, order, n, 32, sort_scratch, st);
+    } else if (by_depth) {
+      radix_sort(dkeys, iota, dsorted, order, n, 32, sort_scratch, st);
+    }
+    if (order_out) (void)hipMemcpyAsync(order_out, order, n * 4, hipMemcpyDeviceToDevice, st);
+  }
   if (m > 0) {
-    const bool by_depth = rec != nullptr || depth != nullptr;
-    hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, counts,
-                       n, dkeys, by_depth ? iota : order);
-    if (sorted_keys) (void)hipMemcpyAsync(dkey_of, dkeys, n * 4, hipMemcpyDeviceToDevice, st);
-    if (by_depth) radix_sort(dkeys, iota, dsorted, order, n, 32, sort_scratch, st);
     hipLaunchKernelGGL(gather_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, counts, n,
                        scounts);
     scan_rec(scounts, soffs, n, scan_scratch, st);
@@ -459,11 +506,12 @@ static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, 
                          soffs, n, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     }
     radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
-    hipLaunchKernelGGL(ranges_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, ranges);
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
                          dkey_of, m, sorted_keys);
   }
+  hipLaunchKernelGGL(tile_ranges_kernel, dim3(grid_for(n_tiles, 256)), dim3(256), 0, st, tsorted, m, n_tiles,
+                     ranges, tile_offsets);
   hipLaunchKernelGGL(bucket_count_kernel, dim3(grid_for(n_tiles, 256)), dim3(256), 0, st, ranges,
                      n_tiles, bcount);
   scan_rec(bcount, bucket_offsets, n_tiles, tile_scratch, st);
@@ -513,9 +561,9 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touc
              "binning workspace too small: need %zu bytes", need);
   GS_REQUIRE(m == 0 || (splat_rec && tiles_touched && point_list), GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
-  bin_fill(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, tiles_touched, n, k.tiles_x,
-           n_tiles, m, sorted_keys, point_list, ranges, bucket_offsets, static_cast<char*>(workspace),
-           as_stream(stream));
+  bin_fill(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, nullptr, tiles_touched, n,
+           k.tiles_x, n_tiles, m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, nullptr,
+           static_cast<char*>(workspace), as_stream(stream));
   return check_launch("bin_fill_3d");
 }
 
@@ -531,22 +579,29 @@ extern "C" int gs_rect_counts(const int32_t* rects, int64_t n, int tiles_x, int 
   return check_launch("rect_counts");
 }
 
-extern "C" int gs_bin_fill_rect(const int32_t* rects, const float* depth, const uint32_t* counts,
-                                int64_t n, int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
-                                uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
+extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int depth_dtype,
+                                const uint32_t* counts, int64_t n, int tiles_x, int tiles_y, int64_t m,
+                                uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
+                                uint32_t* tile_offsets, uint32_t* bucket_offsets, uint32_t* order,
                                 void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32) && tiles_x > 0 && tiles_y > 0, GS_ERR_ARG,
              "invalid sizes");
+  GS_REQUIRE(depth_dtype == GS_FLOAT32 || depth_dtype == GS_FLOAT64, GS_ERR_ARG, "invalid depth dtype");
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const int n_tiles = tiles_x * tiles_y;
   const size_t need = bin_ws(n, m, n_tiles);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
   GS_REQUIRE(m == 0 || (rects && counts && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(!(depth && depth_dtype == GS_FLOAT64 && sorted_keys), GS_ERR_ARG,
+             "sorted_keys are 32-bit depth keys: not available with a float64 depth");
   GS_REQUIRE(aligned(rects, 16), GS_ERR_ALIGN, "rects must be 16-byte aligned");
-  bin_fill(nullptr, reinterpret_cast<const int4*>(rects), depth, counts, n, tiles_x, n_tiles, m,
-           sorted_keys, point_list, ranges, bucket_offsets, static_cast<char*>(workspace), as_stream(stream));
+  const float* d32 = depth_dtype == GS_FLOAT32 ? static_cast<const float*>(depth) : nullptr;
+  const double* d64 = depth_dtype == GS_FLOAT64 ? static_cast<const double*>(depth) : nullptr;
+  bin_fill(nullptr, reinterpret_cast<const int4*>(rects), d32, d64, counts, n, tiles_x, n_tiles, m,
+           sorted_keys, point_list, ranges, tile_offsets, bucket_offsets, order, static_cast<char*>(workspace),
+           as_stream(stream));
   return check_launch("bin_fill_rect");
 }
 

@@ -1,25 +1,24 @@
-// 3D alpha blending: forward (one 16x16 tile per 256-lane workgroup) and the bucketed
-// backward (one wavefront per 32-entry bucket, each lane owning 4 pixels).
+// Alpha blending for all three rule sets (gs_rules.h): the forward (one 16x16 tile per
+// 256-lane workgroup), the bucketed backward (one wavefront per 32-entry bucket, each lane
+// owning 4 pixels, replaying T from the forward's checkpoints), and the per-pixel backward
+// of the 2D surfaces (one thread per pixel, back to front, one atomic per pair).
 //
-// Pixel layout inside a tile: thread t owns pixel (t % 16, t / 16), so wavefront w owns
-// rows 4w .. 4w+3 (a 16x4 "strip"). A splat is evaluated for a strip only if its pixel
-// bounds overlap the strip's rows; the forward, the backward and the CPU oracle apply this
-// rule identically, so the backward replays exactly the forward's splat sequence (the same
-// purpose as Faster-GS's per-subtile culling, phase1/fastergs_macro.patch:92-104).
+// Pixel layout inside a tile: lane t owns pixel (t % 16, t / 16) in the forward (the
+// references' thread-to-pixel map: toy2d/csrc/rasterize.cu:110-113,
+// phase0/csrc/macrotile/splat2d_common.h:83-88), so checkpoint [bucket][t] has the
+// references' [B, 256, 4] layout. In the backward, lane l of the wavefront owns pixels
+// 64 r + l (rows 4 r + l / 16), r = 0..3. 3D only: a splat is evaluated for the 16x4 strip
+// of a wavefront only if its pixel bounds overlap the strip's rows; forward, backward and
+// oracle apply this rule identically, so the backward replays exactly the forward's splat
+// sequence (the purpose of Faster-GS's per-subtile culling, phase1/fastergs_macro.patch:92-104).
+#include <limits.h>
+
+#include <type_traits>
+
 #include "gs_host.h"
+#include "gs_rules.h"
 
 namespace gs {
-
-// log2-domain exponent of the Gaussian at offset (dx, dy) = mean - pixel centre, with the
-// conic pre-scaled by (-1/2 log2 e, -log2 e, -1/2 log2 e). Clamped at 0.
-__device__ __forceinline__ float power2(float qa, float qb, float qc, float dx, float dy) {
-  float t = qb * dy;
-  t = fmaf(qa, dx, t);
-  float u = qc * dy;
-  u = u * dy;
-  const float e = fmaf(dx, t, u);
-  return fminf(e, 0.0f);
-}
 
 __device__ __forceinline__ uint32_t strip_mask(const int4 d, int tile_y0) {
   uint32_t m = 0;
@@ -31,88 +30,150 @@ __device__ __forceinline__ uint32_t strip_mask(const int4 d, int tile_y0) {
   return m;
 }
 
+template <typename S>
+struct BlendArgs {
+  const S* rec;                    // [n, 16]
+  const uint32_t* ranges;          // tile t: [ranges[t * stride], ranges[t * stride + 1])
+  int range_stride;                // 2: (T, 2) ranges; 1: (T + 1) CSR offsets
+  const uint32_t* point_list;      // [m]
+  const uint32_t* bucket_offsets;  // [T + 1] (first bucket of each tile)
+  int W, H, tiles_x, n_tiles;
+  S bg0, bg1, bg2;
+  // forward outputs / backward inputs
+  S* image;
+  S* final_T;
+  int32_t* n_contrib;     // 3D, toy2d: last position + 1; phase0: number of splats
+  int32_t* last_contrib;  // phase0: last position + 1 (may be null)
+  uint32_t* tile_max;     // [T] max over pixels of last position + 1 (may be null in backward)
+  S* ckpt;                // [B, 256, 4]
+  unsigned long long* counters;  // [3]: atomic adds, checkpoint bytes, splat-pixel evaluations
+  // backward
+  const uint32_t* bucket_to_tile;
+  const uint32_t* n_buckets_dev;  // bucket count on device (may be null)
+  int64_t n_buckets;              // grid bound (host)
+  const S* grad_image;
+  const S* grad_alpha;  // 3D: gradient of alpha = 1 - final_T (may be null)
+  S* grad_rec;          // [n, 12]
+};
+
+// Per-wavefront counter increment (one atomic per wavefront).
+__device__ __forceinline__ void count_add(unsigned long long* c, uint32_t v) {
+  uint32_t s = v;
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0 && s) atomicAdd(c, static_cast<unsigned long long>(s));
+}
+
 // ---------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(kTilePixels) void blend_fwd_3d_kernel(
-    const SplatRec* __restrict__ rec, const uint2* __restrict__ ranges,
-    const uint32_t* __restrict__ point_list, const uint32_t* __restrict__ bucket_offsets, int W,
-    int H, int tiles_x, float bg_r, float bg_g, float bg_b, float* __restrict__ image,
-    float* __restrict__ final_T, int32_t* __restrict__ n_contrib, uint32_t* __restrict__ tile_max,
-    float4* __restrict__ ckpt) {
-  __shared__ float4 s_p0[kTilePixels];  // mx, my, qa, qb
-  __shared__ float4 s_p1[kTilePixels];  // qc, o, r, g
-  __shared__ float2 s_p2[kTilePixels];  // b, strip mask
+template <int R, typename S>
+__global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) {
+  using Ru = Rule<R, S>;
+  __shared__ Staged<S> s_sp[kTilePixels];
+  __shared__ uint32_t s_mask[Ru::kStrips ? kTilePixels : 1];
   __shared__ uint32_t s_max;
 
   const int tile = blockIdx.x;
-  const int tx = tile % tiles_x, ty = tile / tiles_x;
+  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int px = tx * kTile + (t & 15), py = ty * kTile + (t >> 4);
-  const bool inside = px < W && py < H;
-  const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
-  const uint2 range = ranges[tile];
-  const int len = static_cast<int>(range.y - range.x);
-  float4* ck = ckpt + static_cast<int64_t>(bucket_offsets[tile]) * kTilePixels + t;
+  const bool inside = px < a.W && py < a.H;
+  const S pxf = static_cast<S>(px) + Ru::pix_off(), pyf = static_cast<S>(py) + Ru::pix_off();
+  const uint32_t r0 = a.ranges[static_cast<int64_t>(tile) * a.range_stride];
+  const uint32_t r1 = a.ranges[static_cast<int64_t>(tile) * a.range_stride + 1];
+  const int len = static_cast<int>(r1 - r0);
+  S* ck = a.ckpt ? a.ckpt + (static_cast<int64_t>(a.bucket_offsets[tile]) * kTilePixels + t) * 4 : nullptr;
   if (t == 0) s_max = 0;
 
-  float T = 1.0f, Cr = 0.0f, Cg = 0.0f, Cb = 0.0f;
-  int last = 0;
+  S T = S(1), Cr = S(0), Cg = S(0), Cb = S(0);
+  int last = 0, count = 0;
+  uint32_t evals = 0;
   bool done = !inside;
+  int covered = len;  // list positions whose bucket checkpoints the loop wrote
   for (int b0 = 0; b0 < len; b0 += kTilePixels) {
-    if (__syncthreads_count(done ? 1 : 0) == kTilePixels) break;
+    if (__syncthreads_count(done ? 1 : 0) == kTilePixels) {
+      covered = b0;
+      break;
+    }
     const int j = b0 + t;
     if (j < len) {
-      const uint32_t g = point_list[range.x + j];
-      const SplatRec r = rec[g];
-      s_p0[t] = make_float4(r.a.x, r.a.y, r.a.z * kNegHalfLog2e, r.a.w * kNegLog2e);
-      s_p1[t] = make_float4(r.b.x * kNegHalfLog2e, r.b.y, r.c.x, r.c.y);
-      s_p2[t] = make_float2(r.c.z, __uint_as_float(strip_mask(r.d, ty * kTile)));
+      const uint32_t g = a.point_list[r0 + j];
+      const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
+      s_sp[t] = Ru::stage(rp);
+      if constexpr (Ru::kStrips) s_mask[t] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
     }
     __syncthreads();
     const int nb = min(kTilePixels, len - b0);
     for (int jj = 0; jj < nb; ++jj) {
       const int idx = b0 + jj;
-      if ((idx & (kBucket - 1)) == 0) ck[static_cast<int64_t>(idx / kBucket) * kTilePixels] = make_float4(Cr, Cg, Cb, T);
+      if (ck && (idx & (kBucket - 1)) == 0) {
+        S* c = ck + static_cast<int64_t>(idx / kBucket) * kTilePixels * 4;
+        if constexpr (Ru::kCkptTFirst) {
+          c[0] = T; c[1] = Cr; c[2] = Cg; c[3] = Cb;
+        } else {
+          c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
+        }
+      }
       if (done) continue;
-      const float2 p2 = s_p2[jj];
-      if (((__float_as_uint(p2.y) >> wave) & 1u) == 0u) continue;  // wave-uniform
-      const float4 p0 = s_p0[jj];
-      const float4 p1 = s_p1[jj];
-      const float dx = p0.x - pxf, dy = p0.y - pyf;
-      const float G = exp2_neg(power2(p0.z, p0.w, p1.x, dx, dy));
-      const float alpha = p1.y * G;
-      if (alpha < kAlphaMin) continue;
-      const float w = alpha * T;
-      Cr = fmaf(p1.z, w, Cr);
-      Cg = fmaf(p1.w, w, Cg);
-      Cb = fmaf(p2.x, w, Cb);
-      T = T * (1.0f - alpha);
+      if constexpr (Ru::kStrips) {
+        if (((s_mask[jj] >> wave) & 1u) == 0u) continue;  // wave-uniform
+      }
+      const Staged<S> sp = s_sp[jj];
+      Eval<S> e;
+      ++evals;
+      if (!Ru::eval(sp, pxf, pyf, e)) continue;
+      if constexpr (Ru::kStopBefore) {
+        if (T * (S(1) - e.alpha) < Ru::t_stop()) {
+          done = true;
+          continue;
+        }
+      }
+      composite<R, S>(Cr, Cg, Cb, T, sp, e.alpha);
+      ++count;
       last = idx + 1;
-      if (T < kTStop) done = true;
+      if constexpr (!Ru::kStopBefore) {
+        if (T < Ru::t_stop()) done = true;
+      }
+    }
+  }
+  if (a.counters) count_add(a.counters + 2, evals);
+  if constexpr (R == kRulesPhase0) {
+    // phase0 writes every checkpoint slot: buckets after the workgroup stopped keep the
+    // final state (phase0/csrc/macrotile/bindings.cpp:167-169)
+    if (ck) {
+      for (int q = (covered + kBucket - 1) / kBucket; q < (len + kBucket - 1) / kBucket; ++q) {
+        S* c = ck + static_cast<int64_t>(q) * kTilePixels * 4;
+        c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
+      }
     }
   }
   if (inside) {
-    const int64_t pix = static_cast<int64_t>(py) * W + px;
-    const int64_t HW = static_cast<int64_t>(H) * W;
-    image[pix] = fmaf(T, bg_r, Cr);
-    image[HW + pix] = fmaf(T, bg_g, Cg);
-    image[2 * HW + pix] = fmaf(T, bg_b, Cb);
-    final_T[pix] = T;
-    n_contrib[pix] = last;
+    const int64_t pix = static_cast<int64_t>(py) * a.W + px;
+    if constexpr (Ru::kInterleaved) {
+      a.image[3 * pix] = Cr;
+      a.image[3 * pix + 1] = Cg;
+      a.image[3 * pix + 2] = Cb;
+    } else {
+      const int64_t HW = static_cast<int64_t>(a.H) * a.W;
+      a.image[pix] = fma(T, a.bg0, Cr);
+      a.image[HW + pix] = fma(T, a.bg1, Cg);
+      a.image[2 * HW + pix] = fma(T, a.bg2, Cb);
+    }
+    a.final_T[pix] = T;
+    a.n_contrib[pix] = Ru::kCountContrib ? count : last;
+    if (a.last_contrib) a.last_contrib[pix] = last;
     if (last > 0) atomicMax(&s_max, static_cast<uint32_t>(last));
   }
   __syncthreads();
-  if (t == 0) tile_max[tile] = s_max;
+  if (t == 0 && a.tile_max) a.tile_max[tile] = s_max;
 }
 
 // ---------------------------------------------------------------------------------------
-// Backward
+// Wavefront reductions
 // ---------------------------------------------------------------------------------------
-
-// Sum over the wavefront; the result is returned to every lane (via lane 63 and a
-// readlane). Row reductions use DPP row shifts, rows are combined with row_bcast.
+// Sum over the wavefront, returned to every lane: DPP row shifts reduce each row of 16
+// lanes, row_bcast15 / row_bcast31 combine the rows, lane 63 holds the total.
 __device__ __forceinline__ float wave_sum(float v) {
   int x = __float_as_int(v);
   float s = v;
@@ -130,132 +191,326 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
 }
 
+// Double: butterfly over lane-crossing shuffles (the 2D surfaces' float64 mode).
+__device__ __forceinline__ double wave_sum(double v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ void atomic_add_grad(float* p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAtomicAdd(p, v); }
+
+// ---------------------------------------------------------------------------------------
+// Bucketed backward
+// ---------------------------------------------------------------------------------------
 constexpr int kBwdWaves = 4;
 
-__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_3d_kernel(
-    const SplatRec* __restrict__ rec, const uint2* __restrict__ ranges,
-    const uint32_t* __restrict__ point_list, const uint32_t* __restrict__ bucket_offsets,
-    const uint32_t* __restrict__ bucket_to_tile, int n_tiles, int W, int H, int tiles_x,
-    const float* __restrict__ image, const float* __restrict__ grad_image,
-    const float* __restrict__ final_T, const float* __restrict__ grad_alpha,
-    const int32_t* __restrict__ n_contrib, const uint32_t* __restrict__ tile_max,
-    const float4* __restrict__ ckpt, float* __restrict__ grad2d) {
-  __shared__ float4 s_p0[kBwdWaves][kBucket];  // mx, my, qa, qb
-  __shared__ float4 s_p1[kBwdWaves][kBucket];  // qc, o, A, B
-  __shared__ float4 s_p2[kBwdWaves][kBucket];  // C, r, g, b
-  __shared__ uint32_t s_m[kBwdWaves][kBucket];  // strip mask
+template <int R, typename S>
+__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(BlendArgs<S> a) {
+  using Ru = Rule<R, S>;
+  constexpr int NV = Ru::kGradVals;
+  __shared__ Staged<S> s_sp[kBwdWaves][kBucket];
+  __shared__ uint32_t s_m[kBwdWaves][kBucket];
   __shared__ uint32_t s_id[kBwdWaves][kBucket];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
-  const uint32_t n_buckets = bucket_offsets[n_tiles];
-  if (b >= n_buckets) return;  // whole wavefront
-  const uint32_t tile = bucket_to_tile[b];
-  const int bstart = static_cast<int>(b - bucket_offsets[tile]) * kBucket;
-  const int tmax = static_cast<int>(tile_max[tile]);
+  if (b >= a.n_buckets) return;  // whole wavefront
+  if (a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)) return;
+  const uint32_t tile = a.bucket_to_tile[b];
+  const int bstart = static_cast<int>(b - a.bucket_offsets[tile]) * kBucket;
+  const int tmax = a.tile_max ? static_cast<int>(a.tile_max[tile]) : INT_MAX;
   if (bstart >= tmax) return;
-  const int bsize = min(kBucket, tmax - bstart);
-  const uint2 range = ranges[tile];
-  const int tx = static_cast<int>(tile) % tiles_x, ty = static_cast<int>(tile) / tiles_x;
+  const uint32_t r0 = a.ranges[static_cast<int64_t>(tile) * a.range_stride];
+  const uint32_t r1 = a.ranges[static_cast<int64_t>(tile) * a.range_stride + 1];
+  const int bsize = min(kBucket, min(static_cast<int>(r1 - r0), tmax) - bstart);
+  if (bsize <= 0) return;
+  const int tx = static_cast<int>(tile) % a.tiles_x, ty = static_cast<int>(tile) / a.tiles_x;
 
   if (lane < bsize) {
-    const uint32_t g = point_list[range.x + bstart + lane];
-    const SplatRec r = rec[g];
-    s_p0[wave][lane] = make_float4(r.a.x, r.a.y, r.a.z * kNegHalfLog2e, r.a.w * kNegLog2e);
-    s_p1[wave][lane] = make_float4(r.b.x * kNegHalfLog2e, r.b.y, r.a.z, r.a.w);
-    s_p2[wave][lane] = make_float4(r.b.x, r.c.x, r.c.y, r.c.z);
-    s_m[wave][lane] = strip_mask(r.d, ty * kTile);
+    const uint32_t g = a.point_list[r0 + bstart + lane];
+    const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
+    s_sp[wave][lane] = Ru::stage(rp);
+    if constexpr (Ru::kStrips) s_m[wave][lane] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
     s_id[wave][lane] = g;
   }
 
   // per-pixel state: pixel p = 64 r + lane, row 4 r + lane / 16, column lane % 16
-  const int64_t HW = static_cast<int64_t>(H) * W;
+  const int64_t HW = static_cast<int64_t>(a.H) * a.W;
   const int px = tx * kTile + (lane & 15);
-  const float pxf = static_cast<float>(px) + 0.5f;
-  float T[kPixPerLane], rho[kPixPerLane], Gr[kPixPerLane], Gg[kPixPerLane], Gb[kPixPerLane];
-  float pyf[kPixPerLane];
+  const S pxf = static_cast<S>(px) + Ru::pix_off();
+  S T[kPixPerLane], rho[kPixPerLane], Gr[kPixPerLane], Gg[kPixPerLane], Gb[kPixPerLane];
+  S pyf[kPixPerLane];
   int lim[kPixPerLane];
+  int lim_max = 0;
 #pragma unroll
   for (int r = 0; r < kPixPerLane; ++r) {
     const int py = ty * kTile + kStripRows * r + (lane >> 4);
-    pyf[r] = static_cast<float>(py) + 0.5f;
-    T[r] = 0.0f;
-    rho[r] = 0.0f;
-    Gr[r] = Gg[r] = Gb[r] = 0.0f;
+    pyf[r] = static_cast<S>(py) + Ru::pix_off();
+    T[r] = S(0);
+    rho[r] = S(0);
+    Gr[r] = Gg[r] = Gb[r] = S(0);
     lim[r] = 0;
-    if (px < W && py < H) {
-      const int64_t pix = static_cast<int64_t>(py) * W + px;
-      const int used = n_contrib[pix] - bstart;
+    if (px < a.W && py < a.H) {
+      const int64_t pix = static_cast<int64_t>(py) * a.W + px;
+      // phase0 without a limit table: every inside pixel replays the bucket and stops by the
+      // T < 1e-4 rule (phase0/csrc/macrotile/splat2d_bwd_splat.cu:69)
+      const int32_t* lp = a.last_contrib ? a.last_contrib : a.n_contrib;
+      const int used = lp ? lp[pix] - bstart : kBucket;
       if (used > 0) {
         lim[r] = used;
-        Gr[r] = grad_image[pix];
-        Gg[r] = grad_image[HW + pix];
-        Gb[r] = grad_image[2 * HW + pix];
-        const float4 c = ckpt[b * kTilePixels + kWave * r + lane];
-        T[r] = c.w;
-        rho[r] = Gr[r] * (image[pix] - c.x) + Gg[r] * (image[HW + pix] - c.y) +
-                 Gb[r] * (image[2 * HW + pix] - c.z);
+        lim_max = max(lim_max, used);
+        S img0, img1, img2;
+        if constexpr (Ru::kInterleaved) {
+          Gr[r] = a.grad_image[3 * pix];
+          Gg[r] = a.grad_image[3 * pix + 1];
+          Gb[r] = a.grad_image[3 * pix + 2];
+          img0 = a.image[3 * pix];
+          img1 = a.image[3 * pix + 1];
+          img2 = a.image[3 * pix + 2];
+        } else {
+          Gr[r] = a.grad_image[pix];
+          Gg[r] = a.grad_image[HW + pix];
+          Gb[r] = a.grad_image[2 * HW + pix];
+          img0 = a.image[pix];
+          img1 = a.image[HW + pix];
+          img2 = a.image[2 * HW + pix];
+        }
+        const S* c = a.ckpt + (b * kTilePixels + kWave * r + lane) * 4;
+        S c0, c1, c2;
+        if constexpr (Ru::kCkptTFirst) {
+          T[r] = c[0]; c0 = c[1]; c1 = c[2]; c2 = c[3];
+        } else {
+          c0 = c[0]; c1 = c[1]; c2 = c[2]; T[r] = c[3];
+        }
+        // rho = G . (image - C): the colour still to come (background included)
+        rho[r] = Gr[r] * (img0 - c0) + Gg[r] * (img1 - c1) + Gb[r] * (img2 - c2);
         // alpha = 1 - T_final output: its gradient enters like a background term
-        if (grad_alpha) rho[r] -= grad_alpha[pix] * final_T[pix];
+        if constexpr (R == kRules3D) {
+          if (a.grad_alpha) rho[r] -= a.grad_alpha[pix] * a.final_T[pix];
+        }
       }
     }
   }
+  const int jmax = min(bsize, wave_max(lim_max));
   wave_sync();
 
-  for (int j = 0; j < bsize; ++j) {
-    const uint32_t m = s_m[wave][j];
-    const float4 p0 = s_p0[wave][j];
-    const float4 p1 = s_p1[wave][j];
-    const float4 p2 = s_p2[wave][j];
-    float acc[11];
+  uint32_t evals = 0, atomics = 0;
+  for (int j = 0; j < jmax; ++j) {
+    const Staged<S> sp = s_sp[wave][j];
+    uint32_t m = 0xfu;
+    if constexpr (Ru::kStrips) m = s_m[wave][j];
+    S acc[11];
 #pragma unroll
-    for (int k = 0; k < 11; ++k) acc[k] = 0.0f;
+    for (int k = 0; k < 11; ++k) acc[k] = S(0);
     bool used = false;
 #pragma unroll
     for (int r = 0; r < kPixPerLane; ++r) {
       if (((m >> r) & 1u) == 0u) continue;  // wave-uniform
       if (j >= lim[r]) continue;
-      const float dx = p0.x - pxf, dy = p0.y - pyf[r];
-      const float G = exp2_neg(power2(p0.z, p0.w, p1.x, dx, dy));
-      const float alpha = p1.y * G;
-      if (alpha < kAlphaMin) continue;
+      if constexpr (R == kRulesPhase0) {
+        if (T[r] < Ru::t_stop()) continue;
+      }
+      Eval<S> e;
+      ++evals;
+      if (!Ru::eval(sp, pxf, pyf[r], e)) continue;
       used = true;
-      const float w = T[r] * alpha;
-      const float dot = Gr[r] * p2.y + Gg[r] * p2.z + Gb[r] * p2.w;
+      const S w = T[r] * e.alpha;
+      const S dot = Gr[r] * sp.cr + Gg[r] * sp.cg + Gb[r] * sp.cb;
       acc[6] += w * Gr[r];
       acc[7] += w * Gg[r];
       acc[8] += w * Gb[r];
-      rho[r] = fmaf(-w, dot, rho[r]);
-      const float oma = 1.0f - alpha;
-      const float dLda = T[r] * dot - rho[r] * __builtin_amdgcn_rcpf(fmaxf(oma, kOneMinusAlphaEps));
-      acc[5] += G * dLda;
-      const float hp = alpha * dLda;  // dL/dpower (natural)
-      acc[2] += -0.5f * hp * dx * dx;
-      acc[3] += -hp * dx * dy;
-      acc[4] += -0.5f * hp * dy * dy;
-      const float gmx = -hp * (p1.z * dx + p1.w * dy);
-      const float gmy = -hp * (p1.w * dx + p2.x * dy);
-      acc[0] += gmx;
-      acc[1] += gmy;
-      acc[9] += fabsf(gmx);
-      acc[10] += fabsf(gmy);
+      rho[r] = fma(-w, dot, rho[r]);
+      const S oma = S(1) - e.alpha;
+      S dLda;
+      if constexpr (R == kRules3D) {
+        dLda = T[r] * dot - rho[r] * __builtin_amdgcn_rcpf(fmaxf(oma, kOneMinusAlphaEps));
+      } else {
+        dLda = T[r] * dot - rho[r] / oma;
+      }
+      shape_grads<R, S>(sp, e, dLda, acc);
       T[r] = T[r] * oma;
     }
     if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
-    float mine = 0.0f;
+    S mine = S(0);
 #pragma unroll
-    for (int k = 0; k < 11; ++k) {
-      const float s = wave_sum(acc[k]);
+    for (int k = 0; k < NV; ++k) {
+      const S s = wave_sum(acc[k]);
       mine = (lane == k) ? s : mine;
     }
-    if (lane < 11) unsafeAtomicAdd(grad2d + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + lane, mine);
+    if constexpr (R == kRulesPhase0) {
+      if (lane == 5) mine = mine * sp.o * (S(1) - sp.o);  // dL/dlogit = dL/do o (1 - o)
+    }
+    if (lane < NV) atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + lane, mine);
+    atomics += NV;
+  }
+  if (a.counters) {
+    if (lane == 0 && atomics) atomicAdd(a.counters, static_cast<unsigned long long>(atomics));
+    count_add(a.counters + 2, evals);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Per-pixel backward (2D surfaces): each thread walks its pixel's list back to front,
+// recovers T by dividing by (1 - alpha), and issues one atomic per parameter per pair
+// (toy2d/csrc/rasterize.cu:182-258, phase0/csrc/macrotile/splat2d_bwd_pixel.cu:13-62).
+// ---------------------------------------------------------------------------------------
+template <int R, typename S>
+__global__ __launch_bounds__(kTilePixels) void blend_bwd_pixel_kernel(BlendArgs<S> a) {
+  using Ru = Rule<R, S>;
+  __shared__ Staged<S> s_sp[kTilePixels];
+  __shared__ uint32_t s_id[kTilePixels];
+
+  const int tile = blockIdx.x;
+  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
+  const int t = threadIdx.x;
+  const int px = tx * kTile + (t & 15), py = ty * kTile + (t >> 4);
+  const bool inside = px < a.W && py < a.H;
+  const S pxf = static_cast<S>(px) + Ru::pix_off(), pyf = static_cast<S>(py) + Ru::pix_off();
+  const uint32_t r0 = a.ranges[static_cast<int64_t>(tile) * a.range_stride];
+  const uint32_t r1 = a.ranges[static_cast<int64_t>(tile) * a.range_stride + 1];
+  const int len = static_cast<int>(r1 - r0);
+  const int64_t pix = static_cast<int64_t>(py) * a.W + px;
+  const int64_t HW = static_cast<int64_t>(a.H) * a.W;
+
+  S Tcur = S(0), G0 = S(0), G1 = S(0), G2 = S(0), bg_dot = S(0), T_final = S(0);
+  int lim = 0;
+  if (inside) {
+    T_final = a.final_T[pix];
+    Tcur = T_final;
+    lim = (a.last_contrib ? a.last_contrib : a.n_contrib)[pix];
+    if constexpr (Ru::kInterleaved) {
+      G0 = a.grad_image[3 * pix];
+      G1 = a.grad_image[3 * pix + 1];
+      G2 = a.grad_image[3 * pix + 2];
+    } else {
+      G0 = a.grad_image[pix];
+      G1 = a.grad_image[HW + pix];
+      G2 = a.grad_image[2 * HW + pix];
+    }
+    if constexpr (Ru::kBackground) bg_dot = a.bg0 * G0 + a.bg1 * G1 + a.bg2 * G2;
+  }
+  S acc0 = S(0), acc1 = S(0), acc2 = S(0);  // colour behind the current splat, over T
+  uint32_t evals = 0, atomics = 0;
+  for (int b0 = 0; b0 < len; b0 += kTilePixels) {
+    __syncthreads();  // the previous batch is no longer in use
+    const int k = len - 1 - (b0 + t);  // position in the tile list, back to front
+    if (k >= 0) {
+      const uint32_t g = a.point_list[r0 + k];
+      s_sp[t] = Ru::stage(a.rec + static_cast<int64_t>(g) * kRecFloats);
+      s_id[t] = g;
+    }
+    __syncthreads();
+    const int nb = min(kTilePixels, len - b0);
+    for (int jj = 0; jj < nb; ++jj) {
+      const int pos = len - 1 - (b0 + jj);
+      if (!inside || pos >= lim) continue;
+      const Staged<S> sp = s_sp[jj];
+      Eval<S> e;
+      ++evals;
+      if (!Ru::eval(sp, pxf, pyf, e)) continue;
+      const S oma = S(1) - e.alpha;
+      const S Tb = Tcur / oma;  // T in front of this splat
+      const S dot = G0 * (sp.cr - acc0) + G1 * (sp.cg - acc1) + G2 * (sp.cb - acc2);
+      acc0 = e.alpha * sp.cr + oma * acc0;
+      acc1 = e.alpha * sp.cg + oma * acc1;
+      acc2 = e.alpha * sp.cb + oma * acc2;
+      Tcur = Tb;
+      S dLda = Tb * dot;
+      if constexpr (Ru::kBackground) dLda += (-T_final / oma) * bg_dot;
+      S g[11];
+#pragma unroll
+      for (int q = 0; q < 11; ++q) g[q] = S(0);
+      const S w = e.alpha * Tb;
+      g[6] = w * G0;
+      g[7] = w * G1;
+      g[8] = w * G2;
+      shape_grads<R, S>(sp, e, dLda, g);
+      if constexpr (R == kRulesPhase0) g[5] = g[5] * sp.o * (S(1) - sp.o);
+      S* dst = a.grad_rec + static_cast<int64_t>(s_id[jj]) * kGrad2D;
+#pragma unroll
+      for (int q = 0; q < 9; ++q) atomic_add_grad(dst + q, g[q]);
+      atomics += 9;
+    }
+  }
+  if (a.counters) {
+    count_add(a.counters, atomics);
+    count_add(a.counters + 2, evals);
   }
 }
 
 }  // namespace gs
 
 using namespace gs;
+
+// ---------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------
+namespace {
+
+template <int R, typename S>
+void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
+  hipLaunchKernelGGL((blend_fwd_kernel<R, S>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
+}
+
+template <int R, typename S>
+void launch_bwd_bucket(const BlendArgs<S>& a, hipStream_t st) {
+  const int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
+  hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kBwdWaves * kWave), 0, st, a);
+}
+
+template <int R, typename S>
+void launch_bwd_pixel(const BlendArgs<S>& a, hipStream_t st) {
+  hipLaunchKernelGGL((blend_bwd_pixel_kernel<R, S>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
+}
+
+int check_rules(int rules, int dtype) {
+  GS_REQUIRE(rules == GS_RULES_TOY2D || rules == GS_RULES_PHASE0, GS_ERR_ARG,
+             "rules must be GS_RULES_TOY2D or GS_RULES_PHASE0 (got %d)", rules);
+  GS_REQUIRE(dtype == GS_FLOAT32 || dtype == GS_FLOAT64, GS_ERR_ARG,
+             "dtype must be GS_FLOAT32 or GS_FLOAT64 (got %d)", dtype);
+  return GS_OK;
+}
+
+template <typename S>
+BlendArgs<S> make_args(const void* rec, const uint32_t* ranges, int range_stride,
+                       const uint32_t* point_list, const uint32_t* bucket_offsets, int W, int H,
+                       const double* bg) {
+  BlendArgs<S> a{};
+  a.rec = static_cast<const S*>(rec);
+  a.ranges = ranges;
+  a.range_stride = range_stride;
+  a.point_list = point_list;
+  a.bucket_offsets = bucket_offsets;
+  a.W = W;
+  a.H = H;
+  a.tiles_x = (W + kTile - 1) / kTile;
+  a.n_tiles = a.tiles_x * ((H + kTile - 1) / kTile);
+  a.bg0 = bg ? static_cast<S>(bg[0]) : S(0);
+  a.bg1 = bg ? static_cast<S>(bg[1]) : S(0);
+  a.bg2 = bg ? static_cast<S>(bg[2]) : S(0);
+  return a;
+}
+
+template <typename F>
+void dispatch2d(int rules, int dtype, F&& f) {
+  if (rules == GS_RULES_TOY2D) {
+    if (dtype == GS_FLOAT32) f(std::integral_constant<int, kRulesToy2D>{}, float{});
+    else f(std::integral_constant<int, kRulesToy2D>{}, double{});
+  } else {
+    if (dtype == GS_FLOAT32) f(std::integral_constant<int, kRulesPhase0>{}, float{});
+    else f(std::integral_constant<int, kRulesPhase0>{}, double{});
+  }
+}
+
+}  // namespace
 
 extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
                                const uint32_t* point_list, const uint32_t* bucket_offsets,
@@ -267,15 +522,16 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
   // splat_rec, point_list and ckpt may be NULL when the scene has no instances
   GS_REQUIRE(ranges && bucket_offsets && image && final_T && n_contrib && tile_max, GS_ERR_ARG,
              "null pointer argument");
-  GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16) && aligned(ranges, 8), GS_ERR_ALIGN,
-             "splat_rec/ckpt must be 16-byte and ranges 8-byte aligned");
-  const int tiles_x = (width + kTile - 1) / kTile, tiles_y = (height + kTile - 1) / kTile;
-  const float br = bg ? bg[0] : 0.0f, bgg = bg ? bg[1] : 0.0f, bb = bg ? bg[2] : 0.0f;
-  hipLaunchKernelGGL(blend_fwd_3d_kernel, dim3(tiles_x * tiles_y), dim3(kTilePixels), 0,
-                     as_stream(stream), reinterpret_cast<const SplatRec*>(splat_rec),
-                     reinterpret_cast<const uint2*>(ranges), point_list, bucket_offsets, width,
-                     height, tiles_x, br, bgg, bb, image, final_T, n_contrib, tile_max,
-                     reinterpret_cast<float4*>(ckpt));
+  GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16), GS_ERR_ALIGN,
+             "splat_rec and ckpt must be 16-byte aligned");
+  const double bgd[3] = {bg ? bg[0] : 0.0, bg ? bg[1] : 0.0, bg ? bg[2] : 0.0};
+  BlendArgs<float> a = make_args<float>(splat_rec, ranges, 2, point_list, bucket_offsets, width, height, bgd);
+  a.image = image;
+  a.final_T = final_T;
+  a.n_contrib = n_contrib;
+  a.tile_max = tile_max;
+  a.ckpt = ckpt;
+  launch_fwd<kRules3D, float>(a, as_stream(stream));
   return check_launch("blend_fwd_3d");
 }
 
@@ -298,14 +554,127 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
   GS_REQUIRE(ranges && bucket_offsets && bucket_to_tile && image && grad_image && n_contrib &&
                  tile_max && (final_T || !grad_alpha),
              GS_ERR_ARG, "null pointer argument");
-  GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16) && aligned(ranges, 8), GS_ERR_ALIGN,
-             "splat_rec/ckpt must be 16-byte and ranges 8-byte aligned");
-  const int tiles_x = (width + kTile - 1) / kTile, tiles_y = (height + kTile - 1) / kTile;
-  const int64_t blocks = (n_buckets_max + kBwdWaves - 1) / kBwdWaves;
-  hipLaunchKernelGGL(blend_bwd_3d_kernel, dim3(static_cast<unsigned>(blocks)),
-                     dim3(kBwdWaves * kWave), 0, st, reinterpret_cast<const SplatRec*>(splat_rec),
-                     reinterpret_cast<const uint2*>(ranges), point_list, bucket_offsets,
-                     bucket_to_tile, tiles_x * tiles_y, width, height, tiles_x, image, grad_image,
-                     final_T, grad_alpha, n_contrib, tile_max, reinterpret_cast<const float4*>(ckpt), grad2d);
+  GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16), GS_ERR_ALIGN,
+             "splat_rec and ckpt must be 16-byte aligned");
+  BlendArgs<float> a = make_args<float>(splat_rec, ranges, 2, point_list, bucket_offsets, width, height, nullptr);
+  a.image = const_cast<float*>(image);
+  a.final_T = const_cast<float*>(final_T);
+  a.n_contrib = const_cast<int32_t*>(n_contrib);
+  a.tile_max = const_cast<uint32_t*>(tile_max);
+  a.ckpt = const_cast<float*>(ckpt);
+  a.bucket_to_tile = bucket_to_tile;
+  a.n_buckets_dev = bucket_offsets + a.n_tiles;
+  a.n_buckets = n_buckets_max;
+  a.grad_image = grad_image;
+  a.grad_alpha = grad_alpha;
+  a.grad_rec = grad2d;
+  launch_bwd_bucket<kRules3D, float>(a, st);
   return check_launch("blend_bwd_3d");
+}
+
+extern "C" int gs2d_blend_fwd(int rules, int dtype, const void* rec, const uint32_t* ranges,
+                              int range_stride, const uint32_t* point_list,
+                              const uint32_t* bucket_offsets, int width, int height,
+                              const double* bg, void* image, void* final_T, int32_t* n_contrib,
+                              int32_t* last_contrib, uint32_t* tile_max, void* ckpt,
+                              unsigned long long* counters, void* stream) {
+  clear_error();
+  if (int e = check_rules(rules, dtype)) return e;
+  GS_REQUIRE(width > 0 && height > 0 && (range_stride == 1 || range_stride == 2), GS_ERR_ARG,
+             "invalid image size or range stride");
+  GS_REQUIRE(ranges && image && final_T && n_contrib && (bucket_offsets || !ckpt), GS_ERR_ARG,
+             "null pointer argument");
+  GS_REQUIRE(aligned(rec, 16) && aligned(ckpt, 16), GS_ERR_ALIGN, "rec and ckpt must be 16-byte aligned");
+  int rc = GS_OK;
+  dispatch2d(rules, dtype, [&](auto rr, auto s) {
+    using S = decltype(s);
+    constexpr int R = decltype(rr)::value;
+    BlendArgs<S> a = make_args<S>(rec, ranges, range_stride, point_list, bucket_offsets, width, height, bg);
+    a.image = static_cast<S*>(image);
+    a.final_T = static_cast<S*>(final_T);
+    a.n_contrib = n_contrib;
+    a.last_contrib = last_contrib;
+    a.tile_max = tile_max;
+    a.ckpt = static_cast<S*>(ckpt);
+    a.counters = counters;
+    launch_fwd<R, S>(a, as_stream(stream));
+    rc = check_launch("gs2d_blend_fwd");
+  });
+  return rc;
+}
+
+extern "C" int gs2d_blend_bwd_bucket(int rules, int dtype, const void* rec, const uint32_t* ranges,
+                                     int range_stride, const uint32_t* point_list,
+                                     const uint32_t* bucket_offsets, const uint32_t* bucket_to_tile,
+                                     int64_t n_buckets, int64_t n, int width, int height,
+                                     const void* image, const void* grad_image, const int32_t* limit,
+                                     const uint32_t* tile_max, const void* ckpt, void* grad_rec,
+                                     unsigned long long* counters, void* stream) {
+  clear_error();
+  if (int e = check_rules(rules, dtype)) return e;
+  GS_REQUIRE(width > 0 && height > 0 && n >= 0 && n_buckets >= 0 &&
+                 (range_stride == 1 || range_stride == 2),
+             GS_ERR_ARG, "invalid sizes");
+  GS_REQUIRE(grad_rec || n == 0, GS_ERR_ARG, "null grad_rec");
+  hipStream_t st = as_stream(stream);
+  const size_t esz = dtype == GS_FLOAT64 ? 8 : 4;
+  if (n > 0) fill_zero_f32(static_cast<float*>(grad_rec), n * kGrad2D * static_cast<int64_t>(esz / 4), st);
+  if (int e = check_launch("gs2d_blend_bwd_bucket (zero fill)")) return e;
+  if (n_buckets == 0 || n == 0) return GS_OK;
+  GS_REQUIRE(rec && ranges && point_list && bucket_offsets && bucket_to_tile && image && grad_image && ckpt &&
+                 (limit || rules == GS_RULES_PHASE0),
+             GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(aligned(rec, 16) && aligned(ckpt, 16), GS_ERR_ALIGN, "rec and ckpt must be 16-byte aligned");
+  int rc = GS_OK;
+  dispatch2d(rules, dtype, [&](auto rr, auto s) {
+    using S = decltype(s);
+    constexpr int R = decltype(rr)::value;
+    BlendArgs<S> a = make_args<S>(rec, ranges, range_stride, point_list, bucket_offsets, width, height, nullptr);
+    a.image = const_cast<S*>(static_cast<const S*>(image));
+    a.n_contrib = const_cast<int32_t*>(limit);
+    a.tile_max = const_cast<uint32_t*>(tile_max);
+    a.ckpt = const_cast<S*>(static_cast<const S*>(ckpt));
+    a.counters = counters;
+    a.bucket_to_tile = bucket_to_tile;
+    a.n_buckets = n_buckets;
+    a.grad_image = static_cast<const S*>(grad_image);
+    a.grad_rec = static_cast<S*>(grad_rec);
+    launch_bwd_bucket<R, S>(a, st);
+    rc = check_launch("gs2d_blend_bwd_bucket");
+  });
+  return rc;
+}
+
+extern "C" int gs2d_blend_bwd_pixel(int rules, int dtype, const void* rec, const uint32_t* ranges,
+                                    int range_stride, const uint32_t* point_list, int64_t n,
+                                    int width, int height, const double* bg, const void* final_T,
+                                    const int32_t* limit, const void* grad_image, void* grad_rec,
+                                    unsigned long long* counters, void* stream) {
+  clear_error();
+  if (int e = check_rules(rules, dtype)) return e;
+  GS_REQUIRE(width > 0 && height > 0 && n >= 0 && (range_stride == 1 || range_stride == 2),
+             GS_ERR_ARG, "invalid sizes");
+  GS_REQUIRE(grad_rec || n == 0, GS_ERR_ARG, "null grad_rec");
+  hipStream_t st = as_stream(stream);
+  const size_t esz = dtype == GS_FLOAT64 ? 8 : 4;
+  if (n > 0) fill_zero_f32(static_cast<float*>(grad_rec), n * kGrad2D * static_cast<int64_t>(esz / 4), st);
+  if (int e = check_launch("gs2d_blend_bwd_pixel (zero fill)")) return e;
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(rec && ranges && point_list && final_T && limit && grad_image, GS_ERR_ARG,
+             "null pointer argument");
+  GS_REQUIRE(aligned(rec, 16), GS_ERR_ALIGN, "rec must be 16-byte aligned");
+  int rc = GS_OK;
+  dispatch2d(rules, dtype, [&](auto rr, auto s) {
+    using S = decltype(s);
+    constexpr int R = decltype(rr)::value;
+    BlendArgs<S> a = make_args<S>(rec, ranges, range_stride, point_list, nullptr, width, height, bg);
+    a.final_T = const_cast<S*>(static_cast<const S*>(final_T));
+    a.n_contrib = const_cast<int32_t*>(limit);
+    a.counters = counters;
+    a.grad_image = static_cast<const S*>(grad_image);
+    a.grad_rec = static_cast<S*>(grad_rec);
+    launch_bwd_pixel<R, S>(a, st);
+    rc = check_launch("gs2d_blend_bwd_pixel");
+  });
+  return rc;
 }

@@ -2,15 +2,15 @@
 //
 // Numerics policy. Every decision the rasterizer takes (tile membership, alpha >= 1/255,
 // early termination) must come out the same on the GPU and in the CPU oracle, so the
-// forward path uses only correctly rounded IEEE operations: +, -, *, fmaf, IEEE division
-// and sqrt, rint and ldexp. Transcendentals are evaluated by the polynomial routines
-// below instead of the hardware v_exp_f32 / v_log_f32 approximations, whose last bits are
-// not specified. The library is compiled with -ffp-contract=off, so every fused
-// multiply-add is an explicit fmaf().
+// forward path uses only correctly rounded IEEE operations: +, -, *, fma, IEEE division
+// and sqrt, rint and ldexp; transcendentals come from gs_math.h. The library is compiled
+// with -ffp-contract=off, so every fused multiply-add is an explicit fma().
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "gs_math.h"
 
 namespace gs {
 
@@ -30,75 +30,6 @@ constexpr float kTStop = 1e-4f;
 constexpr float kAlphaMax2D = 0.99f;          // 2D rule sets clamp alpha at 0.99
 constexpr float kOneMinusAlphaEps = 1e-6f;    // 3D backward floors (1 - alpha)
 constexpr float kDilation = 0.3f;             // screen-space low-pass added to cov2d
-
-constexpr float kLog2e = 1.44269504f;
-constexpr float kNegHalfLog2e = -0.72134752f;
-constexpr float kNegLog2e = -1.44269504f;
-constexpr float kLn2 = 0.693147182f;
-constexpr float kSqrt2 = 1.41421354f;
-
-// Degree-6 polynomial for 2^f on [-0.5, 0.5] (Chebyshev interpolant, float32 Horner error
-// below 0.7 ulp).
-constexpr float kP0 = 1.0f;
-constexpr float kP1 = 0.6931471824645996f;
-constexpr float kP2 = 0.24022650718688965f;
-constexpr float kP3 = 0.05550327152013779f;
-constexpr float kP4 = 0.00961802527308464f;
-constexpr float kP5 = 0.0013400432653725147f;
-constexpr float kP6 = 0.00015469732170458883f;
-
-__device__ __forceinline__ float poly_exp2_frac(float f) {
-  float p = kP6;
-  p = fmaf(p, f, kP5);
-  p = fmaf(p, f, kP4);
-  p = fmaf(p, f, kP3);
-  p = fmaf(p, f, kP2);
-  p = fmaf(p, f, kP1);
-  p = fmaf(p, f, kP0);
-  return p;
-}
-
-// 2^x for x <= 0, with x clamped at -64 so the result stays a normal float.
-__device__ __forceinline__ float exp2_neg(float x) {
-  x = fmaxf(x, -64.0f);
-  const float k = rintf(x);
-  const float f = x - k;  // exact: |f| <= 0.5
-  return ldexpf(poly_exp2_frac(f), static_cast<int>(k));
-}
-
-// 2^x for x clamped to [-126, 126].
-__device__ __forceinline__ float exp2_any(float x) {
-  x = fminf(fmaxf(x, -126.0f), 126.0f);
-  const float k = rintf(x);
-  const float f = x - k;
-  return ldexpf(poly_exp2_frac(f), static_cast<int>(k));
-}
-
-__device__ __forceinline__ float exp_any(float x) { return exp2_any(x * kLog2e); }
-
-__device__ __forceinline__ float sigmoid(float z) { return 1.0f / (1.0f + exp_any(-z)); }
-
-// Natural log of a positive normal float: x = 2^e m, m in [sqrt(1/2), sqrt(2)],
-// ln m = 2 atanh(s) with s = (m - 1) / (m + 1), |s| <= 0.1716, series to s^9.
-__device__ __forceinline__ float log_pos(float x) {
-  const uint32_t bits = __float_as_uint(x);
-  int e = static_cast<int>((bits >> 23) & 0xffu) - 127;
-  float m = __uint_as_float((bits & 0x007fffffu) | 0x3f800000u);
-  if (m > kSqrt2) {
-    m = m * 0.5f;
-    e = e + 1;
-  }
-  const float s = (m - 1.0f) / (m + 1.0f);
-  const float s2 = s * s;
-  float p = 1.0f / 9.0f;
-  p = fmaf(p, s2, 1.0f / 7.0f);
-  p = fmaf(p, s2, 1.0f / 5.0f);
-  p = fmaf(p, s2, 1.0f / 3.0f);
-  p = fmaf(p, s2, 1.0f);
-  float t = s * p;
-  t = t + t;
-  return fmaf(static_cast<float>(e), kLn2, t);
-}
 
 // ---------------------------------------------------------------------------------------
 // 3D splat record written by the preprocess (64 bytes, one per Gaussian):
@@ -121,9 +52,10 @@ constexpr int kRecFloats = 16;
 //   [9,10] sum over pixels of |dL/dmean2d| (densification statistic), [11] unused
 constexpr int kGrad2D = 12;
 
-// Orderable 32-bit image of a float: unsigned order equals float order.
+// Orderable 32-bit image of a float: unsigned order equals float order, and -0 and +0 map
+// to one key (they compare equal, so a stable sort keeps them in input order).
 __device__ __forceinline__ uint32_t float_order_key(float v) {
-  const uint32_t u = __float_as_uint(v);
+  const uint32_t u = __float_as_uint(v + 0.0f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 

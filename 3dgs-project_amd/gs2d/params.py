@@ -1,0 +1,52 @@
+"""Learnable 2D Gaussians and their activation (caller side of the rasterizer; the same
+parametrisation and seeded initialisation as toy2d/gs2d/params.py:16-59, so a seed gives
+the same Gaussians as the reference).
+
+The rasterizer sees four tensors per Gaussian: means [N,2] (pixels), conic [N,3] = (A, B, C)
+of the inverse covariance [[A, B], [B, C]], color [N,3] in [0,1], opacity [N] in [0,1].
+"""
+import math
+
+import torch
+
+
+class Gaussians2D(torch.nn.Module):
+    def __init__(self, n: int, H: int, W: int, seed: int = 0, dtype=torch.float32):
+        super().__init__()
+        gen = torch.Generator().manual_seed(seed)
+        spacing = math.sqrt(H * W / n) * 0.5
+        # draw order: positions, scales, angles, colours, opacities, depths
+        self.xy = torch.nn.Parameter(torch.rand(n, 2, generator=gen, dtype=dtype) * torch.tensor([W, H], dtype=dtype))
+        self.log_scale = torch.nn.Parameter(torch.log(spacing * (0.5 + torch.rand(n, 2, generator=gen, dtype=dtype))))
+        self.theta = torch.nn.Parameter(torch.rand(n, generator=gen, dtype=dtype) * math.pi)
+        self.rgb_logit = torch.nn.Parameter(0.5 * torch.randn(n, 3, generator=gen, dtype=dtype))
+        self.opacity_logit = torch.nn.Parameter(0.5 * torch.randn(n, generator=gen, dtype=dtype))
+        # fixed draw order: smaller depth is in front
+        self.register_buffer("depth", torch.rand(n, generator=gen, dtype=dtype))
+
+    def activated(self):
+        return activate(self.xy, self.log_scale, self.theta, self.rgb_logit, self.opacity_logit)
+
+
+def activate(xy, log_scale, theta, rgb_logit, opacity_logit):
+    """(means, conic, color, opacity, cov): cov = (xx, xy, yy) of R diag(s^2) R^T."""
+    var = torch.exp(2.0 * log_scale)
+    c, s = torch.cos(theta), torch.sin(theta)
+    vx, vy = var[:, 0], var[:, 1]
+    cxx = c * c * vx + s * s * vy
+    cxy = c * s * (vx - vy)
+    cyy = s * s * vx + c * c * vy
+    det = cxx * cyy - cxy * cxy
+    conic = torch.stack([cyy / det, -cxy / det, cxx / det], dim=-1)
+    return xy, conic, torch.sigmoid(rgb_logit), torch.sigmoid(opacity_logit), torch.stack([cxx, cxy, cyy], dim=-1)
+
+
+@torch.no_grad()
+def radii_from_cov(cov: torch.Tensor) -> torch.Tensor:
+    """Integer 3-sigma radius of the larger eigenvalue (0 for a degenerate covariance)."""
+    cxx, cxy, cyy = cov.unbind(-1)
+    det = cxx * cyy - cxy * cxy
+    mid = 0.5 * (cxx + cyy)
+    lam = mid + torch.sqrt(torch.clamp(mid * mid - det, min=0.1))
+    r = torch.ceil(3.0 * torch.sqrt(lam))
+    return torch.where(det > 0, r, torch.zeros_like(r)).to(torch.int32)

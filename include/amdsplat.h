@@ -35,6 +35,14 @@ enum {
   GS_ERR_ALIGN = 4       /* a pointer does not have the required alignment */
 };
 
+/* Rule sets (the three operator surfaces) and floating types of the 2D entry points. */
+enum {
+  GS_RULES_3D = 0,      /* 3D rasterize: Faster-GS rules (phase1/fastergs_macro.patch:181-205) */
+  GS_RULES_TOY2D = 1,   /* gs2d.rasterize: toy2d/csrc/rasterize.cu:37-101, toy2d/gs2d/reference.py:3-8 */
+  GS_RULES_PHASE0 = 2   /* splat2d.render: phase0/csrc/macrotile/splat2d_common.h:7-11 */
+};
+enum { GS_FLOAT32 = 0, GS_FLOAT64 = 1 };
+
 /* Pinhole camera. viewmat is the row-major 4x4 world-to-camera matrix with OpenCV axes
  * (x right, y down, z forward); pixel (i, j) covers [i, i+1) x [j, j+1), so its centre is
  * at (i + 0.5, j + 0.5). */
@@ -102,14 +110,18 @@ int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, int64_
 /* Rectangle binning for the 2D operators (replaces toy2d/gs2d/binning.py:34-88, whose
  * per-tile lists are ordered by a stable depth rank, and phase0/splat2d/ops.py:206-255, whose
  * lists are in index order). rects [n,4] int32 = (tx0, ty0, tx1, ty1) tile rectangle, max
- * exclusive, 16-byte aligned; depth [n] (NULL = index order). counts from gs_rect_counts.
- * Outputs as gs_bin_fill_3d; the depth key is the orderable image of the float depth. */
+ * exclusive, 16-byte aligned (clipped to the grid); depth [n] of depth_dtype (NULL = index
+ * order); counts from gs2d_rects_toy / gs2d_rects_phase0 / gs_rect_counts. Outputs as
+ * gs_bin_fill_3d, plus (each may be NULL) tile_offsets [T+1] (CSR form of ranges) and
+ * order [n] = the stable argsort of depth (toy2d Bins.order). sorted_keys needs a float32
+ * depth. Ranges of empty tiles are empty ranges at their CSR position. */
 int gs_rect_counts(const int32_t* rects, int64_t n, int tiles_x, int tiles_y, uint32_t* counts,
                    void* stream);
-int gs_bin_fill_rect(const int32_t* rects, const float* depth, const uint32_t* counts, int64_t n,
-                     int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
-                     uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
-                     void* workspace, size_t workspace_bytes, void* stream);
+int gs_bin_fill_rect(const int32_t* rects, const void* depth, int depth_dtype, const uint32_t* counts,
+                     int64_t n, int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
+                     uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
+                     uint32_t* bucket_offsets, uint32_t* order, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* bucket_to_tile[b] = tile of bucket b, for b < bucket_offsets[n_tiles] (read on device);
  * entries up to n_buckets_max are written, unused ones with 0xffffffff. */
@@ -155,6 +167,68 @@ int gs_preprocess_bwd(const float* means, const float* log_scales, const float* 
                       const uint32_t* tiles_touched, const float* grad2d, float* grad_means,
                       float* grad_log_scales, float* grad_quats, float* grad_opacity_logits,
                       float* grad_sh, void* stream);
+
+/* =======================================================================================
+ * 2D surfaces (rules GS_RULES_TOY2D / GS_RULES_PHASE0; dtype GS_FLOAT32 / GS_FLOAT64)
+ * ===================================================================================== */
+
+/* toy2d tile rectangles from the 3-sigma radius (replaces the getRect part of
+ * toy2d/gs2d/binning.py:44-57): means [n,2] float32 (8-byte aligned), radii [n] int32 ->
+ * rects [n,4] (xmin, ymin, xmax, ymax in tiles, max exclusive, empty = collapsed to
+ * (xmin, ymin)), counts [n] = tiles covered. */
+int gs2d_rects_toy(const float* means, const int32_t* radii, int64_t n, int width, int height,
+                   int32_t* rects, uint32_t* counts, void* stream);
+
+/* phase0 tile rectangles of the alpha >= 1/255 ellipse bounding box with one pixel of slack,
+ * evaluated in float64 (replaces phase0/splat2d/ops.py:206-235): means [n,2], chol [n,3],
+ * opacity_logit [n] of dtype -> rects [n,4] (tx0, ty0, tx1+1, ty1+1), counts [n]. */
+int gs2d_rects_phase0(int dtype, const void* means, const void* chol, const void* opacity_logit,
+                      int64_t n, int width, int height, int32_t* rects, uint32_t* counts, void* stream);
+
+/* Splat records rec [n,16] of dtype (16-byte aligned) from the 2D parameters: toy2d
+ * (means [n,2], conic [n,3], color [n,3], opacity [n]); phase0 (means [n,2], chol [n,3],
+ * colors [n,3], opacity_logit [n]; the record holds sigmoid(logit)). */
+int gs2d_pack(int rules, int dtype, const void* means, const void* shape, const void* color,
+              const void* opacity, int64_t n, void* rec, void* stream);
+
+/* 2D forward blend (replaces toy2d rasterize_forward, toy2d/csrc/rasterize.cu:366-394, and
+ * phase0 forward, phase0/csrc/macrotile/bindings.cpp:156-178). Tile t's list is
+ * point_list[ranges[t*range_stride] .. ranges[t*range_stride+1]) (range_stride 2 for (T,2)
+ * ranges, 1 for (T+1) CSR offsets). Outputs: image ([3,H,W] toy2d, [H,W,3] phase0) of dtype,
+ * final_T [H,W], n_contrib [H,W] (toy2d: last list position + 1; phase0: number of splats),
+ * last_contrib [H,W] (phase0, may be NULL), tile_max [T] (may be NULL), ckpt [B,256,4]
+ * (toy2d (T, C); phase0 (C, T); NULL = not saved; bucket_offsets [T+1] needed with it).
+ * bg: 3 host doubles (toy2d) or NULL. counters: NULL or 3 device uint64 (atomic adds,
+ * checkpoint bytes, splat-pixel evaluations) that the kernels add to
+ * (phase0/csrc/macrotile/splat2d_common.h:260-266). */
+int gs2d_blend_fwd(int rules, int dtype, const void* rec, const uint32_t* ranges, int range_stride,
+                   const uint32_t* point_list, const uint32_t* bucket_offsets, int width, int height,
+                   const double* bg, void* image, void* final_T, int32_t* n_contrib,
+                   int32_t* last_contrib, uint32_t* tile_max, void* ckpt,
+                   unsigned long long* counters, void* stream);
+
+/* 2D bucketed backward (replaces toy2d rasterize_backward_splat, toy2d/csrc/rasterize.cu:
+ * 419-448, and phase0 backward_splat, phase0/csrc/macrotile/bindings.cpp:201-220). One
+ * wavefront per 32-entry bucket; limit [H,W] = list position + 1 of each pixel's last splat
+ * (toy2d n_contrib, phase0 last_contrib); tile_max may be NULL. grad_rec [n,12] of dtype is
+ * zeroed by the call and receives dL/d(mean 2, shape 3, opacity, colour 3) in slots 0..8
+ * (phase0: the opacity slot holds dL/dlogit). */
+int gs2d_blend_bwd_bucket(int rules, int dtype, const void* rec, const uint32_t* ranges,
+                          int range_stride, const uint32_t* point_list,
+                          const uint32_t* bucket_offsets, const uint32_t* bucket_to_tile,
+                          int64_t n_buckets, int64_t n, int width, int height, const void* image,
+                          const void* grad_image, const int32_t* limit, const uint32_t* tile_max,
+                          const void* ckpt, void* grad_rec, unsigned long long* counters,
+                          void* stream);
+
+/* 2D per-pixel backward (replaces toy2d rasterize_backward_pixel, toy2d/csrc/rasterize.cu:
+ * 396-417, and phase0 backward_pixel, phase0/csrc/macrotile/bindings.cpp:180-199): back to
+ * front, T recovered by division, one atomic per parameter per (pixel, splat) pair. */
+int gs2d_blend_bwd_pixel(int rules, int dtype, const void* rec, const uint32_t* ranges,
+                         int range_stride, const uint32_t* point_list, int64_t n, int width,
+                         int height, const double* bg, const void* final_T, const int32_t* limit,
+                         const void* grad_image, void* grad_rec, unsigned long long* counters,
+                         void* stream);
 
 #ifdef __cplusplus
 }

@@ -450,13 +450,18 @@ int64_t or_bin(const float* rec, const uint32_t* touched, int64_t n, const or_ca
     return -1;
   }
   qsort(inst, (size_t)m, sizeof(Inst), inst_cmp);
+  /* CSR ranges: tile t holds [start, end); an empty tile has an empty range at its position */
   for (int t = 0; t < 2 * n_tiles; ++t) ranges[t] = 0;
   for (int64_t p = 0; p < m; ++p) {
     keys_out[p] = inst[p].key;
     point_list[p] = inst[p].val;
-    uint32_t t = (uint32_t)(inst[p].key >> 32);
-    if (p == 0 || (uint32_t)(inst[p - 1].key >> 32) != t) ranges[2 * t] = (uint32_t)p;
-    if (p == m - 1 || (uint32_t)(inst[p + 1].key >> 32) != t) ranges[2 * t + 1] = (uint32_t)(p + 1);
+    ranges[2 * (inst[p].key >> 32) + 1]++;
+  }
+  uint32_t run = 0;
+  for (int t = 0; t < n_tiles; ++t) {
+    ranges[2 * t] = run;
+    run += ranges[2 * t + 1];
+    ranges[2 * t + 1] = run;
   }
   free(inst);
   bucket_offsets[0] = 0;

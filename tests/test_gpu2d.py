@@ -1,0 +1,293 @@
+"""GPU parity of the 2D surfaces (gs2d with toy2d rules, splat2d with phase0 rules): the HIP
+kernels, called through the C ABI by the drop-in packages, against the golden fixtures of the
+reference's own Python code and against the CPU oracle.
+
+Bars: binning (rectangles, depth order, lists, ranges, buckets) bit-exact; per-pixel counts
+bit-exact against the oracle; float32 images and gradients within the reference's 1e-5 gate
+(toy2d/tests/test_cuda.py:8-31, phase0/tests/gradcheck/test_gradcheck.py:62-70); float64
+within 1e-12 (forward) / 1e-10 (gradients) (test_gradcheck.py:73-100).
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle2d as O2
+import gs2d
+import splat2d
+from gs2d.params import Gaussians2D, radii_from_cov
+from splat2d import ops as P0
+
+pytestmark = pytest.mark.gpu
+
+GOLD = Path(__file__).resolve().parent / "golden"
+TOY = ["tiny", "sparse_odd", "dense", "opaque"]
+PH0 = [f"seed{s}_n{n}" for s in (0, 1, 2) for n in (8, 32)] + ["dense_n96", "sparse_n150"]
+
+
+def load(name):
+    with np.load(GOLD / f"{name}.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def rel(a, b):
+    a = a.detach().double().cpu().numpy() if torch.is_tensor(a) else np.asarray(a, np.float64)
+    b = b.detach().double().cpu().numpy() if torch.is_tensor(b) else np.asarray(b, np.float64)
+    nb = np.linalg.norm(b.ravel())
+    d = np.linalg.norm((a - b).ravel())
+    return float(d / nb) if nb > 0 else float(d)
+
+
+def cuda(a, dtype=None):
+    t = torch.as_tensor(a).cuda()
+    return t.to(dtype) if dtype is not None else t
+
+
+# ---------------------------------------------------------------------------------------
+# toy2d / gs2d
+# ---------------------------------------------------------------------------------------
+def toy_bins(f):
+    return gs2d.bin_gaussians(cuda(f["means"]), cuda(f["radii"]), cuda(f["depth"]), int(f["H"]), int(f["W"]))
+
+
+@pytest.mark.parametrize("name", TOY)
+def test_gs2d_binning_bit_exact(name):
+    f = load(f"toy2d_{name}")
+    b = toy_bins(f)
+    torch.cuda.synchronize()
+    assert np.array_equal(b.rect.cpu().numpy(), f["rect"])
+    assert np.array_equal(b.order.cpu().numpy(), f["order"])
+    assert np.array_equal(b.point_list.cpu().numpy(), f["point_list"])
+    assert np.array_equal(b.ranges.cpu().numpy(), f["ranges"])
+    assert np.array_equal(b.bucket_offsets.cpu().numpy(), f["bucket_offsets"])
+    assert np.array_equal(b.bucket_to_tile.cpu().numpy(), f["bucket_to_tile"])
+    assert b.num_buckets == int(f["num_buckets"])
+
+
+@pytest.mark.parametrize("backend", ["splat", "pixel"])
+@pytest.mark.parametrize("name", TOY)
+def test_gs2d_float32_matches_reference(name, backend):
+    """toy2d/tests/test_cuda.py:17-31: fp32 GPU vs the fp64 reference, rel err < 1e-5."""
+    f = load(f"toy2d_{name}")
+    bins = toy_bins(f)
+    x = [cuda(f[k], torch.float32).requires_grad_(True) for k in ("means", "conic", "color", "opacity")]
+    out = gs2d.rasterize(*x, bins, cuda(f["bg"], torch.float32), backend=backend)
+    assert rel(out, f["image"]) < 1e-5
+    grads = torch.autograd.grad(out, x, cuda(f["dout"], torch.float32))
+    for key, g in zip(("g_means", "g_conic", "g_color", "g_opacity"), grads):
+        assert rel(g, f[key]) < 1e-5, f"{backend}/{name}/{key}: {rel(g, f[key]):.2e}"
+
+
+@pytest.mark.parametrize("backend", ["splat", "pixel"])
+@pytest.mark.parametrize("name", TOY)
+def test_gs2d_float64(name, backend):
+    f = load(f"toy2d_{name}")
+    bins = toy_bins(f)
+    x = [cuda(f[k]).requires_grad_(True) for k in ("means", "conic", "color", "opacity")]
+    out = gs2d.rasterize(*x, bins, cuda(f["bg"]), backend=backend)
+    assert rel(out, f["image"]) < 1e-12
+    grads = torch.autograd.grad(out, x, cuda(f["dout"]))
+    for key, g in zip(("g_means", "g_conic", "g_color", "g_opacity"), grads):
+        assert rel(g, f[key]) < 1e-9, f"{backend}/{name}/{key}: {rel(g, f[key]):.2e}"
+
+
+@pytest.mark.parametrize("name", TOY)
+def test_gs2d_forward_matches_oracle_bit_for_bit(name):
+    f = load(f"toy2d_{name}")
+    bins = toy_bins(f)
+    W, H = int(f["W"]), int(f["H"])
+    p32 = [f[k].astype(np.float32) for k in ("means", "conic", "color", "opacity")]
+    e = gs2d.raster.ext()
+    out, fT, nc, bstate = e.forward(*[cuda(a) for a in p32], cuda(f["bg"], torch.float32), bins.ranges,
+                                    bins.point_list, bins.bucket_offsets, bins.num_buckets, H, W, True)
+    rects, _ = O2.rects_toy(f["means"].astype(np.float32), f["radii"], W, H)
+    order, pl, ranges, boff = O2.bin_rects(rects, f["depth"], W, H)
+    ref = O2.forward(O2.TOY2D, *p32, pl, ranges, boff, W, H, bg=f["bg"])
+    assert np.array_equal(nc.cpu().numpy(), ref["n_contrib"])
+    assert np.abs(out.cpu().numpy() - ref["image"]).max() <= 1e-6
+    assert np.abs(fT.cpu().numpy() - ref["final_T"]).max() <= 1e-6
+    # checkpoints the backward reads (bucket start < the pixel's n_contrib)
+    ck, rck = bstate.cpu().numpy(), ref["ckpt"]
+    for tile in range(len(ranges)):
+        for b in range(int(boff[tile]), int(boff[tile + 1])):
+            bstart = (b - int(boff[tile])) * 32
+            tx, ty = tile % ((W + 15) // 16), tile // ((W + 15) // 16)
+            for t in range(256):
+                px, py = tx * 16 + t % 16, ty * 16 + t // 16
+                if px < W and py < H and ref["n_contrib"][py, px] > bstart:
+                    assert np.abs(ck[b, t] - rck[b, t]).max() <= 1e-6
+
+
+def test_gs2d_bench_scene_against_oracle():
+    """512x512, 50k Gaussians of the reference benchmark: pair / bucket counts of its results
+    file, bit-exact lists and counts, forward within 1e-5, gradients within 1e-4 (atomic order)."""
+    rows = json.loads((GOLD / "toy2d_bench_counts.json").read_text())["rows"]
+    row = rows[1]
+    S, n = row["size"], row["n"]
+    g = Gaussians2D(n, S, S, seed=0)
+    with torch.no_grad():
+        means, conic, color, opacity, cov = (t.detach() for t in g.activated())
+        radii = radii_from_cov(cov)
+    bins = gs2d.bin_gaussians(means.cuda(), radii.cuda(), g.depth.cuda(), S, S)
+    assert bins.point_list.numel() == row["pairs"] and bins.num_buckets == row["buckets"]
+    rects, _ = O2.rects_toy(means.numpy(), radii.numpy(), S, S)
+    order, pl, ranges, boff = O2.bin_rects(rects, g.depth.numpy(), S, S)
+    assert np.array_equal(bins.point_list.cpu().numpy(), pl)
+    x = [t.cuda().requires_grad_(True) for t in (means, conic, color, opacity)]
+    bg = torch.tensor([0.2, 0.5, 0.8])
+    out = gs2d.rasterize(*x, bins, bg.cuda())
+    dout = torch.randn(3, S, S, generator=torch.Generator().manual_seed(1))
+    grads = torch.autograd.grad(out, x, dout.cuda())
+    p = [t.numpy() for t in (means, conic, color, opacity)]
+    ref = O2.forward(O2.TOY2D, *p, pl, ranges, boff, S, S, bg=bg.double().numpy())
+    assert np.abs(out.detach().cpu().numpy() - ref["image"]).max() <= 1e-5
+    gr, _ = O2.backward_bucket(O2.TOY2D, *p, pl, ranges, boff, S, S, ref["image"], dout.numpy(), ref["n_contrib"],
+                               ref["ckpt"])
+    for cols, gg in (((0, 1), grads[0]), ((2, 3, 4), grads[1]), ((6, 7, 8), grads[2]), ((5,), grads[3])):
+        assert rel(gg.reshape(-1, len(cols)), gr[:, list(cols)]) < 1e-4
+
+
+def test_gs2d_empty_scene():
+    means = torch.rand(50, 2, dtype=torch.float32) * 40
+    radii = torch.zeros(50, dtype=torch.int32)
+    bins = gs2d.bin_gaussians(means.cuda(), radii.cuda(), torch.rand(50).cuda(), 40, 40)
+    assert bins.point_list.numel() == 0 and bins.num_buckets == 0
+    x = [means.cuda().requires_grad_(True), torch.ones(50, 3).cuda().requires_grad_(True),
+         torch.rand(50, 3).cuda().requires_grad_(True), torch.rand(50).cuda().requires_grad_(True)]
+    bg = torch.tensor([0.2, 0.5, 0.8]).cuda()
+    out = gs2d.rasterize(*x, bins, bg)
+    assert torch.allclose(out, bg[:, None, None].expand_as(out))
+    grads = torch.autograd.grad(out.sum(), x)
+    assert all(float(g.abs().sum()) == 0.0 for g in grads)
+
+
+def test_gs2d_rejects_cpu_tensors():
+    with pytest.raises(RuntimeError, match="GPU"):
+        gs2d.bin_gaussians(torch.rand(4, 2), torch.ones(4, dtype=torch.int32), torch.rand(4), 16, 16)
+
+
+# ---------------------------------------------------------------------------------------
+# phase0 / splat2d
+# ---------------------------------------------------------------------------------------
+def ph0_params(f, dtype, grad=True):
+    return [cuda(f[k], dtype).requires_grad_(grad) for k in ("means", "chol", "opacity_logit", "colors")]
+
+
+@pytest.mark.parametrize("name", PH0)
+def test_splat2d_binning_bit_exact(name):
+    f = load(f"phase0_{name}")
+    m, c, l, _ = ph0_params(f, torch.float64, grad=False)
+    b = splat2d.bin_tiles(m, c, l, int(f["H"]), int(f["W"]))
+    torch.cuda.synchronize()
+    for key in ("tile_offsets", "tile_ids", "bucket_offsets", "bucket_tile"):
+        assert np.array_equal(getattr(b, key).cpu().numpy(), f[key]), key
+
+
+@pytest.mark.parametrize("mode", ["splat", "pixel"])
+@pytest.mark.parametrize("name", PH0)
+def test_splat2d_float32_and_float64(name, mode):
+    f = load(f"phase0_{name}")
+    H, W = int(f["H"]), int(f["W"])
+    for dtype, ftol, gtol in ((torch.float32, 1e-5, 1e-5), (torch.float64, 1e-12, 1e-10)):
+        params = ph0_params(f, dtype)
+        image = splat2d.render(*params, H, W, mode=mode)
+        assert rel(image, f["image"]) < ftol
+        grads = torch.autograd.grad(image, params, cuda(f["grad_image"], dtype))
+        for key, g in zip(("g_means", "g_chol", "g_opacity_logit", "g_colors"), grads):
+            assert rel(g, f[key]) < gtol, f"{name}/{mode}/{dtype}/{key}: {rel(g, f[key]):.2e}"
+
+
+@pytest.mark.parametrize("name", ["seed0_n8", "seed1_n32", "dense_n96"])
+def test_splat2d_modes_agree_and_counts(name):
+    """phase0/tests/gradcheck/test_gradcheck.py:84-92 (modes agree) and test_opcount.py:63-123
+    (n_contrib, atomic-count formulas, checkpoint bytes)."""
+    f = load(f"phase0_{name}")
+    H, W = int(f["H"]), int(f["W"])
+    ext = P0.load_extension()
+    for dtype, tol in ((torch.float32, 3e-6), (torch.float64, 1e-12)):
+        res = {}
+        for mode in ("pixel", "splat"):
+            params = ph0_params(f, dtype)
+            ext.reset_counters()
+            image = splat2d.render(*params, H, W, mode=mode)
+            res[mode] = torch.autograd.grad(image, params, cuda(f["grad_image"], dtype))
+            res[mode + "_ctr"] = ext.get_counters()
+        for a, b in zip(res["splat"], res["pixel"]):
+            assert rel(a, b) < tol
+        # counts from the oracle's emulation of the same thread mappings
+        b = splat2d.bin_tiles(*ph0_params(f, dtype, grad=False)[:3], H, W)
+        pl = b.tile_ids.cpu().numpy().astype(np.uint32)
+        toff = b.tile_offsets.cpu().numpy()
+        ranges = np.stack([toff[:-1], toff[1:]], 1).astype(np.uint32)
+        boff = b.bucket_offsets.cpu().numpy().astype(np.uint32)
+        npd = np.float64 if dtype == torch.float64 else np.float32
+        p = [f[k].astype(npd) for k in ("means", "chol", "colors", "opacity_logit")]
+        out = O2.forward(O2.PHASE0, *p, pl, ranges, boff, W, H)
+        _, at_b = O2.backward_bucket(O2.PHASE0, *p, pl, ranges, boff, W, H, out["image"],
+                                     f["grad_image"].astype(npd), out["last_contrib"], out["ckpt"])
+        _, at_p = O2.backward_pixel(O2.PHASE0, *p, pl, ranges, W, H, out["final_T"], out["last_contrib"],
+                                    f["grad_image"].astype(npd))
+        assert res["splat_ctr"]["atomic_adds"] == at_b
+        assert res["pixel_ctr"]["atomic_adds"] == at_p == int(out["n_contrib"].sum()) * 9
+        assert res["splat_ctr"]["checkpoint_bytes"] == b.num_buckets * 256 * 4 * (8 if dtype == torch.float64 else 4)
+
+
+@pytest.mark.parametrize("name", ["seed0_n8", "seed2_n8"])
+@pytest.mark.parametrize("mode", ["splat", "pixel"])
+def test_splat2d_gradcheck_float64(name, mode):
+    """phase0/tests/gradcheck/test_gradcheck.py:51-59 on the GPU."""
+    f = load(f"phase0_{name}")
+    H, W = int(f["H"]), int(f["W"])
+
+    def fn(means, chol, opacity_logit, colors):
+        return splat2d.render(means, chol, opacity_logit, colors, H, W, mode=mode)
+
+    assert torch.autograd.gradcheck(fn, tuple(ph0_params(f, torch.float64)), eps=1e-6, atol=1e-8, rtol=1e-6)
+
+
+def test_splat2d_extension_surface_and_limitless_backward():
+    """The extension functions of phase0/csrc/macrotile/bindings.cpp:156-239 with their return
+    values; backward_splat without a per-pixel limit (the reference's signature) equals the
+    autograd path's."""
+    f = load("phase0_sparse_n150")
+    H, W = int(f["H"]), int(f["W"])
+    m, c, l, col = ph0_params(f, torch.float32, grad=False)
+    b = splat2d.bin_tiles(m, c, l, H, W)
+    ext = P0.load_extension()
+    image, t_final, n_contrib, last_contrib, ckpt = ext.forward(m, c, l, col, b.tile_offsets, b.tile_ids,
+                                                                b.bucket_offsets, b.bucket_tile, H, W)
+    assert image.shape == (H, W, 3) and ckpt.shape == (b.num_buckets, 256, 4)
+    # float32 decisions against the float32 oracle (the float64 reference may flip a threshold)
+    toff = b.tile_offsets.cpu().numpy()
+    ranges = np.stack([toff[:-1], toff[1:]], 1).astype(np.uint32)
+    p32 = [f[k].astype(np.float32) for k in ("means", "chol", "colors", "opacity_logit")]
+    ref = O2.forward(O2.PHASE0, *p32, b.tile_ids.cpu().numpy().astype(np.uint32), ranges,
+                     b.bucket_offsets.cpu().numpy().astype(np.uint32), W, H)
+    assert np.array_equal(n_contrib.cpu().numpy(), ref["n_contrib"])
+    assert np.array_equal(last_contrib.cpu().numpy(), ref["last_contrib"])
+    assert np.abs(ckpt.cpu().numpy() - ref["ckpt"]).max() <= 1e-6
+    m64 = ph0_params(f, torch.float64, grad=False)
+    n64 = ext.forward(*m64, b.tile_offsets, b.tile_ids, b.bucket_offsets, b.bucket_tile, H, W)[2]
+    assert np.array_equal(n64.cpu().numpy(), f["n_contrib"])  # test_opcount.py:89-92
+    gi = cuda(f["grad_image"], torch.float32)
+    tabs = (b.tile_offsets, b.tile_ids, b.bucket_offsets, b.bucket_tile)
+    g_ref = ext.backward_splat(gi, m, c, l, col, *tabs, image, ckpt, H, W)
+    g_lim = ext.backward_splat(gi, m, c, l, col, *tabs, image, ckpt, H, W, last_contrib=last_contrib)
+    g_pix = ext.backward_pixel(gi, m, c, l, col, *tabs, t_final, last_contrib, H, W)
+    for a, bb, p in zip(g_ref, g_lim, g_pix):
+        assert rel(a, bb) < 1e-6 and rel(a, p) < 1e-5
+    with pytest.raises(RuntimeError):
+        P0.load_extension(with_cuda=False)
+
+
+def test_splat2d_depth_order():
+    f = load("phase0_dense_n96")
+    H, W = int(f["H"]), int(f["W"])
+    params = ph0_params(f, torch.float64, grad=False)
+    depths = torch.rand(params[0].shape[0], generator=torch.Generator().manual_seed(3), dtype=torch.float64).cuda()
+    order = torch.argsort(depths, stable=True)
+    a = splat2d.render(*params, H, W, depths=depths)
+    b = splat2d.render(*[p[order] for p in params], H, W)
+    assert torch.equal(a, b)
