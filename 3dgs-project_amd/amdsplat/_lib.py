@@ -32,6 +32,9 @@ class GsCamera(C.Structure):
     ]
 
 
+GS_ACCUMULATE = 1  # gs_blend_bwd_3d flag: add to grad2d instead of zeroing it first
+
+
 class AmdSplatError(RuntimeError):
     pass
 
@@ -52,7 +55,7 @@ _SIGS = {
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                               _vp, _vp]),
+                               _vp, _i32, _vp, _vp]),
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp]),
     # 2D rule sets

@@ -199,8 +199,10 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
 
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
-                  grad_alpha=None, timing: bool = False):
-    """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings)."""
+                  grad_alpha=None, timing: bool = False, counters: torch.Tensor | None = None):
+    """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings).
+    counters: optional int64 [3] CUDA tensor that the blend backward adds its atomic count and
+    pair-evaluation count to (slots 0 and 2)."""
     dev = means.device
     n = fs.n
     cam = fs.cam
@@ -210,10 +212,12 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
         grad_alpha = grad_alpha.contiguous().float()
     tm = timing if isinstance(timing, StageTimer) else StageTimer(bool(timing))
     tm.mark("start")
-    grad2d = torch.empty(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+    grad2d = torch.zeros(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+    tm.mark("grad_zero")
     call("gs_blend_bwd_3d", ptr(fs.rec), ptr(fs.ranges), ptr(fs.point_list), ptr(fs.bucket_offsets),
          ptr(fs.bucket_to_tile), fs.n_buckets_max, n, cam.width, cam.height, ptr(fs.image), ptr(grad_image),
-         ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(grad2d), st)
+         ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(grad2d),
+         _lib.GS_ACCUMULATE, ptr(counters), st)
     tm.mark("blend_bwd")
     g_means = torch.empty(n, 3, dtype=torch.float32, device=dev)
     g_ls = torch.empty(n, 3, dtype=torch.float32, device=dev)

@@ -541,14 +541,17 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
                                int width, int height, const float* image, const float* grad_image,
                                const float* final_T, const float* grad_alpha,
                                const int32_t* n_contrib, const uint32_t* tile_max,
-                               const float* ckpt, float* grad2d, void* stream) {
+                               const float* ckpt, float* grad2d, int flags,
+                               unsigned long long* counters, void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0 && n >= 0 && n_buckets_max >= 0, GS_ERR_ARG,
              "invalid sizes");
   GS_REQUIRE(grad2d || n == 0, GS_ERR_ARG, "null grad2d");
   hipStream_t st = as_stream(stream);
-  fill_zero_f32(grad2d, n * kGrad2D, st);
-  if (int e = check_launch("blend_bwd_3d (zero fill)")) return e;
+  if (!(flags & GS_ACCUMULATE)) {
+    fill_zero_f32(grad2d, n * kGrad2D, st);
+    if (int e = check_launch("blend_bwd_3d (zero fill)")) return e;
+  }
   if (n_buckets_max == 0 || n == 0) return GS_OK;
   // splat_rec, point_list and ckpt may be NULL when there are no instances (no bucket reads them)
   GS_REQUIRE(ranges && bucket_offsets && bucket_to_tile && image && grad_image && n_contrib &&
@@ -568,6 +571,7 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
   a.grad_image = grad_image;
   a.grad_alpha = grad_alpha;
   a.grad_rec = grad2d;
+  a.counters = counters;
   launch_bwd_bucket<kRules3D, float>(a, st);
   return check_launch("blend_bwd_3d");
 }

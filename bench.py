@@ -5,15 +5,18 @@ Workload (default): 1M Gaussians, SH degree 3, 1297x840, fx=fy=1160, 8 seeded or
 N(0,1) upstream image gradient. Inputs are resident in HBM before the timed region.
 
     python bench.py [--steps K] [--warmup W] [--workload sh3_1m|sh3_3m|sh_rgb_100k] [--no-cpu-baseline]
+    python bench.py --copy-probe      # a plain 1 GiB device copy, to calibrate HBM counters
 
 Prints ONE JSON line. Per-stage times come from HIP events recorded on the launch stream
-inside the timed region; the roofline block is for the dominant kernel of the step.
+inside the timed region; `roofline` is for the kernel with the largest share of the step
+(the bucketed blend backward), from its algorithmic bytes and its event-timed duration.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -24,6 +27,9 @@ sys.path.insert(0, str(ROOT / "3dgs-project_amd"))
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "fwd+bwd ms/iter @1M Gaussians SH3 1297x840; per-stage HBM GB/s vs roofline"
+# stages that are one kernel each (the others group several kernels)
+SINGLE_KERNEL = {"preprocess": "preprocess_fwd_kernel", "blend_fwd": "blend_fwd_kernel",
+                 "blend_bwd": "blend_bwd_bucket_kernel", "preprocess_bwd": "preprocess_bwd_kernel"}
 
 
 def parse():
@@ -33,31 +39,36 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "sh3_3m", "sh_rgb_100k"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="threads for the CPU baseline (0 = all)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="threads for the CPU baseline (0 = OMP default)")
+    ap.add_argument("--copy-probe", action="store_true", help="time a plain 1 GiB device copy and exit")
     ap.add_argument("--json-out", default=None)
     return ap.parse_args()
 
 
 def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs):
-    """Algorithmic (compulsory) HBM bytes per stage for the measured counts."""
+    """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
+    written once (fp32)."""
     n, m, K = fs.n, fs.m, fs.sh_coeffs
     T = fs.cam.n_tiles
     P = fs.cam.width * fs.cam.height
     B = int(fs.bucket_offsets[-1].item())
     return {
-        # params 44 B/Gaussian + SH of visible Gaussians; record 64 B per visible + tiles_touched
-        "preprocess": 44 * n + 12 * K * n_visible + 64 * n_visible + 4 * n,
+        # params 44 B/Gaussian + tiles_touched 4 B; SH 12 K B and the 64 B record per visible one
+        "preprocess": 44 * n + 4 * n + n_visible * (12 * K + 64),
         "scan": 8 * n,
-        # emit (record read 64 B per visible, 12 B per instance) + 6 radix passes (read+write 12 B)
-        # + ranges (8 B/instance) + bucket counts
-        "binning": 64 * n_visible + 12 * m + 6 * 24 * m + 8 * m + 16 * T,
+        # depth keys + 4 radix passes over N (read+write key and value), emission (record of the
+        # visible, key+value per instance), 2 radix passes over M, ranges and bucket counts
+        "binning": 8 * n + 4 * 16 * n + 64 * n_visible + 8 * m + 2 * 16 * m + 8 * T,
         "buckets": 8 * T + 4 * B,
-        # ids + gathered record per instance, image/T/n_contrib, checkpoints
+        # per instance: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4; the
+        # checkpoints 4 KiB per bucket; tile max
         "blend_fwd": m * (4 + 64) + P * 20 + B * 4096 + 4 * T,
-        # checkpoints + image/grad/n_contrib per active bucket, bucket splats, 11 atomics per used splat
-        "blend_bwd": active_buckets * (4096 + 256 * 28) + splat_steps * (4 + 64) + used_pairs * 44 + 48 * n,
-        # params + SH + grad record + outputs (all N rows written)
-        "preprocess_bwd": n_visible * (44 + 12 * K + 48 + 64) + n * (44 + 12 * K),
+        "grad_zero": 48 * n,
+        # per active bucket: checkpoints 4 KiB + grad image 12, image 12, n_contrib 4 per pixel;
+        # per bucket-splat step: id + record; per reduced bucket-splat: 11 fp32 atomics
+        "blend_bwd": active_buckets * (4096 + 256 * 28) + splat_steps * (4 + 64) + used_pairs * 44,
+        # params, SH, record and grad2d of the visible; every output row written
+        "preprocess_bwd": n_visible * (44 + 12 * K + 64 + 48) + n * (44 + 12 * K),
     }
 
 
@@ -68,14 +79,22 @@ def bucket_stats(fs):
     tmax = fs.tile_max.cpu().numpy().astype(np.int64)
     nbk = np.diff(boff)
     active = np.minimum(nbk, (tmax + 31) // 32)
-    steps = np.minimum(tmax, (np.diff(fs.ranges.cpu().numpy().astype(np.int64), axis=1)[:, 0]))
-    return int(active.sum()), int(steps.sum())
+    return int(active.sum()), int(tmax.sum())
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE, calibrated with a plain copy), or None."""
+    f = ROOT / "profiles" / f"{kernel}_hbm_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
 
 
 def cpu_baseline(scene, pose, threads):
-    """The C oracle (the CPU restatement of the same rules) timed on the host: one full
-    fwd+bwd of one view. Bounded sample: the 1M-Gaussian scene restricted to its first
-    `frac` of Gaussians so that a run takes ~10-30 s, scaled linearly to the full N."""
+    """The C oracle (the CPU restatement of the same rules, OpenMP where the loops allow) timed
+    on the host: one full fwd+bwd of one view of the workload (~10 s)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -84,29 +103,50 @@ def cpu_baseline(scene, pose, threads):
     import oracle as O
 
     cam = scene.cameras[pose]
-    n_full = scene.n
-    frac = float(os.environ.get("AMDSPLAT_CPU_SAMPLE", "0.25"))
-    n = max(1000, int(n_full * frac))
-    p = [t[:n].numpy() for t in scene.params()]
+    p = [t.numpy() for t in scene.params()]
     gi = np.random.default_rng(0).standard_normal((3, cam.height, cam.width)).astype(np.float32)
     t0 = time.perf_counter()
     r = O.render(*p, cam, 3)
     g2 = O.blend_bwd(r["rec"], r["point_list"], r["ranges"], r["bucket_offsets"], cam.width, cam.height,
-                     r["image"], gi, r["final_T"], r["n_contrib"], r["tile_max"], r["ckpt"], n)
+                     r["image"], gi, r["final_T"], r["n_contrib"], r["tile_max"], r["ckpt"], scene.n)
     O.preprocess_bwd(*p, cam, 3, r["rec"], r["touched"], g2)
     dt = time.perf_counter() - t0
-    cores = threads if threads > 0 else (os.cpu_count() or 1)
-    return {"value": round(dt * 1000.0 / (n / n_full), 1), "unit": "ms/iter", "cores": cores, "kind": "port",
-            "sample": f"C oracle (OpenMP) fwd+bwd of pose {pose} on the first {n} of {n_full} Gaussians "
-                      f"({dt:.1f} s), scaled by N"}
+    cores = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return {"value": round(dt * 1000.0, 1), "unit": "ms/iter", "cores": cores, "kind": "port",
+            "sample": f"C oracle fwd+bwd of pose {pose}, all {scene.n} Gaussians ({dt:.1f} s; preprocess and "
+                      f"forward blend on {cores} OpenMP threads, sort and backward blend single-threaded)"}
+
+
+def copy_probe():
+    import torch
+
+    n = 1 << 28  # 1 GiB of float32
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    reps = 10
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "ms": round(ms, 4),
+                      "GBps_read_plus_write": round(8 * n / (ms * 1e6), 1)}))
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU runs are not part of it",
+        print(json.dumps({"error": "this build runs on one GPU; runs on several GPUs are not part of it",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.copy_probe:
+        copy_probe()
+        return
     import torch
 
     from amdsplat import raster3d as R
@@ -120,10 +160,10 @@ def main():
     g = torch.Generator().manual_seed(1234)
     grads = [torch.randn(3, c.height, c.width, generator=g).cuda() for c in cams]
 
-    def step(k, timer=None):
+    def step(k, timer=None, counters=None):
         pose = k % len(cams)
         fs = R.forward_pass(*params, cams[pose], sh_degree=None, timing=timer if timer else False)
-        out = R.backward_pass(fs, *params, grads[pose], timing=timer if timer else False)
+        out = R.backward_pass(fs, *params, grads[pose], timing=timer if timer else False, counters=counters)
         return fs, out
 
     for k in range(args.warmup):
@@ -145,18 +185,21 @@ def main():
         step_ms.append(sum(r.values()))
         for k2, v in r.items():
             per_stage.setdefault(k2, []).append(v)
-    stage_ms = {k2: statistics.mean(v) for k2, v in per_stage.items()}
+    stage_ms = {k2: statistics.mean(v) for k2, v in per_stage.items() if k2 != "start"}
 
-    # counts for the byte model (outside the timed region)
-    fs, _ = step(0)
+    # counts for the byte model, from one pose-0 step outside the timed region
+    ctr = torch.zeros(3, dtype=torch.int64, device="cuda")
+    fs, _ = step(0, counters=ctr)
     torch.cuda.synchronize()
     n_visible = int((fs.touched > 0).sum().item())
     active_buckets, splat_steps = bucket_stats(fs)
-    used_pairs = splat_steps  # upper bound: every bucket-splat reduced and written once
+    used_pairs = int(ctr[0].item()) // 11
+    evals = int(ctr[2].item())
     sb = stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs)
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
-    dominant = max((k2 for k2 in stage_ms if k2 in sb), key=lambda k2: stage_ms[k2])
+    dominant = max((k2 for k2 in stage_ms if k2 in SINGLE_KERNEL), key=lambda k2: stage_ms[k2])
     achieved = stage_gbs[dominant]
+    traffic = measured_traffic(SINGLE_KERNEL[dominant])
 
     out = {
         "metric": METRIC,
@@ -180,9 +223,12 @@ def main():
         "stage_hbm_frac": {k2: round(v / HBM_PEAK_GBS, 4) for k2, v in stage_gbs.items()},
         "event_sum_ms": round(statistics.mean(step_ms), 4),
         "counts": {"visible": n_visible, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
-                   "active_buckets": active_buckets, "bucket_splat_steps": splat_steps},
-        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                   "active_buckets": active_buckets, "bucket_splat_steps": splat_steps,
+                   "reduced_bucket_splats": used_pairs, "bwd_pair_evals": evals},
+        "roofline": {"kernel": SINGLE_KERNEL[dominant], "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes": sb[dominant],
+                     "avg_launch_ms": round(stage_ms[dominant], 4)},
     }
     if not args.no_cpu_baseline:
         try:

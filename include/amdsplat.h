@@ -143,17 +143,21 @@ int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32
 
 /* ---------------------------------------------------------------------------------------
  * 3D bucketed blend backward (replaces blend_backward_cu / blend_backward_macro_cu,
- * phase1/fastergs_macro.patch:40-314). One wavefront per bucket; grad2d [n,12] is zeroed
- * by the call and receives dL/d(mean2d, conic A B C, opacity, colour) and |dL/dmean2d|.
+ * phase1/fastergs_macro.patch:40-314). One wavefront per bucket; grad2d [n,12] receives
+ * dL/d(mean2d, conic A B C, opacity, colour) and |dL/dmean2d| (slots 9-10). It is zeroed by
+ * the call unless flags has GS_ACCUMULATE (then the call adds to it, e.g. over views).
  * n_buckets is read on device from bucket_offsets[T]; n_buckets_max bounds the grid.
  * grad_alpha [H,W] (may be NULL) is the gradient of the alpha = 1 - final_T output.
+ * counters: NULL or 3 device uint64 that receive the atomic adds issued (11 per reduced
+ * bucket-splat) and, in [2], the (pixel, splat) pairs evaluated.
  * ------------------------------------------------------------------------------------- */
+enum { GS_ACCUMULATE = 1 };
 int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, const uint32_t* bucket_to_tile,
                     int64_t n_buckets_max, int64_t n, int width, int height, const float* image,
                     const float* grad_image, const float* final_T, const float* grad_alpha,
                     const int32_t* n_contrib, const uint32_t* tile_max, const float* ckpt,
-                    float* grad2d, void* stream);
+                    float* grad2d, int flags, unsigned long long* counters, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 3D preprocess backward (replaces Faster-GS preprocess_backward_cu, csv:4): chains grad2d
