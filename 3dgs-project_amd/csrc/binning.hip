@@ -135,24 +135,30 @@ __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Stable LSD radix sort of (uint32 key, uint32 value) pairs, 8-bit digits.
+// Stable LSD radix sort of (uint32 key, uint32 value) pairs, BITS <= 8 bits per pass.
 //
-// Each workgroup owns a contiguous chunk of kChunk pairs; inside it, wavefront w owns the
-// contiguous sub-chunk [w * kSub, (w + 1) * kSub), read in kRounds coalesced rounds (once to
-// count, once to scatter). Keys with equal digits are matched with eight ballots; the
-// lowest lane of each match group updates that wavefront's digit counter in LDS. Order
-// inside a digit is therefore (workgroup, wavefront, round, lane) = input order: stable.
+// Per pass three kernels, none of which waits on another workgroup:
+//   upsweep  each 4096-key tile counts its digits -> tile_hist[digit][tile], and adds them to
+//            the pass's digit totals (global atomics)
+//   rowscan  one workgroup per digit: exclusive scan of its row over the tiles, plus the
+//            number of keys with smaller digits -> global start of (digit, tile)
+//   scatter  each tile ranks its keys stably (per-wavefront digit counters in LDS; equal
+//            digits inside a 64-key round matched with BITS ballots), stages the tile in LDS
+//            in digit order and writes it out as one contiguous run per digit (coalesced)
+// Wavefront w of a tile owns the contiguous keys [1024 w, 1024 (w + 1)), read in 16
+// coalesced rounds, so (wavefront, round, lane) is input order: the sort is stable.
 // ---------------------------------------------------------------------------------------
-constexpr int kSortWaves = 8;
-constexpr int kSortThreads = kSortWaves * kWave;  // 512
-constexpr int kRounds = 16;
-constexpr int kSub = kRounds * kWave;             // 1024 pairs per wavefront
-constexpr int kChunk = kSortWaves * kSub;         // 8192 pairs per workgroup
+constexpr int kRsThreads = 256;
+constexpr int kRsWaves = kRsThreads / kWave;      // 4
+constexpr int kRsRounds = 16;                     // 64-key rounds per wavefront
+constexpr int kRsWaveKeys = kRsRounds * kWave;    // 1024
+constexpr int kRsTile = kRsWaves * kRsWaveKeys;   // 4096 keys per workgroup
 
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
+template <int BITS>
+__device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
   uint64_t peers = __ballot(valid ? 1 : 0);
 #pragma unroll
-  for (int bit = 0; bit < 8; ++bit) {
+  for (int bit = 0; bit < BITS; ++bit) {
     const bool set = (d >> bit) & 1u;
     const uint64_t bm = __ballot(set ? 1 : 0);
     peers &= set ? bm : ~bm;
@@ -160,122 +166,210 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
   return valid ? peers : 0ull;
 }
 
-__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys,
-                                                                  int64_t m, int shift,
-                                                                  uint32_t* __restrict__ hist,
-                                                                  int n_blocks) {
-  __shared__ uint32_t s_h[256];
+template <int BITS>
+__global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* __restrict__ keys, int64_t m,
+                                                                int shift, uint32_t* __restrict__ tile_hist,
+                                                                int n_tiles, uint32_t* __restrict__ totals) {
+  constexpr int R = 1 << BITS;
+  __shared__ uint32_t s_h[R];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  if (threadIdx.x < 256) s_h[threadIdx.x] = 0;
+  for (int k = threadIdx.x; k < R; k += kRsThreads) s_h[k] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + wave * kSub;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kRsTile + wave * kRsWaveKeys;
   const uint64_t lt = lanemask_lt(lane);
-  for (int r = 0; r < kRounds; ++r) {
+  uint32_t key[kRsRounds];
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {  // all loads in flight before the first ballot
     const int64_t idx = base + r * kWave + lane;
-    const bool valid = idx < m;
-    const uint32_t d = valid ? (keys[idx] >> shift) & 255u : 0u;
-    const uint64_t peers = match_digit(d, valid);
+    key[r] = idx < m ? keys[idx] : 0u;
+  }
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const bool valid = base + r * kWave + lane < m;
+    const uint32_t d = (key[r] >> shift) & (R - 1);
+    const uint64_t peers = match_bits<BITS>(d, valid);
     if (valid && (peers & lt) == 0ull) atomicAdd(&s_h[d], static_cast<uint32_t>(__popcll(peers)));
   }
   __syncthreads();
-  if (threadIdx.x < 256) hist[static_cast<int64_t>(threadIdx.x) * n_blocks + blockIdx.x] = s_h[threadIdx.x];
+  for (int k = threadIdx.x; k < R; k += kRsThreads) {
+    const uint32_t c = s_h[k];
+    tile_hist[static_cast<int64_t>(k) * n_tiles + blockIdx.x] = c;
+    if (c) atomicAdd(&totals[k], c);
+  }
 }
 
-__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
-    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
-    uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t m, int shift,
-    const uint32_t* __restrict__ offs, int n_blocks) {
-  __shared__ uint32_t s_cnt[kSortWaves][256];
+// Workgroup `d`: entries [d][0 .. n_tiles) become (keys with digit < d) + (keys with digit d in
+// earlier tiles).
+__global__ __launch_bounds__(kScanThreads) void rs_rowscan_kernel(uint32_t* __restrict__ tile_hist, int n_tiles,
+                                                                  const uint32_t* __restrict__ totals) {
+  __shared__ uint32_t s_wave[4];
+  const int d = blockIdx.x;
+  uint32_t base;
+  block_inclusive_scan(static_cast<int>(threadIdx.x) < d ? totals[threadIdx.x] : 0u, s_wave, base);
+  uint32_t* row = tile_hist + static_cast<int64_t>(d) * n_tiles;
+  uint32_t run = base;
+  for (int c0 = 0; c0 < n_tiles; c0 += kScanTile) {
+    uint32_t loc[kScanItems];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int e = 0; e < kScanItems; ++e) {
+      const int idx = c0 + static_cast<int>(threadIdx.x) * kScanItems + e;
+      loc[e] = idx < n_tiles ? row[idx] : 0u;
+      sum += loc[e];
+    }
+    uint32_t total;
+    const uint32_t incl = block_inclusive_scan(sum, s_wave, total);
+    uint32_t pos = run + incl - sum;
+#pragma unroll
+    for (int e = 0; e < kScanItems; ++e) {
+      const int idx = c0 + static_cast<int>(threadIdx.x) * kScanItems + e;
+      if (idx < n_tiles) row[idx] = pos;
+      pos += loc[e];
+    }
+    run += total;
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
+    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin, uint32_t* __restrict__ kout,
+    uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles) {
+  constexpr int R = 1 << BITS;
+  __shared__ uint32_t s_cnt[kRsWaves][R];  // per-wavefront digit counts, then wavefront offsets
+  __shared__ uint32_t s_excl[R];           // start of each digit inside the staged tile
+  __shared__ uint32_t s_goff[R];           // global start of this tile's keys of each digit
+  __shared__ uint32_t s_key[kRsTile];
+  __shared__ uint32_t s_val[kRsTile];
+  __shared__ uint32_t s_wave[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  for (int k = threadIdx.x; k < kSortWaves * 256; k += kSortThreads) (&s_cnt[0][0])[k] = 0;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk + wave * kSub;
+  for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_cnt[0][0])[k] = 0;
+  for (int k = threadIdx.x; k < R; k += kRsThreads)
+    s_goff[k] = tile_offs[static_cast<int64_t>(k) * n_tiles + blockIdx.x];
+  __syncthreads();
+  const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kRsTile;
+  const int64_t base = tile_base + wave * kRsWaveKeys;
   const uint64_t lt = lanemask_lt(lane);
-  __syncthreads();
-  // per-wavefront digit counts
-  for (int r = 0; r < kRounds; ++r) {
+  uint32_t key[kRsRounds], val[kRsRounds], rank[kRsRounds];
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
     const int64_t idx = base + r * kWave + lane;
     const bool valid = idx < m;
-    const uint32_t d = valid ? (kin[idx] >> shift) & 255u : 0u;
-    const uint64_t peers = match_digit(d, valid);
+    key[r] = valid ? kin[idx] : 0u;
+    val[r] = valid ? vin[idx] : 0u;
+  }
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const bool valid = base + r * kWave + lane < m;
+    const uint32_t d = (key[r] >> shift) & (R - 1);
+    const uint64_t peers = match_bits<BITS>(d, valid);
+    rank[r] = valid ? s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt)) : 0u;
+    wave_sync();
     if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
     wave_sync();
   }
   __syncthreads();
-  // per-wavefront starting positions: global digit offset of this workgroup + earlier wavefronts
-  if (threadIdx.x < 256) {
-    const int d = threadIdx.x;
-    uint32_t run = offs[static_cast<int64_t>(d) * n_blocks + blockIdx.x];
-    for (int w = 0; w < kSortWaves; ++w) {
+  // digit totals of the tile -> wavefront offsets inside each digit, digit starts in the tile
+  uint32_t total = 0;
+  for (int d = threadIdx.x; d < R; d += kRsThreads) {
+#pragma unroll
+    for (int w = 0; w < kRsWaves; ++w) {
       const uint32_t c = s_cnt[w][d];
-      s_cnt[w][d] = run;
-      run += c;
+      s_cnt[w][d] = total;
+      total += c;
+    }
+  }
+  uint32_t all;
+  const uint32_t incl = block_inclusive_scan(total, s_wave, all);
+  if (static_cast<int>(threadIdx.x) < R) s_excl[threadIdx.x] = incl - total;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    if (base + r * kWave + lane < m) {
+      const uint32_t d = (key[r] >> shift) & (R - 1);
+      const uint32_t pos = s_excl[d] + s_cnt[wave][d] + rank[r];
+      s_key[pos] = key[r];
+      s_val[pos] = val[r];
     }
   }
   __syncthreads();
-  // scatter (the chunk was just read, so these loads hit the cache)
-  for (int r = 0; r < kRounds; ++r) {
-    const int64_t idx = base + r * kWave + lane;
-    const bool valid = idx < m;
-    uint32_t key = 0, val = 0;
-    if (valid) {
-      key = kin[idx];
-      val = vin[idx];
-    }
-    const uint32_t d = (key >> shift) & 255u;
-    const uint64_t peers = match_digit(d, valid);
-    uint32_t pos = 0;
-    if (valid) pos = s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt));
-    wave_sync();
-    if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
-    if (valid) {
-      kout[pos] = key;
-      vout[pos] = val;
-    }
-    wave_sync();
+  const int count = static_cast<int>(min<int64_t>(kRsTile, m - tile_base));
+  for (int p = threadIdx.x; p < count; p += kRsThreads) {
+    const uint32_t k = s_key[p];
+    const uint32_t d = (k >> shift) & (R - 1);
+    const uint32_t g = s_goff[d] + (static_cast<uint32_t>(p) - s_excl[d]);
+    kout[g] = k;
+    vout[g] = s_val[p];
   }
+}
+
+struct SortPlan {
+  int passes, bits;
+};
+
+static SortPlan sort_plan(int bits) {
+  SortPlan p;
+  p.passes = bits <= 0 ? 0 : (bits + 7) / 8;
+  p.bits = p.passes ? (bits + p.passes - 1) / p.passes : 0;
+  return p;
 }
 
 static size_t sort_ws(int64_t m) {
-  const int64_t nb = (m + kChunk - 1) / kChunk;
-  const int64_t hist = 256 * (nb > 0 ? nb : 1);
-  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up((hist + 1) * 4) + scan_ws(hist);
+  const int64_t nt = (m + kRsTile - 1) / kRsTile;
+  const int64_t hist = 256 * (nt > 0 ? nt : 1);
+  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * 256 * 4);
+}
+
+template <int BITS>
+static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
+                      uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st) {
+  hipLaunchKernelGGL(rs_upsweep_kernel<BITS>, dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
+                     n_tiles, totals);
+  hipLaunchKernelGGL(rs_rowscan_kernel, dim3(1 << BITS), dim3(kScanThreads), 0, st, tile_hist, n_tiles, totals);
+  hipLaunchKernelGGL(rs_scatter_kernel<BITS>, dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
+                     tile_hist, n_tiles);
 }
 
 // Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
 static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, uint32_t* v_out, int64_t m,
                        int bits, char* ws, hipStream_t st) {
   if (m <= 0) return;
-  const int64_t nb = (m + kChunk - 1) / kChunk;
-  const int64_t hist_n = 256 * nb;
-  uint32_t* k_alt = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(m * 4);
-  uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(m * 4);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(hist_n * 4);
-  uint32_t* hist_scan = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up((hist_n + 1) * 4);
-  const int passes = bits <= 0 ? 0 : (bits + 7) / 8;
-  if (passes == 0) {
+  const SortPlan plan = sort_plan(bits);
+  if (plan.passes == 0) {
     (void)hipMemcpyAsync(k_out, k, m * 4, hipMemcpyDeviceToDevice, st);
     (void)hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
     return;
   }
+  const int n_tiles = static_cast<int>((m + kRsTile - 1) / kRsTile);
+  uint32_t* k_alt = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up(m * 4);
+  uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up(m * 4);
+  uint32_t* tile_hist = reinterpret_cast<uint32_t*>(ws);
+  ws += align_up(static_cast<int64_t>(256) * n_tiles * 4);
+  uint32_t* totals = reinterpret_cast<uint32_t*>(ws);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, totals, int64_t(4 * 256), 0u);
   // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
   // the last pass lands in (k_out, v_out) and no pass works in place
   const uint32_t* src_k = k;
   const uint32_t* src_v = v;
-  for (int p = 0; p < passes; ++p) {
-    const bool to_out = ((passes - 1 - p) % 2) == 0;
+  for (int p = 0; p < plan.passes; ++p) {
+    const bool to_out = ((plan.passes - 1 - p) % 2) == 0;
     uint32_t* dst_k = to_out ? k_out : k_alt;
     uint32_t* dst_v = to_out ? v_out : v_alt;
-    hipLaunchKernelGGL(radix_hist_kernel, dim3(static_cast<unsigned>(nb)), dim3(kSortThreads), 0, st,
-                       src_k, m, 8 * p, hist, static_cast<int>(nb));
-    scan_rec(hist, hist_scan, hist_n, ws, st);
-    hipLaunchKernelGGL(radix_scatter_kernel, dim3(static_cast<unsigned>(nb)), dim3(kSortThreads), 0,
-                       st, src_k, src_v, dst_k, dst_v, m, 8 * p, hist_scan, static_cast<int>(nb));
+    uint32_t* tot = totals + 256 * p;
+    const int shift = plan.bits * p;
+    switch (plan.bits) {
+      case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 2: sort_pass<2>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 3: sort_pass<3>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 4: sort_pass<4>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      default: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+    }
     src_k = dst_k;
     src_v = dst_v;
   }
@@ -333,6 +427,11 @@ __device__ __forceinline__ int4 clamp_rect(int4 r, int tiles_x, int tiles_y) {
 }
 
 // 3D: tiles from the row-band rule; 2D: every tile of the rectangle [x0, x1) x [y0, y1).
+// A lane emits its own Gaussian's instances unless the Gaussian has more than kEmitLane of
+// them; those are emitted by the whole wavefront, a lane per tile row for the row ranges and
+// a lane per instance for the (then contiguous, coalesced) writes.
+constexpr uint32_t kEmitLane = 8;
+
 template <bool kRect>
 __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ rec,
                                                    const int4* __restrict__ rects,
@@ -340,31 +439,99 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
                                                    const uint32_t* __restrict__ offs, int64_t n,
                                                    int tiles_x, int tiles_y, uint32_t* __restrict__ tkeys,
                                                    uint32_t* __restrict__ vals) {
+  __shared__ uint32_t s_excl[4][kWave];
+  __shared__ uint32_t s_row[4][kWave];  // (tile row << 16) | first tile column of the row
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (j >= n) return;
-  const uint32_t off = offs[j];
-  const uint32_t cap = offs[j + 1] - off;  // never write past this Gaussian's slots
-  if (cap == 0) return;
-  const uint32_t g = order[j];
-  if constexpr (kRect) {
-    const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
-    uint32_t k = 0;
-    for (int ty = r.y; ty < r.w; ++ty)
-      for (int tx = r.x; tx < r.z; ++tx) {
-        if (k < cap) {
-          tkeys[off + k] = static_cast<uint32_t>(ty * tiles_x + tx);
+  uint32_t off = 0, cap = 0, g = 0;  // cap: this Gaussian's slots; never write past them
+  if (j < n) {
+    off = offs[j];
+    cap = offs[j + 1] - off;
+    if (cap) g = order[j];
+  }
+  const bool wide = cap > kEmitLane;
+  if (cap && !wide) {
+    if constexpr (kRect) {
+      const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
+      uint32_t k = 0;
+      for (int ty = r.y; ty < r.w; ++ty)
+        for (int tx = r.x; tx < r.z; ++tx) {
+          if (k < cap) {
+            tkeys[off + k] = static_cast<uint32_t>(ty * tiles_x + tx);
+            vals[off + k] = g;
+          }
+          ++k;
+        }
+    } else {
+      const SplatRec r = rec[g];
+      for_each_touched_tile(r.a, r.b, r.d, tiles_x, [&](int tile, int k) {
+        if (static_cast<uint32_t>(k) < cap) {
+          tkeys[off + k] = static_cast<uint32_t>(tile);
           vals[off + k] = g;
         }
-        ++k;
+      });
+    }
+  }
+  for (uint64_t wm = __ballot(wide ? 1 : 0); wm != 0ull; wm &= wm - 1ull) {
+    const int src = __ffsll(static_cast<unsigned long long>(wm)) - 1;
+    const uint32_t wg = __shfl(g, src, 64), woff = __shfl(off, src, 64), wcap = __shfl(cap, src, 64);
+    int ty0, ty1;
+    int4 rr;
+    BandSetup bs;
+    int4 bd;
+    if constexpr (kRect) {
+      rr = clamp_rect(rects[wg], tiles_x, tiles_y);
+      ty0 = rr.y;
+      ty1 = rr.w - 1;
+    } else {
+      const SplatRec r = rec[wg];
+      bs = band_setup(r.a, r.b);
+      bd = r.d;
+      ty0 = bd.z / kTile;
+      ty1 = bd.w / kTile;
+    }
+    uint32_t done = 0;
+    for (int row0 = ty0; row0 <= ty1; row0 += kWave) {
+      const int ty = row0 + lane;
+      uint32_t nt = 0;
+      int tx0 = 0;
+      if (ty <= ty1) {
+        if constexpr (kRect) {
+          tx0 = rr.x;
+          nt = static_cast<uint32_t>(max(rr.z - rr.x, 0));
+        } else {
+          nt = row_tiles(bs, bd, ty, tx0);
+        }
       }
-  } else {
-    const SplatRec r = rec[g];
-    for_each_touched_tile(r.a, r.b, r.d, tiles_x, [&](int tile, int k) {
-      if (static_cast<uint32_t>(k) < cap) {
-        tkeys[off + k] = static_cast<uint32_t>(tile);
-        vals[off + k] = g;
+      uint32_t incl = nt;
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
       }
-    });
+      const uint32_t total = __shfl(incl, kWave - 1, 64);
+      s_excl[wave][lane] = incl - nt;
+      s_row[wave][lane] = (static_cast<uint32_t>(ty) << 16) | static_cast<uint32_t>(tx0);
+      wave_sync();
+      for (uint32_t it = lane; it < total; it += kWave) {
+        // row of item it: the last lane whose exclusive start is <= it (it has tiles)
+        int lo = 0, hi = kWave - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_excl[wave][mid] <= it) lo = mid;
+          else hi = mid - 1;
+        }
+        const uint32_t rw = s_row[wave][lo];
+        const uint32_t tile = (rw >> 16) * static_cast<uint32_t>(tiles_x) + (rw & 0xffffu) + (it - s_excl[wave][lo]);
+        const uint32_t k = done + it;
+        if (k < wcap) {
+          tkeys[woff + k] = tile;
+          vals[woff + k] = wg;
+        }
+      }
+      done += total;
+      wave_sync();
+    }
   }
 }
 

@@ -66,7 +66,7 @@ __device__ __forceinline__ void count_add(unsigned long long* c, uint32_t v) {
 // ---------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------
-template <int R, typename S>
+template <int R, typename S, bool kCount>
 __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) {
   using Ru = Rule<R, S>;
   __shared__ Staged<S> s_sp[kTilePixels];
@@ -76,6 +76,7 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
   const int tile = blockIdx.x;
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int t = threadIdx.x;
+  const int lane = t & 63;
   const int wave = t >> 6;
   const int px = tx * kTile + (t & 15), py = ty * kTile + (t >> 4);
   const bool inside = px < a.W && py < a.H;
@@ -105,39 +106,54 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
     }
     __syncthreads();
     const int nb = min(kTilePixels, len - b0);
-    for (int jj = 0; jj < nb; ++jj) {
-      const int idx = b0 + jj;
-      if (ck && (idx & (kBucket - 1)) == 0) {
-        S* c = ck + static_cast<int64_t>(idx / kBucket) * kTilePixels * 4;
+    // this wavefront's strip bit of every staged splat, as four 64-bit masks (3D)
+    uint64_t wm[4] = {~0ull, ~0ull, ~0ull, ~0ull};
+    if constexpr (Ru::kStrips) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int jj = 64 * q + lane;
+        wm[q] = __ballot((jj < nb && ((s_mask[jj] >> wave) & 1u)) ? 1 : 0);
+      }
+    }
+    // one 32-entry bucket at a time: its checkpoint, then its splats
+    for (int c0 = 0; c0 < nb; c0 += kBucket) {
+      if (ck) {
+        S* c = ck + static_cast<int64_t>((b0 + c0) / kBucket) * kTilePixels * 4;
         if constexpr (Ru::kCkptTFirst) {
           c[0] = T; c[1] = Cr; c[2] = Cg; c[3] = Cb;
         } else {
           c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
         }
       }
-      if (done) continue;
-      if constexpr (Ru::kStrips) {
-        if (((s_mask[jj] >> wave) & 1u) == 0u) continue;  // wave-uniform
-      }
-      const Staged<S> sp = s_sp[jj];
-      Eval<S> e;
-      ++evals;
-      if (!Ru::eval(sp, pxf, pyf, e)) continue;
-      if constexpr (Ru::kStopBefore) {
-        if (T * (S(1) - e.alpha) < Ru::t_stop()) {
-          done = true;
-          continue;
+      if (__ballot(done ? 0 : 1) == 0ull) continue;  // the whole wavefront has terminated
+      const int c1 = min(c0 + kBucket, nb);
+      const uint64_t qm = (c0 < 64) ? wm[0] : (c0 < 128) ? wm[1] : (c0 < 192) ? wm[2] : wm[3];
+      uint32_t cm = static_cast<uint32_t>(qm >> (c0 & 63));
+      if (c1 - c0 < kBucket) cm &= (1u << (c1 - c0)) - 1u;
+      while (cm != 0u) {  // wave-uniform: the splats whose bounds reach this wavefront's rows
+        const int jj = c0 + __builtin_ctz(cm);
+        cm &= cm - 1u;
+        if (done) continue;
+        const Staged<S> sp = s_sp[jj];
+        Eval<S> e;
+        if constexpr (kCount) ++evals;
+        if (!Ru::eval(sp, pxf, pyf, e)) continue;
+        if constexpr (Ru::kStopBefore) {
+          if (T * (S(1) - e.alpha) < Ru::t_stop()) {
+            done = true;
+            continue;
+          }
         }
-      }
-      composite<R, S>(Cr, Cg, Cb, T, sp, e.alpha);
-      ++count;
-      last = idx + 1;
-      if constexpr (!Ru::kStopBefore) {
-        if (T < Ru::t_stop()) done = true;
+        composite<R, S>(Cr, Cg, Cb, T, sp, e.alpha);
+        ++count;
+        last = b0 + jj + 1;
+        if constexpr (!Ru::kStopBefore) {
+          if (T < Ru::t_stop()) done = true;
+        }
       }
     }
   }
-  if (a.counters) count_add(a.counters + 2, evals);
+  if constexpr (kCount) count_add(a.counters + 2, evals);
   if constexpr (R == kRulesPhase0) {
     // phase0 writes every checkpoint slot: buckets after the workgroup stopped keep the
     // final state (phase0/csrc/macrotile/bindings.cpp:167-169)
@@ -205,12 +221,126 @@ __device__ __forceinline__ int wave_max(int v) {
 __device__ __forceinline__ void atomic_add_grad(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAtomicAdd(p, v); }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Transposing reduction of 12 per-lane values over the wavefront. Each exchange step halves
+// the values a lane carries (the partner keeps the other half): xor 32 with
+// v_permlane32_swap, xor 16 with v_permlane16_swap, xor 8 with DPP row_ror:8; then the two
+// remaining values are summed over their 8-lane group (half-row mirror, quad xor 1, quad xor 2).
+// ~30 instructions instead of 12 separate 6-level reductions. On return every lane of group
+// g = lane / 8 holds the totals of value indices 6 b5 + 3 b4 + 2 b3 + {0, 1} (b = bits of
+// lane; index 3 + 6 b5 + 3 b4 with b3 = 1 does not exist) in u0 and u1.
+__device__ __forceinline__ void wave_reduce12(const float* v, float& u0, float& u1) {
+  const int lane = threadIdx.x & 63;
+  float s[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 6]), false, false);
+    s[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float t[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[i]), __float_as_uint(s[i + 3]), false, false);
+    t[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool b3 = (lane & 8) != 0;
+  const float send0 = b3 ? t[0] : t[2], keep0 = b3 ? t[2] : t[0];
+  const float send1 = b3 ? t[1] : 0.0f, keep1 = b3 ? 0.0f : t[1];
+  u0 = keep0 + dpp<0x128>(send0);  // row_ror:8 = partner lane ^ 8
+  u1 = keep1 + dpp<0x128>(send1);
+  u0 += dpp<0x141>(u0);  // row_half_mirror
+  u1 += dpp<0x141>(u1);
+  u0 += dpp<0xB1>(u0);  // quad_perm [1,0,3,2]
+  u1 += dpp<0xB1>(u1);
+  u0 += dpp<0x4E>(u0);  // quad_perm [2,3,0,1]
+  u1 += dpp<0x4E>(u1);
+}
+
+__device__ __forceinline__ void wave_reduce12(const double* v, double& u0, double& u1) {
+  // float64 (2D surfaces): full butterflies, then the float path's placement of the totals
+  const int g = (threadIdx.x & 63) >> 3;
+  const int base = 6 * (g >> 2) + 3 * ((g >> 1) & 1) + 2 * (g & 1);
+  u0 = 0.0;
+  u1 = 0.0;
+#pragma unroll
+  for (int k = 0; k < 12; ++k) {
+    const double t = wave_sum(v[k]);
+    if (k == base) u0 = t;
+    if (k == base + 1) u1 = t;
+  }
+}
+
+// Raw per-pair sums of the bucketed backward (the splat-constant factors are applied once
+// per splat in finish_grad): [0] sum h dx (phase0: h a), [1] sum h dy (phase0: h b),
+// [2] sum h dx dx (h a dx), [3] sum h dx dy (h a dy), [4] sum h dy dy (h b dy), [5] sum G dL/dalpha,
+// [6..8] colour, [9..10] |dL/dmean| (3D); h = alpha dL/dalpha = dL/dpower.
+template <int R, typename S>
+__device__ __forceinline__ void pair_sums(const Staged<S>& s, const Eval<S>& e, S dLda, S* acc) {
+  if (e.clamped) return;
+  acc[5] = fma(e.G, dLda, acc[5]);
+  const S h = e.alpha * dLda;
+  S hx, hy;
+  if constexpr (R == kRulesPhase0) {
+    hx = h * e.a;
+    hy = h * e.b;
+    acc[2] = fma(hx, e.dx, acc[2]);
+    acc[3] = fma(hx, e.dy, acc[3]);
+    acc[4] = fma(hy, e.dy, acc[4]);
+  } else {
+    hx = h * e.dx;
+    hy = h * e.dy;
+    acc[2] = fma(hx, e.dx, acc[2]);
+    acc[3] = fma(hx, e.dy, acc[3]);
+    acc[4] = fma(hy, e.dy, acc[4]);
+    if constexpr (R == kRules3D) {
+      acc[9] += fabs(fma(s.n0, hx, s.n1 * hy));
+      acc[10] += fabs(fma(s.n1, hx, s.nat2 * hy));
+    }
+  }
+  acc[0] += hx;
+  acc[1] += hy;
+}
+
+// Final gradient of value index k from its total u (u0, u1: totals of indices 0 and 1).
+template <int R, typename S>
+__device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S u1) {
+  if constexpr (R == kRulesPhase0) {
+    // power = -(a^2 + b^2) / 2 with a = l0 dx + l1 dy, b = l2 dy, d = pixel - mean
+    if (k == 0) return s.s0 * u0;
+    if (k == 1) return fma(s.s1, u0, s.s2 * u1);
+    if (k >= 2 && k <= 4) return -u;
+    if (k == 5) return u * s.o * (S(1) - s.o);  // dL/dlogit = dL/do o (1 - o)
+    return u;
+  } else {
+    S A, B, C;
+    if constexpr (R == kRules3D) {
+      A = s.n0;
+      B = s.n1;
+      C = s.nat2;
+    } else {
+      A = s.s0;
+      B = s.s1;
+      C = s.s2;
+    }
+    // power = -1/2 (A dx^2 + 2 B dx dy + C dy^2), d = mean - pixel
+    if (k == 0) return -fma(A, u0, B * u1);
+    if (k == 1) return -fma(B, u0, C * u1);
+    if (k == 2 || k == 4) return S(-0.5) * u;
+    if (k == 3) return -u;
+    return u;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Bucketed backward
 // ---------------------------------------------------------------------------------------
 constexpr int kBwdWaves = 4;
 
-template <int R, typename S>
+template <int R, typename S, bool kCount>
 __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(BlendArgs<S> a) {
   using Ru = Rule<R, S>;
   constexpr int NV = Ru::kGradVals;
@@ -302,13 +432,17 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
   wave_sync();
 
   uint32_t evals = 0, atomics = 0;
+  // value index k owned by this lane after wave_reduce12 (lo = 0 or 1 within the 8-lane group)
+  const int grp = lane >> 3, lo = lane & 7;
+  const int kidx = 6 * (grp >> 2) + 3 * ((grp >> 1) & 1) + 2 * (grp & 1) + lo;
+  const bool owner = lo < 2 && (2 * (grp & 1) + lo) < 3 && kidx < NV;
   for (int j = 0; j < jmax; ++j) {
     const Staged<S> sp = s_sp[wave][j];
     uint32_t m = 0xfu;
     if constexpr (Ru::kStrips) m = s_m[wave][j];
-    S acc[11];
+    S acc[12];
 #pragma unroll
-    for (int k = 0; k < 11; ++k) acc[k] = S(0);
+    for (int k = 0; k < 12; ++k) acc[k] = S(0);
     bool used = false;
 #pragma unroll
     for (int r = 0; r < kPixPerLane; ++r) {
@@ -318,39 +452,36 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
         if (T[r] < Ru::t_stop()) continue;
       }
       Eval<S> e;
-      ++evals;
+      if constexpr (kCount) ++evals;
       if (!Ru::eval(sp, pxf, pyf[r], e)) continue;
       used = true;
       const S w = T[r] * e.alpha;
-      const S dot = Gr[r] * sp.cr + Gg[r] * sp.cg + Gb[r] * sp.cb;
-      acc[6] += w * Gr[r];
-      acc[7] += w * Gg[r];
-      acc[8] += w * Gb[r];
+      const S dot = fma(Gb[r], sp.cb, fma(Gg[r], sp.cg, Gr[r] * sp.cr));
+      acc[6] = fma(w, Gr[r], acc[6]);
+      acc[7] = fma(w, Gg[r], acc[7]);
+      acc[8] = fma(w, Gb[r], acc[8]);
       rho[r] = fma(-w, dot, rho[r]);
       const S oma = S(1) - e.alpha;
       S dLda;
       if constexpr (R == kRules3D) {
-        dLda = T[r] * dot - rho[r] * __builtin_amdgcn_rcpf(fmaxf(oma, kOneMinusAlphaEps));
+        dLda = fma(T[r], dot, -(rho[r] * __builtin_amdgcn_rcpf(fmaxf(oma, kOneMinusAlphaEps))));
       } else {
         dLda = T[r] * dot - rho[r] / oma;
       }
-      shape_grads<R, S>(sp, e, dLda, acc);
+      pair_sums<R, S>(sp, e, dLda, acc);
       T[r] = T[r] * oma;
     }
     if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
-    S mine = S(0);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const S s = wave_sum(acc[k]);
-      mine = (lane == k) ? s : mine;
+    S u0, u1;
+    wave_reduce12(acc, u0, u1);
+    if (owner) {
+      const S u = lo == 0 ? u0 : u1;
+      atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + kidx,
+                      finish_grad<R, S>(sp, kidx, u, u0, u1));
     }
-    if constexpr (R == kRulesPhase0) {
-      if (lane == 5) mine = mine * sp.o * (S(1) - sp.o);  // dL/dlogit = dL/do o (1 - o)
-    }
-    if (lane < NV) atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + lane, mine);
-    atomics += NV;
+    if constexpr (kCount) atomics += NV;
   }
-  if (a.counters) {
+  if constexpr (kCount) {
     if (lane == 0 && atomics) atomicAdd(a.counters, static_cast<unsigned long long>(atomics));
     count_add(a.counters + 2, evals);
   }
@@ -456,14 +587,19 @@ namespace {
 
 template <int R, typename S>
 void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
-  hipLaunchKernelGGL((blend_fwd_kernel<R, S>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
+  if (a.counters)
+    hipLaunchKernelGGL((blend_fwd_kernel<R, S, true>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
+  else
+    hipLaunchKernelGGL((blend_fwd_kernel<R, S, false>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
 }
 
 template <int R, typename S>
 void launch_bwd_bucket(const BlendArgs<S>& a, hipStream_t st) {
-  const int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
-  hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kBwdWaves * kWave), 0, st, a);
+  const unsigned blocks = static_cast<unsigned>((a.n_buckets + kBwdWaves - 1) / kBwdWaves);
+  if (a.counters)
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, true>), dim3(blocks), dim3(kBwdWaves * kWave), 0, st, a);
+  else
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, false>), dim3(blocks), dim3(kBwdWaves * kWave), 0, st, a);
 }
 
 template <int R, typename S>

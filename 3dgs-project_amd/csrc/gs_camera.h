@@ -94,6 +94,34 @@ __device__ __forceinline__ int for_each_touched_tile(const float4 a, const float
   return count;
 }
 
+// Tiles [tx0, tx0 + nt) touched in tile row ty (nt = 0 if the row is missed).
+__device__ __forceinline__ uint32_t row_tiles(const BandSetup& s, const int4 d, int ty, int& tx0) {
+  const int py0 = max(ty * kTile, d.z), py1 = min(ty * kTile + kTile - 1, d.w);
+  int c0, c1;
+  if (!band_columns(s, static_cast<float>(py0) + 0.5f, static_cast<float>(py1) + 0.5f, d.x, d.y, c0, c1)) {
+    tx0 = 0;
+    return 0u;
+  }
+  tx0 = c0 / kTile;
+  return static_cast<uint32_t>(c1 / kTile - tx0 + 1);
+}
+
+// Number of touched tiles of a splat whose tile rows are shared out over the wavefront's
+// lanes (lane r takes rows ty0 + r, ty0 + r + 64, ...). Every lane of the wavefront must call
+// it with the same splat; returns the total to every lane.
+__device__ __forceinline__ uint32_t wave_count_touched_tiles(const float4 a, const float4 b, const int4 d,
+                                                             int lane) {
+  const BandSetup s = band_setup(a, b);
+  const int ty0 = d.z / kTile, ty1 = d.w / kTile;
+  uint32_t cnt = 0;
+  for (int ty = ty0 + lane; ty <= ty1; ty += kWave) {
+    int tx0;
+    cnt += row_tiles(s, d, ty, tx0);
+  }
+  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+  return cnt;
+}
+
 // Number of touched tiles (same rule, without enumerating them).
 __device__ __forceinline__ int count_touched_tiles(const float4 a, const float4 b, const int4 d) {
   const BandSetup s = band_setup(a, b);

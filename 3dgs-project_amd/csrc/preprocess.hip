@@ -13,6 +13,8 @@
 
 namespace gs {
 
+constexpr int kWideRows = 4;  // splats spanning more tile rows than this share rows over the wavefront
+
 struct Geom {
   bool vis;
   float vx, vy, vz, iz, tx, ty, txc, tyc;
@@ -154,13 +156,27 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     }
   }
   uint32_t count = 0;
-  float4 ra, rb;
+  float4 ra = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rb = ra;
+  // splats spanning many tile rows are counted by the whole wavefront (a lane per row), the
+  // rest by their own lane, so one large splat does not serialise its wavefront
+  const bool wide = g.vis && (bnd.w / kTile - bnd.z / kTile) >= kWideRows;
   if (g.vis) {
     ra = make_float4(g.mx, g.my, g.A, g.B);
     rb = make_float4(g.C, g.o, g.vz, thr);
-    count = static_cast<uint32_t>(count_touched_tiles(ra, rb, bnd));
-    g.vis = count > 0;
+    if (!wide) count = static_cast<uint32_t>(count_touched_tiles(ra, rb, bnd));
   }
+  for (uint64_t wm = __ballot(wide ? 1 : 0); wm != 0ull; wm &= wm - 1ull) {
+    const int src = __ffsll(static_cast<unsigned long long>(wm)) - 1;
+    const float4 sa = make_float4(__shfl(ra.x, src, 64), __shfl(ra.y, src, 64), __shfl(ra.z, src, 64),
+                                  __shfl(ra.w, src, 64));
+    const float4 sb = make_float4(__shfl(rb.x, src, 64), __shfl(rb.y, src, 64), __shfl(rb.z, src, 64),
+                                  __shfl(rb.w, src, 64));
+    const int4 sd = make_int4(__shfl(bnd.x, src, 64), __shfl(bnd.y, src, 64), __shfl(bnd.z, src, 64),
+                              __shfl(bnd.w, src, 64));
+    const uint32_t c = wave_count_touched_tiles(sa, sb, sd, lane);
+    if (lane == src) count = c;
+  }
+  if (g.vis) g.vis = count > 0;
 
   // Colour: stage the wavefront's SH rows through LDS (wave-uniform branch).
   const uint64_t vmask = __ballot(g.vis ? 1 : 0);
