@@ -153,6 +153,7 @@ constexpr int kRsWaves = kRsThreads / kWave;      // 4
 constexpr int kRsRounds = 16;                     // 64-key rounds per wavefront
 constexpr int kRsWaveKeys = kRsRounds * kWave;    // 1024
 constexpr int kRsTile = kRsWaves * kRsWaveKeys;   // 4096 keys per workgroup
+constexpr int kRsTotCopies = 64;                  // copies of each pass's digit totals
 
 template <int BITS>
 __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
@@ -192,10 +193,13 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* 
     if (valid && (peers & lt) == 0ull) atomicAdd(&s_h[d], static_cast<uint32_t>(__popcll(peers)));
   }
   __syncthreads();
+  // digit totals are spread over kRsTotCopies copies so no address takes more than
+  // n_tiles / kRsTotCopies atomics (a single copy serialises at the L2 on hot digits)
+  uint32_t* tot = totals + (blockIdx.x % kRsTotCopies) * 256;
   for (int k = threadIdx.x; k < R; k += kRsThreads) {
     const uint32_t c = s_h[k];
     tile_hist[static_cast<int64_t>(k) * n_tiles + blockIdx.x] = c;
-    if (c) atomicAdd(&totals[k], c);
+    if (c) atomicAdd(&tot[k], c);
   }
 }
 
@@ -205,8 +209,15 @@ __global__ __launch_bounds__(kScanThreads) void rs_rowscan_kernel(uint32_t* __re
                                                                   const uint32_t* __restrict__ totals) {
   __shared__ uint32_t s_wave[4];
   const int d = blockIdx.x;
+  // base = keys with a smaller digit: thread t sums the copies of digit t's total when t < d
+  static_assert(kScanThreads == 256, "one thread per 8-bit digit");
+  uint32_t part = 0;
+  if (static_cast<int>(threadIdx.x) < d) {
+#pragma unroll 16
+    for (int c = 0; c < kRsTotCopies; ++c) part += totals[c * 256 + threadIdx.x];
+  }
   uint32_t base;
-  block_inclusive_scan(static_cast<int>(threadIdx.x) < d ? totals[threadIdx.x] : 0u, s_wave, base);
+  block_inclusive_scan(part, s_wave, base);
   uint32_t* row = tile_hist + static_cast<int64_t>(d) * n_tiles;
   uint32_t run = base;
   for (int c0 = 0; c0 < n_tiles; c0 += kScanTile) {
@@ -318,7 +329,7 @@ static SortPlan sort_plan(int bits) {
 static size_t sort_ws(int64_t m) {
   const int64_t nt = (m + kRsTile - 1) / kRsTile;
   const int64_t hist = 256 * (nt > 0 ? nt : 1);
-  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * 256 * 4);
+  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * kRsTotCopies * 256 * 4);
 }
 
 template <int BITS>
@@ -349,7 +360,9 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
   uint32_t* tile_hist = reinterpret_cast<uint32_t*>(ws);
   ws += align_up(static_cast<int64_t>(256) * n_tiles * 4);
   uint32_t* totals = reinterpret_cast<uint32_t*>(ws);
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(4), dim3(256), 0, st, totals, int64_t(4 * 256), 0u);
+  const int64_t tot_words = int64_t(4) * kRsTotCopies * 256;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(tot_words / 256)), dim3(256), 0, st, totals,
+                     tot_words, 0u);
   // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
   // the last pass lands in (k_out, v_out) and no pass works in place
   const uint32_t* src_k = k;
@@ -358,7 +371,7 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     const bool to_out = ((plan.passes - 1 - p) % 2) == 0;
     uint32_t* dst_k = to_out ? k_out : k_alt;
     uint32_t* dst_v = to_out ? v_out : v_alt;
-    uint32_t* tot = totals + 256 * p;
+    uint32_t* tot = totals + kRsTotCopies * 256 * p;
     const int shift = plan.bits * p;
     switch (plan.bits) {
       case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
