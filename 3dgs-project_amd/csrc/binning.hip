@@ -440,10 +440,29 @@ __device__ __forceinline__ int4 clamp_rect(int4 r, int tiles_x, int tiles_y) {
 }
 
 // 3D: tiles from the row-band rule; 2D: every tile of the rectangle [x0, x1) x [y0, y1).
-// A lane emits its own Gaussian's instances unless the Gaussian has more than kEmitLane of
-// them; those are emitted by the whole wavefront, a lane per tile row for the row ranges and
-// a lane per instance for the (then contiguous, coalesced) writes.
-constexpr uint32_t kEmitLane = 8;
+// A wavefront emits the instances of 64 consecutive Gaussians of the depth order, whose
+// instances form one contiguous output range. It numbers their tile rows, computes the
+// touched columns of up to kEmitChunk rows at a time (a lane per row), and writes the
+// instances of those rows with one lane per instance, so stores are coalesced and a wide
+// Gaussian costs its own rows and instances only.
+constexpr int kEmitChunk = 256;
+constexpr int64_t kMaxTiles = int64_t(1) << 26;  // tile ids share a word with a 6-bit lane index
+
+struct EmitSetup {
+  float mx, my, A, B, det, tA, vmax, vr;  // 3D band setup
+  int4 d;                                 // 3D: pixel bounds; rectangles: clamped tile rectangle
+};
+
+// Exclusive prefix sum over the wavefront; `total` receives the sum of all lanes.
+__device__ __forceinline__ uint32_t wave_excl_scan(uint32_t v, int lane, uint32_t& total) {
+  uint32_t incl = v;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  total = __shfl(incl, kWave - 1, 64);
+  return incl - v;
+}
 
 template <bool kRect>
 __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ rec,
@@ -452,99 +471,110 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
                                                    const uint32_t* __restrict__ offs, int64_t n,
                                                    int tiles_x, int tiles_y, uint32_t* __restrict__ tkeys,
                                                    uint32_t* __restrict__ vals) {
-  __shared__ uint32_t s_excl[4][kWave];
-  __shared__ uint32_t s_row[4][kWave];  // (tile row << 16) | first tile column of the row
+  __shared__ EmitSetup s_set[4][kWave];
+  __shared__ uint32_t s_rex[4][kWave];       // exclusive prefix of tile rows over the 64 Gaussians
+  __shared__ uint32_t s_gid[4][kWave];
+  __shared__ uint32_t s_iex[4][kEmitChunk];  // row instance counts, then their exclusive prefix
+  __shared__ uint32_t s_row[4][kEmitChunk];  // (owner lane << 26) | first tile of the row
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  uint32_t off = 0, cap = 0, g = 0;  // cap: this Gaussian's slots; never write past them
+  const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kWave;
+  if (j0 >= n) return;  // whole wavefront
+  const int64_t j = j0 + lane;
+  uint32_t off = 0, cap = 0, rows = 0;
   if (j < n) {
     off = offs[j];
     cap = offs[j + 1] - off;
-    if (cap) g = order[j];
   }
-  const bool wide = cap > kEmitLane;
-  if (cap && !wide) {
+  EmitSetup es = {};
+  uint32_t g = 0;
+  if (cap) {
+    g = order[j];
     if constexpr (kRect) {
       const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
-      uint32_t k = 0;
-      for (int ty = r.y; ty < r.w; ++ty)
-        for (int tx = r.x; tx < r.z; ++tx) {
-          if (k < cap) {
-            tkeys[off + k] = static_cast<uint32_t>(ty * tiles_x + tx);
-            vals[off + k] = g;
-          }
-          ++k;
-        }
+      es.d = r;
+      rows = (r.z > r.x && r.w > r.y) ? static_cast<uint32_t>(r.w - r.y) : 0u;
     } else {
-      const SplatRec r = rec[g];
-      for_each_touched_tile(r.a, r.b, r.d, tiles_x, [&](int tile, int k) {
-        if (static_cast<uint32_t>(k) < cap) {
-          tkeys[off + k] = static_cast<uint32_t>(tile);
-          vals[off + k] = g;
-        }
-      });
+      const float4 a = rec[g].a, b = rec[g].b;
+      const int4 d = rec[g].d;
+      const BandSetup bs = band_setup(a, b);
+      es.mx = bs.mx; es.my = bs.my; es.A = bs.A; es.B = bs.B;
+      es.det = bs.det; es.tA = bs.tA; es.vmax = bs.vmax; es.vr = bs.vr;
+      es.d = d;
+      rows = static_cast<uint32_t>(max(d.w / kTile - d.z / kTile + 1, 0));
     }
   }
-  for (uint64_t wm = __ballot(wide ? 1 : 0); wm != 0ull; wm &= wm - 1ull) {
-    const int src = __ffsll(static_cast<unsigned long long>(wm)) - 1;
-    const uint32_t wg = __shfl(g, src, 64), woff = __shfl(off, src, 64), wcap = __shfl(cap, src, 64);
-    int ty0, ty1;
-    int4 rr;
-    BandSetup bs;
-    int4 bd;
-    if constexpr (kRect) {
-      rr = clamp_rect(rects[wg], tiles_x, tiles_y);
-      ty0 = rr.y;
-      ty1 = rr.w - 1;
-    } else {
-      const SplatRec r = rec[wg];
-      bs = band_setup(r.a, r.b);
-      bd = r.d;
-      ty0 = bd.z / kTile;
-      ty1 = bd.w / kTile;
-    }
-    uint32_t done = 0;
-    for (int row0 = ty0; row0 <= ty1; row0 += kWave) {
-      const int ty = row0 + lane;
-      uint32_t nt = 0;
-      int tx0 = 0;
-      if (ty <= ty1) {
+  s_set[wave][lane] = es;
+  s_gid[wave][lane] = g;
+  uint32_t total_rows;
+  s_rex[wave][lane] = wave_excl_scan(rows, lane, total_rows);
+  const uint32_t base = __shfl(off, 0, 64);
+  const int last = static_cast<int>(min<int64_t>(kWave - 1, n - 1 - j0));
+  const uint32_t wave_cap = __shfl(off + cap, last, 64) - base;  // never write past the range
+  wave_sync();
+
+  uint32_t done = 0;
+  for (uint32_t rc = 0; rc < total_rows; rc += kEmitChunk) {
+    const int nr = static_cast<int>(min<uint32_t>(kEmitChunk, total_rows - rc));
+    for (int q = lane; q < ((nr + kWave - 1) & ~(kWave - 1)); q += kWave) {
+      uint32_t nt = 0, first = 0;
+      if (q < nr) {
+        const uint32_t item = rc + static_cast<uint32_t>(q);
+        int own = 0;  // last Gaussian whose first row is <= item
+#pragma unroll
+        for (int step = 32; step > 0; step >>= 1)
+          if (s_rex[wave][own + step] <= item) own += step;
+        const EmitSetup& e = s_set[wave][own];
+        const int r = static_cast<int>(item - s_rex[wave][own]);
+        int ty, tx0;
         if constexpr (kRect) {
-          tx0 = rr.x;
-          nt = static_cast<uint32_t>(max(rr.z - rr.x, 0));
+          ty = e.d.y + r;
+          tx0 = e.d.x;
+          nt = static_cast<uint32_t>(e.d.z - e.d.x);
         } else {
-          nt = row_tiles(bs, bd, ty, tx0);
+          BandSetup bs;
+          bs.mx = e.mx; bs.my = e.my; bs.A = e.A; bs.B = e.B;
+          bs.det = e.det; bs.tA = e.tA; bs.vmax = e.vmax; bs.vr = e.vr;
+          bs.ok = e.det > 0.0f;
+          ty = e.d.z / kTile + r;
+          nt = row_tiles(bs, e.d, ty, tx0);
         }
+        first = (static_cast<uint32_t>(own) << 26) | static_cast<uint32_t>(ty * tiles_x + tx0);
       }
-      uint32_t incl = nt;
-      for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t u = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += u;
-      }
-      const uint32_t total = __shfl(incl, kWave - 1, 64);
-      s_excl[wave][lane] = incl - nt;
-      s_row[wave][lane] = (static_cast<uint32_t>(ty) << 16) | static_cast<uint32_t>(tx0);
-      wave_sync();
-      for (uint32_t it = lane; it < total; it += kWave) {
-        // row of item it: the last lane whose exclusive start is <= it (it has tiles)
-        int lo = 0, hi = kWave - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (s_excl[wave][mid] <= it) lo = mid;
-          else hi = mid - 1;
-        }
-        const uint32_t rw = s_row[wave][lo];
-        const uint32_t tile = (rw >> 16) * static_cast<uint32_t>(tiles_x) + (rw & 0xffffu) + (it - s_excl[wave][lo]);
-        const uint32_t k = done + it;
-        if (k < wcap) {
-          tkeys[woff + k] = tile;
-          vals[woff + k] = wg;
-        }
-      }
-      done += total;
-      wave_sync();
+      s_iex[wave][q] = nt;
+      s_row[wave][q] = first;
     }
+    wave_sync();
+    uint32_t c[4], lsum = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int q = 4 * lane + e;
+      c[e] = q < nr ? s_iex[wave][q] : 0u;
+      lsum += c[e];
+    }
+    uint32_t ctotal;
+    uint32_t ex = wave_excl_scan(lsum, lane, ctotal);
+    wave_sync();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s_iex[wave][4 * lane + e] = ex;
+      ex += c[e];
+    }
+    wave_sync();
+    for (uint32_t p = lane; p < ctotal; p += kWave) {
+      int q = 0;  // last row whose first instance is <= p
+#pragma unroll
+      for (int step = kEmitChunk / 2; step > 0; step >>= 1)
+        if (q + step < nr && s_iex[wave][q + step] <= p) q += step;
+      const uint32_t rw = s_row[wave][q];
+      const uint32_t k = done + p;
+      if (k < wave_cap) {
+        tkeys[base + k] = (rw & 0x3ffffffu) + (p - s_iex[wave][q]);
+        vals[base + k] = s_gid[wave][rw >> 26];
+      }
+    }
+    done += ctotal;
+    wave_sync();
   }
 }
 
@@ -735,6 +765,7 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touc
              static_cast<long long>(n), static_cast<long long>(m));
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const CamK k = make_cam(*cam);
+  GS_REQUIRE(static_cast<int64_t>(k.tiles_x) * k.tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
   const int n_tiles = k.tiles_x * k.tiles_y;
   const size_t need = bin_ws(n, m, n_tiles);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
@@ -767,6 +798,7 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   clear_error();
   GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32) && tiles_x > 0 && tiles_y > 0, GS_ERR_ARG,
              "invalid sizes");
+  GS_REQUIRE(static_cast<int64_t>(tiles_x) * tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
   GS_REQUIRE(depth_dtype == GS_FLOAT32 || depth_dtype == GS_FLOAT64, GS_ERR_ARG, "invalid depth dtype");
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const int n_tiles = tiles_x * tiles_y;
