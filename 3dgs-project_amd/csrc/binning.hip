@@ -138,13 +138,14 @@ __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
 // Stable LSD radix sort of (uint32 key, uint32 value) pairs, BITS <= 8 bits per pass.
 //
 // Per pass three kernels, none of which waits on another workgroup:
-//   upsweep  each 4096-key tile counts its digits -> tile_hist[digit][tile], and adds them to
-//            the pass's digit totals (global atomics)
-//   rowscan  one workgroup per digit: exclusive scan of its row over the tiles, plus the
-//            number of keys with smaller digits -> global start of (digit, tile)
-//   scatter  each tile ranks its keys stably (per-wavefront digit counters in LDS; equal
-//            digits inside a 64-key round matched with BITS ballots), stages the tile in LDS
-//            in digit order and writes it out as one contiguous run per digit (coalesced)
+//   upsweep  each 4096-key tile counts its digits (LDS atomics) -> tile_hist[digit][tile]
+//   rowscan  one workgroup per digit: exclusive scan of its row over the tiles, and the
+//            digit's total
+//   scatter  each tile scans the digit totals (start of each digit), adds its row entries
+//            -> global start of (digit, tile); ranks its keys stably (per-wavefront digit
+//            counters in LDS; equal digits inside a 64-key round matched with BITS ballots),
+//            stages the tile in LDS in digit order and writes it out as one contiguous run
+//            per digit (coalesced)
 // Wavefront w of a tile owns the contiguous keys [1024 w, 1024 (w + 1)), read in 16
 // coalesced rounds, so (wavefront, round, lane) is input order: the sort is stable.
 // ---------------------------------------------------------------------------------------
@@ -153,7 +154,6 @@ constexpr int kRsWaves = kRsThreads / kWave;      // 4
 constexpr int kRsRounds = 16;                     // 64-key rounds per wavefront
 constexpr int kRsWaveKeys = kRsRounds * kWave;    // 1024
 constexpr int kRsTile = kRsWaves * kRsWaveKeys;   // 4096 keys per workgroup
-constexpr int kRsTotCopies = 64;                  // copies of each pass's digit totals
 
 template <int BITS>
 __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
@@ -170,56 +170,41 @@ __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
 template <int BITS>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* __restrict__ keys, int64_t m,
                                                                 int shift, uint32_t* __restrict__ tile_hist,
-                                                                int n_tiles, uint32_t* __restrict__ totals) {
+                                                                int n_tiles) {
   constexpr int R = 1 << BITS;
-  __shared__ uint32_t s_h[R];
+  __shared__ uint32_t s_h[kRsWaves][R];  // per-wavefront counts (LDS atomics)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  for (int k = threadIdx.x; k < R; k += kRsThreads) s_h[k] = 0;
+  for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_h[0][0])[k] = 0;
   __syncthreads();
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kRsTile + wave * kRsWaveKeys;
-  const uint64_t lt = lanemask_lt(lane);
   uint32_t key[kRsRounds];
 #pragma unroll
-  for (int r = 0; r < kRsRounds; ++r) {  // all loads in flight before the first ballot
+  for (int r = 0; r < kRsRounds; ++r) {  // all loads in flight before the first count
     const int64_t idx = base + r * kWave + lane;
     key[r] = idx < m ? keys[idx] : 0u;
   }
 #pragma unroll
   for (int r = 0; r < kRsRounds; ++r) {
-    const bool valid = base + r * kWave + lane < m;
-    const uint32_t d = (key[r] >> shift) & (R - 1);
-    const uint64_t peers = match_bits<BITS>(d, valid);
-    if (valid && (peers & lt) == 0ull) atomicAdd(&s_h[d], static_cast<uint32_t>(__popcll(peers)));
+    if (base + r * kWave + lane < m) atomicAdd(&s_h[wave][(key[r] >> shift) & (R - 1)], 1u);
   }
   __syncthreads();
-  // digit totals are spread over kRsTotCopies copies so no address takes more than
-  // n_tiles / kRsTotCopies atomics (a single copy serialises at the L2 on hot digits)
-  uint32_t* tot = totals + (blockIdx.x % kRsTotCopies) * 256;
   for (int k = threadIdx.x; k < R; k += kRsThreads) {
-    const uint32_t c = s_h[k];
+    uint32_t c = 0;
+#pragma unroll
+    for (int w = 0; w < kRsWaves; ++w) c += s_h[w][k];
     tile_hist[static_cast<int64_t>(k) * n_tiles + blockIdx.x] = c;
-    if (c) atomicAdd(&tot[k], c);
   }
 }
 
-// Workgroup `d`: entries [d][0 .. n_tiles) become (keys with digit < d) + (keys with digit d in
-// earlier tiles).
+// Workgroup `d`: entries [d][0 .. n_tiles) become the number of keys with digit d in earlier
+// tiles; totals[d] receives the row total.
 __global__ __launch_bounds__(kScanThreads) void rs_rowscan_kernel(uint32_t* __restrict__ tile_hist, int n_tiles,
-                                                                  const uint32_t* __restrict__ totals) {
+                                                                  uint32_t* __restrict__ totals) {
   __shared__ uint32_t s_wave[4];
   const int d = blockIdx.x;
-  // base = keys with a smaller digit: thread t sums the copies of digit t's total when t < d
-  static_assert(kScanThreads == 256, "one thread per 8-bit digit");
-  uint32_t part = 0;
-  if (static_cast<int>(threadIdx.x) < d) {
-#pragma unroll 16
-    for (int c = 0; c < kRsTotCopies; ++c) part += totals[c * 256 + threadIdx.x];
-  }
-  uint32_t base;
-  block_inclusive_scan(part, s_wave, base);
   uint32_t* row = tile_hist + static_cast<int64_t>(d) * n_tiles;
-  uint32_t run = base;
+  uint32_t run = 0;
   for (int c0 = 0; c0 < n_tiles; c0 += kScanTile) {
     uint32_t loc[kScanItems];
     uint32_t sum = 0;
@@ -240,12 +225,14 @@ __global__ __launch_bounds__(kScanThreads) void rs_rowscan_kernel(uint32_t* __re
     }
     run += total;
   }
+  if (threadIdx.x == 0) totals[d] = run;
 }
 
 template <int BITS>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin, uint32_t* __restrict__ kout,
-    uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles) {
+    uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles,
+    const uint32_t* __restrict__ totals) {
   constexpr int R = 1 << BITS;
   __shared__ uint32_t s_cnt[kRsWaves][R];  // per-wavefront digit counts, then wavefront offsets
   __shared__ uint32_t s_excl[R];           // start of each digit inside the staged tile
@@ -256,8 +243,15 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_cnt[0][0])[k] = 0;
-  for (int k = threadIdx.x; k < R; k += kRsThreads)
-    s_goff[k] = tile_offs[static_cast<int64_t>(k) * n_tiles + blockIdx.x];
+  {
+    // global start of (digit, tile): keys with a smaller digit + keys of the digit in earlier tiles
+    static_assert(kRsThreads >= 256, "a thread per digit");
+    const int d = threadIdx.x;
+    const uint32_t t = d < R ? totals[d] : 0u;
+    uint32_t all;
+    const uint32_t incl = block_inclusive_scan(t, s_wave, all);
+    if (d < R) s_goff[d] = incl - t + tile_offs[static_cast<int64_t>(d) * n_tiles + blockIdx.x];
+  }
   __syncthreads();
   const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kRsTile;
   const int64_t base = tile_base + wave * kRsWaveKeys;
@@ -329,17 +323,17 @@ static SortPlan sort_plan(int bits) {
 static size_t sort_ws(int64_t m) {
   const int64_t nt = (m + kRsTile - 1) / kRsTile;
   const int64_t hist = 256 * (nt > 0 ? nt : 1);
-  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * kRsTotCopies * 256 * 4);
+  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * 256 * 4);
 }
 
 template <int BITS>
 static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
                       uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st) {
   hipLaunchKernelGGL(rs_upsweep_kernel<BITS>, dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
-                     n_tiles, totals);
+                     n_tiles);
   hipLaunchKernelGGL(rs_rowscan_kernel, dim3(1 << BITS), dim3(kScanThreads), 0, st, tile_hist, n_tiles, totals);
   hipLaunchKernelGGL(rs_scatter_kernel<BITS>, dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
-                     tile_hist, n_tiles);
+                     tile_hist, n_tiles, totals);
 }
 
 // Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
@@ -360,9 +354,6 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
   uint32_t* tile_hist = reinterpret_cast<uint32_t*>(ws);
   ws += align_up(static_cast<int64_t>(256) * n_tiles * 4);
   uint32_t* totals = reinterpret_cast<uint32_t*>(ws);
-  const int64_t tot_words = int64_t(4) * kRsTotCopies * 256;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(tot_words / 256)), dim3(256), 0, st, totals,
-                     tot_words, 0u);
   // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
   // the last pass lands in (k_out, v_out) and no pass works in place
   const uint32_t* src_k = k;
@@ -371,7 +362,7 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     const bool to_out = ((plan.passes - 1 - p) % 2) == 0;
     uint32_t* dst_k = to_out ? k_out : k_alt;
     uint32_t* dst_v = to_out ? v_out : v_alt;
-    uint32_t* tot = totals + kRsTotCopies * 256 * p;
+    uint32_t* tot = totals + 256 * p;
     const int shift = plan.bits * p;
     switch (plan.bits) {
       case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
@@ -440,13 +431,32 @@ __device__ __forceinline__ int4 clamp_rect(int4 r, int tiles_x, int tiles_y) {
 }
 
 // 3D: tiles from the row-band rule; 2D: every tile of the rectangle [x0, x1) x [y0, y1).
-// A wavefront emits the instances of 64 consecutive Gaussians of the depth order, whose
-// instances form one contiguous output range. It numbers their tile rows, computes the
-// touched columns of up to kEmitChunk rows at a time (a lane per row), and writes the
-// instances of those rows with one lane per instance, so stores are coalesced and a wide
-// Gaussian costs its own rows and instances only.
+// Emission is balanced by instances: wavefront w emits the Gaussians (in depth order) whose
+// first instance lies in [kEmitSpan w, kEmitSpan (w + 1)), 64 at a time. The instances of 64
+// consecutive Gaussians form one contiguous output range: the wavefront numbers their tile
+// rows, computes the touched columns of up to kEmitChunk rows at a time (a lane per row), then
+// writes rows of at least kEmitWide tiles one row at a time (a lane per tile) and the other
+// rows' instances a lane per instance, so stores are coalesced.
+constexpr uint32_t kEmitSpan = 512;
 constexpr int kEmitChunk = 256;
+constexpr uint32_t kEmitWide = 32;
 constexpr int64_t kMaxTiles = int64_t(1) << 26;  // tile ids share a word with a 6-bit lane index
+
+// First Gaussian of every emission window: Gaussian j starts the windows w with
+// offs[j - 1] < kEmitSpan w <= offs[j]. wstart[n_windows] = the first Gaussian with
+// offs[j] = m, which ends the last window (Gaussians after it have no instances).
+__global__ void emit_windows_kernel(const uint32_t* __restrict__ offs, int64_t n, int64_t n_windows,
+                                    uint32_t* __restrict__ wstart) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j > n) return;
+  const int64_t cur = offs[j];
+  const int64_t prev = j == 0 ? -1 : static_cast<int64_t>(offs[j - 1]);
+  const int64_t w_lo = j == 0 ? 0 : prev / kEmitSpan + 1;
+  const int64_t w_hi = min(cur / kEmitSpan, n_windows - 1);
+  for (int64_t w = w_lo; w <= w_hi; ++w) wstart[w] = static_cast<uint32_t>(j);
+  const int64_t m = offs[n];
+  if (prev < m && cur >= m) wstart[n_windows] = static_cast<uint32_t>(j);
+}
 
 struct EmitSetup {
   float mx, my, A, B, det, tA, vmax, vr;  // 3D band setup
@@ -469,138 +479,238 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
                                                    const int4* __restrict__ rects,
                                                    const uint32_t* __restrict__ order,
                                                    const uint32_t* __restrict__ offs, int64_t n,
+                                                   const uint32_t* __restrict__ wstart, int64_t n_windows,
                                                    int tiles_x, int tiles_y, uint32_t* __restrict__ tkeys,
                                                    uint32_t* __restrict__ vals) {
   __shared__ EmitSetup s_set[4][kWave];
   __shared__ uint32_t s_rex[4][kWave];       // exclusive prefix of tile rows over the 64 Gaussians
   __shared__ uint32_t s_gid[4][kWave];
   __shared__ uint32_t s_iex[4][kEmitChunk];  // row instance counts, then their exclusive prefix
+  __shared__ uint32_t s_nex[4][kEmitChunk];  // exclusive prefix over the narrow rows only
   __shared__ uint32_t s_row[4][kEmitChunk];  // (owner lane << 26) | first tile of the row
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t j0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * kWave;
-  if (j0 >= n) return;  // whole wavefront
-  const int64_t j = j0 + lane;
-  uint32_t off = 0, cap = 0, rows = 0;
-  if (j < n) {
-    off = offs[j];
-    cap = offs[j + 1] - off;
-  }
-  EmitSetup es = {};
-  uint32_t g = 0;
-  if (cap) {
-    g = order[j];
-    if constexpr (kRect) {
-      const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
-      es.d = r;
-      rows = (r.z > r.x && r.w > r.y) ? static_cast<uint32_t>(r.w - r.y) : 0u;
-    } else {
-      const float4 a = rec[g].a, b = rec[g].b;
-      const int4 d = rec[g].d;
-      const BandSetup bs = band_setup(a, b);
-      es.mx = bs.mx; es.my = bs.my; es.A = bs.A; es.B = bs.B;
-      es.det = bs.det; es.tA = bs.tA; es.vmax = bs.vmax; es.vr = bs.vr;
-      es.d = d;
-      rows = static_cast<uint32_t>(max(d.w / kTile - d.z / kTile + 1, 0));
-    }
-  }
-  s_set[wave][lane] = es;
-  s_gid[wave][lane] = g;
-  uint32_t total_rows;
-  s_rex[wave][lane] = wave_excl_scan(rows, lane, total_rows);
-  const uint32_t base = __shfl(off, 0, 64);
-  const int last = static_cast<int>(min<int64_t>(kWave - 1, n - 1 - j0));
-  const uint32_t wave_cap = __shfl(off + cap, last, 64) - base;  // never write past the range
-  wave_sync();
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (w >= n_windows) return;  // whole wavefront
+  const int64_t ja = wstart[w];
+  const int64_t jb = wstart[w + 1];
 
-  uint32_t done = 0;
-  for (uint32_t rc = 0; rc < total_rows; rc += kEmitChunk) {
-    const int nr = static_cast<int>(min<uint32_t>(kEmitChunk, total_rows - rc));
-    for (int q = lane; q < ((nr + kWave - 1) & ~(kWave - 1)); q += kWave) {
-      uint32_t nt = 0, first = 0;
-      if (q < nr) {
-        const uint32_t item = rc + static_cast<uint32_t>(q);
-        int own = 0;  // last Gaussian whose first row is <= item
+  for (int64_t j0 = ja; j0 < jb; j0 += kWave) {
+    const int64_t j = j0 + lane;
+    uint32_t off = 0, cap = 0, rows = 0;
+    if (j < jb) {
+      off = offs[j];
+      cap = offs[j + 1] - off;
+    }
+    EmitSetup es = {};
+    uint32_t g = 0;
+    if (cap) {
+      g = order[j];
+      if constexpr (kRect) {
+        const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
+        es.d = r;
+        rows = (r.z > r.x && r.w > r.y) ? static_cast<uint32_t>(r.w - r.y) : 0u;
+      } else {
+        const float4 a = rec[g].a, b = rec[g].b;
+        const int4 d = rec[g].d;
+        const BandSetup bs = band_setup(a, b);
+        es.mx = bs.mx; es.my = bs.my; es.A = bs.A; es.B = bs.B;
+        es.det = bs.det; es.tA = bs.tA; es.vmax = bs.vmax; es.vr = bs.vr;
+        es.d = d;
+        rows = static_cast<uint32_t>(max(d.w / kTile - d.z / kTile + 1, 0));
+      }
+    }
+    wave_sync();  // the previous group is done with the LDS
+    s_set[wave][lane] = es;
+    s_gid[wave][lane] = g;
+    uint32_t total_rows;
+    s_rex[wave][lane] = wave_excl_scan(rows, lane, total_rows);
+    const uint32_t base = __shfl(off, 0, 64);
+    const int last = static_cast<int>(min<int64_t>(kWave - 1, jb - 1 - j0));
+    const uint32_t wave_cap = __shfl(off + cap, last, 64) - base;  // never write past the range
+    wave_sync();
+
+    uint32_t done = 0;
+    for (uint32_t rc = 0; rc < total_rows; rc += kEmitChunk) {
+      const int nr = static_cast<int>(min<uint32_t>(kEmitChunk, total_rows - rc));
+      for (int q = lane; q < ((nr + kWave - 1) & ~(kWave - 1)); q += kWave) {
+        uint32_t nt = 0, first = 0;
+        if (q < nr) {
+          const uint32_t item = rc + static_cast<uint32_t>(q);
+          int own = 0;  // last Gaussian whose first row is <= item
 #pragma unroll
-        for (int step = 32; step > 0; step >>= 1)
-          if (s_rex[wave][own + step] <= item) own += step;
-        const EmitSetup& e = s_set[wave][own];
-        const int r = static_cast<int>(item - s_rex[wave][own]);
-        int ty, tx0;
-        if constexpr (kRect) {
-          ty = e.d.y + r;
-          tx0 = e.d.x;
-          nt = static_cast<uint32_t>(e.d.z - e.d.x);
-        } else {
-          BandSetup bs;
-          bs.mx = e.mx; bs.my = e.my; bs.A = e.A; bs.B = e.B;
-          bs.det = e.det; bs.tA = e.tA; bs.vmax = e.vmax; bs.vr = e.vr;
-          bs.ok = e.det > 0.0f;
-          ty = e.d.z / kTile + r;
-          nt = row_tiles(bs, e.d, ty, tx0);
+          for (int step = 32; step > 0; step >>= 1)
+            if (s_rex[wave][own + step] <= item) own += step;
+          const EmitSetup& e = s_set[wave][own];
+          const int r = static_cast<int>(item - s_rex[wave][own]);
+          int ty, tx0;
+          if constexpr (kRect) {
+            ty = e.d.y + r;
+            tx0 = e.d.x;
+            nt = static_cast<uint32_t>(e.d.z - e.d.x);
+          } else {
+            BandSetup bs;
+            bs.mx = e.mx; bs.my = e.my; bs.A = e.A; bs.B = e.B;
+            bs.det = e.det; bs.tA = e.tA; bs.vmax = e.vmax; bs.vr = e.vr;
+            bs.ok = e.det > 0.0f;
+            ty = e.d.z / kTile + r;
+            nt = row_tiles(bs, e.d, ty, tx0);
+          }
+          first = (static_cast<uint32_t>(own) << 26) | static_cast<uint32_t>(ty * tiles_x + tx0);
         }
-        first = (static_cast<uint32_t>(own) << 26) | static_cast<uint32_t>(ty * tiles_x + tx0);
+        s_iex[wave][q] = nt;
+        s_row[wave][q] = first;
       }
-      s_iex[wave][q] = nt;
-      s_row[wave][q] = first;
-    }
-    wave_sync();
-    uint32_t c[4], lsum = 0;
+      wave_sync();
+      uint32_t c[4], ex[4], lsum = 0, nsum = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int q = 4 * lane + e;
-      c[e] = q < nr ? s_iex[wave][q] : 0u;
-      lsum += c[e];
-    }
-    uint32_t ctotal;
-    uint32_t ex = wave_excl_scan(lsum, lane, ctotal);
-    wave_sync();
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      s_iex[wave][4 * lane + e] = ex;
-      ex += c[e];
-    }
-    wave_sync();
-    for (uint32_t p = lane; p < ctotal; p += kWave) {
-      int q = 0;  // last row whose first instance is <= p
-#pragma unroll
-      for (int step = kEmitChunk / 2; step > 0; step >>= 1)
-        if (q + step < nr && s_iex[wave][q + step] <= p) q += step;
-      const uint32_t rw = s_row[wave][q];
-      const uint32_t k = done + p;
-      if (k < wave_cap) {
-        tkeys[base + k] = (rw & 0x3ffffffu) + (p - s_iex[wave][q]);
-        vals[base + k] = s_gid[wave][rw >> 26];
+      for (int e = 0; e < 4; ++e) {
+        const int q = 4 * lane + e;
+        c[e] = q < nr ? s_iex[wave][q] : 0u;
+        lsum += c[e];
+        nsum += c[e] < kEmitWide ? c[e] : 0u;
       }
+      uint32_t ctotal, ntotal;
+      uint32_t run = wave_excl_scan(lsum, lane, ctotal);
+      uint32_t nrun = wave_excl_scan(nsum, lane, ntotal);
+      wave_sync();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ex[e] = run;
+        s_iex[wave][4 * lane + e] = run;
+        s_nex[wave][4 * lane + e] = nrun;
+        run += c[e];
+        nrun += c[e] < kEmitWide ? c[e] : 0u;
+      }
+      wave_sync();
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        for (uint64_t wm = __ballot(c[e] >= kEmitWide ? 1 : 0); wm != 0ull; wm &= wm - 1ull) {
+          const int src = __ffsll(static_cast<unsigned long long>(wm)) - 1;
+          const uint32_t nt = __shfl(c[e], src, 64), start = done + __shfl(ex[e], src, 64);
+          const uint32_t rw = s_row[wave][4 * src + e];
+          const uint32_t gw = s_gid[wave][rw >> 26];
+          for (uint32_t t = lane; t < nt; t += kWave) {
+            const uint32_t k = start + t;
+            if (k < wave_cap) {
+              tkeys[base + k] = (rw & 0x3ffffffu) + t;
+              vals[base + k] = gw;
+            }
+          }
+        }
+      }
+      for (uint32_t p = lane; p < ntotal; p += kWave) {
+        int q = 0;  // last row whose first narrow-row instance is <= p
+#pragma unroll
+        for (int step = kEmitChunk / 2; step > 0; step >>= 1)
+          if (q + step < nr && s_nex[wave][q + step] <= p) q += step;
+        const uint32_t rw = s_row[wave][q];
+        const uint32_t t = p - s_nex[wave][q];
+        const uint32_t k = done + s_iex[wave][q] + t;
+        if (k < wave_cap) {
+          tkeys[base + k] = (rw & 0x3ffffffu) + t;
+          vals[base + k] = s_gid[wave][rw >> 26];
+        }
+      }
+      done += ctotal;
+      wave_sync();
     }
-    done += ctotal;
-    wave_sync();
   }
 }
 
-// Per-tile [start, end) of the sorted instances by binary search of the sorted tile keys;
-// empty tiles get an empty range at their CSR position. Optionally the CSR offsets [T + 1].
-__device__ __forceinline__ uint32_t lower_bound_u32(const uint32_t* __restrict__ a, int64_t m, uint32_t v) {
-  int64_t lo = 0, hi = m;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (a[mid] < v) lo = mid + 1;
-    else hi = mid;
+// Per-tile [start, end) of the sorted instances from the key changes: the thread at the first
+// instance of a tile writes its start (and gives the empty tiles before it the empty range at
+// that position), the thread at its last instance writes its end (and closes the empty tiles
+// after the last tile at m).
+__global__ void tile_bounds_kernel(const uint32_t* __restrict__ tkeys, int64_t m, int n_tiles,
+                                   uint32_t* __restrict__ ranges) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p >= m) return;
+  const uint32_t t = tkeys[p];
+  if (t >= static_cast<uint32_t>(n_tiles)) return;  // not a tile id
+  const uint32_t pos = static_cast<uint32_t>(p);
+  const uint32_t prev = p > 0 ? tkeys[p - 1] : 0u;
+  if (p == 0 || prev != t) {
+    const uint32_t lo = p == 0 ? 0u : (prev < t ? prev + 1u : t);
+    for (uint32_t u = lo; u < t; ++u) {
+      ranges[2 * u] = pos;
+      ranges[2 * u + 1] = pos;
+    }
+    ranges[2 * t] = pos;
   }
-  return static_cast<uint32_t>(lo);
+  const bool last = p == m - 1;
+  if (last || tkeys[p + 1] != t) {
+    ranges[2 * t + 1] = pos + 1u;
+    if (last) {
+      for (uint32_t u = t + 1u; u < static_cast<uint32_t>(n_tiles); ++u) {
+        ranges[2 * u] = pos + 1u;
+        ranges[2 * u + 1] = pos + 1u;
+      }
+    }
+  }
 }
 
-__global__ void tile_ranges_kernel(const uint32_t* __restrict__ tkeys, int64_t m, int n_tiles,
-                                   uint32_t* __restrict__ ranges, uint32_t* __restrict__ offsets) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_tiles) return;
-  const uint32_t s = m > 0 ? lower_bound_u32(tkeys, m, static_cast<uint32_t>(t)) : 0u;
-  const uint32_t e = m > 0 ? lower_bound_u32(tkeys, m, static_cast<uint32_t>(t) + 1u) : 0u;
-  ranges[2 * t] = s;
-  ranges[2 * t + 1] = e;
-  if (offsets) {
-    offsets[t] = s;
-    if (t == n_tiles - 1) offsets[n_tiles] = e;
+// One workgroup: bucket counts ceil(len / 32) per tile, their exclusive scan into
+// bucket_offsets [T + 1], and optionally the CSR tile offsets [T + 1]. With m == 0 it also
+// writes the (empty) ranges.
+constexpr int kBoThreads = 1024;
+constexpr int kBoItems = 8;
+
+__global__ __launch_bounds__(kBoThreads) void bucket_offsets_kernel(uint32_t* __restrict__ ranges, int n_tiles,
+                                                                    int64_t m, uint32_t* __restrict__ boff,
+                                                                    uint32_t* __restrict__ tile_offsets) {
+  __shared__ uint32_t s_wave[kBoThreads / kWave];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t run = 0;
+  for (int c0 = 0; c0 < n_tiles; c0 += kBoThreads * kBoItems) {
+    uint32_t cnt[kBoItems], start[kBoItems], sum = 0;
+#pragma unroll
+    for (int e = 0; e < kBoItems; ++e) {
+      const int t = c0 + static_cast<int>(threadIdx.x) * kBoItems + e;
+      cnt[e] = 0;
+      start[e] = 0;
+      if (t < n_tiles) {
+        if (m > 0) {
+          start[e] = ranges[2 * t];
+          cnt[e] = (ranges[2 * t + 1] - start[e] + kBucket - 1) / kBucket;
+        } else {
+          ranges[2 * t] = 0;
+          ranges[2 * t + 1] = 0;
+        }
+      }
+      sum += cnt[e];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (int w = 0; w < kBoThreads / kWave; ++w) {
+      const uint32_t v = s_wave[w];
+      before += w < wave ? v : 0u;
+      total += v;
+    }
+    __syncthreads();
+    uint32_t pos = run + before + incl - sum;
+#pragma unroll
+    for (int e = 0; e < kBoItems; ++e) {
+      const int t = c0 + static_cast<int>(threadIdx.x) * kBoItems + e;
+      if (t < n_tiles) {
+        boff[t] = pos;
+        if (tile_offsets) tile_offsets[t] = start[e];
+      }
+      pos += cnt[e];
+    }
+    run += total;
+  }
+  if (threadIdx.x == 0) {
+    boff[n_tiles] = run;
+    if (tile_offsets) tile_offsets[n_tiles] = static_cast<uint32_t>(m);
   }
 }
 
@@ -609,14 +719,6 @@ __global__ void full_keys_kernel(const uint32_t* __restrict__ tkeys, const uint3
                                  const uint32_t* __restrict__ dkey_of, int64_t m, uint64_t* __restrict__ out) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p < m) out[p] = (static_cast<uint64_t>(tkeys[p]) << 32) | dkey_of[vals[p]];
-}
-
-__global__ void bucket_count_kernel(const uint32_t* __restrict__ ranges, int n_tiles,
-                                    uint32_t* __restrict__ counts) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_tiles) return;
-  const uint32_t len = ranges[2 * t + 1] - ranges[2 * t];
-  counts[t] = (len + kBucket - 1) / kBucket;
 }
 
 // One thread per bucket slot: binary search of the tile whose bucket range holds b.
@@ -663,7 +765,7 @@ static size_t bin_ws(int64_t n, int64_t m, int n_tiles) {
   s += align_up(m * 4);                     // sorted tile keys
   s += std::max(sort_ws(n), sort_ws(m));    // sort scratch (reused)
   s += scan_ws(n + 1);
-  s += align_up(static_cast<size_t>(n_tiles) * 4) + scan_ws(n_tiles);
+  s += align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);  // emission windows
   return s;
 }
 
@@ -684,8 +786,7 @@ static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, 
   uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
   char* sort_scratch = ws; ws += std::max(sort_ws(n), sort_ws(m));
   char* scan_scratch = ws; ws += scan_ws(n + 1);
-  uint32_t* bcount = reinterpret_cast<uint32_t*>(ws); ws += align_up(static_cast<size_t>(n_tiles) * 4);
-  char* tile_scratch = ws;
+  uint32_t* wstart = reinterpret_cast<uint32_t*>(ws); ws += align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);
 
   const bool by_depth = rec != nullptr || depth != nullptr || depth64 != nullptr;
   if (n > 0 && (m > 0 || order_out)) {
@@ -708,23 +809,25 @@ static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, 
     hipLaunchKernelGGL(gather_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, counts, n,
                        scounts);
     scan_rec(scounts, soffs, n, scan_scratch, st);
+    const int64_t n_windows = (m + kEmitSpan - 1) / kEmitSpan;
+    hipLaunchKernelGGL(emit_windows_kernel, dim3(grid_for(n + 1, 256)), dim3(256), 0, st, soffs, n, n_windows,
+                       wstart);
     if (rects) {
-      hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, rects, order,
-                         soffs, n, tiles_x, n_tiles / tiles_x, tkeys, tvals);
+      hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
+                         soffs, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     } else {
-      hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, rects, order,
-                         soffs, n, tiles_x, n_tiles / tiles_x, tkeys, tvals);
+      hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
+                         soffs, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     }
     radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
                          dkey_of, m, sorted_keys);
   }
-  hipLaunchKernelGGL(tile_ranges_kernel, dim3(grid_for(n_tiles, 256)), dim3(256), 0, st, tsorted, m, n_tiles,
-                     ranges, tile_offsets);
-  hipLaunchKernelGGL(bucket_count_kernel, dim3(grid_for(n_tiles, 256)), dim3(256), 0, st, ranges,
-                     n_tiles, bcount);
-  scan_rec(bcount, bucket_offsets, n_tiles, tile_scratch, st);
+  if (m > 0)
+    hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, n_tiles, ranges);
+  hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
+                     tile_offsets);
   return GS_OK;
 }
 
