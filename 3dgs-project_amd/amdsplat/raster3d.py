@@ -82,7 +82,8 @@ class ForwardState:
     sh_degree: int
     rec: torch.Tensor            # [n, 16] splat records
     touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
-    offsets: torch.Tensor        # [n + 1] int32
+    order: torch.Tensor          # [n] int32 Gaussians by depth (culled last)
+    offsets: torch.Tensor        # [n + 1] int32 instance offsets in that order; [n] = m
     m: int                       # instances
     keys: torch.Tensor           # [m] int64 sorted keys (empty unless keep_keys)
     point_list: torch.Tensor     # [m] int32
@@ -165,21 +166,25 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
 
     rec = torch.empty(n, REC_FLOATS, dtype=torch.float32, device=dev)
     touched = torch.empty(n, dtype=torch.int32, device=dev)
+    dkeys = torch.empty(n, dtype=torch.int32, device=dev)
     call("gs_preprocess_fwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh), n, K,
-         sh_degree, ccam, ptr(rec), ptr(touched), st)
+         sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), st)
     tm.mark("preprocess")
+    order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
-    ws = _u8(_lib.size_call("gs_scan_workspace_size", n), dev)
-    call("gs_scan_u32", ptr(touched), ptr(offsets), n, ptr(ws), ws.numel(), st)
-    tm.mark("scan")
+    ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
+    call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ptr(order), ptr(offsets), ptr(ws), ws.numel(),
+         st)
+    tm.mark("depth_order")
     m = int(offsets[n].item()) if n > 0 else 0  # host readback: instance count
     keys = torch.empty(m if keep_keys else 0, dtype=torch.int64, device=dev)
     point_list = torch.empty(m, dtype=torch.int32, device=dev)
     ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
     bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
     ws = _u8(_lib.size_call("gs_bin_workspace_size", n, m, T), dev)
-    call("gs_bin_fill_3d", ptr(rec), ptr(touched), n, ccam, m, ptr(keys) if keep_keys else None, ptr(point_list),
-         ptr(ranges), ptr(bucket_offsets), ptr(ws), ws.numel(), st)
+    call("gs_bin_fill_3d", ptr(rec), ptr(dkeys), ptr(order), ptr(offsets), n, ccam, m,
+         ptr(keys) if keep_keys else None, ptr(point_list), ptr(ranges), ptr(bucket_offsets), ptr(ws), ws.numel(),
+         st)
     tm.mark("binning")
     nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
     bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
@@ -193,7 +198,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
          ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), st)
     tm.mark("blend_fwd")
-    return ForwardState(cam, n, K, sh_degree, rec, touched, offsets, m, keys, point_list, ranges, bucket_offsets,
+    return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges, bucket_offsets,
                         nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, tuple(bg),
                         {} if isinstance(timing, StageTimer) else tm.result())
 

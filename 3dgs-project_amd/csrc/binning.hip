@@ -41,9 +41,10 @@ __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t* s
   return v + before;
 }
 
-// Exclusive scan of one 2048-value tile. `block_sums` (if not null) receives the tile total;
-// otherwise out[n] receives it.
+// Exclusive scan of one 2048-value tile of in[gather[i]] (in[i] without gather).
+// `block_sums` (if not null) receives the tile total; otherwise out[n] receives it.
 __global__ __launch_bounds__(kScanThreads) void scan_tile_kernel(const uint32_t* __restrict__ in,
+                                                                 const uint32_t* __restrict__ gather,
                                                                  uint32_t* __restrict__ out,
                                                                  int64_t n,
                                                                  uint32_t* __restrict__ block_sums) {
@@ -52,7 +53,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_kernel(const uint32_t*
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
   for (int k = threadIdx.x; k < kScanTile; k += kScanThreads) {
     const int64_t idx = base + k;
-    s_v[k] = idx < n ? in[idx] : 0u;
+    s_v[k] = idx < n ? in[gather ? gather[idx] : idx] : 0u;
   }
   __syncthreads();
   uint32_t local[kScanItems];
@@ -105,17 +106,18 @@ static size_t scan_ws(int64_t n) {
   return align_up(nb * 4) + align_up((nb + 1) * 4) + scan_ws(nb);
 }
 
-static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hipStream_t st) {
+static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hipStream_t st,
+                     const uint32_t* gather = nullptr) {
   const int64_t nb = (n + kScanTile - 1) / kScanTile;
   if (nb <= 1) {
-    hipLaunchKernelGGL(scan_tile_kernel, dim3(1), dim3(kScanThreads), 0, st, in, out, n, nullptr);
+    hipLaunchKernelGGL(scan_tile_kernel, dim3(1), dim3(kScanThreads), 0, st, in, gather, out, n, nullptr);
     return;
   }
   uint32_t* sums = reinterpret_cast<uint32_t*>(ws);
   uint32_t* sums_scan = reinterpret_cast<uint32_t*>(ws + align_up(nb * 4));
   char* next = ws + align_up(nb * 4) + align_up((nb + 1) * 4);
   hipLaunchKernelGGL(scan_tile_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st,
-                     in, out, n, sums);
+                     in, gather, out, n, sums);
   scan_rec(sums, sums_scan, nb, next, st);
   hipLaunchKernelGGL(scan_add_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st,
                      out, n, sums_scan, nb);
@@ -127,6 +129,11 @@ static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hip
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
+}
+
+__global__ void iota_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = static_cast<uint32_t>(i);
 }
 
 __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
@@ -262,7 +269,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const int64_t idx = base + r * kWave + lane;
     const bool valid = idx < m;
     key[r] = valid ? kin[idx] : 0u;
-    val[r] = valid ? vin[idx] : 0u;
+    val[r] = valid ? (vin ? vin[idx] : static_cast<uint32_t>(idx)) : 0u;
   }
 #pragma unroll
   for (int r = 0; r < kRsRounds; ++r) {
@@ -337,13 +344,18 @@ static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint
 }
 
 // Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
+// v = NULL stands for the values 0, 1, ..., m - 1.
 static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, uint32_t* v_out, int64_t m,
                        int bits, char* ws, hipStream_t st) {
   if (m <= 0) return;
   const SortPlan plan = sort_plan(bits);
   if (plan.passes == 0) {
     (void)hipMemcpyAsync(k_out, k, m * 4, hipMemcpyDeviceToDevice, st);
-    (void)hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
+    if (v) {
+      (void)hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
+    } else {
+      hipLaunchKernelGGL(iota_u32_kernel, dim3(static_cast<unsigned>((m + 255) / 256)), dim3(256), 0, st, v_out, m);
+    }
     return;
   }
   const int n_tiles = static_cast<int>((m + kRsTile - 1) / kRsTile);
@@ -385,13 +397,13 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
 // The result equals a stable sort of (tile << 32 | depth key) over instances emitted in
 // Gaussian-index order.
 // ---------------------------------------------------------------------------------------
-// Depth sort keys. 3D: the view depth of the record, culled Gaussians last. 2D: the caller's
-// depth (float32, or float64 split into a high and a low 32-bit key), every Gaussian kept,
-// so the resulting order is the stable argsort of the depths.
+// Depth sort keys. 3D: the view depth of the record, culled Gaussians last (the same keys
+// gs_preprocess_fwd writes). 2D: the caller's depth (float32, or float64 split into a high
+// and a low 32-bit key), every Gaussian kept, so the resulting order is the stable argsort of
+// the depths.
 __global__ void depth_keys_kernel(const SplatRec* __restrict__ rec, const float* __restrict__ depth,
                                   const double* __restrict__ depth64, const uint32_t* __restrict__ counts,
-                                  int64_t n, uint32_t* __restrict__ keys, uint32_t* __restrict__ keys_hi,
-                                  uint32_t* __restrict__ vals) {
+                                  int64_t n, uint32_t* __restrict__ keys, uint32_t* __restrict__ keys_hi) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   uint32_t k = 0u;
@@ -406,19 +418,12 @@ __global__ void depth_keys_kernel(const SplatRec* __restrict__ rec, const float*
     keys_hi[i] = static_cast<uint32_t>(o >> 32);
   }
   keys[i] = k;
-  vals[i] = static_cast<uint32_t>(i);
 }
 
 __global__ void gather_u32_kernel(const uint32_t* __restrict__ src, const uint32_t* __restrict__ idx, int64_t n,
                                   uint32_t* __restrict__ out) {
   const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (j < n) out[j] = src[idx[j]];
-}
-
-__global__ void gather_counts_kernel(const uint32_t* __restrict__ order, const uint32_t* __restrict__ counts,
-                                     int64_t n, uint32_t* __restrict__ out) {
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (j < n) out[j] = counts[order[j]];
 }
 
 // Tile rectangle (tx0, ty0, tx1, ty1), max exclusive, clipped to the tile grid.
@@ -758,77 +763,82 @@ static int bits_for(int64_t n_values) {
   return b;
 }
 
-static size_t bin_ws(int64_t n, int64_t m, int n_tiles) {
-  size_t s = align_up(n * 4) * 6;           // depth keys (in/sorted), identity, order, counts, key copy
-  s += align_up((n + 1) * 4);
-  s += align_up(m * 4) * 2;                 // emitted tile keys and values
-  s += align_up(m * 4);                     // sorted tile keys
-  s += std::max(sort_ws(n), sort_ws(m));    // sort scratch (reused)
-  s += scan_ws(n + 1);
-  s += align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);  // emission windows
-  return s;
+// Workspace of the depth ordering (keys, sorted keys, float64 high keys, temporary values,
+// sort and scan scratch) and of the emission (tile keys and values, sorted tile keys, sort
+// scratch, window starts).
+static size_t prep_ws(int64_t n) { return align_up(n * 4) * 4 + sort_ws(n) + scan_ws(n); }
+
+static size_t emit_ws(int64_t m) {
+  return align_up(m * 4) * 3 + sort_ws(m) + align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);
 }
 
-// Shared driver of the 3D and rectangle binnings.
-static int bin_fill(const SplatRec* rec, const int4* rects, const float* depth, const double* depth64,
-                    const uint32_t* counts, int64_t n, int tiles_x, int n_tiles, int64_t m,
-                    uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
-                    uint32_t* bucket_offsets, uint32_t* order_out, char* ws, hipStream_t st) {
+// Stable order of the Gaussians by depth key (keys_in: precomputed 32-bit keys, else computed
+// from rec / depth / depth64; none of them: index order) and, if offsets is not NULL, the
+// exclusive scan of their instance counts in that order (offsets[n] = m).
+static void bin_prepare(const SplatRec* rec, const float* depth, const double* depth64, const uint32_t* keys_in,
+                        const uint32_t* counts, int64_t n, uint32_t* order, uint32_t* offsets, char* ws,
+                        hipStream_t st) {
   uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
   uint32_t* dsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* iota = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* order = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* scounts = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* dkey_of = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* soffs = reinterpret_cast<uint32_t*>(ws); ws += align_up((n + 1) * 4);
+  uint32_t* khi = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* tmpv = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  char* sort_scratch = ws; ws += sort_ws(n);
+  char* scan_scratch = ws;
+  if (n <= 0) {
+    if (offsets) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, offsets, int64_t(1), 0u);
+    return;
+  }
+  if (keys_in || rec || depth || depth64) {
+    const uint32_t* keys = keys_in;
+    if (!keys) {
+      hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, depth64,
+                         counts, n, dkeys, depth64 ? khi : nullptr);
+      keys = dkeys;
+    }
+    if (depth64) {
+      // low key halves first, then stably by the high halves gathered into that order
+      radix_sort(keys, nullptr, dsorted, tmpv, n, 32, sort_scratch, st);
+      hipLaunchKernelGGL(gather_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, khi, tmpv, n, dkeys);
+      radix_sort(dkeys, tmpv, dsorted, order, n, 32, sort_scratch, st);
+    } else {
+      radix_sort(keys, nullptr, dsorted, order, n, 32, sort_scratch, st);
+    }
+  } else {
+    hipLaunchKernelGGL(iota_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, n);
+  }
+  if (offsets) scan_rec(counts, offsets, n, scan_scratch, st, order);
+}
+
+// Emission of the instances in depth order, stable sort by tile, tile ranges and bucket
+// offsets. dkey_of [n]: the depth key of every Gaussian (only read for sorted_keys).
+static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, const uint32_t* order,
+                     const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles, int64_t m,
+                     uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
+                     uint32_t* bucket_offsets, char* ws, hipStream_t st) {
   uint32_t* tkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
   uint32_t* tvals = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
   uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
-  char* sort_scratch = ws; ws += std::max(sort_ws(n), sort_ws(m));
-  char* scan_scratch = ws; ws += scan_ws(n + 1);
-  uint32_t* wstart = reinterpret_cast<uint32_t*>(ws); ws += align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);
-
-  const bool by_depth = rec != nullptr || depth != nullptr || depth64 != nullptr;
-  if (n > 0 && (m > 0 || order_out)) {
-    // a float64 depth sorts by its low key half first, then stably by the high half (kept in
-    // scounts, gathered into dkey_of in the order of the first sort)
-    uint32_t* khi = dkey_of;
-    hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, depth64,
-                       counts, n, dkeys, depth64 ? scounts : nullptr, by_depth ? iota : order);
-    if (sorted_keys && m > 0 && !depth64) (void)hipMemcpyAsync(dkey_of, dkeys, n * 4, hipMemcpyDeviceToDevice, st);
-    if (depth64) {
-      radix_sort(dkeys, iota, dsorted, soffs, n, 32, sort_scratch, st);
-      hipLaunchKernelGGL(gather_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, scounts, soffs, n, khi);
-      radix_sort(khi, soffs, dsorted, order, n, 32, sort_scratch, st);
-    } else if (by_depth) {
-      radix_sort(dkeys, iota, dsorted, order, n, 32, sort_scratch, st);
-    }
-    if (order_out) (void)hipMemcpyAsync(order_out, order, n * 4, hipMemcpyDeviceToDevice, st);
-  }
+  char* sort_scratch = ws; ws += sort_ws(m);
+  uint32_t* wstart = reinterpret_cast<uint32_t*>(ws);
   if (m > 0) {
-    hipLaunchKernelGGL(gather_counts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, counts, n,
-                       scounts);
-    scan_rec(scounts, soffs, n, scan_scratch, st);
     const int64_t n_windows = (m + kEmitSpan - 1) / kEmitSpan;
-    hipLaunchKernelGGL(emit_windows_kernel, dim3(grid_for(n + 1, 256)), dim3(256), 0, st, soffs, n, n_windows,
+    hipLaunchKernelGGL(emit_windows_kernel, dim3(grid_for(n + 1, 256)), dim3(256), 0, st, offsets, n, n_windows,
                        wstart);
     if (rects) {
       hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
-                         soffs, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
+                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     } else {
       hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
-                         soffs, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
+                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
     }
     radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
                          dkey_of, m, sorted_keys);
-  }
-  if (m > 0)
     hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, n_tiles, ranges);
+  }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
                      tile_offsets);
-  return GS_OK;
 }
 
 }  // namespace gs
@@ -853,15 +863,36 @@ extern "C" int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* w
   return check_launch("scan");
 }
 
-extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles) {
-  if (n < 0 || m < 0 || n_tiles <= 0) return 0;
-  return bin_ws(n, m, n_tiles);
+extern "C" size_t gs_bin_prepare_workspace_size(int64_t n) { return prep_ws(n < 0 ? 0 : n); }
+
+extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched,
+                                 const uint32_t* depth_keys, int64_t n, uint32_t* order, uint32_t* offsets,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0 && n < (int64_t(1) << 32) && offsets, GS_ERR_ARG, "invalid bin_prepare arguments");
+  GS_REQUIRE(n == 0 || (tiles_touched && order && (depth_keys || splat_rec)), GS_ERR_ARG,
+             "null pointer argument");
+  GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
+  const size_t need = prep_ws(n);
+  GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
+             "bin_prepare workspace too small: need %zu bytes", need);
+  bin_prepare(depth_keys ? nullptr : reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, depth_keys,
+              tiles_touched, n, order, offsets, static_cast<char*>(workspace), as_stream(stream));
+  return check_launch("bin_prepare_3d");
 }
 
-extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, int64_t n,
-                              const gs_camera* cam, int64_t m, uint64_t* sorted_keys,
-                              uint32_t* point_list, uint32_t* ranges, uint32_t* bucket_offsets,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles) {
+  (void)n_tiles;
+  n = n < 0 ? 0 : n;
+  m = m < 0 ? 0 : m;
+  // the rectangle binning runs the depth ordering itself: its scratch, order and offsets too
+  return prep_ws(n) + align_up(n * 4) + align_up((n + 1) * 4) + emit_ws(m);
+}
+
+extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
+                              const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
+                              uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
+                              uint32_t* bucket_offsets, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (int e = check_cam(cam)) return e;
   GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32), GS_ERR_ARG, "invalid sizes n=%lld m=%lld",
@@ -870,14 +901,15 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touc
   const CamK k = make_cam(*cam);
   GS_REQUIRE(static_cast<int64_t>(k.tiles_x) * k.tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
   const int n_tiles = k.tiles_x * k.tiles_y;
-  const size_t need = bin_ws(n, m, n_tiles);
+  const size_t need = emit_ws(m);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
-  GS_REQUIRE(m == 0 || (splat_rec && tiles_touched && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(m == 0 || (splat_rec && order && offsets && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(!(sorted_keys && m > 0 && !depth_keys), GS_ERR_ARG, "sorted_keys need depth_keys");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
-  bin_fill(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, nullptr, tiles_touched, n,
-           k.tiles_x, n_tiles, m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, nullptr,
-           static_cast<char*>(workspace), as_stream(stream));
+  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, order, offsets, n, k.tiles_x, n_tiles,
+           m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, static_cast<char*>(workspace),
+           as_stream(stream));
   return check_launch("bin_fill_3d");
 }
 
@@ -905,7 +937,7 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   GS_REQUIRE(depth_dtype == GS_FLOAT32 || depth_dtype == GS_FLOAT64, GS_ERR_ARG, "invalid depth dtype");
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const int n_tiles = tiles_x * tiles_y;
-  const size_t need = bin_ws(n, m, n_tiles);
+  const size_t need = gs_bin_workspace_size(n, m, n_tiles);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
   GS_REQUIRE(m == 0 || (rects && counts && point_list), GS_ERR_ARG, "null pointer argument");
@@ -914,9 +946,19 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   GS_REQUIRE(aligned(rects, 16), GS_ERR_ALIGN, "rects must be 16-byte aligned");
   const float* d32 = depth_dtype == GS_FLOAT32 ? static_cast<const float*>(depth) : nullptr;
   const double* d64 = depth_dtype == GS_FLOAT64 ? static_cast<const double*>(depth) : nullptr;
-  bin_fill(nullptr, reinterpret_cast<const int4*>(rects), d32, d64, counts, n, tiles_x, n_tiles, m,
-           sorted_keys, point_list, ranges, tile_offsets, bucket_offsets, order, static_cast<char*>(workspace),
-           as_stream(stream));
+  hipStream_t st = as_stream(stream);
+  char* ws = static_cast<char*>(workspace);
+  uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws);  // first region of the depth-ordering scratch
+  char* prep = ws; ws += prep_ws(n);
+  uint32_t* ord = order ? order : reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
+  uint32_t* offs = reinterpret_cast<uint32_t*>(ws); ws += align_up((n + 1) * 4);
+  if (n > 0 && (m > 0 || order)) {
+    bin_prepare(nullptr, d32, d64, nullptr, counts, n, ord, m > 0 ? offs : nullptr, prep, st);
+    if (sorted_keys && m > 0 && !d32)  // index order: the depth part of the keys is 0
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
+  }
+  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, ord, offs, n, tiles_x, n_tiles, m, sorted_keys,
+           point_list, ranges, tile_offsets, bucket_offsets, ws, st);
   return check_launch("bin_fill_rect");
 }
 

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
     const float* __restrict__ sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
-    uint32_t* __restrict__ tiles_touched) {
+    uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys) {
   constexpr int R = 3 * K;      // floats per Gaussian row
   constexpr int RP = R | 1;     // padded LDS row
   __shared__ float s_sh[4][64 * RP];
@@ -231,6 +231,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   }
   if (valid) {
     tiles_touched[i] = g.vis ? count : 0u;
+    // depth sort key: the orderable bits of the view depth, culled Gaussians last
+    if (depth_keys) depth_keys[i] = g.vis ? float_order_key(rb.z) : 0xffffffffu;
     if (g.vis) {
       SplatRec r;
       r.a = ra;
@@ -452,10 +454,10 @@ using namespace gs;
 template <int K>
 static void launch_pre_fwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
                            const float* quats, const float* op, const float* sh, int64_t n,
-                           int active, const CamK& cam, float* rec, uint32_t* touched) {
+                           int active, const CamK& cam, float* rec, uint32_t* touched, uint32_t* dkeys) {
   hipLaunchKernelGGL(preprocess_fwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
-                     reinterpret_cast<SplatRec*>(rec), touched);
+                     reinterpret_cast<SplatRec*>(rec), touched, dkeys);
 }
 
 template <int K>
@@ -481,7 +483,8 @@ static int check_sh(int sh_coeffs, int sh_degree) {
 extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, const float* quats,
                                  const float* opacity_logits, const float* sh, int64_t n,
                                  int sh_coeffs, int sh_degree, const gs_camera* cam,
-                                 float* splat_rec, uint32_t* tiles_touched, void* stream) {
+                                 float* splat_rec, uint32_t* tiles_touched, uint32_t* depth_keys,
+                                 void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
   if (int e = check_cam(cam)) return e;
@@ -496,10 +499,10 @@ extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, co
   const int64_t blocks = (n + 255) / 256;
   hipStream_t st = as_stream(stream);
   switch (sh_coeffs) {
-    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
-    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
-    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
-    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched); break;
+    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
   }
   return check_launch("preprocess_fwd");
 }

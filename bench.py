@@ -53,12 +53,15 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs):
     P = fs.cam.width * fs.cam.height
     B = int(fs.bucket_offsets[-1].item())
     return {
-        # params 44 B/Gaussian + tiles_touched 4 B; SH 12 K B and the 64 B record per visible one
-        "preprocess": 44 * n + 4 * n + n_visible * (12 * K + 64),
-        "scan": 8 * n,
-        # depth keys + 4 radix passes over N (read+write key and value), emission (record of the
-        # visible, key+value per instance), 2 radix passes over M, ranges and bucket counts
-        "binning": 8 * n + 4 * 16 * n + 64 * n_visible + 8 * m + 2 * 16 * m + 8 * T,
+        # params 44 B/Gaussian + tiles_touched and depth key 8 B; SH 12 K B and the 64 B record
+        # per visible one
+        "preprocess": 44 * n + 8 * n + n_visible * (12 * K + 64),
+        # 4 radix passes over N (read+write key and value), then the order, the gathered counts
+        # and the offsets of the scan
+        "depth_order": 4 * 16 * n + 12 * n,
+        # emission (record of the visible, order and offsets per Gaussian, key+value per
+        # instance), 2 radix passes over M, tile bounds (one key read per instance)
+        "binning": 64 * n_visible + 8 * n + 8 * m + 2 * 16 * m + 4 * m + 8 * T,
         "buckets": 8 * T + 4 * B,
         # per instance: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4; the
         # checkpoints 4 KiB per bucket; tile max

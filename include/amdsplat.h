@@ -12,7 +12,7 @@
  *
  * The 3D path replaces Faster-GS's _C.forward / _C.backward (called at
  * phase1/tests/test_parity.py:90,97-98 and cluster/patches/fastergs_lean_adam.patch:328-345):
- *   gs_preprocess_fwd -> gs_scan_u32 (tiles touched) -> [host reads M] -> gs_bin_fill_3d
+ *   gs_preprocess_fwd -> gs_bin_prepare_3d -> [host reads M = offsets[n]] -> gs_bin_fill_3d
  *   -> gs_bucket_fill -> gs_blend_fwd_3d;   backward: gs_blend_bwd_3d -> gs_preprocess_bwd.
  * The 2D entry points replace the extension functions of toy2d/csrc/rasterize.cu:366-448
  * and phase0/csrc/macrotile/bindings.cpp:156-239.
@@ -79,33 +79,47 @@ int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
  * bounds, and the number of 16x16 tiles the ellipse reaches (0 = culled).
  *   means, log_scales [n,3]; quats [n,4]; opacity_logits [n]; sh [n, sh_coeffs, 3] with
  *   sh_coeffs in {1,4,9,16} and (sh_degree+1)^2 <= sh_coeffs.
- *   out: splat_rec [n,16] floats (16-byte aligned), tiles_touched [n] uint32.
+ *   out: splat_rec [n,16] floats (16-byte aligned), tiles_touched [n] uint32, and (may be
+ *   NULL) depth_keys [n] uint32: the orderable bits of the view depth of a Gaussian with
+ *   tiles, 0xffffffff for a culled one (the keys gs_bin_prepare_3d sorts by).
  * ------------------------------------------------------------------------------------- */
 int gs_preprocess_fwd(const float* means, const float* log_scales, const float* quats,
                       const float* opacity_logits, const float* sh, int64_t n, int sh_coeffs,
                       int sh_degree, const gs_camera* cam, float* splat_rec,
-                      uint32_t* tiles_touched, void* stream);
+                      uint32_t* tiles_touched, uint32_t* depth_keys, void* stream);
 
 /* ---------------------------------------------------------------------------------------
- * 3D binning (replaces create_instances_cu, the two cub Onesweep sorts,
- * extract_instance_ranges_cu and extract_bucket_counts; the call sequence is visible in
- * results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:10-31).
- * m = sum of tiles_touched (the caller reads it, e.g. from gs_scan_u32's out[n]).
+ * 3D binning (replaces the cub DeviceScan of tiles_touched, create_instances_cu, the two cub
+ * Onesweep sorts, extract_instance_ranges_cu and extract_bucket_counts; the call sequence is
+ * visible in results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:10-31).
  * Produces the stable order of instances by (tile, depth, Gaussian index) -- the order of a
  * stable sort of 64-bit keys (tile << 32 | orderable depth bits) over instances emitted in
- * Gaussian-index order -- with two stable LSD radix sorts: the Gaussians by depth, then the
- * instances (emitted in depth order) by tile. Writes
+ * Gaussian-index order -- in two levels: a stable radix sort of the Gaussians by depth, then a
+ * stable radix sort by tile of the instances emitted in that order.
+ *
+ * gs_bin_prepare_3d: depth ordering.
+ *   depth_keys [n] from gs_preprocess_fwd, or NULL (then computed from splat_rec).
+ *   out: order [n]        Gaussian indices by depth key, stable (culled Gaussians last)
+ *        offsets [n + 1]  exclusive scan of tiles_touched[order[j]]; offsets[n] = m, the
+ *                         number of instances (the caller reads it)
+ *   Workspace from gs_bin_prepare_workspace_size(n).
+ * gs_bin_fill_3d: emission, tile sort, ranges, bucket offsets. Writes
  *   point_list [m]        Gaussian index per instance, tile-major, front to back
- *   sorted_keys [m]       the 64-bit keys in that order (may be NULL: not needed downstream)
+ *   sorted_keys [m]       the 64-bit keys in that order (may be NULL: not needed downstream;
+ *                         needs depth_keys)
  *   ranges [T,2]          [start, end) of each tile in point_list
  *   bucket_offsets [T+1]  exclusive scan of ceil(len/32); bucket_offsets[T] = number of buckets
- * Workspace from gs_bin_workspace_size(n, m, T).
+ *   Workspace from gs_bin_workspace_size(n, m, T).
  * ------------------------------------------------------------------------------------- */
+size_t gs_bin_prepare_workspace_size(int64_t n);
+int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched, const uint32_t* depth_keys,
+                      int64_t n, uint32_t* order, uint32_t* offsets, void* workspace,
+                      size_t workspace_bytes, void* stream);
 size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles);
-int gs_bin_fill_3d(const float* splat_rec, const uint32_t* tiles_touched, int64_t n,
-                   const gs_camera* cam, int64_t m, uint64_t* sorted_keys, uint32_t* point_list,
-                   uint32_t* ranges, uint32_t* bucket_offsets, void* workspace,
-                   size_t workspace_bytes, void* stream);
+int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
+                   const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
+                   uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
+                   uint32_t* bucket_offsets, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Rectangle binning for the 2D operators (replaces toy2d/gs2d/binning.py:34-88, whose
  * per-tile lists are ordered by a stable depth rank, and phase0/splat2d/ops.py:206-255, whose
