@@ -153,14 +153,14 @@ __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
 //            counters in LDS; equal digits inside a 64-key round matched with BITS ballots),
 //            stages the tile in LDS in digit order and writes it out as one contiguous run
 //            per digit (coalesced)
-// Wavefront w of a tile owns the contiguous keys [1024 w, 1024 (w + 1)), read in 16
-// coalesced rounds, so (wavefront, round, lane) is input order: the sort is stable.
+// Wavefront w of a tile owns the contiguous keys [64 ROUNDS w, 64 ROUNDS (w + 1)), read in
+// ROUNDS coalesced rounds, so (wavefront, round, lane) is input order: the sort is stable.
 // ---------------------------------------------------------------------------------------
 constexpr int kRsThreads = 256;
 constexpr int kRsWaves = kRsThreads / kWave;      // 4
-constexpr int kRsRounds = 16;                     // 64-key rounds per wavefront
-constexpr int kRsWaveKeys = kRsRounds * kWave;    // 1024
-constexpr int kRsTile = kRsWaves * kRsWaveKeys;   // 4096 keys per workgroup
+// A workgroup sorts a tile of 4 * 64 * ROUNDS keys; ROUNDS (4, 8 or 16) is chosen so that a
+// sort has about 1000 tiles or more (enough workgroups to fill the chip).
+constexpr int kRsMinTile = kRsWaves * kWave * 4;  // 1024 keys: smallest tile (sizes scratch)
 
 template <int BITS>
 __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
@@ -174,7 +174,7 @@ __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
   return valid ? peers : 0ull;
 }
 
-template <int BITS>
+template <int BITS, int ROUNDS>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* __restrict__ keys, int64_t m,
                                                                 int shift, uint32_t* __restrict__ tile_hist,
                                                                 int n_tiles) {
@@ -184,15 +184,15 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* 
   const int wave = threadIdx.x >> 6;
   for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_h[0][0])[k] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kRsTile + wave * kRsWaveKeys;
-  uint32_t key[kRsRounds];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kRsWaves * kWave * ROUNDS) + wave * (kWave * ROUNDS);
+  uint32_t key[ROUNDS];
 #pragma unroll
-  for (int r = 0; r < kRsRounds; ++r) {  // all loads in flight before the first count
+  for (int r = 0; r < ROUNDS; ++r) {  // all loads in flight before the first count
     const int64_t idx = base + r * kWave + lane;
     key[r] = idx < m ? keys[idx] : 0u;
   }
 #pragma unroll
-  for (int r = 0; r < kRsRounds; ++r) {
+  for (int r = 0; r < ROUNDS; ++r) {
     if (base + r * kWave + lane < m) atomicAdd(&s_h[wave][(key[r] >> shift) & (R - 1)], 1u);
   }
   __syncthreads();
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(kScanThreads) void rs_rowscan_kernel(uint32_t* __re
   if (threadIdx.x == 0) totals[d] = run;
 }
 
-template <int BITS>
+template <int BITS, int ROUNDS>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin, uint32_t* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles,
@@ -244,8 +244,9 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
   __shared__ uint32_t s_cnt[kRsWaves][R];  // per-wavefront digit counts, then wavefront offsets
   __shared__ uint32_t s_excl[R];           // start of each digit inside the staged tile
   __shared__ uint32_t s_goff[R];           // global start of this tile's keys of each digit
-  __shared__ uint32_t s_key[kRsTile];
-  __shared__ uint32_t s_val[kRsTile];
+  constexpr int kTileKeys = kRsWaves * kWave * ROUNDS;
+  __shared__ uint32_t s_key[kTileKeys];
+  __shared__ uint32_t s_val[kTileKeys];
   __shared__ uint32_t s_wave[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -260,19 +261,19 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     if (d < R) s_goff[d] = incl - t + tile_offs[static_cast<int64_t>(d) * n_tiles + blockIdx.x];
   }
   __syncthreads();
-  const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kRsTile;
-  const int64_t base = tile_base + wave * kRsWaveKeys;
+  const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kTileKeys;
+  const int64_t base = tile_base + wave * (kWave * ROUNDS);
   const uint64_t lt = lanemask_lt(lane);
-  uint32_t key[kRsRounds], val[kRsRounds], rank[kRsRounds];
+  uint32_t key[ROUNDS], val[ROUNDS], rank[ROUNDS];
 #pragma unroll
-  for (int r = 0; r < kRsRounds; ++r) {
+  for (int r = 0; r < ROUNDS; ++r) {
     const int64_t idx = base + r * kWave + lane;
     const bool valid = idx < m;
     key[r] = valid ? kin[idx] : 0u;
     val[r] = valid ? (vin ? vin[idx] : static_cast<uint32_t>(idx)) : 0u;
   }
 #pragma unroll
-  for (int r = 0; r < kRsRounds; ++r) {
+  for (int r = 0; r < ROUNDS; ++r) {
     const bool valid = base + r * kWave + lane < m;
     const uint32_t d = (key[r] >> shift) & (R - 1);
     const uint64_t peers = match_bits<BITS>(d, valid);
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
   if (static_cast<int>(threadIdx.x) < R) s_excl[threadIdx.x] = incl - total;
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kRsRounds; ++r) {
+  for (int r = 0; r < ROUNDS; ++r) {
     if (base + r * kWave + lane < m) {
       const uint32_t d = (key[r] >> shift) & (R - 1);
       const uint32_t pos = s_excl[d] + s_cnt[wave][d] + rank[r];
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     }
   }
   __syncthreads();
-  const int count = static_cast<int>(min<int64_t>(kRsTile, m - tile_base));
+  const int count = static_cast<int>(min<int64_t>(kTileKeys, m - tile_base));
   for (int p = threadIdx.x; p < count; p += kRsThreads) {
     const uint32_t k = s_key[p];
     const uint32_t d = (k >> shift) & (R - 1);
@@ -328,19 +329,34 @@ static SortPlan sort_plan(int bits) {
 }
 
 static size_t sort_ws(int64_t m) {
-  const int64_t nt = (m + kRsTile - 1) / kRsTile;
+  const int64_t nt = (m + kRsMinTile - 1) / kRsMinTile;
   const int64_t hist = 256 * (nt > 0 ? nt : 1);
   return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * 256 * 4);
 }
 
-template <int BITS>
-static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
-                      uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st) {
-  hipLaunchKernelGGL(rs_upsweep_kernel<BITS>, dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
+template <int BITS, int ROUNDS>
+static void sort_pass_r(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
+                        uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st) {
+  hipLaunchKernelGGL((rs_upsweep_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
                      n_tiles);
   hipLaunchKernelGGL(rs_rowscan_kernel, dim3(1 << BITS), dim3(kScanThreads), 0, st, tile_hist, n_tiles, totals);
-  hipLaunchKernelGGL(rs_scatter_kernel<BITS>, dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
+  hipLaunchKernelGGL((rs_scatter_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
                      tile_hist, n_tiles, totals);
+}
+
+static int sort_rounds(int64_t m) {
+  if (m >= int64_t(1024) * 4096) return 16;
+  if (m >= int64_t(1024) * 2048) return 8;
+  return 4;
+}
+
+template <int BITS>
+static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
+                      uint32_t* tile_hist, int rounds, uint32_t* totals, hipStream_t st) {
+  const int n_tiles = static_cast<int>((m + kRsWaves * kWave * rounds - 1) / (kRsWaves * kWave * rounds));
+  if (rounds == 16) sort_pass_r<BITS, 16>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st);
+  else if (rounds == 8) sort_pass_r<BITS, 8>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st);
+  else sort_pass_r<BITS, 4>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st);
 }
 
 // Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
@@ -358,7 +374,8 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     }
     return;
   }
-  const int n_tiles = static_cast<int>((m + kRsTile - 1) / kRsTile);
+  const int rounds = sort_rounds(m);
+  const int n_tiles = static_cast<int>((m + kRsMinTile - 1) / kRsMinTile);  // scratch sizing
   uint32_t* k_alt = reinterpret_cast<uint32_t*>(ws);
   ws += align_up(m * 4);
   uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
@@ -377,14 +394,14 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     uint32_t* tot = totals + 256 * p;
     const int shift = plan.bits * p;
     switch (plan.bits) {
-      case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      case 2: sort_pass<2>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      case 3: sort_pass<3>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      case 4: sort_pass<4>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
-      default: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, n_tiles, tot, st); break;
+      case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 2: sort_pass<2>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 3: sort_pass<3>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 4: sort_pass<4>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      default: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
     }
     src_k = dst_k;
     src_v = dst_v;
