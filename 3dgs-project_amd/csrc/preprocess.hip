@@ -2,10 +2,12 @@
 //
 // One thread per Gaussian, 256-thread workgroups. A wavefront's 64 Gaussians own one
 // contiguous block of the [n, K, 3] SH tensor (64 * 3K floats); the wavefront moves that
-// block through LDS with 16-byte loads/stores (rows padded to an odd stride, so a lane's
-// row reads are bank-conflict free), instead of each lane streaming its own 3K floats 12K
-// bytes apart. Same idea as the reference's coalesced SH access
-// (phase2/sh_coalesce.patch:20-170, upstream/upstream_main_kernels.patch:26-76).
+// block through LDS with coalesced loads/stores (rows padded to an odd stride, so a lane's
+// row reads are bank-conflict free), instead of each lane streaming its own 3K floats 3K * 4
+// bytes apart. Degree-3 rows (48 floats) go through in two 24-float column halves, which
+// halves the LDS per wavefront and doubles the wavefronts a CU can hold. Same idea as the
+// reference's coalesced SH access (phase2/sh_coalesce.patch:20-170,
+// upstream/upstream_main_kernels.patch:26-76).
 #include <stdarg.h>
 
 #include "gs_host.h"
@@ -14,6 +16,71 @@
 namespace gs {
 
 constexpr int kWideRows = 4;  // splats spanning more tile rows than this share rows over the wavefront
+
+// Floats of an SH row staged through LDS at a time (degree 3: two halves of 24).
+template <int K>
+struct ShStage {
+  static constexpr int R = 3 * K;                  // floats per Gaussian row
+  static constexpr int CW = K > 9 ? 24 : R;        // staged columns
+  static constexpr int NH = R / CW;                // passes
+  static constexpr int CP = CW + 1;                // padded LDS row (odd: conflict-free)
+};
+
+// Copies columns [c0, c0 + CW) of the wavefront's `rows` SH rows into LDS rows of stride CW + 1.
+template <int K>
+__device__ __forceinline__ void stage_sh(const float* __restrict__ src, int rows, int c0, float* srow, int lane) {
+  using St = ShStage<K>;
+  constexpr int R = St::R, CW = St::CW, CP = St::CP;
+  if constexpr (CW % 4 == 0 && R % 4 == 0) {
+    if (aligned16(src)) {
+      constexpr int Q = CW / 4;
+      if (rows == 64) {
+#pragma unroll
+        for (int it = 0; it < Q; ++it) {  // every load in flight before the first store
+          const int f4 = lane + 64 * it;
+          const int row = f4 / Q, q = f4 - row * Q;
+          const float4 v = *reinterpret_cast<const float4*>(src + row * R + c0 + 4 * q);
+          float* d = srow + row * CP + 4 * q;
+          d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        }
+        return;
+      }
+      for (int f4 = lane; f4 < rows * Q; f4 += 64) {
+        const int row = f4 / Q, q = f4 - row * Q;
+        const float4 v = *reinterpret_cast<const float4*>(src + row * R + c0 + 4 * q);
+        float* d = srow + row * CP + 4 * q;
+        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+      }
+      return;
+    }
+  }
+  for (int f = lane; f < rows * CW; f += 64) {
+    const int row = f / CW, c = f - row * CW;
+    srow[row * CP + c] = src[row * R + c0 + c];
+  }
+}
+
+// Writes LDS columns back to columns [c0, c0 + CW) of the wavefront's rows.
+template <int K>
+__device__ __forceinline__ void unstage_sh(float* __restrict__ dst, int rows, int c0, const float* srow, int lane) {
+  using St = ShStage<K>;
+  constexpr int R = St::R, CW = St::CW, CP = St::CP;
+  if constexpr (CW % 4 == 0 && R % 4 == 0) {
+    if (aligned16(dst)) {
+      constexpr int Q = CW / 4;
+      for (int f4 = lane; f4 < rows * Q; f4 += 64) {
+        const int row = f4 / Q, q = f4 - row * Q;
+        const float* d = srow + row * CP + 4 * q;
+        *reinterpret_cast<float4*>(dst + row * R + c0 + 4 * q) = make_float4(d[0], d[1], d[2], d[3]);
+      }
+      return;
+    }
+  }
+  for (int f = lane; f < rows * CW; f += 64) {
+    const int row = f / CW, c = f - row * CW;
+    dst[row * R + c0 + c] = srow[row * CP + c];
+  }
+}
 
 struct Geom {
   bool vis;
@@ -119,9 +186,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
     const float* __restrict__ sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
     uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys) {
-  constexpr int R = 3 * K;      // floats per Gaussian row
-  constexpr int RP = R | 1;     // padded LDS row
-  __shared__ float s_sh[4][64 * RP];
+  using St = ShStage<K>;
+  __shared__ float s_sh[4][64 * St::CP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -185,47 +251,41 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   if (vmask != 0) {
     float* srow = s_sh[wave];
     const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
-    const int total = rows * R;
-    const float* src = sh + wave_first * R;
-    if (aligned16(src)) {
-      const int n4 = total / 4;
-      for (int f4 = lane; f4 < n4; f4 += 64) {
-        const float4 v = reinterpret_cast<const float4*>(src)[f4];
-        const int f = 4 * f4;
-        const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = (f + e) / R, colm = (f + e) - row * R;
-          srow[row * RP + colm] = vv[e];
-        }
-      }
-      for (int f = 4 * n4 + lane; f < total; f += 64) {
-        const int row = f / R, colm = f - row * R;
-        srow[row * RP + colm] = src[f];
-      }
-    } else {
-      for (int f = lane; f < total; f += 64) {
-        const int row = f / R, colm = f - row * R;
-        srow[row * RP + colm] = src[f];
-      }
-    }
-    wave_sync();
+    const float* src = sh + wave_first * St::R;
+    float basis[16];
+    float acc[3] = {0.0f, 0.0f, 0.0f};
     if (g.vis) {
       const float dx = means[3 * i] - cam.campos[0];
       const float dy = means[3 * i + 1] - cam.campos[1];
       const float dz = means[3 * i + 2] - cam.campos[2];
       const float len = sqrtf(fmaf(dx, dx, fmaf(dy, dy, dz * dz)));
       const float il = 1.0f / len;
-      float basis[16];
       sh_basis(dx * il, dy * il, dz * il, active, basis);
-      const float* row = srow + lane * RP;
+    }
+#pragma unroll
+    for (int h = 0; h < St::NH; ++h) {
+      if (h) wave_sync();  // every lane is done with the previous columns
+      stage_sh<K>(src, rows, h * St::CW, srow, lane);
+      wave_sync();
+      if (g.vis) {
+        const float* row = srow + lane * St::CP;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+#pragma unroll
+          for (int j = 0; j < St::CW / 3; ++j) {
+            const int k = h * (St::CW / 3) + j;
+            if (k == 0) acc[ch] = basis[0] * row[ch];
+            else if (k < active) acc[ch] = fmaf(basis[k], row[3 * j + ch], acc[ch]);
+          }
+        }
+      }
+    }
+    if (g.vis) {
 #pragma unroll
       for (int ch = 0; ch < 3; ++ch) {
-        float acc = basis[0] * row[ch];
-        for (int k = 1; k < active; ++k) acc = fmaf(basis[k], row[3 * k + ch], acc);
-        acc = acc + 0.5f;
-        if (acc < 0.0f) mask |= (1u << ch);
-        col[ch] = fmaxf(acc, 0.0f);
+        const float a = acc[ch] + 0.5f;
+        if (a < 0.0f) mask |= (1u << ch);
+        col[ch] = fmaxf(a, 0.0f);
       }
     }
   }
@@ -256,9 +316,8 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const float* __restrict__ grad2d, float* __restrict__ g_means,
     float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
     float* __restrict__ g_opacity, float* __restrict__ g_sh) {
-  constexpr int R = 3 * K;
-  constexpr int RP = R | 1;
-  __shared__ float s_sh[4][64 * RP];
+  using St = ShStage<K>;
+  __shared__ float s_sh[4][64 * St::CP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -269,7 +328,6 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   const uint64_t vmask = __ballot(vis ? 1 : 0);
   float* srow = s_sh[wave];
   const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
-  const int total = rows * R;
 
   float gm[3] = {0.0f, 0.0f, 0.0f};  // dL/dmean (world)
   float gcol[3] = {0.0f, 0.0f, 0.0f};
@@ -277,40 +335,59 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   float4 gq = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   float gop = 0.0f;
 
-  if (vmask != 0) {
-    // stage SH coefficients (needed for the view-direction gradient)
-    const float* src = sh + wave_first * R;
-    for (int f = lane; f < total; f += 64) {
-      const int row = f / R, colm = f - row * R;
-      srow[row * RP + colm] = src[f];
-    }
-  }
-  wave_sync();
-
+  // ---- SH colour: coefficient gradients (through the LDS rows) and view-direction gradient ----
+  const float* g2 = grad2d + i * kGrad2D;
+  float dx = 0.0f, dy = 0.0f, dz = 0.0f, il = 0.0f;
+  float basis[16], gb[16];
   if (vis) {
-    const float* g2 = grad2d + i * kGrad2D;
-    const SplatRec r = rec[i];
-    const uint32_t mask = __float_as_uint(r.c.w);
+    const uint32_t mask = __float_as_uint(rec[i].c.w);
     for (int ch = 0; ch < 3; ++ch) gcol[ch] = (mask & (1u << ch)) ? 0.0f : g2[6 + ch];
-
-    // ---- SH colour: coefficient gradients (into LDS row) and view-direction gradient ----
     const float dxw = means[3 * i] - cam.campos[0];
     const float dyw = means[3 * i + 1] - cam.campos[1];
     const float dzw = means[3 * i + 2] - cam.campos[2];
     const float len = sqrtf(fmaf(dxw, dxw, fmaf(dyw, dyw, dzw * dzw)));
-    const float il = 1.0f / len;
-    const float dx = dxw * il, dy = dyw * il, dz = dzw * il;
-    float basis[16];
+    il = 1.0f / len;
+    dx = dxw * il;
+    dy = dyw * il;
+    dz = dzw * il;
     sh_basis(dx, dy, dz, active, basis);
-    float* row = srow + lane * RP;
-    float gb[16];
-    for (int k = 0; k < K; ++k) {
-      if (k < active) {
-        gb[k] = row[3 * k] * gcol[0] + row[3 * k + 1] * gcol[1] + row[3 * k + 2] * gcol[2];
-      } else {
-        gb[k] = 0.0f;
+  }
+  const float* src = sh + wave_first * St::R;
+  float* dst = g_sh + wave_first * St::R;
+#pragma unroll
+  for (int h = 0; h < St::NH; ++h) {
+    constexpr int NK = St::CW / 3;  // coefficients per pass
+    if (vmask != 0) {
+      if (h) wave_sync();  // the previous columns are written out
+      stage_sh<K>(src, rows, h * St::CW, srow, lane);
+      wave_sync();
+      float* row = srow + lane * St::CP;
+      if (vis) {
+#pragma unroll
+        for (int j = 0; j < NK; ++j) {
+          const int k = h * NK + j;
+          const bool on = k < active;
+          gb[k] = on ? row[3 * j] * gcol[0] + row[3 * j + 1] * gcol[1] + row[3 * j + 2] * gcol[2] : 0.0f;
+          // overwrite the row with the coefficient gradients (after its values were read)
+          const float bk = on ? basis[k] : 0.0f;
+          row[3 * j] = bk * gcol[0];
+          row[3 * j + 1] = bk * gcol[1];
+          row[3 * j + 2] = bk * gcol[2];
+        }
+      } else if (valid) {
+        for (int c = 0; c < St::CW; ++c) row[c] = 0.0f;
+      }
+      wave_sync();
+      unstage_sh<K>(dst, rows, h * St::CW, srow, lane);
+    } else {
+      for (int f = lane; f < rows * St::CW; f += 64) {
+        const int row = f / St::CW, c = f - row * St::CW;
+        dst[row * St::R + h * St::CW + c] = 0.0f;
       }
     }
+  }
+
+  if (vis) {
     float gdx, gdy, gdz;
     sh_basis_grad(dx, dy, dz, active, gb, gdx, gdy, gdz);
     // d dir / d v = (I - d d^T) / |v|
@@ -318,13 +395,6 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     gm[0] = (gdx - dx * dd) * il;
     gm[1] = (gdy - dy * dd) * il;
     gm[2] = (gdz - dz * dd) * il;
-    // overwrite the row with coefficient gradients (after its values were read above)
-    for (int k = 0; k < K; ++k) {
-      const float bk = k < active ? basis[k] : 0.0f;
-      row[3 * k] = bk * gcol[0];
-      row[3 * k + 1] = bk * gcol[1];
-      row[3 * k + 2] = bk * gcol[2];
-    }
 
     // ---- geometry ----
     Geom g;
@@ -419,21 +489,6 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     const float qd = w * gw + x * gx + y * gy + z * gz;
     gq = make_float4((gw - w * qd) * g.qinv, (gx - x * qd) * g.qinv, (gy - y * qd) * g.qinv,
                      (gz - z * qd) * g.qinv);
-  } else if (valid && vmask != 0) {
-    float* row = srow + lane * RP;
-    for (int k = 0; k < R; ++k) row[k] = 0.0f;
-  }
-  wave_sync();
-
-  // SH gradients: whole wavefront writes its contiguous block
-  float* dst = g_sh + wave_first * R;
-  if (vmask != 0) {
-    for (int f = lane; f < total; f += 64) {
-      const int row = f / R, colm = f - row * R;
-      dst[f] = srow[row * RP + colm];
-    }
-  } else {
-    for (int f = lane; f < total; f += 64) dst[f] = 0.0f;
   }
   if (valid) {
     g_means[3 * i] = gm[0];
