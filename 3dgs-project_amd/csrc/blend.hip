@@ -218,6 +218,12 @@ __device__ __forceinline__ int wave_max(int v) {
   return v;
 }
 
+__device__ __forceinline__ float opaque_zero() {
+  float z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 __device__ __forceinline__ void atomic_add_grad(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAtomicAdd(p, v); }
 
@@ -436,6 +442,62 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
   const int grp = lane >> 3, lo = lane & 7;
   const int kidx = 6 * (grp >> 2) + 3 * ((grp >> 1) & 1) + 2 * (grp & 1) + lo;
   const bool owner = lo < 2 && (2 * (grp & 1) + lo) < 3 && kidx < NV;
+  if constexpr (R == kRules3D) {
+    // The lane's 4 pixels share a column: the column terms of the power and of the mean
+    // gradient are computed once per splat, and per pixel only dy-dependent sums are kept;
+    // the dx factors are applied to the lane's sums before the reduction.
+    for (int j = 0; j < jmax; ++j) {
+      const Staged<S> sp = s_sp[wave][j];
+      const uint32_t m = s_m[wave][j];
+      const typename Ru::Col cl = Ru::col(sp, pxf);
+      const float n0dx = sp.n0 * cl.dx, n1dx = sp.n1 * cl.dx;
+      // zeros the compiler cannot see through: each sum then lives in one register from its
+      // zero to its last update, instead of being re-zeroed on every path that skips a pixel
+      float sh = opaque_zero(), shy = opaque_zero(), shyy = opaque_zero(), sg = opaque_zero();
+      float cr = opaque_zero(), cg = opaque_zero(), cb = opaque_zero();
+      float ab0 = opaque_zero(), ab1 = opaque_zero();
+      bool used = false;
+#pragma unroll
+      for (int r = 0; r < kPixPerLane; ++r) {
+        if (((m >> r) & 1u) == 0u) continue;  // wave-uniform
+        if (j >= lim[r]) continue;
+        if constexpr (kCount) ++evals;
+        const float dy = sp.my - pyf[r];
+        const float G = exp2_in_range(Ru::power(sp, cl, dy));
+        const float alpha = sp.o * G;
+        if (alpha < kAlphaMin) continue;
+        used = true;
+        const float w = T[r] * alpha;
+        const float dot = fmaf(Gb[r], sp.cb, fmaf(Gg[r], sp.cg, Gr[r] * sp.cr));
+        cr = fmaf(w, Gr[r], cr);
+        cg = fmaf(w, Gg[r], cg);
+        cb = fmaf(w, Gb[r], cb);
+        rho[r] = fmaf(-w, dot, rho[r]);
+        const float oma = 1.0f - alpha;
+        const float dLda = fmaf(T[r], dot, -(rho[r] * __builtin_amdgcn_rcpf(fmaxf(oma, kOneMinusAlphaEps))));
+        sg = fmaf(G, dLda, sg);
+        const float h = alpha * dLda;  // dL/dpower
+        const float hy = h * dy;
+        sh += h;
+        shy += hy;
+        shyy = fmaf(hy, dy, shyy);
+        ab0 = fmaf(fabsf(h), fabsf(fmaf(sp.n1, dy, n0dx)), ab0);
+        ab1 = fmaf(fabsf(h), fabsf(fmaf(sp.nat2, dy, n1dx)), ab1);
+        T[r] = T[r] * oma;
+      }
+      if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
+      const float dxsh = cl.dx * sh;
+      S acc[12] = {dxsh, shy, cl.dx * dxsh, cl.dx * shy, shyy, sg, cr, cg, cb, ab0, ab1, 0.0f};
+      S u0, u1;
+      wave_reduce12(acc, u0, u1);
+      if (owner) {
+        const S u = lo == 0 ? u0 : u1;
+        atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + kidx,
+                        finish_grad<R, S>(sp, kidx, u, u0, u1));
+      }
+      if constexpr (kCount) atomics += NV;
+    }
+  } else
   for (int j = 0; j < jmax; ++j) {
     const Staged<S> sp = s_sp[wave][j];
     uint32_t m = 0xfu;

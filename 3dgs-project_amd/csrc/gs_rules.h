@@ -87,15 +87,27 @@ struct Rule<kRules3D, float> {
     return s;
   }
 
+  // power (in log2 units) = s0 dx^2 + s1 dx dy + s2 dy^2, evaluated as
+  // a0 + dy (s2 dy + b1) with the column terms a0 = (s0 dx) dx, b1 = s1 dx, which a lane
+  // owning several pixels of one column computes once per splat; clamped to [-64, 0].
+  struct Col {
+    float dx, a0, b1;
+  };
+  __device__ static Col col(const Staged<S>& s, S px) {
+    Col c;
+    c.dx = s.mx - px;
+    c.a0 = (s.s0 * c.dx) * c.dx;
+    c.b1 = s.s1 * c.dx;
+    return c;
+  }
+  __device__ static float power(const Staged<S>& s, const Col& c, float dy) {
+    return clampf(fmaf(dy, fmaf(s.s2, dy, c.b1), c.a0), -64.0f, 0.0f);
+  }
   __device__ static bool eval(const Staged<S>& s, S px, S py, Eval<S>& e) {
-    e.dx = s.mx - px;
+    const Col c = col(s, px);
+    e.dx = c.dx;
     e.dy = s.my - py;
-    float t = s.s1 * e.dy;
-    t = fmaf(s.s0, e.dx, t);
-    float u = s.s2 * e.dy;
-    u = u * e.dy;
-    const float pw = fminf(fmaf(e.dx, t, u), 0.0f);
-    e.G = exp2_neg(pw);
+    e.G = exp2_in_range(power(s, c, e.dy));
     e.alpha = s.o * e.G;
     e.clamped = false;
     return e.alpha >= kAlphaMin;

@@ -473,12 +473,12 @@ int64_t or_bin(const float* rec, const uint32_t* touched, int64_t n, const or_ca
 }
 
 /* ---- blending ---- */
+/* qa dx^2 + qb dx dy + qc dy^2 as a0 + dy (qc dy + b1), a0 = (qa dx) dx, b1 = qb dx (the
+ * column terms a lane owning several pixels of one column shares), clamped to <= 0. */
 static float power2(float qa, float qb, float qc, float dx, float dy) {
-  float t = qb * dy;
-  t = fmaf(qa, dx, t);
-  float u = qc * dy;
-  u = u * dy;
-  float e = fmaf(dx, t, u);
+  float a0 = (qa * dx) * dx;
+  float b1 = qb * dx;
+  float e = fmaf(dy, fmaf(qc, dy, b1), a0);
   return fminf(e, 0.0f);
 }
 
