@@ -130,26 +130,35 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
       const uint64_t qm = (c0 < 64) ? wm[0] : (c0 < 128) ? wm[1] : (c0 < 192) ? wm[2] : wm[3];
       uint32_t cm = static_cast<uint32_t>(qm >> (c0 & 63));
       if (c1 - c0 < kBucket) cm &= (1u << (c1 - c0)) - 1u;
-      while (cm != 0u) {  // wave-uniform: the splats whose bounds reach this wavefront's rows
+      // wave-uniform loop over the splats whose bounds reach this wavefront's rows; the body
+      // has no lane branches (a lane that has stopped or rejects the splat composites nothing),
+      // so the scalar unit only runs the loop control
+      while (cm != 0u) {
         const int jj = c0 + __builtin_ctz(cm);
         cm &= cm - 1u;
-        if (done) continue;
         const Staged<S> sp = s_sp[jj];
         Eval<S> e;
-        if constexpr (kCount) ++evals;
-        if (!Ru::eval(sp, pxf, pyf, e)) continue;
+        if constexpr (kCount) evals += done ? 0u : 1u;
+        bool take = Ru::eval(sp, pxf, pyf, e) && !done;
         if constexpr (Ru::kStopBefore) {
-          if (T * (S(1) - e.alpha) < Ru::t_stop()) {
-            done = true;
-            continue;
-          }
+          const bool stop = take && T * (S(1) - e.alpha) < Ru::t_stop();
+          done = done || stop;
+          take = take && !stop;
         }
-        composite<R, S>(Cr, Cg, Cb, T, sp, e.alpha);
-        ++count;
-        last = b0 + jj + 1;
-        if constexpr (!Ru::kStopBefore) {
-          if (T < Ru::t_stop()) done = true;
+        if constexpr (R == kRules3D) {
+          // alpha 0 leaves C and T bit-identical (the colours of the records are finite)
+          composite<R, S>(Cr, Cg, Cb, T, sp, take ? e.alpha : S(0));
+        } else {
+          S r = Cr, g = Cg, b = Cb, t = T;
+          composite<R, S>(r, g, b, t, sp, e.alpha);
+          Cr = take ? r : Cr;
+          Cg = take ? g : Cg;
+          Cb = take ? b : Cb;
+          T = take ? t : T;
         }
+        count += take ? 1 : 0;
+        last = take ? b0 + jj + 1 : last;
+        if constexpr (!Ru::kStopBefore) done = done || T < Ru::t_stop();
       }
     }
   }
