@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
         if (j >= lim[r]) continue;
         if constexpr (kCount) ++evals;
         const float dy = sp.my - pyf[r];
-        const float G = exp2_in_range(Ru::power(sp, cl, dy));
+        const float G = Ru::falloff(Ru::power(sp, cl, dy));
         const float alpha = sp.o * G;
         if (alpha < kAlphaMin) continue;
         used = true;

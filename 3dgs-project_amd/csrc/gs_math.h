@@ -51,13 +51,6 @@ __device__ __forceinline__ float exp2_neg(float x) {
   return ldexpf(poly_exp2_frac(f), static_cast<int>(k));
 }
 
-// 2^x for x already in [-64, 0] (the caller clamps, e.g. with one v_med3_f32).
-__device__ __forceinline__ float exp2_in_range(float x) {
-  const float k = rintf(x);
-  const float f = x - k;  // exact: |f| <= 0.5
-  return ldexpf(poly_exp2_frac(f), static_cast<int>(k));
-}
-
 // x clamped to [lo, hi] in one instruction (x is never NaN here).
 __device__ __forceinline__ float clampf(float x, float lo, float hi) { return __builtin_amdgcn_fmed3f(x, lo, hi); }
 

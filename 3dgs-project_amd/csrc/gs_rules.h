@@ -103,11 +103,14 @@ struct Rule<kRules3D, float> {
   __device__ static float power(const Staged<S>& s, const Col& c, float dy) {
     return clampf(fmaf(dy, fmaf(s.s2, dy, c.b1), c.a0), -64.0f, 0.0f);
   }
+  // G = 2^power with the hardware exp2 (v_exp_f32, within 1 ulp): about a third of the
+  // instructions of a polynomial exp2 in the loops that dominate the blend.
+  __device__ static float falloff(float pw) { return __builtin_amdgcn_exp2f(pw); }
   __device__ static bool eval(const Staged<S>& s, S px, S py, Eval<S>& e) {
     const Col c = col(s, px);
     e.dx = c.dx;
     e.dy = s.my - py;
-    e.G = exp2_in_range(power(s, c, e.dy));
+    e.G = falloff(power(s, c, e.dy));
     e.alpha = s.o * e.G;
     e.clamped = false;
     return e.alpha >= kAlphaMin;

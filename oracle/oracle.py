@@ -96,12 +96,13 @@ def blend_fwd(rec, point_list, ranges, boff, width, height, bg=(0.0, 0.0, 0.0), 
     n_contrib = np.zeros((height, width), np.int32)
     tile_max = np.zeros(T, np.uint32)
     ckpt = np.zeros((max(nb, 1), 256, 4), np.float32) if with_ckpt else None
+    amb = np.zeros((height, width), np.uint8)
     bgc = np.asarray(bg, np.float32)
     lib().or_blend_fwd(_p(f32(rec)), _p(np.ascontiguousarray(ranges, np.uint32)),
                        _p(np.ascontiguousarray(point_list, np.uint32)), _p(np.ascontiguousarray(boff, np.uint32)),
                        C.c_int(width), C.c_int(height), _p(bgc), _p(image), _p(final_T), _p(n_contrib),
-                       _p(tile_max), _p(ckpt))
-    return image, final_T, n_contrib, tile_max, ckpt
+                       _p(tile_max), _p(ckpt), _p(amb))
+    return image, final_T, n_contrib, tile_max, ckpt, amb.astype(bool)
 
 
 def blend_bwd(rec, point_list, ranges, boff, width, height, image, grad_image, final_T, n_contrib, tile_max,
@@ -135,9 +136,9 @@ def render(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg=(0.0
     """Full forward. Returns a dict of every intermediate."""
     rec, touched = preprocess_fwd(means, log_scales, quats, opacity_logits, sh, cam, sh_degree)
     keys, pl, ranges, boff = bin_instances(rec, touched, cam)
-    image, final_T, n_contrib, tile_max, ckpt = blend_fwd(rec, pl, ranges, boff, cam.width, cam.height, bg)
+    image, final_T, n_contrib, tile_max, ckpt, amb = blend_fwd(rec, pl, ranges, boff, cam.width, cam.height, bg)
     return dict(rec=rec, touched=touched, keys=keys, point_list=pl, ranges=ranges, bucket_offsets=boff,
-                image=image, final_T=final_T, n_contrib=n_contrib, tile_max=tile_max, ckpt=ckpt)
+                image=image, final_T=final_T, n_contrib=n_contrib, tile_max=tile_max, ckpt=ckpt, amb=amb)
 
 
 def exp2_neg(x: float) -> float:

@@ -14,6 +14,8 @@
  * dependency not present in the reference tree; its rules are taken from the in-tree patches):
  *   - pixel centre (x + 0.5, y + 0.5)                 upstream/upstream_main_kernels.patch:98
  *   - G = exp(min(power, 0)), alpha = o G, no clamp  phase1/fastergs_macro.patch:181-185, PLAN.md:53
+ *     (the kernels take 2^x from the hardware exp2, this restatement from its own polynomial:
+ *     forward decisions within a few ulp of a threshold are reported as ambiguous)
  *   - skip alpha < 1/255; stop after T < 1e-4        phase2/blend_stats.patch:132,246
  *   - (C, T) checkpoint every 32 list entries         phase1/fastergs_macro.patch:131,150-152
  *   - dL/dalpha = T (G.c) - rho_after / max(1-alpha, 1e-6), rho = G.(image - C)
@@ -488,10 +490,21 @@ static int strip_hit(const float* r, int tile_y0, int strip) {
   return d[2] <= r1 && d[3] >= r0;
 }
 
-/* ckpt may be NULL. Checkpoints are written for every bucket the pixel loop reaches. */
+/* A forward decision is ambiguous between this restatement's polynomial exp2 and the
+ * kernels' hardware exp2 (each within about 1 ulp) when it falls inside the error the two can
+ * accumulate: alpha >= 1/255 within AMB_ALPHA (relative; the two alphas are at most ~3 ulp
+ * apart), and T < 1e-4 within a running relative bound on T that every composite grows by
+ * AMB_ALPHA * alpha / (1 - alpha) (the alpha error carried through 1 - alpha) plus one
+ * rounding of the product. */
+#define AMB_ALPHA 4e-7f
+#define AMB_ROUND 1.2e-7f
+
+/* ckpt and amb may be NULL. Checkpoints are written for every bucket the pixel loop reaches.
+ * amb [H, W] = 1 where some decision of the pixel fell within the margins above (its
+ * n_contrib, and the image from that point on, may then legitimately differ). */
 int or_blend_fwd(const float* rec, const uint32_t* ranges, const uint32_t* point_list,
                  const uint32_t* bucket_offsets, int W, int H, const float* bg, float* image,
-                 float* final_T, int32_t* n_contrib, uint32_t* tile_max, float* ckpt) {
+                 float* final_T, int32_t* n_contrib, uint32_t* tile_max, float* ckpt, uint8_t* amb) {
   int tiles_x = (W + TILE - 1) / TILE, tiles_y = (H + TILE - 1) / TILE;
   int64_t HW = (int64_t)W * H;
   float bgc[3] = {bg ? bg[0] : 0.0f, bg ? bg[1] : 0.0f, bg ? bg[2] : 0.0f};
@@ -506,7 +519,8 @@ int or_blend_fwd(const float* rec, const uint32_t* ranges, const uint32_t* point
       float pxf = (float)px + 0.5f, pyf = (float)py + 0.5f;
       int strip = (t >> 4) / STRIP_ROWS;
       float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f};
-      int last = 0, done = !inside;
+      int last = 0, done = !inside, near = 0;
+      float tbound = 0.0f; /* relative error bound of T between the two exp2s */
       for (uint32_t idx = 0; idx < e - s; ++idx) {
         if (done) break; /* later checkpoints of this pixel keep (C, T) */
         if ((idx % BUCKET) == 0 && ckpt) {
@@ -519,13 +533,16 @@ int or_blend_fwd(const float* rec, const uint32_t* ranges, const uint32_t* point
         float dx = r[0] - pxf, dy = r[1] - pyf;
         float G = or_exp2_neg(power2(qa, qb, qc, dx, dy));
         float alpha = r[5] * G;
+        if (fabsf(alpha - ALPHA_MIN) <= AMB_ALPHA * ALPHA_MIN) near = 1;
         if (alpha < ALPHA_MIN) continue;
         float w = alpha * T;
         C[0] = fmaf(r[8], w, C[0]);
         C[1] = fmaf(r[9], w, C[1]);
         C[2] = fmaf(r[10], w, C[2]);
         T = T * (1.0f - alpha);
+        tbound += AMB_ALPHA * alpha / (1.0f - alpha) + AMB_ROUND;
         last = (int)idx + 1;
+        if (fabsf(T - T_STOP) <= tbound * T_STOP) near = 1;
         if (T < T_STOP) done = 1;
       }
       if (ckpt) { /* checkpoints past the termination point keep the final state */
@@ -541,6 +558,7 @@ int or_blend_fwd(const float* rec, const uint32_t* ranges, const uint32_t* point
         image[2 * HW + pix] = fmaf(T, bgc[2], C[2]);
         final_T[pix] = T;
         n_contrib[pix] = last;
+        if (amb) amb[pix] = (uint8_t)near;
         if ((uint32_t)last > tmax) tmax = (uint32_t)last;
       }
     }

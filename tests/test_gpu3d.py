@@ -64,6 +64,23 @@ def read_ckpt_mask(n_contrib, boff, tile_max, W, H):
     return np.array(sel, dtype=np.int64).reshape(-1, 2)
 
 
+def tile_any(mask, cam):
+    """Per tile: any pixel of the [H, W] mask set."""
+    H, W = mask.shape
+    pad = np.zeros((cam.tiles_y * 16, cam.tiles_x * 16), bool)
+    pad[:H, :W] = mask
+    return pad.reshape(cam.tiles_y, 16, cam.tiles_x, 16).any(axis=(1, 3)).reshape(-1)
+
+
+def pixel_of(sel, boff, cam):
+    """Flat pixel index (py * W + px, clipped) of (bucket, tile pixel) pairs."""
+    tile = np.searchsorted(np.asarray(boff, np.int64), sel[:, 0], side="right") - 1
+    tx, ty = tile % cam.tiles_x, tile // cam.tiles_x
+    px = np.minimum(tx * 16 + sel[:, 1] % 16, cam.width - 1)
+    py = np.minimum(ty * 16 + sel[:, 1] // 16, cam.height - 1)
+    return py * cam.width + px
+
+
 @pytest.mark.parametrize("name", list(SCENES))
 def test_forward_matches_oracle(name):
     sc = make(name)
@@ -79,14 +96,21 @@ def test_forward_matches_oracle(name):
     assert np.array_equal(np_(fs.point_list).view(np.uint32), ref["point_list"]), "point list differs"
     assert np.array_equal(np_(fs.ranges).view(np.uint32), ref["ranges"]), "tile ranges differ"
     assert np.array_equal(np_(fs.bucket_offsets).view(np.uint32), ref["bucket_offsets"]), "bucket offsets differ"
-    assert np.array_equal(np_(fs.n_contrib), ref["n_contrib"]), "n_contrib differs"
-    assert np.array_equal(np_(fs.tile_max).view(np.uint32), ref["tile_max"]), "tile max differs"
+    # the blend takes 2^x from the hardware exp2 and the oracle from its own polynomial (both
+    # within about 1 ulp): pixels with a decision within a few ulp of a threshold (the oracle's
+    # amb mask, rare) may take the other branch; every other pixel must agree exactly
+    ok = ~ref["amb"]
+    assert ref["amb"].mean() <= 1e-3, f"{ref['amb'].sum()} ambiguous pixels"
+    assert np.array_equal(np_(fs.n_contrib)[ok], ref["n_contrib"][ok]), "n_contrib differs"
+    tiles_ok = ~tile_any(ref["amb"], cam)
+    assert np.array_equal(np_(fs.tile_max).view(np.uint32)[tiles_ok], ref["tile_max"][tiles_ok]), "tile max differs"
     img, fT = np_(fs.image), np_(fs.final_T)
-    assert np.abs(img - ref["image"]).max() <= FWD_TOL
-    assert np.abs(fT - ref["final_T"]).max() <= FWD_TOL
+    assert np.abs(img - ref["image"])[:, ok].max(initial=0.0) <= FWD_TOL
+    assert np.abs(fT - ref["final_T"])[ok].max(initial=0.0) <= FWD_TOL
     sel = read_ckpt_mask(ref["n_contrib"], ref["bucket_offsets"], ref["tile_max"], cam.width, cam.height)
+    sel = sel[ok.reshape(-1)[pixel_of(sel, ref["bucket_offsets"], cam)]]
     ck = np_(fs.ckpt)
-    assert np.abs(ck[sel[:, 0], sel[:, 1]] - ref["ckpt"][sel[:, 0], sel[:, 1]]).max() <= FWD_TOL
+    assert np.abs(ck[sel[:, 0], sel[:, 1]] - ref["ckpt"][sel[:, 0], sel[:, 1]]).max(initial=0.0) <= FWD_TOL
     b2t = np_(fs.bucket_to_tile).view(np.uint32)[: int(ref["bucket_offsets"][-1])]
     expect = np.repeat(np.arange(len(ref["tile_max"]), dtype=np.uint32), np.diff(ref["bucket_offsets"]))
     assert np.array_equal(b2t, expect)
@@ -109,7 +133,7 @@ def test_gradients_match_float64_autograd(name):
     pre = D.preprocess64(*P, cam, deg)
     img, fT = D.blend64(pre["mean2d"], pre["conic"], pre["opacity"], pre["color"], ref["point_list"],
                         ref["ranges"], mask, cam.width, cam.height, BG)
-    assert np.abs(img.detach().numpy() - np_(fs.image)).max() <= FWD_TOL
+    assert np.abs(img.detach().numpy() - np_(fs.image))[:, ~ref["amb"]].max(initial=0.0) <= FWD_TOL
     ((img * gi).sum() + ((1 - fT) * ga).sum()).backward()
     for gname, a, b in zip(("means", "log_scales", "quats", "opacity_logits", "sh"), grads[:5], P):
         e = D.rel_err(np_(a), b.grad)
@@ -239,13 +263,17 @@ def test_full_size_1m_sampled_tiles():
     ranges[~keep] = 0
     pl = np_(fs.point_list).view(np.uint32)
     boff = np_(fs.bucket_offsets).view(np.uint32)
-    img, fT, nc, tmax, _ = O.blend_fwd(ref_rec, pl, ranges, boff, cam.width, cam.height, with_ckpt=False)
+    img, fT, nc, tmax, _, amb = O.blend_fwd(ref_rec, pl, ranges, boff, cam.width, cam.height, with_ckpt=False)
     tiles_x = cam.tiles_x
+    n_amb = 0
     for t in sample:
         tx, ty = t % tiles_x, t // tiles_x
         ys, xs = slice(ty * 16, min(ty * 16 + 16, cam.height)), slice(tx * 16, min(tx * 16 + 16, cam.width))
-        assert np.abs(np_(fs.image)[:, ys, xs] - img[:, ys, xs]).max() <= FWD_TOL
-        assert np.array_equal(np_(fs.n_contrib)[ys, xs], nc[ys, xs])
+        ok = ~amb[ys, xs]  # near-threshold decisions (hardware vs polynomial exp2) excluded
+        n_amb += int((~ok).sum())
+        assert np.abs(np_(fs.image)[:, ys, xs] - img[:, ys, xs])[:, ok].max(initial=0.0) <= FWD_TOL
+        assert np.array_equal(np_(fs.n_contrib)[ys, xs][ok], nc[ys, xs][ok])
+    assert n_amb <= 64 * 256 // 1000
 
 
 def test_equal_depths_keep_index_order():
