@@ -4,8 +4,9 @@
 // contiguous block of the [n, K, 3] SH tensor (64 * 3K floats); the wavefront moves that
 // block through LDS with coalesced loads/stores (rows padded to an odd stride, so a lane's
 // row reads are bank-conflict free), instead of each lane streaming its own 3K floats 3K * 4
-// bytes apart. Degree-3 rows (48 floats) go through in two 24-float column halves, which
-// halves the LDS per wavefront and doubles the wavefronts a CU can hold. Same idea as the
+// bytes apart. Degree-3 rows (48 floats) go through 32 rows at a time (each pass one
+// contiguous block), which halves the LDS per wavefront and doubles the wavefronts a CU can
+// hold. Same idea as the
 // reference's coalesced SH access (phase2/sh_coalesce.patch:20-170,
 // upstream/upstream_main_kernels.patch:26-76).
 #include <stdarg.h>
@@ -17,68 +18,77 @@ namespace gs {
 
 constexpr int kWideRows = 4;  // splats spanning more tile rows than this share rows over the wavefront
 
-// Floats of an SH row staged through LDS at a time (degree 3: two halves of 24).
+// SH rows staged through LDS at a time: degree 3 in two passes of 32 rows (each pass one
+// contiguous 6 KB block of the tensor), lower degrees in one pass of 64.
 template <int K>
 struct ShStage {
-  static constexpr int R = 3 * K;                  // floats per Gaussian row
-  static constexpr int CW = K > 9 ? 24 : R;        // staged columns
-  static constexpr int NH = R / CW;                // passes
-  static constexpr int CP = CW + 1;                // padded LDS row (odd: conflict-free)
+  static constexpr int R = 3 * K;            // floats per Gaussian row
+  static constexpr int RH = K > 9 ? 32 : 64;  // rows per pass
+  static constexpr int NH = 64 / RH;         // passes
+  static constexpr int CP = R | 1;           // padded LDS row (odd: conflict-free)
 };
 
-// Copies columns [c0, c0 + CW) of the wavefront's `rows` SH rows into LDS rows of stride CW + 1.
+// Copies rows [RH h, RH h + RH) of the wavefront's `rows` SH rows into LDS rows of stride CP.
 template <int K>
-__device__ __forceinline__ void stage_sh(const float* __restrict__ src, int rows, int c0, float* srow, int lane) {
+__device__ __forceinline__ void stage_sh(const float* __restrict__ src, int rows, int h, float* srow, int lane) {
   using St = ShStage<K>;
-  constexpr int R = St::R, CW = St::CW, CP = St::CP;
-  if constexpr (CW % 4 == 0 && R % 4 == 0) {
-    if (aligned16(src)) {
-      constexpr int Q = CW / 4;
-      if (rows == 64) {
+  constexpr int R = St::R, CP = St::CP, RH = St::RH;
+  const int r0 = RH * h;
+  const int nr = min(RH, rows - r0);
+  if (nr <= 0) return;
+  const float* blk = src + static_cast<int64_t>(r0) * R;
+  if constexpr (R % 4 == 0) {
+    if (aligned16(blk)) {
+      constexpr int Q = R / 4;
+      if (nr == RH) {
 #pragma unroll
-        for (int it = 0; it < Q; ++it) {  // every load in flight before the first store
+        for (int it = 0; it < RH * Q / 64; ++it) {  // every load in flight before the first store
           const int f4 = lane + 64 * it;
           const int row = f4 / Q, q = f4 - row * Q;
-          const float4 v = *reinterpret_cast<const float4*>(src + row * R + c0 + 4 * q);
+          const float4 v = reinterpret_cast<const float4*>(blk)[f4];
           float* d = srow + row * CP + 4 * q;
           d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
         }
         return;
       }
-      for (int f4 = lane; f4 < rows * Q; f4 += 64) {
+      for (int f4 = lane; f4 < nr * Q; f4 += 64) {
         const int row = f4 / Q, q = f4 - row * Q;
-        const float4 v = *reinterpret_cast<const float4*>(src + row * R + c0 + 4 * q);
+        const float4 v = reinterpret_cast<const float4*>(blk)[f4];
         float* d = srow + row * CP + 4 * q;
         d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
       }
       return;
     }
   }
-  for (int f = lane; f < rows * CW; f += 64) {
-    const int row = f / CW, c = f - row * CW;
-    srow[row * CP + c] = src[row * R + c0 + c];
+  for (int f = lane; f < nr * R; f += 64) {
+    const int row = f / R, c = f - row * R;
+    srow[row * CP + c] = blk[f];
   }
 }
 
-// Writes LDS columns back to columns [c0, c0 + CW) of the wavefront's rows.
+// Writes the staged rows of pass h back to the wavefront's rows.
 template <int K>
-__device__ __forceinline__ void unstage_sh(float* __restrict__ dst, int rows, int c0, const float* srow, int lane) {
+__device__ __forceinline__ void unstage_sh(float* __restrict__ dst, int rows, int h, const float* srow, int lane) {
   using St = ShStage<K>;
-  constexpr int R = St::R, CW = St::CW, CP = St::CP;
-  if constexpr (CW % 4 == 0 && R % 4 == 0) {
-    if (aligned16(dst)) {
-      constexpr int Q = CW / 4;
-      for (int f4 = lane; f4 < rows * Q; f4 += 64) {
+  constexpr int R = St::R, CP = St::CP, RH = St::RH;
+  const int r0 = RH * h;
+  const int nr = min(RH, rows - r0);
+  if (nr <= 0) return;
+  float* blk = dst + static_cast<int64_t>(r0) * R;
+  if constexpr (R % 4 == 0) {
+    if (aligned16(blk)) {
+      constexpr int Q = R / 4;
+      for (int f4 = lane; f4 < nr * Q; f4 += 64) {
         const int row = f4 / Q, q = f4 - row * Q;
         const float* d = srow + row * CP + 4 * q;
-        *reinterpret_cast<float4*>(dst + row * R + c0 + 4 * q) = make_float4(d[0], d[1], d[2], d[3]);
+        reinterpret_cast<float4*>(blk)[f4] = make_float4(d[0], d[1], d[2], d[3]);
       }
       return;
     }
   }
-  for (int f = lane; f < rows * CW; f += 64) {
-    const int row = f / CW, c = f - row * CW;
-    dst[row * R + c0 + c] = srow[row * CP + c];
+  for (int f = lane; f < nr * R; f += 64) {
+    const int row = f / R, c = f - row * R;
+    blk[f] = srow[row * CP + c];
   }
 }
 
@@ -187,7 +197,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float* __restrict__ sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
     uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys) {
   using St = ShStage<K>;
-  __shared__ float s_sh[4][64 * St::CP];
+  __shared__ float s_sh[4][St::RH * St::CP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -264,19 +274,15 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     }
 #pragma unroll
     for (int h = 0; h < St::NH; ++h) {
-      if (h) wave_sync();  // every lane is done with the previous columns
-      stage_sh<K>(src, rows, h * St::CW, srow, lane);
+      if (h) wave_sync();  // every lane is done with the previous rows
+      stage_sh<K>(src, rows, h, srow, lane);
       wave_sync();
-      if (g.vis) {
-        const float* row = srow + lane * St::CP;
+      if (g.vis && lane / St::RH == h) {
+        const float* row = srow + (lane - St::RH * h) * St::CP;
 #pragma unroll
         for (int ch = 0; ch < 3; ++ch) {
-#pragma unroll
-          for (int j = 0; j < St::CW / 3; ++j) {
-            const int k = h * (St::CW / 3) + j;
-            if (k == 0) acc[ch] = basis[0] * row[ch];
-            else if (k < active) acc[ch] = fmaf(basis[k], row[3 * j + ch], acc[ch]);
-          }
+          acc[ch] = basis[0] * row[ch];
+          for (int k = 1; k < active; ++k) acc[ch] = fmaf(basis[k], row[3 * k + ch], acc[ch]);
         }
       }
     }
@@ -317,7 +323,7 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
     float* __restrict__ g_opacity, float* __restrict__ g_sh) {
   using St = ShStage<K>;
-  __shared__ float s_sh[4][64 * St::CP];
+  __shared__ float s_sh[4][St::RH * St::CP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -356,35 +362,33 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
   float* dst = g_sh + wave_first * St::R;
 #pragma unroll
   for (int h = 0; h < St::NH; ++h) {
-    constexpr int NK = St::CW / 3;  // coefficients per pass
     if (vmask != 0) {
-      if (h) wave_sync();  // the previous columns are written out
-      stage_sh<K>(src, rows, h * St::CW, srow, lane);
+      if (h) wave_sync();  // the previous rows are written out
+      stage_sh<K>(src, rows, h, srow, lane);
       wave_sync();
-      float* row = srow + lane * St::CP;
-      if (vis) {
+      if (lane / St::RH == h) {
+        float* row = srow + (lane - St::RH * h) * St::CP;
+        if (vis) {
 #pragma unroll
-        for (int j = 0; j < NK; ++j) {
-          const int k = h * NK + j;
-          const bool on = k < active;
-          gb[k] = on ? row[3 * j] * gcol[0] + row[3 * j + 1] * gcol[1] + row[3 * j + 2] * gcol[2] : 0.0f;
-          // overwrite the row with the coefficient gradients (after its values were read)
-          const float bk = on ? basis[k] : 0.0f;
-          row[3 * j] = bk * gcol[0];
-          row[3 * j + 1] = bk * gcol[1];
-          row[3 * j + 2] = bk * gcol[2];
+          for (int k = 0; k < K; ++k) {
+            const bool on = k < active;
+            gb[k] = on ? row[3 * k] * gcol[0] + row[3 * k + 1] * gcol[1] + row[3 * k + 2] * gcol[2] : 0.0f;
+            // overwrite the row with the coefficient gradients (after its values were read)
+            const float bk = on ? basis[k] : 0.0f;
+            row[3 * k] = bk * gcol[0];
+            row[3 * k + 1] = bk * gcol[1];
+            row[3 * k + 2] = bk * gcol[2];
+          }
+        } else if (valid) {
+          for (int c = 0; c < St::R; ++c) row[c] = 0.0f;
         }
-      } else if (valid) {
-        for (int c = 0; c < St::CW; ++c) row[c] = 0.0f;
       }
       wave_sync();
-      unstage_sh<K>(dst, rows, h * St::CW, srow, lane);
-    } else {
-      for (int f = lane; f < rows * St::CW; f += 64) {
-        const int row = f / St::CW, c = f - row * St::CW;
-        dst[row * St::R + h * St::CW + c] = 0.0f;
-      }
+      unstage_sh<K>(dst, rows, h, srow, lane);
     }
+  }
+  if (vmask == 0) {
+    for (int f = lane; f < rows * St::R; f += 64) dst[f] = 0.0f;
   }
 
   if (vis) {

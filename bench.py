@@ -26,6 +26,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "3dgs-project_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# wave64 FP32 VALU instructions per second: the published 157.3 TFLOP/s FP32 vector peak, an FMA
+# counting 2 FLOP on each of 64 lanes
+VALU_PEAK_INSTR = 157.3e12 / 2 / 64
 METRIC = "fwd+bwd ms/iter @1M Gaussians SH3 1297x840; per-stage HBM GB/s vs roofline"
 # stages that are one kernel each (the others group several kernels)
 SINGLE_KERNEL = {"preprocess": "preprocess_fwd_kernel", "blend_fwd": "blend_fwd_kernel",
@@ -95,6 +98,25 @@ def measured_traffic(kernel: str):
     return float(m.group(1)) if m else None
 
 
+def measured_valu_instr(kernel: str):
+    """VALU instructions per launch of `kernel` from the committed rocprofv3 SQ summary, or None."""
+    f = ROOT / "profiles" / f"{kernel}_sq.md"
+    if not f.exists():
+        return None
+    m = re.search(r"valu_instr_per_launch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(scene, pose, threads):
     """The C oracle (the CPU restatement of the same rules, OpenMP where the loops allow) timed
     on the host: one full fwd+bwd of one view of the workload (~10 s)."""
@@ -116,6 +138,7 @@ def cpu_baseline(scene, pose, threads):
     dt = time.perf_counter() - t0
     cores = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     return {"value": round(dt * 1000.0, 1), "unit": "ms/iter", "cores": cores, "kind": "port",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
             "sample": f"C oracle fwd+bwd of pose {pose}, all {scene.n} Gaussians ({dt:.1f} s; preprocess and "
                       f"forward blend on {cores} OpenMP threads, sort and backward blend single-threaded)"}
 
@@ -203,6 +226,12 @@ def main():
     dominant = max((k2 for k2 in stage_ms if k2 in SINGLE_KERNEL), key=lambda k2: stage_ms[k2])
     achieved = stage_gbs[dominant]
     traffic = measured_traffic(SINGLE_KERNEL[dominant])
+    valu_instr = measured_valu_instr(SINGLE_KERNEL[dominant])
+    valu = None
+    if valu_instr:
+        rate = valu_instr / (stage_ms[dominant] * 1e-3)
+        valu = {"achieved": round(rate / 1e12, 4), "peak": round(VALU_PEAK_INSTR / 1e12, 4),
+                "unit": "T wave64 instr/s", "frac": round(rate / VALU_PEAK_INSTR, 4), "instr_per_launch": valu_instr}
 
     out = {
         "metric": METRIC,
@@ -231,7 +260,7 @@ def main():
         "roofline": {"kernel": SINGLE_KERNEL[dominant], "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes": sb[dominant],
-                     "avg_launch_ms": round(stage_ms[dominant], 4)},
+                     "avg_launch_ms": round(stage_ms[dominant], 4), "valu": valu},
     }
     if not args.no_cpu_baseline:
         try:
