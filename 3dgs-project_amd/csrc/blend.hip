@@ -87,13 +87,16 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
   S* ck = a.ckpt ? a.ckpt + (static_cast<int64_t>(a.bucket_offsets[tile]) * kTilePixels + t) * 4 : nullptr;
   if (t == 0) s_max = 0;
 
-  S T = S(1), Cr = S(0), Cg = S(0), Cb = S(0);
+  // 3D: a pixel has stopped exactly when T < 1e-4 (T only decreases; pixels outside the
+  // image start at T = 0), so no separate per-lane flag is kept
+  constexpr bool kStopByT = R == kRules3D;
+  S T = (kStopByT && !inside) ? S(0) : S(1), Cr = S(0), Cg = S(0), Cb = S(0);
   int last = 0, count = 0;
   uint32_t evals = 0;
   bool done = !inside;
   int covered = len;  // list positions whose bucket checkpoints the loop wrote
   for (int b0 = 0; b0 < len; b0 += kTilePixels) {
-    if (__syncthreads_count(done ? 1 : 0) == kTilePixels) {
+    if (__syncthreads_count((kStopByT ? T < Ru::t_stop() : done) ? 1 : 0) == kTilePixels) {
       covered = b0;
       break;
     }
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
           c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
         }
       }
-      if (__ballot(done ? 0 : 1) == 0ull) continue;  // the whole wavefront has terminated
+      if (__ballot((kStopByT ? T < Ru::t_stop() : done) ? 0 : 1) == 0ull) continue;  // all lanes stopped
       const int c1 = min(c0 + kBucket, nb);
       const uint64_t qm = (c0 < 64) ? wm[0] : (c0 < 128) ? wm[1] : (c0 < 192) ? wm[2] : wm[3];
       uint32_t cm = static_cast<uint32_t>(qm >> (c0 & 63));
@@ -138,8 +141,9 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
         cm &= cm - 1u;
         const Staged<S> sp = s_sp[jj];
         Eval<S> e;
-        if constexpr (kCount) evals += done ? 0u : 1u;
-        bool take = Ru::eval(sp, pxf, pyf, e) && !done;
+        const bool live = kStopByT ? T >= Ru::t_stop() : !done;
+        if constexpr (kCount) evals += live ? 1u : 0u;
+        bool take = Ru::eval(sp, pxf, pyf, e) && live;
         if constexpr (Ru::kStopBefore) {
           const bool stop = take && T * (S(1) - e.alpha) < Ru::t_stop();
           done = done || stop;
@@ -158,7 +162,7 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
         }
         count += take ? 1 : 0;
         last = take ? b0 + jj + 1 : last;
-        if constexpr (!Ru::kStopBefore) done = done || T < Ru::t_stop();
+        if constexpr (!Ru::kStopBefore && !kStopByT) done = done || T < Ru::t_stop();
       }
     }
   }
