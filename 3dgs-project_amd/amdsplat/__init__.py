@@ -4,6 +4,7 @@
 the 3D path through hand-written HIP kernels behind a C ABI (include/amdsplat.h). The 2D
 drop-in surfaces live in the sibling packages `gs2d` and `splat2d`.
 """
+from .adam import FusedAdam, adam_step, adam_step_sparse
 from .raster3d import Camera, backward_pass, forward_pass, rasterize
 
-__all__ = ["Camera", "rasterize", "forward_pass", "backward_pass"]
+__all__ = ["Camera", "rasterize", "forward_pass", "backward_pass", "FusedAdam", "adam_step", "adam_step_sparse"]

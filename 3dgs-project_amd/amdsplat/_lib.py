@@ -33,6 +33,24 @@ class GsCamera(C.Structure):
 
 
 GS_ACCUMULATE = 1  # gs_blend_bwd_3d flag: add to grad2d instead of zeroing it first
+GS_FLOAT32, GS_FLOAT64, GS_BFLOAT16 = 0, 1, 2
+GS_ADAM_MAX_GROUPS = 8
+
+
+class GsAdamGroup(C.Structure):
+    _fields_ = [
+        ("grad", C.c_void_p),
+        ("param", C.c_void_p),
+        ("exp_avg", C.c_void_p),
+        ("exp_avg_sq", C.c_void_p),
+        ("n_elements", C.c_int64),
+        ("moment_dtype", C.c_int32),
+        ("step", C.c_int32),
+        ("lr", C.c_double),
+        ("beta1", C.c_double),
+        ("beta2", C.c_double),
+        ("eps", C.c_double),
+    ]
 
 
 class AmdSplatError(RuntimeError):
@@ -62,6 +80,7 @@ _SIGS = {
                                _vp, _i32, _vp, _vp]),
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs_adam_step": (_i32, [C.POINTER(GsAdamGroup), _i32, _i64, _vp, _vp]),
     # 2D rule sets
     "gs2d_rects_toy": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "gs2d_rects_phase0": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),

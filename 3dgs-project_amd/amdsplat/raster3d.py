@@ -237,9 +237,17 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
 
 
 class _Rasterize3D(torch.autograd.Function):
+    # visibility hand-off for the sparse optimizer (cluster/patches/fastergs_lean_adam.patch:333-343):
+    # with track_visibility set, each differentiable forward keeps its tiles_touched (int32 [n],
+    # > 0 = visible in that view) in last_visibility
+    track_visibility: bool = False
+    last_visibility: "torch.Tensor | None" = None
+
     @staticmethod
     def forward(ctx, means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg):
         fs = forward_pass(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg)
+        if _Rasterize3D.track_visibility:
+            _Rasterize3D.last_visibility = fs.touched
         ctx.fs = fs
         ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh)
         alpha = 1.0 - fs.final_T

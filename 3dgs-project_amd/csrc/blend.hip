@@ -461,7 +461,7 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
     // the dx factors are applied to the lane's sums before the reduction.
     for (int j = 0; j < jmax; ++j) {
       const Staged<S> sp = s_sp[wave][j];
-      const uint32_t m = s_m[wave][j];
+      const uint32_t m = __builtin_amdgcn_readfirstlane(s_m[wave][j]);  // wave-uniform: scalar tests
       const typename Ru::Col cl = Ru::col(sp, pxf);
       const float n0dx = sp.n0 * cl.dx, n1dx = sp.n1 * cl.dx;
       // zeros the compiler cannot see through: each sum then lives in one register from its

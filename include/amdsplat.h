@@ -41,7 +41,7 @@ enum {
   GS_RULES_TOY2D = 1,   /* gs2d.rasterize: toy2d/csrc/rasterize.cu:37-101, toy2d/gs2d/reference.py:3-8 */
   GS_RULES_PHASE0 = 2   /* splat2d.render: phase0/csrc/macrotile/splat2d_common.h:7-11 */
 };
-enum { GS_FLOAT32 = 0, GS_FLOAT64 = 1 };
+enum { GS_FLOAT32 = 0, GS_FLOAT64 = 1, GS_BFLOAT16 = 2 };
 
 /* Pinhole camera. viewmat is the row-major 4x4 world-to-camera matrix with OpenCV axes
  * (x right, y down, z forward); pixel (i, j) covers [i, i+1) x [j, j+1), so its centre is
@@ -247,6 +247,33 @@ int gs2d_blend_bwd_pixel(int rules, int dtype, const void* rec, const uint32_t* 
                          int height, const double* bg, const void* final_T, const int32_t* limit,
                          const void* grad_image, void* grad_rec, unsigned long long* counters,
                          void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Fused Adam over several parameter groups in one launch (replaces Faster-GS adam_step and
+ * adam_step_sparse, cluster/patches/fastergs_lean_adam.patch:80-186, called per group by
+ * FusedAdam.step, :65-81). Per element, with g the gradient and m, v the moments:
+ *   m' = fma(beta1, m - g, g);  v' = fma(beta2, v - g*g, g*g)
+ *   p' = p - (step_size * m') / (sqrt(v') * bc2 + eps)
+ * with step_size = lr / (1 - beta1^step) and bc2 = 1 / sqrt(1 - beta2^step), both computed in
+ * double and rounded to float. visibility [n_primitives] int32 (may be NULL = dense): rows of a
+ * primitive with visibility 0 are not touched (parameters and moments). Moments are float32, or
+ * bfloat16 (moment_dtype GS_BFLOAT16) written with stochastic rounding: the 16 dropped bits get
+ * uniform noise from an integer hash of (element index ^ seed), seed = 0x9E3779B9 * step +
+ * 0x85EBCA6B (uint32). Each group is [n_primitives, ...] contiguous; at most GS_ADAM_MAX_GROUPS.
+ * ------------------------------------------------------------------------------------- */
+#define GS_ADAM_MAX_GROUPS 8
+typedef struct gs_adam_group {
+  const float* grad;
+  float* param;
+  void* exp_avg;      /* float32 or bfloat16 (uint16 bits), n_elements each */
+  void* exp_avg_sq;
+  int64_t n_elements; /* n_primitives * features per primitive */
+  int32_t moment_dtype; /* GS_FLOAT32 or GS_BFLOAT16 */
+  int32_t step;       /* the group's step count after this update (>= 1) */
+  double lr, beta1, beta2, eps;
+} gs_adam_group;
+int gs_adam_step(const gs_adam_group* groups, int n_groups, int64_t n_primitives,
+                 const int32_t* visibility, void* stream);
 
 #ifdef __cplusplus
 }

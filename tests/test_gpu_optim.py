@@ -1,0 +1,147 @@
+"""GPU parity of the fused Adam (gs_adam_step) against the C restatement (bit-exact), and the
+checks of cluster/tests/test_lean_adam.py:37-134: dense, masked rows, bfloat16 moments with
+stochastic rounding, and the visibility hand-off from a real forward pass."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import optim as P
+from amdsplat import FusedAdam, adam_step, adam_step_sparse
+from amdsplat import raster3d as R
+from amdsplat import scenes
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("shape", [(10_003, 3), (10_003, 1), (10_003, 4), (10_003, 15, 3), (5, 2)])
+def test_dense_bit_exact_vs_oracle(shape):
+    g = torch.Generator().manual_seed(0)
+    p0 = torch.randn(*shape, generator=g)
+    p, m, v = p0.clone().to(dev), torch.zeros(shape, device=dev), torch.zeros(shape, device=dev)
+    pn, mn, vn = p0.numpy().copy(), np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+    for step in range(1, 6):
+        gr = torch.randn(*shape, generator=g) * 1e-3
+        adam_step(gr.to(dev), p, m, v, step, 1e-3, 0.9, 0.999, 1e-15)
+        P.adam_step(gr.numpy(), pn, mn, vn, step, 1e-3, 0.9, 0.999, 1e-15)
+    assert np.array_equal(np_(p).view(np.uint32), pn.view(np.uint32))
+    assert np.array_equal(np_(m).view(np.uint32), mn.view(np.uint32))
+    assert np.array_equal(np_(v).view(np.uint32), vn.view(np.uint32))
+
+
+def test_masked_rows():
+    N = 20_011
+    g = torch.Generator().manual_seed(1)
+    vis = ((torch.rand(N, generator=g) < 0.4).int() * torch.randint(1, 50, (N,), generator=g, dtype=torch.int32))
+    sel = vis > 0
+    for shape in [(N, 15, 3), (N, 3), (N, 1), (N, 4), (N, 1, 3)]:
+        p0 = torch.randn(*shape, generator=g)
+        m0, v0 = torch.randn(*shape, generator=g).abs(), torch.rand(*shape, generator=g)
+        gr = torch.randn(*shape, generator=g) * 1e-3
+        pa, ma, va = p0.to(dev), m0.to(dev), v0.to(dev)
+        pb, mb, vb = p0.to(dev), m0.to(dev), v0.to(dev)
+        adam_step(gr.to(dev), pa, ma, va, 7, 1e-3, 0.9, 0.999, 1e-15)
+        adam_step_sparse(gr.to(dev), pb, mb, vb, vis.to(dev), 7, 1e-3, 0.9, 0.999, 1e-15)
+        pa, ma, va, pb, mb, vb = map(lambda t: t.cpu(), (pa, ma, va, pb, mb, vb))
+        assert torch.equal(pa[sel], pb[sel]) and torch.equal(ma[sel], mb[sel]) and torch.equal(va[sel], vb[sel])
+        assert torch.equal(pb[~sel], p0[~sel]) and torch.equal(mb[~sel], m0[~sel]) and torch.equal(vb[~sel], v0[~sel])
+        # (a visible update can be below half an ulp of its parameter: most, not all, change)
+        assert float((pb[sel] != p0[sel]).float().mean()) > 0.9
+
+
+def test_one_launch_for_all_groups_equals_per_group():
+    N = 3001
+    shapes = [(N, 3), (N, 3), (N, 4), (N, 1), (N, 1, 3), (N, 15, 3)]
+    g = torch.Generator().manual_seed(2)
+    params = [torch.randn(*s, generator=g).to(dev) for s in shapes]
+    grads = [torch.randn(*s, generator=g).to(dev) * 1e-3 for s in shapes]
+    lrs = [1.6e-4, 5e-3, 1e-3, 5e-2, 2.5e-3, 1.25e-4]
+    ref = [p.clone() for p in params]
+    ref_m = [torch.zeros_like(p) for p in params]
+    ref_v = [torch.zeros_like(p) for p in params]
+    groups = [{"params": [torch.nn.Parameter(p)], "lr": lr, "name": f"g{i}"} for i, (p, lr) in enumerate(zip(params, lrs))]
+    opt = FusedAdam(groups, lr=0.0, eps=1e-15)
+    for step in range(1, 4):
+        for grp, gr in zip(opt.param_groups, grads):
+            grp["params"][0].grad = gr * step
+        opt.step()
+        for i in range(len(shapes)):
+            adam_step(grads[i] * step, ref[i], ref_m[i], ref_v[i], step, lrs[i], 0.9, 0.999, 1e-15)
+    for grp, r in zip(opt.param_groups, ref):
+        assert torch.equal(grp["params"][0].detach(), r)
+
+
+def test_bf16_moments_bit_exact_vs_oracle():
+    shape = (4099, 15, 3)
+    g = torch.Generator().manual_seed(3)
+    p0 = torch.randn(*shape, generator=g)
+    p = p0.to(dev)
+    m = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+    v = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+    pn, mn, vn = p0.numpy().copy(), np.zeros(shape, np.uint16), np.zeros(shape, np.uint16)
+    for step in range(1, 6):
+        gr = torch.randn(*shape, generator=g) * 1e-3
+        adam_step_sparse(gr.to(dev), p, m, v, None, step, 1.25e-4, 0.9, 0.999, 1e-15)
+        P.adam_step(gr.numpy(), pn, mn, vn, step, 1.25e-4, 0.9, 0.999, 1e-15)
+    assert np.array_equal(np_(p).view(np.uint32), pn.view(np.uint32))
+    assert np.array_equal(np_(m.view(torch.int16)).view(np.uint16), mn)
+    assert np.array_equal(np_(v.view(torch.int16)).view(np.uint16), vn)
+
+
+def test_bf16_moments_track_float32_and_do_not_stall():
+    N = 20_000
+    g = torch.Generator(device="cpu").manual_seed(4)
+    pr = torch.randn(N, 15, 3, generator=g).to(dev)
+    pinit, pl = pr.clone(), pr.clone()
+    mr, vr = torch.zeros_like(pr), torch.zeros_like(pr)
+    ml, vl = torch.zeros_like(pr, dtype=torch.bfloat16), torch.zeros_like(pr, dtype=torch.bfloat16)
+    scale = (torch.rand(N, 1, 1, generator=g) * 1e-3 + 1e-6).to(dev)
+    bias = torch.randn(N, 15, 3, generator=g).to(dev) * scale
+    gd = torch.Generator(device=dev).manual_seed(5)
+    for step in range(1, 1001):
+        gr = bias + torch.randn(pr.shape, generator=gd, device=dev) * scale
+        adam_step(gr, pr, mr, vr, step, 1.25e-4, 0.9, 0.999, 1e-15)
+        adam_step_sparse(gr, pl, ml, vl, None, step, 1.25e-4, 0.9, 0.999, 1e-15)
+    rel_v = ((vl.float() - vr).abs() / (vr.abs() + 1e-30)).median()
+    rel_m = (ml.float() - mr).norm() / mr.norm()
+    rel_upd = ((pr - pinit) - (pl - pinit)).norm() / (pr - pinit).norm()
+    assert float(rel_v) < 0.05 and float(rel_m) < 0.05 and float(rel_upd) < 0.02
+    # constant gradient from v = 0.5: the beta2 = 0.999 average must keep moving toward g^2
+    gc = torch.ones(1 << 18, device=dev)
+    v_sr = torch.full_like(gc, 0.5).to(torch.bfloat16)
+    m_sr = torch.zeros_like(v_sr)
+    q = torch.zeros_like(gc)
+    for step in range(1, 3001):
+        adam_step_sparse(gc, q, m_sr, v_sr, None, 10_000 + step, 0.0, 0.9, 0.999, 1e-15)
+    expected = 1.0 - 0.5 * 0.999 ** 3000
+    assert abs(float(v_sr.float().mean()) - expected) < 0.005
+
+
+def test_visibility_from_forward_and_sparse_step():
+    sc = scenes.small_scene(4000, 160, 120, seed=3)
+    cam = sc.cameras[0]
+    params = [torch.nn.Parameter(t.to(dev).contiguous()) for t in sc.params()]
+    names = ["means", "scales", "quats", "opacities", "sh"]
+    groups = [{"params": [p], "lr": lr, "name": nm} for p, lr, nm in
+              zip(params, [1.6e-4, 5e-3, 1e-3, 5e-2, 2.5e-3], names)]
+    opt = FusedAdam(groups, lr=0.0, eps=1e-15, sparse=True, lowp_moment_groups=("sh",))
+    K = torch.tensor([[cam.fx, 0.0, cam.cx], [0.0, cam.fy, cam.cy], [0.0, 0.0, 1.0]])
+    img, alpha, aux = R.rasterize(*params, cam.viewmat, K, cam.width, cam.height, near=cam.near, far=cam.far)
+    img.sum().backward()
+    vis = R._Rasterize3D.last_visibility
+    assert vis is not None and vis.dtype == torch.int32 and vis.shape == (sc.n,)
+    gnz = params[0].grad.abs().sum(1) > 0
+    assert bool((vis[gnz] > 0).all()) and int((vis > 0).sum()) > 0 and int((vis == 0).sum()) > 0
+    before = [p.detach().clone() for p in params]
+    opt.step()
+    hid = vis == 0
+    for p, b in zip(params, before):
+        assert torch.equal(p.detach()[hid], b[hid])
+    assert opt.state[params[4]]["exp_avg"].dtype == torch.bfloat16
+    R._Rasterize3D.track_visibility = False
