@@ -5,6 +5,8 @@ the 3D path through hand-written HIP kernels behind a C ABI (include/amdsplat.h)
 drop-in surfaces live in the sibling packages `gs2d` and `splat2d`.
 """
 from .adam import FusedAdam, adam_step, adam_step_sparse
+from .loss import fused_ssim, l1_ssim_loss
 from .raster3d import Camera, backward_pass, forward_pass, rasterize
 
-__all__ = ["Camera", "rasterize", "forward_pass", "backward_pass", "FusedAdam", "adam_step", "adam_step_sparse"]
+__all__ = ["Camera", "rasterize", "forward_pass", "backward_pass", "FusedAdam", "adam_step", "adam_step_sparse",
+           "l1_ssim_loss", "fused_ssim"]

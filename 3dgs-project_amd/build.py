@@ -19,7 +19,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 OUT = HERE / "amdsplat" / "libamdsplat.so"
-SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "blend.hip", "raster2d.hip", "adam.hip"]
+SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "blend.hip", "raster2d.hip", "adam.hip", "loss.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

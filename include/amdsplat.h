@@ -275,6 +275,24 @@ typedef struct gs_adam_group {
 int gs_adam_step(const gs_adam_group* groups, int n_groups, int64_t n_primitives,
                  const int32_t* visibility, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Fused L1 + D-SSIM loss on [C, H, W] float32 images (replaces the fused-ssim extension's
+ * fusedssimCUDA / fusedssim_backwardCUDA, results/phase1/README.md:46-47, with the trainers'
+ * L1 term; LAMBDA_DSSIM of phase2/logs/run_4559238/runs/b_room_up_s10/training_config.yaml:100):
+ *   L = (1 - lambda) mean|x - y| + lambda (1 - mean SSIM(x, y)),
+ * SSIM with an 11x11 Gaussian window (sigma 1.5), C1 = 0.01^2, C2 = 0.03^2, zero padding.
+ * gs_l1_ssim_fwd writes loss[3] = (L, mean|x - y|, mean SSIM) on the device and, if dmap is not
+ * NULL, dmap [C, 3, H, W] = (dS/dmu_x, dS/dE[x^2], dS/dE[xy]) per pixel for the backward.
+ * Workspace from gs_l1_ssim_workspace_size. gs_l1_ssim_bwd writes grad_image [C, H, W] =
+ * dL/dx, scaled by grad_loss[0] (a device float; NULL = 1).
+ * ------------------------------------------------------------------------------------- */
+size_t gs_l1_ssim_workspace_size(int channels, int height, int width);
+int gs_l1_ssim_fwd(const float* image, const float* target, int channels, int height, int width,
+                   float lambda_dssim, float* dmap, float* loss, void* workspace, size_t workspace_bytes,
+                   void* stream);
+int gs_l1_ssim_bwd(const float* image, const float* target, const float* dmap, int channels, int height,
+                   int width, float lambda_dssim, const float* grad_loss, float* grad_image, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
