@@ -64,8 +64,8 @@ _SIGS = {
     "gs_grad2d_floats": (_i32, []),
     "gs_scan_workspace_size": (_sz, [_i64]),
     "gs_scan_u32": (_i32, [_vp, _vp, _i64, _vp, _sz, _vp]),
-    "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp,
-                                 _vp]),
+    "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
+                                 _vp, _vp]),
     "gs_bin_prepare_workspace_size": (_sz, [_i64]),
     "gs_bin_prepare_3d": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _sz, _vp]),
     "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32]),
@@ -78,8 +78,8 @@ _SIGS = {
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _vp, _i32, _vp, _vp]),
-    "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp, _vp,
-                                 _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
+                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_adam_step": (_i32, [C.POINTER(GsAdamGroup), _i32, _i64, _vp, _vp]),
     "gs_l1_ssim_workspace_size": (_sz, [_i32, _i32, _i32]),
     "gs_l1_ssim_fwd": (_i32, [_vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp, _sz, _vp]),

@@ -140,21 +140,39 @@ def _check_inputs(means, log_scales, quats, opacity_logits, sh):
             raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
         if t.dtype != torch.float32 or t.device != dev:
             raise ValueError(f"{name} must be float32 on {dev}")
-    if sh.dim() != 3 or sh.shape[0] != n or sh.shape[2] != 3 or sh.shape[1] not in (1, 4, 9, 16):
-        raise ValueError(f"sh must have shape [N, K, 3] with K in (1, 4, 9, 16), got {tuple(sh.shape)}")
-    if sh.dtype != torch.float32 or sh.device != dev:
-        raise ValueError(f"sh must be float32 on {dev}")
+    sh_a, sh_b = sh if isinstance(sh, (tuple, list)) else (sh, None)
+    if sh_b is None:
+        if sh_a.dim() != 3 or sh_a.shape[0] != n or sh_a.shape[2] != 3 or sh_a.shape[1] not in (1, 4, 9, 16):
+            raise ValueError(f"sh must have shape [N, K, 3] with K in (1, 4, 9, 16), got {tuple(sh_a.shape)}")
+    else:
+        if tuple(sh_a.shape) != (n, 1, 3) or sh_b.dim() != 3 or sh_b.shape[0] != n or sh_b.shape[2] != 3 \
+                or sh_b.shape[1] + 1 not in (4, 9, 16):
+            raise ValueError(f"split SH must be ([N, 1, 3], [N, K - 1, 3]) with K in (4, 9, 16), got "
+                             f"{tuple(sh_a.shape)}, {tuple(sh_b.shape)}")
+    for t in (sh_a, sh_b):
+        if t is not None and (t.dtype != torch.float32 or t.device != dev):
+            raise ValueError(f"sh must be float32 on {dev}")
+
+
+def _sh_parts(sh):
+    """(coefficients or DC, rest or None, K) of an [N, K, 3] tensor or a (DC, rest) pair."""
+    if isinstance(sh, (tuple, list)):
+        a, b = sh[0].contiguous(), sh[1].contiguous()
+        return a, b, 1 + b.shape[1]
+    sh = sh.contiguous()
+    return sh, None, sh.shape[1]
 
 
 def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_degree: int | None = None,
                  bg=(0.0, 0.0, 0.0), timing: bool = False, keep_keys: bool = False) -> ForwardState:
-    """Runs the forward stages; inputs are contiguous float32 CUDA tensors (raw parameters)."""
+    """Runs the forward stages; inputs are contiguous float32 CUDA tensors (raw parameters). sh is
+    [N, K, 3] or the (DC [N, 1, 3], rest [N, K - 1, 3]) pair."""
     means, log_scales, quats = means.contiguous(), log_scales.contiguous(), quats.contiguous()
-    opacity_logits, sh = opacity_logits.contiguous(), sh.contiguous()
-    _check_inputs(means, log_scales, quats, opacity_logits, sh)
+    opacity_logits = opacity_logits.contiguous()
+    sh_a, sh_b, K = _sh_parts(sh)
+    _check_inputs(means, log_scales, quats, opacity_logits, (sh_a, sh_b))
     n = means.shape[0]
     dev = means.device
-    K = sh.shape[1]
     if sh_degree is None:
         sh_degree = int(round(math.sqrt(K))) - 1
     T = cam.n_tiles
@@ -167,8 +185,8 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     rec = torch.empty(n, REC_FLOATS, dtype=torch.float32, device=dev)
     touched = torch.empty(n, dtype=torch.int32, device=dev)
     dkeys = torch.empty(n, dtype=torch.int32, device=dev)
-    call("gs_preprocess_fwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh), n, K,
-         sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), st)
+    call("gs_preprocess_fwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh_a), ptr(sh_b),
+         n, K, sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), st)
     tm.mark("preprocess")
     order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
@@ -205,7 +223,8 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
                   grad_alpha=None, timing: bool = False, counters: torch.Tensor | None = None):
-    """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings).
+    """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings);
+    grad_sh is a (DC, rest) pair when sh is.
     counters: optional int64 [3] CUDA tensor that the blend backward adds its atomic count and
     pair-evaluation count to (slots 0 and 2)."""
     dev = means.device
@@ -228,10 +247,17 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
     g_ls = torch.empty(n, 3, dtype=torch.float32, device=dev)
     g_q = torch.empty(n, 4, dtype=torch.float32, device=dev)
     g_op = torch.empty(n, dtype=torch.float32, device=dev)
-    g_sh = torch.empty(n, fs.sh_coeffs, 3, dtype=torch.float32, device=dev)
-    call("gs_preprocess_bwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh), n,
-         fs.sh_coeffs, fs.sh_degree, cam.c_struct(), ptr(fs.rec), ptr(fs.touched), ptr(grad2d), ptr(g_means),
-         ptr(g_ls), ptr(g_q), ptr(g_op), ptr(g_sh), st)
+    sh_a, sh_b, _ = _sh_parts(sh)
+    if sh_b is None:
+        g_sh = torch.empty(n, fs.sh_coeffs, 3, dtype=torch.float32, device=dev)
+        g_a, g_b = g_sh, None
+    else:
+        g_a = torch.empty(n, 1, 3, dtype=torch.float32, device=dev)
+        g_b = torch.empty(n, fs.sh_coeffs - 1, 3, dtype=torch.float32, device=dev)
+        g_sh = (g_a, g_b)
+    call("gs_preprocess_bwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh_a), ptr(sh_b),
+         n, fs.sh_coeffs, fs.sh_degree, cam.c_struct(), ptr(fs.rec), ptr(fs.touched), ptr(grad2d), ptr(g_means),
+         ptr(g_ls), ptr(g_q), ptr(g_op), ptr(g_a), ptr(g_b), st)
     tm.mark("preprocess_bwd")
     return g_means, g_ls, g_q, g_op, g_sh, grad2d, {} if isinstance(timing, StageTimer) else tm.result()
 
@@ -244,27 +270,31 @@ class _Rasterize3D(torch.autograd.Function):
     last_visibility: "torch.Tensor | None" = None
 
     @staticmethod
-    def forward(ctx, means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg):
-        fs = forward_pass(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg)
+    def forward(ctx, means, log_scales, quats, opacity_logits, sh, sh_rest, cam, sh_degree, bg):
+        shp = sh if sh_rest is None else (sh, sh_rest)
+        fs = forward_pass(means, log_scales, quats, opacity_logits, shp, cam, sh_degree, bg)
         if _Rasterize3D.track_visibility:
             _Rasterize3D.last_visibility = fs.touched
         ctx.fs = fs
-        ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh)
+        ctx.split = sh_rest is not None
+        ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh, sh_rest)
         alpha = 1.0 - fs.final_T
         ctx.mark_non_differentiable(fs.touched)
         return fs.image, alpha, fs.touched
 
     @staticmethod
     def backward(ctx, grad_image, grad_alpha, _grad_touched):
-        means, log_scales, quats, opacity_logits, sh = ctx.saved_tensors
+        means, log_scales, quats, opacity_logits, sh, sh_rest = ctx.saved_tensors
         fs = ctx.fs
         if grad_image is None:
             grad_image = torch.zeros_like(fs.image)
+        shp = (sh, sh_rest) if ctx.split else sh
         gm, gls, gq, gop, gsh, grad2d, _ = backward_pass(fs, means.contiguous(), log_scales.contiguous(),
                                                          quats.contiguous(), opacity_logits.contiguous(),
-                                                         sh.contiguous(), grad_image, grad_alpha)
+                                                         shp, grad_image, grad_alpha)
         ctx.grad2d = grad2d
-        return gm, gls, gq, gop, gsh, None, None, None
+        g_a, g_b = gsh if ctx.split else (gsh, None)
+        return gm, gls, gq, gop, g_a, g_b, None, None, None
 
 
 def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None, near: float = 0.01,
@@ -274,7 +304,8 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
     Parameters follow Faster-GS's raw convention unless `activated=True`:
       means [N,3]; scales [N,3] log-scales (activated: positive scales); quats [N,4] (w, x, y, z),
       any norm; opacities [N] or [N,1] logits (activated: opacities in (0,1)); sh [N,K,3] SH
-      coefficients, K in {1,4,9,16}; viewmat [4,4] world-to-camera (OpenCV axes); K [3,3] intrinsics.
+      coefficients, K in {1,4,9,16}, or the pair (DC [N,1,3], rest [N,K-1,3]) that trainers keep
+      as two parameters; viewmat [4,4] world-to-camera (OpenCV axes); K [3,3] intrinsics.
     aux: {"tiles_touched": [N] int32 (> 0 = visible; the visibility mask for a sparse optimizer),
           "n_visible", "n_instances", "n_buckets"}.
     Gradients flow to means, scales, quats, opacities and sh.
@@ -288,7 +319,8 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
     if bg is None:
         bg = (0.0, 0.0, 0.0)
     bg = tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
-    image, alpha, touched = _Rasterize3D.apply(means, scales, quats, opacities, sh, cam, sh_degree, bg)
+    sh_a, sh_b = sh if isinstance(sh, (tuple, list)) else (sh, None)
+    image, alpha, touched = _Rasterize3D.apply(means, scales, quats, opacities, sh_a, sh_b, cam, sh_degree, bg)
     aux = {"tiles_touched": touched}
     aux["n_visible"] = lambda: int((touched > 0).sum().item())
     return image, alpha, aux

@@ -28,67 +28,148 @@ struct ShStage {
   static constexpr int CP = R | 1;           // padded LDS row (odd: conflict-free)
 };
 
-// Copies rows [RH h, RH h + RH) of the wavefront's `rows` SH rows into LDS rows of stride CP.
+// SH coefficients of the Gaussians: one [n, K, 3] array, or (split) the DC [n, 1, 3] and the
+// rest [n, K - 1, 3] as two arrays, the layout of trainers that give the two their own
+// learning rates.
+struct ShPtr {
+  const float* a;  // [n, K, 3], or the DC [n, 1, 3] when b is set
+  const float* b;  // the rest [n, K - 1, 3], or NULL
+};
+struct ShOut {
+  float* a;
+  float* b;
+};
+
+// rows x RW floats at blk (contiguous) -> LDS rows of pitch CP from column c0 (RW, CP fixed;
+// FULL rows, if not 0: the unrolled path for a whole pass, every load in flight before the
+// first store).
+template <int RW, int CP, int FULL>
+__device__ __forceinline__ void rows_to_lds(const float* __restrict__ blk, int nr, float* srow, int c0, int lane) {
+  if constexpr (RW > 0) {
+    constexpr int N4 = FULL * RW / 4;
+    if constexpr (FULL > 0 && (FULL * RW) % 4 == 0) {
+      if (nr == FULL && aligned16(blk)) {
+        constexpr int IT = (N4 + 63) / 64;
+        float4 v[IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+          const int f4 = lane + 64 * it;
+          if (N4 % 64 == 0 || f4 < N4) v[it] = reinterpret_cast<const float4*>(blk)[f4];
+        }
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+          const int f4 = lane + 64 * it;
+          if (N4 % 64 == 0 || f4 < N4) {
+            if constexpr (RW % 4 == 0) {  // a float4 never crosses a row
+              const int row = f4 / (RW / 4), q = f4 - row * (RW / 4);
+              float* d = srow + row * CP + c0 + 4 * q;
+              d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+            } else {
+              const float vv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int idx = 4 * f4 + e, row = idx / RW;
+                srow[row * CP + c0 + idx - row * RW] = vv[e];
+              }
+            }
+          }
+        }
+        return;
+      }
+    }
+    const int total = nr * RW;
+    if (aligned16(blk)) {
+      const int n4 = total >> 2;
+      for (int f4 = lane; f4 < n4; f4 += 64) {
+        const float4 v = reinterpret_cast<const float4*>(blk)[f4];
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int idx = 4 * f4 + e, row = idx / RW;
+          srow[row * CP + c0 + idx - row * RW] = vv[e];
+        }
+      }
+      for (int idx = 4 * n4 + lane; idx < total; idx += 64) {
+        const int row = idx / RW;
+        srow[row * CP + c0 + idx - row * RW] = blk[idx];
+      }
+    } else {
+      for (int idx = lane; idx < total; idx += 64) {
+        const int row = idx / RW;
+        srow[row * CP + c0 + idx - row * RW] = blk[idx];
+      }
+    }
+  }
+}
+
+template <int RW, int CP>
+__device__ __forceinline__ void lds_to_rows(float* __restrict__ blk, int nr, const float* srow, int c0, int lane) {
+  if constexpr (RW > 0) {
+    const int total = nr * RW;
+    if (aligned16(blk)) {
+      const int n4 = total >> 2;
+      for (int f4 = lane; f4 < n4; f4 += 64) {
+        float vv[4];
+        if constexpr (RW % 4 == 0) {  // a float4 never crosses a row
+          const int row = f4 / (RW / 4), q = f4 - row * (RW / 4);
+          const float* d = srow + row * CP + c0 + 4 * q;
+          vv[0] = d[0]; vv[1] = d[1]; vv[2] = d[2]; vv[3] = d[3];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * f4 + e, row = idx / RW;
+            vv[e] = srow[row * CP + c0 + idx - row * RW];
+          }
+        }
+        reinterpret_cast<float4*>(blk)[f4] = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      }
+      for (int idx = 4 * n4 + lane; idx < total; idx += 64) {
+        const int row = idx / RW;
+        blk[idx] = srow[row * CP + c0 + idx - row * RW];
+      }
+    } else {
+      for (int idx = lane; idx < total; idx += 64) {
+        const int row = idx / RW;
+        blk[idx] = srow[row * CP + c0 + idx - row * RW];
+      }
+    }
+  }
+}
+
+// Copies rows [RH h, RH h + RH) of the wavefront's `rows` SH rows (the wavefront's first row is
+// `first`) into LDS rows of stride CP.
 template <int K>
-__device__ __forceinline__ void stage_sh(const float* __restrict__ src, int rows, int h, float* srow, int lane) {
+__device__ __forceinline__ void stage_sh(ShPtr src, int64_t first, int rows, int h, float* srow, int lane) {
   using St = ShStage<K>;
   constexpr int R = St::R, CP = St::CP, RH = St::RH;
   const int r0 = RH * h;
   const int nr = min(RH, rows - r0);
   if (nr <= 0) return;
-  const float* blk = src + static_cast<int64_t>(r0) * R;
-  if constexpr (R % 4 == 0) {
-    if (aligned16(blk)) {
-      constexpr int Q = R / 4;
-      if (nr == RH) {
-#pragma unroll
-        for (int it = 0; it < RH * Q / 64; ++it) {  // every load in flight before the first store
-          const int f4 = lane + 64 * it;
-          const int row = f4 / Q, q = f4 - row * Q;
-          const float4 v = reinterpret_cast<const float4*>(blk)[f4];
-          float* d = srow + row * CP + 4 * q;
-          d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-        }
-        return;
-      }
-      for (int f4 = lane; f4 < nr * Q; f4 += 64) {
-        const int row = f4 / Q, q = f4 - row * Q;
-        const float4 v = reinterpret_cast<const float4*>(blk)[f4];
-        float* d = srow + row * CP + 4 * q;
-        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-      }
-      return;
-    }
-  }
-  for (int f = lane; f < nr * R; f += 64) {
-    const int row = f / R, c = f - row * R;
-    srow[row * CP + c] = blk[f];
+  const int64_t row = first + r0;
+  if (src.b == nullptr) {
+    rows_to_lds<R, CP, RH>(src.a + row * R, nr, srow, 0, lane);
+  } else {
+    // (the split layout takes the plain loop: an unrolled one for rows not a multiple of four
+    // floats costs the kernel registers, i.e. occupancy, on the single-array path too)
+    rows_to_lds<3, CP, 0>(src.a + row * 3, nr, srow, 0, lane);
+    rows_to_lds<R - 3, CP, 0>(src.b + row * (R - 3), nr, srow, 3, lane);
   }
 }
 
 // Writes the staged rows of pass h back to the wavefront's rows.
 template <int K>
-__device__ __forceinline__ void unstage_sh(float* __restrict__ dst, int rows, int h, const float* srow, int lane) {
+__device__ __forceinline__ void unstage_sh(ShOut dst, int64_t first, int rows, int h, const float* srow, int lane) {
   using St = ShStage<K>;
   constexpr int R = St::R, CP = St::CP, RH = St::RH;
   const int r0 = RH * h;
   const int nr = min(RH, rows - r0);
   if (nr <= 0) return;
-  float* blk = dst + static_cast<int64_t>(r0) * R;
-  if constexpr (R % 4 == 0) {
-    if (aligned16(blk)) {
-      constexpr int Q = R / 4;
-      for (int f4 = lane; f4 < nr * Q; f4 += 64) {
-        const int row = f4 / Q, q = f4 - row * Q;
-        const float* d = srow + row * CP + 4 * q;
-        reinterpret_cast<float4*>(blk)[f4] = make_float4(d[0], d[1], d[2], d[3]);
-      }
-      return;
-    }
-  }
-  for (int f = lane; f < nr * R; f += 64) {
-    const int row = f / R, c = f - row * R;
-    blk[f] = srow[row * CP + c];
+  const int64_t row = first + r0;
+  if (dst.b == nullptr) {
+    lds_to_rows<R, CP>(dst.a + row * R, nr, srow, 0, lane);
+  } else {
+    lds_to_rows<3, CP>(dst.a + row * 3, nr, srow, 0, lane);
+    lds_to_rows<R - 3, CP>(dst.b + row * (R - 3), nr, srow, 3, lane);
   }
 }
 
@@ -194,7 +275,7 @@ template <int K>
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
-    const float* __restrict__ sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
+    ShPtr sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
     uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys) {
   using St = ShStage<K>;
   __shared__ float s_sh[4][St::RH * St::CP];
@@ -261,7 +342,6 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   if (vmask != 0) {
     float* srow = s_sh[wave];
     const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
-    const float* src = sh + wave_first * St::R;
     float basis[16];
     float acc[3] = {0.0f, 0.0f, 0.0f};
     if (g.vis) {
@@ -275,7 +355,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 #pragma unroll
     for (int h = 0; h < St::NH; ++h) {
       if (h) wave_sync();  // every lane is done with the previous rows
-      stage_sh<K>(src, rows, h, srow, lane);
+      stage_sh<K>(sh, wave_first, rows, h, srow, lane);
       wave_sync();
       if (g.vis && lane / St::RH == h) {
         const float* row = srow + (lane - St::RH * h) * St::CP;
@@ -314,14 +394,14 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 // Backward
 // ---------------------------------------------------------------------------------------
 template <int K>
-__global__ __launch_bounds__(256) void preprocess_bwd_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void preprocess_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
-    const float* __restrict__ sh, int64_t n, int active, CamK cam,
+    ShPtr sh, int64_t n, int active, CamK cam,
     const SplatRec* __restrict__ rec, const uint32_t* __restrict__ tiles_touched,
     const float* __restrict__ grad2d, float* __restrict__ g_means,
     float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
-    float* __restrict__ g_opacity, float* __restrict__ g_sh) {
+    float* __restrict__ g_opacity, ShOut g_sh) {
   using St = ShStage<K>;
   __shared__ float s_sh[4][St::RH * St::CP];
   const int lane = threadIdx.x & 63;
@@ -358,13 +438,11 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
     dz = dzw * il;
     sh_basis(dx, dy, dz, active, basis);
   }
-  const float* src = sh + wave_first * St::R;
-  float* dst = g_sh + wave_first * St::R;
 #pragma unroll
   for (int h = 0; h < St::NH; ++h) {
     if (vmask != 0) {
       if (h) wave_sync();  // the previous rows are written out
-      stage_sh<K>(src, rows, h, srow, lane);
+      stage_sh<K>(sh, wave_first, rows, h, srow, lane);
       wave_sync();
       if (lane / St::RH == h) {
         float* row = srow + (lane - St::RH * h) * St::CP;
@@ -384,11 +462,19 @@ __global__ __launch_bounds__(256) void preprocess_bwd_kernel(
         }
       }
       wave_sync();
-      unstage_sh<K>(dst, rows, h, srow, lane);
+      unstage_sh<K>(g_sh, wave_first, rows, h, srow, lane);
     }
   }
-  if (vmask == 0) {
-    for (int f = lane; f < rows * St::R; f += 64) dst[f] = 0.0f;
+  if (vmask == 0) {  // no visible Gaussian: zero rows
+    if (g_sh.b == nullptr) {
+      float* dst = g_sh.a + wave_first * St::R;
+      for (int f = lane; f < rows * St::R; f += 64) dst[f] = 0.0f;
+    } else {
+      float* d0 = g_sh.a + wave_first * 3;
+      float* d1 = g_sh.b + wave_first * (St::R - 3);
+      for (int f = lane; f < rows * 3; f += 64) d0[f] = 0.0f;
+      for (int f = lane; f < rows * (St::R - 3); f += 64) d1[f] = 0.0f;
+    }
   }
 
   if (vis) {
@@ -512,7 +598,7 @@ using namespace gs;
 
 template <int K>
 static void launch_pre_fwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
-                           const float* quats, const float* op, const float* sh, int64_t n,
+                           const float* quats, const float* op, ShPtr sh, int64_t n,
                            int active, const CamK& cam, float* rec, uint32_t* touched, uint32_t* dkeys) {
   hipLaunchKernelGGL(preprocess_fwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
@@ -521,10 +607,10 @@ static void launch_pre_fwd(int64_t blocks, hipStream_t st, const float* means, c
 
 template <int K>
 static void launch_pre_bwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
-                           const float* quats, const float* op, const float* sh, int64_t n,
+                           const float* quats, const float* op, ShPtr sh, int64_t n,
                            int active, const CamK& cam, const float* rec, const uint32_t* touched,
                            const float* g2, float* gm, float* gls, float* gq, float* gop,
-                           float* gsh) {
+                           ShOut gsh) {
   hipLaunchKernelGGL(preprocess_bwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
                      reinterpret_cast<const SplatRec*>(rec), touched, g2, gm, gls,
@@ -540,8 +626,8 @@ static int check_sh(int sh_coeffs, int sh_degree) {
 }
 
 extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, const float* quats,
-                                 const float* opacity_logits, const float* sh, int64_t n,
-                                 int sh_coeffs, int sh_degree, const gs_camera* cam,
+                                 const float* opacity_logits, const float* sh, const float* sh_rest,
+                                 int64_t n, int sh_coeffs, int sh_degree, const gs_camera* cam,
                                  float* splat_rec, uint32_t* tiles_touched, uint32_t* depth_keys,
                                  void* stream) {
   clear_error();
@@ -551,28 +637,30 @@ extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, co
   if (n == 0) return GS_OK;
   GS_REQUIRE(means && log_scales && quats && opacity_logits && sh && splat_rec && tiles_touched,
              GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(!(sh_rest && sh_coeffs == 1), GS_ERR_ARG, "sh_rest given for a DC-only model");
   GS_REQUIRE(aligned(quats, 16) && aligned(splat_rec, 16), GS_ERR_ALIGN,
              "quats and splat_rec must be 16-byte aligned");
   const CamK k = make_cam(*cam);
   const int active = (sh_degree + 1) * (sh_degree + 1);
   const int64_t blocks = (n + 255) / 256;
   hipStream_t st = as_stream(stream);
+  const ShPtr shp{sh, sh_rest};
   switch (sh_coeffs) {
-    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
-    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
-    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
-    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
   }
   return check_launch("preprocess_fwd");
 }
 
 extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, const float* quats,
-                                 const float* opacity_logits, const float* sh, int64_t n,
-                                 int sh_coeffs, int sh_degree, const gs_camera* cam,
+                                 const float* opacity_logits, const float* sh, const float* sh_rest,
+                                 int64_t n, int sh_coeffs, int sh_degree, const gs_camera* cam,
                                  const float* splat_rec, const uint32_t* tiles_touched,
                                  const float* grad2d, float* grad_means, float* grad_log_scales,
                                  float* grad_quats, float* grad_opacity_logits, float* grad_sh,
-                                 void* stream) {
+                                 float* grad_sh_rest, void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
   if (int e = check_cam(cam)) return e;
@@ -582,17 +670,21 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
                  grad2d && grad_means && grad_log_scales && grad_quats && grad_opacity_logits &&
                  grad_sh,
              GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(!sh_rest == !grad_sh_rest, GS_ERR_ARG, "sh_rest and grad_sh_rest go together");
+  GS_REQUIRE(!(sh_rest && sh_coeffs == 1), GS_ERR_ARG, "sh_rest given for a DC-only model");
   GS_REQUIRE(aligned(quats, 16) && aligned(splat_rec, 16) && aligned(grad_quats, 16), GS_ERR_ALIGN,
              "quats, splat_rec and grad_quats must be 16-byte aligned");
   const CamK k = make_cam(*cam);
   const int active = (sh_degree + 1) * (sh_degree + 1);
   const int64_t blocks = (n + 255) / 256;
   hipStream_t st = as_stream(stream);
+  const ShPtr shp{sh, sh_rest};
+  const ShOut gsh{grad_sh, grad_sh_rest};
   switch (sh_coeffs) {
-    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
-    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
-    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
-    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, sh, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh); break;
+    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
   }
   return check_launch("preprocess_bwd");
 }

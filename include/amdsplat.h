@@ -78,14 +78,16 @@ int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
  * conic, SH colour of degree sh_degree (+0.5, clamped at 0), the alpha >= 1/255 ellipse
  * bounds, and the number of 16x16 tiles the ellipse reaches (0 = culled).
  *   means, log_scales [n,3]; quats [n,4]; opacity_logits [n]; sh [n, sh_coeffs, 3] with
- *   sh_coeffs in {1,4,9,16} and (sh_degree+1)^2 <= sh_coeffs.
+ *   sh_coeffs in {1,4,9,16} and (sh_degree+1)^2 <= sh_coeffs; or, with sh_rest not NULL, the
+ *   DC coefficients sh [n, 1, 3] and the rest sh_rest [n, sh_coeffs - 1, 3] as two arrays (the
+ *   sh_coefficients_0 / sh_coefficients_rest split of Faster-GS's model).
  *   out: splat_rec [n,16] floats (16-byte aligned), tiles_touched [n] uint32, and (may be
  *   NULL) depth_keys [n] uint32: the orderable bits of the view depth of a Gaussian with
  *   tiles, 0xffffffff for a culled one (the keys gs_bin_prepare_3d sorts by).
  * ------------------------------------------------------------------------------------- */
 int gs_preprocess_fwd(const float* means, const float* log_scales, const float* quats,
-                      const float* opacity_logits, const float* sh, int64_t n, int sh_coeffs,
-                      int sh_degree, const gs_camera* cam, float* splat_rec,
+                      const float* opacity_logits, const float* sh, const float* sh_rest, int64_t n,
+                      int sh_coeffs, int sh_degree, const gs_camera* cam, float* splat_rec,
                       uint32_t* tiles_touched, uint32_t* depth_keys, void* stream);
 
 /* ---------------------------------------------------------------------------------------
@@ -177,14 +179,15 @@ int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32
  * 3D preprocess backward (replaces Faster-GS preprocess_backward_cu, csv:4): chains grad2d
  * into the parameters. Every output row is written (zeros for culled Gaussians).
  *   grad_means, grad_log_scales [n,3]; grad_quats [n,4]; grad_opacity_logits [n];
- *   grad_sh [n, sh_coeffs, 3] (coefficients above the active degree get 0).
+ *   grad_sh [n, sh_coeffs, 3] (coefficients above the active degree get 0); with the split
+ *   layout (sh_rest not NULL) grad_sh [n, 1, 3] and grad_sh_rest [n, sh_coeffs - 1, 3].
  * ------------------------------------------------------------------------------------- */
 int gs_preprocess_bwd(const float* means, const float* log_scales, const float* quats,
-                      const float* opacity_logits, const float* sh, int64_t n, int sh_coeffs,
-                      int sh_degree, const gs_camera* cam, const float* splat_rec,
+                      const float* opacity_logits, const float* sh, const float* sh_rest, int64_t n,
+                      int sh_coeffs, int sh_degree, const gs_camera* cam, const float* splat_rec,
                       const uint32_t* tiles_touched, const float* grad2d, float* grad_means,
                       float* grad_log_scales, float* grad_quats, float* grad_opacity_logits,
-                      float* grad_sh, void* stream);
+                      float* grad_sh, float* grad_sh_rest, void* stream);
 
 /* =======================================================================================
  * 2D surfaces (rules GS_RULES_TOY2D / GS_RULES_PHASE0; dtype GS_FLOAT32 / GS_FLOAT64)

@@ -289,3 +289,28 @@ def test_equal_depths_keep_index_order():
     rng = np_(fs.ranges)
     for s, e in rng:
         assert np.all(np.diff(pl[s:e].astype(np.int64)) > 0)
+
+
+@pytest.mark.parametrize("K", [4, 9, 16])
+def test_split_sh_layout_equals_single_tensor(K):
+    """The (DC, rest) pair of Faster-GS's model gives the records and gradients of the single
+    [N, K, 3] tensor bit for bit."""
+    sc = make("partial_tiles", seed=5, sh_coeffs=K)
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    deg = int(round(K ** 0.5)) - 1
+    split = (p[4][:, :1].contiguous(), p[4][:, 1:].contiguous())
+    fs_a = R.forward_pass(*p, cam, sh_degree=deg, bg=BG)
+    fs_b = R.forward_pass(*p[:4], split, cam, sh_degree=deg, bg=BG)
+    torch.cuda.synchronize()
+    vis = fs_a.touched > 0  # records of culled Gaussians are not written
+    assert torch.equal(fs_a.touched, fs_b.touched) and torch.equal(fs_a.rec[vis], fs_b.rec[vis])
+    assert torch.equal(fs_a.image, fs_b.image)
+    gi = torch.randn(fs_a.image.shape, generator=torch.Generator().manual_seed(2)).cuda()
+    ga = R.backward_pass(fs_a, *p, gi)
+    gb = R.backward_pass(fs_b, *p[:4], split, gi)
+    rel = lambda a, b: float((a - b).norm() / max(float(b.norm()), 1e-30))
+    # two backward runs: the blend's atomics may add in another order, hence 1e-5 relative
+    for a, b in zip(ga[:4], gb[:4]):
+        assert rel(a, b) < 1e-5
+    assert rel(gb[4][0], ga[4][:, :1]) < 1e-5 and rel(gb[4][1], ga[4][:, 1:]) < 1e-5
