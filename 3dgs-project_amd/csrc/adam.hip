@@ -85,25 +85,54 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamArgs a) {
     any = any || live[k];
   }
   if (!any) return;
-  const bool vec = cnt == kAdamPerThread && live[0] && live[1] && live[2] && live[3] &&
-                   ((reinterpret_cast<uintptr_t>(G.grad + e0) | reinterpret_cast<uintptr_t>(G.param + e0)) & 15u) == 0;
-  float g[kAdamPerThread], p[kAdamPerThread], m[kAdamPerThread], v[kAdamPerThread];
-  if (vec && !G.lowp && ((reinterpret_cast<uintptr_t>(static_cast<float*>(G.m) + e0) |
-                          reinterpret_cast<uintptr_t>(static_cast<float*>(G.v) + e0)) & 15u) == 0) {
+  // 16-byte accesses whenever the four elements exist and are aligned; elements of hidden rows
+  // are written back bit-identical (no other thread owns them)
+  const bool al = cnt == kAdamPerThread &&
+                  ((reinterpret_cast<uintptr_t>(G.grad + e0) | reinterpret_cast<uintptr_t>(G.param + e0)) & 15u) == 0;
+  if (al) {
+    float g[kAdamPerThread], p[kAdamPerThread], m[kAdamPerThread], v[kAdamPerThread];
     const float4 g4 = *reinterpret_cast<const float4*>(G.grad + e0);
     const float4 p4 = *reinterpret_cast<const float4*>(G.param + e0);
-    const float4 m4 = *reinterpret_cast<const float4*>(static_cast<float*>(G.m) + e0);
-    const float4 v4 = *reinterpret_cast<const float4*>(static_cast<float*>(G.v) + e0);
     g[0] = g4.x; g[1] = g4.y; g[2] = g4.z; g[3] = g4.w;
     p[0] = p4.x; p[1] = p4.y; p[2] = p4.z; p[3] = p4.w;
-    m[0] = m4.x; m[1] = m4.y; m[2] = m4.z; m[3] = m4.w;
-    v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
+    if (!G.lowp && ((reinterpret_cast<uintptr_t>(static_cast<float*>(G.m) + e0) |
+                     reinterpret_cast<uintptr_t>(static_cast<float*>(G.v) + e0)) & 15u) == 0) {
+      const float4 m4 = *reinterpret_cast<const float4*>(static_cast<float*>(G.m) + e0);
+      const float4 v4 = *reinterpret_cast<const float4*>(static_cast<float*>(G.v) + e0);
+      m[0] = m4.x; m[1] = m4.y; m[2] = m4.z; m[3] = m4.w;
+      v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
 #pragma unroll
-    for (int k = 0; k < kAdamPerThread; ++k) adam_elem(G, g[k], p[k], m[k], v[k]);
-    *reinterpret_cast<float4*>(G.param + e0) = make_float4(p[0], p[1], p[2], p[3]);
-    *reinterpret_cast<float4*>(static_cast<float*>(G.m) + e0) = make_float4(m[0], m[1], m[2], m[3]);
-    *reinterpret_cast<float4*>(static_cast<float*>(G.v) + e0) = make_float4(v[0], v[1], v[2], v[3]);
-    return;
+      for (int k = 0; k < kAdamPerThread; ++k)
+        if (live[k]) adam_elem(G, g[k], p[k], m[k], v[k]);
+      *reinterpret_cast<float4*>(G.param + e0) = make_float4(p[0], p[1], p[2], p[3]);
+      *reinterpret_cast<float4*>(static_cast<float*>(G.m) + e0) = make_float4(m[0], m[1], m[2], m[3]);
+      *reinterpret_cast<float4*>(static_cast<float*>(G.v) + e0) = make_float4(v[0], v[1], v[2], v[3]);
+      return;
+    }
+    if (G.lowp && ((reinterpret_cast<uintptr_t>(static_cast<uint16_t*>(G.m) + e0) |
+                    reinterpret_cast<uintptr_t>(static_cast<uint16_t*>(G.v) + e0)) & 7u) == 0) {
+      const uint2 mb = *reinterpret_cast<const uint2*>(static_cast<uint16_t*>(G.m) + e0);
+      const uint2 vb = *reinterpret_cast<const uint2*>(static_cast<uint16_t*>(G.v) + e0);
+      uint32_t mw[2] = {mb.x, mb.y}, vw[2] = {vb.x, vb.y};
+#pragma unroll
+      for (int k = 0; k < kAdamPerThread; ++k) {
+        const uint32_t sh = 16u * (k & 1);
+        m[k] = __uint_as_float(((mw[k >> 1] >> sh) & 0xffffu) << 16);
+        v[k] = __uint_as_float(((vw[k >> 1] >> sh) & 0xffffu) << 16);
+        if (!live[k]) continue;
+        adam_elem(G, g[k], p[k], m[k], v[k]);
+        const int64_t idx = e0 + k;
+        const uint32_t r1 = sr_hash(static_cast<uint32_t>(idx) ^ G.seed);
+        const uint32_t r2 = sr_hash(r1);
+        const uint32_t keep = 0xffffu << (16u - sh);  // the other half-word
+        mw[k >> 1] = (mw[k >> 1] & keep) | (static_cast<uint32_t>(to_bf16_sr(m[k], r1)) << sh);
+        vw[k >> 1] = (vw[k >> 1] & keep) | (static_cast<uint32_t>(to_bf16_sr(v[k], r2)) << sh);
+      }
+      *reinterpret_cast<float4*>(G.param + e0) = make_float4(p[0], p[1], p[2], p[3]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(G.m) + e0) = make_uint2(mw[0], mw[1]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(G.v) + e0) = make_uint2(vw[0], vw[1]);
+      return;
+    }
   }
 #pragma unroll
   for (int k = 0; k < kAdamPerThread; ++k) {

@@ -5,11 +5,15 @@ Workload (default): 1M Gaussians, SH degree 3, 1297x840, fx=fy=1160, 8 seeded or
 N(0,1) upstream image gradient. Inputs are resident in HBM before the timed region.
 
     python bench.py [--steps K] [--warmup W] [--workload sh3_1m|sh3_3m|sh_rgb_100k] [--no-cpu-baseline]
+                    [--no-train-step]
     python bench.py --copy-probe      # a plain 1 GiB device copy, to calibrate HBM counters
 
 Prints ONE JSON line. Per-stage times come from HIP events recorded on the launch stream
 inside the timed region; `roofline` is for the kernel with the largest share of the step
-(the bucketed blend backward), from its algorithmic bytes and its event-timed duration.
+(the bucketed blend backward), from its algorithmic bytes and its event-timed duration, plus
+its VALU issue rate from the committed SQ counter summary. `train_step` (secondary) times the
+full training step on the same scene: forward, L1 + D-SSIM loss, backward and fused Adam
+(dense and visibility-masked), with the optimizer's HBM rate.
 """
 from __future__ import annotations
 
@@ -44,6 +48,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="threads for the CPU baseline (0 = OMP default)")
     ap.add_argument("--copy-probe", action="store_true", help="time a plain 1 GiB device copy and exit")
+    ap.add_argument("--no-train-step", action="store_true", help="skip the training-step measurement")
     ap.add_argument("--json-out", default=None)
     return ap.parse_args()
 
@@ -141,6 +146,74 @@ def cpu_baseline(scene, pose, threads):
             "nproc": os.cpu_count(), "cpu_model": cpu_model(),
             "sample": f"C oracle fwd+bwd of pose {pose}, all {scene.n} Gaussians ({dt:.1f} s; preprocess and "
                       f"forward blend on {cores} OpenMP threads, sort and backward blend single-threaded)"}
+
+
+# learning rates of the training-step workload (means, log-scales, quats, SH DC, SH rest, opacity)
+TRAIN_LR = {"means": 1.6e-4, "scales": 5e-3, "quats": 1e-3, "sh_dc": 2.5e-3, "sh_rest": 1.25e-4, "opacity": 5e-2}
+
+
+def train_step_bench(scene, steps: int, warmup: int) -> dict:
+    """The full training step on the same scene: forward, L1 + D-SSIM (lambda 0.2) against a
+    seeded U(0,1) target, backward, fused Adam over all 59 parameters per Gaussian (dense, and
+    masked to the Gaussians visible in the view). Poses cycle as in the main measurement."""
+    import torch
+
+    from amdsplat import FusedAdam, l1_ssim_loss, rasterize
+
+    sc = scene.to("cuda")
+    m, ls, q, op, sh = [t.contiguous() for t in sc.params()]
+    P = {"means": m, "scales": ls, "quats": q, "opacity": op, "sh_dc": sh[:, :1].contiguous(),
+         "sh_rest": sh[:, 1:].contiguous()}
+    cams = sc.cameras
+    g = torch.Generator().manual_seed(4321)
+    targets = [torch.rand(3, c.height, c.width, generator=g).cuda() for c in cams]
+    Ks = [torch.tensor([[c.fx, 0.0, c.cx], [0.0, c.fy, c.cy], [0.0, 0.0, 1.0]]) for c in cams]
+    n = m.shape[0]
+    out = {"workload": f"{n} Gaussians SH3 {cams[0].width}x{cams[0].height}: fwd, L1+D-SSIM (11x11, lambda 0.2), "
+                       f"bwd, fused Adam over 59 fp32 parameters per Gaussian",
+           "lr": TRAIN_LR}
+    for mode in ("dense", "masked"):
+        params = {k: torch.nn.Parameter(v.clone()) for k, v in P.items()}
+        groups = [{"params": [params[k]], "lr": lr, "name": k} for k, lr in TRAIN_LR.items()]
+        opt = FusedAdam(groups, lr=0.0, eps=1e-15, sparse=(mode == "masked"))
+        vis_sum = 0
+
+        def step(k, ev=None):
+            c = cams[k % len(cams)]
+            img, _, aux = rasterize(params["means"], params["scales"], params["quats"], params["opacity"],
+                                    (params["sh_dc"], params["sh_rest"]), c.viewmat, Ks[k % len(cams)], c.width,
+                                    c.height, near=c.near, far=c.far)
+            loss = l1_ssim_loss(img, targets[k % len(cams)], 0.2)
+            loss.backward()
+            if ev:
+                ev[0].record()
+            opt.step()
+            if ev:
+                ev[1].record()
+            opt.zero_grad(set_to_none=True)
+            return aux["tiles_touched"]
+
+        for k in range(warmup):
+            step(k)
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        t0 = time.perf_counter()
+        touched = []
+        for k in range(steps):
+            touched.append(step(k, evs[k]))
+        torch.cuda.synchronize()
+        step_ms = (time.perf_counter() - t0) * 1000.0 / steps
+        adam_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+        vis_sum = sum(int((t > 0).sum().item()) for t in touched) / steps
+        nbytes = 1652 * n if mode == "dense" else int(1652 * vis_sum) + 4 * n
+        out[mode] = {"step_ms": round(step_ms, 4), "adam_ms": round(adam_ms, 4),
+                     "adam_hbm_gbs": round(nbytes / (adam_ms * 1e6), 1),
+                     "adam_hbm_frac": round(nbytes / (adam_ms * 1e6) / HBM_PEAK_GBS, 4),
+                     "adam_algorithmic_bytes": nbytes, "visible_per_view": round(vis_sum)}
+        from amdsplat.raster3d import _Rasterize3D
+
+        _Rasterize3D.track_visibility = False
+    return out
 
 
 def copy_probe():
@@ -262,6 +335,8 @@ def main():
                      "traffic": traffic, "algorithmic_bytes": sb[dominant],
                      "avg_launch_ms": round(stage_ms[dominant], 4), "valu": valu},
     }
+    if not args.no_train_step:
+        out["train_step"] = train_step_bench(scene, steps=max(args.steps // 2, 5), warmup=3)
     if not args.no_cpu_baseline:
         try:
             out["cpu_baseline"] = cpu_baseline(scene, 0, args.cpu_threads)

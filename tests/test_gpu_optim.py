@@ -145,3 +145,21 @@ def test_visibility_from_forward_and_sparse_step():
         assert torch.equal(p.detach()[hid], b[hid])
     assert opt.state[params[4]]["exp_avg"].dtype == torch.bfloat16
     R._Rasterize3D.track_visibility = False
+
+
+@pytest.mark.parametrize("shape", [(3001, 3), (3001, 15, 3), (3001, 1)])
+def test_masked_bf16_bit_exact_vs_oracle(shape):
+    g = torch.Generator().manual_seed(6)
+    vis = (torch.rand(shape[0], generator=g) < 0.5).int()
+    p0 = torch.randn(*shape, generator=g)
+    p = p0.to(dev)
+    m = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+    v = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+    pn, mn, vn = p0.numpy().copy(), np.zeros(shape, np.uint16), np.zeros(shape, np.uint16)
+    for step in range(1, 4):
+        gr = torch.randn(*shape, generator=g) * 1e-3
+        adam_step_sparse(gr.to(dev), p, m, v, vis.to(dev), step, 2.5e-3, 0.9, 0.999, 1e-15)
+        P.adam_step(gr.numpy(), pn, mn, vn, step, 2.5e-3, 0.9, 0.999, 1e-15, visibility=vis.numpy())
+    assert np.array_equal(np_(p).view(np.uint32), pn.view(np.uint32))
+    assert np.array_equal(np_(m.view(torch.int16)).view(np.uint16), mn)
+    assert np.array_equal(np_(v.view(torch.int16)).view(np.uint16), vn)
