@@ -81,6 +81,7 @@ _SIGS = {
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_adam_step": (_i32, [C.POINTER(GsAdamGroup), _i32, _i64, _vp, _vp]),
+    "gs_densification_stats": (_i32, [_vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp]),
     "gs_l1_ssim_workspace_size": (_sz, [_i32, _i32, _i32]),
     "gs_l1_ssim_fwd": (_i32, [_vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp, _sz, _vp]),
     "gs_l1_ssim_bwd": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp]),

@@ -262,6 +262,18 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
     return g_means, g_ls, g_q, g_op, g_sh, grad2d, {} if isinstance(timing, StageTimer) else tm.result()
 
 
+def densification_stats(grad2d: torch.Tensor, touched: torch.Tensor, width: int, height: int,
+                        info: torch.Tensor) -> None:
+    """Adds one view's densification statistics to info [2 or 3, N] (float32, in place): a visible
+    count, the NDC norm of the mean2d gradient and (3 rows) the NDC norm of the summed |dL/dmean2d|."""
+    n = touched.shape[0]
+    if info.dim() != 2 or info.shape[1] != n or info.shape[0] not in (2, 3) or info.dtype != torch.float32 \
+            or not info.is_contiguous():
+        raise ValueError(f"densification_info must be contiguous float32 [2 or 3, {n}]")
+    call("gs_densification_stats", ptr(grad2d), ptr(touched), n, int(width), int(height), int(info.shape[0]),
+         ptr(info), _lib.stream_handle(info.device))
+
+
 class _Rasterize3D(torch.autograd.Function):
     # visibility hand-off for the sparse optimizer (cluster/patches/fastergs_lean_adam.patch:333-343):
     # with track_visibility set, each differentiable forward keeps its tiles_touched (int32 [n],
@@ -270,12 +282,13 @@ class _Rasterize3D(torch.autograd.Function):
     last_visibility: "torch.Tensor | None" = None
 
     @staticmethod
-    def forward(ctx, means, log_scales, quats, opacity_logits, sh, sh_rest, cam, sh_degree, bg):
+    def forward(ctx, means, log_scales, quats, opacity_logits, sh, sh_rest, cam, sh_degree, bg, dinfo=None):
         shp = sh if sh_rest is None else (sh, sh_rest)
         fs = forward_pass(means, log_scales, quats, opacity_logits, shp, cam, sh_degree, bg)
         if _Rasterize3D.track_visibility:
             _Rasterize3D.last_visibility = fs.touched
         ctx.fs = fs
+        ctx.dinfo = dinfo
         ctx.split = sh_rest is not None
         ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh, sh_rest)
         alpha = 1.0 - fs.final_T
@@ -293,12 +306,15 @@ class _Rasterize3D(torch.autograd.Function):
                                                          quats.contiguous(), opacity_logits.contiguous(),
                                                          shp, grad_image, grad_alpha)
         ctx.grad2d = grad2d
+        if ctx.dinfo is not None:
+            densification_stats(grad2d, fs.touched, fs.cam.width, fs.cam.height, ctx.dinfo)
         g_a, g_b = gsh if ctx.split else (gsh, None)
-        return gm, gls, gq, gop, g_a, g_b, None, None, None
+        return gm, gls, gq, gop, g_a, g_b, None, None, None, None
 
 
 def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None, near: float = 0.01,
-              far: float = 100.0, sh_degree: int | None = None, activated: bool = False):
+              far: float = 100.0, sh_degree: int | None = None, activated: bool = False,
+              densification_info: torch.Tensor | None = None):
     """Renders one view. Returns (image [3, H, W], alpha [H, W], aux).
 
     Parameters follow Faster-GS's raw convention unless `activated=True`:
@@ -308,7 +324,9 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
       as two parameters; viewmat [4,4] world-to-camera (OpenCV axes); K [3,3] intrinsics.
     aux: {"tiles_touched": [N] int32 (> 0 = visible; the visibility mask for a sparse optimizer),
           "n_visible", "n_instances", "n_buckets"}.
-    Gradients flow to means, scales, quats, opacities and sh.
+    Gradients flow to means, scales, quats, opacities and sh. densification_info [2 or 3, N]
+    float32 (optional, as the first argument of Faster-GS's backward): the backward adds this view's
+    statistics to it (see densification_stats).
     """
     if opacities.dim() == 2:
         opacities = opacities.reshape(-1)
@@ -320,7 +338,8 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
         bg = (0.0, 0.0, 0.0)
     bg = tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
     sh_a, sh_b = sh if isinstance(sh, (tuple, list)) else (sh, None)
-    image, alpha, touched = _Rasterize3D.apply(means, scales, quats, opacities, sh_a, sh_b, cam, sh_degree, bg)
+    image, alpha, touched = _Rasterize3D.apply(means, scales, quats, opacities, sh_a, sh_b, cam, sh_degree, bg,
+                                               densification_info)
     aux = {"tiles_touched": touched}
     aux["n_visible"] = lambda: int((touched > 0).sum().item())
     return image, alpha, aux

@@ -688,3 +688,37 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
   }
   return check_launch("preprocess_bwd");
 }
+
+// ---------------------------------------------------------------------------------------
+// Densification statistics
+// ---------------------------------------------------------------------------------------
+namespace gs {
+
+__global__ void densification_stats_kernel(const float* __restrict__ grad2d, const uint32_t* __restrict__ touched,
+                                           int64_t n, float sx, float sy, int rows, float* __restrict__ info) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n || touched[i] == 0u) return;
+  const float* g = grad2d + i * kGrad2D;
+  const float gx = g[0] * sx, gy = g[1] * sy;
+  info[i] += 1.0f;
+  info[n + i] += sqrtf(fmaf(gx, gx, gy * gy));
+  if (rows > 2) {
+    const float ax = g[9] * sx, ay = g[10] * sy;
+    info[2 * n + i] += sqrtf(fmaf(ax, ax, ay * ay));
+  }
+}
+
+}  // namespace gs
+
+extern "C" int gs_densification_stats(const float* grad2d, const uint32_t* tiles_touched, int64_t n, int width,
+                                      int height, int rows, float* info, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0 && width > 0 && height > 0 && (rows == 2 || rows == 3), GS_ERR_ARG,
+             "invalid densification_stats arguments");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(grad2d && tiles_touched && info, GS_ERR_ARG, "null pointer argument");
+  hipLaunchKernelGGL(densification_stats_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), grad2d, tiles_touched, n, 0.5f * static_cast<float>(width),
+                     0.5f * static_cast<float>(height), rows, info);
+  return check_launch("densification_stats");
+}

@@ -189,6 +189,15 @@ int gs_preprocess_bwd(const float* means, const float* log_scales, const float* 
                       float* grad_log_scales, float* grad_quats, float* grad_opacity_logits,
                       float* grad_sh, float* grad_sh_rest, void* stream);
 
+/* Densification statistics of one backward, accumulated into info [rows, n] (rows 2 or 3) for
+ * the visible Gaussians (tiles_touched > 0): info[0] += 1; info[1] += |(W/2 g_x, H/2 g_y)|, the
+ * norm of the mean2d gradient in NDC units (grad2d[:, 0:2]); info[2] (rows == 3) += the same
+ * norm of the summed per-pixel |dL/dmean2d| (grad2d[:, 9:11]). The densification_info rows of
+ * Faster-GS's backward (phase1/tests/test_parity.py:93-106, fastergs_macro.patch:59,206-209);
+ * the NDC scaling is the one of the original 3DGS rasterizer's mean2D gradient. */
+int gs_densification_stats(const float* grad2d, const uint32_t* tiles_touched, int64_t n, int width,
+                           int height, int rows, float* info, void* stream);
+
 /* =======================================================================================
  * 2D surfaces (rules GS_RULES_TOY2D / GS_RULES_PHASE0; dtype GS_FLOAT32 / GS_FLOAT64)
  * ===================================================================================== */

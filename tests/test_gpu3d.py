@@ -314,3 +314,30 @@ def test_split_sh_layout_equals_single_tensor(K):
     for a, b in zip(ga[:4], gb[:4]):
         assert rel(a, b) < 1e-5
     assert rel(gb[4][0], ga[4][:, :1]) < 1e-5 and rel(gb[4][1], ga[4][:, 1:]) < 1e-5
+
+
+@pytest.mark.parametrize("rows", [2, 3])
+def test_densification_info_accumulates_ndc_gradient_norms(rows):
+    sc = make("partial_tiles", seed=9)
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous().requires_grad_(True) for t in sc.params()]
+    K = torch.tensor([[cam.fx, 0.0, cam.cx], [0.0, cam.fy, cam.cy], [0.0, 0.0, 1.0]])
+    info = torch.zeros(rows, sc.n, device="cuda")
+    expect = torch.zeros(rows, sc.n, dtype=torch.float64)
+    for k in range(2):
+        img, alpha, aux = R.rasterize(*p, cam.viewmat, K, cam.width, cam.height, near=cam.near, far=cam.far,
+                                      densification_info=info)
+        gi = torch.randn(img.shape, generator=torch.Generator().manual_seed(k)).cuda()
+        (img * gi).sum().backward()
+        fs = R.forward_pass(*[t.detach() for t in p], cam)
+        g2 = R.backward_pass(fs, *[t.detach() for t in p], gi)[5].double().cpu()
+        vis = (aux["tiles_touched"] > 0).cpu()
+        sx, sy = 0.5 * cam.width, 0.5 * cam.height
+        expect[0] += vis.double()
+        expect[1] += torch.where(vis, torch.hypot(g2[:, 0] * sx, g2[:, 1] * sy), 0.0)
+        if rows == 3:
+            expect[2] += torch.where(vis, torch.hypot(g2[:, 9] * sx, g2[:, 10] * sy), 0.0)
+    got = info.double().cpu()
+    assert torch.equal(got[0], expect[0])
+    for r in range(1, rows):
+        assert float((got[r] - expect[r]).norm() / expect[r].norm()) < 1e-5  # atomics: order differs
