@@ -6,7 +6,8 @@ drop-in surfaces live in the sibling packages `gs2d` and `splat2d`.
 """
 from .adam import FusedAdam, adam_step, adam_step_sparse
 from .loss import fused_ssim, l1_ssim_loss
-from .raster3d import Camera, backward_pass, densification_stats, forward_pass, rasterize
+from .raster3d import (Camera, backward_pass, densification_stats, forward_pass, pruning_scores, rasterize,
+                       rasterize_inference)
 
-__all__ = ["Camera", "rasterize", "forward_pass", "backward_pass", "densification_stats", "FusedAdam", "adam_step", "adam_step_sparse",
+__all__ = ["Camera", "rasterize", "rasterize_inference", "pruning_scores", "forward_pass", "backward_pass", "densification_stats", "FusedAdam", "adam_step", "adam_step_sparse",
            "l1_ssim_loss", "fused_ssim"]

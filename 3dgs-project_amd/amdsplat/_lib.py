@@ -29,11 +29,13 @@ class GsCamera(C.Structure):
         ("height", C.c_int32),
         ("near_plane", C.c_float),
         ("far_plane", C.c_float),
+        ("flags", C.c_int32),
     ]
 
 
 GS_ACCUMULATE = 1  # gs_blend_bwd_3d flag: add to grad2d instead of zeroing it first
 GS_FLOAT32, GS_FLOAT64, GS_BFLOAT16 = 0, 1, 2
+GS_CAM_PROPER_ANTIALIASING = 1  # gs_camera.flags bit
 GS_ADAM_MAX_GROUPS = 8
 
 
@@ -76,6 +78,7 @@ _SIGS = {
                                 _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs_blend_scores_3d": (_i32, [_vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _vp, _i32, _vp, _vp]),
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
@@ -161,7 +164,7 @@ def float3(v) -> C.Array:
 
 
 def make_camera(viewmat, fx: float, fy: float, cx: float, cy: float, width: int, height: int,
-                near: float, far: float) -> GsCamera:
+                near: float, far: float, flags: int = 0) -> GsCamera:
     cam = GsCamera()
     flat = [float(x) for x in viewmat.reshape(-1).tolist()] if hasattr(viewmat, "reshape") else \
         [float(x) for row in viewmat for x in row]
@@ -172,6 +175,7 @@ def make_camera(viewmat, fx: float, fy: float, cx: float, cy: float, width: int,
     cam.fx, cam.fy, cam.cx, cam.cy = float(fx), float(fy), float(cx), float(cy)
     cam.width, cam.height = int(width), int(height)
     cam.near_plane, cam.far_plane = float(near), float(far)
+    cam.flags = int(flags)
     return cam
 
 

@@ -47,13 +47,15 @@ class Camera:
     height: int
     near: float = 0.01
     far: float = 100.0
+    proper_antialiasing: bool = False
 
     @staticmethod
-    def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0) -> "Camera":
+    def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0,
+               proper_antialiasing: bool = False) -> "Camera":
         K = torch.as_tensor(K, dtype=torch.float64).cpu()
         vm = torch.as_tensor(viewmat, dtype=torch.float32).detach().cpu().reshape(4, 4)
         return Camera(vm, float(K[0, 0]), float(K[1, 1]), float(K[0, 2]), float(K[1, 2]), int(width),
-                      int(height), float(near), float(far))
+                      int(height), float(near), float(far), bool(proper_antialiasing))
 
     @property
     def tiles_x(self) -> int:
@@ -69,7 +71,8 @@ class Camera:
 
     def c_struct(self) -> _lib.GsCamera:
         return _lib.make_camera(self.viewmat.detach().cpu().float(), self.fx, self.fy, self.cx, self.cy,
-                                self.width, self.height, self.near, self.far)
+                                self.width, self.height, self.near, self.far,
+                                _lib.GS_CAM_PROPER_ANTIALIASING if self.proper_antialiasing else 0)
 
 
 @dataclass
@@ -90,12 +93,12 @@ class ForwardState:
     ranges: torch.Tensor         # [T, 2] int32
     bucket_offsets: torch.Tensor  # [T + 1] int32
     n_buckets_max: int
-    bucket_to_tile: torch.Tensor  # [n_buckets_max] int32
-    image: torch.Tensor          # [3, H, W]
-    final_T: torch.Tensor        # [H, W]
-    n_contrib: torch.Tensor      # [H, W] int32
-    tile_max: torch.Tensor       # [T] int32
-    ckpt: torch.Tensor           # [n_buckets_max, 256, 4]
+    bucket_to_tile: torch.Tensor | None  # [n_buckets_max] int32 (None: inference)
+    image: torch.Tensor | None   # [3, H, W]
+    final_T: torch.Tensor | None  # [H, W]
+    n_contrib: torch.Tensor | None  # [H, W] int32 (None: inference)
+    tile_max: torch.Tensor | None  # [T] int32 (None: inference)
+    ckpt: torch.Tensor | None    # [n_buckets_max, 256, 4] (None: inference)
     bg: tuple = (0.0, 0.0, 0.0)
     timings: dict = field(default_factory=dict)
 
@@ -164,9 +167,11 @@ def _sh_parts(sh):
 
 
 def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_degree: int | None = None,
-                 bg=(0.0, 0.0, 0.0), timing: bool = False, keep_keys: bool = False) -> ForwardState:
+                 bg=(0.0, 0.0, 0.0), timing: bool = False, keep_keys: bool = False,
+                 for_backward: bool = True, _scores: torch.Tensor | None = None) -> ForwardState:
     """Runs the forward stages; inputs are contiguous float32 CUDA tensors (raw parameters). sh is
-    [N, K, 3] or the (DC [N, 1, 3], rest [N, K - 1, 3]) pair."""
+    [N, K, 3] or the (DC [N, 1, 3], rest [N, K - 1, 3]) pair. for_backward=False is the inference
+    blend: no bucket table, checkpoints or n_contrib (those fields are None), same image bits."""
     means, log_scales, quats = means.contiguous(), log_scales.contiguous(), quats.contiguous()
     opacity_logits = opacity_logits.contiguous()
     sh_a, sh_b, K = _sh_parts(sh)
@@ -204,14 +209,22 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
          ptr(keys) if keep_keys else None, ptr(point_list), ptr(ranges), ptr(bucket_offsets), ptr(ws), ws.numel(),
          st)
     tm.mark("binning")
-    nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
-    bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
-    call("gs_bucket_fill", ptr(bucket_offsets), T, ptr(bucket_to_tile), nb_max, st)
+    if _scores is not None:  # pruning scores: the blend's weights, no image
+        call("gs_blend_scores_3d", ptr(rec), ptr(ranges), ptr(point_list), W, H, n, ptr(_scores), st)
+        tm.mark("scores")
+        return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges,
+                            bucket_offsets, 0, None, None, None, None, None, None, tuple(bg),
+                            {} if isinstance(timing, StageTimer) else tm.result())
+    nb_max, bucket_to_tile, n_contrib, tile_max, ckpt = 0, None, None, None, None
+    if for_backward:
+        nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
+        bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
+        call("gs_bucket_fill", ptr(bucket_offsets), T, ptr(bucket_to_tile), nb_max, st)
+        n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
+        tile_max = torch.empty(T, dtype=torch.int32, device=dev)
+        ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
     image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
     final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
-    n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
-    tile_max = torch.empty(T, dtype=torch.int32, device=dev)
-    ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
     tm.mark("buckets")
     call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
          ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), st)
@@ -314,7 +327,7 @@ class _Rasterize3D(torch.autograd.Function):
 
 def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None, near: float = 0.01,
               far: float = 100.0, sh_degree: int | None = None, activated: bool = False,
-              densification_info: torch.Tensor | None = None):
+              densification_info: torch.Tensor | None = None, proper_antialiasing: bool = False):
     """Renders one view. Returns (image [3, H, W], alpha [H, W], aux).
 
     Parameters follow Faster-GS's raw convention unless `activated=True`:
@@ -326,14 +339,12 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
           "n_visible", "n_instances", "n_buckets"}.
     Gradients flow to means, scales, quats, opacities and sh. densification_info [2 or 3, N]
     float32 (optional, as the first argument of Faster-GS's backward): the backward adds this view's
-    statistics to it (see densification_stats).
+    statistics to it (see densification_stats). proper_antialiasing: Faster-GS's setting of that
+    name -- each splat's opacity is scaled by sqrt(det S / det(S + 0.3 I)) so that the 0.3 px^2
+    low-pass does not add energy (S the projected 2D covariance); gradients include the factor.
     """
-    if opacities.dim() == 2:
-        opacities = opacities.reshape(-1)
-    if activated:
-        scales = torch.log(scales)
-        opacities = torch.logit(opacities)
-    cam = Camera.from_K(viewmat, K, W, H, near, far)
+    means, scales, quats, opacities, _ = _prepare(means, scales, quats, opacities, sh, activated)
+    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing)
     if bg is None:
         bg = (0.0, 0.0, 0.0)
     bg = tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
@@ -343,3 +354,50 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
     aux = {"tiles_touched": touched}
     aux["n_visible"] = lambda: int((touched > 0).sum().item())
     return image, alpha, aux
+
+
+def _prepare(means, scales, quats, opacities, sh, activated):
+    if opacities.dim() == 2:
+        opacities = opacities.reshape(-1)
+    if activated:
+        scales = torch.log(scales)
+        opacities = torch.logit(opacities)
+    return means, scales, quats, opacities, tuple(sh) if isinstance(sh, (tuple, list)) else sh
+
+
+@torch.no_grad()
+def rasterize_inference(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None,
+                        near: float = 0.01, far: float = 100.0, sh_degree: int | None = None,
+                        activated: bool = False, proper_antialiasing: bool = False):
+    """Forward only, for evaluation and viewers (Faster-GS's inference blend,
+    upstream/upstream_main_kernels.patch:131-150): returns (image [3, H, W], alpha [H, W]), the
+    same bits as rasterize, without the backward's bucket table, checkpoints or autograd state."""
+    means, scales, quats, opacities, sh = _prepare(means, scales, quats, opacities, sh, activated)
+    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing)
+    bg = (0.0, 0.0, 0.0) if bg is None else tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
+    fs = forward_pass(means.detach(), scales.detach(), quats.detach(), opacities.detach(),
+                      tuple(t.detach() for t in sh) if isinstance(sh, tuple) else sh.detach(), cam,
+                      sh_degree=sh_degree, bg=bg, for_backward=False)
+    return fs.image, 1.0 - fs.final_T
+
+
+@torch.no_grad()
+def pruning_scores(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, near: float = 0.01,
+                   far: float = 100.0, sh_degree: int | None = None, activated: bool = False,
+                   proper_antialiasing: bool = False, scores: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-Gaussian contribution of one view (the role of Faster-GS's pruning-score blend,
+    upstream/upstream_main_kernels.patch:152-198): scores[g] += sum over the pixels g is blended
+    into of its blending weight alpha * T, under the forward's rules. Pass the same `scores`
+    ([N] float32 CUDA) for every view to accumulate over a set of views; returns it."""
+    means, scales, quats, opacities, sh = _prepare(means, scales, quats, opacities, sh, activated)
+    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing)
+    n = means.shape[0]
+    if scores is None:
+        scores = torch.zeros(n, dtype=torch.float32, device=means.device)
+    if tuple(scores.shape) != (n,) or scores.dtype != torch.float32 or not scores.is_contiguous() \
+            or scores.device != means.device:
+        raise ValueError(f"scores must be a contiguous float32 [{n}] tensor on {means.device}")
+    forward_pass(means.detach(), scales.detach(), quats.detach(), opacities.detach(),
+                 tuple(t.detach() for t in sh) if isinstance(sh, tuple) else sh.detach(), cam,
+                 sh_degree=sh_degree, _scores=scores)
+    return scores

@@ -54,6 +54,8 @@ struct BlendArgs {
   const S* grad_image;
   const S* grad_alpha;  // 3D: gradient of alpha = 1 - final_T (may be null)
   S* grad_rec;          // [n, 12]
+  // pruning scores (3D): scores[g] += sum over pixels of the blending weight alpha T of g
+  float* scores;
 };
 
 // Per-wavefront counter increment (one atomic per wavefront).
@@ -61,141 +63,6 @@ __device__ __forceinline__ void count_add(unsigned long long* c, uint32_t v) {
   uint32_t s = v;
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
   if ((threadIdx.x & 63) == 0 && s) atomicAdd(c, static_cast<unsigned long long>(s));
-}
-
-// ---------------------------------------------------------------------------------------
-// Forward
-// ---------------------------------------------------------------------------------------
-template <int R, typename S, bool kCount>
-__global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) {
-  using Ru = Rule<R, S>;
-  __shared__ Staged<S> s_sp[kTilePixels];
-  __shared__ uint32_t s_mask[Ru::kStrips ? kTilePixels : 1];
-  __shared__ uint32_t s_max;
-
-  const int tile = blockIdx.x;
-  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int wave = t >> 6;
-  const int px = tx * kTile + (t & 15), py = ty * kTile + (t >> 4);
-  const bool inside = px < a.W && py < a.H;
-  const S pxf = static_cast<S>(px) + Ru::pix_off(), pyf = static_cast<S>(py) + Ru::pix_off();
-  const uint32_t r0 = a.ranges[static_cast<int64_t>(tile) * a.range_stride];
-  const uint32_t r1 = a.ranges[static_cast<int64_t>(tile) * a.range_stride + 1];
-  const int len = static_cast<int>(r1 - r0);
-  S* ck = a.ckpt ? a.ckpt + (static_cast<int64_t>(a.bucket_offsets[tile]) * kTilePixels + t) * 4 : nullptr;
-  if (t == 0) s_max = 0;
-
-  // 3D: a pixel has stopped exactly when T < 1e-4 (T only decreases; pixels outside the
-  // image start at T = 0), so no separate per-lane flag is kept
-  constexpr bool kStopByT = R == kRules3D;
-  S T = (kStopByT && !inside) ? S(0) : S(1), Cr = S(0), Cg = S(0), Cb = S(0);
-  int last = 0, count = 0;
-  uint32_t evals = 0;
-  bool done = !inside;
-  int covered = len;  // list positions whose bucket checkpoints the loop wrote
-  for (int b0 = 0; b0 < len; b0 += kTilePixels) {
-    if (__syncthreads_count((kStopByT ? T < Ru::t_stop() : done) ? 1 : 0) == kTilePixels) {
-      covered = b0;
-      break;
-    }
-    const int j = b0 + t;
-    if (j < len) {
-      const uint32_t g = a.point_list[r0 + j];
-      const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
-      s_sp[t] = Ru::stage(rp);
-      if constexpr (Ru::kStrips) s_mask[t] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
-    }
-    __syncthreads();
-    const int nb = min(kTilePixels, len - b0);
-    // this wavefront's strip bit of every staged splat, as four 64-bit masks (3D)
-    uint64_t wm[4] = {~0ull, ~0ull, ~0ull, ~0ull};
-    if constexpr (Ru::kStrips) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int jj = 64 * q + lane;
-        wm[q] = __ballot((jj < nb && ((s_mask[jj] >> wave) & 1u)) ? 1 : 0);
-      }
-    }
-    // one 32-entry bucket at a time: its checkpoint, then its splats
-    for (int c0 = 0; c0 < nb; c0 += kBucket) {
-      if (ck) {
-        S* c = ck + static_cast<int64_t>((b0 + c0) / kBucket) * kTilePixels * 4;
-        if constexpr (Ru::kCkptTFirst) {
-          c[0] = T; c[1] = Cr; c[2] = Cg; c[3] = Cb;
-        } else {
-          c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
-        }
-      }
-      if (__ballot((kStopByT ? T < Ru::t_stop() : done) ? 0 : 1) == 0ull) continue;  // all lanes stopped
-      const int c1 = min(c0 + kBucket, nb);
-      const uint64_t qm = (c0 < 64) ? wm[0] : (c0 < 128) ? wm[1] : (c0 < 192) ? wm[2] : wm[3];
-      uint32_t cm = static_cast<uint32_t>(qm >> (c0 & 63));
-      if (c1 - c0 < kBucket) cm &= (1u << (c1 - c0)) - 1u;
-      // wave-uniform loop over the splats whose bounds reach this wavefront's rows; the body
-      // has no lane branches (a lane that has stopped or rejects the splat composites nothing),
-      // so the scalar unit only runs the loop control
-      while (cm != 0u) {
-        const int jj = c0 + __builtin_ctz(cm);
-        cm &= cm - 1u;
-        const Staged<S> sp = s_sp[jj];
-        Eval<S> e;
-        const bool live = kStopByT ? T >= Ru::t_stop() : !done;
-        if constexpr (kCount) evals += live ? 1u : 0u;
-        bool take = Ru::eval(sp, pxf, pyf, e) && live;
-        if constexpr (Ru::kStopBefore) {
-          const bool stop = take && T * (S(1) - e.alpha) < Ru::t_stop();
-          done = done || stop;
-          take = take && !stop;
-        }
-        if constexpr (R == kRules3D) {
-          // alpha 0 leaves C and T bit-identical (the colours of the records are finite)
-          composite<R, S>(Cr, Cg, Cb, T, sp, take ? e.alpha : S(0));
-        } else {
-          S r = Cr, g = Cg, b = Cb, t = T;
-          composite<R, S>(r, g, b, t, sp, e.alpha);
-          Cr = take ? r : Cr;
-          Cg = take ? g : Cg;
-          Cb = take ? b : Cb;
-          T = take ? t : T;
-        }
-        count += take ? 1 : 0;
-        last = take ? b0 + jj + 1 : last;
-        if constexpr (!Ru::kStopBefore && !kStopByT) done = done || T < Ru::t_stop();
-      }
-    }
-  }
-  if constexpr (kCount) count_add(a.counters + 2, evals);
-  if constexpr (R == kRulesPhase0) {
-    // phase0 writes every checkpoint slot: buckets after the workgroup stopped keep the
-    // final state (phase0/csrc/macrotile/bindings.cpp:167-169)
-    if (ck) {
-      for (int q = (covered + kBucket - 1) / kBucket; q < (len + kBucket - 1) / kBucket; ++q) {
-        S* c = ck + static_cast<int64_t>(q) * kTilePixels * 4;
-        c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
-      }
-    }
-  }
-  if (inside) {
-    const int64_t pix = static_cast<int64_t>(py) * a.W + px;
-    if constexpr (Ru::kInterleaved) {
-      a.image[3 * pix] = Cr;
-      a.image[3 * pix + 1] = Cg;
-      a.image[3 * pix + 2] = Cb;
-    } else {
-      const int64_t HW = static_cast<int64_t>(a.H) * a.W;
-      a.image[pix] = fma(T, a.bg0, Cr);
-      a.image[HW + pix] = fma(T, a.bg1, Cg);
-      a.image[2 * HW + pix] = fma(T, a.bg2, Cb);
-    }
-    a.final_T[pix] = T;
-    a.n_contrib[pix] = Ru::kCountContrib ? count : last;
-    if (a.last_contrib) a.last_contrib[pix] = last;
-    if (last > 0) atomicMax(&s_max, static_cast<uint32_t>(last));
-  }
-  __syncthreads();
-  if (t == 0 && a.tile_max) a.tile_max[tile] = s_max;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -239,6 +106,163 @@ __device__ __forceinline__ float opaque_zero() {
 
 __device__ __forceinline__ void atomic_add_grad(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAtomicAdd(p, v); }
+
+// ---------------------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------------------
+// kScore: instead of the image, accumulate every splat's blending weights alpha T over the
+// tile's pixels into a.scores (a wavefront sum per splat into LDS, one global atomic per
+// staged splat and tile); the blend itself is the forward's, decision for decision.
+template <int R, typename S, bool kCount, bool kScore = false>
+__global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) {
+  using Ru = Rule<R, S>;
+  static_assert(!kScore || (R == kRules3D && std::is_same<S, float>::value), "scores: 3D float only");
+  __shared__ Staged<S> s_sp[kTilePixels];
+  __shared__ uint32_t s_mask[Ru::kStrips ? kTilePixels : 1];
+  __shared__ uint32_t s_max;
+  __shared__ float s_score[kScore ? kTilePixels : 1];
+  __shared__ uint32_t s_gid[kScore ? kTilePixels : 1];
+
+  const int tile = blockIdx.x;
+  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int px = tx * kTile + (t & 15), py = ty * kTile + (t >> 4);
+  const bool inside = px < a.W && py < a.H;
+  const S pxf = static_cast<S>(px) + Ru::pix_off(), pyf = static_cast<S>(py) + Ru::pix_off();
+  const uint32_t r0 = a.ranges[static_cast<int64_t>(tile) * a.range_stride];
+  const uint32_t r1 = a.ranges[static_cast<int64_t>(tile) * a.range_stride + 1];
+  const int len = static_cast<int>(r1 - r0);
+  S* ck = a.ckpt ? a.ckpt + (static_cast<int64_t>(a.bucket_offsets[tile]) * kTilePixels + t) * 4 : nullptr;
+  if (t == 0) s_max = 0;
+
+  // 3D: a pixel has stopped exactly when T < 1e-4 (T only decreases; pixels outside the
+  // image start at T = 0), so no separate per-lane flag is kept
+  constexpr bool kStopByT = R == kRules3D;
+  S T = (kStopByT && !inside) ? S(0) : S(1), Cr = S(0), Cg = S(0), Cb = S(0);
+  int last = 0, count = 0;
+  uint32_t evals = 0;
+  bool done = !inside;
+  int covered = len;  // list positions whose bucket checkpoints the loop wrote
+  for (int b0 = 0; b0 < len; b0 += kTilePixels) {
+    if (__syncthreads_count((kStopByT ? T < Ru::t_stop() : done) ? 1 : 0) == kTilePixels) {
+      covered = b0;
+      break;
+    }
+    const int j = b0 + t;
+    if (j < len) {
+      const uint32_t g = a.point_list[r0 + j];
+      const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
+      s_sp[t] = Ru::stage(rp);
+      if constexpr (Ru::kStrips) s_mask[t] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
+      if constexpr (kScore) {
+        s_gid[t] = g;
+        s_score[t] = 0.0f;
+      }
+    }
+    __syncthreads();
+    const int nb = min(kTilePixels, len - b0);
+    // this wavefront's strip bit of every staged splat, as four 64-bit masks (3D)
+    uint64_t wm[4] = {~0ull, ~0ull, ~0ull, ~0ull};
+    if constexpr (Ru::kStrips) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int jj = 64 * q + lane;
+        wm[q] = __ballot((jj < nb && ((s_mask[jj] >> wave) & 1u)) ? 1 : 0);
+      }
+    }
+    // one 32-entry bucket at a time: its checkpoint, then its splats
+    for (int c0 = 0; c0 < nb; c0 += kBucket) {
+      if (ck) {
+        S* c = ck + static_cast<int64_t>((b0 + c0) / kBucket) * kTilePixels * 4;
+        if constexpr (Ru::kCkptTFirst) {
+          c[0] = T; c[1] = Cr; c[2] = Cg; c[3] = Cb;
+        } else {
+          c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
+        }
+      }
+      if (__ballot((kStopByT ? T < Ru::t_stop() : done) ? 0 : 1) == 0ull) continue;  // all lanes stopped
+      const int c1 = min(c0 + kBucket, nb);
+      const uint64_t qm = (c0 < 64) ? wm[0] : (c0 < 128) ? wm[1] : (c0 < 192) ? wm[2] : wm[3];
+      uint32_t cm = static_cast<uint32_t>(qm >> (c0 & 63));
+      if (c1 - c0 < kBucket) cm &= (1u << (c1 - c0)) - 1u;
+      // wave-uniform loop over the splats whose bounds reach this wavefront's rows; the body
+      // has no lane branches (a lane that has stopped or rejects the splat composites nothing),
+      // so the scalar unit only runs the loop control
+      while (cm != 0u) {
+        const int jj = c0 + __builtin_ctz(cm);
+        cm &= cm - 1u;
+        const Staged<S> sp = s_sp[jj];
+        Eval<S> e;
+        const bool live = kStopByT ? T >= Ru::t_stop() : !done;
+        if constexpr (kCount) evals += live ? 1u : 0u;
+        bool take = Ru::eval(sp, pxf, pyf, e) && live;
+        if constexpr (Ru::kStopBefore) {
+          const bool stop = take && T * (S(1) - e.alpha) < Ru::t_stop();
+          done = done || stop;
+          take = take && !stop;
+        }
+        if constexpr (kScore) {
+          if (__ballot(take ? 1 : 0) != 0ull) {
+            const float w = wave_sum(take ? e.alpha * T : 0.0f);
+            if (lane == 0) atomicAdd(&s_score[jj], w);
+          }
+        }
+        if constexpr (R == kRules3D) {
+          // alpha 0 leaves C and T bit-identical (the colours of the records are finite)
+          composite<R, S>(Cr, Cg, Cb, T, sp, take ? e.alpha : S(0));
+        } else {
+          S r = Cr, g = Cg, b = Cb, t = T;
+          composite<R, S>(r, g, b, t, sp, e.alpha);
+          Cr = take ? r : Cr;
+          Cg = take ? g : Cg;
+          Cb = take ? b : Cb;
+          T = take ? t : T;
+        }
+        count += take ? 1 : 0;
+        last = take ? b0 + jj + 1 : last;
+        if constexpr (!Ru::kStopBefore && !kStopByT) done = done || T < Ru::t_stop();
+      }
+    }
+    if constexpr (kScore) {
+      __syncthreads();  // every wavefront's sums are in
+      if (t < nb && s_score[t] != 0.0f) unsafeAtomicAdd(a.scores + s_gid[t], s_score[t]);
+    }
+  }
+  if constexpr (kCount) count_add(a.counters + 2, evals);
+  if constexpr (kScore) return;
+  if constexpr (R == kRulesPhase0) {
+    // phase0 writes every checkpoint slot: buckets after the workgroup stopped keep the
+    // final state (phase0/csrc/macrotile/bindings.cpp:167-169)
+    if (ck) {
+      for (int q = (covered + kBucket - 1) / kBucket; q < (len + kBucket - 1) / kBucket; ++q) {
+        S* c = ck + static_cast<int64_t>(q) * kTilePixels * 4;
+        c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
+      }
+    }
+  }
+  if (inside) {
+    const int64_t pix = static_cast<int64_t>(py) * a.W + px;
+    if constexpr (Ru::kInterleaved) {
+      a.image[3 * pix] = Cr;
+      a.image[3 * pix + 1] = Cg;
+      a.image[3 * pix + 2] = Cb;
+    } else {
+      const int64_t HW = static_cast<int64_t>(a.H) * a.W;
+      a.image[pix] = fma(T, a.bg0, Cr);
+      a.image[HW + pix] = fma(T, a.bg1, Cg);
+      a.image[2 * HW + pix] = fma(T, a.bg2, Cb);
+    }
+    a.final_T[pix] = T;
+    if (a.n_contrib) a.n_contrib[pix] = Ru::kCountContrib ? count : last;
+    if (a.last_contrib) a.last_contrib[pix] = last;
+    if (last > 0) atomicMax(&s_max, static_cast<uint32_t>(last));
+  }
+  __syncthreads();
+  if (t == 0 && a.tile_max) a.tile_max[tile] = s_max;
+}
+
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -730,8 +754,9 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
                                float* ckpt, void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARG, "image size must be positive");
-  // splat_rec, point_list and ckpt may be NULL when the scene has no instances
-  GS_REQUIRE(ranges && bucket_offsets && image && final_T && n_contrib && tile_max, GS_ERR_ARG,
+  // splat_rec, point_list and ckpt may be NULL when the scene has no instances; without ckpt
+  // (inference) bucket_offsets, n_contrib and tile_max may be NULL as well
+  GS_REQUIRE(ranges && image && final_T && (!ckpt || (bucket_offsets && n_contrib && tile_max)), GS_ERR_ARG,
              "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16) && aligned(ckpt, 16), GS_ERR_ALIGN,
              "splat_rec and ckpt must be 16-byte aligned");
@@ -744,6 +769,21 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
   a.ckpt = ckpt;
   launch_fwd<kRules3D, float>(a, as_stream(stream));
   return check_launch("blend_fwd_3d");
+}
+
+extern "C" int gs_blend_scores_3d(const float* splat_rec, const uint32_t* ranges,
+                                  const uint32_t* point_list, int width, int height, int64_t n,
+                                  float* scores, void* stream) {
+  clear_error();
+  GS_REQUIRE(width > 0 && height > 0 && n >= 0, GS_ERR_ARG, "invalid sizes");
+  GS_REQUIRE(ranges && (scores || n == 0), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
+  const double bgd[3] = {0.0, 0.0, 0.0};
+  BlendArgs<float> a = make_args<float>(splat_rec, ranges, 2, point_list, nullptr, width, height, bgd);
+  a.scores = scores;
+  hipLaunchKernelGGL((blend_fwd_kernel<kRules3D, float, false, true>), dim3(a.n_tiles), dim3(kTilePixels), 0,
+                     as_stream(stream), a);
+  return check_launch("blend_scores_3d");
 }
 
 extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,

@@ -18,6 +18,7 @@ struct CamK {
   float campos[3];       // camera centre in world space
   float lim_x_lo, lim_x_hi, lim_y_lo, lim_y_hi;  // clamp of x/z and y/z for the EWA Jacobian
   int tiles_x, tiles_y;
+  int flags;  // GS_CAM_* bits
 };
 
 // Tile assignment. A tile row is a horizontal band of pixel-centre rows [Y0, Y1] (the

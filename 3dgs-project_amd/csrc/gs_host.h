@@ -51,6 +51,7 @@ inline CamK make_cam(const gs_camera& c) {
   k.height = c.height;
   k.znear = c.near_plane;
   k.zfar = c.far_plane;
+  k.flags = c.flags;
   for (int j = 0; j < 3; ++j) {
     double s = 0.0;
     for (int i = 0; i < 3; ++i) s -= static_cast<double>(c.viewmat[4 * i + j]) * c.viewmat[4 * i + 3];

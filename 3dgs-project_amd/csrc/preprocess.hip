@@ -176,7 +176,9 @@ __device__ __forceinline__ void unstage_sh(ShOut dst, int64_t first, int rows, i
 struct Geom {
   bool vis;
   float vx, vy, vz, iz, tx, ty, txc, tyc;
-  float o;
+  float o;                     // blended opacity (sigmoid, times rho under proper antialiasing)
+  float os;                    // sigmoid of the opacity logit
+  float rho, ratio;            // antialiasing compensation sqrt(ratio), ratio = det raw / det
   float qw, qx, qy, qz, qinv;  // normalised quaternion and 1/|q|
   float R[9];                  // rotation of the Gaussian
   float s[3];                  // scales
@@ -184,6 +186,7 @@ struct Geom {
   float S[6];                  // 3D covariance (00 01 02 11 12 22)
   float T[6];                  // J W, 2x3
   float a, b, c;               // 2D covariance incl. dilation
+  float ar, cr;                // diagonal of the 2D covariance without dilation
   float det, A, B, C;          // conic
   float mx, my;                // mean2d
 };
@@ -257,11 +260,24 @@ __device__ __forceinline__ void compute_geom(const float* __restrict__ means,
   const float u10 = fmaf(T[3], S[0], fmaf(T[4], S[1], T[5] * S[2]));
   const float u11 = fmaf(T[3], S[1], fmaf(T[4], S[3], T[5] * S[4]));
   const float u12 = fmaf(T[3], S[2], fmaf(T[4], S[4], T[5] * S[5]));
-  g.a = fmaf(u00, T[0], fmaf(u01, T[1], u02 * T[2])) + kDilation;
+  g.ar = fmaf(u00, T[0], fmaf(u01, T[1], u02 * T[2]));
   g.b = fmaf(u00, T[3], fmaf(u01, T[4], u02 * T[5]));
-  g.c = fmaf(u10, T[3], fmaf(u11, T[4], u12 * T[5])) + kDilation;
+  g.cr = fmaf(u10, T[3], fmaf(u11, T[4], u12 * T[5]));
+  g.a = g.ar + kDilation;
+  g.c = g.cr + kDilation;
   g.det = fmaf(g.a, g.c, -(g.b * g.b));
   vis = vis && (g.det > 0.0f);
+  g.os = g.o;
+  g.rho = 1.0f;
+  g.ratio = 1.0f;
+  if (cam.flags & GS_CAM_PROPER_ANTIALIASING) {
+    // opacity compensation of the 0.3 px^2 low-pass: o sqrt(det(S) / det(S + 0.3 I))
+    const float det_raw = fmaf(g.ar, g.cr, -(g.b * g.b));
+    g.ratio = fmaxf(det_raw / g.det, 0.0f);
+    g.rho = sqrtf(g.ratio);
+    g.o = g.os * g.rho;
+    vis = vis && (g.o >= kAlphaMin);
+  }
   const float idet = 1.0f / g.det;
   g.A = g.c * idet;
   g.B = -g.b * idet;
@@ -490,6 +506,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void p
     Geom g;
     compute_geom(means, log_scales, quats, opacity_logits, i, cam, g);
     gop = g2[5] * g.o * (1.0f - g.o);
+    const bool aa = cam.flags & GS_CAM_PROPER_ANTIALIASING;
+    if (aa) gop = ((g2[5] * g.rho) * g.os) * (1.0f - g.os);
 
     // mean2d = (fx vx/vz + cx, fy vy/vz + cy)
     float gvx = g2[0] * cam.fx * g.iz;
@@ -500,9 +518,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void p
     const float gA = g2[2], gB = g2[3], gC = g2[4];
     const float a = g.a, b = g.b, c = g.c;
     const float id2 = 1.0f / (g.det * g.det);
-    const float ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
-    const float gbb = (2.0f * b * c * gA - (a * c + b * b) * gB + 2.0f * a * b * gC) * id2;
-    const float gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
+    float ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
+    float gbb = (2.0f * b * c * gA - (a * c + b * b) * gB + 2.0f * a * b * gC) * id2;
+    float gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
+    if (aa) {
+      // rho^2 = (ar cr - b^2) / (a c - b^2), a = ar + 0.3, c = cr + 0.3:
+      // d rho = d(rho^2) / (2 rho), d(rho^2)/da = (cr - rho^2 c) / det,
+      // d(rho^2)/dc = (ar - rho^2 a) / det, d(rho^2)/db = -2 b (1 - rho^2) / det
+      const float k = (g2[5] * g.os) / (2.0f * g.rho * g.det);
+      ga += k * (g.cr - g.ratio * c);
+      gc += k * (g.ar - g.ratio * a);
+      gbb += -2.0f * k * b * (1.0f - g.ratio);
+    }
     // cov2d = T S T^T (+ dilation); Gc = [[ga, gbb/2], [gbb/2, gc]]
     const float Gc00 = ga, Gc01 = 0.5f * gbb, Gc11 = gc;
     const float* T = g.T;

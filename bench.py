@@ -13,7 +13,8 @@ inside the timed region; `roofline` is for the kernel with the largest share of 
 (the bucketed blend backward), from its algorithmic bytes and its event-timed duration, plus
 its VALU issue rate from the committed SQ counter summary. `train_step` (secondary) times the
 full training step on the same scene: forward, L1 + D-SSIM loss, backward and fused Adam
-(dense and visibility-masked), with the optimizer's HBM rate.
+(dense and visibility-masked), with the optimizer's HBM rate; `variants` the inference forward,
+the pruning-score blend and fwd+bwd under proper antialiasing, per view.
 """
 from __future__ import annotations
 
@@ -216,6 +217,49 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
     return out
 
 
+def variants_bench(sc, grads, steps: int, warmup: int) -> dict:
+    """ms per view of the path's variants on the same scene and poses: the inference forward (no
+    backward state), the pruning-score blend (preprocess, binning, summed blending weights) and
+    fwd+bwd under proper antialiasing."""
+    import dataclasses
+
+    import torch
+
+    from amdsplat import raster3d as R
+
+    params = sc.params()
+    cams = sc.cameras
+    Ks = [torch.tensor([[c.fx, 0.0, c.cx], [0.0, c.fy, c.cy], [0.0, 0.0, 1.0]]) for c in cams]
+    scores = torch.zeros(params[0].shape[0], dtype=torch.float32, device="cuda")
+    aa_cams = [dataclasses.replace(c, proper_antialiasing=True) for c in cams]
+
+    def inference(k):
+        c = cams[k % len(cams)]
+        R.rasterize_inference(*params, c.viewmat, Ks[k % len(cams)], c.width, c.height, near=c.near, far=c.far)
+
+    def pruning(k):
+        c = cams[k % len(cams)]
+        R.pruning_scores(*params, c.viewmat, Ks[k % len(cams)], c.width, c.height, near=c.near, far=c.far,
+                         scores=scores)
+
+    def aa_fwd_bwd(k):
+        fs = R.forward_pass(*params, aa_cams[k % len(cams)])
+        R.backward_pass(fs, *params, grads[k % len(cams)])
+
+    out = {}
+    for name, fn in (("inference_fwd", inference), ("pruning_scores", pruning),
+                     ("proper_antialiasing_fwd_bwd", aa_fwd_bwd)):
+        for k in range(warmup):
+            fn(k)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(steps):
+            fn(k)
+        torch.cuda.synchronize()
+        out[name + "_ms"] = round((time.perf_counter() - t0) * 1000.0 / steps, 4)
+    return out
+
+
 def copy_probe():
     import torch
 
@@ -335,6 +379,7 @@ def main():
                      "traffic": traffic, "algorithmic_bytes": sb[dominant],
                      "avg_launch_ms": round(stage_ms[dominant], 4), "valu": valu},
     }
+    out["variants"] = variants_bench(sc, grads, steps=max(args.steps // 2, 5), warmup=3)
     if not args.no_train_step:
         out["train_step"] = train_step_bench(scene, steps=max(args.steps // 2, 5), warmup=3)
     if not args.no_cpu_baseline:

@@ -45,13 +45,20 @@ enum { GS_FLOAT32 = 0, GS_FLOAT64 = 1, GS_BFLOAT16 = 2 };
 
 /* Pinhole camera. viewmat is the row-major 4x4 world-to-camera matrix with OpenCV axes
  * (x right, y down, z forward); pixel (i, j) covers [i, i+1) x [j, j+1), so its centre is
- * at (i + 0.5, j + 0.5). */
+ * at (i + 0.5, j + 0.5). flags: GS_CAM_* bits (0 = the plain rules). */
 typedef struct gs_camera {
   float viewmat[16];
   float fx, fy, cx, cy;
   int32_t width, height;
   float near_plane, far_plane; /* near_plane must be > 0 */
+  int32_t flags;
 } gs_camera;
+
+/* Faster-GS's proper_antialiasing setting (phase1/tests/test_parity.py:82, consumed at
+ * phase1/fastergs_macro.patch:215): the blended opacity is o * sqrt(max(det S / det S', 0)),
+ * S the projected 2D covariance and S' = S + 0.3 I the dilated one (the Mip-Splatting 2D
+ * filter), and its gradient flows through the compensation factor into the covariance. */
+#define GS_CAM_PROPER_ANTIALIASING 1
 
 /* Thread-local message of the last failed call. */
 const char* gs_last_error(void);
@@ -151,11 +158,24 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
  *   tile; ckpt [n_buckets, 256, 4] = (C.r, C.g, C.b, T) at the start of every 32-entry
  *   bucket. bg is host memory (3 floats) or NULL for black. splat_rec, point_list and ckpt
  *   may be NULL when there are no instances (every tile range empty).
+ *   Inference (Faster-GS's inference blend, upstream/upstream_main_kernels.patch:131-150):
+ *   ckpt NULL, and then bucket_offsets, n_contrib and tile_max may be NULL too; image and
+ *   final_T are the same bits as with them.
  * ------------------------------------------------------------------------------------- */
 int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, int width, int height, const float* bg,
                     float* image, float* final_T, int32_t* n_contrib, uint32_t* tile_max,
                     float* ckpt, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Pruning scores (replaces Faster-GS's pruning-score blend, kernels_pruning_scores.cuh, seen
+ * at upstream/upstream_main_kernels.patch:152-198): for every splat g,
+ *   scores[g] += sum over the pixels it is blended into of its blending weight alpha * T,
+ * with the forward's rules decision for decision (same list walk, skip and stop). Accumulates
+ * (zero scores before the first view). n = length of scores.
+ * ------------------------------------------------------------------------------------- */
+int gs_blend_scores_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
+                       int width, int height, int64_t n, float* scores, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 3D bucketed blend backward (replaces blend_backward_cu / blend_backward_macro_cu,

@@ -62,8 +62,9 @@ def quat_to_rot(q: torch.Tensor) -> torch.Tensor:
 
 
 def preprocess64(means, log_scales, quats, opacity_logits, sh, cam, sh_degree):
-    """Returns dict(mean2d [N,2], conic [N,3] (A,B,C), opacity [N], color [N,3] (clamped), depth [N],
-    cov2d [N,3] (a,b,c)) as differentiable float64 tensors."""
+    """Returns dict(mean2d [N,2], conic [N,3] (A,B,C), opacity [N] (blended: compensated when
+    cam.proper_antialiasing), color [N,3] (clamped), depth [N], cov2d [N,3] (a,b,c)) as
+    differentiable float64 tensors."""
     R, t, campos, (lxlo, lxhi, lylo, lyhi) = cam_derived(cam)
     v = means @ R.T + t
     vx, vy, vz = v.unbind(1)
@@ -82,6 +83,9 @@ def preprocess64(means, log_scales, quats, opacity_logits, sh, cam, sh_degree):
     b = cov[:, 0, 1]
     c = cov[:, 1, 1] + 0.3
     det = a * c - b * b
+    if getattr(cam, "proper_antialiasing", False):
+        # Mip-Splatting's 2D filter: the dilated splat keeps the undilated splat's integral
+        o = o * torch.sqrt(torch.clamp((cov[:, 0, 0] * cov[:, 1, 1] - b * b) / det, min=0.0))
     conic = torch.stack([c / det, -b / det, a / det], -1)
     mean2d = torch.stack([cam.fx * tx + cam.cx, cam.fy * ty + cam.cy], -1)
     d = means - campos
@@ -93,9 +97,11 @@ def preprocess64(means, log_scales, quats, opacity_logits, sh, cam, sh_degree):
     return dict(mean2d=mean2d, conic=conic, opacity=o, color=color, depth=vz, cov2d=torch.stack([a, b, c], -1))
 
 
-def blend64(mean2d, conic, opacity, color, point_list, ranges, mask, width, height, bg=(0.0, 0.0, 0.0)):
+def blend64(mean2d, conic, opacity, color, point_list, ranges, mask, width, height, bg=(0.0, 0.0, 0.0),
+            scores=None):
     """Front-to-back compositing per 16x16 tile given the blended-entry mask [M, 256].
-    Returns (image [3,H,W], final_T [H,W]) as differentiable float64 tensors."""
+    Returns (image [3,H,W], final_T [H,W]) as differentiable float64 tensors. scores (optional
+    float64 [N] tensor) receives each Gaussian's blending weights summed over the image."""
     dev = mean2d.device
     tiles_x = (width + 15) // 16
     img = torch.zeros(3, height, width, dtype=torch.float64, device=dev)
@@ -126,6 +132,8 @@ def blend64(mean2d, conic, opacity, color, point_list, ranges, mask, width, heig
             one_minus = 1.0 - a
             Tb = torch.cumprod(torch.cat([torch.ones_like(one_minus[:1]), one_minus[:-1]], 0), 0)
             w = a * Tb
+            if scores is not None:
+                scores.index_add_(0, ids, (w * inside[None, :]).sum(1).detach())
             C = w.T @ color[ids]  # [256, 3]
             T_fin = Tb[-1] * one_minus[-1]
         else:

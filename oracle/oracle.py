@@ -18,7 +18,7 @@ LIB = HERE / "liboracle.so"
 class OrCamera(C.Structure):
     _fields_ = [("viewmat", C.c_float * 16), ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float),
                 ("cy", C.c_float), ("width", C.c_int32), ("height", C.c_int32), ("near_plane", C.c_float),
-                ("far_plane", C.c_float)]
+                ("far_plane", C.c_float), ("flags", C.c_int32)]
 
 
 def build(force: bool = False) -> Path:
@@ -57,6 +57,7 @@ def camera(cam) -> OrCamera:
     oc.fx, oc.fy, oc.cx, oc.cy = cam.fx, cam.fy, cam.cx, cam.cy
     oc.width, oc.height = cam.width, cam.height
     oc.near_plane, oc.far_plane = cam.near, cam.far
+    oc.flags = 1 if getattr(cam, "proper_antialiasing", False) else 0
     return oc
 
 
@@ -88,7 +89,8 @@ def bin_instances(rec, touched, cam):
     return keys[:m], pl[:m], ranges, boff
 
 
-def blend_fwd(rec, point_list, ranges, boff, width, height, bg=(0.0, 0.0, 0.0), with_ckpt=True):
+def blend_fwd(rec, point_list, ranges, boff, width, height, bg=(0.0, 0.0, 0.0), with_ckpt=True, scores=None):
+    """scores: None, or a float64 [n] array that receives each splat's summed blending weights."""
     T = ranges.shape[0]
     nb = int(boff[-1])
     image = np.zeros((3, height, width), np.float32)
@@ -101,7 +103,7 @@ def blend_fwd(rec, point_list, ranges, boff, width, height, bg=(0.0, 0.0, 0.0), 
     lib().or_blend_fwd(_p(f32(rec)), _p(np.ascontiguousarray(ranges, np.uint32)),
                        _p(np.ascontiguousarray(point_list, np.uint32)), _p(np.ascontiguousarray(boff, np.uint32)),
                        C.c_int(width), C.c_int(height), _p(bgc), _p(image), _p(final_T), _p(n_contrib),
-                       _p(tile_max), _p(ckpt), _p(amb))
+                       _p(tile_max), _p(ckpt), _p(amb), _p(scores))
     return image, final_T, n_contrib, tile_max, ckpt, amb.astype(bool)
 
 
@@ -133,12 +135,15 @@ def preprocess_bwd(means, log_scales, quats, opacity_logits, sh, cam, sh_degree,
 
 
 def render(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, bg=(0.0, 0.0, 0.0)):
-    """Full forward. Returns a dict of every intermediate."""
+    """Full forward. Returns a dict of every intermediate, with the pruning scores (float64 [n])."""
     rec, touched = preprocess_fwd(means, log_scales, quats, opacity_logits, sh, cam, sh_degree)
     keys, pl, ranges, boff = bin_instances(rec, touched, cam)
-    image, final_T, n_contrib, tile_max, ckpt, amb = blend_fwd(rec, pl, ranges, boff, cam.width, cam.height, bg)
+    scores = np.zeros(rec.shape[0], np.float64)
+    image, final_T, n_contrib, tile_max, ckpt, amb = blend_fwd(rec, pl, ranges, boff, cam.width, cam.height, bg,
+                                                               scores=scores)
     return dict(rec=rec, touched=touched, keys=keys, point_list=pl, ranges=ranges, bucket_offsets=boff,
-                image=image, final_T=final_T, n_contrib=n_contrib, tile_max=tile_max, ckpt=ckpt, amb=amb)
+                image=image, final_T=final_T, n_contrib=n_contrib, tile_max=tile_max, ckpt=ckpt, amb=amb,
+                scores=scores)
 
 
 def exp2_neg(x: float) -> float:

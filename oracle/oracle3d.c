@@ -121,13 +121,17 @@ typedef struct {
   float fx, fy, cx, cy;
   int32_t width, height;
   float near_plane, far_plane;
+  int32_t flags;
 } or_camera;
+
+#define CAM_PROPER_ANTIALIASING 1
 
 typedef struct {
   float r[9], t[3];
   float fx, fy, cx, cy;
   int W, H;
   float znear, zfar;
+  int flags;
   float campos[3];
   float lxlo, lxhi, lylo, lyhi;
   int tiles_x, tiles_y;
@@ -142,6 +146,7 @@ static Cam make_cam(const or_camera* c) {
   k.fx = c->fx; k.fy = c->fy; k.cx = c->cx; k.cy = c->cy;
   k.W = c->width; k.H = c->height;
   k.znear = c->near_plane; k.zfar = c->far_plane;
+  k.flags = c->flags;
   for (int j = 0; j < 3; ++j) {
     double s = 0.0;
     for (int i = 0; i < 3; ++i) s -= (double)c->viewmat[4 * i + j] * c->viewmat[4 * i + 3];
@@ -232,6 +237,7 @@ static void sh_basis_grad(double x, double y, double z, int n, const double* g, 
 typedef struct {
   int vis;
   float vx, vy, vz, iz, tx, ty, txc, tyc, o;
+  float os, rho, ratio, ar, cr; /* sigmoid, antialiasing factor sqrt(ratio), undilated diagonal */
   float qw, qx, qy, qz, qinv;
   float R[9], s[3], M[9], S[6], T[6];
   float a, b, c, det, A, B, C, mx, my;
@@ -292,11 +298,25 @@ static void geom(const float* means, const float* ls, const float* quats, const 
   float u10 = fmaf(T[3], S[0], fmaf(T[4], S[1], T[5] * S[2]));
   float u11 = fmaf(T[3], S[1], fmaf(T[4], S[3], T[5] * S[4]));
   float u12 = fmaf(T[3], S[2], fmaf(T[4], S[4], T[5] * S[5]));
-  g->a = fmaf(u00, T[0], fmaf(u01, T[1], u02 * T[2])) + DILATION;
+  g->ar = fmaf(u00, T[0], fmaf(u01, T[1], u02 * T[2]));
   g->b = fmaf(u00, T[3], fmaf(u01, T[4], u02 * T[5]));
-  g->c = fmaf(u10, T[3], fmaf(u11, T[4], u12 * T[5])) + DILATION;
+  g->cr = fmaf(u10, T[3], fmaf(u11, T[4], u12 * T[5]));
+  g->a = g->ar + DILATION;
+  g->c = g->cr + DILATION;
   g->det = fmaf(g->a, g->c, -(g->b * g->b));
   vis = vis && (g->det > 0.0f);
+  /* proper antialiasing: the 0.3 px^2 low-pass keeps the splat's integral, o sqrt(det S / det S')
+   * (Mip-Splatting's 2D filter; Faster-GS's flag, phase1/fastergs_macro.patch:215) */
+  g->os = g->o;
+  g->rho = 1.0f;
+  g->ratio = 1.0f;
+  if (cam->flags & CAM_PROPER_ANTIALIASING) {
+    float det_raw = fmaf(g->ar, g->cr, -(g->b * g->b));
+    g->ratio = fmaxf(det_raw / g->det, 0.0f);
+    g->rho = sqrtf(g->ratio);
+    g->o = g->os * g->rho;
+    vis = vis && (g->o >= ALPHA_MIN);
+  }
   float idet = 1.0f / g->det;
   g->A = g->c * idet;
   g->B = -g->b * idet;
@@ -501,10 +521,13 @@ static int strip_hit(const float* r, int tile_y0, int strip) {
 
 /* ckpt and amb may be NULL. Checkpoints are written for every bucket the pixel loop reaches.
  * amb [H, W] = 1 where some decision of the pixel fell within the margins above (its
- * n_contrib, and the image from that point on, may then legitimately differ). */
+ * n_contrib, and the image from that point on, may then legitimately differ).
+ * scores (may be NULL): scores[g] += the blending weight alpha T of splat g at every pixel it is
+ * blended into (the pruning-score blend). */
 int or_blend_fwd(const float* rec, const uint32_t* ranges, const uint32_t* point_list,
                  const uint32_t* bucket_offsets, int W, int H, const float* bg, float* image,
-                 float* final_T, int32_t* n_contrib, uint32_t* tile_max, float* ckpt, uint8_t* amb) {
+                 float* final_T, int32_t* n_contrib, uint32_t* tile_max, float* ckpt, uint8_t* amb,
+                 double* scores) {
   int tiles_x = (W + TILE - 1) / TILE, tiles_y = (H + TILE - 1) / TILE;
   int64_t HW = (int64_t)W * H;
   float bgc[3] = {bg ? bg[0] : 0.0f, bg ? bg[1] : 0.0f, bg ? bg[2] : 0.0f};
@@ -536,6 +559,10 @@ int or_blend_fwd(const float* rec, const uint32_t* ranges, const uint32_t* point
         if (fabsf(alpha - ALPHA_MIN) <= AMB_ALPHA * ALPHA_MIN) near = 1;
         if (alpha < ALPHA_MIN) continue;
         float w = alpha * T;
+        if (scores) {
+#pragma omp atomic
+          scores[point_list[s + idx]] += (double)w;
+        }
         C[0] = fmaf(r[8], w, C[0]);
         C[1] = fmaf(r[9], w, C[1]);
         C[2] = fmaf(r[10], w, C[2]);
@@ -704,7 +731,9 @@ int or_preprocess_bwd(const float* means, const float* ls, const float* quats, c
     /* geometry */
     Geom g;
     geom(means, ls, quats, op, i, &cam, &g);
-    g_op[i] = (float)((double)g2[5] * g.o * (1.0 - g.o));
+    int aa = cam.flags & CAM_PROPER_ANTIALIASING;
+    g_op[i] = aa ? (float)((double)g2[5] * g.rho * g.os * (1.0 - g.os))
+                 : (float)((double)g2[5] * g.o * (1.0 - g.o));
     double iz = 1.0 / g.vz;
     double gvx = g2[0] * (double)cam.fx * iz, gvy = g2[1] * (double)cam.fy * iz;
     double gvz = -((double)g2[0] * cam.fx * g.vx + (double)g2[1] * cam.fy * g.vy) * iz * iz;
@@ -713,6 +742,13 @@ int or_preprocess_bwd(const float* means, const float* ls, const float* quats, c
     double ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
     double gbb = (2 * b * c * gA - (a * c + b * b) * gB + 2 * a * b * gC) * id2;
     double gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
+    if (aa) { /* d/d(a, b, c) of rho = sqrt((ar cr - b^2) / (a c - b^2)), ar = a - 0.3, cr = c - 0.3 */
+      double ar = g.ar, cr = g.cr, ratio = (ar * cr - b * b) / det, rho = sqrt(ratio);
+      double k = (double)g2[5] * g.os / (2.0 * rho * det);
+      ga += k * (cr - ratio * c);
+      gc += k * (ar - ratio * a);
+      gbb += -2.0 * k * b * (1.0 - ratio);
+    }
     double Gc[2][2] = {{ga, 0.5 * gbb}, {0.5 * gbb, gc}};
     double T[2][3], Sm[3][3];
     for (int k = 0; k < 3; ++k) { T[0][k] = g.T[k]; T[1][k] = g.T[3 + k]; }

@@ -6,6 +6,8 @@ and alpha within 1e-5 max abs; gradients within 1e-4 relative L2 (atomic order d
 Scenes follow phase1/tests/test_parity.py:43-84 (camera-space scenes with partial tiles,
 heavy overlap, small splats) plus the empty case of :143-153.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -35,8 +37,8 @@ def make(name, seed=0, sh_coeffs=16):
     return scenes.small_scene(n, W, H, seed=seed, sh_coeffs=sh_coeffs, scale=sc, opacity=op, depth=dp)
 
 
-def gpu_forward(scene, sh_degree, bg=BG):
-    cam = scene.cameras[0]
+def gpu_forward(scene, sh_degree, bg=BG, cam=None):
+    cam = scene.cameras[0] if cam is None else cam
     p = [t.cuda().contiguous() for t in scene.params()]
     fs = R.forward_pass(*p, cam, sh_degree=sh_degree, bg=bg, keep_keys=True)
     torch.cuda.synchronize()
@@ -83,10 +85,19 @@ def pixel_of(sel, boff, cam):
 
 @pytest.mark.parametrize("name", list(SCENES))
 def test_forward_matches_oracle(name):
-    sc = make(name)
-    cam = sc.cameras[0]
+    check_forward(make(name))
+
+
+@pytest.mark.parametrize("name", ["tiny", "small_splats", "heavy_overlap"])
+def test_proper_antialiasing_forward_matches_oracle(name):
+    sc = make(name, seed=4)
+    check_forward(sc, dataclasses.replace(sc.cameras[0], proper_antialiasing=True))
+
+
+def check_forward(sc, cam=None):
+    cam = sc.cameras[0] if cam is None else cam
     deg = 3
-    p, fs = gpu_forward(sc, deg)
+    p, fs = gpu_forward(sc, deg, cam=cam)
     ref = O.render(*[t.numpy() for t in sc.params()], cam, deg, bg=BG)
     vis = ref["touched"] > 0
     assert (np_(fs.touched).astype(np.uint32) == ref["touched"]).all(), "tiles touched differ"
@@ -116,12 +127,13 @@ def test_forward_matches_oracle(name):
     assert np.array_equal(b2t, expect)
 
 
-@pytest.mark.parametrize("name", ["tiny", "partial_tiles", "heavy_overlap"])
-def test_gradients_match_float64_autograd(name):
+@pytest.mark.parametrize("name,aa", [("tiny", False), ("partial_tiles", False), ("heavy_overlap", False),
+                                     ("tiny", True), ("small_splats", True)])
+def test_gradients_match_float64_autograd(name, aa):
     sc = make(name, seed=1)
-    cam = sc.cameras[0]
+    cam = dataclasses.replace(sc.cameras[0], proper_antialiasing=aa)
     deg = 3
-    p, fs = gpu_forward(sc, deg)
+    p, fs = gpu_forward(sc, deg, cam=cam)
     g = torch.Generator().manual_seed(7)
     gi = torch.randn(3, cam.height, cam.width, generator=g, dtype=torch.float64)
     ga = torch.randn(cam.height, cam.width, generator=g, dtype=torch.float64)
@@ -341,3 +353,67 @@ def test_densification_info_accumulates_ndc_gradient_norms(rows):
     assert torch.equal(got[0], expect[0])
     for r in range(1, rows):
         assert float((got[r] - expect[r]).norm() / expect[r].norm()) < 1e-5  # atomics: order differs
+
+
+def K_of(cam):
+    return torch.tensor([[cam.fx, 0, cam.cx], [0, cam.fy, cam.cy], [0, 0, 1]])
+
+
+@pytest.mark.parametrize("aa", [False, True], ids=["plain", "proper_antialiasing"])
+def test_inference_blend_equals_training_forward(aa):
+    """The inference forward (no bucket table, checkpoints or n_contrib) gives the training
+    forward's image and alpha bit for bit, with and without proper antialiasing."""
+    sc = make("partial_tiles", seed=13)
+    cam = dataclasses.replace(sc.cameras[0], proper_antialiasing=aa)
+    p, fs = gpu_forward(sc, 3, cam=cam)
+    img, alpha = R.rasterize_inference(*p, cam.viewmat, K_of(cam), cam.width, cam.height, bg=BG, near=cam.near,
+                                       far=cam.far, proper_antialiasing=aa)
+    torch.cuda.synchronize()
+    assert torch.equal(img, fs.image)
+    assert torch.equal(alpha, 1.0 - fs.final_T)
+    leaves = [t.clone().requires_grad_(True) for t in p]
+    img2, _, _ = R.rasterize(*leaves, cam.viewmat, K_of(cam), cam.width, cam.height, bg=BG, near=cam.near,
+                             far=cam.far, proper_antialiasing=aa)
+    assert torch.equal(img2.detach(), img)
+
+
+@pytest.mark.parametrize("name,aa", [("tiny", False), ("partial_tiles", False), ("small_splats", False),
+                                     ("small_splats", True)])
+def test_pruning_scores_match_oracle(name, aa):
+    """Pruning scores (summed blending weights per Gaussian) against the oracle's; splats listed
+    in a tile with an ambiguous pixel (hardware vs polynomial exp2) are compared by the sum only."""
+    sc = make(name, seed=17)
+    cam = dataclasses.replace(sc.cameras[0], proper_antialiasing=aa)
+    p = [t.cuda().contiguous() for t in sc.params()]
+    s = R.pruning_scores(*p, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near, far=cam.far,
+                         proper_antialiasing=aa)
+    torch.cuda.synchronize()
+    ref = O.render(*[t.numpy() for t in sc.params()], cam, 3, bg=BG)
+    got = np_(s).astype(np.float64)
+    exp = ref["scores"]
+    keep = np.ones(sc.n, bool)
+    for t in np.nonzero(tile_any(ref["amb"], cam))[0]:
+        keep[ref["point_list"][ref["ranges"][t, 0]:ref["ranges"][t, 1]].view(np.uint32)] = False
+    assert keep.mean() > 0.9
+    assert (exp[keep] > 0).sum() > 100
+    np.testing.assert_allclose(got[keep], exp[keep], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(got.sum(), exp.sum(), rtol=1e-5)
+    assert np.all(got[ref["touched"] == 0] == 0)
+    # a second view accumulates into the same buffer
+    R.pruning_scores(*p, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near, far=cam.far,
+                     proper_antialiasing=aa, scores=s)
+    np.testing.assert_allclose(np_(s).astype(np.float64), 2 * got, rtol=1e-6, atol=1e-7)
+
+
+def test_pruning_scores_sum_to_image_alpha_full_size():
+    """1M-Gaussian SH3 1297x840 view: the scores of all Gaussians sum to the frame's total alpha
+    (per pixel the blending weights sum to 1 - T_final)."""
+    sc = scenes.sh3_1m()
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    s = R.pruning_scores(*p, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near, far=cam.far)
+    img, alpha = R.rasterize_inference(*p, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near, far=cam.far)
+    torch.cuda.synchronize()
+    total = float(s.double().sum())
+    assert total > 0.05 * cam.width * cam.height
+    np.testing.assert_allclose(total, float(alpha.double().sum()), rtol=1e-4)

@@ -15,6 +15,7 @@ or index, a transposed operand) fails it:
     completeness + blend rules), and the binning against its invariants
     (toy2d/tests/test_cpu.py:10-21: complete lists, depth order, bucket count).
 """
+import dataclasses
 import math
 import re
 from pathlib import Path
@@ -171,6 +172,44 @@ def test_preprocess_on_axis_isotropic_closed_form():
     assert b[0] == math.ceil(64.3 - ext - 0.5) and b[1] == math.floor(64.3 + ext - 0.5)
 
 
+def aa_camera(cam):
+    return dataclasses.replace(cam, proper_antialiasing=True)
+
+
+def test_proper_antialiasing_on_axis_closed_form():
+    """Isotropic on-axis Gaussian: S = sigma^2 I, S' = (sigma^2 + 0.3) I, so the blended
+    opacity is o sigma^2 / (sigma^2 + 0.3) and the conic is unchanged."""
+    cam = scenes.Camera(torch.eye(4), 500.0, 500.0, 64.3, 47.8, 128, 96, 0.2, 100.0)
+    z, s = 4.0, 0.01
+    g = one_gaussian((0.0, 0.0, z), math.log(s))
+    plain, _ = O.preprocess_fwd(*g, cam, 0)
+    rec, touched = O.preprocess_fwd(*g, aa_camera(cam), 0)
+    assert touched[0] > 0
+    sig2 = (500.0 * s / z) ** 2
+    o = 1.0 / (1.0 + math.exp(-2.0))
+    np.testing.assert_allclose(rec[0, 5], o * sig2 / (sig2 + 0.3), rtol=2e-6)
+    np.testing.assert_allclose(rec[0, 7], math.log(255.0 * o * sig2 / (sig2 + 0.3)), rtol=2e-6)
+    assert np.array_equal(rec[0, 2:5], plain[0, 2:5]) and rec[0, 6] == plain[0, 6]
+
+
+@pytest.mark.parametrize("s", [0.003, 0.006, 0.012])
+def test_proper_antialiasing_keeps_the_splat_integral(s):
+    """Summed over the pixels, one Gaussian's alpha is 2 pi sqrt(det S') (o' - 1/255) (the
+    integral of o' G' over o' G' >= 1/255). With the compensation o' sqrt(det S') = o sqrt(det S):
+    the dilated splat carries the undilated one's mass, without it (sigma^2 + 0.3) / sigma^2 more."""
+    cam = scenes.Camera(torch.eye(4), 500.0, 500.0, 64.0, 48.0, 128, 96, 0.2, 100.0)
+    z, logit = 4.0, 3.0
+    g = list(one_gaussian((0.0, 0.0, z), math.log(s), logit=logit, sh0=(0.5 / D.SH0, 0.0, 0.0)))
+    o = 1.0 / (1.0 + math.exp(-logit))
+    sig2 = (500.0 * s / z) ** 2
+    for c, expect in ((cam, 2 * math.pi * (sig2 + 0.3) * (o - 1 / 255)),
+                      (aa_camera(cam), 2 * math.pi * (o * sig2 - (sig2 + 0.3) / 255))):
+        ref = O.render(*g, c, 0, bg=(0.0, 0.0, 0.0))
+        total = float(ref["image"][0].astype(np.float64).sum())  # colour 1: image = alpha
+        np.testing.assert_allclose(total, expect, rtol=0.01)
+    assert (sig2 + 0.3) / sig2 > 1.1  # the two cases differ by far more than the tolerance
+
+
 def test_preprocess_off_axis_mean_and_rotation_invariance():
     cam = scenes.Camera(torch.eye(4), 400.0, 300.0, 50.0, 40.0, 100, 80, 0.2, 100.0)
     p = (0.3, -0.2, 5.0)
@@ -191,9 +230,10 @@ def test_preprocess_culls_behind_and_far():
         assert touched[0] == 0
 
 
-def test_preprocess_matches_float64_restatement():
+@pytest.mark.parametrize("aa", [False, True], ids=["plain", "proper_antialiasing"])
+def test_preprocess_matches_float64_restatement(aa):
     sc = small(seed=3)
-    cam = sc.cameras[0]
+    cam = aa_camera(sc.cameras[0]) if aa else sc.cameras[0]
     rec, touched = O.preprocess_fwd(*np_params(sc), cam, 3)
     vis = touched > 0
     assert vis.sum() > 50
@@ -204,6 +244,7 @@ def test_preprocess_matches_float64_restatement():
     scale = np.abs(conic).max(1, keepdims=True)
     assert np.abs(rec[vis, 2:5] - conic).max() / 1 <= 1e-4 * scale.max()
     np.testing.assert_allclose(rec[vis, 8:11], pre["color"][vis].numpy(), atol=2e-6)
+    np.testing.assert_allclose(rec[vis, 5], pre["opacity"][vis].numpy(), rtol=2e-6)
 
 
 # ---------------------------------------------------------------------------------------
@@ -341,6 +382,24 @@ def test_blend_forward_matches_dense_float64():
     assert np.abs(fT.numpy() - ref["final_T"]).max() <= 1e-5
 
 
+def test_pruning_scores_sum_to_the_image_coverage_and_match_dense_weights():
+    """Per pixel the blending weights sum to 1 - T_final, so the scores of all splats sum to the
+    image's total alpha; per splat they equal the float64 dense weights of the same blend."""
+    sc = small(n=500, seed=21)
+    cam = sc.cameras[0]
+    ref = O.render(*np_params(sc), cam, 3, bg=BG)
+    np.testing.assert_allclose(ref["scores"].sum(), (1.0 - ref["final_T"].astype(np.float64)).sum(), rtol=1e-5)
+    assert np.all(ref["scores"][ref["touched"] == 0] == 0)
+    mask = O.contrib_mask(ref["rec"], ref["point_list"], ref["ranges"], cam.width, cam.height, ref["n_contrib"])
+    r = torch.tensor(ref["rec"], dtype=torch.float64)
+    conic = r[:, 2:5]
+    s64 = torch.zeros(sc.n, dtype=torch.float64)
+    D.blend64(r[:, 0:2], conic, r[:, 5], r[:, 8:11], ref["point_list"], ref["ranges"], mask, cam.width,
+              cam.height, BG, scores=s64)
+    assert (ref["scores"] > 0).sum() > 100
+    np.testing.assert_allclose(ref["scores"], s64.numpy(), rtol=2e-5, atol=1e-6)
+
+
 def test_blend_backward_replay_matches_autograd():
     sc = small(n=400, seed=10)
     cam = sc.cameras[0]
@@ -366,9 +425,10 @@ def test_blend_backward_replay_matches_autograd():
         assert D.rel_err(a, b) < 2e-5, (cols, D.rel_err(a, b))
 
 
-def test_preprocess_backward_matches_autograd():
+@pytest.mark.parametrize("aa", [False, True], ids=["plain", "proper_antialiasing"])
+def test_preprocess_backward_matches_autograd(aa):
     sc = small(n=300, seed=11)
-    cam = sc.cameras[0]
+    cam = aa_camera(sc.cameras[0]) if aa else sc.cameras[0]
     rec, touched = O.preprocess_fwd(*np_params(sc), cam, 3)
     vis = touched > 0
     rng = np.random.default_rng(2)
