@@ -34,6 +34,7 @@ class GsCamera(C.Structure):
 
 
 GS_ACCUMULATE = 1  # gs_blend_bwd_3d flag: add to grad2d instead of zeroing it first
+GS_ABS_GRAD = 2  # gs_blend_bwd_3d flag: also accumulate |dL/dmean2d| into grad2d[:, 9:11]
 GS_FLOAT32, GS_FLOAT64, GS_BFLOAT16 = 0, 1, 2
 GS_CAM_PROPER_ANTIALIASING = 1  # gs_camera.flags bit
 GS_ADAM_MAX_GROUPS = 8
@@ -77,10 +78,11 @@ _SIGS = {
     "gs_bin_fill_rect": (_i32, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                 _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
-    "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp,
+                               _vp]),
     "gs_blend_scores_3d": (_i32, [_vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                               _vp, _i32, _vp, _vp]),
+                               _vp, _vp, _i32, _vp, _vp]),
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_adam_step": (_i32, [C.POINTER(GsAdamGroup), _i32, _i64, _vp, _vp]),

@@ -99,6 +99,7 @@ class ForwardState:
     n_contrib: torch.Tensor | None  # [H, W] int32 (None: inference)
     tile_max: torch.Tensor | None  # [T] int32 (None: inference)
     ckpt: torch.Tensor | None    # [n_buckets_max, 256, 4] (None: inference)
+    bucket_list: torch.Tensor | None = None  # [4 + n_buckets_max] int32: buckets the backward reads
     bg: tuple = (0.0, 0.0, 0.0)
     timings: dict = field(default_factory=dict)
 
@@ -213,9 +214,9 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         call("gs_blend_scores_3d", ptr(rec), ptr(ranges), ptr(point_list), W, H, n, ptr(_scores), st)
         tm.mark("scores")
         return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges,
-                            bucket_offsets, 0, None, None, None, None, None, None, tuple(bg),
+                            bucket_offsets, 0, None, None, None, None, None, None, None, tuple(bg),
                             {} if isinstance(timing, StageTimer) else tm.result())
-    nb_max, bucket_to_tile, n_contrib, tile_max, ckpt = 0, None, None, None, None
+    nb_max, bucket_to_tile, n_contrib, tile_max, ckpt, blist = 0, None, None, None, None, None
     if for_backward:
         nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
         bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
@@ -223,21 +224,24 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
         tile_max = torch.empty(T, dtype=torch.int32, device=dev)
         ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
+        blist = torch.empty(4 + nb_max, dtype=torch.int32, device=dev)
     image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
     final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
     tm.mark("buckets")
     call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
-         ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), st)
+         ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), ptr(blist), st)
     tm.mark("blend_fwd")
     return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges, bucket_offsets,
-                        nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, tuple(bg),
+                        nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist, tuple(bg),
                         {} if isinstance(timing, StageTimer) else tm.result())
 
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
-                  grad_alpha=None, timing: bool = False, counters: torch.Tensor | None = None):
+                  grad_alpha=None, timing: bool = False, counters: torch.Tensor | None = None,
+                  abs_grad: bool = True):
     """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings);
-    grad_sh is a (DC, rest) pair when sh is.
+    grad_sh is a (DC, rest) pair when sh is. abs_grad: also sum |dL/dmean2d| into grad2d[:, 9:11]
+    (densification by absolute gradient); otherwise those columns stay zero.
     counters: optional int64 [3] CUDA tensor that the blend backward adds its atomic count and
     pair-evaluation count to (slots 0 and 2)."""
     dev = means.device
@@ -253,8 +257,9 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
     tm.mark("grad_zero")
     call("gs_blend_bwd_3d", ptr(fs.rec), ptr(fs.ranges), ptr(fs.point_list), ptr(fs.bucket_offsets),
          ptr(fs.bucket_to_tile), fs.n_buckets_max, n, cam.width, cam.height, ptr(fs.image), ptr(grad_image),
-         ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(grad2d),
-         _lib.GS_ACCUMULATE, ptr(counters), st)
+         ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(fs.bucket_list),
+         ptr(grad2d),
+         _lib.GS_ACCUMULATE | (_lib.GS_ABS_GRAD if abs_grad else 0), ptr(counters), st)
     tm.mark("blend_bwd")
     g_means = torch.empty(n, 3, dtype=torch.float32, device=dev)
     g_ls = torch.empty(n, 3, dtype=torch.float32, device=dev)
@@ -315,9 +320,11 @@ class _Rasterize3D(torch.autograd.Function):
         if grad_image is None:
             grad_image = torch.zeros_like(fs.image)
         shp = (sh, sh_rest) if ctx.split else sh
+        # |dL/dmean2d| only when the caller's densification_info has its third row
+        abs_grad = ctx.dinfo is not None and ctx.dinfo.shape[0] == 3
         gm, gls, gq, gop, gsh, grad2d, _ = backward_pass(fs, means.contiguous(), log_scales.contiguous(),
                                                          quats.contiguous(), opacity_logits.contiguous(),
-                                                         shp, grad_image, grad_alpha)
+                                                         shp, grad_image, grad_alpha, abs_grad=abs_grad)
         ctx.grad2d = grad2d
         if ctx.dinfo is not None:
             densification_stats(grad2d, fs.touched, fs.cam.width, fs.cam.height, ctx.dinfo)

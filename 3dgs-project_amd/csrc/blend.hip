@@ -56,6 +56,8 @@ struct BlendArgs {
   S* grad_rec;          // [n, 12]
   // pruning scores (3D): scores[g] += sum over pixels of the blending weight alpha T of g
   float* scores;
+  // 3D: buckets the backward reads (appended by the forward, consumed by the backward)
+  uint32_t* bucket_list;
 };
 
 // Per-wavefront counter increment (one atomic per wavefront).
@@ -110,6 +112,10 @@ __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAto
 // ---------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------
+// Bucket list written by the 3D forward: [0] buckets the backward reads, [1..3] zero,
+// [4 + i] bucket indices (any order).
+constexpr int kListHeader = 4;
+
 // kScore: instead of the image, accumulate every splat's blending weights alpha T over the
 // tile's pixels into a.scores (a wavefront sum per splat into LDS, one global atomic per
 // staged splat and tile); the blend itself is the forward's, decision for decision.
@@ -261,6 +267,15 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
   }
   __syncthreads();
   if (t == 0 && a.tile_max) a.tile_max[tile] = s_max;
+  if (a.bucket_list) {
+    // append the buckets the backward reads: those starting before the tile's last blended entry
+    __shared__ uint32_t s_base;
+    const uint32_t n_act = (s_max + kBucket - 1) / kBucket;
+    if (t == 0) s_base = n_act ? atomicAdd(a.bucket_list, n_act) : 0u;
+    __syncthreads();
+    const uint32_t first = a.bucket_offsets[tile];
+    for (uint32_t k = t; k < n_act; k += kTilePixels) a.bucket_list[kListHeader + s_base + k] = first + k;
+  }
 }
 
 
@@ -370,6 +385,9 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
       C = s.s2;
     }
     // power = -1/2 (A dx^2 + 2 B dx dy + C dy^2), d = mean - pixel
+    if constexpr (R == kRules3D) {
+      if (k == 5) return u * __builtin_amdgcn_rcpf(s.o);  // 3D: u = sum alpha dL/dalpha
+    }
     if (k == 0) return -fma(A, u0, B * u1);
     if (k == 1) return -fma(B, u0, C * u1);
     if (k == 2 || k == 4) return S(-0.5) * u;
@@ -383,19 +401,16 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
 // ---------------------------------------------------------------------------------------
 constexpr int kBwdWaves = 4;
 
-template <int R, typename S, bool kCount>
-__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(BlendArgs<S> a) {
+// kAbs (3D): also accumulate |dL/dmean2d| (grad2d slots 9-10) for densification by absolute
+// gradient, as Faster-GS's compute_abs_grad instantiation does; without it those slots are
+// left untouched.
+// One bucket b, by one wavefront (whose LDS slots are s_sp, s_m, s_id).
+template <int R, typename S, bool kCount, bool kAbs>
+__device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Staged<S>* s_sp, uint32_t* s_m,
+                                           uint32_t* s_id, uint32_t& evals, uint32_t& atomics) {
   using Ru = Rule<R, S>;
   constexpr int NV = Ru::kGradVals;
-  __shared__ Staged<S> s_sp[kBwdWaves][kBucket];
-  __shared__ uint32_t s_m[kBwdWaves][kBucket];
-  __shared__ uint32_t s_id[kBwdWaves][kBucket];
-
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
-  if (b >= a.n_buckets) return;  // whole wavefront
-  if (a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)) return;
   const uint32_t tile = a.bucket_to_tile[b];
   const int bstart = static_cast<int>(b - a.bucket_offsets[tile]) * kBucket;
   const int tmax = a.tile_max ? static_cast<int>(a.tile_max[tile]) : INT_MAX;
@@ -409,9 +424,9 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
   if (lane < bsize) {
     const uint32_t g = a.point_list[r0 + bstart + lane];
     const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
-    s_sp[wave][lane] = Ru::stage(rp);
-    if constexpr (Ru::kStrips) s_m[wave][lane] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
-    s_id[wave][lane] = g;
+    s_sp[lane] = Ru::stage(rp);
+    if constexpr (Ru::kStrips) s_m[lane] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
+    s_id[lane] = g;
   }
 
   // per-pixel state: pixel p = 64 r + lane, row 4 r + lane / 16, column lane % 16
@@ -474,7 +489,6 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
   const int jmax = min(bsize, wave_max(lim_max));
   wave_sync();
 
-  uint32_t evals = 0, atomics = 0;
   // value index k owned by this lane after wave_reduce12 (lo = 0 or 1 within the 8-lane group)
   const int grp = lane >> 3, lo = lane & 7;
   const int kidx = 6 * (grp >> 2) + 3 * ((grp >> 1) & 1) + 2 * (grp & 1) + lo;
@@ -482,28 +496,36 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
   if constexpr (R == kRules3D) {
     // The lane's 4 pixels share a column: the column terms of the power and of the mean
     // gradient are computed once per splat, and per pixel only dy-dependent sums are kept;
-    // the dx factors are applied to the lane's sums before the reduction.
+    // the dx factors are applied to the lane's sums before the reduction. Pixel r of every
+    // lane lies in strip r, so the strip test and the wavefront's largest limit of row r are
+    // scalar; inside, the pixel body has no branches: a lane past its limit or below the
+    // alpha threshold blends alpha = 0, which leaves its T, rho and every sum unchanged.
+    // dL/dopacity = sum G dL/dalpha = (sum alpha dL/dalpha) / o: the sum h is reduced instead.
+    int lim_row[kPixPerLane];
+#pragma unroll
+    for (int r = 0; r < kPixPerLane; ++r) lim_row[r] = __builtin_amdgcn_readfirstlane(wave_max(lim[r]));
     for (int j = 0; j < jmax; ++j) {
-      const Staged<S> sp = s_sp[wave][j];
-      const uint32_t m = __builtin_amdgcn_readfirstlane(s_m[wave][j]);  // wave-uniform: scalar tests
+      const Staged<S> sp = s_sp[j];
+      const uint32_t m = __builtin_amdgcn_readfirstlane(s_m[j]);  // wave-uniform: scalar tests
       const typename Ru::Col cl = Ru::col(sp, pxf);
       const float n0dx = sp.n0 * cl.dx, n1dx = sp.n1 * cl.dx;
       // zeros the compiler cannot see through: each sum then lives in one register from its
       // zero to its last update, instead of being re-zeroed on every path that skips a pixel
-      float sh = opaque_zero(), shy = opaque_zero(), shyy = opaque_zero(), sg = opaque_zero();
+      float sh = opaque_zero(), shy = opaque_zero(), shyy = opaque_zero();
       float cr = opaque_zero(), cg = opaque_zero(), cb = opaque_zero();
       float ab0 = opaque_zero(), ab1 = opaque_zero();
       bool used = false;
 #pragma unroll
       for (int r = 0; r < kPixPerLane; ++r) {
-        if (((m >> r) & 1u) == 0u) continue;  // wave-uniform
-        if (j >= lim[r]) continue;
-        if constexpr (kCount) ++evals;
+        if (((m >> r) & 1u) == 0u || j >= lim_row[r]) continue;  // wave-uniform
+        const bool live = j < lim[r];
+        if constexpr (kCount) evals += live ? 1u : 0u;
         const float dy = sp.my - pyf[r];
         const float G = Ru::falloff(Ru::power(sp, cl, dy));
-        const float alpha = sp.o * G;
-        if (alpha < kAlphaMin) continue;
-        used = true;
+        const float a_raw = sp.o * G;
+        const bool take = live && a_raw >= kAlphaMin;
+        used = used || take;
+        const float alpha = take ? a_raw : 0.0f;
         const float w = T[r] * alpha;
         const float dot = fmaf(Gb[r], sp.cb, fmaf(Gg[r], sp.cg, Gr[r] * sp.cr));
         cr = fmaf(w, Gr[r], cr);
@@ -512,33 +534,34 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
         rho[r] = fmaf(-w, dot, rho[r]);
         const float oma = 1.0f - alpha;
         const float dLda = fmaf(T[r], dot, -(rho[r] * __builtin_amdgcn_rcpf(fmaxf(oma, kOneMinusAlphaEps))));
-        sg = fmaf(G, dLda, sg);
         const float h = alpha * dLda;  // dL/dpower
         const float hy = h * dy;
         sh += h;
         shy += hy;
         shyy = fmaf(hy, dy, shyy);
-        ab0 = fmaf(fabsf(h), fabsf(fmaf(sp.n1, dy, n0dx)), ab0);
-        ab1 = fmaf(fabsf(h), fabsf(fmaf(sp.nat2, dy, n1dx)), ab1);
+        if constexpr (kAbs) {
+          ab0 = fmaf(fabsf(h), fabsf(fmaf(sp.n1, dy, n0dx)), ab0);
+          ab1 = fmaf(fabsf(h), fabsf(fmaf(sp.nat2, dy, n1dx)), ab1);
+        }
         T[r] = T[r] * oma;
       }
       if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
       const float dxsh = cl.dx * sh;
-      S acc[12] = {dxsh, shy, cl.dx * dxsh, cl.dx * shy, shyy, sg, cr, cg, cb, ab0, ab1, 0.0f};
+      S acc[12] = {dxsh, shy, cl.dx * dxsh, cl.dx * shy, shyy, sh, cr, cg, cb, ab0, ab1, 0.0f};
       S u0, u1;
       wave_reduce12(acc, u0, u1);
-      if (owner) {
+      if (owner && (kAbs || kidx < 9)) {
         const S u = lo == 0 ? u0 : u1;
-        atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + kidx,
+        atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kidx,
                         finish_grad<R, S>(sp, kidx, u, u0, u1));
       }
-      if constexpr (kCount) atomics += NV;
+      if constexpr (kCount) atomics += kAbs ? NV : 9;
     }
   } else
   for (int j = 0; j < jmax; ++j) {
-    const Staged<S> sp = s_sp[wave][j];
+    const Staged<S> sp = s_sp[j];
     uint32_t m = 0xfu;
-    if constexpr (Ru::kStrips) m = s_m[wave][j];
+    if constexpr (Ru::kStrips) m = s_m[j];
     S acc[12];
 #pragma unroll
     for (int k = 0; k < 12; ++k) acc[k] = S(0);
@@ -575,10 +598,34 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
     wave_reduce12(acc, u0, u1);
     if (owner) {
       const S u = lo == 0 ? u0 : u1;
-      atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[wave][j]) * kGrad2D + kidx,
+      atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kidx,
                       finish_grad<R, S>(sp, kidx, u, u0, u1));
     }
     if constexpr (kCount) atomics += NV;
+  }
+}
+
+// One wavefront per bucket: with a.bucket_list (3D), wavefront i takes the i-th bucket of the
+// forward's list of buckets with blended entries, so buckets past their tile's last blended
+// entry cost no wavefront beyond reading the list length; without it, bucket i of the table.
+template <int R, typename S, bool kCount, bool kAbs = true, bool kList = false>
+__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(BlendArgs<S> a) {
+  __shared__ Staged<S> s_sp[kBwdWaves][kBucket];
+  __shared__ uint32_t s_m[kBwdWaves][kBucket];
+  __shared__ uint32_t s_id[kBwdWaves][kBucket];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t evals = 0, atomics = 0;
+  if constexpr (kList) {
+    // wavefronts past the list's length (the grid is sized for every bucket) leave at once
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
+    if (i < static_cast<int64_t>(a.bucket_list[0]))
+      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], evals,
+                                     atomics);
+  } else {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
+    if (b < a.n_buckets && !(a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)))
+      bwd_bucket<R, S, kCount, kAbs>(a, b, s_sp[wave], s_m[wave], s_id[wave], evals, atomics);
   }
   if constexpr (kCount) {
     if (lane == 0 && atomics) atomicAdd(a.counters, static_cast<unsigned long long>(atomics));
@@ -692,13 +739,21 @@ void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
     hipLaunchKernelGGL((blend_fwd_kernel<R, S, false>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
 }
 
-template <int R, typename S>
-void launch_bwd_bucket(const BlendArgs<S>& a, hipStream_t st) {
-  const unsigned blocks = static_cast<unsigned>((a.n_buckets + kBwdWaves - 1) / kBwdWaves);
-  if (a.counters)
-    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, true>), dim3(blocks), dim3(kBwdWaves * kWave), 0, st, a);
+template <int R, typename S, bool kCount, bool kAbs>
+void launch_bwd_bucket_k(const BlendArgs<S>& a, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((a.n_buckets + kBwdWaves - 1) / kBwdWaves));
+  if (a.bucket_list)
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, true>), grid, dim3(kBwdWaves * kWave), 0, st, a);
   else
-    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, false>), dim3(blocks), dim3(kBwdWaves * kWave), 0, st, a);
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, false>), grid, dim3(kBwdWaves * kWave), 0, st, a);
+}
+
+template <int R, typename S, bool kAbs = true>
+void launch_bwd_bucket(const BlendArgs<S>& a, hipStream_t st) {
+  if (a.counters)
+    launch_bwd_bucket_k<R, S, true, kAbs>(a, st);
+  else
+    launch_bwd_bucket_k<R, S, false, kAbs>(a, st);
 }
 
 template <int R, typename S>
@@ -751,7 +806,7 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
                                const uint32_t* point_list, const uint32_t* bucket_offsets,
                                int width, int height, const float* bg, float* image,
                                float* final_T, int32_t* n_contrib, uint32_t* tile_max,
-                               float* ckpt, void* stream) {
+                               float* ckpt, uint32_t* bucket_list, void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARG, "image size must be positive");
   // splat_rec, point_list and ckpt may be NULL when the scene has no instances; without ckpt
@@ -767,6 +822,10 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
   a.n_contrib = n_contrib;
   a.tile_max = tile_max;
   a.ckpt = ckpt;
+  GS_REQUIRE(!bucket_list || ckpt, GS_ERR_ARG, "bucket_list needs the checkpoints");
+  GS_REQUIRE(aligned(bucket_list, 16), GS_ERR_ALIGN, "bucket_list must be 16-byte aligned");
+  a.bucket_list = bucket_list;
+  if (bucket_list) fill_zero_f32(reinterpret_cast<float*>(bucket_list), kListHeader, as_stream(stream));
   launch_fwd<kRules3D, float>(a, as_stream(stream));
   return check_launch("blend_fwd_3d");
 }
@@ -792,7 +851,7 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
                                int width, int height, const float* image, const float* grad_image,
                                const float* final_T, const float* grad_alpha,
                                const int32_t* n_contrib, const uint32_t* tile_max,
-                               const float* ckpt, float* grad2d, int flags,
+                               const float* ckpt, uint32_t* bucket_list, float* grad2d, int flags,
                                unsigned long long* counters, void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0 && n >= 0 && n_buckets_max >= 0, GS_ERR_ARG,
@@ -823,7 +882,12 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
   a.grad_alpha = grad_alpha;
   a.grad_rec = grad2d;
   a.counters = counters;
-  launch_bwd_bucket<kRules3D, float>(a, st);
+  GS_REQUIRE(aligned(bucket_list, 16), GS_ERR_ALIGN, "bucket_list must be 16-byte aligned");
+  a.bucket_list = bucket_list;
+  if (flags & GS_ABS_GRAD)
+    launch_bwd_bucket<kRules3D, float, true>(a, st);
+  else
+    launch_bwd_bucket<kRules3D, float, false>(a, st);
   return check_launch("blend_bwd_3d");
 }
 

@@ -8,8 +8,8 @@ N(0,1) upstream image gradient. Inputs are resident in HBM before the timed regi
                     [--no-train-step]
     python bench.py --copy-probe      # a plain 1 GiB device copy, to calibrate HBM counters
 
-Prints ONE JSON line. Per-stage times come from HIP events recorded on the launch stream
-inside the timed region; `roofline` is for the kernel with the largest share of the step
+Prints ONE JSON line. `value` is the wall time of K plain steps; per-stage times come from
+HIP events recorded on the launch stream in a second pass over the same K steps; `roofline` is for the kernel with the largest share of the step
 (the bucketed blend backward), from its algorithmic bytes and its event-timed duration, plus
 its VALU issue rate from the committed SQ counter summary. `train_step` (secondary) times the
 full training step on the same scene: forward, L1 + D-SSIM loss, backward and fused Adam
@@ -54,7 +54,7 @@ def parse():
     return ap.parse_args()
 
 
-def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs):
+def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, atomics_per_pair=9):
     """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
     written once (fp32)."""
     n, m, K = fs.n, fs.m, fs.sh_coeffs
@@ -77,8 +77,9 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs):
         "blend_fwd": m * (4 + 64) + P * 20 + B * 4096 + 4 * T,
         "grad_zero": 48 * n,
         # per active bucket: checkpoints 4 KiB + grad image 12, image 12, n_contrib 4 per pixel;
-        # per bucket-splat step: id + record; per reduced bucket-splat: 11 fp32 atomics
-        "blend_bwd": active_buckets * (4096 + 256 * 28) + splat_steps * (4 + 64) + used_pairs * 44,
+        # per bucket-splat step: id + record; per reduced bucket-splat: 9 fp32 atomics (11 with
+        # the |dL/dmean2d| sums)
+        "blend_bwd": active_buckets * (4096 + 256 * 28) + splat_steps * (4 + 64) + used_pairs * 4 * atomics_per_pair,
         # params, SH, record and grad2d of the visible; every output row written
         "preprocess_bwd": n_visible * (44 + 12 * K + 64 + 48) + n * (44 + 12 * K),
     }
@@ -219,8 +220,9 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
 
 def variants_bench(sc, grads, steps: int, warmup: int) -> dict:
     """ms per view of the path's variants on the same scene and poses: the inference forward (no
-    backward state), the pruning-score blend (preprocess, binning, summed blending weights) and
-    fwd+bwd under proper antialiasing."""
+    backward state), the pruning-score blend (preprocess, binning, summed blending weights),
+    fwd+bwd under proper antialiasing, and fwd+bwd with the |dL/dmean2d| sums that densification
+    by absolute gradient reads."""
     import dataclasses
 
     import torch
@@ -244,11 +246,15 @@ def variants_bench(sc, grads, steps: int, warmup: int) -> dict:
 
     def aa_fwd_bwd(k):
         fs = R.forward_pass(*params, aa_cams[k % len(cams)])
-        R.backward_pass(fs, *params, grads[k % len(cams)])
+        R.backward_pass(fs, *params, grads[k % len(cams)], abs_grad=False)
+
+    def abs_fwd_bwd(k):
+        fs = R.forward_pass(*params, cams[k % len(cams)])
+        R.backward_pass(fs, *params, grads[k % len(cams)], abs_grad=True)
 
     out = {}
     for name, fn in (("inference_fwd", inference), ("pruning_scores", pruning),
-                     ("proper_antialiasing_fwd_bwd", aa_fwd_bwd)):
+                     ("proper_antialiasing_fwd_bwd", aa_fwd_bwd), ("abs_grad_fwd_bwd", abs_fwd_bwd)):
         for k in range(warmup):
             fn(k)
         torch.cuda.synchronize()
@@ -306,20 +312,31 @@ def main():
     def step(k, timer=None, counters=None):
         pose = k % len(cams)
         fs = R.forward_pass(*params, cams[pose], sh_degree=None, timing=timer if timer else False)
-        out = R.backward_pass(fs, *params, grads[pose], timing=timer if timer else False, counters=counters)
+        out = R.backward_pass(fs, *params, grads[pose], timing=timer if timer else False, counters=counters,
+                              abs_grad=False)
         return fs, out
 
     for k in range(args.warmup):
         step(k)
     torch.cuda.synchronize()
 
-    timers = [R.StageTimer(True) for _ in range(args.steps)]
+    # the timed region: K steps, nothing recorded between the stages
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
-        step(k, timers[k])
+        step(k)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+
+    # the per-stage breakdown: the same K steps again with HIP events between the stages (the
+    # events cost a few microseconds each, so this pass is not the headline number)
+    timers = [R.StageTimer(True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for k in range(args.steps):
+        step(k, timers[k])
+    torch.cuda.synchronize()
+    staged_wall_ms = (time.perf_counter() - t1) * 1000.0 / args.steps
 
     per_stage = {}
     step_ms = []
@@ -336,7 +353,7 @@ def main():
     torch.cuda.synchronize()
     n_visible = int((fs.touched > 0).sum().item())
     active_buckets, splat_steps = bucket_stats(fs)
-    used_pairs = int(ctr[0].item()) // 11
+    used_pairs = int(ctr[0].item()) // 9
     evals = int(ctr[2].item())
     sb = stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs)
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
@@ -371,6 +388,7 @@ def main():
         "stage_hbm_gbs": {k2: round(v, 1) for k2, v in stage_gbs.items()},
         "stage_hbm_frac": {k2: round(v / HBM_PEAK_GBS, 4) for k2, v in stage_gbs.items()},
         "event_sum_ms": round(statistics.mean(step_ms), 4),
+        "staged_pass_ms_per_step": round(staged_wall_ms, 4),
         "counts": {"visible": n_visible, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
                    "active_buckets": active_buckets, "bucket_splat_steps": splat_steps,
                    "reduced_bucket_splats": used_pairs, "bwd_pair_evals": evals},

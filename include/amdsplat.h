@@ -158,14 +158,18 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
  *   tile; ckpt [n_buckets, 256, 4] = (C.r, C.g, C.b, T) at the start of every 32-entry
  *   bucket. bg is host memory (3 floats) or NULL for black. splat_rec, point_list and ckpt
  *   may be NULL when there are no instances (every tile range empty).
+ *   bucket_list (NULL, or 16-byte aligned uint32 [4 + n_buckets_max] with the bound of
+ *   gs_bucket_fill; needs ckpt): receives the buckets the backward reads (those starting before
+ *   their tile's tile_max) for gs_blend_bwd_3d: [0] their number, [4 ...] their indices in any
+ *   order.
  *   Inference (Faster-GS's inference blend, upstream/upstream_main_kernels.patch:131-150):
- *   ckpt NULL, and then bucket_offsets, n_contrib and tile_max may be NULL too; image and
- *   final_T are the same bits as with them.
+ *   ckpt NULL, and then bucket_offsets, n_contrib, tile_max and bucket_list may be NULL too;
+ *   image and final_T are the same bits as with them.
  * ------------------------------------------------------------------------------------- */
 int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, int width, int height, const float* bg,
                     float* image, float* final_T, int32_t* n_contrib, uint32_t* tile_max,
-                    float* ckpt, void* stream);
+                    float* ckpt, uint32_t* bucket_list, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Pruning scores (replaces Faster-GS's pruning-score blend, kernels_pruning_scores.cuh, seen
@@ -180,20 +184,25 @@ int gs_blend_scores_3d(const float* splat_rec, const uint32_t* ranges, const uin
 /* ---------------------------------------------------------------------------------------
  * 3D bucketed blend backward (replaces blend_backward_cu / blend_backward_macro_cu,
  * phase1/fastergs_macro.patch:40-314). One wavefront per bucket; grad2d [n,12] receives
- * dL/d(mean2d, conic A B C, opacity, colour) and |dL/dmean2d| (slots 9-10). It is zeroed by
- * the call unless flags has GS_ACCUMULATE (then the call adds to it, e.g. over views).
+ * dL/d(mean2d, conic A B C, opacity, colour) and, with GS_ABS_GRAD in flags, |dL/dmean2d|
+ * (slots 9-10; Faster-GS's compute_abs_grad instantiation, phase1/fastergs_macro.patch:206-209).
+ * It is zeroed by the call unless flags has GS_ACCUMULATE (then the call adds to it, e.g. over
+ * views).
  * n_buckets is read on device from bucket_offsets[T]; n_buckets_max bounds the grid.
  * grad_alpha [H,W] (may be NULL) is the gradient of the alpha = 1 - final_T output.
- * counters: NULL or 3 device uint64 that receive the atomic adds issued (11 per reduced
- * bucket-splat) and, in [2], the (pixel, splat) pairs evaluated.
+ * bucket_list: the forward's (or NULL): only the listed buckets are processed (the others
+ * have no blended entry); NULL: every bucket of the table is examined.
+ * counters: NULL or 3 device uint64 that receive the atomic adds issued (9 per reduced
+ * bucket-splat, 11 with GS_ABS_GRAD) and, in [2], the (pixel, splat) pairs evaluated.
  * ------------------------------------------------------------------------------------- */
-enum { GS_ACCUMULATE = 1 };
+enum { GS_ACCUMULATE = 1, GS_ABS_GRAD = 2 };
 int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, const uint32_t* bucket_to_tile,
                     int64_t n_buckets_max, int64_t n, int width, int height, const float* image,
                     const float* grad_image, const float* final_T, const float* grad_alpha,
                     const int32_t* n_contrib, const uint32_t* tile_max, const float* ckpt,
-                    float* grad2d, int flags, unsigned long long* counters, void* stream);
+                    uint32_t* bucket_list, float* grad2d, int flags, unsigned long long* counters,
+                    void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 3D preprocess backward (replaces Faster-GS preprocess_backward_cu, csv:4): chains grad2d

@@ -417,3 +417,23 @@ def test_pruning_scores_sum_to_image_alpha_full_size():
     total = float(s.double().sum())
     assert total > 0.05 * cam.width * cam.height
     np.testing.assert_allclose(total, float(alpha.double().sum()), rtol=1e-4)
+
+
+def test_backward_over_bucket_list_equals_bucket_table():
+    """The backward over the forward's list of buckets with blended entries gives the gradients
+    of the backward that examines every bucket of the table (atomic order aside), also when
+    run twice on one forward."""
+    sc = make("heavy_overlap", seed=19)  # opaque enough that some buckets are past every pixel's end
+    cam = sc.cameras[0]
+    p, fs = gpu_forward(sc, 3, cam=cam)
+    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(5)).cuda()
+    listed = [R.backward_pass(fs, *p, gi) for _ in range(2)]
+    table = R.backward_pass(dataclasses.replace(fs, bucket_list=None), *p, gi)
+    torch.cuda.synchronize()
+    n_list = int(fs.bucket_list[0].item())
+    assert 0 < n_list < fs.n_buckets
+    ids = np.sort(np_(fs.bucket_list[4:4 + n_list]).astype(np.int64))
+    assert np.array_equal(np.unique(ids), ids)  # no bucket listed twice
+    for out in listed:
+        for a, b in zip(out[:6], table[:6]):
+            assert D.rel_err(np_(a), np_(b)) < 1e-6
