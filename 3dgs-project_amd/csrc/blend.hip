@@ -385,9 +385,6 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
       C = s.s2;
     }
     // power = -1/2 (A dx^2 + 2 B dx dy + C dy^2), d = mean - pixel
-    if constexpr (R == kRules3D) {
-      if (k == 5) return u * __builtin_amdgcn_rcpf(s.o);  // 3D: u = sum alpha dL/dalpha
-    }
     if (k == 0) return -fma(A, u0, B * u1);
     if (k == 1) return -fma(B, u0, C * u1);
     if (k == 2 || k == 4) return S(-0.5) * u;
@@ -504,6 +501,13 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     int lim_row[kPixPerLane];
 #pragma unroll
     for (int r = 0; r < kPixPerLane; ++r) lim_row[r] = __builtin_amdgcn_readfirstlane(wave_max(lim[r]));
+    // the final gradient of the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total):
+    // k 0, 1 (mean2d): -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity):
+    // u / o; colour and |dL/dmean2d|: u. The lane-constant parts are chosen once here.
+    const bool k0 = kidx == 0, k1 = kidx == 1, k5 = kidx == 5;
+    const float kc = (kidx == 2 || kidx == 4) ? -0.5f : kidx == 3 ? -1.0f : kidx >= 6 ? 1.0f : 0.0f;
+    const bool live_owner = owner && (kAbs || kidx < 9);
+    const int64_t kofs = kidx;
     for (int j = 0; j < jmax; ++j) {
       const Staged<S> sp = s_sp[j];
       const uint32_t m = __builtin_amdgcn_readfirstlane(s_m[j]);  // wave-uniform: scalar tests
@@ -550,11 +554,11 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       S acc[12] = {dxsh, shy, cl.dx * dxsh, cl.dx * shy, shyy, sh, cr, cg, cb, ab0, ab1, 0.0f};
       S u0, u1;
       wave_reduce12(acc, u0, u1);
-      if (owner && (kAbs || kidx < 9)) {
-        const S u = lo == 0 ? u0 : u1;
-        atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kidx,
-                        finish_grad<R, S>(sp, kidx, u, u0, u1));
-      }
+      const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : 0.0f;
+      const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : 0.0f;
+      const float c = k5 ? __builtin_amdgcn_rcpf(sp.o) : kc;
+      const float g = fmaf(c0, u0, fmaf(c1, u1, c * (lo == 0 ? u0 : u1)));
+      if (live_owner) atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kofs, g);
       if constexpr (kCount) atomics += kAbs ? NV : 9;
     }
   } else
