@@ -481,7 +481,7 @@ __global__ void emit_windows_kernel(const uint32_t* __restrict__ offs, int64_t n
 }
 
 struct EmitSetup {
-  float mx, my, A, B, det, tA, vmax, vr;  // 3D band setup
+  float mx, my, invA, B, det, tA, vmax, vr;  // 3D band setup (what band_columns reads)
   int4 d;                                 // 3D: pixel bounds; rectangles: clamped tile rectangle
 };
 
@@ -536,7 +536,7 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
         const float4 a = rec[g].a, b = rec[g].b;
         const int4 d = rec[g].d;
         const BandSetup bs = band_setup(a, b);
-        es.mx = bs.mx; es.my = bs.my; es.A = bs.A; es.B = bs.B;
+        es.mx = bs.mx; es.my = bs.my; es.invA = bs.invA; es.B = bs.B;
         es.det = bs.det; es.tA = bs.tA; es.vmax = bs.vmax; es.vr = bs.vr;
         es.d = d;
         rows = static_cast<uint32_t>(max(d.w / kTile - d.z / kTile + 1, 0));
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
             nt = static_cast<uint32_t>(e.d.z - e.d.x);
           } else {
             BandSetup bs;
-            bs.mx = e.mx; bs.my = e.my; bs.A = e.A; bs.B = e.B;
+            bs.mx = e.mx; bs.my = e.my; bs.A = 0.0f; bs.invA = e.invA; bs.B = e.B;
             bs.det = e.det; bs.tA = e.tA; bs.vmax = e.vmax; bs.vr = e.vr;
             bs.ok = e.det > 0.0f;
             ty = e.d.z / kTile + r;

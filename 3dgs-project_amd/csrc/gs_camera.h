@@ -27,7 +27,7 @@ struct CamK {
 // a closed form; the splat touches the tiles that own a pixel column c (inside its bounds)
 // with c + 0.5 in [xl, xr]. Cost is O(tile rows) per splat instead of O(tiles).
 struct BandSetup {
-  float mx, my, A, B, det, tA, vmax, vr;
+  float mx, my, A, B, det, tA, vmax, vr, invA;
   bool ok;
 };
 
@@ -42,9 +42,12 @@ __device__ __forceinline__ BandSetup band_setup(const float4 a, const float4 b) 
   s.det = fmaf(s.A, C, -(s.B * s.B));
   s.ok = s.det > 0.0f;
   s.tA = t2 * s.A;
-  s.vmax = sqrtf(s.tA / s.det);  // half height of the ellipse
+  // reciprocals once per splat, so the per-row work below has no division
+  const float idet = 1.0f / s.det;
+  s.invA = 1.0f / s.A;
+  s.vmax = sqrtf(s.tA * idet);  // half height of the ellipse
   // the rightmost point of the ellipse is (ur, vr) relative to the mean
-  const float ur = sqrtf((t2 * C) / s.det);
+  const float ur = sqrtf((t2 * C) * idet);
   s.vr = -((s.B / C) * ur);
   return s;
 }
@@ -61,11 +64,11 @@ __device__ __forceinline__ bool band_columns(const BandSetup& s, float Y0, float
   const float vc = fminf(fmaxf(s.vr, v0), v1);
   const float dr = fmaxf(fmaf(-s.det, vc * vc, s.tA), 0.0f);
   const float br = s.B * vc;
-  const float xr = s.mx + (sqrtf(dr) - br) / s.A;
+  const float xr = s.mx + (sqrtf(dr) - br) * s.invA;
   const float vl = fminf(fmaxf(-s.vr, v0), v1);
   const float dl = fmaxf(fmaf(-s.det, vl * vl, s.tA), 0.0f);
   const float bl = s.B * vl;
-  const float xl = s.mx + (-bl - sqrtf(dl)) / s.A;
+  const float xl = s.mx + (-bl - sqrtf(dl)) * s.invA;
   const float f0 = fmaxf(ceilf(xl - 0.5f), static_cast<float>(bx0));
   const float f1 = fminf(floorf(xr - 0.5f), static_cast<float>(bx1));
   if (!(f0 <= f1)) return false;

@@ -336,8 +336,9 @@ int or_band_columns(float mx, float my, float A, float B, float C, float thr, fl
   float det = fmaf(A, C, -(B * B));
   if (!(det > 0.0f)) return 0;
   float tA = t2 * A;
-  float vmax = sqrtf(tA / det);
-  float ur = sqrtf((t2 * C) / det);
+  float idet = 1.0f / det, invA = 1.0f / A;
+  float vmax = sqrtf(tA * idet);
+  float ur = sqrtf((t2 * C) * idet);
   float vr = -((B / C) * ur);
   float v0 = fmaxf(Y0 - my, -vmax);
   float v1 = fminf(Y1 - my, vmax);
@@ -345,11 +346,11 @@ int or_band_columns(float mx, float my, float A, float B, float C, float thr, fl
   float vc = fminf(fmaxf(vr, v0), v1);
   float dr = fmaxf(fmaf(-det, vc * vc, tA), 0.0f);
   float br = B * vc;
-  float xr = mx + (sqrtf(dr) - br) / A;
+  float xr = mx + (sqrtf(dr) - br) * invA;
   float vl = fminf(fmaxf(-vr, v0), v1);
   float dl = fmaxf(fmaf(-det, vl * vl, tA), 0.0f);
   float bl = B * vl;
-  float xl = mx + (-bl - sqrtf(dl)) / A;
+  float xl = mx + (-bl - sqrtf(dl)) * invA;
   float f0 = fmaxf(ceilf(xl - 0.5f), (float)bx0);
   float f1 = fminf(floorf(xr - 0.5f), (float)bx1);
   if (!(f0 <= f1)) return 0;
