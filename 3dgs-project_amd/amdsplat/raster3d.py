@@ -197,8 +197,8 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
-    call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ptr(order), ptr(offsets), ptr(ws), ws.numel(),
-         st)
+    call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
+         ws.numel(), st)
     tm.mark("depth_order")
     m = int(offsets[n].item()) if n > 0 else 0  # host readback: instance count
     keys = torch.empty(m if keep_keys else 0, dtype=torch.int64, device=dev)

@@ -251,14 +251,24 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_cnt[0][0])[k] = 0;
+  constexpr int DPT = (R + kRsThreads - 1) / kRsThreads;  // consecutive digits per thread (1 or 2)
   {
     // global start of (digit, tile): keys with a smaller digit + keys of the digit in earlier tiles
-    static_assert(kRsThreads >= 256, "a thread per digit");
-    const int d = threadIdx.x;
-    const uint32_t t = d < R ? totals[d] : 0u;
+    uint32_t t[DPT], tsum = 0;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      const int d = static_cast<int>(threadIdx.x) * DPT + e;
+      t[e] = d < R ? totals[d] : 0u;
+      tsum += t[e];
+    }
     uint32_t all;
-    const uint32_t incl = block_inclusive_scan(t, s_wave, all);
-    if (d < R) s_goff[d] = incl - t + tile_offs[static_cast<int64_t>(d) * n_tiles + blockIdx.x];
+    uint32_t run = block_inclusive_scan(tsum, s_wave, all) - tsum;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      const int d = static_cast<int>(threadIdx.x) * DPT + e;
+      if (d < R) s_goff[d] = run + tile_offs[static_cast<int64_t>(d) * n_tiles + blockIdx.x];
+      run += t[e];
+    }
   }
   __syncthreads();
   const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kTileKeys;
@@ -284,18 +294,32 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
   }
   __syncthreads();
   // digit totals of the tile -> wavefront offsets inside each digit, digit starts in the tile
-  uint32_t total = 0;
-  for (int d = threadIdx.x; d < R; d += kRsThreads) {
+  {
+    uint32_t dt[DPT], tsum = 0;
 #pragma unroll
-    for (int w = 0; w < kRsWaves; ++w) {
-      const uint32_t c = s_cnt[w][d];
-      s_cnt[w][d] = total;
-      total += c;
+    for (int e = 0; e < DPT; ++e) {
+      const int d = static_cast<int>(threadIdx.x) * DPT + e;
+      uint32_t acc = 0;
+      if (d < R) {
+#pragma unroll
+        for (int w = 0; w < kRsWaves; ++w) {
+          const uint32_t c = s_cnt[w][d];
+          s_cnt[w][d] = acc;
+          acc += c;
+        }
+      }
+      dt[e] = acc;
+      tsum += acc;
+    }
+    uint32_t all;
+    uint32_t run = block_inclusive_scan(tsum, s_wave, all) - tsum;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) {
+      const int d = static_cast<int>(threadIdx.x) * DPT + e;
+      if (d < R) s_excl[d] = run;
+      run += dt[e];
     }
   }
-  uint32_t all;
-  const uint32_t incl = block_inclusive_scan(total, s_wave, all);
-  if (static_cast<int>(threadIdx.x) < R) s_excl[threadIdx.x] = incl - total;
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < ROUNDS; ++r) {
@@ -321,17 +345,22 @@ struct SortPlan {
   int passes, bits;
 };
 
+// Digits of at most kRsMaxBits bits (a 512-bin histogram per wavefront still fits LDS
+// comfortably): 27-bit depth keys take 3 passes, 13-bit tile keys 2.
+constexpr int kRsMaxBits = 9;
+constexpr int kRsMaxPasses = 4;  // 32-bit keys
+
 static SortPlan sort_plan(int bits) {
   SortPlan p;
-  p.passes = bits <= 0 ? 0 : (bits + 7) / 8;
+  p.passes = bits <= 0 ? 0 : (bits + kRsMaxBits - 1) / kRsMaxBits;
   p.bits = p.passes ? (bits + p.passes - 1) / p.passes : 0;
   return p;
 }
 
 static size_t sort_ws(int64_t m) {
   const int64_t nt = (m + kRsMinTile - 1) / kRsMinTile;
-  const int64_t hist = 256 * (nt > 0 ? nt : 1);
-  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(4 * 256 * 4);
+  const int64_t hist = (int64_t(1) << kRsMaxBits) * (nt > 0 ? nt : 1);
+  return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(kRsMaxPasses * (1 << kRsMaxBits) * 4);
 }
 
 template <int BITS, int ROUNDS>
@@ -381,7 +410,7 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
   uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
   ws += align_up(m * 4);
   uint32_t* tile_hist = reinterpret_cast<uint32_t*>(ws);
-  ws += align_up(static_cast<int64_t>(256) * n_tiles * 4);
+  ws += align_up((static_cast<int64_t>(1) << kRsMaxBits) * n_tiles * 4);
   uint32_t* totals = reinterpret_cast<uint32_t*>(ws);
   // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
   // the last pass lands in (k_out, v_out) and no pass works in place
@@ -391,7 +420,7 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     const bool to_out = ((plan.passes - 1 - p) % 2) == 0;
     uint32_t* dst_k = to_out ? k_out : k_alt;
     uint32_t* dst_v = to_out ? v_out : v_alt;
-    uint32_t* tot = totals + 256 * p;
+    uint32_t* tot = totals + (1 << kRsMaxBits) * p;
     const int shift = plan.bits * p;
     switch (plan.bits) {
       case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
@@ -401,7 +430,8 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
       case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
       case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
       case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      default: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 8: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      default: sort_pass<9>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
     }
     src_k = dst_k;
     src_v = dst_v;
@@ -737,10 +767,12 @@ __global__ __launch_bounds__(kBoThreads) void bucket_offsets_kernel(uint32_t* __
 }
 
 // Full 64-bit keys of the sorted instances (tile << 32 | depth key), for callers that want them.
+// (tile << 32 | depth order key); dkey0 is added back to keys stored relative to it.
 __global__ void full_keys_kernel(const uint32_t* __restrict__ tkeys, const uint32_t* __restrict__ vals,
-                                 const uint32_t* __restrict__ dkey_of, int64_t m, uint64_t* __restrict__ out) {
+                                 const uint32_t* __restrict__ dkey_of, uint32_t dkey0, int64_t m,
+                                 uint64_t* __restrict__ out) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (p < m) out[p] = (static_cast<uint64_t>(tkeys[p]) << 32) | dkey_of[vals[p]];
+  if (p < m) out[p] = (static_cast<uint64_t>(tkeys[p]) << 32) | (dkey_of[vals[p]] + dkey0);
 }
 
 // One thread per bucket slot: binary search of the tile whose bucket range holds b.
@@ -793,8 +825,8 @@ static size_t emit_ws(int64_t m) {
 // from rec / depth / depth64; none of them: index order) and, if offsets is not NULL, the
 // exclusive scan of their instance counts in that order (offsets[n] = m).
 static void bin_prepare(const SplatRec* rec, const float* depth, const double* depth64, const uint32_t* keys_in,
-                        const uint32_t* counts, int64_t n, uint32_t* order, uint32_t* offsets, char* ws,
-                        hipStream_t st) {
+                        int key_bits, const uint32_t* counts, int64_t n, uint32_t* order, uint32_t* offsets,
+                        char* ws, hipStream_t st) {
   uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
   uint32_t* dsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
   uint32_t* khi = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
@@ -807,6 +839,7 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
   }
   if (keys_in || rec || depth || depth64) {
     const uint32_t* keys = keys_in;
+    int bits = keys_in ? key_bits : 32;
     if (!keys) {
       hipLaunchKernelGGL(depth_keys_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, rec, depth, depth64,
                          counts, n, dkeys, depth64 ? khi : nullptr);
@@ -818,7 +851,7 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
       hipLaunchKernelGGL(gather_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, khi, tmpv, n, dkeys);
       radix_sort(dkeys, tmpv, dsorted, order, n, 32, sort_scratch, st);
     } else {
-      radix_sort(keys, nullptr, dsorted, order, n, 32, sort_scratch, st);
+      radix_sort(keys, nullptr, dsorted, order, n, bits, sort_scratch, st);
     }
   } else {
     hipLaunchKernelGGL(iota_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, n);
@@ -828,7 +861,8 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
 
 // Emission of the instances in depth order, stable sort by tile, tile ranges and bucket
 // offsets. dkey_of [n]: the depth key of every Gaussian (only read for sorted_keys).
-static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, const uint32_t* order,
+static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
+                     const uint32_t* order,
                      const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
                      uint32_t* bucket_offsets, char* ws, hipStream_t st) {
@@ -851,7 +885,7 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
     radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
-                         dkey_of, m, sorted_keys);
+                         dkey_of, dkey0, m, sorted_keys);
     hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, n_tiles, ranges);
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
@@ -883,9 +917,10 @@ extern "C" int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* w
 extern "C" size_t gs_bin_prepare_workspace_size(int64_t n) { return prep_ws(n < 0 ? 0 : n); }
 
 extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched,
-                                 const uint32_t* depth_keys, int64_t n, uint32_t* order, uint32_t* offsets,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
+                                 const uint32_t* depth_keys, int64_t n, const gs_camera* cam, uint32_t* order,
+                                 uint32_t* offsets, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
+  if (int e = check_cam(cam)) return e;
   GS_REQUIRE(n >= 0 && n < (int64_t(1) << 32) && offsets, GS_ERR_ARG, "invalid bin_prepare arguments");
   GS_REQUIRE(n == 0 || (tiles_touched && order && (depth_keys || splat_rec)), GS_ERR_ARG,
              "null pointer argument");
@@ -894,7 +929,8 @@ extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_t
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "bin_prepare workspace too small: need %zu bytes", need);
   bin_prepare(depth_keys ? nullptr : reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, depth_keys,
-              tiles_touched, n, order, offsets, static_cast<char*>(workspace), as_stream(stream));
+              depth_key_bits(make_cam(*cam)), tiles_touched, n, order, offsets, static_cast<char*>(workspace),
+              as_stream(stream));
   return check_launch("bin_prepare_3d");
 }
 
@@ -924,7 +960,8 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   GS_REQUIRE(m == 0 || (splat_rec && order && offsets && point_list), GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(!(sorted_keys && m > 0 && !depth_keys), GS_ERR_ARG, "sorted_keys need depth_keys");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
-  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, order, offsets, n, k.tiles_x, n_tiles,
+  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, order, offsets, n, k.tiles_x,
+           n_tiles,
            m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, static_cast<char*>(workspace),
            as_stream(stream));
   return check_launch("bin_fill_3d");
@@ -970,11 +1007,11 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   uint32_t* ord = order ? order : reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
   uint32_t* offs = reinterpret_cast<uint32_t*>(ws); ws += align_up((n + 1) * 4);
   if (n > 0 && (m > 0 || order)) {
-    bin_prepare(nullptr, d32, d64, nullptr, counts, n, ord, m > 0 ? offs : nullptr, prep, st);
+    bin_prepare(nullptr, d32, d64, nullptr, 32, counts, n, ord, m > 0 ? offs : nullptr, prep, st);
     if (sorted_keys && m > 0 && !d32)  // index order: the depth part of the keys is 0
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
   }
-  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, ord, offs, n, tiles_x, n_tiles, m, sorted_keys,
+  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, n_tiles, m, sorted_keys,
            point_list, ranges, tile_offsets, bucket_offsets, ws, st);
   return check_launch("bin_fill_rect");
 }

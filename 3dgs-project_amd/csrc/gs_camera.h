@@ -19,6 +19,10 @@ struct CamK {
   float lim_x_lo, lim_x_hi, lim_y_lo, lim_y_hi;  // clamp of x/z and y/z for the EWA Jacobian
   int tiles_x, tiles_y;
   int flags;  // GS_CAM_* bits
+  // depth sort keys are order keys relative to the near plane's: a visible Gaussian
+  // (near < z < far) gets key(z) - dkey0 in [1, dkey_cull), a culled one dkey_cull, so the
+  // sort needs only bit_width(dkey_cull) bits (27 for near/far = 0.01/100)
+  uint32_t dkey0, dkey_cull;
 };
 
 // Tile assignment. A tile row is a horizontal band of pixel-centre rows [Y0, Y1] (the

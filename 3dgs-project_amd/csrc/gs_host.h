@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
+#include <string.h>
 #include <string>
 
 #include "../../include/amdsplat.h"
@@ -35,6 +36,21 @@ inline bool aligned(const void* p, size_t a) {
   return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
 
+// Host twin of float_order_key (the 32-bit key whose unsigned order is the float order).
+inline uint32_t host_order_key(float v) {
+  uint32_t u;
+  v = v + 0.0f;
+  memcpy(&u, &v, 4);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Bits the 3D depth sort needs for the keys of gs_preprocess_fwd (see CamK::dkey_cull).
+inline int depth_key_bits(const CamK& k) {
+  int b = 0;
+  while (b < 32 && (k.dkey_cull >> b) != 0u) ++b;
+  return b;
+}
+
 // Builds the kernel camera. Derived values are computed in double and rounded once, the
 // same way the CPU oracle derives them.
 inline CamK make_cam(const gs_camera& c) {
@@ -63,6 +79,8 @@ inline CamK make_cam(const gs_camera& c) {
   k.lim_y_hi = static_cast<float>(1.3 * (static_cast<double>(c.height) - c.cy) / c.fy);
   k.tiles_x = (c.width + kTile - 1) / kTile;
   k.tiles_y = (c.height + kTile - 1) / kTile;
+  k.dkey0 = host_order_key(c.near_plane);
+  k.dkey_cull = host_order_key(c.far_plane) - k.dkey0;
   return k;
 }
 

@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   if (valid) {
     tiles_touched[i] = g.vis ? count : 0u;
     // depth sort key: the orderable bits of the view depth, culled Gaussians last
-    if (depth_keys) depth_keys[i] = g.vis ? float_order_key(rb.z) : 0xffffffffu;
+    if (depth_keys) depth_keys[i] = g.vis ? float_order_key(rb.z) - cam.dkey0 : cam.dkey_cull;
     if (g.vis) {
       SplatRec r;
       r.a = ra;

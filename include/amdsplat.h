@@ -107,7 +107,9 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  * stable radix sort by tile of the instances emitted in that order.
  *
  * gs_bin_prepare_3d: depth ordering.
- *   depth_keys [n] from gs_preprocess_fwd, or NULL (then computed from splat_rec).
+ *   depth_keys [n] from gs_preprocess_fwd with the same camera (order keys of the view depth
+ *   relative to the near plane's, culled Gaussians after every visible one, so the sort reads
+ *   only as many bits as the near/far range needs), or NULL (then computed from splat_rec).
  *   out: order [n]        Gaussian indices by depth key, stable (culled Gaussians last)
  *        offsets [n + 1]  exclusive scan of tiles_touched[order[j]]; offsets[n] = m, the
  *                         number of instances (the caller reads it)
@@ -122,8 +124,8 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  * ------------------------------------------------------------------------------------- */
 size_t gs_bin_prepare_workspace_size(int64_t n);
 int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched, const uint32_t* depth_keys,
-                      int64_t n, uint32_t* order, uint32_t* offsets, void* workspace,
-                      size_t workspace_bytes, void* stream);
+                      int64_t n, const gs_camera* cam, uint32_t* order, uint32_t* offsets,
+                      void* workspace, size_t workspace_bytes, void* stream);
 size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles);
 int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
                    const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
