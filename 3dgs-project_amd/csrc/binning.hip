@@ -670,33 +670,58 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
   }
 }
 
-// Per-tile [start, end) of the sorted instances from the key changes: the thread at the first
-// instance of a tile writes its start (and gives the empty tiles before it the empty range at
-// that position), the thread at its last instance writes its end (and closes the empty tiles
-// after the last tile at m).
-__global__ void tile_bounds_kernel(const uint32_t* __restrict__ tkeys, int64_t m, int n_tiles,
-                                   uint32_t* __restrict__ ranges) {
-  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (p >= m) return;
-  const uint32_t t = tkeys[p];
-  if (t >= static_cast<uint32_t>(n_tiles)) return;  // not a tile id
-  const uint32_t pos = static_cast<uint32_t>(p);
-  const uint32_t prev = p > 0 ? tkeys[p - 1] : 0u;
-  if (p == 0 || prev != t) {
-    const uint32_t lo = p == 0 ? 0u : (prev < t ? prev + 1u : t);
-    for (uint32_t u = lo; u < t; ++u) {
-      ranges[2 * u] = pos;
-      ranges[2 * u + 1] = pos;
+// Per-tile [start, end) of the sorted instances from the key changes: the instance that
+// starts a tile writes its start (and gives the empty tiles before it the empty range at that
+// position), the one that ends a tile writes its end (and closes the empty tiles after the
+// last tile at m). Each thread takes kBoundsPer consecutive keys (16-byte loads).
+constexpr int kBoundsPer = 16;
+
+__global__ __launch_bounds__(256) void tile_bounds_kernel(const uint32_t* __restrict__ tkeys, int64_t m,
+                                                          int n_tiles, uint32_t* __restrict__ ranges) {
+  const int64_t p0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * kBoundsPer;
+  if (p0 >= m) return;
+  uint32_t k[kBoundsPer + 2];  // k[0] = key p0 - 1, k[1 + e] = key p0 + e, k[kBoundsPer + 1] = key p0 + kBoundsPer
+  const int cnt = static_cast<int>(min<int64_t>(kBoundsPer, m - p0));
+  if (cnt == kBoundsPer) {
+    const uint4* v = reinterpret_cast<const uint4*>(tkeys + p0);
+#pragma unroll
+    for (int q = 0; q < kBoundsPer / 4; ++q) {
+      const uint4 x = v[q];
+      k[1 + 4 * q] = x.x;
+      k[2 + 4 * q] = x.y;
+      k[3 + 4 * q] = x.z;
+      k[4 + 4 * q] = x.w;
     }
-    ranges[2 * t] = pos;
+  } else {
+#pragma unroll
+    for (int e = 0; e < kBoundsPer; ++e) k[1 + e] = e < cnt ? tkeys[p0 + e] : 0u;
   }
-  const bool last = p == m - 1;
-  if (last || tkeys[p + 1] != t) {
-    ranges[2 * t + 1] = pos + 1u;
-    if (last) {
-      for (uint32_t u = t + 1u; u < static_cast<uint32_t>(n_tiles); ++u) {
-        ranges[2 * u] = pos + 1u;
-        ranges[2 * u + 1] = pos + 1u;
+  k[0] = p0 > 0 ? tkeys[p0 - 1] : 0u;
+  k[kBoundsPer + 1] = p0 + kBoundsPer < m ? tkeys[p0 + kBoundsPer] : 0u;
+#pragma unroll
+  for (int e = 0; e < kBoundsPer; ++e) {
+    if (e >= cnt) break;
+    const int64_t p = p0 + e;
+    const uint32_t t = k[1 + e];
+    if (t >= static_cast<uint32_t>(n_tiles)) continue;  // not a tile id
+    const uint32_t pos = static_cast<uint32_t>(p);
+    const uint32_t prev = k[e];
+    if (p == 0 || prev != t) {
+      const uint32_t lo = p == 0 ? 0u : (prev < t ? prev + 1u : t);
+      for (uint32_t u = lo; u < t; ++u) {
+        ranges[2 * u] = pos;
+        ranges[2 * u + 1] = pos;
+      }
+      ranges[2 * t] = pos;
+    }
+    const bool last = p == m - 1;
+    if (last || k[2 + e] != t) {
+      ranges[2 * t + 1] = pos + 1u;
+      if (last) {
+        for (uint32_t u = t + 1u; u < static_cast<uint32_t>(n_tiles); ++u) {
+          ranges[2 * u] = pos + 1u;
+          ranges[2 * u + 1] = pos + 1u;
+        }
       }
     }
   }
@@ -886,7 +911,8 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
                          dkey_of, dkey0, m, sorted_keys);
-    hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, m, n_tiles, ranges);
+    hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for((m + kBoundsPer - 1) / kBoundsPer, 256)), dim3(256), 0, st,
+                       tsorted, m, n_tiles, ranges);
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
                      tile_offsets);

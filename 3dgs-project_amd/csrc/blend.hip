@@ -609,10 +609,11 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
   }
 }
 
-// One wavefront per bucket: with a.bucket_list (3D), wavefront i takes the i-th bucket of the
-// forward's list of buckets with blended entries, so buckets past their tile's last blended
-// entry cost no wavefront beyond reading the list length; without it, bucket i of the table.
-template <int R, typename S, bool kCount, bool kAbs = true, bool kList = false>
+// kList 0: wavefront i takes bucket i of the table. With a.bucket_list (3D), the forward's list
+// of the buckets with blended entries: kList 1, wavefront i takes entry i (a wavefront past the
+// list's length only reads that length); kList 2, a bounded grid strides over the list (the
+// loop keeps more registers live, so it is used only when the table is much longer).
+template <int R, typename S, bool kCount, bool kAbs = true, int kList = 0>
 __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(BlendArgs<S> a) {
   __shared__ Staged<S> s_sp[kBwdWaves][kBucket];
   __shared__ uint32_t s_m[kBwdWaves][kBucket];
@@ -620,10 +621,17 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(Ble
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   uint32_t evals = 0, atomics = 0;
-  if constexpr (kList) {
-    // wavefronts past the list's length (the grid is sized for every bucket) leave at once
+  if constexpr (kList == 1) {
+    // one wavefront per list entry; wavefronts past the list's length leave at once
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
     if (i < static_cast<int64_t>(a.bucket_list[0]))
+      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], evals,
+                                     atomics);
+  } else if constexpr (kList == 2) {
+    // a bounded grid strides over the list (for bucket tables far longer than the list)
+    const int64_t cnt = a.bucket_list[0];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBwdWaves;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave; i < cnt; i += stride)
       bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], evals,
                                      atomics);
   } else {
@@ -743,13 +751,24 @@ void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
     hipLaunchKernelGGL((blend_fwd_kernel<R, S, false>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
 }
 
+// Workgroups of the striding list-driven backward: every CU holds its share several times
+// over. Tables longer than kBwdStrideFrom workgroups use it.
+constexpr int64_t kBwdListBlocks = 256 * 16;
+constexpr int64_t kBwdStrideFrom = 4 * kBwdListBlocks * 4;
+
 template <int R, typename S, bool kCount, bool kAbs>
 void launch_bwd_bucket_k(const BlendArgs<S>& a, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((a.n_buckets + kBwdWaves - 1) / kBwdWaves));
-  if (a.bucket_list)
-    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, true>), grid, dim3(kBwdWaves * kWave), 0, st, a);
+  const int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
+  const dim3 block(kBwdWaves * kWave);
+  if (a.bucket_list && blocks > kBwdStrideFrom)
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, 2>), dim3(static_cast<unsigned>(kBwdListBlocks)),
+                       block, 0, st, a);
+  else if (a.bucket_list)
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, 1>), dim3(static_cast<unsigned>(blocks)), block,
+                       0, st, a);
   else
-    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, false>), grid, dim3(kBwdWaves * kWave), 0, st, a);
+    hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, 0>), dim3(static_cast<unsigned>(blocks)), block,
+                       0, st, a);
 }
 
 template <int R, typename S, bool kAbs = true>
