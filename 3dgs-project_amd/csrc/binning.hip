@@ -174,6 +174,16 @@ __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
   return valid ? peers : 0ull;
 }
 
+
+// Logical tile of radix workgroup b (of n). Workgroups are dealt to the 8 XCDs round-robin
+// (b % 8); giving XCD x the contiguous logical range x * (n / 8) ... (a bijection for any n)
+// keeps neighbouring tiles -- whose runs of one digit are adjacent in the output, often in
+// one cache line -- in one L2.
+__device__ __forceinline__ int xcd_tile(int b, int n) {
+  const int q = n / 8, r = n % 8, x = b % 8, k = b / 8;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
+}
+
 template <int BITS, int ROUNDS>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* __restrict__ keys, int64_t m,
                                                                 int shift, uint32_t* __restrict__ tile_hist,
@@ -184,7 +194,8 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* 
   const int wave = threadIdx.x >> 6;
   for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_h[0][0])[k] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kRsWaves * kWave * ROUNDS) + wave * (kWave * ROUNDS);
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t base = static_cast<int64_t>(tile) * (kRsWaves * kWave * ROUNDS) + wave * (kWave * ROUNDS);
   uint32_t key[ROUNDS];
 #pragma unroll
   for (int r = 0; r < ROUNDS; ++r) {  // all loads in flight before the first count
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* 
     uint32_t c = 0;
 #pragma unroll
     for (int w = 0; w < kRsWaves; ++w) c += s_h[w][k];
-    tile_hist[static_cast<int64_t>(k) * n_tiles + blockIdx.x] = c;
+    tile_hist[static_cast<int64_t>(k) * n_tiles + tile] = c;
   }
 }
 
@@ -250,6 +261,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
   __shared__ uint32_t s_wave[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
   for (int k = threadIdx.x; k < kRsWaves * R; k += kRsThreads) (&s_cnt[0][0])[k] = 0;
   constexpr int DPT = (R + kRsThreads - 1) / kRsThreads;  // consecutive digits per thread (1 or 2)
   {
@@ -266,12 +278,12 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
 #pragma unroll
     for (int e = 0; e < DPT; ++e) {
       const int d = static_cast<int>(threadIdx.x) * DPT + e;
-      if (d < R) s_goff[d] = run + tile_offs[static_cast<int64_t>(d) * n_tiles + blockIdx.x];
+      if (d < R) s_goff[d] = run + tile_offs[static_cast<int64_t>(d) * n_tiles + tile];
       run += t[e];
     }
   }
   __syncthreads();
-  const int64_t tile_base = static_cast<int64_t>(blockIdx.x) * kTileKeys;
+  const int64_t tile_base = static_cast<int64_t>(tile) * kTileKeys;
   const int64_t base = tile_base + wave * (kWave * ROUNDS);
   const uint64_t lt = lanemask_lt(lane);
   uint32_t key[ROUNDS], val[ROUNDS], rank[ROUNDS];
