@@ -68,7 +68,7 @@ _SIGS = {
     "gs_scan_workspace_size": (_sz, [_i64]),
     "gs_scan_u32": (_i32, [_vp, _vp, _i64, _vp, _sz, _vp]),
     "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
-                                 _vp, _vp]),
+                                 _vp, _vp, _vp]),
     "gs_bin_prepare_workspace_size": (_sz, [_i64]),
     "gs_bin_prepare_3d": (_i32, [_vp, _vp, _vp, _i64, C.POINTER(GsCamera), _vp, _vp, _vp, _sz, _vp]),
     "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32]),

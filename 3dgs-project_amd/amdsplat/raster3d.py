@@ -133,6 +133,18 @@ class StageTimer:
         return out
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(dev) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for the instance-count copy."""
+    key = torch.device(dev).index if torch.device(dev).index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(key)
+    if s is None:
+        s = _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
+    return s
+
+
 def _check_inputs(means, log_scales, quats, opacity_logits, sh):
     n = means.shape[0]
     dev = means.device
@@ -191,16 +203,38 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     rec = torch.empty(n, REC_FLOATS, dtype=torch.float32, device=dev)
     touched = torch.empty(n, dtype=torch.int32, device=dev)
     dkeys = torch.empty(n, dtype=torch.int32, device=dev)
+    n_waves = (n + 63) // 64
+    wave_counts = torch.empty(n_waves, dtype=torch.int32, device=dev)
     call("gs_preprocess_fwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh_a), ptr(sh_b),
-         n, K, sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), st)
+         n, K, sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), ptr(wave_counts), st)
     tm.mark("preprocess")
+    # The instance count m (the total of the per-wavefront tile counts) needs only the
+    # preprocess: a side stream copies the counts to host memory while the depth sort runs on
+    # this stream, so the host sizes the fill's buffers without the stream draining first.
+    m_ready = None
+    if n > 0:
+        side = _side_stream(dev)
+        pre_done = torch.cuda.Event()
+        pre_done.record()
+        side.wait_event(pre_done)
+        wave_counts.record_stream(side)
+        counts_host = torch.empty(n_waves, dtype=torch.int32, pin_memory=True)
+        with torch.cuda.stream(side):
+            counts_host.copy_(wave_counts, non_blocking=True)
+            m_ready = torch.cuda.Event()
+            m_ready.record()
     order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
     call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
          ws.numel(), st)
     tm.mark("depth_order")
-    m = int(offsets[n].item()) if n > 0 else 0  # host readback: instance count
+    m = 0
+    if m_ready is not None:
+        m_ready.synchronize()
+        m = int(counts_host.sum(dtype=torch.int64))
+        if m >= 1 << 32:
+            raise _lib.AmdSplatError(f"{m} tile instances exceed the 32-bit instance index")
     keys = torch.empty(m if keep_keys else 0, dtype=torch.int64, device=dev)
     point_list = torch.empty(m, dtype=torch.int32, device=dev)
     ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)

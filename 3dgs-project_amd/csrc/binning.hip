@@ -141,6 +141,8 @@ __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
   if (i < n) p[i] = v;
 }
 
+
+
 // ---------------------------------------------------------------------------------------
 // Stable LSD radix sort of (uint32 key, uint32 value) pairs, BITS <= 8 bits per pass.
 //

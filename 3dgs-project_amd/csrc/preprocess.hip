@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
     ShPtr sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
-    uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys) {
+    uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys, uint32_t* __restrict__ wave_counts) {
   using St = ShStage<K>;
   __shared__ float s_sh[4][St::RH * St::CP];
   const int lane = threadIdx.x & 63;
@@ -403,6 +403,12 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
       r.d = bnd;
       rec[i] = r;
     }
+  }
+  if (wave_counts) {
+    // tiles touched by this wavefront's 64 Gaussians: the instance count m is their total
+    uint32_t s = (valid && g.vis) ? count : 0u;
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) wave_counts[wave_first / 64] = s;
   }
 }
 
@@ -626,10 +632,11 @@ using namespace gs;
 template <int K>
 static void launch_pre_fwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
                            const float* quats, const float* op, ShPtr sh, int64_t n,
-                           int active, const CamK& cam, float* rec, uint32_t* touched, uint32_t* dkeys) {
+                           int active, const CamK& cam, float* rec, uint32_t* touched, uint32_t* dkeys,
+                           uint32_t* wave_counts) {
   hipLaunchKernelGGL(preprocess_fwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
-                     reinterpret_cast<SplatRec*>(rec), touched, dkeys);
+                     reinterpret_cast<SplatRec*>(rec), touched, dkeys, wave_counts);
 }
 
 template <int K>
@@ -656,7 +663,7 @@ extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, co
                                  const float* opacity_logits, const float* sh, const float* sh_rest,
                                  int64_t n, int sh_coeffs, int sh_degree, const gs_camera* cam,
                                  float* splat_rec, uint32_t* tiles_touched, uint32_t* depth_keys,
-                                 void* stream) {
+                                 uint32_t* wave_counts, void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
   if (int e = check_cam(cam)) return e;
@@ -673,10 +680,10 @@ extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, co
   hipStream_t st = as_stream(stream);
   const ShPtr shp{sh, sh_rest};
   switch (sh_coeffs) {
-    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
-    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
-    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
-    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys); break;
+    case 1: launch_pre_fwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys, wave_counts); break;
+    case 4: launch_pre_fwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys, wave_counts); break;
+    case 9: launch_pre_fwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys, wave_counts); break;
+    default: launch_pre_fwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, depth_keys, wave_counts); break;
   }
   return check_launch("preprocess_fwd");
 }

@@ -12,7 +12,8 @@
  *
  * The 3D path replaces Faster-GS's _C.forward / _C.backward (called at
  * phase1/tests/test_parity.py:90,97-98 and cluster/patches/fastergs_lean_adam.patch:328-345):
- *   gs_preprocess_fwd -> gs_bin_prepare_3d -> [host reads M = offsets[n]] -> gs_bin_fill_3d
+ *   gs_preprocess_fwd -> gs_bin_prepare_3d -> [host reads M, the sum of the preprocess's
+ *   wave_counts] -> gs_bin_fill_3d
  *   -> gs_bucket_fill -> gs_blend_fwd_3d;   backward: gs_blend_bwd_3d -> gs_preprocess_bwd.
  * The 2D entry points replace the extension functions of toy2d/csrc/rasterize.cu:366-448
  * and phase0/csrc/macrotile/bindings.cpp:156-239.
@@ -91,11 +92,17 @@ int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
  *   out: splat_rec [n,16] floats (16-byte aligned), tiles_touched [n] uint32, and (may be
  *   NULL) depth_keys [n] uint32: the orderable bits of the view depth of a Gaussian with
  *   tiles, 0xffffffff for a culled one (the keys gs_bin_prepare_3d sorts by).
+ *   wave_counts (may be NULL): [ceil(n / 64)] uint32, the tiles touched by each group of 64
+ *   consecutive Gaussians. Their total is the instance count m (= offsets[n] of
+ *   gs_bin_prepare_3d): the caller can copy these few bytes to host memory right after the
+ *   preprocess, while the depth sort runs, instead of reading offsets[n] after it (Faster-GS
+ *   reads the count back after its tiles_touched scan, phase2/fastergs_readback.patch:46-85).
  * ------------------------------------------------------------------------------------- */
 int gs_preprocess_fwd(const float* means, const float* log_scales, const float* quats,
                       const float* opacity_logits, const float* sh, const float* sh_rest, int64_t n,
                       int sh_coeffs, int sh_degree, const gs_camera* cam, float* splat_rec,
-                      uint32_t* tiles_touched, uint32_t* depth_keys, void* stream);
+                      uint32_t* tiles_touched, uint32_t* depth_keys, uint32_t* wave_counts,
+                      void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 3D binning (replaces the cub DeviceScan of tiles_touched, create_instances_cu, the two cub

@@ -103,6 +103,7 @@ def check_forward(sc, cam=None):
     assert (np_(fs.touched).astype(np.uint32) == ref["touched"]).all(), "tiles touched differ"
     assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref["rec"][vis].view(np.uint32)), "splat records differ"
     assert fs.m == len(ref["keys"])
+    assert int(fs.offsets[-1]) == fs.m, "early instance count differs from the scan's total"
     assert np.array_equal(np_(fs.keys).view(np.uint64), ref["keys"]), "sorted keys differ"
     assert np.array_equal(np_(fs.point_list).view(np.uint32), ref["point_list"]), "point list differs"
     assert np.array_equal(np_(fs.ranges).view(np.uint32), ref["ranges"]), "tile ranges differ"
@@ -456,3 +457,12 @@ def test_backward_over_long_bucket_table_equals_table_walk():
     # them deterministically, amplifying atomic-order rounding where its terms cancel
     for k in range(9):
         assert D.rel_err(np_(listed[:, k]), np_(table[:, k])) < 1e-5, k
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 4097])
+def test_instance_count_from_wave_counts(n):
+    """The host's instance count (the total of the preprocess's per-wavefront counts, copied on a
+    side stream) equals the depth-ordered scan's total and the sum of tiles touched, at ragged n."""
+    sc = scenes.small_scene(n, 160, 120, seed=n, scale=(0.01, 0.2))
+    p, fs = gpu_forward(sc, 3)
+    assert fs.m == int(fs.offsets[-1]) == int(fs.touched.long().sum())
