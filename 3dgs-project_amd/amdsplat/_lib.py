@@ -35,6 +35,7 @@ class GsCamera(C.Structure):
 
 GS_ACCUMULATE = 1  # gs_blend_bwd_3d flag: add to grad2d instead of zeroing it first
 GS_ABS_GRAD = 2  # gs_blend_bwd_3d flag: also accumulate |dL/dmean2d| into grad2d[:, 9:11]
+GS_BLEND_LIST_CLEARED = 1  # gs_blend_fwd_3d flag: gs_bin_fill_3d cleared the bucket list's header
 GS_FLOAT32, GS_FLOAT64, GS_BFLOAT16 = 0, 1, 2
 GS_CAM_PROPER_ANTIALIASING = 1  # gs_camera.flags bit
 GS_ADAM_MAX_GROUPS = 8
@@ -72,14 +73,14 @@ _SIGS = {
     "gs_bin_prepare_workspace_size": (_sz, [_i64]),
     "gs_bin_prepare_3d": (_i32, [_vp, _vp, _vp, _i64, C.POINTER(GsCamera), _vp, _vp, _vp, _sz, _vp]),
     "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32]),
-    "gs_bin_fill_3d": (_i32, [_vp, _vp, _vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _sz,
-                              _vp]),
+    "gs_bin_fill_3d": (_i32, [_vp, _vp, _vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _sz, _vp]),
     "gs_rect_counts": (_i32, [_vp, _i64, _i32, _i32, _vp, _vp]),
     "gs_bin_fill_rect": (_i32, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                 _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
     "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp,
-                               _vp]),
+                               _vp, _vp, _i64, _i32, _vp]),
     "gs_blend_scores_3d": (_i32, [_vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _vp, _vp, _i32, _vp, _vp]),

@@ -102,6 +102,7 @@ class ForwardState:
     bucket_list: torch.Tensor | None = None  # [4 + n_buckets_max] int32: buckets the backward reads
     bg: tuple = (0.0, 0.0, 0.0)
     timings: dict = field(default_factory=dict)
+    grad2d: torch.Tensor | None = None  # [n, 12] zeroed by the forward blend, for the first backward
 
     @property
     def n_buckets(self) -> int:
@@ -239,10 +240,21 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     point_list = torch.empty(m, dtype=torch.int32, device=dev)
     ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
     bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
+    nb_max, bucket_to_tile, n_contrib, tile_max, ckpt, blist, grad2d = 0, None, None, None, None, None, None
+    if for_backward and _scores is None:
+        nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
+        bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
+        n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
+        tile_max = torch.empty(T, dtype=torch.int32, device=dev)
+        ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
+        blist = torch.empty(4 + nb_max, dtype=torch.int32, device=dev)
+        # the backward's screen gradients, zeroed by the forward blend's workgroups
+        grad2d = torch.empty(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
     ws = _u8(_lib.size_call("gs_bin_workspace_size", n, m, T), dev)
+    # the fill also clears the bucket list's header for the forward blend
     call("gs_bin_fill_3d", ptr(rec), ptr(dkeys), ptr(order), ptr(offsets), n, ccam, m,
-         ptr(keys) if keep_keys else None, ptr(point_list), ptr(ranges), ptr(bucket_offsets), ptr(ws), ws.numel(),
-         st)
+         ptr(keys) if keep_keys else None, ptr(point_list), ptr(ranges), ptr(bucket_offsets), ptr(blist), ptr(ws),
+         ws.numel(), st)
     tm.mark("binning")
     if _scores is not None:  # pruning scores: the blend's weights, no image
         call("gs_blend_scores_3d", ptr(rec), ptr(ranges), ptr(point_list), W, H, n, ptr(_scores), st)
@@ -250,24 +262,17 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges,
                             bucket_offsets, 0, None, None, None, None, None, None, None, tuple(bg),
                             {} if isinstance(timing, StageTimer) else tm.result())
-    nb_max, bucket_to_tile, n_contrib, tile_max, ckpt, blist = 0, None, None, None, None, None
-    if for_backward:
-        nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
-        bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
-        call("gs_bucket_fill", ptr(bucket_offsets), T, ptr(bucket_to_tile), nb_max, st)
-        n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
-        tile_max = torch.empty(T, dtype=torch.int32, device=dev)
-        ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
-        blist = torch.empty(4 + nb_max, dtype=torch.int32, device=dev)
     image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
     final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
     tm.mark("buckets")
     call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
-         ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), ptr(blist), st)
+         ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), ptr(blist), ptr(bucket_to_tile),
+         ptr(grad2d), grad2d.numel() if grad2d is not None else 0,
+         _lib.GS_BLEND_LIST_CLEARED if blist is not None else 0, st)
     tm.mark("blend_fwd")
     return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges, bucket_offsets,
                         nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist, tuple(bg),
-                        {} if isinstance(timing, StageTimer) else tm.result())
+                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d)
 
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
@@ -287,7 +292,11 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
         grad_alpha = grad_alpha.contiguous().float()
     tm = timing if isinstance(timing, StageTimer) else StageTimer(bool(timing))
     tm.mark("start")
-    grad2d = torch.zeros(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+    if fs.grad2d is not None:
+        # zeroed by the forward blend; a second backward of the same forward starts from zeros
+        grad2d, fs.grad2d = fs.grad2d, None
+    else:
+        grad2d = torch.zeros(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
     tm.mark("grad_zero")
     call("gs_blend_bwd_3d", ptr(fs.rec), ptr(fs.ranges), ptr(fs.point_list), ptr(fs.bucket_offsets),
          ptr(fs.bucket_to_tile), fs.n_buckets_max, n, cam.width, cam.height, ptr(fs.image), ptr(grad_image),

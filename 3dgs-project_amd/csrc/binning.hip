@@ -749,8 +749,10 @@ constexpr int kBoItems = 8;
 
 __global__ __launch_bounds__(kBoThreads) void bucket_offsets_kernel(uint32_t* __restrict__ ranges, int n_tiles,
                                                                     int64_t m, uint32_t* __restrict__ boff,
-                                                                    uint32_t* __restrict__ tile_offsets) {
+                                                                    uint32_t* __restrict__ tile_offsets,
+                                                                    uint32_t* __restrict__ list_header) {
   __shared__ uint32_t s_wave[kBoThreads / kWave];
+  if (list_header && threadIdx.x < kListHeader) list_header[threadIdx.x] = 0u;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   uint32_t run = 0;
@@ -904,7 +906,7 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
                      const uint32_t* order,
                      const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
-                     uint32_t* bucket_offsets, char* ws, hipStream_t st) {
+                     uint32_t* bucket_offsets, uint32_t* list_header, char* ws, hipStream_t st) {
   uint32_t* tkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
   uint32_t* tvals = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
   uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
@@ -929,7 +931,7 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
                        tsorted, m, n_tiles, ranges);
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
-                     tile_offsets);
+                     tile_offsets, list_header);
 }
 
 }  // namespace gs
@@ -985,7 +987,8 @@ extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles) {
 extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
                               const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
                               uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
-                              uint32_t* bucket_offsets, void* workspace, size_t workspace_bytes, void* stream) {
+                              uint32_t* bucket_offsets, uint32_t* bucket_list, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   clear_error();
   if (int e = check_cam(cam)) return e;
   GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32), GS_ERR_ARG, "invalid sizes n=%lld m=%lld",
@@ -1002,7 +1005,7 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
   bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, order, offsets, n, k.tiles_x,
            n_tiles,
-           m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, static_cast<char*>(workspace),
+           m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, bucket_list, static_cast<char*>(workspace),
            as_stream(stream));
   return check_launch("bin_fill_3d");
 }
@@ -1052,7 +1055,7 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
   }
   bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, n_tiles, m, sorted_keys,
-           point_list, ranges, tile_offsets, bucket_offsets, ws, st);
+           point_list, ranges, tile_offsets, bucket_offsets, nullptr, ws, st);
   return check_launch("bin_fill_rect");
 }
 

@@ -58,6 +58,11 @@ struct BlendArgs {
   float* scores;
   // 3D: buckets the backward reads (appended by the forward, consumed by the backward)
   uint32_t* bucket_list;
+  // 3D forward: bucket_to_tile of the tile's buckets (may be null), and a float4 buffer that
+  // the workgroups zero between them (may be null; the backward's screen gradients)
+  uint32_t* b2t_out;
+  float4* clear4;
+  int64_t clear4_n;
 };
 
 // Per-wavefront counter increment (one atomic per wavefront).
@@ -113,8 +118,7 @@ __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAto
 // Forward
 // ---------------------------------------------------------------------------------------
 // Bucket list written by the 3D forward: [0] buckets the backward reads, [1..3] zero,
-// [4 + i] bucket indices (any order).
-constexpr int kListHeader = 4;
+// [kListHeader + i] bucket indices (any order).
 
 // kScore: instead of the image, accumulate every splat's blending weights alpha T over the
 // tile's pixels into a.scores (a wavefront sum per splat into LDS, one global atomic per
@@ -142,6 +146,18 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
   const int len = static_cast<int>(r1 - r0);
   S* ck = a.ckpt ? a.ckpt + (static_cast<int64_t>(a.bucket_offsets[tile]) * kTilePixels + t) * 4 : nullptr;
   if (t == 0) s_max = 0;
+  if (a.b2t_out) {
+    // the tile of each of this tile's buckets (what a separate bucket_to_tile pass would write)
+    const uint32_t bf = a.bucket_offsets[tile], bl = a.bucket_offsets[tile + 1];
+    for (uint32_t b = bf + t; b < bl; b += kTilePixels) a.b2t_out[b] = static_cast<uint32_t>(tile);
+  }
+  if (a.clear4) {
+    // this workgroup's share of the buffer to zero: stores only, hidden under the blend's
+    // arithmetic
+    const int64_t per = (a.clear4_n + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = per * tile, hi = min(lo + per, a.clear4_n);
+    for (int64_t q = lo + t; q < hi; q += kTilePixels) a.clear4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
 
   // 3D: a pixel has stopped exactly when T < 1e-4 (T only decreases; pixels outside the
   // image start at T = 0), so no separate per-lane flag is kept
@@ -829,9 +845,14 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
                                const uint32_t* point_list, const uint32_t* bucket_offsets,
                                int width, int height, const float* bg, float* image,
                                float* final_T, int32_t* n_contrib, uint32_t* tile_max,
-                               float* ckpt, uint32_t* bucket_list, void* stream) {
+                               float* ckpt, uint32_t* bucket_list, uint32_t* bucket_to_tile,
+                               float* clear, int64_t clear_floats, int flags, void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARG, "image size must be positive");
+  GS_REQUIRE(clear_floats >= 0 && clear_floats % 4 == 0 && (clear || clear_floats == 0), GS_ERR_ARG,
+             "clear must hold a multiple of 4 floats");
+  GS_REQUIRE(aligned(clear, 16), GS_ERR_ALIGN, "clear must be 16-byte aligned");
+  GS_REQUIRE(!bucket_to_tile || bucket_offsets, GS_ERR_ARG, "bucket_to_tile needs bucket_offsets");
   // splat_rec, point_list and ckpt may be NULL when the scene has no instances; without ckpt
   // (inference) bucket_offsets, n_contrib and tile_max may be NULL as well
   GS_REQUIRE(ranges && image && final_T && (!ckpt || (bucket_offsets && n_contrib && tile_max)), GS_ERR_ARG,
@@ -848,7 +869,11 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
   GS_REQUIRE(!bucket_list || ckpt, GS_ERR_ARG, "bucket_list needs the checkpoints");
   GS_REQUIRE(aligned(bucket_list, 16), GS_ERR_ALIGN, "bucket_list must be 16-byte aligned");
   a.bucket_list = bucket_list;
-  if (bucket_list) fill_zero_f32(reinterpret_cast<float*>(bucket_list), kListHeader, as_stream(stream));
+  a.b2t_out = bucket_to_tile;
+  a.clear4 = clear_floats ? reinterpret_cast<float4*>(clear) : nullptr;
+  a.clear4_n = clear_floats / 4;
+  if (bucket_list && !(flags & GS_BLEND_LIST_CLEARED))
+    fill_zero_f32(reinterpret_cast<float*>(bucket_list), kListHeader, as_stream(stream));
   launch_fwd<kRules3D, float>(a, as_stream(stream));
   return check_launch("blend_fwd_3d");
 }

@@ -24,6 +24,7 @@ constexpr int kWave = 64;                    // CDNA wavefront
 constexpr int kStripRows = kWave / kTile;    // 4 tile rows per wavefront
 constexpr int kStrips = kTile / kStripRows;  // 4 strips per tile
 constexpr int kPixPerLane = kTilePixels / kWave;  // 4 pixels per lane in the bucket backward
+constexpr int kListHeader = 4;  // words before the entries of the 3D bucket list ([0] = count)
 
 constexpr float kAlphaMin = 1.0f / 255.0f;
 constexpr float kTStop = 1e-4f;

@@ -13,8 +13,8 @@
  * The 3D path replaces Faster-GS's _C.forward / _C.backward (called at
  * phase1/tests/test_parity.py:90,97-98 and cluster/patches/fastergs_lean_adam.patch:328-345):
  *   gs_preprocess_fwd -> gs_bin_prepare_3d -> [host reads M, the sum of the preprocess's
- *   wave_counts] -> gs_bin_fill_3d
- *   -> gs_bucket_fill -> gs_blend_fwd_3d;   backward: gs_blend_bwd_3d -> gs_preprocess_bwd.
+ *   wave_counts] -> gs_bin_fill_3d -> gs_blend_fwd_3d;   backward: gs_blend_bwd_3d ->
+ *   gs_preprocess_bwd.
  * The 2D entry points replace the extension functions of toy2d/csrc/rasterize.cu:366-448
  * and phase0/csrc/macrotile/bindings.cpp:156-239.
  */
@@ -127,6 +127,8 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *                         needs depth_keys)
  *   ranges [T,2]          [start, end) of each tile in point_list
  *   bucket_offsets [T+1]  exclusive scan of ceil(len/32); bucket_offsets[T] = number of buckets
+ *   bucket_list (may be NULL): the list gs_blend_fwd_3d appends to; its header is cleared
+ *                         here, so that call can take GS_BLEND_LIST_CLEARED
  *   Workspace from gs_bin_workspace_size(n, m, T).
  * ------------------------------------------------------------------------------------- */
 size_t gs_bin_prepare_workspace_size(int64_t n);
@@ -137,7 +139,8 @@ size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles);
 int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
                    const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
                    uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
-                   uint32_t* bucket_offsets, void* workspace, size_t workspace_bytes, void* stream);
+                   uint32_t* bucket_offsets, uint32_t* bucket_list, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /* Rectangle binning for the 2D operators (replaces toy2d/gs2d/binning.py:34-88, whose
  * per-tile lists are ordered by a stable depth rank, and phase0/splat2d/ops.py:206-255, whose
@@ -170,7 +173,13 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
  *   bucket_list (NULL, or 16-byte aligned uint32 [4 + n_buckets_max] with the bound of
  *   gs_bucket_fill; needs ckpt): receives the buckets the backward reads (those starting before
  *   their tile's tile_max) for gs_blend_bwd_3d: [0] their number, [4 ...] their indices in any
- *   order.
+ *   order. Its header is cleared by this call, unless flags has GS_BLEND_LIST_CLEARED (the
+ *   caller passed the list to gs_bin_fill_3d, which cleared it).
+ *   bucket_to_tile (may be NULL; needs bucket_offsets): receives the tile of every bucket
+ *   b < bucket_offsets[T], as gs_bucket_fill would write it.
+ *   clear (may be NULL): 16-byte aligned float buffer of clear_floats (a multiple of 4) that
+ *   the call sets to zero while it blends -- the grad2d that gs_blend_bwd_3d with
+ *   GS_ACCUMULATE adds to.
  *   Inference (Faster-GS's inference blend, upstream/upstream_main_kernels.patch:131-150):
  *   ckpt NULL, and then bucket_offsets, n_contrib, tile_max and bucket_list may be NULL too;
  *   image and final_T are the same bits as with them.
@@ -178,7 +187,9 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
 int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, int width, int height, const float* bg,
                     float* image, float* final_T, int32_t* n_contrib, uint32_t* tile_max,
-                    float* ckpt, uint32_t* bucket_list, void* stream);
+                    float* ckpt, uint32_t* bucket_list, uint32_t* bucket_to_tile, float* clear,
+                    int64_t clear_floats, int flags, void* stream);
+enum { GS_BLEND_LIST_CLEARED = 1 };
 
 /* ---------------------------------------------------------------------------------------
  * Pruning scores (replaces Faster-GS's pruning-score blend, kernels_pruning_scores.cuh, seen

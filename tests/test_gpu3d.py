@@ -466,3 +466,19 @@ def test_instance_count_from_wave_counts(n):
     sc = scenes.small_scene(n, 160, 120, seed=n, scale=(0.01, 0.2))
     p, fs = gpu_forward(sc, 3)
     assert fs.m == int(fs.offsets[-1]) == int(fs.touched.long().sum())
+
+
+def test_forward_clears_grad2d_and_bucket_table():
+    """The forward blend zeroes the backward's screen-gradient buffer (handed over in the forward
+    state) and writes bucket_to_tile; memory that held NaNs is reused for it."""
+    sc = make("partial_tiles")
+    n = sc.n
+    junk = torch.full((n, 12), float("nan"), device="cuda")
+    del junk  # the caching allocator hands this block to the forward's grad2d
+    p, fs = gpu_forward(sc, 3)
+    assert fs.grad2d is not None and bool((fs.grad2d == 0).all()), "grad2d not cleared"
+    boff = np_(fs.bucket_offsets).astype(np.int64)
+    b2t = np_(fs.bucket_to_tile).view(np.uint32)[: boff[-1]]
+    want = np.repeat(np.arange(len(boff) - 1, dtype=np.uint32), np.diff(boff))
+    assert np.array_equal(b2t, want)
+    assert int(fs.bucket_list[0]) <= int(boff[-1])
