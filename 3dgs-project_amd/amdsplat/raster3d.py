@@ -212,24 +212,27 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     # The instance count m (the total of the per-wavefront tile counts) needs only the
     # preprocess: a side stream copies the counts to host memory while the depth sort runs on
     # this stream, so the host sizes the fill's buffers without the stream draining first.
-    m_ready = None
-    if n > 0:
-        side = _side_stream(dev)
+    # (The host enqueues the depth sort before it sets up the copy, so the sort follows the
+    # preprocess without a gap.)
+    side = _side_stream(dev) if n > 0 else None
+    if side is not None:
         pre_done = torch.cuda.Event()
         pre_done.record()
         side.wait_event(pre_done)
-        wave_counts.record_stream(side)
-        counts_host = torch.empty(n_waves, dtype=torch.int32, pin_memory=True)
-        with torch.cuda.stream(side):
-            counts_host.copy_(wave_counts, non_blocking=True)
-            m_ready = torch.cuda.Event()
-            m_ready.record()
     order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
     call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
          ws.numel(), st)
     tm.mark("depth_order")
+    m_ready = None
+    if side is not None:
+        wave_counts.record_stream(side)
+        counts_host = torch.empty(n_waves, dtype=torch.int32, pin_memory=True)
+        with torch.cuda.stream(side):
+            counts_host.copy_(wave_counts, non_blocking=True)
+            m_ready = torch.cuda.Event()
+            m_ready.record()
     m = 0
     if m_ready is not None:
         m_ready.synchronize()

@@ -81,27 +81,6 @@ __device__ __forceinline__ bool band_columns(const BandSetup& s, float Y0, float
   return true;
 }
 
-// Visits the touched tiles in row-major order; returns their number.
-template <typename F>
-__device__ __forceinline__ int for_each_touched_tile(const float4 a, const float4 b, const int4 d,
-                                                     int tiles_x, F&& visit) {
-  const BandSetup s = band_setup(a, b);
-  const int ty0 = d.z / kTile, ty1 = d.w / kTile;
-  int count = 0;
-  for (int ty = ty0; ty <= ty1; ++ty) {
-    const int py0 = max(ty * kTile, d.z), py1 = min(ty * kTile + kTile - 1, d.w);
-    int c0, c1;
-    if (!band_columns(s, static_cast<float>(py0) + 0.5f, static_cast<float>(py1) + 0.5f, d.x, d.y,
-                      c0, c1))
-      continue;
-    for (int tx = c0 / kTile; tx <= c1 / kTile; ++tx) {
-      visit(ty * tiles_x + tx, count);
-      ++count;
-    }
-  }
-  return count;
-}
-
 // Tiles [tx0, tx0 + nt) touched in tile row ty (nt = 0 if the row is missed).
 __device__ __forceinline__ uint32_t row_tiles(const BandSetup& s, const int4 d, int ty, int& tx0) {
   const int py0 = max(ty * kTile, d.z), py1 = min(ty * kTile + kTile - 1, d.w);
@@ -114,35 +93,58 @@ __device__ __forceinline__ uint32_t row_tiles(const BandSetup& s, const int4 d, 
   return static_cast<uint32_t>(c1 / kTile - tx0 + 1);
 }
 
-// Number of touched tiles of a splat whose tile rows are shared out over the wavefront's
-// lanes (lane r takes rows ty0 + r, ty0 + r + 64, ...). Every lane of the wavefront must call
-// it with the same splat; returns the total to every lane.
-__device__ __forceinline__ uint32_t wave_count_touched_tiles(const float4 a, const float4 b, const int4 d,
-                                                             int lane) {
-  const BandSetup s = band_setup(a, b);
-  const int ty0 = d.z / kTile, ty1 = d.w / kTile;
-  uint32_t cnt = 0;
-  for (int ty = ty0 + lane; ty <= ty1; ty += kWave) {
-    int tx0;
-    cnt += row_tiles(s, d, ty, tx0);
-  }
-  for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
-  return cnt;
-}
+// Touched-tile counts of a wavefront's 64 splats, their tile rows shared out over the lanes:
+// the rows of all splats are numbered in lane order, each lane takes one row at a time
+// (binary search for its splat in the row prefix), and the row's tiles are added to the
+// splat's count in LDS. Every splat costs the wavefront about its number of rows, so neither
+// a few tall splats nor lanes with more rows than others leave lanes idle. `vis` lanes give
+// their record halves a, b and pixel bounds d; every lane of the wavefront must call it.
+// scratch: kCountScratchWords words of LDS owned by the wavefront. Returns the lane's count.
+constexpr int kCountScratchWords = 64 * 12 + 64 + 64;
 
-// Number of touched tiles (same rule, without enumerating them).
-__device__ __forceinline__ int count_touched_tiles(const float4 a, const float4 b, const int4 d) {
-  const BandSetup s = band_setup(a, b);
-  const int ty0 = d.z / kTile, ty1 = d.w / kTile;
-  int count = 0;
-  for (int ty = ty0; ty <= ty1; ++ty) {
-    const int py0 = max(ty * kTile, d.z), py1 = min(ty * kTile + kTile - 1, d.w);
-    int c0, c1;
-    if (band_columns(s, static_cast<float>(py0) + 0.5f, static_cast<float>(py1) + 0.5f, d.x, d.y, c0,
-                     c1))
-      count += c1 / kTile - c0 / kTile + 1;
+__device__ __forceinline__ uint32_t wave_count_rows(bool vis, const float4 a, const float4 b, const int4 d,
+                                                    int lane, uint32_t* scratch) {
+  float4* s_set = reinterpret_cast<float4*>(scratch);  // [64][3]: band setup and bounds
+  uint32_t* s_rex = scratch + 64 * 12;                  // exclusive prefix of the rows
+  uint32_t* s_cnt = s_rex + 64;                         // tiles per splat
+  uint32_t rows = 0;
+  if (vis) {
+    const BandSetup s = band_setup(a, b);
+    rows = static_cast<uint32_t>(max(d.w / kTile - d.z / kTile + 1, 0));
+    s_set[3 * lane] = make_float4(s.mx, s.my, s.B, s.det);
+    s_set[3 * lane + 1] = make_float4(s.tA, s.vmax, s.vr, s.invA);
+    s_set[3 * lane + 2] = make_float4(__int_as_float(d.x), __int_as_float(d.y), __int_as_float(d.z),
+                                      __int_as_float(d.w));
   }
-  return count;
+  uint32_t incl = rows;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  const uint32_t total = __shfl(incl, kWave - 1, 64);
+  s_rex[lane] = incl - rows;
+  s_cnt[lane] = 0u;
+  wave_sync();
+  for (uint32_t base = 0; base < total; base += kWave) {
+    const uint32_t item = base + static_cast<uint32_t>(lane);
+    if (item < total) {
+      int own = 0;  // last splat whose first row is <= item
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1)
+        if (s_rex[own + step] <= item) own += step;
+      const float4 u = s_set[3 * own], v = s_set[3 * own + 1], w = s_set[3 * own + 2];
+      BandSetup s;
+      s.mx = u.x; s.my = u.y; s.A = 0.0f; s.B = u.z; s.det = u.w;
+      s.tA = v.x; s.vmax = v.y; s.vr = v.z; s.invA = v.w;
+      s.ok = s.det > 0.0f;
+      const int4 dd = make_int4(__float_as_int(w.x), __float_as_int(w.y), __float_as_int(w.z), __float_as_int(w.w));
+      int tx0;
+      const uint32_t nt = row_tiles(s, dd, dd.z / kTile + static_cast<int>(item - s_rex[own]), tx0);
+      if (nt) atomicAdd(&s_cnt[own], nt);
+    }
+  }
+  wave_sync();
+  return s_cnt[lane];
 }
 
 }  // namespace gs

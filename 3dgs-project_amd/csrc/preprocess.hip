@@ -16,8 +16,6 @@
 
 namespace gs {
 
-constexpr int kWideRows = 4;  // splats spanning more tile rows than this share rows over the wavefront
-
 // SH rows staged through LDS at a time: degree 3 in two passes of 32 rows (each pass one
 // contiguous 6 KB block of the tensor), lower degrees in one pass of 64.
 template <int K>
@@ -294,7 +292,9 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     ShPtr sh, int64_t n, int active, CamK cam, SplatRec* __restrict__ rec,
     uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys, uint32_t* __restrict__ wave_counts) {
   using St = ShStage<K>;
-  __shared__ float s_sh[4][St::RH * St::CP];
+  // per wavefront: the tile-count scratch, then the SH rows
+  constexpr int kWords = St::RH * St::CP > kCountScratchWords ? St::RH * St::CP : kCountScratchWords;
+  __shared__ float s_sh[4][kWords];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -328,27 +328,13 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
       g.vis = ok;
     }
   }
-  uint32_t count = 0;
   float4 ra = make_float4(0.0f, 0.0f, 0.0f, 0.0f), rb = ra;
-  // splats spanning many tile rows are counted by the whole wavefront (a lane per row), the
-  // rest by their own lane, so one large splat does not serialise its wavefront
-  const bool wide = g.vis && (bnd.w / kTile - bnd.z / kTile) >= kWideRows;
   if (g.vis) {
     ra = make_float4(g.mx, g.my, g.A, g.B);
     rb = make_float4(g.C, g.o, g.vz, thr);
-    if (!wide) count = static_cast<uint32_t>(count_touched_tiles(ra, rb, bnd));
   }
-  for (uint64_t wm = __ballot(wide ? 1 : 0); wm != 0ull; wm &= wm - 1ull) {
-    const int src = __ffsll(static_cast<unsigned long long>(wm)) - 1;
-    const float4 sa = make_float4(__shfl(ra.x, src, 64), __shfl(ra.y, src, 64), __shfl(ra.z, src, 64),
-                                  __shfl(ra.w, src, 64));
-    const float4 sb = make_float4(__shfl(rb.x, src, 64), __shfl(rb.y, src, 64), __shfl(rb.z, src, 64),
-                                  __shfl(rb.w, src, 64));
-    const int4 sd = make_int4(__shfl(bnd.x, src, 64), __shfl(bnd.y, src, 64), __shfl(bnd.z, src, 64),
-                              __shfl(bnd.w, src, 64));
-    const uint32_t c = wave_count_touched_tiles(sa, sb, sd, lane);
-    if (lane == src) count = c;
-  }
+  // tile rows of the wavefront's splats shared out over its lanes
+  const uint32_t count = wave_count_rows(g.vis, ra, rb, bnd, lane, reinterpret_cast<uint32_t*>(s_sh[wave]));
   if (g.vis) g.vis = count > 0;
 
   // Colour: stage the wavefront's SH rows through LDS (wave-uniform branch).
