@@ -177,15 +177,6 @@ __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
 }
 
 
-// Logical tile of radix workgroup b (of n). Workgroups are dealt to the 8 XCDs round-robin
-// (b % 8); giving XCD x the contiguous logical range x * (n / 8) ... (a bijection for any n)
-// keeps neighbouring tiles -- whose runs of one digit are adjacent in the output, often in
-// one cache line -- in one L2.
-__device__ __forceinline__ int xcd_tile(int b, int n) {
-  const int q = n / 8, r = n % 8, x = b % 8, k = b / 8;
-  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
-}
-
 template <int BITS, int ROUNDS>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* __restrict__ keys, int64_t m,
                                                                 int shift, uint32_t* __restrict__ tile_hist,

@@ -74,4 +74,13 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Logical index of workgroup b of n. Workgroups are dealt to the 8 XCDs round-robin
+// (b % 8); giving XCD x the contiguous logical range x * (n / 8) ... (a bijection for any n)
+// keeps neighbouring radix tiles -- whose runs of one digit are adjacent in the output, often
+// in one cache line -- in one L2.
+__device__ __forceinline__ int xcd_tile(int b, int n) {
+  const int q = n / 8, r = n % 8, x = b % 8, k = b / 8;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
+}
+
 }  // namespace gs
