@@ -50,3 +50,21 @@ def radii_from_cov(cov: torch.Tensor) -> torch.Tensor:
     lam = mid + torch.sqrt(torch.clamp(mid * mid - det, min=0.1))
     r = torch.ceil(3.0 * torch.sqrt(lam))
     return torch.where(det > 0, r, torch.zeros_like(r)).to(torch.int32)
+
+
+def fit_scene_4k(n: int = 4096, size: int = 256, seed: int = 0):
+    """The 2D image-fit workload: n Gaussians on a size x size image with means U(0, size)^2,
+    log-scales N(ln 2, 0.3) per axis, angle U(0, pi), opacity sigmoid(N(0, 1)), colour U(0, 1),
+    a fixed U(0, 1) depth and a U(0, 1) target image [3, size, size], drawn in that order from
+    one seeded CPU generator. Returns the rasterizer inputs (means, conic, color, opacity), the
+    covariance, the depth and the target (float32, CPU)."""
+    g = torch.Generator().manual_seed(seed)
+    xy = torch.rand(n, 2, generator=g) * float(size)
+    log_scale = math.log(2.0) + 0.3 * torch.randn(n, 2, generator=g)
+    theta = torch.rand(n, generator=g) * math.pi
+    opacity = torch.sigmoid(torch.randn(n, generator=g))
+    color = torch.rand(n, 3, generator=g)
+    depth = torch.rand(n, generator=g)
+    target = torch.rand(3, size, size, generator=g)
+    means, conic, _, _, cov = activate(xy, log_scale, theta, torch.zeros(n, 3), torch.zeros(n))
+    return means, conic, color, opacity, cov, depth, target
