@@ -111,6 +111,14 @@ __device__ __forceinline__ float opaque_zero() {
   return z;
 }
 
+// An integer zero in a vector register: an LDS address offset by it is computed once into a
+// VGPR, and unrolled reads from it then take their offsets as immediates.
+__device__ __forceinline__ int opaque_zero_vgpr() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 __device__ __forceinline__ void atomic_add_grad(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAtomicAdd(p, v); }
 
@@ -209,13 +217,10 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
       const uint64_t qm = (c0 < 64) ? wm[0] : (c0 < 128) ? wm[1] : (c0 < 192) ? wm[2] : wm[3];
       uint32_t cm = static_cast<uint32_t>(qm >> (c0 & 63));
       if (c1 - c0 < kBucket) cm &= (1u << (c1 - c0)) - 1u;
-      // wave-uniform loop over the splats whose bounds reach this wavefront's rows; the body
+      // wave-uniform walk over the splats whose bounds reach this wavefront's rows; the body
       // has no lane branches (a lane that has stopped or rejects the splat composites nothing),
-      // so the scalar unit only runs the loop control
-      while (cm != 0u) {
-        const int jj = c0 + __builtin_ctz(cm);
-        cm &= cm - 1u;
-        const Staged<S> sp = s_sp[jj];
+      // so the scalar unit only runs the walk
+      auto body = [&](const Staged<S>& sp, int jj) -> bool {
         Eval<S> e;
         const bool live = kStopByT ? T >= Ru::t_stop() : !done;
         if constexpr (kCount) evals += live ? 1u : 0u;
@@ -243,8 +248,26 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
           T = take ? t : T;
         }
         count += take ? 1 : 0;
-        last = take ? b0 + jj + 1 : last;
         if constexpr (!Ru::kStopBefore && !kStopByT) done = done || T < Ru::t_stop();
+        return take;
+      };
+      if constexpr (R == kRules3D && !kScore) {
+        // unrolled over the bucket's 32 slots: each staged splat at an immediate LDS offset
+        // from the bucket's base address (one VGPR), one scalar bit test per slot; the slot of
+        // the last blended splat is kept as a constant and turned into a list position once
+        cm = __builtin_amdgcn_readfirstlane(cm);
+        const Staged<S>* bp = s_sp + (c0 + opaque_zero_vgpr());
+        int lastk = -1;
+#pragma unroll
+        for (int k = 0; k < kBucket; ++k)
+          if ((cm >> k) & 1u) lastk = body(bp[k], c0 + k) ? k : lastk;
+        last = lastk >= 0 ? b0 + c0 + lastk + 1 : last;
+      } else {
+        while (cm != 0u) {
+          const int jj = c0 + __builtin_ctz(cm);
+          cm &= cm - 1u;
+          last = body(s_sp[jj], jj) ? b0 + jj + 1 : last;
+        }
       }
     }
     if constexpr (kScore) {
