@@ -5,7 +5,7 @@ Workload (default): 1M Gaussians, SH degree 3, 1297x840, fx=fy=1160, 8 seeded or
 N(0,1) upstream image gradient. Inputs are resident in HBM before the timed region.
 
     python bench.py [--steps K] [--warmup W] [--workload sh3_1m|sh3_3m|sh_rgb_100k] [--no-cpu-baseline]
-                    [--no-train-step]
+                    [--no-train-step] [--no-variants]
     python bench.py --copy-probe      # a plain 1 GiB device copy, to calibrate HBM counters
 
 Prints ONE JSON line. `value` is the wall time of K plain steps; per-stage times come from
@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0, help="threads for the CPU baseline (0 = OMP default)")
     ap.add_argument("--copy-probe", action="store_true", help="time a plain 1 GiB device copy and exit")
     ap.add_argument("--no-train-step", action="store_true", help="skip the training-step measurement")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the inference / pruning-score / antialiasing variants (profiling runs)")
     ap.add_argument("--json-out", default=None)
     return ap.parse_args()
 
@@ -347,15 +349,22 @@ def main():
             per_stage.setdefault(k2, []).append(v)
     stage_ms = {k2: statistics.mean(v) for k2, v in per_stage.items() if k2 != "start"}
 
-    # counts for the byte model, from one pose-0 step outside the timed region
-    ctr = torch.zeros(3, dtype=torch.int64, device="cuda")
-    fs, _ = step(0, counters=ctr)
-    torch.cuda.synchronize()
-    n_visible = int((fs.touched > 0).sum().item())
-    active_buckets, splat_steps = bucket_stats(fs)
-    used_pairs = int(ctr[0].item()) // 9
-    evals = int(ctr[2].item())
-    sb = stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs)
+    # counts for the byte model: one counting step per pose outside the timed regions, averaged
+    # over the poses like the timings
+    per_pose = []
+    for pose in range(len(cams)):
+        ctr = torch.zeros(3, dtype=torch.int64, device="cuda")
+        fs, _ = step(pose, counters=ctr)
+        torch.cuda.synchronize()
+        nv = int((fs.touched > 0).sum().item())
+        ab, ss = bucket_stats(fs)
+        up = int(ctr[0].item()) // 9
+        per_pose.append({"visible": nv, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
+                         "active_buckets": ab, "bucket_splat_steps": ss, "reduced_bucket_splats": up,
+                         "bwd_pair_evals": int(ctr[2].item()),
+                         "bytes": stage_bytes(fs, nv, ab, ss, up)})
+    counts = {k2: round(statistics.mean(pp[k2] for pp in per_pose)) for k2 in per_pose[0] if k2 != "bytes"}
+    sb = {k2: statistics.mean(pp["bytes"][k2] for pp in per_pose) for k2 in per_pose[0]["bytes"]}
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
     dominant = max((k2 for k2 in stage_ms if k2 in SINGLE_KERNEL), key=lambda k2: stage_ms[k2])
     achieved = stage_gbs[dominant]
@@ -389,15 +398,14 @@ def main():
         "stage_hbm_frac": {k2: round(v / HBM_PEAK_GBS, 4) for k2, v in stage_gbs.items()},
         "event_sum_ms": round(statistics.mean(step_ms), 4),
         "staged_pass_ms_per_step": round(staged_wall_ms, 4),
-        "counts": {"visible": n_visible, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
-                   "active_buckets": active_buckets, "bucket_splat_steps": splat_steps,
-                   "reduced_bucket_splats": used_pairs, "bwd_pair_evals": evals},
+        "counts": counts,
         "roofline": {"kernel": SINGLE_KERNEL[dominant], "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes": sb[dominant],
+                     "traffic": traffic, "algorithmic_bytes": round(sb[dominant]),
                      "avg_launch_ms": round(stage_ms[dominant], 4), "valu": valu},
     }
-    out["variants"] = variants_bench(sc, grads, steps=max(args.steps // 2, 5), warmup=3)
+    if not args.no_variants:
+        out["variants"] = variants_bench(sc, grads, steps=max(args.steps // 2, 5), warmup=3)
     if not args.no_train_step:
         out["train_step"] = train_step_bench(scene, steps=max(args.steps // 2, 5), warmup=3)
     if not args.no_cpu_baseline:
