@@ -85,6 +85,63 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_kernel(const uint32_t*
   }
 }
 
+// Sum of one 2048-value tile of in[gather[i]] (in[i] without gather) into block_sums[tile].
+__global__ __launch_bounds__(kScanThreads) void scan_sum_kernel(const uint32_t* __restrict__ in,
+                                                                const uint32_t* __restrict__ gather, int64_t n,
+                                                                uint32_t* __restrict__ block_sums) {
+  __shared__ uint32_t s_wave[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  uint32_t sum = 0;
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) {
+    const int64_t idx = base + e * kScanThreads + threadIdx.x;
+    if (idx < n) sum += in[gather ? gather[idx] : idx];
+  }
+  uint32_t total;
+  block_inclusive_scan(sum, s_wave, total);
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
+}
+
+// Exclusive scan of tile b of in[gather[i]], offset by the sum of the tiles before it (read
+// from block_sums by the whole workgroup); the last tile also writes out[n].
+__global__ __launch_bounds__(kScanThreads) void scan_tile_offset_kernel(const uint32_t* __restrict__ in,
+                                                                        const uint32_t* __restrict__ gather,
+                                                                        uint32_t* __restrict__ out, int64_t n,
+                                                                        const uint32_t* __restrict__ block_sums) {
+  __shared__ uint32_t s_v[kScanTile];
+  __shared__ uint32_t s_wave[4];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  for (int k = threadIdx.x; k < kScanTile; k += kScanThreads) {
+    const int64_t idx = base + k;
+    s_v[k] = idx < n ? in[gather ? gather[idx] : idx] : 0u;
+  }
+  uint32_t before = 0;
+  for (int b = threadIdx.x; b < static_cast<int>(blockIdx.x); b += kScanThreads) before += block_sums[b];
+  uint32_t prefix;
+  block_inclusive_scan(before, s_wave, prefix);  // (the workgroup total of the partial sums)
+  uint32_t local[kScanItems];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) {
+    local[e] = s_v[threadIdx.x * kScanItems + e];
+    sum += local[e];
+  }
+  uint32_t total;
+  const uint32_t incl = block_inclusive_scan(sum, s_wave, total);
+  uint32_t run = prefix + incl - sum;
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) {
+    s_v[threadIdx.x * kScanItems + e] = run;
+    run += local[e];
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < kScanTile; k += kScanThreads) {
+    const int64_t idx = base + k;
+    if (idx < n) out[idx] = s_v[k];
+  }
+  if (threadIdx.x == 0 && blockIdx.x == gridDim.x - 1) out[n] = prefix + total;
+}
+
 __global__ __launch_bounds__(kScanThreads) void scan_add_kernel(uint32_t* __restrict__ out,
                                                                 int64_t n,
                                                                 const uint32_t* __restrict__ offs,
@@ -106,6 +163,10 @@ static size_t scan_ws(int64_t n) {
   return align_up(nb * 4) + align_up((nb + 1) * 4) + scan_ws(nb);
 }
 
+// Tiles up to which a scan is two launches (tile sums; each tile adds the sums before it to its
+// own scan); beyond, the tile sums are scanned recursively (three launches per level).
+constexpr int64_t kScanDirectTiles = 4096;
+
 static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hipStream_t st,
                      const uint32_t* gather = nullptr) {
   const int64_t nb = (n + kScanTile - 1) / kScanTile;
@@ -114,6 +175,13 @@ static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hip
     return;
   }
   uint32_t* sums = reinterpret_cast<uint32_t*>(ws);
+  if (nb <= kScanDirectTiles) {
+    hipLaunchKernelGGL(scan_sum_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st, in, gather, n,
+                       sums);
+    hipLaunchKernelGGL(scan_tile_offset_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st, in,
+                       gather, out, n, sums);
+    return;
+  }
   uint32_t* sums_scan = reinterpret_cast<uint32_t*>(ws + align_up(nb * 4));
   char* next = ws + align_up(nb * 4) + align_up((nb + 1) * 4);
   hipLaunchKernelGGL(scan_tile_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st,

@@ -513,3 +513,19 @@ def test_full_size_100k_sh0_matches_oracle():
     want = O.preprocess_bwd(*host, cam, 0, ref["rec"], ref["touched"], g2)
     for k, (got, w) in enumerate(zip(p, want)):
         assert D.rel_err(np_(got.grad).reshape(w.shape), w) < GRAD_TOL, k
+
+
+@pytest.mark.parametrize("n", [1, 2048, 2049, 1_000_003, 8_388_608, 9_000_001])
+def test_scan_u32_sizes(n):
+    """gs_scan_u32 (two launches up to 4096 tiles of 2048 values, recursive beyond) equals the
+    exclusive prefix sum, with out[n] = total."""
+    from amdsplat import _lib
+
+    g = torch.Generator().manual_seed(n % 1000)
+    vals = torch.randint(0, 64, (n,), generator=g, dtype=torch.int32)
+    out = torch.full((n + 1,), -1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(max(_lib.size_call("gs_scan_workspace_size", n), 1), dtype=torch.uint8, device="cuda")
+    dv = vals.cuda()
+    _lib.call("gs_scan_u32", _lib.ptr(dv), _lib.ptr(out), n, _lib.ptr(ws), ws.numel(), _lib.stream_handle())
+    want = np.concatenate([[0], np.cumsum(vals.numpy().astype(np.int64))])
+    assert np.array_equal(out.cpu().numpy().astype(np.int64), want)
