@@ -342,12 +342,16 @@ def main():
 
     per_stage = {}
     step_ms = []
-    for tm in timers:
+    pose_ms = [[] for _ in cams]
+    for k, tm in enumerate(timers):
         r = tm.result(sync=False)
         step_ms.append(sum(r.values()))
+        pose_ms[k % len(cams)].append(step_ms[-1])
         for k2, v in r.items():
             per_stage.setdefault(k2, []).append(v)
     stage_ms = {k2: statistics.mean(v) for k2, v in per_stage.items() if k2 != "start"}
+    # per pose: the median over its event-timed steps; then the median and the max over the poses
+    pose_medians = [statistics.median(v) for v in pose_ms if v]
 
     # counts for the byte model: one counting step per pose outside the timed regions, averaged
     # over the poses like the timings
@@ -397,6 +401,8 @@ def main():
         "stage_hbm_gbs": {k2: round(v, 1) for k2, v in stage_gbs.items()},
         "stage_hbm_frac": {k2: round(v / HBM_PEAK_GBS, 4) for k2, v in stage_gbs.items()},
         "event_sum_ms": round(statistics.mean(step_ms), 4),
+        "per_pose_ms": {"median": round(statistics.median(pose_medians), 4), "max": round(max(pose_medians), 4),
+                        "poses": [round(v, 4) for v in pose_medians]},
         "staged_pass_ms_per_step": round(staged_wall_ms, 4),
         "counts": counts,
         "roofline": {"kernel": SINGLE_KERNEL[dominant], "bound": "hbm", "achieved": round(achieved, 1),
