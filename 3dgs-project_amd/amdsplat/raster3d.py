@@ -320,7 +320,7 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
         g_b = torch.empty(n, fs.sh_coeffs - 1, 3, dtype=torch.float32, device=dev)
         g_sh = (g_a, g_b)
     call("gs_preprocess_bwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh_a), ptr(sh_b),
-         n, fs.sh_coeffs, fs.sh_degree, cam.c_struct(), ptr(fs.rec), ptr(fs.touched), ptr(grad2d), ptr(g_means),
+         n, fs.sh_coeffs, fs.sh_degree, cam.c_struct(), ptr(fs.touched), ptr(grad2d), ptr(g_means),
          ptr(g_ls), ptr(g_q), ptr(g_op), ptr(g_a), ptr(g_b), st)
     tm.mark("preprocess_bwd")
     return g_means, g_ls, g_q, g_op, g_sh, grad2d, {} if isinstance(timing, StageTimer) else tm.result()

@@ -405,8 +405,7 @@ template <int K>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void preprocess_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
-    ShPtr sh, int64_t n, int active, CamK cam,
-    const SplatRec* __restrict__ rec, const uint32_t* __restrict__ tiles_touched,
+    ShPtr sh, int64_t n, int active, CamK cam, const uint32_t* __restrict__ tiles_touched,
     const float* __restrict__ grad2d, float* __restrict__ g_means,
     float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
     float* __restrict__ g_opacity, ShOut g_sh) {
@@ -434,8 +433,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void p
   float dx = 0.0f, dy = 0.0f, dz = 0.0f, il = 0.0f;
   float basis[16], gb[16];
   if (vis) {
-    const uint32_t mask = __float_as_uint(rec[i].c.w);
-    for (int ch = 0; ch < 3; ++ch) gcol[ch] = (mask & (1u << ch)) ? 0.0f : g2[6 + ch];
     const float dxw = means[3 * i] - cam.campos[0];
     const float dyw = means[3 * i + 1] - cam.campos[1];
     const float dzw = means[3 * i + 2] - cam.campos[2];
@@ -455,6 +452,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void p
       if (lane / St::RH == h) {
         float* row = srow + (lane - St::RH * h) * St::CP;
         if (vis) {
+          // the forward's colour clamp (a channel clamped at 0 passes no gradient), recomputed
+          // from the same rows and basis in the forward's operation order: the same bits, without
+          // reading the 64-byte splat record for its mask
+#pragma unroll
+          for (int ch = 0; ch < 3; ++ch) {
+            float acc = basis[0] * row[ch];
+            for (int k = 1; k < active; ++k) acc = fmaf(basis[k], row[3 * k + ch], acc);
+            gcol[ch] = (acc + 0.5f < 0.0f) ? 0.0f : g2[6 + ch];
+          }
 #pragma unroll
           for (int k = 0; k < K; ++k) {
             const bool on = k < active;
@@ -628,12 +634,12 @@ static void launch_pre_fwd(int64_t blocks, hipStream_t st, const float* means, c
 template <int K>
 static void launch_pre_bwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
                            const float* quats, const float* op, ShPtr sh, int64_t n,
-                           int active, const CamK& cam, const float* rec, const uint32_t* touched,
+                           int active, const CamK& cam, const uint32_t* touched,
                            const float* g2, float* gm, float* gls, float* gq, float* gop,
                            ShOut gsh) {
   hipLaunchKernelGGL(preprocess_bwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
-                     reinterpret_cast<const SplatRec*>(rec), touched, g2, gm, gls,
+                     touched, g2, gm, gls,
                      reinterpret_cast<float4*>(gq), gop, gsh);
 }
 
@@ -677,7 +683,7 @@ extern "C" int gs_preprocess_fwd(const float* means, const float* log_scales, co
 extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, const float* quats,
                                  const float* opacity_logits, const float* sh, const float* sh_rest,
                                  int64_t n, int sh_coeffs, int sh_degree, const gs_camera* cam,
-                                 const float* splat_rec, const uint32_t* tiles_touched,
+                                 const uint32_t* tiles_touched,
                                  const float* grad2d, float* grad_means, float* grad_log_scales,
                                  float* grad_quats, float* grad_opacity_logits, float* grad_sh,
                                  float* grad_sh_rest, void* stream) {
@@ -686,14 +692,14 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
   if (int e = check_cam(cam)) return e;
   if (int e = check_sh(sh_coeffs, sh_degree)) return e;
   if (n == 0) return GS_OK;
-  GS_REQUIRE(means && log_scales && quats && opacity_logits && sh && splat_rec && tiles_touched &&
+  GS_REQUIRE(means && log_scales && quats && opacity_logits && sh && tiles_touched &&
                  grad2d && grad_means && grad_log_scales && grad_quats && grad_opacity_logits &&
                  grad_sh,
              GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(!sh_rest == !grad_sh_rest, GS_ERR_ARG, "sh_rest and grad_sh_rest go together");
   GS_REQUIRE(!(sh_rest && sh_coeffs == 1), GS_ERR_ARG, "sh_rest given for a DC-only model");
-  GS_REQUIRE(aligned(quats, 16) && aligned(splat_rec, 16) && aligned(grad_quats, 16), GS_ERR_ALIGN,
-             "quats, splat_rec and grad_quats must be 16-byte aligned");
+  GS_REQUIRE(aligned(quats, 16) && aligned(grad_quats, 16), GS_ERR_ALIGN,
+             "quats and grad_quats must be 16-byte aligned");
   const CamK k = make_cam(*cam);
   const int active = (sh_degree + 1) * (sh_degree + 1);
   const int64_t blocks = (n + 255) / 256;
@@ -701,10 +707,10 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
   const ShPtr shp{sh, sh_rest};
   const ShOut gsh{grad_sh, grad_sh_rest};
   switch (sh_coeffs) {
-    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
-    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
-    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
-    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, splat_rec, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
   }
   return check_launch("preprocess_bwd");
 }

@@ -230,10 +230,12 @@ int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32
  *   grad_means, grad_log_scales [n,3]; grad_quats [n,4]; grad_opacity_logits [n];
  *   grad_sh [n, sh_coeffs, 3] (coefficients above the active degree get 0); with the split
  *   layout (sh_rest not NULL) grad_sh [n, 1, 3] and grad_sh_rest [n, sh_coeffs - 1, 3].
+ *   The colour clamp of the forward is recomputed from the SH rows it reads anyway (the same
+ *   operations, so the same bits), so the splat records are not needed.
  * ------------------------------------------------------------------------------------- */
 int gs_preprocess_bwd(const float* means, const float* log_scales, const float* quats,
                       const float* opacity_logits, const float* sh, const float* sh_rest, int64_t n,
-                      int sh_coeffs, int sh_degree, const gs_camera* cam, const float* splat_rec,
+                      int sh_coeffs, int sh_degree, const gs_camera* cam,
                       const uint32_t* tiles_touched, const float* grad2d, float* grad_means,
                       float* grad_log_scales, float* grad_quats, float* grad_opacity_logits,
                       float* grad_sh, float* grad_sh_rest, void* stream);
