@@ -204,6 +204,12 @@ __global__ void iota_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = static_cast<uint32_t>(i);
 }
 
+__global__ void gather_u32_kernel(const uint32_t* __restrict__ src, const uint32_t* __restrict__ idx, int64_t n,
+                                  uint32_t* __restrict__ out) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j < n) out[j] = src[idx[j]];
+}
+
 __global__ void fill_f32_kernel(float* __restrict__ p, int64_t n, float v) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -311,7 +317,7 @@ template <int BITS, int ROUNDS>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin, uint32_t* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles,
-    const uint32_t* __restrict__ totals) {
+    const uint32_t* __restrict__ totals, const uint32_t* __restrict__ aux_src, uint32_t* __restrict__ aux_out) {
   constexpr int R = 1 << BITS;
   __shared__ uint32_t s_cnt[kRsWaves][R];  // per-wavefront digit counts, then wavefront offsets
   __shared__ uint32_t s_excl[R];           // start of each digit inside the staged tile
@@ -411,6 +417,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t g = s_goff[d] + (static_cast<uint32_t>(p) - s_excl[d]);
     kout[g] = k;
     vout[g] = s_val[p];
+    if (aux_out) aux_out[g] = aux_src[s_val[p]];  // a per-value array, gathered into sorted order
   }
 }
 
@@ -438,12 +445,13 @@ static size_t sort_ws(int64_t m) {
 
 template <int BITS, int ROUNDS>
 static void sort_pass_r(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
-                        uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st) {
+                        uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st,
+                        const uint32_t* aux_src, uint32_t* aux_out) {
   hipLaunchKernelGGL((rs_upsweep_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
                      n_tiles);
   hipLaunchKernelGGL(rs_rowscan_kernel, dim3(1 << BITS), dim3(kScanThreads), 0, st, tile_hist, n_tiles, totals);
   hipLaunchKernelGGL((rs_scatter_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
-                     tile_hist, n_tiles, totals);
+                     tile_hist, n_tiles, totals, aux_src, aux_out);
 }
 
 static int sort_rounds(int64_t m) {
@@ -454,17 +462,20 @@ static int sort_rounds(int64_t m) {
 
 template <int BITS>
 static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
-                      uint32_t* tile_hist, int rounds, uint32_t* totals, hipStream_t st) {
+                      uint32_t* tile_hist, int rounds, uint32_t* totals, hipStream_t st, const uint32_t* aux_src,
+                      uint32_t* aux_out) {
   const int n_tiles = static_cast<int>((m + kRsWaves * kWave * rounds - 1) / (kRsWaves * kWave * rounds));
-  if (rounds == 16) sort_pass_r<BITS, 16>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st);
-  else if (rounds == 8) sort_pass_r<BITS, 8>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st);
-  else sort_pass_r<BITS, 4>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st);
+  if (rounds == 16) sort_pass_r<BITS, 16>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out);
+  else if (rounds == 8) sort_pass_r<BITS, 8>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out);
+  else sort_pass_r<BITS, 4>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out);
 }
 
 // Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
 // v = NULL stands for the values 0, 1, ..., m - 1.
+// aux_src / aux_out (both or neither): the last pass also writes aux_out[j] = aux_src[v_out[j]].
 static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, uint32_t* v_out, int64_t m,
-                       int bits, char* ws, hipStream_t st) {
+                       int bits, char* ws, hipStream_t st, const uint32_t* aux_src = nullptr,
+                       uint32_t* aux_out = nullptr) {
   if (m <= 0) return;
   const SortPlan plan = sort_plan(bits);
   if (plan.passes == 0) {
@@ -474,6 +485,9 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     } else {
       hipLaunchKernelGGL(iota_u32_kernel, dim3(static_cast<unsigned>((m + 255) / 256)), dim3(256), 0, st, v_out, m);
     }
+    if (aux_out)
+      hipLaunchKernelGGL(gather_u32_kernel, dim3(static_cast<unsigned>((m + 255) / 256)), dim3(256), 0, st, aux_src,
+                         v_out, m, aux_out);
     return;
   }
   const int rounds = sort_rounds(m);
@@ -495,16 +509,19 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     uint32_t* dst_v = to_out ? v_out : v_alt;
     uint32_t* tot = totals + (1 << kRsMaxBits) * p;
     const int shift = plan.bits * p;
+    const bool last = p == plan.passes - 1;
+    const uint32_t* as = last ? aux_src : nullptr;
+    uint32_t* ao = last ? aux_out : nullptr;
     switch (plan.bits) {
-      case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 2: sort_pass<2>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 3: sort_pass<3>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 4: sort_pass<4>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      case 8: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
-      default: sort_pass<9>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st); break;
+      case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 2: sort_pass<2>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 3: sort_pass<3>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 4: sort_pass<4>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 8: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      default: sort_pass<9>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
     }
     src_k = dst_k;
     src_v = dst_v;
@@ -540,11 +557,6 @@ __global__ void depth_keys_kernel(const SplatRec* __restrict__ rec, const float*
   keys[i] = k;
 }
 
-__global__ void gather_u32_kernel(const uint32_t* __restrict__ src, const uint32_t* __restrict__ idx, int64_t n,
-                                  uint32_t* __restrict__ out) {
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (j < n) out[j] = src[idx[j]];
-}
 
 // Tile rectangle (tx0, ty0, tx1, ty1), max exclusive, clipped to the tile grid.
 __device__ __forceinline__ int4 clamp_rect(int4 r, int tiles_x, int tiles_y) {
@@ -945,18 +957,24 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
                          counts, n, dkeys, depth64 ? khi : nullptr);
       keys = dkeys;
     }
+    // the final pass also writes the counts in depth order (into khi, free by then), so the scan
+    // reads them contiguously instead of through the order
+    uint32_t* sorted_counts = offsets ? khi : nullptr;
     if (depth64) {
       // low key halves first, then stably by the high halves gathered into that order
       radix_sort(keys, nullptr, dsorted, tmpv, n, 32, sort_scratch, st);
       hipLaunchKernelGGL(gather_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, khi, tmpv, n, dkeys);
-      radix_sort(dkeys, tmpv, dsorted, order, n, 32, sort_scratch, st);
+      radix_sort(dkeys, tmpv, dsorted, order, n, 32, sort_scratch, st, sorted_counts ? counts : nullptr,
+                 sorted_counts);
     } else {
-      radix_sort(keys, nullptr, dsorted, order, n, bits, sort_scratch, st);
+      radix_sort(keys, nullptr, dsorted, order, n, bits, sort_scratch, st, sorted_counts ? counts : nullptr,
+                 sorted_counts);
     }
+    if (offsets) scan_rec(sorted_counts, offsets, n, scan_scratch, st);
   } else {
     hipLaunchKernelGGL(iota_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, n);
+    if (offsets) scan_rec(counts, offsets, n, scan_scratch, st);  // index order
   }
-  if (offsets) scan_rec(counts, offsets, n, scan_scratch, st, order);
 }
 
 // Emission of the instances in depth order, stable sort by tile, tile ranges and bucket
