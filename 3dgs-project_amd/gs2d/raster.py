@@ -117,7 +117,7 @@ class _Rasterize(torch.autograd.Function):
 def rasterize(means, conic, color, opacity, bins: Bins, bg=None, backend: str = "splat"):
     """Render a (3, H, W) image. backend: 'splat' (bucketed backward) or 'pixel' (per-pixel backward)."""
     if backend == "ref":
-        raise ValueError("backend 'ref' (the dense PyTorch CPU reference) is not part of this build; "
+        raise ValueError("backend 'ref' (the dense PyTorch CPU reference) is not provided; "
                          "use 'splat' or 'pixel' on a GPU")
     if backend not in ("pixel", "splat"):
         raise ValueError(f"unknown backend {backend!r}")

@@ -168,7 +168,7 @@ def load_extension(with_cuda: bool | None = None, verbose: bool = False) -> _Ext
     `with_cuda=False` raises."""
     global _EXT
     if with_cuda is False:
-        raise RuntimeError("splat2d on this build runs on the GPU only (no CPU extension)")
+        raise RuntimeError("splat2d runs on the GPU only (there is no CPU extension)")
     if _EXT is None:
         from amdsplat import _lib
 

@@ -292,7 +292,7 @@ def copy_probe():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; runs on several GPUs are not part of it",
+        print(json.dumps({"error": "the benchmark runs on one GPU; several GPUs are not supported",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.copy_probe:

@@ -1,7 +1,7 @@
 """GPU parity of the 3D path: HIP kernels (through the C ABI) against the CPU oracle and the
 float64 autograd reference, on identical seeded inputs.
 
-Bar (north star): tile assignment, sorted keys and per-tile ranges bit-exact; forward image
+Bar: tile assignment, sorted keys and per-tile ranges bit-exact; forward image
 and alpha within 1e-5 max abs; gradients within 1e-4 relative L2 (atomic order differs).
 Scenes follow phase1/tests/test_parity.py:43-84 (camera-space scenes with partial tiles,
 heavy overlap, small splats) plus the empty case of :143-153.
