@@ -317,7 +317,8 @@ template <int BITS, int ROUNDS>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin, uint32_t* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles,
-    const uint32_t* __restrict__ totals, const uint32_t* __restrict__ aux_src, uint32_t* __restrict__ aux_out) {
+    const uint32_t* __restrict__ totals, const uint32_t* __restrict__ aux_src, uint32_t* __restrict__ aux_out,
+    uint32_t* __restrict__ ranges) {
   constexpr int R = 1 << BITS;
   __shared__ uint32_t s_cnt[kRsWaves][R];  // per-wavefront digit counts, then wavefront offsets
   __shared__ uint32_t s_excl[R];           // start of each digit inside the staged tile
@@ -415,9 +416,16 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t k = s_key[p];
     const uint32_t d = (k >> shift) & (R - 1);
     const uint32_t g = s_goff[d] + (static_cast<uint32_t>(p) - s_excl[d]);
-    kout[g] = k;
+    if (kout) kout[g] = k;
     vout[g] = s_val[p];
     if (aux_out) aux_out[g] = aux_src[s_val[p]];  // a per-value array, gathered into sorted order
+    if (ranges) {
+      // last pass: the lower digits are sorted already, so a key's copies in this tile form one
+      // run of consecutive output positions; the runs' ends give each key's [start, end) over
+      // all tiles (ranges preset to [~0, 0])
+      if (p == 0 || s_key[p - 1] != k) atomicMin(&ranges[2 * static_cast<int64_t>(k)], g);
+      if (p == count - 1 || s_key[p + 1] != k) atomicMax(&ranges[2 * static_cast<int64_t>(k) + 1], g + 1u);
+    }
   }
 }
 
@@ -446,12 +454,12 @@ static size_t sort_ws(int64_t m) {
 template <int BITS, int ROUNDS>
 static void sort_pass_r(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
                         uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st,
-                        const uint32_t* aux_src, uint32_t* aux_out) {
+                        const uint32_t* aux_src, uint32_t* aux_out, uint32_t* ranges) {
   hipLaunchKernelGGL((rs_upsweep_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
                      n_tiles);
   hipLaunchKernelGGL(rs_rowscan_kernel, dim3(1 << BITS), dim3(kScanThreads), 0, st, tile_hist, n_tiles, totals);
   hipLaunchKernelGGL((rs_scatter_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
-                     tile_hist, n_tiles, totals, aux_src, aux_out);
+                     tile_hist, n_tiles, totals, aux_src, aux_out, ranges);
 }
 
 static int sort_rounds(int64_t m) {
@@ -463,19 +471,22 @@ static int sort_rounds(int64_t m) {
 template <int BITS>
 static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
                       uint32_t* tile_hist, int rounds, uint32_t* totals, hipStream_t st, const uint32_t* aux_src,
-                      uint32_t* aux_out) {
+                      uint32_t* aux_out, uint32_t* ranges) {
   const int n_tiles = static_cast<int>((m + kRsWaves * kWave * rounds - 1) / (kRsWaves * kWave * rounds));
-  if (rounds == 16) sort_pass_r<BITS, 16>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out);
-  else if (rounds == 8) sort_pass_r<BITS, 8>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out);
-  else sort_pass_r<BITS, 4>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out);
+  if (rounds == 16) sort_pass_r<BITS, 16>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out, ranges);
+  else if (rounds == 8) sort_pass_r<BITS, 8>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out, ranges);
+  else sort_pass_r<BITS, 4>(sk, sv, dk, dv, m, shift, tile_hist, n_tiles, totals, st, aux_src, aux_out, ranges);
 }
 
 // Sorts (k, v) by the low `bits` bits of k into (k_out, v_out), which must not alias (k, v).
 // v = NULL stands for the values 0, 1, ..., m - 1.
 // aux_src / aux_out (both or neither): the last pass also writes aux_out[j] = aux_src[v_out[j]].
+// ranges (the sort has at least one pass): the last pass also takes every key value's [start,
+// end) in the output by atomic min / max (ranges preset to [~0, 0]). drop_keys: the last pass
+// writes only the values (k_out is still used by earlier passes).
 static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, uint32_t* v_out, int64_t m,
                        int bits, char* ws, hipStream_t st, const uint32_t* aux_src = nullptr,
-                       uint32_t* aux_out = nullptr) {
+                       uint32_t* aux_out = nullptr, uint32_t* ranges = nullptr, bool drop_keys = false) {
   if (m <= 0) return;
   const SortPlan plan = sort_plan(bits);
   if (plan.passes == 0) {
@@ -512,16 +523,18 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     const bool last = p == plan.passes - 1;
     const uint32_t* as = last ? aux_src : nullptr;
     uint32_t* ao = last ? aux_out : nullptr;
+    uint32_t* rg = last ? ranges : nullptr;
+    uint32_t* dk = (last && drop_keys) ? nullptr : dst_k;
     switch (plan.bits) {
-      case 1: sort_pass<1>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 2: sort_pass<2>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 3: sort_pass<3>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 4: sort_pass<4>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 5: sort_pass<5>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 6: sort_pass<6>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 7: sort_pass<7>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      case 8: sort_pass<8>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
-      default: sort_pass<9>(src_k, src_v, dst_k, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao); break;
+      case 1: sort_pass<1>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 2: sort_pass<2>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 3: sort_pass<3>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 4: sort_pass<4>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 5: sort_pass<5>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 6: sort_pass<6>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 7: sort_pass<7>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 8: sort_pass<8>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      default: sort_pass<9>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
     }
     src_k = dst_k;
     src_v = dst_v;
@@ -618,7 +631,8 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
                                                    const uint32_t* __restrict__ offs, int64_t n,
                                                    const uint32_t* __restrict__ wstart, int64_t n_windows,
                                                    int tiles_x, int tiles_y, uint32_t* __restrict__ tkeys,
-                                                   uint32_t* __restrict__ vals) {
+                                                   uint32_t* __restrict__ vals, uint32_t* __restrict__ ranges_preset,
+                                                   int n_tiles) {
   __shared__ EmitSetup s_set[4][kWave];
   __shared__ uint32_t s_rex[4][kWave];       // exclusive prefix of tile rows over the 64 Gaussians
   __shared__ uint32_t s_gid[4][kWave];
@@ -627,6 +641,13 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
   __shared__ uint32_t s_row[4][kEmitChunk];  // (owner lane << 26) | first tile of the row
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  if (ranges_preset) {
+    // [~0, 0] for every tile: the tile sort's last pass narrows them by atomic min / max
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < 2 * static_cast<int64_t>(n_tiles);
+         q += stride)
+      ranges_preset[q] = (q & 1) ? 0u : 0xffffffffu;
+  }
   const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + wave;
   if (w >= n_windows) return;  // whole wavefront
   const int64_t ja = wstart[w];
@@ -821,56 +842,83 @@ constexpr int kBoItems = 8;
 __global__ __launch_bounds__(kBoThreads) void bucket_offsets_kernel(uint32_t* __restrict__ ranges, int n_tiles,
                                                                     int64_t m, uint32_t* __restrict__ boff,
                                                                     uint32_t* __restrict__ tile_offsets,
-                                                                    uint32_t* __restrict__ list_header) {
+                                                                    uint32_t* __restrict__ list_header,
+                                                                    bool fix_empty) {
   __shared__ uint32_t s_wave[kBoThreads / kWave];
+  __shared__ uint32_t s_wave_inst[kBoThreads / kWave];
   if (list_header && threadIdx.x < kListHeader) list_header[threadIdx.x] = 0u;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  uint32_t run = 0;
+  // fix_empty: ranges come from the sort's atomic min / max, so a tile without instances still
+  // holds [~0, 0]; the instance counts are scanned beside the bucket counts and such a tile gets
+  // the empty range at its CSR position
+  uint32_t run = 0, run_inst = 0;
   for (int c0 = 0; c0 < n_tiles; c0 += kBoThreads * kBoItems) {
-    uint32_t cnt[kBoItems], start[kBoItems], sum = 0;
+    uint32_t cnt[kBoItems], start[kBoItems], len[kBoItems], sum = 0, sum_inst = 0;
 #pragma unroll
     for (int e = 0; e < kBoItems; ++e) {
       const int t = c0 + static_cast<int>(threadIdx.x) * kBoItems + e;
       cnt[e] = 0;
       start[e] = 0;
+      len[e] = 0;
       if (t < n_tiles) {
         if (m > 0) {
           start[e] = ranges[2 * t];
-          cnt[e] = (ranges[2 * t + 1] - start[e] + kBucket - 1) / kBucket;
+          const uint32_t end = ranges[2 * t + 1];
+          len[e] = (fix_empty && start[e] == 0xffffffffu) ? 0u : end - start[e];
+          cnt[e] = (len[e] + kBucket - 1) / kBucket;
         } else {
           ranges[2 * t] = 0;
           ranges[2 * t + 1] = 0;
         }
       }
       sum += cnt[e];
+      sum_inst += len[e];
     }
-    uint32_t incl = sum;
+    uint32_t incl = sum, incl_inst = sum_inst;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
       const uint32_t u = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += u;
+      const uint32_t ui = __shfl_up(incl_inst, o, 64);
+      if (lane >= o) {
+        incl += u;
+        incl_inst += ui;
+      }
     }
-    if (lane == kWave - 1) s_wave[wave] = incl;
+    if (lane == kWave - 1) {
+      s_wave[wave] = incl;
+      s_wave_inst[wave] = incl_inst;
+    }
     __syncthreads();
-    uint32_t before = 0, total = 0;
+    uint32_t before = 0, total = 0, before_inst = 0, total_inst = 0;
     for (int w = 0; w < kBoThreads / kWave; ++w) {
       const uint32_t v = s_wave[w];
+      const uint32_t vi = s_wave_inst[w];
       before += w < wave ? v : 0u;
+      before_inst += w < wave ? vi : 0u;
       total += v;
+      total_inst += vi;
     }
     __syncthreads();
     uint32_t pos = run + before + incl - sum;
+    uint32_t pos_inst = run_inst + before_inst + incl_inst - sum_inst;
 #pragma unroll
     for (int e = 0; e < kBoItems; ++e) {
       const int t = c0 + static_cast<int>(threadIdx.x) * kBoItems + e;
       if (t < n_tiles) {
         boff[t] = pos;
+        if (fix_empty && m > 0 && len[e] == 0) {
+          start[e] = pos_inst;
+          ranges[2 * t] = pos_inst;
+          ranges[2 * t + 1] = pos_inst;
+        }
         if (tile_offsets) tile_offsets[t] = start[e];
       }
       pos += cnt[e];
+      pos_inst += len[e];
     }
     run += total;
+    run_inst += total_inst;
   }
   if (threadIdx.x == 0) {
     boff[n_tiles] = run;
@@ -993,22 +1041,31 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
     const int64_t n_windows = (m + kEmitSpan - 1) / kEmitSpan;
     hipLaunchKernelGGL(emit_windows_kernel, dim3(grid_for(n + 1, 256)), dim3(256), 0, st, offsets, n, n_windows,
                        wstart);
+    // with at least one sort pass, the last pass takes the tile ranges (preset by the emission)
+    // and the sorted keys are written only if the caller wants them
+    const bool sort_ranges = bits_for(n_tiles) > 0;
+    uint32_t* preset = sort_ranges ? ranges : nullptr;
     if (rects) {
       hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
-                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
+                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
     } else {
       hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
-                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals);
+                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
     }
-    radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st);
+    radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st, nullptr, nullptr, preset,
+               sort_ranges && !sorted_keys);
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
                          dkey_of, dkey0, m, sorted_keys);
-    hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for((m + kBoundsPer - 1) / kBoundsPer, 256)), dim3(256), 0, st,
-                       tsorted, m, n_tiles, ranges);
+    if (!sort_ranges)
+      hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for((m + kBoundsPer - 1) / kBoundsPer, 256)), dim3(256), 0,
+                         st, tsorted, m, n_tiles, ranges);
+    hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
+                       tile_offsets, list_header, sort_ranges);
+    return;
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
-                     tile_offsets, list_header);
+                     tile_offsets, list_header, false);
 }
 
 }  // namespace gs
