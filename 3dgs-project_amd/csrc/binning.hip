@@ -587,8 +587,9 @@ __device__ __forceinline__ int4 clamp_rect(int4 r, int tiles_x, int tiles_y) {
 // rows, computes the touched columns of up to kEmitChunk rows at a time (a lane per row), then
 // writes rows of at least kEmitWide tiles one row at a time (a lane per tile) and the other
 // rows' instances a lane per instance, so stores are coalesced.
-constexpr uint32_t kEmitSpan = 512;
-constexpr int kEmitChunk = 256;
+constexpr uint32_t kEmitSpan = 256;
+constexpr int kEmitChunk = 128;
+constexpr int kEmitPer = kEmitChunk / kWave;  // rows per lane in the prefix step
 constexpr uint32_t kEmitWide = 32;
 constexpr int64_t kMaxTiles = int64_t(1) << 26;  // tile ids share a word with a 6-bit lane index
 
@@ -720,10 +721,10 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
         s_row[wave][q] = first;
       }
       wave_sync();
-      uint32_t c[4], ex[4], lsum = 0, nsum = 0;
+      uint32_t c[kEmitPer], ex[kEmitPer], lsum = 0, nsum = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int q = 4 * lane + e;
+      for (int e = 0; e < kEmitPer; ++e) {
+        const int q = kEmitPer * lane + e;
         c[e] = q < nr ? s_iex[wave][q] : 0u;
         lsum += c[e];
         nsum += c[e] < kEmitWide ? c[e] : 0u;
@@ -733,20 +734,20 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
       uint32_t nrun = wave_excl_scan(nsum, lane, ntotal);
       wave_sync();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < kEmitPer; ++e) {
         ex[e] = run;
-        s_iex[wave][4 * lane + e] = run;
-        s_nex[wave][4 * lane + e] = nrun;
+        s_iex[wave][kEmitPer * lane + e] = run;
+        s_nex[wave][kEmitPer * lane + e] = nrun;
         run += c[e];
         nrun += c[e] < kEmitWide ? c[e] : 0u;
       }
       wave_sync();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < kEmitPer; ++e) {
         for (uint64_t wm = __ballot(c[e] >= kEmitWide ? 1 : 0); wm != 0ull; wm &= wm - 1ull) {
           const int src = __ffsll(static_cast<unsigned long long>(wm)) - 1;
           const uint32_t nt = __shfl(c[e], src, 64), start = done + __shfl(ex[e], src, 64);
-          const uint32_t rw = s_row[wave][4 * src + e];
+          const uint32_t rw = s_row[wave][kEmitPer * src + e];
           const uint32_t gw = s_gid[wave][rw >> 26];
           for (uint32_t t = lane; t < nt; t += kWave) {
             const uint32_t k = start + t;
