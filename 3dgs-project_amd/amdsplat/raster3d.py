@@ -267,7 +267,6 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
                             {} if isinstance(timing, StageTimer) else tm.result())
     image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
     final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
-    tm.mark("buckets")
     call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
          ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), ptr(blist), ptr(bucket_to_tile),
          ptr(grad2d), grad2d.numel() if grad2d is not None else 0,
@@ -300,7 +299,6 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
         grad2d, fs.grad2d = fs.grad2d, None
     else:
         grad2d = torch.zeros(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
-    tm.mark("grad_zero")
     call("gs_blend_bwd_3d", ptr(fs.rec), ptr(fs.ranges), ptr(fs.point_list), ptr(fs.bucket_offsets),
          ptr(fs.bucket_to_tile), fs.n_buckets_max, n, cam.width, cam.height, ptr(fs.image), ptr(grad_image),
          ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(fs.bucket_list),

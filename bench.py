@@ -56,7 +56,8 @@ def parse():
     return ap.parse_args()
 
 
-def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, atomics_per_pair=9):
+def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, ckpt_written,
+                atomics_per_pair=9):
     """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
     written once (fp32)."""
     n, m, K = fs.n, fs.m, fs.sh_coeffs
@@ -67,17 +68,17 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, atomics_
         # params 44 B/Gaussian + tiles_touched and depth key 8 B; SH 12 K B and the 64 B record
         # per visible one
         "preprocess": 44 * n + 8 * n + n_visible * (12 * K + 64),
-        # 4 radix passes over N (read+write key and value), then the order, the gathered counts
-        # and the offsets of the scan
-        "depth_order": 4 * 16 * n + 12 * n,
-        # emission (record of the visible, order and offsets per Gaussian, key+value per
-        # instance), 2 radix passes over M, tile bounds (one key read per instance)
-        "binning": 64 * n_visible + 8 * n + 8 * m + 2 * 16 * m + 4 * m + 8 * T,
-        "buckets": 8 * T + 4 * B,
-        # per instance: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4; the
-        # checkpoints 4 KiB per bucket; tile max
-        "blend_fwd": m * (4 + 64) + P * 20 + B * 4096 + 4 * T,
-        "grad_zero": 48 * n,
+        # 3 radix passes over N (histogram read 4 B, key+value read and write 16 B), the counts
+        # gathered into depth order (read + write), the scan (counts read, offsets written)
+        "depth_order": 3 * 20 * n + 8 * n + 8 * n,
+        # emission (48 B of the record of the visible, order and offset per Gaussian, key+value
+        # per instance), tile sort pass 1 (histogram 4, key+value read and write 16) and pass 2
+        # (histogram 4, key+value read 8, value write 4), ranges and bucket offsets per tile
+        "binning": 48 * n_visible + 8 * n + 8 * m + 20 * m + 16 * m + 20 * T + 4 * B,
+        # per staged list entry: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4;
+        # the checkpoints written (4 KiB per bucket reached); tile max, bucket_to_tile, and the
+        # backward's screen-space gradient buffer the forward zeroes (48 B per Gaussian)
+        "blend_fwd": staged * (4 + 64) + P * 20 + ckpt_written * 4096 + 4 * T + 4 * B + 48 * n,
         # per active bucket: checkpoints 4 KiB + grad image 12, image 12, n_contrib 4 per pixel;
         # per bucket-splat step: id + record; per reduced bucket-splat: 9 fp32 atomics (11 with
         # the |dL/dmean2d| sums)
@@ -88,13 +89,19 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, atomics_
 
 
 def bucket_stats(fs):
+    """(active buckets, sum of tile_max, staged list entries, checkpoints written) of a forward:
+    the forward blend stages 256 list entries at a time and stops after the batch in which every
+    pixel of the tile has stopped (at or after its tile_max)."""
     import numpy as np
 
     boff = fs.bucket_offsets.cpu().numpy().astype(np.int64)
     tmax = fs.tile_max.cpu().numpy().astype(np.int64)
+    rg = fs.ranges.cpu().numpy().astype(np.int64)
+    length = rg[:, 1] - rg[:, 0]
     nbk = np.diff(boff)
     active = np.minimum(nbk, (tmax + 31) // 32)
-    return int(active.sum()), int(tmax.sum())
+    staged = np.minimum(length, (tmax + 255) // 256 * 256)
+    return int(active.sum()), int(tmax.sum()), int(staged.sum()), int(((staged + 31) // 32).sum())
 
 
 def measured_traffic(kernel: str):
@@ -361,12 +368,13 @@ def main():
         fs, _ = step(pose, counters=ctr)
         torch.cuda.synchronize()
         nv = int((fs.touched > 0).sum().item())
-        ab, ss = bucket_stats(fs)
+        ab, ss, stg, ckw = bucket_stats(fs)
         up = int(ctr[0].item()) // 9
         per_pose.append({"visible": nv, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
-                         "active_buckets": ab, "bucket_splat_steps": ss, "reduced_bucket_splats": up,
+                         "active_buckets": ab, "bucket_splat_steps": ss, "staged_entries": stg,
+                         "ckpt_written": ckw, "reduced_bucket_splats": up,
                          "bwd_pair_evals": int(ctr[2].item()),
-                         "bytes": stage_bytes(fs, nv, ab, ss, up)})
+                         "bytes": stage_bytes(fs, nv, ab, ss, up, stg, ckw)})
     counts = {k2: round(statistics.mean(pp[k2] for pp in per_pose)) for k2 in per_pose[0] if k2 != "bytes"}
     sb = {k2: statistics.mean(pp["bytes"][k2] for pp in per_pose) for k2 in per_pose[0]["bytes"]}
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
