@@ -1007,17 +1007,18 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
       keys = dkeys;
     }
     // the final pass also writes the counts in depth order (into khi, free by then), so the scan
-    // reads them contiguously instead of through the order
+    // reads them contiguously instead of through the order; the sorted keys themselves are not
+    // needed, so it writes none
     uint32_t* sorted_counts = offsets ? khi : nullptr;
     if (depth64) {
       // low key halves first, then stably by the high halves gathered into that order
       radix_sort(keys, nullptr, dsorted, tmpv, n, 32, sort_scratch, st);
       hipLaunchKernelGGL(gather_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, khi, tmpv, n, dkeys);
       radix_sort(dkeys, tmpv, dsorted, order, n, 32, sort_scratch, st, sorted_counts ? counts : nullptr,
-                 sorted_counts);
+                 sorted_counts, nullptr, true);
     } else {
       radix_sort(keys, nullptr, dsorted, order, n, bits, sort_scratch, st, sorted_counts ? counts : nullptr,
-                 sorted_counts);
+                 sorted_counts, nullptr, true);
     }
     if (offsets) scan_rec(sorted_counts, offsets, n, scan_scratch, st);
   } else {
