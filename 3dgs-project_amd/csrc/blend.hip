@@ -318,6 +318,155 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
 }
 
 
+// 3D forward with the tile's 4 strips split over 4 / P wavefronts. A lane owns the P pixels of
+// one column that lie in its wavefront's strips (pixel 64 r + lane of the tile: row 4 r + lane /
+// 16, column lane % 16, the pixel layout of the bucketed backward): the column terms of the power
+// are computed once per splat for its P pixels, the strip test of pixel r is one scalar bit test,
+// and each wavefront stages the tile's list 64 entries at a time in its own LDS, so it waits for
+// no other wavefront until the tile's end. The per-pixel operations and decisions are
+// blend_fwd_kernel's (same image, T, n_contrib and checkpoints).
+template <int P>
+__global__ __launch_bounds__(4 * kWave) void blend_fwd_strip_kernel(BlendArgs<float> a) {
+  using Ru = Rule<kRules3D, float>;
+  constexpr int kWT = kStrips / P;  // wavefronts per tile
+  constexpr int kTPB = 4 / kWT;     // tiles per workgroup
+  __shared__ Staged<float> s_sp[4][kWave];
+  __shared__ uint32_t s_max[kTPB];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = wave % kWT;  // the wavefront's strips: sub P ... sub P + P - 1
+  const int tile = static_cast<int>(blockIdx.x) * kTPB + wave / kWT;
+  const bool real = tile < a.n_tiles;
+  if (lane == 0 && sub == 0) s_max[wave / kWT] = 0u;
+  Staged<float>* sw = s_sp[wave];
+  const int tt = real ? tile : 0;
+  const int tx = tt % a.tiles_x, ty = tt / a.tiles_x;
+  const uint32_t r0 = a.ranges[static_cast<int64_t>(tt) * a.range_stride];
+  const uint32_t r1 = a.ranges[static_cast<int64_t>(tt) * a.range_stride + 1];
+  const int len = real ? static_cast<int>(r1 - r0) : 0;
+  const int px = tx * kTile + (lane & 15);
+  const float pxf = static_cast<float>(px) + Ru::pix_off();
+  float T[P], Cr[P], Cg[P], Cb[P], pyf[P];
+  int last[P];
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int py = ty * kTile + kStripRows * (sub * P + r) + (lane >> 4);
+    pyf[r] = static_cast<float>(py) + Ru::pix_off();
+    T[r] = (real && px < a.W && py < a.H) ? 1.0f : 0.0f;  // a pixel outside the image has stopped
+    Cr[r] = Cg[r] = Cb[r] = 0.0f;
+    last[r] = 0;
+  }
+  const uint32_t bfirst = (real && a.bucket_offsets) ? a.bucket_offsets[tt] : 0u;
+  if (real && sub == 0) {
+    if (a.b2t_out) {
+      const uint32_t bl = a.bucket_offsets[tt + 1];
+      for (uint32_t b = bfirst + lane; b < bl; b += kWave) a.b2t_out[b] = static_cast<uint32_t>(tt);
+    }
+    if (a.clear4) {
+      const int64_t per = (a.clear4_n + a.n_tiles - 1) / a.n_tiles;
+      const int64_t lo = per * tt, hi = min(lo + per, a.clear4_n);
+      for (int64_t q = lo + lane; q < hi; q += kWave) a.clear4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+  float* ck = a.ckpt ? a.ckpt + (static_cast<int64_t>(bfirst) * kTilePixels + kWave * sub * P + lane) * 4 : nullptr;
+
+  bool stopped = false;
+  for (int b0 = 0; b0 < len && !stopped; b0 += kWave) {
+    wave_sync();  // every lane is done with the previous batch
+    const int j = b0 + lane;
+    uint32_t sm = 0;
+    if (j < len) {
+      const float* rp = a.rec + static_cast<int64_t>(a.point_list[r0 + j]) * kRecFloats;
+      sw[lane] = Ru::stage(rp);
+      sm = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile) >> (sub * P);
+    }
+    // staged entries reaching pixel r of every lane, as 64-bit masks
+    uint64_t wm[P];
+#pragma unroll
+    for (int r = 0; r < P; ++r) wm[r] = __ballot(((sm >> r) & 1u) ? 1 : 0);
+    wave_sync();
+    const int nb = min(kWave, len - b0);
+    for (int c0 = 0; c0 < nb; c0 += kBucket) {
+      if (ck) {
+        float* c = ck + static_cast<int64_t>((b0 + c0) / kBucket) * kTilePixels * 4;
+#pragma unroll
+        for (int r = 0; r < P; ++r)
+          reinterpret_cast<float4*>(c)[kWave * r] = make_float4(Cr[r], Cg[r], Cb[r], T[r]);
+      }
+      bool live = false;
+#pragma unroll
+      for (int r = 0; r < P; ++r) live = live || T[r] >= Ru::t_stop();
+      if (__ballot(live ? 1 : 0) == 0ull) {  // every pixel of the wavefront has stopped
+        stopped = true;
+        break;
+      }
+      uint32_t cm[P], cany = 0;
+#pragma unroll
+      for (int r = 0; r < P; ++r) {
+        cm[r] = static_cast<uint32_t>(wm[r] >> c0);
+        if (nb - c0 < kBucket) cm[r] &= (1u << (nb - c0)) - 1u;
+        cm[r] = __builtin_amdgcn_readfirstlane(cm[r]);
+        cany |= cm[r];
+      }
+      const Staged<float>* bp = sw + (c0 + opaque_zero_vgpr());
+      int lastk[P];
+#pragma unroll
+      for (int r = 0; r < P; ++r) lastk[r] = -1;
+#pragma unroll
+      for (int k = 0; k < kBucket; ++k) {
+        if (((cany >> k) & 1u) == 0u) continue;  // wave-uniform
+        const Staged<float> sp = bp[k];
+        const Ru::Col cl = Ru::col(sp, pxf);
+#pragma unroll
+        for (int r = 0; r < P; ++r) {
+          if (P > 1 && ((cm[r] >> k) & 1u) == 0u) continue;  // wave-uniform strip test
+          const float dy = sp.my - pyf[r];
+          const float alpha = sp.o * Ru::falloff(Ru::power(sp, cl, dy));
+          const bool take = alpha >= Ru::alpha_min() && T[r] >= Ru::t_stop();
+          composite<kRules3D, float>(Cr[r], Cg[r], Cb[r], T[r], sp, take ? alpha : 0.0f);
+          lastk[r] = take ? k : lastk[r];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < P; ++r) last[r] = lastk[r] >= 0 ? b0 + c0 + lastk[r] + 1 : last[r];
+    }
+  }
+
+  int lmax = 0;
+  const int64_t HW = static_cast<int64_t>(a.H) * a.W;
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int py = ty * kTile + kStripRows * (sub * P + r) + (lane >> 4);
+    if (real && px < a.W && py < a.H) {
+      const int64_t pix = static_cast<int64_t>(py) * a.W + px;
+      a.image[pix] = fmaf(T[r], a.bg0, Cr[r]);
+      a.image[HW + pix] = fmaf(T[r], a.bg1, Cg[r]);
+      a.image[2 * HW + pix] = fmaf(T[r], a.bg2, Cb[r]);
+      a.final_T[pix] = T[r];
+      if (a.n_contrib) a.n_contrib[pix] = last[r];
+      lmax = max(lmax, last[r]);
+    }
+  }
+  lmax = wave_max(lmax);
+  if (kWT > 1) {
+    __syncthreads();  // s_max cleared
+    if (lane == 0 && lmax > 0) atomicMax(&s_max[wave / kWT], static_cast<uint32_t>(lmax));
+    __syncthreads();
+    lmax = static_cast<int>(s_max[wave / kWT]);
+  }
+  if (!real || sub != 0) return;
+  const uint32_t tmax = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lmax));
+  if (lane == 0 && a.tile_max) a.tile_max[tt] = tmax;
+  if (a.bucket_list) {
+    // append the buckets the backward reads: those starting before the tile's last blended entry
+    const uint32_t n_act = (tmax + kBucket - 1) / kBucket;
+    uint32_t base = 0;
+    if (lane == 0 && n_act) base = atomicAdd(a.bucket_list, n_act);
+    base = __shfl(base, 0, 64);
+    for (uint32_t k = lane; k < n_act; k += kWave) a.bucket_list[kListHeader + base + k] = bfirst + k;
+  }
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -784,6 +933,18 @@ namespace {
 
 template <int R, typename S>
 void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
+  if constexpr (R == kRules3D && std::is_same<S, float>::value) {
+    if (!a.counters) {
+      // one pixel per lane (a wavefront per strip) measured fastest: 114 us at 1M SH3 against
+      // 118 with two and 165 with four (a wavefront per tile: too few wavefronts, and the
+      // heaviest tiles run alone), and 120 for the shared-staging blend_fwd_kernel
+      constexpr int P = 1;
+      constexpr int kTPB = 4 / (kStrips / P);
+      hipLaunchKernelGGL(blend_fwd_strip_kernel<P>, dim3(static_cast<unsigned>((a.n_tiles + kTPB - 1) / kTPB)),
+                         dim3(4 * kWave), 0, st, a);
+      return;
+    }
+  }
   if (a.counters)
     hipLaunchKernelGGL((blend_fwd_kernel<R, S, true>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
   else
