@@ -464,7 +464,7 @@ static void sort_pass_r(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, ui
 
 static int sort_rounds(int64_t m) {
   if (m >= int64_t(1024) * 8192) return 16;
-  if (m >= int64_t(1024) * 2048) return 8;
+  if (m >= int64_t(1024) * 512) return 8;
   return 4;
 }
 
