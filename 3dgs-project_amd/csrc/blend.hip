@@ -128,6 +128,9 @@ __device__ __forceinline__ void atomic_add_grad(double* p, double v) { unsafeAto
 // Bucket list written by the 3D forward: [0] buckets the backward reads, [1..3] zero,
 // [kListHeader + i] bucket indices (any order).
 
+// Forward blend with a workgroup per tile and a pixel per thread, the tile's list staged 256
+// entries at a time for the 4 wavefronts together: the 2D rule sets, float64, the counting
+// variant and the pruning scores. (The plain 3D float forward is blend_fwd_strip_kernel.)
 // kScore: instead of the image, accumulate every splat's blending weights alpha T over the
 // tile's pixels into a.scores (a wavefront sum per splat into LDS, one global atomic per
 // staged splat and tile); the blend itself is the forward's, decision for decision.
@@ -251,23 +254,10 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
         if constexpr (!Ru::kStopBefore && !kStopByT) done = done || T < Ru::t_stop();
         return take;
       };
-      if constexpr (R == kRules3D && !kScore) {
-        // unrolled over the bucket's 32 slots: each staged splat at an immediate LDS offset
-        // from the bucket's base address (one VGPR), one scalar bit test per slot; the slot of
-        // the last blended splat is kept as a constant and turned into a list position once
-        cm = __builtin_amdgcn_readfirstlane(cm);
-        const Staged<S>* bp = s_sp + (c0 + opaque_zero_vgpr());
-        int lastk = -1;
-#pragma unroll
-        for (int k = 0; k < kBucket; ++k)
-          if ((cm >> k) & 1u) lastk = body(bp[k], c0 + k) ? k : lastk;
-        last = lastk >= 0 ? b0 + c0 + lastk + 1 : last;
-      } else {
-        while (cm != 0u) {
-          const int jj = c0 + __builtin_ctz(cm);
-          cm &= cm - 1u;
-          last = body(s_sp[jj], jj) ? b0 + jj + 1 : last;
-        }
+      while (cm != 0u) {
+        const int jj = c0 + __builtin_ctz(cm);
+        cm &= cm - 1u;
+        last = body(s_sp[jj], jj) ? b0 + jj + 1 : last;
       }
     }
     if constexpr (kScore) {
@@ -934,21 +924,19 @@ namespace {
 template <int R, typename S>
 void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
   if constexpr (R == kRules3D && std::is_same<S, float>::value) {
-    if (!a.counters) {
-      // one pixel per lane (a wavefront per strip) measured fastest: 114 us at 1M SH3 against
-      // 118 with two and 165 with four (a wavefront per tile: too few wavefronts, and the
-      // heaviest tiles run alone), and 120 for the shared-staging blend_fwd_kernel
-      constexpr int P = 1;
-      constexpr int kTPB = 4 / (kStrips / P);
-      hipLaunchKernelGGL(blend_fwd_strip_kernel<P>, dim3(static_cast<unsigned>((a.n_tiles + kTPB - 1) / kTPB)),
-                         dim3(4 * kWave), 0, st, a);
-      return;
-    }
-  }
-  if (a.counters)
+    // (the 3D forward takes no counters) one pixel per lane, a wavefront per strip, measured
+    // fastest: 114 us at 1M SH3 against 118 with two and 165 with four (a wavefront per tile:
+    // too few wavefronts, and the heaviest tiles run alone), and 120 for the shared-staging
+    // blend_fwd_kernel
+    constexpr int P = 1;
+    constexpr int kTPB = 4 / (kStrips / P);
+    hipLaunchKernelGGL(blend_fwd_strip_kernel<P>, dim3(static_cast<unsigned>((a.n_tiles + kTPB - 1) / kTPB)),
+                       dim3(4 * kWave), 0, st, a);
+  } else if (a.counters) {
     hipLaunchKernelGGL((blend_fwd_kernel<R, S, true>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
-  else
+  } else {
     hipLaunchKernelGGL((blend_fwd_kernel<R, S, false>), dim3(a.n_tiles), dim3(kTilePixels), 0, st, a);
+  }
 }
 
 // Workgroups of the striding list-driven backward: every CU holds its share several times
