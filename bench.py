@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 VALU_PEAK_INSTR = 157.3e12 / 2 / 64
 METRIC = "fwd+bwd ms/iter @1M Gaussians SH3 1297x840; per-stage HBM GB/s vs roofline"
 # stages that are one kernel each (the others group several kernels)
-SINGLE_KERNEL = {"preprocess": "preprocess_fwd_kernel", "blend_fwd": "blend_fwd_kernel",
+SINGLE_KERNEL = {"preprocess": "preprocess_fwd_kernel", "blend_fwd": "blend_fwd_strip_kernel",
                  "blend_bwd": "blend_bwd_bucket_kernel", "preprocess_bwd": "preprocess_bwd_kernel"}
 
 
