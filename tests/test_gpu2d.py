@@ -149,6 +149,29 @@ def test_gs2d_bench_scene_against_oracle():
         assert rel(gg.reshape(-1, len(cols)), gr[:, list(cols)]) < 1e-4
 
 
+def test_gs2d_sparse_wide_canvas_ranges():
+    """A 2048x1280 canvas (10240 tiles: more than one 8192-tile chunk of the bucket-offset scan)
+    with two clusters of small Gaussians, so most tiles (the first and last ones included) hold
+    no instance: the ranges the tile sort's last pass takes by atomic min / max, the empty
+    tiles' positions, the bucket offsets and the lists equal the oracle's bit for bit."""
+    W, H = 2048, 1280
+    gen = torch.Generator().manual_seed(7)
+    n = 3000
+    centre = torch.tensor([[700.0, 300.0], [1500.0, 1000.0]])
+    means = centre[torch.randint(0, 2, (n,), generator=gen)] + 120.0 * torch.randn(n, 2, generator=gen)
+    radii = torch.randint(0, 40, (n,), generator=gen, dtype=torch.int32)
+    depth = torch.rand(n, generator=gen)
+    bins = gs2d.bin_gaussians(means.cuda(), radii.cuda(), depth.cuda(), H, W)
+    rects, _ = O2.rects_toy(means.numpy(), radii.numpy(), W, H)
+    order, pl, ranges, boff = O2.bin_rects(rects, depth.numpy(), W, H)
+    assert bins.tiles_x * bins.tiles_y == 10240
+    rg = bins.ranges.cpu().numpy()
+    assert (rg[:, 1] == rg[:, 0]).sum() > 5000 and rg[0, 0] == rg[0, 1] and rg[-1, 0] == rg[-1, 1]
+    assert np.array_equal(rg.astype(np.int64), ranges.astype(np.int64))
+    assert np.array_equal(bins.point_list.cpu().numpy(), pl)
+    assert np.array_equal(bins.offsets_ext().cpu().numpy().astype(np.int64), boff.astype(np.int64))
+
+
 def test_gs2d_empty_scene():
     means = torch.rand(50, 2, dtype=torch.float32) * 40
     radii = torch.zeros(50, dtype=torch.int32)
