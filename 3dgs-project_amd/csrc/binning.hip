@@ -780,7 +780,8 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
 // Per-tile [start, end) of the sorted instances from the key changes: the instance that
 // starts a tile writes its start (and gives the empty tiles before it the empty range at that
 // position), the one that ends a tile writes its end (and closes the empty tiles after the
-// last tile at m). Each thread takes kBoundsPer consecutive keys (16-byte loads).
+// last tile at m). Each thread takes kBoundsPer consecutive keys (16-byte loads). Used when
+// the tile sort has no pass (a single tile); otherwise its last pass takes the ranges.
 constexpr int kBoundsPer = 16;
 
 __global__ __launch_bounds__(256) void tile_bounds_kernel(const uint32_t* __restrict__ tkeys, int64_t m,
@@ -805,7 +806,6 @@ __global__ __launch_bounds__(256) void tile_bounds_kernel(const uint32_t* __rest
   }
   k[0] = p0 > 0 ? tkeys[p0 - 1] : 0u;
   k[kBoundsPer + 1] = p0 + kBoundsPer < m ? tkeys[p0 + kBoundsPer] : 0u;
-#pragma unroll
   for (int e = 0; e < kBoundsPer; ++e) {
     if (e >= cnt) break;
     const int64_t p = p0 + e;

@@ -172,6 +172,25 @@ def test_gs2d_sparse_wide_canvas_ranges():
     assert np.array_equal(bins.offsets_ext().cpu().numpy().astype(np.int64), boff.astype(np.int64))
 
 
+@pytest.mark.parametrize("size", [(16, 16), (12, 9)])
+def test_gs2d_single_tile_canvas(size):
+    """A canvas of one tile: the tile sort has no pass, so the ranges come from the key-change
+    kernel; lists and ranges equal the oracle's."""
+    W, H = size
+    gen = torch.Generator().manual_seed(3)
+    n = 40
+    means = torch.rand(n, 2, generator=gen) * torch.tensor([W, H], dtype=torch.float32)
+    radii = torch.randint(0, 6, (n,), generator=gen, dtype=torch.int32)
+    depth = torch.rand(n, generator=gen)
+    bins = gs2d.bin_gaussians(means.cuda(), radii.cuda(), depth.cuda(), H, W)
+    rects, _ = O2.rects_toy(means.numpy(), radii.numpy(), W, H)
+    order, pl, ranges, boff = O2.bin_rects(rects, depth.numpy(), W, H)
+    assert len(ranges) == 1 and len(pl) > 0
+    assert np.array_equal(bins.ranges.cpu().numpy().astype(np.int64), ranges.astype(np.int64))
+    assert np.array_equal(bins.point_list.cpu().numpy(), pl)
+    assert np.array_equal(bins.offsets_ext().cpu().numpy().astype(np.int64), boff.astype(np.int64))
+
+
 def test_gs2d_empty_scene():
     means = torch.rand(50, 2, dtype=torch.float32) * 40
     radii = torch.zeros(50, dtype=torch.int32)
