@@ -313,8 +313,9 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
 // 16, column lane % 16, the pixel layout of the bucketed backward): the column terms of the power
 // are computed once per splat for its P pixels, the strip test of pixel r is one scalar bit test,
 // and each wavefront stages the tile's list 64 entries at a time in its own LDS, so it waits for
-// no other wavefront until the tile's end. The per-pixel operations and decisions are
-// blend_fwd_kernel's (same image, T, n_contrib and checkpoints).
+// no other wavefront until the tile's end. Per pixel it takes the decisions of Rule<kRules3D>
+// with the operations of the pruning-score pass of blend_fwd_kernel and of the oracle's forward
+// (alpha >= 1/255 while T >= 1e-4; composite with alpha 0 otherwise). P = 1 is launched.
 template <int P>
 __global__ __launch_bounds__(4 * kWave) void blend_fwd_strip_kernel(BlendArgs<float> a) {
   using Ru = Rule<kRules3D, float>;
