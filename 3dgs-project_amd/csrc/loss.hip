@@ -13,6 +13,8 @@
 // Backward: the same separable filter on the three partial maps (the Gaussian is symmetric, so
 // the transpose of the zero-padded filter is itself), then
 //   dL/dx = (1 - lambda) sign(x - y) / N - lambda / N (G*a + 2 x G*b + y G*c).
+#include <mutex>
+
 #include "gs_host.h"
 
 namespace gs {
@@ -213,24 +215,93 @@ extern "C" size_t gs_l1_ssim_workspace_size(int channels, int height, int width)
   return static_cast<size_t>(ssim_blocks(channels, height, width)) * 2 * sizeof(float);
 }
 
-extern "C" int gs_l1_ssim_fwd(const float* image, const float* target, int channels, int height, int width,
-                              float lambda_dssim, float* dmap, float* loss, void* workspace, size_t workspace_bytes,
-                              void* stream) {
-  clear_error();
-  GS_REQUIRE(channels > 0 && channels <= 65535 && height > 0 && width > 0, GS_ERR_ARG, "invalid image size");
-  GS_REQUIRE(image && target && loss, GS_ERR_ARG, "null pointer argument");
-  GS_REQUIRE(lambda_dssim >= 0.0f && lambda_dssim <= 1.0f, GS_ERR_ARG, "lambda_dssim must be in [0, 1]");
-  const size_t need = gs_l1_ssim_workspace_size(channels, height, width);
-  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
-  hipStream_t st = as_stream(stream);
+// Both forward entry points: the per-tile partial sums go to `partials` (2 floats per tile and
+// channel, every one written by ssim_fwd_kernel before ssim_reduce_kernel reads it, so nothing
+// has to start at zero).
+static int l1_ssim_fwd_launch(const float* image, const float* target, int channels, int height, int width,
+                              float lambda_dssim, float* dmap, float* loss, float* partials, hipStream_t st) {
   const dim3 grid((width + kSsTile - 1) / kSsTile, (height + kSsTile - 1) / kSsTile, channels);
-  float* partials = static_cast<float*>(workspace);
   hipLaunchKernelGGL(ssim_fwd_kernel, grid, dim3(256), 0, st, image, target, height, width, ssim_weights(), dmap,
                      partials);
   const double n = static_cast<double>(channels) * height * width;
   hipLaunchKernelGGL(ssim_reduce_kernel, dim3(1), dim3(256), 0, st, partials, ssim_blocks(channels, height, width),
                      n, lambda_dssim, loss);
   return check_launch("l1_ssim_fwd");
+}
+
+static int l1_ssim_check_args(const float* image, const float* target, int channels, int height, int width,
+                              float lambda_dssim, const float* loss) {
+  GS_REQUIRE(channels > 0 && channels <= 65535 && height > 0 && width > 0, GS_ERR_ARG, "invalid image size");
+  GS_REQUIRE(image && target && loss, GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(lambda_dssim >= 0.0f && lambda_dssim <= 1.0f, GS_ERR_ARG, "lambda_dssim must be in [0, 1]");
+  return GS_OK;
+}
+
+extern "C" int gs_l1_ssim_fwd(const float* image, const float* target, int channels, int height, int width,
+                              float lambda_dssim, float* dmap, float* loss, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  clear_error();
+  const int rc = l1_ssim_check_args(image, target, channels, height, width, lambda_dssim, loss);
+  if (rc != GS_OK) return rc;
+  const size_t need = gs_l1_ssim_workspace_size(channels, height, width);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  return l1_ssim_fwd_launch(image, target, channels, height, width, lambda_dssim, dmap, loss,
+                            static_cast<float*>(workspace), as_stream(stream));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free forward: the partial sums live in a static device array of the library (one
+// copy per GPU, held until the process ends). Host code never passes `scratch` itself (in host
+// code that name is a stand-in, not a device address): each device's address is looked up once
+// with hipGetSymbolAddress while that device is current, and kept per device.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[2 * GS_L1_SSIM_NOALLOC_MAX_TILES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (NULL and an error message on failure).
+static float* scratch_on_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("l1_ssim_fwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("l1_ssim_fwd_noalloc: device %d beyond the %d the library keeps scratch addresses for", dev,
+              kMaxScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    float* p = nullptr;
+    e = hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("l1_ssim_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" int gs_l1_ssim_fwd_noalloc(const float* image, const float* target, int channels, int height, int width,
+                                      float lambda_dssim, float* dmap, float* loss, void* stream) {
+  clear_error();
+  const int rc = l1_ssim_check_args(image, target, channels, height, width, lambda_dssim, loss);
+  if (rc != GS_OK) return rc;
+  const int64_t tiles = ssim_blocks(channels, height, width);
+  GS_REQUIRE(tiles <= GS_L1_SSIM_NOALLOC_MAX_TILES, GS_ERR_ARG,
+             "l1_ssim_fwd_noalloc: %d x %d x %d images have %lld tiles x channels, more than the %d its static "
+             "buffer holds (use gs_l1_ssim_fwd with a workspace)",
+             channels, height, width, static_cast<long long>(tiles), GS_L1_SSIM_NOALLOC_MAX_TILES);
+  float* partials = scratch_on_current_device();
+  if (partials == nullptr) return GS_ERR_LAUNCH;
+  return l1_ssim_fwd_launch(image, target, channels, height, width, lambda_dssim, dmap, loss, partials,
+                            as_stream(stream));
 }
 
 extern "C" int gs_l1_ssim_bwd(const float* image, const float* target, const float* dmap, int channels, int height,

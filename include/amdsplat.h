@@ -356,6 +356,23 @@ int gs_l1_ssim_fwd(const float* image, const float* target, int channels, int he
 int gs_l1_ssim_bwd(const float* image, const float* target, const float* dmap, int channels, int height,
                    int width, float lambda_dssim, const float* grad_loss, float* grad_image, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Allocation-free gs_l1_ssim_fwd. It has no counterpart in the reference. It is for callers
+ * that cannot allocate device memory: code under HIP graph capture, tight serving loops, and
+ * harnesses that forbid hipMalloc.
+ * Same arguments and results as gs_l1_ssim_fwd (the same kernels, so the same bits), without
+ * the workspace: the per-tile partial sums go to a static device buffer of the library of
+ * 2 * GS_L1_SSIM_NOALLOC_MAX_TILES floats (1 MiB), one per GPU, held until the process ends.
+ * channels * ceil(height/16) * ceil(width/16) must not exceed GS_L1_SSIM_NOALLOC_MAX_TILES
+ * (e.g. 3 x 2048 x 2048 fits); larger images return GS_ERR_ARG. The call allocates nothing.
+ * Every call on one GPU shares that GPU's buffer and leaves its partial sums there (nothing
+ * in it has to start at zero): calls that can overlap on one GPU (on streams not ordered
+ * with each other) race, so order them.
+ * ------------------------------------------------------------------------------------- */
+#define GS_L1_SSIM_NOALLOC_MAX_TILES 131072
+int gs_l1_ssim_fwd_noalloc(const float* image, const float* target, int channels, int height, int width,
+                           float lambda_dssim, float* dmap, float* loss, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
