@@ -223,6 +223,168 @@ def test_preprocess_off_axis_mean_and_rotation_invariance():
     np.testing.assert_allclose(r1[0, 2:5], r2[0, 2:5], rtol=1e-5, atol=1e-6)
 
 
+# ---------------------------------------------------------------------------------------
+# Projection pinned independently of the oracle's formulas: rotations from scipy (a library
+# routine), the covariance from a closed form or a float64 central-difference Jacobian of the
+# pinhole map, and the SH view direction from the camera centre of the inverted view matrix.
+# A transposed rotation, one wrong sign in a Jacobian cross term or a reversed view direction
+# fails these.
+# ---------------------------------------------------------------------------------------
+def wxyz_quat(rot) -> np.ndarray:
+    """(w, x, y, z) quaternion of a scipy Rotation (scipy's own order is (x, y, z, w))."""
+    x, y, z, w = rot.as_quat()
+    return np.array([w, x, y, z])
+
+
+def conic_of(cov) -> np.ndarray:
+    """(A, B, C) of the inverse of the symmetric 2x2 [[a, b], [b, c]]: (c, -b, a) / det."""
+    a, b, c = cov[0, 0], cov[0, 1], cov[1, 1]
+    det = a * c - b * b
+    return np.array([c / det, -b / det, a / det])
+
+
+def viewmat_np(rot, t) -> np.ndarray:
+    vm = np.eye(4)
+    vm[:3, :3] = rot.as_matrix()
+    vm[:3, 3] = t
+    return vm
+
+
+def pinhole_jacobian_fd(vm, p_world, fx, fy, cx, cy, h=1e-6):
+    """float64 central differences of p -> (fx X/Z + cx, fy Y/Z + cy), (X, Y, Z) = R p + t."""
+    def proj(p):
+        X, Y, Z = vm[:3, :3] @ p + vm[:3, 3]
+        return np.array([fx * X / Z + cx, fy * Y / Z + cy])
+
+    J = np.zeros((2, 3))
+    for k in range(3):
+        e = np.zeros(3)
+        e[k] = h
+        J[:, k] = (proj(p_world + e) - proj(p_world - e)) / (2 * h)
+    return J
+
+
+def assert_conic_close(got, cov_expect, rtol=2e-5):
+    want = conic_of(cov_expect)
+    scale = np.abs(want).max()
+    assert np.abs(np.asarray(got, np.float64) - want).max() <= rtol * scale, (got, want)
+
+
+@pytest.mark.parametrize("theta", [0.4, -0.4, 1.1, -1.1])
+def test_preprocess_anisotropic_on_axis_closed_form(theta):
+    """A Gaussian on the optical axis with scales (s1, s2, s3), turned by theta about the axis:
+    cov2d = (f/z)^2 R(theta) diag(s1^2, s2^2) R(theta)^T + 0.3 I, R(theta) the 2D rotation
+    (image x right, y down, as the camera's x and y). The off-diagonal term
+    (f/z)^2 (s1^2 - s2^2) sin(theta) cos(theta) changes sign with theta, so a transposed
+    rotation fails."""
+    from scipy.spatial.transform import Rotation
+
+    f, z = 500.0, 4.0
+    s = np.array([0.06, 0.02, 0.04])
+    cam = scenes.Camera(torch.eye(4), f, f, 64.3, 47.8, 128, 96, 0.2, 100.0)
+    q = wxyz_quat(Rotation.from_euler("z", theta))
+    g = one_gaussian((0.0, 0.0, z), 0.0, tuple(q))
+    g[1][0] = np.log(s).astype(np.float32)
+    rec, touched = O.preprocess_fwd(*g, cam, 0)
+    assert touched[0] > 0
+    c, sn = math.cos(theta), math.sin(theta)
+    s1, s2 = float(np.float32(s[0])) ** 2, float(np.float32(s[1])) ** 2
+    k = (f / z) ** 2
+    cov = np.array([[k * (s1 * c * c + s2 * sn * sn) + 0.3, k * (s1 - s2) * sn * c],
+                    [k * (s1 - s2) * sn * c, k * (s1 * sn * sn + s2 * c * c) + 0.3]])
+    assert abs(cov[0, 1]) > 0.5  # the cross term is far from zero: its sign is tested
+    assert_conic_close(rec[0, 2:5], cov)
+    assert r_sign(rec[0, 3]) == -r_sign(cov[0, 1])  # B = -b / det
+
+
+def r_sign(v) -> int:
+    return 1 if v > 0 else (-1 if v < 0 else 0)
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_preprocess_covariance_against_finite_difference_jacobian(case):
+    """General camera pose and Gaussian orientation, off the optical axis: cov2d - 0.3 I equals
+    J Sigma J^T with J the float64 central-difference Jacobian of the pinhole map at the mean
+    (through the world-to-camera transform) and Sigma = R diag(s^2) R^T, R from scipy. The last
+    case sits outside the 1.3x frustum (to the right and above the image): the covariance is
+    then the one at the clamped direction, i.e. J is the Jacobian at the point of the same
+    depth on the clamp boundary."""
+    from scipy.spatial.transform import Rotation
+
+    rng = np.random.default_rng(100 + case)
+    W, H, fx, fy, cx, cy = 160, 120, 150.0, 170.0, 83.0, 55.0
+    rview = Rotation.from_rotvec(rng.normal(size=3) * 0.4)
+    t = rng.normal(size=3) * 0.5
+    vm = viewmat_np(rview, t)
+    cam = scenes.Camera(torch.tensor(vm, dtype=torch.float32), fx, fy, cx, cy, W, H, 0.2, 100.0)
+    vm32 = cam.viewmat.double().numpy()  # the float32 matrix the oracle sees
+    z = 3.0 + case * 0.5
+    if case < 5:
+        u, v = rng.uniform(0.15, 0.85) * W, rng.uniform(0.15, 0.85) * H  # target pixel
+        s = np.exp(rng.uniform(np.log(0.01), np.log(0.08), size=3))
+    else:
+        u, v = W + 0.5 * W * 1.3, -0.6 * H  # beyond both clamp limits; a wide Gaussian reaches the image
+        s = np.array([1.2, 0.9, 1.0])
+    p_cam = np.array([(u - cx) / fx * z, (v - cy) / fy * z, z])
+    Rv, tv = vm32[:3, :3], vm32[:3, 3]
+    p_world = np.linalg.solve(Rv, p_cam - tv).astype(np.float32).astype(np.float64)
+    rq = Rotation.from_quat(rng.normal(size=4))
+    q = wxyz_quat(rq) * rng.uniform(0.5, 2.0)  # any norm
+    g = one_gaussian(tuple(p_world), 0.0, tuple(q))
+    g[1][0] = np.log(s).astype(np.float32)
+    rec, touched = O.preprocess_fwd(*g, cam, 0)
+    assert touched[0] > 0, "the test Gaussian must be visible"
+    Rg = rq.as_matrix()
+    s32 = g[1][0].astype(np.float64)
+    Sigma = Rg @ np.diag(np.exp(s32) ** 2) @ Rg.T
+    if case < 5:
+        J = pinhole_jacobian_fd(vm32, p_world, fx, fy, cx, cy)
+    else:
+        X, Y, Z = Rv @ p_world + tv
+        txc = min(max(X / Z, -1.3 * cx / fx), 1.3 * (W - cx) / fx)
+        tyc = min(max(Y / Z, -1.3 * cy / fy), 1.3 * (H - cy) / fy)
+        assert txc != X / Z and tyc != Y / Z  # both clamps active
+        p_clamp = np.linalg.solve(Rv, np.array([txc * Z, tyc * Z, Z]) - tv)
+        J = pinhole_jacobian_fd(vm32, p_clamp, fx, fy, cx, cy)
+    cov = J @ Sigma @ J.T + 0.3 * np.eye(2)
+    assert abs(cov[0, 1]) > 1e-3 * np.sqrt(cov[0, 0] * cov[1, 1])  # a real cross term
+    assert_conic_close(rec[0, 2:5], cov, rtol=5e-5)
+    # the mean projects to the pixel it was placed at (unclamped), the depth is Z
+    np.testing.assert_allclose(rec[0, 0:2], [u, v], rtol=1e-5, atol=2e-3)
+    np.testing.assert_allclose(rec[0, 6], z, rtol=1e-6)
+
+
+@pytest.mark.parametrize("band,axis", [(1, 1), (2, 2), (3, 0)], ids=["y", "z", "x"])
+def test_sh_degree1_colour_follows_the_view_direction(band, axis):
+    """Degree 1 with one band coefficient c only: colour = 0.5 + c b(d), with the 3DGS basis
+    (-C1 y, C1 z, -C1 x) at d = (mean - camera centre) / |mean - camera centre|, the camera
+    centre taken from the inverted view matrix. A reversed direction flips the sign of the
+    band's contribution."""
+    from scipy.spatial.transform import Rotation
+
+    W, H, f = 128, 96, 120.0
+    vm = viewmat_np(Rotation.from_rotvec([0.3, -0.5, 0.2]), [0.4, -0.3, 2.5])
+    cam = scenes.Camera(torch.tensor(vm, dtype=torch.float32), f, f, 64.0, 48.0, W, H, 0.2, 100.0)
+    vm32 = cam.viewmat.double().numpy()
+    campos = np.linalg.inv(vm32)[:3, 3]
+    p_cam = np.array([0.5, 0.7, 2.5])  # in view, off axis: every direction component well away from 0
+    p_world = np.linalg.solve(vm32[:3, :3], p_cam - vm32[:3, 3]).astype(np.float32).astype(np.float64)
+    g = list(one_gaussian(tuple(p_world), math.log(0.05), sh0=(0.0, 0.0, 0.0)))
+    cvals = np.array([0.3, -0.4, 0.5])
+    g[4][0, band] = cvals
+    rec, touched = O.preprocess_fwd(*g, cam, 1)
+    assert touched[0] > 0
+    d = p_world - campos
+    d /= np.linalg.norm(d)
+    assert abs(d[axis]) > 0.1
+    c1 = D.sh_norm_constant(1, 0)
+    sign = -1.0 if band in (1, 3) else 1.0
+    want = 0.5 + sign * c1 * d[axis] * cvals
+    np.testing.assert_allclose(rec[0, 8:11], want, rtol=0, atol=2e-6)
+    # the reversed direction would give a colour that differs by far more than the tolerance
+    assert np.abs((0.5 - sign * c1 * d[axis] * cvals) - want).min() > 1e-2
+
+
 def test_preprocess_culls_behind_and_far():
     cam = scenes.Camera(torch.eye(4), 400.0, 400.0, 50.0, 40.0, 100, 80, 0.2, 10.0)
     for z in (-1.0, 0.1, 12.0):
