@@ -401,8 +401,27 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 // ---------------------------------------------------------------------------------------
 // Backward
 // ---------------------------------------------------------------------------------------
+// Adds v = dL/dR[idx] (R row-major, the rotation of the unit quaternion (w, x, y, z)) to half the
+// quaternion gradient: R[0] = 1 - 2(y^2 + z^2), R[1] = 2(xy - wz), R[2] = 2(xz + wy),
+// R[3] = 2(xy + wz), R[4] = 1 - 2(x^2 + z^2), R[5] = 2(yz - wx), R[6] = 2(xz - wy),
+// R[7] = 2(yz + wx), R[8] = 1 - 2(x^2 + y^2). idx is a compile-time constant after unrolling.
+__device__ __forceinline__ void quat_grad_add(int idx, double v, double w, double x, double y, double z, double& gw,
+                                              double& gx, double& gy, double& gz) {
+  switch (idx) {
+    case 0: gy -= 2.0 * y * v; gz -= 2.0 * z * v; break;
+    case 1: gw -= z * v; gx += y * v; gy += x * v; gz -= w * v; break;
+    case 2: gw += y * v; gx += z * v; gy += w * v; gz += x * v; break;
+    case 3: gw += z * v; gx += y * v; gy += x * v; gz += w * v; break;
+    case 4: gx -= 2.0 * x * v; gz -= 2.0 * z * v; break;
+    case 5: gw -= x * v; gx -= w * v; gy += z * v; gz += y * v; break;
+    case 6: gw -= y * v; gx += z * v; gy -= w * v; gz += x * v; break;
+    case 7: gw += x * v; gx += w * v; gy += z * v; gz += y * v; break;
+    default: gx -= 2.0 * x * v; gy -= 2.0 * y * v; break;
+  }
+}
+
 template <int K>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void preprocess_bwd_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void preprocess_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
     ShPtr sh, int64_t n, int active, CamK cam, const uint32_t* __restrict__ tiles_touched,
@@ -500,110 +519,116 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5))) void p
     gm[1] = (gdy - dy * dd) * il;
     gm[2] = (gdz - dz * dd) * il;
 
-    // ---- geometry ----
+    // ---- geometry: the forward's float32 intermediates (the same bits as the forward), the
+    // chain rule in float64. The conic -> covariance step divides by det^2 and its terms cancel
+    // for elongated splats (det << a c); in float32 such Gaussians get gradients off by more than
+    // their own size. FP64 costs this memory-bound kernel nothing measurable. ----
     Geom g;
     compute_geom(means, log_scales, quats, opacity_logits, i, cam, g);
-    gop = g2[5] * g.o * (1.0f - g.o);
     const bool aa = cam.flags & GS_CAM_PROPER_ANTIALIASING;
-    if (aa) gop = ((g2[5] * g.rho) * g.os) * (1.0f - g.os);
+    gop = aa ? static_cast<float>(static_cast<double>(g2[5]) * g.rho * g.os * (1.0 - g.os))
+             : static_cast<float>(static_cast<double>(g2[5]) * g.o * (1.0 - g.o));
 
     // mean2d = (fx vx/vz + cx, fy vy/vz + cy)
-    float gvx = g2[0] * cam.fx * g.iz;
-    float gvy = g2[1] * cam.fy * g.iz;
-    float gvz = -(g2[0] * cam.fx * g.tx + g2[1] * cam.fy * g.ty) * g.iz;
+    const double fx = cam.fx, fy = cam.fy;
+    const double iz = 1.0 / static_cast<double>(g.vz), iz2 = iz * iz;
+    double gvx = g2[0] * fx * iz;
+    double gvy = g2[1] * fy * iz;
+    double gvz = -(g2[0] * fx * g.vx + g2[1] * fy * g.vy) * iz2;
 
     // conic (A, B, C) = (c, -b, a) / det  ->  2D covariance (a, b, c)
-    const float gA = g2[2], gB = g2[3], gC = g2[4];
-    const float a = g.a, b = g.b, c = g.c;
-    const float id2 = 1.0f / (g.det * g.det);
-    float ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
-    float gbb = (2.0f * b * c * gA - (a * c + b * b) * gB + 2.0f * a * b * gC) * id2;
-    float gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
+    const double gA = g2[2], gB = g2[3], gC = g2[4];
+    const double a = g.a, b = g.b, c = g.c;
+    const double det = a * c - b * b;
+    const double id2 = 1.0 / (det * det);
+    double ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
+    double gbb = (2.0 * b * c * gA - (a * c + b * b) * gB + 2.0 * a * b * gC) * id2;
+    double gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
     if (aa) {
       // rho^2 = (ar cr - b^2) / (a c - b^2), a = ar + 0.3, c = cr + 0.3:
       // d rho = d(rho^2) / (2 rho), d(rho^2)/da = (cr - rho^2 c) / det,
       // d(rho^2)/dc = (ar - rho^2 a) / det, d(rho^2)/db = -2 b (1 - rho^2) / det
-      const float k = (g2[5] * g.os) / (2.0f * g.rho * g.det);
-      ga += k * (g.cr - g.ratio * c);
-      gc += k * (g.ar - g.ratio * a);
-      gbb += -2.0f * k * b * (1.0f - g.ratio);
+      const double ar = g.ar, cr = g.cr;
+      const double ratio = (ar * cr - b * b) / det;
+      const double k = static_cast<double>(g2[5]) * g.os / (2.0 * sqrt(ratio) * det);
+      ga += k * (cr - ratio * c);
+      gc += k * (ar - ratio * a);
+      gbb += -2.0 * k * b * (1.0 - ratio);
     }
     // cov2d = T S T^T (+ dilation); Gc = [[ga, gbb/2], [gbb/2, gc]]
-    const float Gc00 = ga, Gc01 = 0.5f * gbb, Gc11 = gc;
+    const double Gc01 = 0.5 * gbb;
     const float* T = g.T;
-    const float* S = g.S;
-    // dL/dS = T^T Gc T (symmetric, 3x3)
-    float GT[6];  // Gc T (2x3)
+    // Gc T (2x3)
+    double GT[6];
     for (int k = 0; k < 3; ++k) {
-      GT[k] = Gc00 * T[k] + Gc01 * T[3 + k];
-      GT[3 + k] = Gc01 * T[k] + Gc11 * T[3 + k];
+      GT[k] = ga * T[k] + Gc01 * T[3 + k];
+      GT[3 + k] = Gc01 * T[k] + gc * T[3 + k];
     }
-    float dS[9];
-    for (int r0 = 0; r0 < 3; ++r0)
-      for (int c0 = 0; c0 < 3; ++c0) dS[3 * r0 + c0] = T[r0] * GT[c0] + T[3 + r0] * GT[3 + c0];
-    // dL/dT = 2 Gc T S
-    const float Sf[9] = {S[0], S[1], S[2], S[1], S[3], S[4], S[2], S[4], S[5]};
-    float dT[6];
-    for (int r0 = 0; r0 < 2; ++r0)
-      for (int c0 = 0; c0 < 3; ++c0) {
-        float acc = 0.0f;
-        for (int k = 0; k < 3; ++k) acc += GT[3 * r0 + k] * Sf[3 * k + c0];
-        dT[3 * r0 + c0] = 2.0f * acc;
-      }
+    // dL/dT = 2 Gc T S, S symmetric with rows (S0 S1 S2), (S1 S3 S4), (S2 S4 S5)
+    const double S0 = g.S[0], S1 = g.S[1], S2 = g.S[2], S3 = g.S[3], S4 = g.S[4], S5 = g.S[5];
+    double dT[6];
+    for (int r0 = 0; r0 < 2; ++r0) {
+      const double* G = GT + 3 * r0;
+      dT[3 * r0 + 0] = 2.0 * (G[0] * S0 + G[1] * S1 + G[2] * S2);
+      dT[3 * r0 + 1] = 2.0 * (G[0] * S1 + G[1] * S3 + G[2] * S4);
+      dT[3 * r0 + 2] = 2.0 * (G[0] * S2 + G[1] * S4 + G[2] * S5);
+    }
     // T = J W with J = [[j00, 0, j02], [0, j11, j12]]
-    float gj00 = 0.0f, gj02 = 0.0f, gj11 = 0.0f, gj12 = 0.0f;
+    double gj00 = 0.0, gj02 = 0.0, gj11 = 0.0, gj12 = 0.0;
     for (int k = 0; k < 3; ++k) {
       gj00 += dT[k] * cam.r[k];
       gj02 += dT[k] * cam.r[6 + k];
       gj11 += dT[3 + k] * cam.r[3 + k];
       gj12 += dT[3 + k] * cam.r[6 + k];
     }
-    const float iz = g.iz, iz2 = iz * iz;
     // j00 = fx/vz, j02 = -fx txc/vz (txc = clamp(vx/vz)), same for y
-    gvz += -cam.fx * iz2 * gj00 - cam.fy * iz2 * gj11;
-    gvz += cam.fx * g.txc * iz2 * gj02 + cam.fy * g.tyc * iz2 * gj12;
+    gvz += -fx * iz2 * gj00 - fy * iz2 * gj11;
+    gvz += fx * static_cast<double>(g.txc) * iz2 * gj02 + fy * static_cast<double>(g.tyc) * iz2 * gj12;
     if (g.tx >= cam.lim_x_lo && g.tx <= cam.lim_x_hi) {
-      gvx += -cam.fx * iz2 * gj02;
-      gvz += cam.fx * g.vx * iz2 * iz * gj02;
+      gvx += -fx * iz2 * gj02;
+      gvz += fx * static_cast<double>(g.vx) * iz2 * iz * gj02;
     }
     if (g.ty >= cam.lim_y_lo && g.ty <= cam.lim_y_hi) {
-      gvy += -cam.fy * iz2 * gj12;
-      gvz += cam.fy * g.vy * iz2 * iz * gj12;
+      gvy += -fy * iz2 * gj12;
+      gvz += fy * static_cast<double>(g.vy) * iz2 * iz * gj12;
     }
     // v = W p + t
-    gm[0] += cam.r[0] * gvx + cam.r[3] * gvy + cam.r[6] * gvz;
-    gm[1] += cam.r[1] * gvx + cam.r[4] * gvy + cam.r[7] * gvz;
-    gm[2] += cam.r[2] * gvx + cam.r[5] * gvy + cam.r[8] * gvz;
+    gm[0] = static_cast<float>(gm[0] + (cam.r[0] * gvx + cam.r[3] * gvy + cam.r[6] * gvz));
+    gm[1] = static_cast<float>(gm[1] + (cam.r[1] * gvx + cam.r[4] * gvy + cam.r[7] * gvz));
+    gm[2] = static_cast<float>(gm[2] + (cam.r[2] * gvx + cam.r[5] * gvy + cam.r[8] * gvz));
 
-    // S = M M^T, M = R diag(s): dL/dM = 2 dS M
-    float dM[9];
-    for (int r0 = 0; r0 < 3; ++r0)
-      for (int c0 = 0; c0 < 3; ++c0) {
-        float acc = 0.0f;
-        for (int k = 0; k < 3; ++k) acc += dS[3 * r0 + k] * g.M[3 * k + c0];
-        dM[3 * r0 + c0] = 2.0f * acc;
-      }
-    float dR[9];
+    // dL/dS = T^T Gc T (symmetric); S = M M^T, M = R diag(s) (the forward's float32 M):
+    // dL/dM = 2 dS M; dL/dR[r][k] = dL/dM[r][k] s[k] and dL/ds[k] = sum_r dL/dM[r][k] R[r][k].
+    // Each dL/dR[r][k] goes straight into the gradient of the normalised quaternion (w, x, y, z)
+    // of R (nothing 3x3 is kept).
+    const double w = g.qw, x = g.qx, y = g.qy, z = g.qz;
+    double gw = 0.0, gx = 0.0, gy = 0.0, gz = 0.0;
+#pragma unroll
     for (int k = 0; k < 3; ++k) {
-      float ds = 0.0f;
+      const double sk = g.s[k];
+      double ds = 0.0;
+#pragma unroll
       for (int r0 = 0; r0 < 3; ++r0) {
-        ds += dM[3 * r0 + k] * g.R[3 * r0 + k];
-        dR[3 * r0 + k] = dM[3 * r0 + k] * g.s[k];
+        double acc = 0.0;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const double dSrj = static_cast<double>(g.T[r0]) * GT[j] + static_cast<double>(g.T[3 + r0]) * GT[3 + j];
+          acc += dSrj * static_cast<double>(g.M[3 * j + k]);
+        }
+        const double dMrk = 2.0 * acc;
+        ds += dMrk * static_cast<double>(g.R[3 * r0 + k]);
+        quat_grad_add(3 * r0 + k, dMrk * sk, w, x, y, z, gw, gx, gy, gz);
       }
-      gdl[k] = ds * g.s[k];
+      gdl[k] = static_cast<float>(ds * sk);
     }
-    // rotation matrix of the normalised quaternion (w, x, y, z)
-    const float w = g.qw, x = g.qx, y = g.qy, z = g.qz;
-    const float gw = 2.0f * (-z * dR[1] + y * dR[2] + z * dR[3] - x * dR[5] - y * dR[6] + x * dR[7]);
-    const float gx = 2.0f * (y * dR[1] + z * dR[2] + y * dR[3] - 2.0f * x * dR[4] - w * dR[5] +
-                             z * dR[6] + w * dR[7] - 2.0f * x * dR[8]);
-    const float gy = 2.0f * (-2.0f * y * dR[0] + x * dR[1] + w * dR[2] + x * dR[3] + z * dR[5] -
-                             w * dR[6] + z * dR[7] - 2.0f * y * dR[8]);
-    const float gz = 2.0f * (-2.0f * z * dR[0] - w * dR[1] + x * dR[2] + w * dR[3] -
-                             2.0f * z * dR[4] + y * dR[5] + x * dR[6] + y * dR[7]);
-    const float qd = w * gw + x * gx + y * gy + z * gz;
-    gq = make_float4((gw - w * qd) * g.qinv, (gx - x * qd) * g.qinv, (gy - y * qd) * g.qinv,
-                     (gz - z * qd) * g.qinv);
+    gw *= 2.0;
+    gx *= 2.0;
+    gy *= 2.0;
+    gz *= 2.0;
+    const double qd = w * gw + x * gx + y * gy + z * gz;
+    const double qinv = g.qinv;
+    gq = make_float4(static_cast<float>((gw - w * qd) * qinv), static_cast<float>((gx - x * qd) * qinv),
+                     static_cast<float>((gy - y * qd) * qinv), static_cast<float>((gz - z * qd) * qinv));
   }
   if (valid) {
     g_means[3 * i] = gm[0];
