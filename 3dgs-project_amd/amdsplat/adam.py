@@ -3,9 +3,12 @@ cluster/patches/fastergs_lean_adam.patch:221-312).
 
 `FusedAdam(params, lr, eps, sparse=False, lowp_moment_groups=())` is a torch.optim.Adam whose
 step() runs every parameter group in one HIP launch (gs_adam_step). sparse: only primitives
-visible in the last differentiable 3D forward (tiles_touched > 0) are updated; the others keep
-parameters and moments. lowp_moment_groups: names of groups whose exp_avg / exp_avg_sq are kept
-in bfloat16 with stochastic rounding. With both off this is the dense float32 update.
+visible in the view (tiles_touched > 0) are updated; the others keep parameters and moments. The
+mask is step(visibility=aux["visibility"]) of the forward, or, when step() is not handed one,
+the one the last differentiable forward left in the class-attribute hand-off of the reference's
+patch (_Rasterize.last_visibility, cluster/patches/fastergs_lean_adam.patch:329-343).
+lowp_moment_groups: names of groups whose exp_avg / exp_avg_sq are kept in bfloat16 with
+stochastic rounding. With both off this is the dense float32 update.
 
 `adam_step` / `adam_step_sparse` mirror the extension functions `_C.adam_step` and
 `_C.adam_step_sparse` (same argument order) for callers that keep their own optimizer state.
@@ -90,15 +93,22 @@ class FusedAdam(torch.optim.Adam):
         self.sparse = sparse
         self.lowp_moment_groups = set(lowp_moment_groups)
         self.n_dense_fallbacks = 0
+        from .fastergs import _Rasterize
         from .raster3d import _Rasterize3D
 
         _Rasterize3D.track_visibility = sparse
+        _Rasterize.track_visibility = sparse
 
     @torch.no_grad()
-    def step(self) -> None:
+    def step(self, visibility: torch.Tensor | None = None) -> None:
+        """visibility: int32 [n_primitives] (> 0 = update), e.g. aux["visibility"] of the view's
+        forward; None takes the last differentiable forward's (sparse only)."""
         from .raster3d import _Rasterize3D
 
-        visibility = _Rasterize3D.last_visibility if self.sparse else None
+        if not self.sparse:
+            visibility = None
+        elif visibility is None:
+            visibility = _Rasterize3D.last_visibility
         batches: dict = {}
         for group in self.param_groups:
             assert len(group["params"]) == 1, "more than one tensor in group"

@@ -123,14 +123,17 @@ class StageTimer:
             self.marks.append((name, e))
 
     def result(self, sync: bool = True) -> dict:
-        """Per-stage milliseconds; with sync=False the caller must have synchronised."""
+        """Per-stage milliseconds (a stage is the interval that ends at its mark; the interval
+        ending at a "start" mark, e.g. between a forward and its backward, is not a stage); with
+        sync=False the caller must have synchronised."""
         if not self.enabled or len(self.marks) < 2:
             return {}
         if sync:
             torch.cuda.synchronize()
         out = {}
         for (_, a), (name, b) in zip(self.marks[:-1], self.marks[1:]):
-            out[name] = out.get(name, 0.0) + a.elapsed_time(b)
+            if name != "start":
+                out[name] = out.get(name, 0.0) + a.elapsed_time(b)
         return out
 
 
@@ -337,28 +340,36 @@ def densification_stats(grad2d: torch.Tensor, touched: torch.Tensor, width: int,
 
 
 class _Rasterize3D(torch.autograd.Function):
-    # visibility hand-off for the sparse optimizer (cluster/patches/fastergs_lean_adam.patch:333-343):
-    # with track_visibility set, each differentiable forward keeps its tiles_touched (int32 [n],
-    # > 0 = visible in that view) in last_visibility
+    # Compatibility alias of the visibility hand-off of Faster-GS's lean Adam patch
+    # (cluster/patches/fastergs_lean_adam.patch:329-343): with track_visibility set, each
+    # differentiable forward also leaves its tiles_touched (int32 [n], > 0 = visible in that view)
+    # in last_visibility, where FusedAdam(sparse=True).step() looks when it is not handed a mask.
+    # The per-call hand-off is aux["visibility"] (FusedAdam.step(visibility=...)): two forwards in
+    # flight each keep their own.
     track_visibility: bool = False
     last_visibility: "torch.Tensor | None" = None
 
     @staticmethod
-    def forward(ctx, means, log_scales, quats, opacity_logits, sh, sh_rest, cam, sh_degree, bg, dinfo=None):
+    def forward(ctx, means, log_scales, quats, opacity_logits, sh, sh_rest, cam, sh_degree, bg, dinfo=None,
+                timer=None):
         shp = sh if sh_rest is None else (sh, sh_rest)
-        fs = forward_pass(means, log_scales, quats, opacity_logits, shp, cam, sh_degree, bg)
+        fs = forward_pass(means, log_scales, quats, opacity_logits, shp, cam, sh_degree, bg,
+                          timing=timer if timer is not None else False)
         if _Rasterize3D.track_visibility:
             _Rasterize3D.last_visibility = fs.touched
         ctx.fs = fs
+        ctx.timer = timer
         ctx.dinfo = dinfo
         ctx.split = sh_rest is not None
         ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh, sh_rest)
         alpha = 1.0 - fs.final_T
-        ctx.mark_non_differentiable(fs.touched)
-        return fs.image, alpha, fs.touched
+        n_buckets = fs.bucket_offsets[-1]
+        m = torch.tensor(fs.m, dtype=torch.int64)  # host tensor: the count is already on the host
+        ctx.mark_non_differentiable(fs.touched, n_buckets, m)
+        return fs.image, alpha, fs.touched, n_buckets, m
 
     @staticmethod
-    def backward(ctx, grad_image, grad_alpha, _grad_touched):
+    def backward(ctx, grad_image, grad_alpha, _grad_touched, _grad_nb, _grad_m):
         means, log_scales, quats, opacity_logits, sh, sh_rest = ctx.saved_tensors
         fs = ctx.fs
         if grad_image is None:
@@ -368,17 +379,20 @@ class _Rasterize3D(torch.autograd.Function):
         abs_grad = ctx.dinfo is not None and ctx.dinfo.shape[0] == 3
         gm, gls, gq, gop, gsh, grad2d, _ = backward_pass(fs, means.contiguous(), log_scales.contiguous(),
                                                          quats.contiguous(), opacity_logits.contiguous(),
-                                                         shp, grad_image, grad_alpha, abs_grad=abs_grad)
+                                                         shp, grad_image, grad_alpha,
+                                                         timing=ctx.timer if ctx.timer is not None else False,
+                                                         abs_grad=abs_grad)
         ctx.grad2d = grad2d
         if ctx.dinfo is not None:
             densification_stats(grad2d, fs.touched, fs.cam.width, fs.cam.height, ctx.dinfo)
         g_a, g_b = gsh if ctx.split else (gsh, None)
-        return gm, gls, gq, gop, g_a, g_b, None, None, None, None
+        return gm, gls, gq, gop, g_a, g_b, None, None, None, None, None
 
 
 def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None, near: float = 0.01,
               far: float = 100.0, sh_degree: int | None = None, activated: bool = False,
-              densification_info: torch.Tensor | None = None, proper_antialiasing: bool = False):
+              densification_info: torch.Tensor | None = None, proper_antialiasing: bool = False,
+              timing: bool = False):
     """Renders one view. Returns (image [3, H, W], alpha [H, W], aux).
 
     Parameters follow Faster-GS's raw convention unless `activated=True`:
@@ -386,8 +400,14 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
       any norm; opacities [N] or [N,1] logits (activated: opacities in (0,1)); sh [N,K,3] SH
       coefficients, K in {1,4,9,16}, or the pair (DC [N,1,3], rest [N,K-1,3]) that trainers keep
       as two parameters; viewmat [4,4] world-to-camera (OpenCV axes); K [3,3] intrinsics.
-    aux: {"tiles_touched": [N] int32 (> 0 = visible; the visibility mask for a sparse optimizer),
-          "n_visible", "n_instances", "n_buckets"}.
+    aux (gsplat's `meta`, cluster/build_env.sbatch:54; nothing in it makes the host wait):
+      "tiles_touched"  [N] int32, tiles each Gaussian reaches (0 = culled)
+      "visibility"     the same tensor: the mask FusedAdam(sparse=True).step(visibility=...) takes
+      "n_instances"    int, the (tile, Gaussian) instances sorted (Faster-GS's n_instances)
+      "n_buckets"      0-dim int32 device tensor, 32-entry buckets of the tile lists (n_buckets)
+      "n_visible"      0-dim int64 device tensor, Gaussians with tiles_touched > 0
+      "timings"        (timing=True only) a StageTimer: aux["timings"].result() gives the ms of
+                       each forward stage and, once the backward has run, of the backward stages
     Gradients flow to means, scales, quats, opacities and sh. densification_info [2 or 3, N]
     float32 (optional, as the first argument of Faster-GS's backward): the backward adds this view's
     statistics to it (see densification_stats). proper_antialiasing: Faster-GS's setting of that
@@ -400,10 +420,13 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
         bg = (0.0, 0.0, 0.0)
     bg = tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
     sh_a, sh_b = sh if isinstance(sh, (tuple, list)) else (sh, None)
-    image, alpha, touched = _Rasterize3D.apply(means, scales, quats, opacities, sh_a, sh_b, cam, sh_degree, bg,
-                                               densification_info)
-    aux = {"tiles_touched": touched}
-    aux["n_visible"] = lambda: int((touched > 0).sum().item())
+    timer = StageTimer(True) if timing else None
+    image, alpha, touched, n_buckets, m = _Rasterize3D.apply(means, scales, quats, opacities, sh_a, sh_b, cam,
+                                                             sh_degree, bg, densification_info, timer)
+    aux = {"tiles_touched": touched, "visibility": touched, "n_instances": int(m.item()), "n_buckets": n_buckets,
+           "n_visible": (touched > 0).sum()}
+    if timer is not None:
+        aux["timings"] = timer
     return image, alpha, aux
 
 

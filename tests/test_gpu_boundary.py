@@ -1,0 +1,238 @@
+"""The 3D operator boundary: rasterize's aux, the per-call visibility hand-off, and the
+Faster-GS-shaped surface (amdsplat.fastergs: `_C.forward` / `_C.backward` as called at
+phase1/tests/test_parity.py:82-98, `diff_rasterize` + `RasterizerSettings` as at
+cluster/tests/test_lean_adam.py:107-134). GPU tests compare the surfaces with each other and with
+forward_pass / backward_pass; the settings checks run on the CPU."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import dense3d as D
+from amdsplat import FusedAdam, rasterize
+from amdsplat import raster3d as R
+from amdsplat import scenes
+from amdsplat.fastergs import _C, RasterizerSettings, _Rasterize, diff_rasterize
+
+gpu = pytest.mark.gpu
+
+
+def K_of(cam):
+    return torch.tensor([[cam.fx, 0.0, cam.cx], [0.0, cam.fy, cam.cy], [0.0, 0.0, 1.0]])
+
+
+def settings_of(cam, active_sh_bases=16, bg=(0.2, 0.5, 0.8), dev="cuda", proper_antialiasing=False):
+    vm = cam.viewmat.double()
+    centre = (-(vm[:3, :3].T @ vm[:3, 3])).float()
+    return RasterizerSettings(cam.viewmat.to(dev), centre.to(dev), torch.tensor(bg, device=dev), active_sh_bases,
+                              cam.width, cam.height, cam.fx, cam.fy, cam.cx, cam.cy, cam.near, cam.far,
+                              proper_antialiasing)
+
+
+def faster_gs_params(sc, dev="cuda"):
+    """(means, log-scales, rotations, opacity logits [N, 1], SH DC [N, 1, 3], SH rest [N, 15, 3])."""
+    m, ls, q, op, sh = [t.to(dev).contiguous() for t in sc.params()]
+    return m, ls, q, op[:, None].contiguous(), sh[:, :1].contiguous(), sh[:, 1:].contiguous()
+
+
+# ---------------------------------------------------------------------------------------
+# CPU: settings
+# ---------------------------------------------------------------------------------------
+def test_settings_fields_and_tuple_order():
+    """The field order of the reference's settings (cluster/tests/test_lean_adam.py:119-121) is
+    the order _C.forward / _C.backward take them in."""
+    assert RasterizerSettings._fields == ("w2c", "cam_position", "bg_color", "active_sh_bases", "width", "height",
+                                          "focal_x", "focal_y", "center_x", "center_y", "near_plane", "far_plane",
+                                          "proper_antialiasing")
+    s = RasterizerSettings(torch.eye(4), torch.zeros(3), torch.zeros(3), 1, 320, 240, 300.0, 300.0, 160.0, 120.0,
+                           0.2, 1000.0, False)
+    assert s.as_tuple() == tuple(s) and len(s.as_tuple()) == 13
+
+
+def test_camera_of_settings_checks_the_camera_centre():
+    vm = scenes.look_at((1.0, -3.0, 2.0))
+    centre = -(vm[:3, :3].double().T @ vm[:3, 3].double())
+    cam = _C.camera(vm, centre, 128, 96, 100.0, 110.0, 64.0, 48.0, 0.2, 50.0, True)
+    assert torch.equal(cam.viewmat, vm.float()) and cam.proper_antialiasing
+    with pytest.raises(ValueError, match="camera centre"):
+        _C.camera(vm, centre + torch.tensor([0.0, 0.1, 0.0], dtype=torch.float64), 128, 96, 100.0, 110.0, 64.0, 48.0,
+                  0.2, 50.0, False)
+    with pytest.raises(ValueError, match="active_sh_bases"):
+        _C.sh_degree_of(5, torch.zeros(2, 15, 3))
+    with pytest.raises(ValueError, match="active_sh_bases"):
+        _C.sh_degree_of(16, torch.zeros(2, 8, 3))
+    assert _C.sh_degree_of(9, torch.zeros(2, 15, 3)) == 2
+
+
+# ---------------------------------------------------------------------------------------
+# GPU
+# ---------------------------------------------------------------------------------------
+@gpu
+def test_rasterize_aux_counts_visibility_and_timings():
+    sc = scenes.small_scene(20_000, 333, 250, seed=3)
+    cam = sc.cameras[0]
+    p = [t.cuda().contiguous() for t in sc.params()]
+    img, alpha, aux = rasterize(*p, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near, far=cam.far,
+                                timing=True)
+    fs = R.forward_pass(*p, cam)
+    torch.cuda.synchronize()
+    assert aux["visibility"] is aux["tiles_touched"] and torch.equal(aux["tiles_touched"], fs.touched)
+    assert aux["n_instances"] == fs.m > 0
+    assert int(aux["n_buckets"]) == fs.n_buckets > 0
+    assert int(aux["n_visible"]) == int((fs.touched > 0).sum())
+    assert torch.equal(img, fs.image)
+    t_fwd = aux["timings"].result()
+    assert set(t_fwd) == {"preprocess", "depth_order", "binning", "blend_fwd"} and min(t_fwd.values()) > 0
+    leaves = [t.clone().requires_grad_(True) for t in p]
+    img2, _, aux2 = rasterize(*leaves, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near, far=cam.far,
+                              timing=True)
+    img2.sum().backward()
+    t_all = aux2["timings"].result()
+    assert set(t_all) == {"preprocess", "depth_order", "binning", "blend_fwd", "blend_bwd", "preprocess_bwd"}
+    assert "timings" not in rasterize(*p, cam.viewmat, K_of(cam), cam.width, cam.height, near=cam.near,
+                                      far=cam.far)[2]
+
+
+@gpu
+def test_explicit_visibility_per_call():
+    """Two forwards in flight: each optimizer step takes the mask of its own view
+    (aux["visibility"]); the class-attribute alias holds only the last one."""
+    sc = scenes.small_scene(4000, 160, 120, seed=3)
+    c0 = sc.cameras[0]
+    shifted = torch.eye(4)
+    shifted[0, 3] = 0.6  # the camera moved sideways: the Gaussians near one image border leave the view
+    cams = [c0, R.Camera(shifted, c0.fx, c0.fy, c0.cx, c0.cy, c0.width, c0.height, c0.near, c0.far)]
+    params = [torch.nn.Parameter(t.cuda().contiguous()) for t in sc.params()]
+    groups = [{"params": [p], "lr": 1e-3, "name": str(i)} for i, p in enumerate(params)]
+    opt = FusedAdam(groups, lr=0.0, eps=1e-15, sparse=True)
+    outs = [rasterize(*params, c.viewmat, K_of(c), c.width, c.height, near=c.near, far=c.far) for c in cams]
+    vis = [o[2]["visibility"] for o in outs]
+    assert not torch.equal(vis[0] > 0, vis[1] > 0)
+    assert R._Rasterize3D.last_visibility is vis[1]
+    (outs[0][0].sum() + outs[1][0].sum()).backward()
+    before = [p.detach().clone() for p in params]
+    opt.step(visibility=vis[0])
+    hid = vis[0] == 0
+    for p, b in zip(params, before):
+        assert torch.equal(p.detach()[hid], b[hid])
+        assert bool((p.detach()[~hid] != b[~hid]).any())
+    R._Rasterize3D.track_visibility = False
+    _Rasterize.track_visibility = False
+
+
+@gpu
+@pytest.mark.parametrize("rows", [0, 2, 3])
+def test_diff_rasterize_equals_rasterize(rows):
+    """diff_rasterize with Faster-GS's parameter layout renders the same bits as rasterize and
+    gives the same gradients (atomic order aside), in the same layout ([N, 1] opacities, SH DC
+    and rest), and fills densification_info like rasterize does."""
+    sc = scenes.small_scene(20_000, 333, 250, seed=5)
+    cam = sc.cameras[0]
+    fp = [t.requires_grad_(True) for t in faster_gs_params(sc)]
+    di_a = torch.zeros(rows, sc.n, device="cuda") if rows else torch.empty(0, device="cuda")
+    img_a = diff_rasterize(*fp, di_a, settings_of(cam))
+    leaves = [t.cuda().contiguous().requires_grad_(True) for t in sc.params()]
+    di_b = torch.zeros(rows, sc.n, device="cuda") if rows else None
+    img_b, _, _ = rasterize(*leaves[:4], (leaves[4][:, :1], leaves[4][:, 1:]), cam.viewmat, K_of(cam), cam.width,
+                            cam.height, bg=(0.2, 0.5, 0.8), near=cam.near, far=cam.far, densification_info=di_b)
+    assert torch.equal(img_a, img_b.detach())
+    gi = torch.randn(img_a.shape, generator=torch.Generator().manual_seed(1)).cuda()
+    (img_a * gi).sum().backward()
+    (img_b * gi).sum().backward()
+    torch.cuda.synchronize()
+    assert fp[3].grad.shape == (sc.n, 1) and fp[4].grad.shape == (sc.n, 1, 3) and fp[5].grad.shape == (sc.n, 15, 3)
+    pairs = [(fp[0].grad, leaves[0].grad), (fp[1].grad, leaves[1].grad), (fp[2].grad, leaves[2].grad),
+             (fp[3].grad[:, 0], leaves[3].grad), (fp[4].grad, leaves[4].grad[:, :1]),
+             (fp[5].grad, leaves[4].grad[:, 1:])]
+    for a, b in pairs:
+        assert D.rel_err(a.cpu(), b.cpu()) < 1e-5
+    if rows:
+        assert torch.equal(di_a[0], di_b[0])
+        for r in range(1, rows):
+            assert D.rel_err(di_a[r].cpu(), di_b[r].cpu()) < 1e-5
+
+
+@gpu
+def test_C_forward_backward_call_shape_and_determinism():
+    """The reference's parity-test call sequence (phase1/tests/test_parity.py:87-98,131-140): one
+    _C.forward, then _C.backward twice on the same buffers (with a mode argument and with a
+    densification buffer); the two runs agree up to atomic order, < 1e-6."""
+    sc = scenes.small_scene(20_000, 333, 250, seed=6)
+    cam = sc.cameras[0]
+    params = faster_gs_params(sc)
+    settings = settings_of(cam).as_tuple()
+    image, pb, tb, ib, bb, n_inst, n_buckets, sel = _C.forward(*params, *settings)
+    assert torch.isfinite(image).all() and isinstance(n_inst, int) and n_inst > 0 and n_buckets > 0
+    assert torch.equal(_C.n_touched_tiles(pb, sc.n), pb.state.touched)
+    gi = torch.randn(image.shape, generator=torch.Generator().manual_seed(2)).cuda()
+    means, scales, rotations, opacities, sh0, sh_rest = params
+    runs = []
+    for mode in (0, 3):
+        di = torch.zeros(3, sc.n, device="cuda")
+        g = _C.backward(di, gi, image, means, scales, rotations, opacities, sh_rest, pb, tb, ib, bb, *settings,
+                        n_inst, n_buckets, sel, mode)
+        runs.append((g, di))
+    torch.cuda.synchronize()
+    assert len(runs[0][0]) == 6
+    for a, b in zip(runs[0][0], runs[1][0]):
+        assert D.rel_err(a.cpu(), b.cpu()) < 1e-6
+    assert torch.equal(runs[0][1][0], runs[1][1][0]) and D.rel_err(runs[0][1][1].cpu(), runs[1][1][1].cpu()) < 1e-6
+    # the same gradients as the forward_pass / backward_pass pair on the raw parameters
+    fs = R.forward_pass(*[t.cuda() for t in sc.params()], cam, bg=(0.2, 0.5, 0.8))
+    ref = R.backward_pass(fs, *[t.cuda() for t in sc.params()], gi, abs_grad=False)
+    assert torch.equal(fs.image, image)
+    assert D.rel_err(runs[0][0][0].cpu(), ref[0].cpu()) < 1e-5
+    assert D.rel_err(runs[0][0][5].cpu(), ref[4][:, 1:].cpu()) < 1e-5
+
+
+@gpu
+def test_C_empty_scene():
+    """All splats behind the camera: no instances, no buckets, zero gradients
+    (phase1/tests/test_parity.py:143-153)."""
+    sc = scenes.small_scene(100, 64, 48, seed=3)
+    cam = sc.cameras[0]
+    params = list(faster_gs_params(sc))
+    params[0] = params[0] * torch.tensor([1.0, 1.0, -1.0], device="cuda")
+    settings = settings_of(cam).as_tuple()
+    image, pb, tb, ib, bb, n_inst, n_buckets, sel = _C.forward(*params, *settings)
+    assert n_inst == 0 and n_buckets == 0
+    means, scales, rotations, opacities, sh0, sh_rest = params
+    grads = _C.backward(torch.empty(0, device="cuda"), torch.ones_like(image), image, means, scales, rotations,
+                        opacities, sh_rest, pb, tb, ib, bb, *settings, n_inst, n_buckets, sel, 3)
+    torch.cuda.synchronize()
+    assert all(float(g.abs().sum()) == 0.0 for g in grads)
+
+
+@gpu
+def test_visibility_export_from_a_real_forward():
+    """cluster/tests/test_lean_adam.py:107-134 with this surface: half the Gaussians in front of
+    the camera, half behind; every Gaussian with a gradient is marked visible, some are culled."""
+    n = 20_000
+    g = torch.Generator().manual_seed(0)
+    sign = torch.where(torch.rand(n, 1, generator=g) < 0.5, -1.0, 1.0)
+    means = (torch.randn(n, 3, generator=g) * torch.tensor([2.0, 2.0, 1.0]) + sign * torch.tensor([0, 0, 5.0]))
+    means = means.cuda().requires_grad_()
+    scales = torch.full((n, 3), math.log(0.03), device="cuda").requires_grad_()
+    rot = torch.zeros(n, 4, device="cuda")
+    rot[:, 0] = 1
+    rot.requires_grad_()
+    opac = torch.zeros(n, 1, device="cuda").requires_grad_()
+    sh0 = torch.rand(n, 1, 3, generator=g).cuda().requires_grad_()
+    shr = torch.zeros(n, 15, 3, device="cuda").requires_grad_()
+    settings = RasterizerSettings(w2c=torch.eye(4, device="cuda"), cam_position=torch.zeros(3, device="cuda"),
+                                  bg_color=torch.zeros(3, device="cuda"), active_sh_bases=1, width=320, height=240,
+                                  focal_x=300.0, focal_y=300.0, center_x=160.0, center_y=120.0, near_plane=0.2,
+                                  far_plane=1000.0, proper_antialiasing=False)
+    _Rasterize.track_visibility = True
+    try:
+        img = diff_rasterize(means, scales, rot, opac, sh0, shr, torch.empty(0), settings)
+        img.sum().backward()
+        vmask = _Rasterize.last_visibility
+    finally:
+        _Rasterize.track_visibility = False
+    gnz = means.grad.abs().sum(1) > 0
+    assert vmask is not None and vmask.shape == (n,) and vmask.dtype == torch.int32
+    assert bool((vmask[gnz] > 0).all())
+    assert int((vmask > 0).sum()) > 0 and int((vmask == 0).sum()) > 0
+    assert np.all(shr.grad.cpu().numpy() == 0)  # active_sh_bases 1: no gradient above degree 0
