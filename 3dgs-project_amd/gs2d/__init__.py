@@ -8,10 +8,12 @@ and the differentiable tile rasterizer, running on the MI355X through libamdspla
     img = rasterize(means, conic, color, opacity, bins, backend="splat")   # [3, H, W]
 
 Binning runs on the GPU (the reference's runs as PyTorch ops); backends "splat" (bucketed
-backward) and "pixel" (per-pixel backward) are HIP kernels. There is no CPU backend.
+backward) and "pixel" (per-pixel backward) are HIP kernels. `render_reference` (backend "ref")
+is the dense PyTorch ground truth of the same rules, on whatever device its inputs are.
 """
 from .binning import BUCKET, TILE, Bins, bin_gaussians
 from .params import Gaussians2D
 from .raster import rasterize
+from .reference import render_reference
 
-__all__ = ["Gaussians2D", "Bins", "bin_gaussians", "TILE", "BUCKET", "rasterize"]
+__all__ = ["Gaussians2D", "Bins", "bin_gaussians", "TILE", "BUCKET", "render_reference", "rasterize"]

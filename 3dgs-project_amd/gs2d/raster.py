@@ -15,6 +15,7 @@ import torch
 from amdsplat import raster2d as R2
 
 from .binning import Bins
+from .reference import render_reference
 
 
 def _offsets_ext(bucket_offsets: torch.Tensor, num_buckets: int) -> torch.Tensor:
@@ -115,12 +116,13 @@ class _Rasterize(torch.autograd.Function):
 
 
 def rasterize(means, conic, color, opacity, bins: Bins, bg=None, backend: str = "splat"):
-    """Render a (3, H, W) image. backend: 'splat' (bucketed backward) or 'pixel' (per-pixel backward)."""
-    if backend == "ref":
-        raise ValueError("backend 'ref' (the dense PyTorch CPU reference) is not provided; "
-                         "use 'splat' or 'pixel' on a GPU")
-    if backend not in ("pixel", "splat"):
-        raise ValueError(f"unknown backend {backend!r}")
+    """Render a (3, H, W) image. backend: 'splat' (HIP, bucketed backward), 'pixel' (HIP,
+    per-pixel backward) or 'ref' (render_reference: dense PyTorch ops on the tensors' device,
+    autograd gradients; only when asked for by name)."""
     if bg is None:
         bg = torch.zeros(3, dtype=means.dtype, device=means.device)
+    if backend == "ref":
+        return render_reference(means, conic, color, opacity, bins, bg)
+    if backend not in ("pixel", "splat"):
+        raise ValueError(f"unknown backend {backend!r}")
     return _Rasterize.apply(means, conic, color, opacity, bg, bins, backend)

@@ -194,3 +194,36 @@ def test_phase0_oracle_matches_reference_cpu_twin(name, dtype):
         gtol = 1e-12 if dtype == np.float64 else 2e-6
         for cols, r in (((0, 1), rg[0]), ((2, 3, 4), rg[1]), ((5,), rg[2]), ((6, 7, 8), rg[3])):
             assert rel(g[:, list(cols)].reshape(r.shape), r) < gtol, (mode, cols)
+
+
+# ---------------------------------------------------------------------------------------
+# gs2d.render_reference (the dense backend 'ref') against the reference's own dense renderer
+# ---------------------------------------------------------------------------------------
+def fixture_bins(f):
+    import gs2d
+
+    H, W = int(f["H"]), int(f["W"])
+    tx, ty = (W + 15) // 16, (H + 15) // 16
+    z = torch.zeros(0, dtype=torch.int32)
+    return gs2d.Bins(H, W, tx, ty, torch.from_numpy(f["rect"]), torch.from_numpy(f["order"]), z, z, z, z, 0)
+
+
+@pytest.mark.parametrize("name", TOY)
+def test_render_reference_matches_reference_renderer(name):
+    """Image and autograd gradients (upstream dout) of gs2d.render_reference in float64 against
+    the values the reference's render_reference gave for the same scene (the golden fixture):
+    1e-12 (toy2d/tests/test_cpu.py:43-48)."""
+    import gs2d
+
+    f = load(f"toy2d_{name}")
+    x = [torch.tensor(f[k], dtype=torch.float64, requires_grad=True) for k in ("means", "conic", "color", "opacity")]
+    img = gs2d.render_reference(*x, fixture_bins(f), torch.tensor(f["bg"]))
+    assert rel(img.detach().numpy(), f["image"]) < 1e-12
+    (img * torch.tensor(f["dout"])).sum().backward()
+    for t, key in zip(x, ("g_means", "g_conic", "g_color", "g_opacity")):
+        assert rel(t.grad.numpy(), f[key]) < 1e-12, key
+    # the same through rasterize(backend='ref'), in blocks of another size
+    img2 = gs2d.rasterize(*[t.detach() for t in x], fixture_bins(f), torch.tensor(f["bg"]), backend="ref")
+    assert rel(img2.numpy(), f["image"]) < 1e-12
+    img3 = gs2d.render_reference(*[t.detach() for t in x], fixture_bins(f), torch.tensor(f["bg"]), pixels_per_block=7)
+    assert rel(img3.numpy(), f["image"]) < 1e-12

@@ -619,3 +619,56 @@ def test_degree0_rest_gradients_are_zero():
     gsh = O.preprocess_bwd(*np_params(sc), cam, 0, rec, touched, g2)[4]
     assert np.all(gsh[:, 1:, :] == 0)
     assert np.any(gsh[:, 0, :] != 0)
+
+
+# ---------------------------------------------------------------------------------------
+# Screen-space mean gradient of one splat against the continuous closed form
+# ---------------------------------------------------------------------------------------
+def single_splat_scene(sigma_px=10.0, logit=1.5, W=160, H=120, mx=81.3, my=58.7):
+    """One isotropic Gaussian on the optical axis whose projected (dilated) std-dev is sigma_px,
+    colour (1, 0, 0) (SH degree 0), at pixel position (mx, my)."""
+    f, z = 500.0, 4.0
+    s = math.sqrt(sigma_px ** 2 - 0.3) * z / f
+    cam = scenes.Camera(torch.eye(4), f, f, mx, my, W, H, 0.2, 100.0)
+    g = one_gaussian((0.0, 0.0, z), math.log(s), logit=logit, sh0=(0.5 / D.SH0, -0.5 / D.SH0, -0.5 / D.SH0))
+    return cam, g
+
+
+def test_mean2d_gradient_of_one_splat_matches_closed_form():
+    """C_p = c alpha_p with alpha_p = o exp(-|p - mu|^2 / (2 sigma^2)) where o G >= 1/255 (radius R,
+    U = R^2 / (2 sigma^2) = ln(255 o)). With the red upstream gradient a (px - mux) + b (py - muy),
+    dL/dmu = (a, b) 2 pi c o sigma^2 (1 - (1 + U) / (255 o)); with the constant upstream gradient 1,
+    sum_p |dL/dmux at p| = (c o / sigma^2) 4 sigma^3 (sqrt(pi/2) erf(R / (sigma sqrt 2)) - (R/sigma) e^-U).
+    The pixel sums approximate the integrals to about 3e-4 at sigma = 10 px. The NDC norm of
+    the densification statistic, |(W/2 g_x, H/2 g_y)|, follows with W != H."""
+    sigma, logit = 10.0, 1.5
+    cam, g = single_splat_scene(sigma, logit)
+    o = 1.0 / (1.0 + math.exp(-logit))
+    ref = O.render(*g, cam, 0)
+    assert ref["touched"][0] > 0 and np.allclose(ref["rec"][0, 8:11], [1.0, 0.0, 0.0], atol=1e-6)
+    mx, my = float(ref["rec"][0, 0]), float(ref["rec"][0, 1])
+    U = math.log(255.0 * o)
+    R_ = sigma * math.sqrt(2.0 * U)
+    ys, xs = np.mgrid[0:cam.height, 0:cam.width]
+    a, b = 0.7, -1.3
+    gi = np.zeros((3, cam.height, cam.width), np.float32)
+    gi[0] = a * (xs + 0.5 - mx) + b * (ys + 0.5 - my)
+
+    def bwd(upstream):
+        return O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width,
+                           cam.height, ref["image"], upstream, ref["final_T"], ref["n_contrib"], ref["tile_max"],
+                           ref["ckpt"], 1)[0]
+
+    g2 = bwd(gi)
+    K = 2.0 * math.pi * o * sigma ** 2 * (1.0 - (1.0 + U) / (255.0 * o))
+    np.testing.assert_allclose(g2[0:2], [a * K, b * K], rtol=2e-3)
+    ndc = math.hypot(cam.width / 2 * g2[0], cam.height / 2 * g2[1])
+    np.testing.assert_allclose(ndc, K * math.hypot(cam.width / 2 * a, cam.height / 2 * b), rtol=2e-3)
+    assert abs(math.hypot(cam.height / 2 * a, cam.width / 2 * b) * K - ndc) > 0.05 * ndc  # W, H not swapped
+    ones = np.zeros_like(gi)
+    ones[0] = 1.0
+    g1 = bwd(ones)
+    absx = (o / sigma ** 2) * 4.0 * sigma ** 3 * (math.sqrt(math.pi / 2) * math.erf(R_ / (sigma * math.sqrt(2)))
+                                                 - (R_ / sigma) * math.exp(-U))
+    np.testing.assert_allclose(g1[9:11], [absx, absx], rtol=2e-3)
+    assert abs(g1[0]) < 1e-3 * absx  # the signed sum cancels by symmetry
