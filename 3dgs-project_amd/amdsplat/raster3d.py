@@ -389,6 +389,17 @@ class _Rasterize3D(torch.autograd.Function):
         return gm, gls, gq, gop, g_a, g_b, None, None, None, None, None
 
 
+class _Aux(dict):
+    """rasterize's aux dict; "n_visible" is counted on the device when first read (two small
+    kernels that a caller who does not read it does not pay for)."""
+
+    def __missing__(self, key):
+        if key == "n_visible":
+            v = self[key] = (self["tiles_touched"] > 0).sum()
+            return v
+        raise KeyError(key)
+
+
 def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, bg=None, near: float = 0.01,
               far: float = 100.0, sh_degree: int | None = None, activated: bool = False,
               densification_info: torch.Tensor | None = None, proper_antialiasing: bool = False,
@@ -423,8 +434,7 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
     timer = StageTimer(True) if timing else None
     image, alpha, touched, n_buckets, m = _Rasterize3D.apply(means, scales, quats, opacities, sh_a, sh_b, cam,
                                                              sh_degree, bg, densification_info, timer)
-    aux = {"tiles_touched": touched, "visibility": touched, "n_instances": int(m.item()), "n_buckets": n_buckets,
-           "n_visible": (touched > 0).sum()}
+    aux = _Aux(tiles_touched=touched, visibility=touched, n_instances=int(m.item()), n_buckets=n_buckets)
     if timer is not None:
         aux["timings"] = timer
     return image, alpha, aux

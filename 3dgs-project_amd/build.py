@@ -19,7 +19,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 OUT = HERE / "amdsplat" / "libamdsplat.so"
-SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "blend.hip", "raster2d.hip", "adam.hip", "loss.hip"]
+SOURCES = ["capi.hip", "preprocess.hip", "binning.hip", "blend.hip", "raster2d.hip", "adam.hip", "loss.hip",
+           "probe.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

@@ -68,3 +68,26 @@ def fit_scene_4k(n: int = 4096, size: int = 256, seed: int = 0):
     target = torch.rand(3, size, size, generator=g)
     means, conic, _, _, cov = activate(xy, log_scale, theta, torch.zeros(n, 3), torch.zeros(n))
     return means, conic, color, opacity, cov, depth, target
+
+
+def fit_model_4k(n: int = 4096, size: int = 256, seed: int = 0):
+    """The 2D image-fit workload as a trainable model: the draws of fit_scene_4k (same generator
+    and order) as the raw parameters of a Gaussians2D (colour and opacity through their logits),
+    and the target image. Returns (model, target), float32 on the CPU."""
+    g = torch.Generator().manual_seed(seed)
+    xy = torch.rand(n, 2, generator=g) * float(size)
+    log_scale = math.log(2.0) + 0.3 * torch.randn(n, 2, generator=g)
+    theta = torch.rand(n, generator=g) * math.pi
+    opacity_logit = torch.randn(n, generator=g)
+    color = torch.rand(n, 3, generator=g)
+    depth = torch.rand(n, generator=g)
+    target = torch.rand(3, size, size, generator=g)
+    model = Gaussians2D(n, size, size, seed=seed)
+    with torch.no_grad():
+        model.xy.copy_(xy)
+        model.log_scale.copy_(log_scale)
+        model.theta.copy_(theta)
+        model.rgb_logit.copy_(torch.logit(color))
+        model.opacity_logit.copy_(opacity_logit)
+        model.depth.copy_(depth)
+    return model, target

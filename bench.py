@@ -1,24 +1,35 @@
 """Benchmark: 3D Gaussian-splat rasterizer fwd+bwd ms/iter on one MI355X.
 
-Workload (default): 1M Gaussians, SH degree 3, 1297x840, fx=fy=1160, 8 seeded orbit poses
-(radius U(3,5)); one step = forward + backward of one view (poses cycled) with a seeded
-N(0,1) upstream image gradient. Inputs are resident in HBM before the timed region.
+Workload (default, sh3_1m): 1M Gaussians, SH degree 3, 1297x840, fx=fy=1160, 8 seeded orbit
+poses (radius U(3,5)); one step = forward + backward of one view (poses cycled) with a seeded
+N(0,1) upstream image gradient, through the autograd operator rasterize(...) -> image.backward.
+Inputs are resident in HBM before the timed region.
 
-    python bench.py [--steps K] [--warmup W] [--workload sh3_1m|sh3_3m|sh_rgb_100k] [--no-cpu-baseline]
-                    [--no-train-step] [--no-variants]
-    python bench.py --copy-probe      # a plain 1 GiB device copy, to calibrate HBM counters
+    python bench.py [--steps K] [--warmup W] [--workload sh3_1m|sh3_3m|sh_rgb_100k|toy2d_fit]
+                    [--no-cpu-baseline] [--no-train-step] [--no-variants] [--no-probes]
+    python bench.py --probes          # only the achievable-ceiling probes (copy, read, FMA)
 
-Prints ONE JSON line. `value` is the wall time of K plain steps; per-stage times come from
-HIP events recorded on the launch stream in a second pass over the same K steps; `roofline` is for the kernel with the largest share of the step
-(the bucketed blend backward), from its algorithmic bytes and its event-timed duration, plus
-its VALU issue rate from the committed SQ counter summary. `train_step` (secondary) times the
-full training step on the same scene: forward, L1 + D-SSIM loss, backward and fused Adam
-(dense and visibility-masked), with the optimizer's HBM rate; `variants` the inference forward,
-the pruning-score blend and fwd+bwd under proper antialiasing, per view.
+Prints ONE JSON line. `value` is the wall time of K autograd steps / K. A second pass over the
+same K steps with HIP events between the stages gives the per-stage times and the per-pose
+medians (K/8 steps per pose). `roofline` is for the kernel with the largest share of the step,
+the bucketed blend backward: it is bound by the FP32 VALU issue rate, so `achieved` is its
+algorithmic VALU work (a per-pair operation model over the pairs it evaluated, counted in a
+separate pass) over its event-timed duration, against the published FP32 vector peak; beside it
+the counter-measured issue rate (committed SQ summary), its HBM rate (algorithmic bytes) and the
+achievable ceilings measured here by plain copy, read-only and FMA kernels. `train_step`
+(secondary) times the full training step on the same scene: forward, L1 + D-SSIM loss,
+backward and fused Adam (dense and visibility-masked), with the optimizer's HBM rate; `variants`
+the inference forward, the pruning-score blend and fwd+bwd under proper antialiasing.
+`cpu_baseline` is the oracle (the C restatement of the same rules) on the host cores, one view's
+fwd+bwd, all cores (median of 5 after a warm-up) and one thread (median of 3).
+
+toy2d_fit is the 2D image fit (4096 Gaussians, 256x256, L1, Adam): the GPU step through the HIP
+kernels, beside the dense PyTorch reference path (render_reference) on the host cores.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import re
@@ -31,24 +42,36 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "3dgs-project_amd"))
 
 HBM_PEAK_GBS = 8000.0
-# wave64 FP32 VALU instructions per second: the published 157.3 TFLOP/s FP32 vector peak, an FMA
-# counting 2 FLOP on each of 64 lanes
-VALU_PEAK_INSTR = 157.3e12 / 2 / 64
+# FP32 VALU lane operations per second: the published 157.3 TFLOP/s FP32 vector peak with an
+# FMA counted as 2 FLOP (one lane operation)
+VALU_PEAK_TOPS = 157.3 / 2
+# the same peak in wave64 instructions per second
+VALU_PEAK_INSTR = VALU_PEAK_TOPS * 1e12 / 64
 METRIC = "fwd+bwd ms/iter @1M Gaussians SH3 1297x840; per-stage HBM GB/s vs roofline"
 # stages that are one kernel each (the others group several kernels)
 SINGLE_KERNEL = {"preprocess": "preprocess_fwd_kernel", "blend_fwd": "blend_fwd_strip_kernel",
                  "blend_bwd": "blend_bwd_bucket_kernel", "preprocess_bwd": "preprocess_bwd_kernel"}
+# VALU work model of the 3D bucketed blend backward (lane operations, an FMA counted once):
+# per evaluated (pixel, splat) pair, the falloff (dy, power 2 FMA, exp2, times opacity, alpha
+# test and select), T alpha, the colour dot (3), the three colour sums, rho, 1 - alpha, the
+# clamp and reciprocal, dL/dalpha (2), dL/dpower and its dy factor, the three power sums and the
+# T update: 27; per splat and lane of a walked bucket, the column terms (dx, a0 (2), b1, and the
+# two mean-gradient column factors): 6; per splat a bucket reduces, 9 values summed over 64
+# lanes: 9 * 63.
+OPS_PER_PAIR, OPS_PER_STEP_LANE, OPS_PER_REDUCTION = 27, 6, 9 * 63
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=40)
-    ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "sh3_3m", "sh_rgb_100k"])
+    ap.add_argument("--steps", type=int, default=160)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="threads for the CPU baseline (0 = OMP default)")
-    ap.add_argument("--copy-probe", action="store_true", help="time a plain 1 GiB device copy and exit")
+    ap.add_argument("--cpu-runs", type=int, default=5, help="all-core CPU baseline runs (median)")
+    ap.add_argument("--cpu-single-runs", type=int, default=3, help="single-thread CPU baseline runs (0 = skip)")
+    ap.add_argument("--probes", action="store_true", help="only run the copy / read / FMA probes and exit")
+    ap.add_argument("--no-probes", action="store_true")
     ap.add_argument("--no-train-step", action="store_true", help="skip the training-step measurement")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the inference / pruning-score / antialiasing variants (profiling runs)")
@@ -56,6 +79,53 @@ def parse():
     return ap.parse_args()
 
 
+# ---------------------------------------------------------------------------------------
+# Achievable ceilings
+# ---------------------------------------------------------------------------------------
+def _event_ms(fn, reps: int, warmup: int = 3) -> float:
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def probes() -> dict:
+    """Plain copy and read-only sweeps of 1 GiB (well beyond the last-level cache) and
+    independent FP32 FMA chains on every SIMD, launched by the library on the current stream."""
+    import torch
+
+    from amdsplat import _lib
+    from amdsplat._lib import call, ptr
+
+    st = _lib.stream_handle()
+    n = 1 << 28  # floats: 1 GiB
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    sums = torch.empty(_lib.size_call("gs_probe_read_sums", n), device="cuda")
+    copy_ms = _event_ms(lambda: call("gs_probe_copy", ptr(a), ptr(b), n, st), 10)
+    read_ms = _event_ms(lambda: call("gs_probe_read", ptr(a), n, ptr(sums), st), 10)
+    del a, b, sums
+    threads, iters = 256 * 4 * 8 * 64, 2048  # 8 wavefronts per SIMD
+    out = torch.empty(threads, device="cuda")
+    fma_ms = _event_ms(lambda: call("gs_probe_fma", ptr(out), threads, iters, st), 5)
+    fma_ops = threads * iters * 32
+    return {"copy_gbs": round(8 * n / (copy_ms * 1e6), 1), "read_gbs": round(4 * n / (read_ms * 1e6), 1),
+            "fma_tops": round(fma_ops / (fma_ms * 1e-3) / 1e12, 2),
+            "note": "copy: 1 GiB read + 1 GiB written; read: 1 GiB read; fma: 8 independent FMA chains per lane, "
+                    "8 wavefronts per SIMD, T lane-op/s"}
+
+
+# ---------------------------------------------------------------------------------------
+# 3D workloads
+# ---------------------------------------------------------------------------------------
 def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, ckpt_written,
                 atomics_per_pair=9):
     """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
@@ -104,23 +174,23 @@ def bucket_stats(fs):
     return int(active.sum()), int(tmax.sum()), int(staged.sum()), int(((staged + 31) // 32).sum())
 
 
+def _profile_value(name: str, key: str):
+    f = ROOT / "profiles" / name
+    if not f.exists():
+        return None
+    m = re.search(rf"{key}:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE and
     WRITE_SIZE, calibrated with a plain copy), or None."""
-    f = ROOT / "profiles" / f"{kernel}_hbm_traffic.md"
-    if not f.exists():
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
-    return float(m.group(1)) if m else None
+    return _profile_value(f"{kernel}_hbm_traffic.md", "traffic_bytes_per_launch")
 
 
 def measured_valu_instr(kernel: str):
     """VALU instructions per launch of `kernel` from the committed rocprofv3 SQ summary, or None."""
-    f = ROOT / "profiles" / f"{kernel}_sq.md"
-    if not f.exists():
-        return None
-    m = re.search(r"valu_instr_per_launch:\s*([0-9.eE+]+)", f.read_text())
-    return float(m.group(1)) if m else None
+    return _profile_value(f"{kernel}_sq.md", "valu_instr_per_launch")
 
 
 def cpu_model() -> str:
@@ -133,34 +203,67 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(scene, pose, threads):
-    """The C oracle (the CPU restatement of the same rules, OpenMP where the loops allow) timed
-    on the host: one full fwd+bwd of one view of the workload (~10 s)."""
+def _omp_threads(n: int) -> None:
+    """Sets the OpenMP thread count of the oracle's parallel loops (libgomp, already loaded)."""
+    ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+
+
+def _median_runs(fn, runs: int) -> tuple[float, list]:
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def cpu_baseline_3d(scene, pose: int, runs: int, single_runs: int) -> dict:
+    """The C oracle (the CPU restatement of the same rules: preprocess, binning and forward blend
+    on OpenMP threads, the backward blend single-threaded) timed on the host: one full fwd+bwd of
+    one view of the workload, all cores (median of `runs` after a warm-up) and one thread."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
-    if threads > 0:
-        os.environ["OMP_NUM_THREADS"] = str(threads)
     import oracle as O
 
     cam = scene.cameras[pose]
     p = [t.numpy() for t in scene.params()]
     gi = np.random.default_rng(0).standard_normal((3, cam.height, cam.width)).astype(np.float32)
-    t0 = time.perf_counter()
-    r = O.render(*p, cam, 3)
-    g2 = O.blend_bwd(r["rec"], r["point_list"], r["ranges"], r["bucket_offsets"], cam.width, cam.height,
-                     r["image"], gi, r["final_T"], r["n_contrib"], r["tile_max"], r["ckpt"], scene.n)
-    O.preprocess_bwd(*p, cam, 3, r["rec"], r["touched"], g2)
-    dt = time.perf_counter() - t0
-    cores = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    return {"value": round(dt * 1000.0, 1), "unit": "ms/iter", "cores": cores, "kind": "port",
-            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
-            "sample": f"C oracle fwd+bwd of pose {pose}, all {scene.n} Gaussians ({dt:.1f} s; preprocess and "
-                      f"forward blend on {cores} OpenMP threads, sort and backward blend single-threaded)"}
+    deg = int(round(scene.sh.shape[1] ** 0.5)) - 1
+
+    def once():
+        r = O.render(*p, cam, deg)
+        g2 = O.blend_bwd(r["rec"], r["point_list"], r["ranges"], r["bucket_offsets"], cam.width, cam.height,
+                         r["image"], gi, r["final_T"], r["n_contrib"], r["tile_max"], r["ckpt"], scene.n)
+        O.preprocess_bwd(*p, cam, deg, r["rec"], r["touched"], g2)
+
+    cores = os.cpu_count() or 1
+    once()  # warm-up (also loads and builds the oracle)
+    _omp_threads(cores)
+    med, times = _median_runs(once, runs)
+    out = {"value": round(med * 1000.0, 1), "unit": "ms/iter", "cores": cores, "kind": "port",
+           "runs_s": [round(t, 2) for t in times], "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+           "sample": f"the C oracle's fwd+bwd of pose {pose} of this workload, all {scene.n} Gaussians: median of "
+                     f"{runs} runs after a warm-up, {cores} OpenMP threads (preprocess, binning and forward "
+                     f"blend parallel; the backward blend single-threaded)"}
+    if single_runs > 0:
+        _omp_threads(1)
+        smed, stimes = _median_runs(once, single_runs)
+        _omp_threads(cores)
+        out["single_thread"] = {"value": round(smed * 1000.0, 1), "unit": "ms/iter", "cores": 1,
+                                "runs_s": [round(t, 2) for t in stimes],
+                                "sample": f"the same view, one thread, median of {single_runs} runs"}
+    return out
 
 
 # learning rates of the training-step workload (means, log-scales, quats, SH DC, SH rest, opacity)
 TRAIN_LR = {"means": 1.6e-4, "scales": 5e-3, "quats": 1e-3, "sh_dc": 2.5e-3, "sh_rest": 1.25e-4, "opacity": 5e-2}
+
+
+def _K(c):
+    import torch
+
+    return torch.tensor([[c.fx, 0.0, c.cx], [0.0, c.fy, c.cy], [0.0, 0.0, 1.0]])
 
 
 def train_step_bench(scene, steps: int, warmup: int) -> dict:
@@ -178,7 +281,7 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
     cams = sc.cameras
     g = torch.Generator().manual_seed(4321)
     targets = [torch.rand(3, c.height, c.width, generator=g).cuda() for c in cams]
-    Ks = [torch.tensor([[c.fx, 0.0, c.cx], [0.0, c.fy, c.cy], [0.0, 0.0, 1.0]]) for c in cams]
+    Ks = [_K(c) for c in cams]
     n = m.shape[0]
     out = {"workload": f"{n} Gaussians SH3 {cams[0].width}x{cams[0].height}: fwd, L1+D-SSIM (11x11, lambda 0.2), "
                        f"bwd, fused Adam over 59 fp32 parameters per Gaussian",
@@ -187,7 +290,6 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
         params = {k: torch.nn.Parameter(v.clone()) for k, v in P.items()}
         groups = [{"params": [params[k]], "lr": lr, "name": k} for k, lr in TRAIN_LR.items()]
         opt = FusedAdam(groups, lr=0.0, eps=1e-15, sparse=(mode == "masked"))
-        vis_sum = 0
 
         def step(k, ev=None):
             c = cams[k % len(cams)]
@@ -198,7 +300,7 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
             loss.backward()
             if ev:
                 ev[0].record()
-            opt.step()
+            opt.step(visibility=aux["visibility"])
             if ev:
                 ev[1].record()
             opt.zero_grad(set_to_none=True)
@@ -221,9 +323,11 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
                      "adam_hbm_gbs": round(nbytes / (adam_ms * 1e6), 1),
                      "adam_hbm_frac": round(nbytes / (adam_ms * 1e6) / HBM_PEAK_GBS, 4),
                      "adam_algorithmic_bytes": nbytes, "visible_per_view": round(vis_sum)}
+        from amdsplat.fastergs import _Rasterize
         from amdsplat.raster3d import _Rasterize3D
 
         _Rasterize3D.track_visibility = False
+        _Rasterize.track_visibility = False
     return out
 
 
@@ -240,7 +344,7 @@ def variants_bench(sc, grads, steps: int, warmup: int) -> dict:
 
     params = sc.params()
     cams = sc.cameras
-    Ks = [torch.tensor([[c.fx, 0.0, c.cx], [0.0, c.fy, c.cy], [0.0, 0.0, 1.0]]) for c in cams]
+    Ks = [_K(c) for c in cams]
     scores = torch.zeros(params[0].shape[0], dtype=torch.float32, device="cuda")
     aa_cams = [dataclasses.replace(c, proper_antialiasing=True) for c in cams]
 
@@ -275,48 +379,30 @@ def variants_bench(sc, grads, steps: int, warmup: int) -> dict:
     return out
 
 
-def copy_probe():
-    import torch
-
-    n = 1 << 28  # 1 GiB of float32
-    a = torch.ones(n, device="cuda")
-    b = torch.empty_like(a)
-    for _ in range(3):
-        b.copy_(a)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    reps = 10
-    for _ in range(reps):
-        b.copy_(a)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "ms": round(ms, 4),
-                      "GBps_read_plus_write": round(8 * n / (ms * 1e6), 1)}))
-
-
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "the benchmark runs on one GPU; several GPUs are not supported",
-                          "n_gpus": args.gpus}))
-        sys.exit(2)
-    if args.copy_probe:
-        copy_probe()
-        return
+def bench_3d(args, ceilings) -> dict:
     import torch
 
     from amdsplat import raster3d as R
-    from amdsplat import scenes
+    from amdsplat import rasterize, scenes
 
     make = {"sh3_1m": scenes.sh3_1m, "sh3_3m": scenes.sh3_3m, "sh_rgb_100k": scenes.sh_rgb_100k}[args.workload]
     scene = make()
     sc = scene.to("cuda")
     params = sc.params()
     cams = sc.cameras
+    Ks = [_K(c) for c in cams]
     g = torch.Generator().manual_seed(1234)
     grads = [torch.randn(3, c.height, c.width, generator=g).cuda() for c in cams]
+    leaves = [t.clone().requires_grad_(True) for t in params]
+
+    def autograd_step(k):
+        """The operator north_star names: rasterize(...) -> image, then image.backward(grad)."""
+        pose = k % len(cams)
+        c = cams[pose]
+        for t in leaves:
+            t.grad = None
+        img, _, _ = rasterize(*leaves, c.viewmat, Ks[pose], c.width, c.height, near=c.near, far=c.far)
+        img.backward(grads[pose])
 
     def step(k, timer=None, counters=None):
         pose = k % len(cams)
@@ -325,17 +411,21 @@ def main():
                               abs_grad=False)
         return fs, out
 
-    for k in range(args.warmup):
-        step(k)
-    torch.cuda.synchronize()
+    def timed(fn, k_steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(k_steps):
+            fn(k)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1000.0 / k_steps
 
-    # the timed region: K steps, nothing recorded between the stages
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
+    for k in range(args.warmup):
+        autograd_step(k)
         step(k)
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    # the timed region: K autograd steps, nothing recorded between the stages
+    wall_ms = timed(autograd_step, args.steps)
+    # the same K steps through forward_pass / backward_pass (no autograd bookkeeping)
+    low_ms = timed(lambda k: step(k), args.steps)
 
     # the per-stage breakdown: the same K steps again with HIP events between the stages (the
     # events cost a few microseconds each, so this pass is not the headline number)
@@ -356,12 +446,12 @@ def main():
         pose_ms[k % len(cams)].append(step_ms[-1])
         for k2, v in r.items():
             per_stage.setdefault(k2, []).append(v)
-    stage_ms = {k2: statistics.mean(v) for k2, v in per_stage.items() if k2 != "start"}
+    stage_ms = {k2: statistics.mean(v) for k2, v in per_stage.items()}
     # per pose: the median over its event-timed steps; then the median and the max over the poses
     pose_medians = [statistics.median(v) for v in pose_ms if v]
 
-    # counts for the byte model: one counting step per pose outside the timed regions, averaged
-    # over the poses like the timings
+    # counts for the byte and operation models: one counting step per pose outside the timed
+    # regions, averaged over the poses like the timings
     per_pose = []
     for pose in range(len(cams)):
         ctr = torch.zeros(3, dtype=torch.int64, device="cuda")
@@ -370,24 +460,51 @@ def main():
         nv = int((fs.touched > 0).sum().item())
         ab, ss, stg, ckw = bucket_stats(fs)
         up = int(ctr[0].item()) // 9
+        ev = int(ctr[2].item())
         per_pose.append({"visible": nv, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
                          "active_buckets": ab, "bucket_splat_steps": ss, "staged_entries": stg,
-                         "ckpt_written": ckw, "reduced_bucket_splats": up,
-                         "bwd_pair_evals": int(ctr[2].item()),
+                         "ckpt_written": ckw, "reduced_bucket_splats": up, "bwd_pair_evals": ev,
+                         "bwd_valu_ops": OPS_PER_PAIR * ev + OPS_PER_STEP_LANE * 64 * ss + OPS_PER_REDUCTION * up,
                          "bytes": stage_bytes(fs, nv, ab, ss, up, stg, ckw)})
     counts = {k2: round(statistics.mean(pp[k2] for pp in per_pose)) for k2 in per_pose[0] if k2 != "bytes"}
     sb = {k2: statistics.mean(pp["bytes"][k2] for pp in per_pose) for k2 in per_pose[0]["bytes"]}
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
     dominant = max((k2 for k2 in stage_ms if k2 in SINGLE_KERNEL), key=lambda k2: stage_ms[k2])
-    achieved = stage_gbs[dominant]
-    traffic = measured_traffic(SINGLE_KERNEL[dominant])
-    valu_instr = measured_valu_instr(SINGLE_KERNEL[dominant])
-    valu = None
+    kernel = SINGLE_KERNEL[dominant]
+    t_dom = stage_ms[dominant]
+    hbm = {"achieved": round(stage_gbs[dominant], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(stage_gbs[dominant] / HBM_PEAK_GBS, 4), "algorithmic_bytes": round(sb[dominant])}
+    if ceilings:
+        hbm["achievable"] = ceilings["copy_gbs"]
+        hbm["frac_of_achievable"] = round(stage_gbs[dominant] / ceilings["copy_gbs"], 4)
+    if dominant == "blend_bwd":
+        ops = counts["bwd_valu_ops"]
+        tops = ops / (t_dom * 1e-3) / 1e12
+        roof = {"kernel": kernel, "bound": "valu", "achieved": round(tops, 3), "peak": VALU_PEAK_TOPS,
+                "unit": "T FP32 lane-op/s (157.3 TFLOP/s with an FMA as 2)", "frac": round(tops / VALU_PEAK_TOPS, 4),
+                "traffic": measured_traffic(kernel), "algorithmic_ops": ops,
+                "ops_model": f"{OPS_PER_PAIR} per evaluated pair + {OPS_PER_STEP_LANE} per lane and bucket-splat "
+                             f"step + {OPS_PER_REDUCTION} per reduced bucket-splat",
+                "avg_launch_ms": round(t_dom, 4), "hbm": hbm}
+        if ceilings:
+            roof["achievable"] = ceilings["fma_tops"]
+            roof["frac_of_achievable"] = round(tops / ceilings["fma_tops"], 4)
+    else:
+        roof = {"kernel": kernel, "bound": "hbm", **{k: v for k, v in hbm.items() if k != "algorithmic_bytes"},
+                "traffic": measured_traffic(kernel), "algorithmic_bytes": hbm["algorithmic_bytes"],
+                "avg_launch_ms": round(t_dom, 4)}
+    valu_instr = measured_valu_instr(kernel)
     if valu_instr:
-        rate = valu_instr / (stage_ms[dominant] * 1e-3)
-        valu = {"achieved": round(rate / 1e12, 4), "peak": round(VALU_PEAK_INSTR / 1e12, 4),
-                "unit": "T wave64 instr/s", "frac": round(rate / VALU_PEAK_INSTR, 4), "instr_per_launch": valu_instr}
+        rate = valu_instr / (t_dom * 1e-3)
+        roof["issue"] = {"valu_instr_per_launch": valu_instr, "achieved": round(rate / 1e12, 4),
+                         "peak": round(VALU_PEAK_INSTR / 1e12, 4), "unit": "T wave64 VALU instr/s",
+                         "frac": round(rate / VALU_PEAK_INSTR, 4)}
+    atomics = _profile_value(f"{kernel}_atomics.md", "atomic_requests_per_launch")
+    if atomics:
+        roof["atomic_requests_per_launch"] = atomics
 
+    views = f"{len(cams)} orbit poses" if len(cams) > 1 else "one camera"
+    fs_cam = cams[0]
     out = {
         "metric": METRIC,
         "value": round(wall_ms, 4),
@@ -401,32 +518,203 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded generator; random-init Gaussians of the configured distribution)",
-        "config": {"workload": f"{args.workload}: {scene.n} Gaussians SH{fs.sh_degree} "
-                               f"{fs.cam.width}x{fs.cam.height}, fwd+bwd per view, 8 orbit poses",
-                   "gaussians": scene.n, "width": fs.cam.width, "height": fs.cam.height,
+        "config": {"workload": f"{args.workload}: {scene.n} Gaussians SH{int(round(scene.sh.shape[1] ** 0.5)) - 1} "
+                               f"{fs_cam.width}x{fs_cam.height}, fwd+bwd per view through rasterize(...) and "
+                               f"autograd, {views}",
+                   "gaussians": scene.n, "width": fs_cam.width, "height": fs_cam.height,
                    "parallelism": "single GPU"},
+        "low_level_ms_per_step": round(low_ms, 4),
         "stage_ms": {k2: round(v, 4) for k2, v in stage_ms.items()},
         "stage_hbm_gbs": {k2: round(v, 1) for k2, v in stage_gbs.items()},
         "stage_hbm_frac": {k2: round(v / HBM_PEAK_GBS, 4) for k2, v in stage_gbs.items()},
         "event_sum_ms": round(statistics.mean(step_ms), 4),
         "per_pose_ms": {"median": round(statistics.median(pose_medians), 4), "max": round(max(pose_medians), 4),
-                        "poses": [round(v, 4) for v in pose_medians]},
+                        "steps_per_pose": args.steps // len(cams), "poses": [round(v, 4) for v in pose_medians]},
         "staged_pass_ms_per_step": round(staged_wall_ms, 4),
         "counts": counts,
-        "roofline": {"kernel": SINGLE_KERNEL[dominant], "bound": "hbm", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes": round(sb[dominant]),
-                     "avg_launch_ms": round(stage_ms[dominant], 4), "valu": valu},
+        "roofline": roof,
     }
+    if ceilings:
+        out["achievable"] = ceilings
+        out["stage_hbm_frac_of_achievable"] = {k2: round(v / ceilings["copy_gbs"], 4) for k2, v in stage_gbs.items()}
     if not args.no_variants:
-        out["variants"] = variants_bench(sc, grads, steps=max(args.steps // 2, 5), warmup=3)
+        out["variants"] = variants_bench(sc, grads, steps=max(args.steps // 4, 16), warmup=4)
     if not args.no_train_step:
-        out["train_step"] = train_step_bench(scene, steps=max(args.steps // 2, 5), warmup=3)
+        out["train_step"] = train_step_bench(scene, steps=max(args.steps // 4, 16), warmup=4)
     if not args.no_cpu_baseline:
         try:
-            out["cpu_baseline"] = cpu_baseline(scene, 0, args.cpu_threads)
+            out["cpu_baseline"] = cpu_baseline_3d(scene, 0, args.cpu_runs, args.cpu_single_runs)
         except Exception as e:  # the baseline is reported, never required
             out["cpu_baseline"] = {"error": repr(e)}
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# 2D image fit (toy2d rules)
+# ---------------------------------------------------------------------------------------
+FIT_LR = lambda H, W: {"xy": 0.002 * max(H, W) / 10, "log_scale": 0.01, "theta": 0.01, "rgb_logit": 0.02,  # noqa: E731
+                       "opacity_logit": 0.02}
+
+
+def _fit_optimizer(model, H, W):
+    import torch
+
+    lr = FIT_LR(H, W)
+    return torch.optim.Adam([{"params": [getattr(model, k)], "lr": v} for k, v in lr.items()])
+
+
+def cpu_baseline_toy2d(bins_cpu, runs: int, single_runs: int) -> dict:
+    """The reference's CPU path of the fit, restated (gs2d.render_reference: every Gaussian
+    against every pixel in PyTorch ops): activate, dense render, L1, autograd backward and Adam
+    on the host cores, with the tile rectangles and depth order of the first step's binning (the
+    binning is a small part of the step)."""
+    import torch
+
+    from gs2d import render_reference
+    from gs2d.params import fit_model_4k
+
+    model, target = fit_model_4k()
+    opt = _fit_optimizer(model, 256, 256)
+
+    def once():
+        means, conic, color, opacity, _ = model.activated()
+        img = render_reference(means, conic, color, opacity, bins_cpu)
+        loss = (img - target).abs().mean()
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+
+    cores = torch.get_num_threads()
+    once()
+    med, times = _median_runs(once, runs)
+    out = {"value": round(med * 1000.0, 1), "unit": "ms/iter", "cores": cores, "kind": "port",
+           "runs_s": [round(t, 3) for t in times], "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+           "sample": f"one fit step of this workload on the dense reference path (render_reference, PyTorch CPU, "
+                     f"{cores} threads): median of {runs} runs after a warm-up"}
+    if single_runs > 0:
+        torch.set_num_threads(1)
+        smed, stimes = _median_runs(once, single_runs)
+        torch.set_num_threads(cores)
+        out["single_thread"] = {"value": round(smed * 1000.0, 1), "unit": "ms/iter", "cores": 1,
+                                "runs_s": [round(t, 3) for t in stimes],
+                                "sample": f"the same step, one thread, median of {single_runs} runs"}
+    return out
+
+
+def bench_toy2d(args, ceilings) -> dict:
+    import torch
+
+    from amdsplat import raster3d as R
+    from gs2d import bin_gaussians, rasterize
+    from gs2d.params import fit_model_4k, radii_from_cov
+    from gs2d.raster import ext
+
+    H = W = 256
+    model, target = fit_model_4k()
+    model = model.cuda()
+    target = target.cuda()
+    opt = _fit_optimizer(model, H, W)
+
+    def step(k, timer=None):
+        tm = timer if timer is not None else R.StageTimer(False)
+        tm.mark("start")
+        means, conic, color, opacity, cov = model.activated()
+        bins = bin_gaussians(means, radii_from_cov(cov.detach()), model.depth, H, W)
+        tm.mark("binning")
+        img = rasterize(means, conic, color, opacity, bins, backend="splat")
+        tm.mark("forward")
+        loss = (img - target).abs().mean()
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        tm.mark("backward")
+        opt.step()
+        tm.mark("adam")
+        return bins
+
+    for k in range(args.warmup):
+        step(k)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        bins = step(k)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    timers = [R.StageTimer(True) for _ in range(args.steps)]
+    for k in range(args.steps):
+        step(k, timers[k])
+    torch.cuda.synchronize()
+    stage_ms = {}
+    for tm in timers:
+        for k2, v in tm.result(sync=False).items():
+            stage_ms.setdefault(k2, []).append(v)
+    stage_ms = {k2: statistics.mean(v) for k2, v in stage_ms.items()}
+
+    # the kernels alone, as the reference's bench times them (toy2d/bench.py:48-73): forward with
+    # checkpoints and the bucketed backward, on the current parameters
+    with torch.no_grad():
+        means, conic, color, opacity, cov = (t.contiguous() for t in model.activated())
+        bins = bin_gaussians(means, radii_from_cov(cov), model.depth, H, W)
+    e = ext()
+    bg = torch.zeros(3, device="cuda")
+    dout = torch.randn(3, H, W, generator=torch.Generator().manual_seed(7)).cuda()
+    common = (means, conic, color, opacity, bg, bins.ranges, bins.point_list)
+    out_s, final_T, n_contrib, bstate = e.forward(*common, bins.bucket_offsets, bins.num_buckets, H, W, True)
+    fwd_ms = _event_ms(lambda: e.forward(*common, bins.bucket_offsets, bins.num_buckets, H, W, True), 50)
+    bwd_ms = _event_ms(lambda: e.backward_splat(*common, bins.bucket_offsets, bins.bucket_to_tile, out_s, final_T,
+                                                n_contrib, bstate, dout), 50)
+    m = int(bins.point_list.numel())
+    nb = int(bins.num_buckets)
+    n = means.shape[0]
+    P = H * W
+    # algorithmic bytes: forward -- ids and 64-byte records of every list entry, image / final T /
+    # n_contrib per pixel, 4 KiB of checkpoints per bucket; backward -- checkpoints, grad image,
+    # image and n_contrib per bucket pixel, ids and records per entry, 9 atomics per entry
+    fwd_bytes = m * (4 + 64) + P * 20 + nb * 4096
+    bwd_bytes = nb * (4096 + 256 * 28) + m * (4 + 64) + m * 36 + n * 48
+    dom, t_dom, by = ("backward_splat", bwd_ms, bwd_bytes) if bwd_ms >= fwd_ms else ("forward", fwd_ms, fwd_bytes)
+    gbs = by / (t_dom * 1e6)
+    roof = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": by,
+            "avg_launch_ms": round(t_dom, 4),
+            "note": "a 256x256 frame with 4096 Gaussians keeps 256 workgroups busy for microseconds: the kernels "
+                    "are launch- and latency-bound at this size, far from either roofline"}
+    if ceilings:
+        roof["achievable"] = ceilings["copy_gbs"]
+        roof["frac_of_achievable"] = round(gbs / ceilings["copy_gbs"], 4)
+    out = {
+        "metric": "toy2d 2D image fit ms/iter (4096 Gaussians, 256x256, L1, Adam)",
+        "value": round(wall_ms, 4), "unit": "ms/iter", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded: means U(0,256)^2, log-scales N(ln 2, 0.3), angle U(0, pi), "
+                                "opacity sigmoid(N(0,1)), colour U(0,1), target U(0,1))",
+        "config": {"workload": "toy2d_fit: 4096 2D Gaussians, 256x256, one fit step (activate, GPU binning, "
+                               "forward, L1, bucketed backward, Adam)", "parallelism": "single GPU"},
+        "stage_ms": {k2: round(v, 4) for k2, v in stage_ms.items()},
+        "kernel_ms": {"forward_with_checkpoints": round(fwd_ms, 4), "backward_splat": round(bwd_ms, 4)},
+        "counts": {"pairs": m, "buckets": nb},
+        "roofline": roof,
+    }
+    if ceilings:
+        out["achievable"] = ceilings
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline_toy2d(bins.to("cpu"), args.cpu_runs, args.cpu_single_runs)
+        except Exception as e:  # the baseline is reported, never required
+            out["cpu_baseline"] = {"error": repr(e)}
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "the benchmark runs on one GPU; several GPUs are not supported",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    if args.probes:
+        print(json.dumps(probes()))
+        return
+    ceilings = None if args.no_probes else probes()
+    out = bench_toy2d(args, ceilings) if args.workload == "toy2d_fit" else bench_3d(args, ceilings)
     line = json.dumps(out)
     print(line, flush=True)
     if args.json_out:

@@ -357,6 +357,22 @@ int gs_l1_ssim_bwd(const float* image, const float* target, const float* dmap, i
                    int width, float lambda_dssim, const float* grad_loss, float* grad_image, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Measurement probes: the achievable ceilings of the GPU the library runs on, against which
+ * bench.py quotes its roofline fractions besides the published peaks (the reference measured
+ * its copy and read-only bandwidth the same way, results/phase1/README.md:10-16).
+ *   gs_probe_copy   out[i] = in[i] for n floats (n a multiple of 4, 16-byte aligned): 8n bytes
+ *   gs_probe_read   reads n floats (n a multiple of 4, 16-byte aligned) once and writes
+ *                   gs_probe_read_sums(n) partial sums (one per wavefront; that many floats
+ *                   in `sums`)
+ *   gs_probe_fma    `threads` threads (a multiple of 256) each run 32 * iters dependent-free
+ *                   FP32 FMAs (8 chains) and write one float to out[threads]
+ * ------------------------------------------------------------------------------------- */
+int gs_probe_copy(const float* in, float* out, int64_t n, void* stream);
+int64_t gs_probe_read_sums(int64_t n);
+int gs_probe_read(const float* in, int64_t n, float* sums, void* stream);
+int gs_probe_fma(float* out, int64_t threads, int iters, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Allocation-free gs_l1_ssim_fwd. It has no counterpart in the reference. It is for callers
  * that cannot allocate device memory: code under HIP graph capture, tight serving loops, and
  * harnesses that forbid hipMalloc.

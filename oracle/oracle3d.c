@@ -634,14 +634,19 @@ int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point
   int tiles_x = (W + TILE - 1) / TILE, tiles_y = (H + TILE - 1) / TILE;
   int64_t HW = (int64_t)W * H;
   double* acc = (double*)calloc((size_t)n * 12, sizeof(double));
+  /* tiles in parallel; each bucket's per-splat sums are formed over its pixels in double, then
+   * added to the shared totals (one atomic add per value and splat of the bucket) */
+#pragma omp parallel for schedule(dynamic, 1)
   for (int tile = 0; tile < tiles_x * tiles_y; ++tile) {
     int tx = tile % tiles_x, ty = tile / tiles_x;
     uint32_t s = ranges[2 * tile];
+    double loc[BUCKET][12];
     for (uint32_t b = bucket_offsets[tile]; b < bucket_offsets[tile + 1]; ++b) {
       int bstart = (int)(b - bucket_offsets[tile]) * BUCKET;
       if (bstart >= (int)tile_max[tile]) break;
       int bsize = (int)tile_max[tile] - bstart;
       if (bsize > BUCKET) bsize = BUCKET;
+      memset(loc, 0, sizeof(loc));
       for (int t = 0; t < TILE_PIX; ++t) {
         int px = tx * TILE + (t & 15), py = ty * TILE + (t >> 4);
         if (px >= W || py >= H) continue;
@@ -667,7 +672,7 @@ int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point
           if (alpha < ALPHA_MIN) continue;
           double w = (double)T * alpha;
           double dot = G[0] * r[8] + G[1] * r[9] + G[2] * r[10];
-          double* a = acc + 12 * (int64_t)id;
+          double* a = loc[j];
           a[6] += w * G[0]; a[7] += w * G[1]; a[8] += w * G[2];
           rho -= w * dot;
           float oma = 1.0f - alpha;
@@ -682,6 +687,14 @@ int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point
           a[0] += gmx; a[1] += gmy;
           a[9] += fabs(gmx); a[10] += fabs(gmy);
           T = T * oma;
+        }
+      }
+      for (int j = 0; j < bsize; ++j) {
+        double* dst = acc + 12 * (int64_t)point_list[s + bstart + j];
+        for (int k = 0; k < 11; ++k) {
+          if (loc[j][k] == 0.0) continue;
+#pragma omp atomic
+          dst[k] += loc[j][k];
         }
       }
     }
