@@ -19,6 +19,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -32,6 +33,16 @@ GRAD2D_FLOATS = 12
 
 def _u8(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _carve(parts: dict, device):
+    """One device allocation split into 256-byte aligned byte views, one per named size."""
+    offs, total = {}, 0
+    for name, nbytes in parts.items():
+        offs[name] = total
+        total += (int(nbytes) + 255) & ~255
+    arena = torch.empty(max(total, 1), dtype=torch.uint8, device=device)
+    return arena, {name: arena[o:o + int(parts[name])] for name, o in offs.items()}
 
 
 @dataclass
@@ -236,27 +247,41 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
             counts_host.copy_(wave_counts, non_blocking=True)
             m_ready = torch.cuda.Event()
             m_ready.record()
+    # Everything whose size does not depend on the instance count is allocated while the copy
+    # and the depth sort run; after the count arrives the host only carves the count-sized
+    # buffers out of one allocation and launches the fill, before the depth sort ends.
+    ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
+    bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
+    backward_state = for_backward and _scores is None
+    n_contrib = tile_max = grad2d = image = final_T = None
+    if backward_state:
+        n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
+        tile_max = torch.empty(T, dtype=torch.int32, device=dev)
+        # the backward's screen gradients, zeroed by the forward blend's workgroups
+        grad2d = torch.empty(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+    if _scores is None:
+        image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
+        final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
     m = 0
     if m_ready is not None:
         m_ready.synchronize()
-        m = int(counts_host.sum(dtype=torch.int64))
+        m = int(counts_host.numpy().sum(dtype=np.int64))
         if m >= 1 << 32:
             raise _lib.AmdSplatError(f"{m} tile instances exceed the 32-bit instance index")
-    keys = torch.empty(m if keep_keys else 0, dtype=torch.int64, device=dev)
-    point_list = torch.empty(m, dtype=torch.int32, device=dev)
-    ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
-    bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
-    nb_max, bucket_to_tile, n_contrib, tile_max, ckpt, blist, grad2d = 0, None, None, None, None, None, None
-    if for_backward and _scores is None:
-        nb_max = (m + (BUCKET - 1) * T) // BUCKET  # >= sum over tiles of ceil(len / 32)
-        bucket_to_tile = torch.empty(max(nb_max, 1), dtype=torch.int32, device=dev)
-        n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
-        tile_max = torch.empty(T, dtype=torch.int32, device=dev)
-        ckpt = torch.empty(max(nb_max, 1), 256, 4, dtype=torch.float32, device=dev)
-        blist = torch.empty(4 + nb_max, dtype=torch.int32, device=dev)
-        # the backward's screen gradients, zeroed by the forward blend's workgroups
-        grad2d = torch.empty(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
-    ws = _u8(_lib.size_call("gs_bin_workspace_size", n, m, T), dev)
+    nb_max = (m + (BUCKET - 1) * T) // BUCKET if backward_state else 0  # >= sum over tiles of ceil(len / 32)
+    ws_bytes = _lib.size_call("gs_bin_workspace_size", n, m, T)
+    parts = {"point_list": 4 * m, "keys": 8 * m if keep_keys else 0, "ws": max(ws_bytes, 1)}
+    if backward_state:
+        parts.update(bucket_to_tile=4 * max(nb_max, 1), blist=4 * (4 + nb_max), ckpt=4096 * max(nb_max, 1))
+    arena, views = _carve(parts, dev)
+    point_list = views["point_list"].view(torch.int32)
+    keys = views["keys"].view(torch.int64) if keep_keys else torch.empty(0, dtype=torch.int64, device=dev)
+    ws = views["ws"]
+    bucket_to_tile = ckpt = blist = None
+    if backward_state:
+        bucket_to_tile = views["bucket_to_tile"].view(torch.int32)
+        blist = views["blist"].view(torch.int32)
+        ckpt = views["ckpt"].view(torch.float32).view(max(nb_max, 1), 256, 4)
     # the fill also clears the bucket list's header for the forward blend
     call("gs_bin_fill_3d", ptr(rec), ptr(dkeys), ptr(order), ptr(offsets), n, ccam, m,
          ptr(keys) if keep_keys else None, ptr(point_list), ptr(ranges), ptr(bucket_offsets), ptr(blist), ptr(ws),
@@ -268,8 +293,6 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges,
                             bucket_offsets, 0, None, None, None, None, None, None, None, tuple(bg),
                             {} if isinstance(timing, StageTimer) else tm.result())
-    image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
-    final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
     call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
          ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), ptr(blist), ptr(bucket_to_tile),
          ptr(grad2d), grad2d.numel() if grad2d is not None else 0,
@@ -357,6 +380,9 @@ class _Rasterize3D(torch.autograd.Function):
                           timing=timer if timer is not None else False)
         if _Rasterize3D.track_visibility:
             _Rasterize3D.last_visibility = fs.touched
+        # an output the loss does not use gets None, not a zero tensor: an alpha nobody
+        # differentiates costs the backward nothing
+        ctx.set_materialize_grads(False)
         ctx.fs = fs
         ctx.timer = timer
         ctx.dinfo = dinfo

@@ -40,36 +40,31 @@ struct ShOut {
 
 // rows x RW floats at blk (contiguous) -> LDS rows of pitch CP from column c0 (RW, CP fixed;
 // FULL rows, if not 0: the unrolled path for a whole pass, every load in flight before the
-// first store).
+// first store). Only the rows whose bit is set in `need` (bit r: row r) are read: the LDS rows
+// of the others keep whatever they held.
 template <int RW, int CP, int FULL>
-__device__ __forceinline__ void rows_to_lds(const float* __restrict__ blk, int nr, float* srow, int c0, int lane) {
+__device__ __forceinline__ void rows_to_lds(const float* __restrict__ blk, int nr, float* srow, int c0, int lane,
+                                            uint64_t need) {
   if constexpr (RW > 0) {
     constexpr int N4 = FULL * RW / 4;
-    if constexpr (FULL > 0 && (FULL * RW) % 4 == 0) {
+    if constexpr (FULL > 0 && (FULL * RW) % 4 == 0 && RW % 4 == 0) {
       if (nr == FULL && aligned16(blk)) {
         constexpr int IT = (N4 + 63) / 64;
         float4 v[IT];
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
           const int f4 = lane + 64 * it;
-          if (N4 % 64 == 0 || f4 < N4) v[it] = reinterpret_cast<const float4*>(blk)[f4];
+          if ((N4 % 64 == 0 || f4 < N4) && ((need >> (f4 / (RW / 4))) & 1u))
+            v[it] = reinterpret_cast<const float4*>(blk)[f4];
         }
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
           const int f4 = lane + 64 * it;
-          if (N4 % 64 == 0 || f4 < N4) {
-            if constexpr (RW % 4 == 0) {  // a float4 never crosses a row
-              const int row = f4 / (RW / 4), q = f4 - row * (RW / 4);
-              float* d = srow + row * CP + c0 + 4 * q;
-              d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
-            } else {
-              const float vv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int idx = 4 * f4 + e, row = idx / RW;
-                srow[row * CP + c0 + idx - row * RW] = vv[e];
-              }
-            }
+          if ((N4 % 64 == 0 || f4 < N4) && ((need >> (f4 / (RW / 4))) & 1u)) {
+            // a float4 never crosses a row
+            const int row = f4 / (RW / 4), q = f4 - row * (RW / 4);
+            float* d = srow + row * CP + c0 + 4 * q;
+            d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
           }
         }
         return;
@@ -79,6 +74,10 @@ __device__ __forceinline__ void rows_to_lds(const float* __restrict__ blk, int n
     if (aligned16(blk)) {
       const int n4 = total >> 2;
       for (int f4 = lane; f4 < n4; f4 += 64) {
+        // a float4 of rows not a multiple of 4 floats long can span two rows: read it if either
+        // is needed
+        const int r0 = (4 * f4) / RW, r1 = (4 * f4 + 3) / RW;
+        if ((((need >> r0) | (need >> r1)) & 1u) == 0u) continue;
         const float4 v = reinterpret_cast<const float4*>(blk)[f4];
         const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -89,12 +88,12 @@ __device__ __forceinline__ void rows_to_lds(const float* __restrict__ blk, int n
       }
       for (int idx = 4 * n4 + lane; idx < total; idx += 64) {
         const int row = idx / RW;
-        srow[row * CP + c0 + idx - row * RW] = blk[idx];
+        if ((need >> row) & 1u) srow[row * CP + c0 + idx - row * RW] = blk[idx];
       }
     } else {
       for (int idx = lane; idx < total; idx += 64) {
         const int row = idx / RW;
-        srow[row * CP + c0 + idx - row * RW] = blk[idx];
+        if ((need >> row) & 1u) srow[row * CP + c0 + idx - row * RW] = blk[idx];
       }
     }
   }
@@ -135,22 +134,25 @@ __device__ __forceinline__ void lds_to_rows(float* __restrict__ blk, int nr, con
 }
 
 // Copies rows [RH h, RH h + RH) of the wavefront's `rows` SH rows (the wavefront's first row is
-// `first`) into LDS rows of stride CP.
+// `first`) into LDS rows of stride CP; only the rows of the Gaussians set in `vmask` (bit l:
+// the wavefront's Gaussian l) are read from memory.
 template <int K>
-__device__ __forceinline__ void stage_sh(ShPtr src, int64_t first, int rows, int h, float* srow, int lane) {
+__device__ __forceinline__ void stage_sh(ShPtr src, int64_t first, int rows, int h, float* srow, int lane,
+                                         uint64_t vmask) {
   using St = ShStage<K>;
   constexpr int R = St::R, CP = St::CP, RH = St::RH;
   const int r0 = RH * h;
   const int nr = min(RH, rows - r0);
   if (nr <= 0) return;
   const int64_t row = first + r0;
+  const uint64_t need = vmask >> r0;
   if (src.b == nullptr) {
-    rows_to_lds<R, CP, RH>(src.a + row * R, nr, srow, 0, lane);
+    rows_to_lds<R, CP, RH>(src.a + row * R, nr, srow, 0, lane, need);
   } else {
     // (the split layout takes the plain loop: an unrolled one for rows not a multiple of four
     // floats costs the kernel registers, i.e. occupancy, on the single-array path too)
-    rows_to_lds<3, CP, 0>(src.a + row * 3, nr, srow, 0, lane);
-    rows_to_lds<R - 3, CP, 0>(src.b + row * (R - 3), nr, srow, 3, lane);
+    rows_to_lds<3, CP, 0>(src.a + row * 3, nr, srow, 0, lane, need);
+    rows_to_lds<R - 3, CP, 0>(src.b + row * (R - 3), nr, srow, 3, lane, need);
   }
 }
 
@@ -357,7 +359,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 #pragma unroll
     for (int h = 0; h < St::NH; ++h) {
       if (h) wave_sync();  // every lane is done with the previous rows
-      stage_sh<K>(sh, wave_first, rows, h, srow, lane);
+      stage_sh<K>(sh, wave_first, rows, h, srow, lane, vmask);
       wave_sync();
       if (g.vis && lane / St::RH == h) {
         const float* row = srow + (lane - St::RH * h) * St::CP;
@@ -466,7 +468,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   for (int h = 0; h < St::NH; ++h) {
     if (vmask != 0) {
       if (h) wave_sync();  // the previous rows are written out
-      stage_sh<K>(sh, wave_first, rows, h, srow, lane);
+      // (rows of culled Gaussians are not read: their lanes write zeros over them below)
+      stage_sh<K>(sh, wave_first, rows, h, srow, lane, vmask);
       wave_sync();
       if (lane / St::RH == h) {
         float* row = srow + (lane - St::RH * h) * St::CP;
