@@ -973,14 +973,66 @@ static int bits_for(int64_t n_values) {
   return b;
 }
 
-// Workspace of the depth ordering (keys, sorted keys, float64 high keys, temporary values,
-// sort and scan scratch) and of the emission (tile keys and values, sorted tile keys, sort
-// scratch, window starts).
-static size_t prep_ws(int64_t n) { return align_up(n * 4) * 4 + sort_ws(n) + scan_ws(n); }
+// Workspace layouts, as byte offsets from the start of the workspace. The size functions
+// below return a layout's `end`, and the code that carves a workspace takes its regions from
+// the same layout, so the two cannot disagree.
+//
+// Depth ordering: keys, sorted keys, float64 high keys (then the counts in depth order),
+// temporary values, sort scratch, scan scratch.
+struct PrepLayout {
+  size_t dkeys, dsorted, khi, tmpv, sort, scan, end;
+};
 
-static size_t emit_ws(int64_t m) {
-  return align_up(m * 4) * 3 + sort_ws(m) + align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);
+static PrepLayout prep_layout(int64_t n) {
+  PrepLayout L;
+  size_t o = 0;
+  L.dkeys = o; o += align_up(n * 4);
+  L.dsorted = o; o += align_up(n * 4);
+  L.khi = o; o += align_up(n * 4);
+  L.tmpv = o; o += align_up(n * 4);
+  L.sort = o; o += sort_ws(n);
+  L.scan = o; o += scan_ws(n);
+  L.end = o;
+  return L;
 }
+
+// Emission and tile sort: tile keys and values, sorted tile keys, sort scratch, window starts.
+struct EmitLayout {
+  size_t tkeys, tvals, tsorted, sort, wstart, end;
+  int tile_bits;
+};
+
+static EmitLayout emit_layout(int64_t m, int n_tiles) {
+  EmitLayout L;
+  L.tile_bits = bits_for(n_tiles);
+  size_t o = 0;
+  L.tkeys = o; o += align_up(m * 4);
+  L.tvals = o; o += align_up(m * 4);
+  L.tsorted = o; o += align_up(m * 4);
+  L.sort = o; o += sort_ws(m);
+  L.wstart = o; o += align_up(static_cast<size_t>((m + kEmitSpan - 1) / kEmitSpan + 1) * 4);
+  L.end = o;
+  return L;
+}
+
+// Rectangle binning: the depth ordering, the order and offsets, then the emission.
+struct RectLayout {
+  size_t prep, order, offs, emit, end;
+};
+
+static RectLayout rect_layout(int64_t n, int64_t m, int n_tiles) {
+  RectLayout L;
+  size_t o = 0;
+  L.prep = o; o += prep_layout(n).end;
+  L.order = o; o += align_up(n * 4);
+  L.offs = o; o += align_up((n + 1) * 4);
+  L.emit = o; o += emit_layout(m, n_tiles).end;
+  L.end = o;
+  return L;
+}
+
+static size_t prep_ws(int64_t n) { return prep_layout(n).end; }
+static size_t emit_ws(int64_t m, int n_tiles) { return emit_layout(m, n_tiles).end; }
 
 // Stable order of the Gaussians by depth key (keys_in: precomputed 32-bit keys, else computed
 // from rec / depth / depth64; none of them: index order) and, if offsets is not NULL, the
@@ -988,12 +1040,13 @@ static size_t emit_ws(int64_t m) {
 static void bin_prepare(const SplatRec* rec, const float* depth, const double* depth64, const uint32_t* keys_in,
                         int key_bits, const uint32_t* counts, int64_t n, uint32_t* order, uint32_t* offsets,
                         char* ws, hipStream_t st) {
-  uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* dsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* khi = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* tmpv = reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  char* sort_scratch = ws; ws += sort_ws(n);
-  char* scan_scratch = ws;
+  const PrepLayout L = prep_layout(n);
+  uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws + L.dkeys);
+  uint32_t* dsorted = reinterpret_cast<uint32_t*>(ws + L.dsorted);
+  uint32_t* khi = reinterpret_cast<uint32_t*>(ws + L.khi);
+  uint32_t* tmpv = reinterpret_cast<uint32_t*>(ws + L.tmpv);
+  char* sort_scratch = ws + L.sort;
+  char* scan_scratch = ws + L.scan;
   if (n <= 0) {
     if (offsets) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, offsets, int64_t(1), 0u);
     return;
@@ -1034,18 +1087,20 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
                      const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
                      uint32_t* bucket_offsets, uint32_t* list_header, char* ws, hipStream_t st) {
-  uint32_t* tkeys = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
-  uint32_t* tvals = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
-  uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws); ws += align_up(m * 4);
-  char* sort_scratch = ws; ws += sort_ws(m);
-  uint32_t* wstart = reinterpret_cast<uint32_t*>(ws);
+  const EmitLayout L = emit_layout(m, n_tiles);
+  uint32_t* tkeys = reinterpret_cast<uint32_t*>(ws + L.tkeys);
+  uint32_t* tvals = reinterpret_cast<uint32_t*>(ws + L.tvals);
+  uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws + L.tsorted);
+  const int tile_bits = L.tile_bits;
+  char* sort_scratch = ws + L.sort;
+  uint32_t* wstart = reinterpret_cast<uint32_t*>(ws + L.wstart);
   if (m > 0) {
     const int64_t n_windows = (m + kEmitSpan - 1) / kEmitSpan;
     hipLaunchKernelGGL(emit_windows_kernel, dim3(grid_for(n + 1, 256)), dim3(256), 0, st, offsets, n, n_windows,
                        wstart);
     // with at least one sort pass, the last pass takes the tile ranges (preset by the emission)
     // and the sorted keys are written only if the caller wants them
-    const bool sort_ranges = bits_for(n_tiles) > 0;
+    const bool sort_ranges = tile_bits > 0;
     uint32_t* preset = sort_ranges ? ranges : nullptr;
     if (rects) {
       hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
@@ -1054,7 +1109,7 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
       hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
                          offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
     }
-    radix_sort(tkeys, tvals, tsorted, point_list, m, bits_for(n_tiles), sort_scratch, st, nullptr, nullptr, preset,
+    radix_sort(tkeys, tvals, tsorted, point_list, m, tile_bits, sort_scratch, st, nullptr, nullptr, preset,
                sort_ranges && !sorted_keys);
     if (sorted_keys)
       hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
@@ -1113,11 +1168,11 @@ extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_t
 }
 
 extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles) {
-  (void)n_tiles;
   n = n < 0 ? 0 : n;
+  n_tiles = n_tiles < 1 ? 1 : n_tiles;
   m = m < 0 ? 0 : m;
   // the rectangle binning runs the depth ordering itself: its scratch, order and offsets too
-  return prep_ws(n) + align_up(n * 4) + align_up((n + 1) * 4) + emit_ws(m);
+  return rect_layout(n, m, n_tiles).end;
 }
 
 extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
@@ -1133,7 +1188,7 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   const CamK k = make_cam(*cam);
   GS_REQUIRE(static_cast<int64_t>(k.tiles_x) * k.tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
   const int n_tiles = k.tiles_x * k.tiles_y;
-  const size_t need = emit_ws(m);
+  const size_t need = emit_ws(m, n_tiles);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
   GS_REQUIRE(m == 0 || (splat_rec && order && offsets && point_list), GS_ERR_ARG, "null pointer argument");
@@ -1181,17 +1236,18 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   const double* d64 = depth_dtype == GS_FLOAT64 ? static_cast<const double*>(depth) : nullptr;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
-  uint32_t* dkeys = reinterpret_cast<uint32_t*>(ws);  // first region of the depth-ordering scratch
-  char* prep = ws; ws += prep_ws(n);
-  uint32_t* ord = order ? order : reinterpret_cast<uint32_t*>(ws); ws += align_up(n * 4);
-  uint32_t* offs = reinterpret_cast<uint32_t*>(ws); ws += align_up((n + 1) * 4);
+  const RectLayout L = rect_layout(n, m, n_tiles);
+  char* prep = ws + L.prep;
+  uint32_t* dkeys = reinterpret_cast<uint32_t*>(prep + prep_layout(n).dkeys);
+  uint32_t* ord = order ? order : reinterpret_cast<uint32_t*>(ws + L.order);
+  uint32_t* offs = reinterpret_cast<uint32_t*>(ws + L.offs);
   if (n > 0 && (m > 0 || order)) {
     bin_prepare(nullptr, d32, d64, nullptr, 32, counts, n, ord, m > 0 ? offs : nullptr, prep, st);
     if (sorted_keys && m > 0 && !d32)  // index order: the depth part of the keys is 0
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
   }
   bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, n_tiles, m, sorted_keys,
-           point_list, ranges, tile_offsets, bucket_offsets, nullptr, ws, st);
+           point_list, ranges, tile_offsets, bucket_offsets, nullptr, ws + L.emit, st);
   return check_launch("bin_fill_rect");
 }
 

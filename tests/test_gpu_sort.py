@@ -1,0 +1,116 @@
+"""GPU checks of the radix sorts behind the binning, against what the definition of a stable
+sort fixes: numpy's stable argsort of the same keys, and the exclusive scan of the counts in
+that order. No oracle is involved; the inputs are chosen to reach every sort configuration
+(1 to 4 passes, 4 / 8 / 16 rounds per tile, one tile up to thousands of tiles, keys that are
+all equal or all distinct) and the tile sort's ranges on canvases with up to 16384 tiles (the
+14-bit tile sort, whose scratch the workspace size must cover).
+"""
+import numpy as np
+import pytest
+import torch
+
+from amdsplat import _lib
+from amdsplat import raster2d as R2
+from amdsplat._lib import call, ptr
+
+pytestmark = pytest.mark.gpu
+
+NEAR, FAR = 0.01, 100.0
+
+
+def host_order_key(v: float) -> int:
+    u = int(np.float32(v).view(np.uint32))
+    return (~u & 0xFFFFFFFF) if u & 0x80000000 else (u | 0x80000000)
+
+
+DKEY_CULL = host_order_key(FAR) - host_order_key(NEAR)  # 27 bits for near/far = 0.01 / 100
+
+
+def camera(W=640, H=480):
+    return _lib.make_camera(np.eye(4, dtype=np.float32), 500.0, 500.0, W / 2, H / 2, W, H, NEAR, FAR)
+
+
+def depth_keys(n, kind, rng):
+    if kind == "distinct":
+        k = rng.integers(1, DKEY_CULL, n, dtype=np.int64)
+    elif kind == "few_values":
+        k = rng.choice(rng.integers(1, DKEY_CULL, 37, dtype=np.int64), n)
+    elif kind == "culled_mix":  # a third culled (the largest key), the rest spread
+        k = rng.integers(1, DKEY_CULL, n, dtype=np.int64)
+        k[rng.random(n) < 0.33] = DKEY_CULL
+    else:  # "equal"
+        k = np.full(n, 12345, np.int64)
+    return k.astype(np.uint32)
+
+
+@pytest.mark.parametrize("n", [1, 63, 4097, 100_003, 1_000_000, 9_000_001])
+@pytest.mark.parametrize("kind", ["distinct", "few_values", "culled_mix", "equal"])
+def test_depth_order_is_the_stable_argsort(n, kind):
+    rng = np.random.default_rng(n + len(kind))
+    keys = depth_keys(n, kind, rng)
+    counts = rng.integers(0, 9, n).astype(np.uint32)
+    dev = torch.device("cuda")
+    kd = torch.from_numpy(keys.view(np.int32)).to(dev)
+    cd = torch.from_numpy(counts.view(np.int32)).to(dev)
+    order = torch.empty(n, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(_lib.size_call("gs_bin_prepare_workspace_size", n), 1), dtype=torch.uint8, device=dev)
+    cam = camera()
+    call("gs_bin_prepare_3d", None, ptr(cd), ptr(kd), n, cam, ptr(order), ptr(offsets), ptr(ws), ws.numel(),
+         _lib.stream_handle(dev))
+    want = np.argsort(keys, kind="stable")
+    assert np.array_equal(order.cpu().numpy(), want)
+    scan = np.zeros(n + 1, np.int64)
+    np.cumsum(counts[want], out=scan[1:])
+    assert np.array_equal(offsets.cpu().numpy().astype(np.int64), scan)
+
+
+def numpy_rect_binning(rects, depth, tiles_x, T):
+    """Lists of a stable depth order, instances emitted row-major per rectangle, then stably
+    sorted by tile; ranges and 32-entry bucket offsets."""
+    order = np.argsort(depth, kind="stable")
+    r = rects[order].astype(np.int64)
+    w, h = r[:, 2] - r[:, 0], r[:, 3] - r[:, 1]
+    cnt = np.where((w > 0) & (h > 0), w * h, 0)
+    m = int(cnt.sum())
+    g = np.repeat(np.arange(len(order)), cnt)
+    start = np.zeros(len(order), np.int64)
+    np.cumsum(cnt[:-1], out=start[1:])
+    local = np.arange(m) - start[g]
+    tile = (r[g, 1] + local // w[g]) * tiles_x + r[g, 0] + local % w[g]
+    srt = np.argsort(tile, kind="stable")
+    point_list = order[g[srt]].astype(np.int32)
+    per_tile = np.bincount(tile, minlength=T)
+    begin = np.zeros(T + 1, np.int64)
+    np.cumsum(per_tile, out=begin[1:])
+    ranges = np.stack([begin[:-1], begin[1:]], 1)
+    boff = np.zeros(T + 1, np.int64)
+    np.cumsum((per_tile + 31) // 32, out=boff[1:])
+    return point_list, ranges, boff
+
+
+@pytest.mark.parametrize("W,H,n,rmax", [
+    (333, 250, 5_000, 5),           # 336 tiles: 9 bits, one pass
+    (1297, 840, 400_000, 5),        # 4346 tiles: 13 bits in two passes of 7
+    (2048, 2048, 200_000, 16),      # 16384 tiles: 14 bits, ~10M instances, 16 rounds per tile
+])
+def test_rect_binning_matches_the_stable_sort(W, H, n, rmax):
+    rng = np.random.default_rng(W * H + n)
+    tiles_x, tiles_y = (W + 15) // 16, (H + 15) // 16
+    T = tiles_x * tiles_y
+    x0 = rng.integers(-2, tiles_x, n)
+    y0 = rng.integers(-2, tiles_y, n)
+    rects = np.stack([x0, y0, x0 + rng.integers(0, rmax, n), y0 + rng.integers(0, rmax, n)], 1).astype(np.int32)
+    rects[:, 2:] = np.minimum(rects[:, 2:], [tiles_x, tiles_y])
+    rects[:, :2] = np.maximum(rects[:, :2], 0)
+    depth = rng.choice(rng.random(n // 3 + 1).astype(np.float32), n)  # ties in depth
+    dev = torch.device("cuda")
+    rd = torch.from_numpy(rects).to(dev).contiguous()
+    counts = torch.empty(n, dtype=torch.int32, device=dev)
+    call("gs_rect_counts", ptr(rd), n, tiles_x, tiles_y, ptr(counts), _lib.stream_handle(dev))
+    rb = R2.bin_rects(rd, counts, torch.from_numpy(depth).to(dev), W, H)
+    pl, ranges, boff = numpy_rect_binning(rects, depth, tiles_x, T)
+    assert len(pl) == rb.point_list.numel()
+    assert np.array_equal(rb.point_list.cpu().numpy(), pl)
+    assert np.array_equal(rb.ranges.cpu().numpy().astype(np.int64), ranges)
+    assert np.array_equal(rb.bucket_offsets.cpu().numpy().astype(np.int64), boff)
