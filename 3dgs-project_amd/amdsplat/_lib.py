@@ -68,6 +68,7 @@ _SIGS = {
     "gs_grad2d_floats": (_i32, []),
     "gs_scan_workspace_size": (_sz, [_i64]),
     "gs_scan_u32": (_i32, [_vp, _vp, _i64, _vp, _sz, _vp]),
+    "gs_sum_u32": (_i32, [_vp, _i64, _vp, _vp]),
     "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
                                  _vp, _vp, _vp]),
     "gs_bin_prepare_workspace_size": (_sz, [_i64]),

@@ -19,7 +19,6 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass, field
 
-import numpy as np
 import torch
 
 from . import _lib
@@ -35,14 +34,13 @@ def _u8(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def _carve(parts: dict, device):
-    """One device allocation split into 256-byte aligned byte views, one per named size."""
+def _layout(parts: dict):
+    """Byte offsets (256-byte aligned) of named regions of one allocation, and its size."""
     offs, total = {}, 0
     for name, nbytes in parts.items():
         offs[name] = total
         total += (int(nbytes) + 255) & ~255
-    arena = torch.empty(max(total, 1), dtype=torch.uint8, device=device)
-    return arena, {name: arena[o:o + int(parts[name])] for name, o in offs.items()}
+    return offs, max(total, 1)
 
 
 @dataclass
@@ -224,8 +222,9 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
          n, K, sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), ptr(wave_counts), st)
     tm.mark("preprocess")
     # The instance count m (the total of the per-wavefront tile counts) needs only the
-    # preprocess: a side stream copies the counts to host memory while the depth sort runs on
-    # this stream, so the host sizes the fill's buffers without the stream draining first.
+    # preprocess: a side stream sums the counts and copies the total to host memory while the
+    # depth sort runs on this stream, so the host sizes the fill's buffers without the stream
+    # draining first.
     # (The host enqueues the depth sort before it sets up the copy, so the sort follows the
     # preprocess without a gap.)
     side = _side_stream(dev) if n > 0 else None
@@ -241,10 +240,13 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     tm.mark("depth_order")
     m_ready = None
     if side is not None:
+        total_dev = torch.empty(1, dtype=torch.int64, device=dev)
         wave_counts.record_stream(side)
-        counts_host = torch.empty(n_waves, dtype=torch.int32, pin_memory=True)
+        total_dev.record_stream(side)
+        total_host = torch.empty(1, dtype=torch.int64, pin_memory=True)
         with torch.cuda.stream(side):
-            counts_host.copy_(wave_counts, non_blocking=True)
+            call("gs_sum_u32", ptr(wave_counts), n_waves, ptr(total_dev), side.cuda_stream)
+            total_host.copy_(total_dev, non_blocking=True)
             m_ready = torch.cuda.Event()
             m_ready.record()
     # Everything whose size does not depend on the instance count is allocated while the copy
@@ -262,41 +264,54 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     if _scores is None:
         image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
         final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
+    # addresses the calls after the readback take (ctypes conversions done before the wait)
+    p_rec, p_dkeys, p_order, p_offsets = ptr(rec), ptr(dkeys), ptr(order), ptr(offsets)
+    p_ranges, p_boff, bg3 = ptr(ranges), ptr(bucket_offsets), _lib.float3(bg)
     m = 0
     if m_ready is not None:
         m_ready.synchronize()
-        m = int(counts_host.numpy().sum(dtype=np.int64))
+        m = int(total_host.numpy()[0])
         if m >= 1 << 32:
             raise _lib.AmdSplatError(f"{m} tile instances exceed the 32-bit instance index")
     nb_max = (m + (BUCKET - 1) * T) // BUCKET if backward_state else 0  # >= sum over tiles of ceil(len / 32)
-    ws_bytes = _lib.size_call("gs_bin_workspace_size", n, m, T)
-    parts = {"point_list": 4 * m, "keys": 8 * m if keep_keys else 0, "ws": max(ws_bytes, 1)}
+    ws_bytes = max(_lib.size_call("gs_bin_workspace_size", n, m, T), 1)
+    parts = {"point_list": 4 * m, "keys": 8 * m if keep_keys else 0, "ws": ws_bytes}
     if backward_state:
         parts.update(bucket_to_tile=4 * max(nb_max, 1), blist=4 * (4 + nb_max), ckpt=4096 * max(nb_max, 1))
-    arena, views = _carve(parts, dev)
-    point_list = views["point_list"].view(torch.int32)
-    keys = views["keys"].view(torch.int64) if keep_keys else torch.empty(0, dtype=torch.int64, device=dev)
-    ws = views["ws"]
-    bucket_to_tile = ckpt = blist = None
-    if backward_state:
-        bucket_to_tile = views["bucket_to_tile"].view(torch.int32)
-        blist = views["blist"].view(torch.int32)
-        ckpt = views["ckpt"].view(torch.float32).view(max(nb_max, 1), 256, 4)
+    offs, total = _layout(parts)
+    arena = torch.empty(total, dtype=torch.uint8, device=dev)
+    # the kernels are launched from raw addresses; the tensor views are made after the launches,
+    # so that the host reaches the fill while the depth sort still runs
+    base = arena.data_ptr()
+    adr = {k: (base + o if parts[k] > 0 else None) for k, o in offs.items()}
     # the fill also clears the bucket list's header for the forward blend
-    call("gs_bin_fill_3d", ptr(rec), ptr(dkeys), ptr(order), ptr(offsets), n, ccam, m,
-         ptr(keys) if keep_keys else None, ptr(point_list), ptr(ranges), ptr(bucket_offsets), ptr(blist), ptr(ws),
-         ws.numel(), st)
+    call("gs_bin_fill_3d", p_rec, p_dkeys, p_order, p_offsets, n, ccam, m, adr["keys"], adr["point_list"], p_ranges,
+         p_boff, adr.get("blist"), adr["ws"], ws_bytes, st)
     tm.mark("binning")
-    if _scores is not None:  # pruning scores: the blend's weights, no image
-        call("gs_blend_scores_3d", ptr(rec), ptr(ranges), ptr(point_list), W, H, n, ptr(_scores), st)
+    if _scores is None:
+        call("gs_blend_fwd_3d", p_rec, p_ranges, adr["point_list"], p_boff, W, H, bg3, ptr(image), ptr(final_T),
+             ptr(n_contrib), ptr(tile_max), adr.get("ckpt"), adr.get("blist"), adr.get("bucket_to_tile"),
+             ptr(grad2d), grad2d.numel() if grad2d is not None else 0,
+             _lib.GS_BLEND_LIST_CLEARED if backward_state else 0, st)
+    else:  # pruning scores: the blend's weights, no image
+        call("gs_blend_scores_3d", p_rec, p_ranges, adr["point_list"], W, H, n, ptr(_scores), st)
+
+    def view(name, dtype):
+        o = offs[name]
+        return arena[o:o + parts[name]].view(dtype)
+
+    point_list = view("point_list", torch.int32)
+    keys = view("keys", torch.int64) if keep_keys else torch.empty(0, dtype=torch.int64, device=dev)
+    if _scores is not None:
         tm.mark("scores")
         return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges,
                             bucket_offsets, 0, None, None, None, None, None, None, None, tuple(bg),
                             {} if isinstance(timing, StageTimer) else tm.result())
-    call("gs_blend_fwd_3d", ptr(rec), ptr(ranges), ptr(point_list), ptr(bucket_offsets), W, H, _lib.float3(bg),
-         ptr(image), ptr(final_T), ptr(n_contrib), ptr(tile_max), ptr(ckpt), ptr(blist), ptr(bucket_to_tile),
-         ptr(grad2d), grad2d.numel() if grad2d is not None else 0,
-         _lib.GS_BLEND_LIST_CLEARED if blist is not None else 0, st)
+    bucket_to_tile = ckpt = blist = None
+    if backward_state:
+        bucket_to_tile = view("bucket_to_tile", torch.int32)
+        blist = view("blist", torch.int32)
+        ckpt = view("ckpt", torch.float32).view(max(nb_max, 1), 256, 4)
     tm.mark("blend_fwd")
     return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges, bucket_offsets,
                         nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist, tuple(bg),

@@ -155,6 +155,29 @@ __global__ __launch_bounds__(kScanThreads) void scan_add_kernel(uint32_t* __rest
   if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = offs[n_blocks];
 }
 
+// out[0] = sum of in[0..n) as a uint64: one workgroup of 1024 threads, 16-byte loads.
+constexpr int kSumThreads = 1024;
+
+__global__ __launch_bounds__(kSumThreads) void sum_u32_kernel(const uint32_t* __restrict__ in, int64_t n,
+                                                              unsigned long long* __restrict__ out) {
+  __shared__ unsigned long long s_w[kSumThreads / kWave];
+  unsigned long long s = 0;
+  const int64_t n4 = aligned16(in) ? n / 4 : 0;
+  for (int64_t i = threadIdx.x; i < n4; i += kSumThreads) {
+    const uint4 v = reinterpret_cast<const uint4*>(in)[i];
+    s += static_cast<unsigned long long>(v.x) + v.y + v.z + v.w;
+  }
+  for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += kSumThreads) s += in[i];
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long t = 0;
+    for (int w = 0; w < kSumThreads / kWave; ++w) t += s_w[w];
+    out[0] = t;
+  }
+}
+
 static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 static size_t scan_ws(int64_t n) {
@@ -1145,6 +1168,15 @@ extern "C" int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* w
   }
   scan_rec(in, out, n, static_cast<char*>(workspace), st);
   return check_launch("scan");
+}
+
+extern "C" int gs_sum_u32(const uint32_t* in, int64_t n, uint64_t* out, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0 && out && (n == 0 || in), GS_ERR_ARG, "invalid sum arguments");
+  GS_REQUIRE(aligned(in, 4) && aligned(out, 8), GS_ERR_ALIGN, "sum: 4-byte aligned input, 8-byte aligned output");
+  hipLaunchKernelGGL(sum_u32_kernel, dim3(1), dim3(kSumThreads), 0, as_stream(stream), in, n,
+                     reinterpret_cast<unsigned long long*>(out));
+  return check_launch("sum_u32");
 }
 
 extern "C" size_t gs_bin_prepare_workspace_size(int64_t n) { return prep_ws(n < 0 ? 0 : n); }

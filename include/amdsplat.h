@@ -78,6 +78,11 @@ size_t gs_scan_workspace_size(int64_t n);
 int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* out[0] = in[0] + ... + in[n-1] as a uint64 (one workgroup, no workspace). With the
+ * preprocess's wave_counts it gives the instance count m as one value to copy to the host
+ * (Faster-GS reads the count back after its scan, phase2/fastergs_readback.patch:46-85). */
+int gs_sum_u32(const uint32_t* in, int64_t n, uint64_t* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * 3D preprocess forward (replaces Faster-GS preprocess_cu; signature evidence
  * results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:7). Per Gaussian: view

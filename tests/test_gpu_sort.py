@@ -114,3 +114,16 @@ def test_rect_binning_matches_the_stable_sort(W, H, n, rmax):
     assert np.array_equal(rb.point_list.cpu().numpy(), pl)
     assert np.array_equal(rb.ranges.cpu().numpy().astype(np.int64), ranges)
     assert np.array_equal(rb.bucket_offsets.cpu().numpy().astype(np.int64), boff)
+
+
+@pytest.mark.parametrize("n,offset", [(0, 0), (1, 0), (3, 1), (4097, 0), (1_000_003, 1), (15_625, 0)])
+def test_sum_u32(n, offset):
+    """gs_sum_u32 (the instance count of the 3D forward) against numpy's uint64 sum, over values up to
+    2^31 (the total exceeds 32 bits) and at an input that is not 16-byte aligned."""
+    rng = np.random.default_rng(n)
+    vals = rng.integers(0, 1 << 31, n + offset, dtype=np.int64).astype(np.uint32)
+    dev = torch.device("cuda")
+    d = torch.from_numpy(vals.view(np.int32)).to(dev)
+    out = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    call("gs_sum_u32", d.data_ptr() + 4 * offset, n, ptr(out), _lib.stream_handle(dev))
+    assert int(out.item()) == int(vals[offset:].astype(np.uint64).sum())
