@@ -57,7 +57,10 @@ class _Rasterize(torch.autograd.Function):
         ctx.buffers = (pb, tb, ib, bb)
         ctx.buffer_state = (n_inst, n_buckets, sel)
         ctx.save_for_backward(image, means, scales, rotations, opacities, sh_coefficients_rest)
-        return image
+        # a new tensor object over the image's storage: the primitive buffers on ctx hold the
+        # forward state and its image, and returning that same object would make a reference cycle
+        # (output -> grad_fn -> ctx -> buffers -> output) that only the cyclic collector frees
+        return image.detach()
 
     @staticmethod
     def backward(ctx: Any, grad_image):

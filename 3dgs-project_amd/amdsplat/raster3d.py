@@ -393,8 +393,6 @@ class _Rasterize3D(torch.autograd.Function):
         shp = sh if sh_rest is None else (sh, sh_rest)
         fs = forward_pass(means, log_scales, quats, opacity_logits, shp, cam, sh_degree, bg,
                           timing=timer if timer is not None else False)
-        if _Rasterize3D.track_visibility:
-            _Rasterize3D.last_visibility = fs.touched
         # an output the loss does not use gets None, not a zero tensor: an alpha nobody
         # differentiates costs the backward nothing
         ctx.set_materialize_grads(False)
@@ -406,8 +404,15 @@ class _Rasterize3D(torch.autograd.Function):
         alpha = 1.0 - fs.final_T
         n_buckets = fs.bucket_offsets[-1]
         m = torch.tensor(fs.m, dtype=torch.int64)  # host tensor: the count is already on the host
-        ctx.mark_non_differentiable(fs.touched, n_buckets, m)
-        return fs.image, alpha, fs.touched, n_buckets, m
+        # The outputs are new tensor objects over the forward state's storage: were they the
+        # state's own objects, output -> grad_fn -> ctx -> state -> output would be a reference
+        # cycle, and each view's buffers (about 1 GB at 1M Gaussians) would wait for Python's
+        # cyclic garbage collector instead of being freed when the output is.
+        image, touched = fs.image.detach(), fs.touched.detach()
+        if _Rasterize3D.track_visibility:
+            _Rasterize3D.last_visibility = touched
+        ctx.mark_non_differentiable(touched, n_buckets, m)
+        return image, alpha, touched, n_buckets, m
 
     @staticmethod
     def backward(ctx, grad_image, grad_alpha, _grad_touched, _grad_nb, _grad_m):

@@ -45,27 +45,27 @@ __global__ __launch_bounds__(kProbeThreads) void probe_read_kernel(const float4*
   if ((threadIdx.x & 63) == 0) sums[static_cast<int64_t>(blockIdx.x) * (kProbeThreads / 64) + (threadIdx.x >> 6)] = s;
 }
 
-// 8 independent FMA chains of `iters` steps per thread (8 * iters wave64 v_fma_f32 per wavefront,
-// plus a few instructions of set-up and loop control), one float written per thread.
+// 16 independent FMA chains of `iters` x 4 steps per thread (64 iters wave64 v_fma_f32 per
+// wavefront, plus a few instructions of set-up and loop control), one float written per thread.
+// The library is built without packed FP32, so this is the FP32 VALU ceiling its kernels face.
+constexpr int kFmaChains = 16;
+
 __global__ __launch_bounds__(kProbeThreads) void probe_fma_kernel(float* __restrict__ out, int iters, float a,
                                                                   float b) {
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kProbeThreads + threadIdx.x;
-  float x0 = static_cast<float>(threadIdx.x) * 1e-7f, x1 = x0 + 1e-3f, x2 = x0 + 2e-3f, x3 = x0 + 3e-3f;
-  float x4 = x0 + 4e-3f, x5 = x0 + 5e-3f, x6 = x0 + 6e-3f, x7 = x0 + 7e-3f;
+  float x[kFmaChains];
+#pragma unroll
+  for (int c = 0; c < kFmaChains; ++c) x[c] = static_cast<float>(threadIdx.x) * 1e-7f + 1e-3f * c;
   for (int k = 0; k < iters; ++k) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      x0 = fmaf(x0, a, b);
-      x1 = fmaf(x1, a, b);
-      x2 = fmaf(x2, a, b);
-      x3 = fmaf(x3, a, b);
-      x4 = fmaf(x4, a, b);
-      x5 = fmaf(x5, a, b);
-      x6 = fmaf(x6, a, b);
-      x7 = fmaf(x7, a, b);
-    }
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int c = 0; c < kFmaChains; ++c) x[c] = fmaf(x[c], a, b);
   }
-  out[tid] = ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7));
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kFmaChains; ++c) s += x[c];
+  out[tid] = s;
 }
 
 }  // namespace gs

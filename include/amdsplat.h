@@ -369,8 +369,8 @@ int gs_l1_ssim_bwd(const float* image, const float* target, const float* dmap, i
  *   gs_probe_read   reads n floats (n a multiple of 4, 16-byte aligned) once and writes
  *                   gs_probe_read_sums(n) partial sums (one per wavefront; that many floats
  *                   in `sums`)
- *   gs_probe_fma    `threads` threads (a multiple of 256) each run 32 * iters dependent-free
- *                   FP32 FMAs (8 chains) and write one float to out[threads]
+ *   gs_probe_fma    `threads` threads (a multiple of 256) each run 64 * iters dependent-free
+ *                   FP32 FMAs (16 chains) and write one float to out[threads]
  * ------------------------------------------------------------------------------------- */
 int gs_probe_copy(const float* in, float* out, int64_t n, void* stream);
 int64_t gs_probe_read_sums(int64_t n);

@@ -236,3 +236,45 @@ def test_visibility_export_from_a_real_forward():
     assert bool((vmask[gnz] > 0).all())
     assert int((vmask > 0).sum()) > 0 and int((vmask == 0).sum()) > 0
     assert np.all(shr.grad.cpu().numpy() == 0)  # active_sh_bases 1: no gradient above degree 0
+
+
+@gpu
+@pytest.mark.parametrize("surface", ["rasterize", "diff_rasterize"])
+def test_step_state_is_freed_without_the_cyclic_collector(surface):
+    """The forward state a differentiable call keeps for its backward (lists, checkpoints, records)
+    is freed as soon as the caller drops the output, with Python's cyclic garbage collector off: no
+    reference cycle runs through the autograd context."""
+    import gc
+
+    sc = scenes.small_scene(20_000, 333, 250, seed=5, sh_coeffs=16)
+    cam = sc.cameras[0]
+    leaves = [t.cuda().contiguous().requires_grad_(True) for t in faster_gs_params(sc)]
+    st = settings_of(cam)
+
+    def step():
+        if surface == "rasterize":
+            m, ls, q, op, sh0, shr = leaves
+            img, _, aux = rasterize(m, ls, q, op, (sh0, shr), cam.viewmat, K_of(cam), cam.width, cam.height,
+                                    near=cam.near, far=cam.far)
+            del aux
+        else:
+            img = diff_rasterize(*leaves, torch.empty(0, device="cuda"), st)
+        img.sum().backward()
+
+    gc.collect()
+    step()  # first call: workspace and allocator warm-up
+    torch.cuda.synchronize()
+    gc.disable()
+    try:
+        base = torch.cuda.memory_allocated()
+        for _ in range(4):
+            for t in leaves:
+                t.grad = None
+            step()
+        for t in leaves:
+            t.grad = None
+        torch.cuda.synchronize()
+        grown = torch.cuda.memory_allocated() - base
+    finally:
+        gc.enable()
+    assert grown <= 0, f"{grown} bytes still held after 4 steps"
