@@ -161,10 +161,19 @@ def ptr(t) -> int | None:
 
 
 def stream_handle(device=None) -> int | None:
+    """The current HIP stream of `device` (a torch.device, an index or None for the current
+    device) as an integer, None for the null stream."""
     import torch
 
-    s = torch.cuda.current_stream(device)
-    return s.cuda_stream or None
+    if isinstance(device, torch.device):
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+    elif isinstance(device, int):
+        idx = device
+    else:
+        idx = torch.cuda.current_device()
+    # the raw handle straight from the stream registry (torch.cuda.current_stream builds a Stream
+    # object and parses the device on every call: ~10 us a call on the host)
+    return torch._C._cuda_getCurrentRawStream(idx) or None
 
 
 def float3(v) -> C.Array:

@@ -112,6 +112,7 @@ class ForwardState:
     bg: tuple = (0.0, 0.0, 0.0)
     timings: dict = field(default_factory=dict)
     grad2d: torch.Tensor | None = None  # [n, 12] zeroed by the forward blend, for the first backward
+    ccam: "_lib.GsCamera | None" = None  # the camera as the C calls take it (built once per forward)
 
     @property
     def n_buckets(self) -> int:
@@ -315,7 +316,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     tm.mark("blend_fwd")
     return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges, bucket_offsets,
                         nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist, tuple(bg),
-                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d)
+                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d, ccam)
 
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
@@ -359,7 +360,8 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
         g_b = torch.empty(n, fs.sh_coeffs - 1, 3, dtype=torch.float32, device=dev)
         g_sh = (g_a, g_b)
     call("gs_preprocess_bwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh_a), ptr(sh_b),
-         n, fs.sh_coeffs, fs.sh_degree, cam.c_struct(), ptr(fs.touched), ptr(grad2d), ptr(g_means),
+         n, fs.sh_coeffs, fs.sh_degree, fs.ccam if fs.ccam is not None else cam.c_struct(), ptr(fs.touched),
+         ptr(grad2d), ptr(g_means),
          ptr(g_ls), ptr(g_q), ptr(g_op), ptr(g_a), ptr(g_b), st)
     tm.mark("preprocess_bwd")
     return g_means, g_ls, g_q, g_op, g_sh, grad2d, {} if isinstance(timing, StageTimer) else tm.result()
