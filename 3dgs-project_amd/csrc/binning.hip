@@ -274,8 +274,8 @@ __device__ __forceinline__ uint64_t match_bits(uint32_t d, bool valid) {
 }
 
 
-template <int BITS, int ROUNDS>
-__global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const uint32_t* __restrict__ keys, int64_t m,
+template <int BITS, int ROUNDS, typename K>
+__global__ __launch_bounds__(kRsThreads) void rs_upsweep_kernel(const K* __restrict__ keys, int64_t m,
                                                                 int shift, uint32_t* __restrict__ tile_hist,
                                                                 int n_tiles) {
   constexpr int R = 1 << BITS;
@@ -336,9 +336,9 @@ __global__ __launch_bounds__(kScanThreads) void rs_rowscan_kernel(uint32_t* __re
   if (threadIdx.x == 0) totals[d] = run;
 }
 
-template <int BITS, int ROUNDS>
+template <int BITS, int ROUNDS, typename K>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
-    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin, uint32_t* __restrict__ kout,
+    const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t m, int shift, const uint32_t* __restrict__ tile_offs, int n_tiles,
     const uint32_t* __restrict__ totals, const uint32_t* __restrict__ aux_src, uint32_t* __restrict__ aux_out,
     uint32_t* __restrict__ ranges) {
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter_kernel(
     const uint32_t k = s_key[p];
     const uint32_t d = (k >> shift) & (R - 1);
     const uint32_t g = s_goff[d] + (static_cast<uint32_t>(p) - s_excl[d]);
-    if (kout) kout[g] = k;
+    if (kout) kout[g] = static_cast<K>(k);
     vout[g] = s_val[p];
     if (aux_out) aux_out[g] = aux_src[s_val[p]];  // a per-value array, gathered into sorted order
     if (ranges) {
@@ -474,14 +474,14 @@ static size_t sort_ws(int64_t m) {
   return align_up(m * 4) * 2 + align_up(hist * 4) + align_up(kRsMaxPasses * (1 << kRsMaxBits) * 4);
 }
 
-template <int BITS, int ROUNDS>
-static void sort_pass_r(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
+template <int BITS, int ROUNDS, typename K>
+static void sort_pass_r(const K* sk, const uint32_t* sv, K* dk, uint32_t* dv, int64_t m, int shift,
                         uint32_t* tile_hist, int n_tiles, uint32_t* totals, hipStream_t st,
                         const uint32_t* aux_src, uint32_t* aux_out, uint32_t* ranges) {
-  hipLaunchKernelGGL((rs_upsweep_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
+  hipLaunchKernelGGL((rs_upsweep_kernel<BITS, ROUNDS, K>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, m, shift, tile_hist,
                      n_tiles);
   hipLaunchKernelGGL(rs_rowscan_kernel, dim3(1 << BITS), dim3(kScanThreads), 0, st, tile_hist, n_tiles, totals);
-  hipLaunchKernelGGL((rs_scatter_kernel<BITS, ROUNDS>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
+  hipLaunchKernelGGL((rs_scatter_kernel<BITS, ROUNDS, K>), dim3(n_tiles), dim3(kRsThreads), 0, st, sk, sv, dk, dv, m, shift,
                      tile_hist, n_tiles, totals, aux_src, aux_out, ranges);
 }
 
@@ -491,8 +491,8 @@ static int sort_rounds(int64_t m) {
   return 4;
 }
 
-template <int BITS>
-static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint32_t* dv, int64_t m, int shift,
+template <int BITS, typename K>
+static void sort_pass(const K* sk, const uint32_t* sv, K* dk, uint32_t* dv, int64_t m, int shift,
                       uint32_t* tile_hist, int rounds, uint32_t* totals, hipStream_t st, const uint32_t* aux_src,
                       uint32_t* aux_out, uint32_t* ranges) {
   const int n_tiles = static_cast<int>((m + kRsWaves * kWave * rounds - 1) / (kRsWaves * kWave * rounds));
@@ -506,14 +506,16 @@ static void sort_pass(const uint32_t* sk, const uint32_t* sv, uint32_t* dk, uint
 // aux_src / aux_out (both or neither): the last pass also writes aux_out[j] = aux_src[v_out[j]].
 // ranges (the sort has at least one pass): the last pass also takes every key value's [start,
 // end) in the output by atomic min / max (ranges preset to [~0, 0]). drop_keys: the last pass
-// writes only the values (k_out is still used by earlier passes).
-static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, uint32_t* v_out, int64_t m,
+// writes only the values (k_out is still used by earlier passes). K: the key type (uint32_t, or
+// uint16_t for keys below 2^16: a quarter fewer bytes per pass); the scratch is sized for 32-bit keys.
+template <typename K>
+static void radix_sort(const K* k, const uint32_t* v, K* k_out, uint32_t* v_out, int64_t m,
                        int bits, char* ws, hipStream_t st, const uint32_t* aux_src = nullptr,
                        uint32_t* aux_out = nullptr, uint32_t* ranges = nullptr, bool drop_keys = false) {
   if (m <= 0) return;
   const SortPlan plan = sort_plan(bits);
   if (plan.passes == 0) {
-    (void)hipMemcpyAsync(k_out, k, m * 4, hipMemcpyDeviceToDevice, st);
+    (void)hipMemcpyAsync(k_out, k, m * sizeof(K), hipMemcpyDeviceToDevice, st);
     if (v) {
       (void)hipMemcpyAsync(v_out, v, m * 4, hipMemcpyDeviceToDevice, st);
     } else {
@@ -526,7 +528,7 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
   }
   const int rounds = sort_rounds(m);
   const int n_tiles = static_cast<int>((m + kRsMinTile - 1) / kRsMinTile);  // scratch sizing
-  uint32_t* k_alt = reinterpret_cast<uint32_t*>(ws);
+  K* k_alt = reinterpret_cast<K*>(ws);
   ws += align_up(m * 4);
   uint32_t* v_alt = reinterpret_cast<uint32_t*>(ws);
   ws += align_up(m * 4);
@@ -535,11 +537,11 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
   uint32_t* totals = reinterpret_cast<uint32_t*>(ws);
   // pass p writes the outputs when (passes - 1 - p) is even, the scratch pair otherwise, so
   // the last pass lands in (k_out, v_out) and no pass works in place
-  const uint32_t* src_k = k;
+  const K* src_k = k;
   const uint32_t* src_v = v;
   for (int p = 0; p < plan.passes; ++p) {
     const bool to_out = ((plan.passes - 1 - p) % 2) == 0;
-    uint32_t* dst_k = to_out ? k_out : k_alt;
+    K* dst_k = to_out ? k_out : k_alt;
     uint32_t* dst_v = to_out ? v_out : v_alt;
     uint32_t* tot = totals + (1 << kRsMaxBits) * p;
     const int shift = plan.bits * p;
@@ -547,17 +549,17 @@ static void radix_sort(const uint32_t* k, const uint32_t* v, uint32_t* k_out, ui
     const uint32_t* as = last ? aux_src : nullptr;
     uint32_t* ao = last ? aux_out : nullptr;
     uint32_t* rg = last ? ranges : nullptr;
-    uint32_t* dk = (last && drop_keys) ? nullptr : dst_k;
+    K* dk = (last && drop_keys) ? nullptr : dst_k;
     switch (plan.bits) {
-      case 1: sort_pass<1>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 2: sort_pass<2>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 3: sort_pass<3>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 4: sort_pass<4>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 5: sort_pass<5>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 6: sort_pass<6>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 7: sort_pass<7>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      case 8: sort_pass<8>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
-      default: sort_pass<9>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 1: sort_pass<1, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 2: sort_pass<2, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 3: sort_pass<3, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 4: sort_pass<4, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 5: sort_pass<5, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 6: sort_pass<6, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 7: sort_pass<7, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      case 8: sort_pass<8, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
+      default: sort_pass<9, K>(src_k, src_v, dk, dst_v, m, shift, tile_hist, rounds, tot, st, as, ao, rg); break;
     }
     src_k = dst_k;
     src_v = dst_v;
@@ -648,13 +650,13 @@ __device__ __forceinline__ uint32_t wave_excl_scan(uint32_t v, int lane, uint32_
   return incl - v;
 }
 
-template <bool kRect>
+template <bool kRect, typename K>
 __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ rec,
                                                    const int4* __restrict__ rects,
                                                    const uint32_t* __restrict__ order,
                                                    const uint32_t* __restrict__ offs, int64_t n,
                                                    const uint32_t* __restrict__ wstart, int64_t n_windows,
-                                                   int tiles_x, int tiles_y, uint32_t* __restrict__ tkeys,
+                                                   int tiles_x, int tiles_y, K* __restrict__ tkeys,
                                                    uint32_t* __restrict__ vals, uint32_t* __restrict__ ranges_preset,
                                                    int n_tiles) {
   __shared__ EmitSetup s_set[4][kWave];
@@ -775,7 +777,7 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
           for (uint32_t t = lane; t < nt; t += kWave) {
             const uint32_t k = start + t;
             if (k < wave_cap) {
-              tkeys[base + k] = (rw & 0x3ffffffu) + t;
+              tkeys[base + k] = static_cast<K>((rw & 0x3ffffffu) + t);
               vals[base + k] = gw;
             }
           }
@@ -790,7 +792,7 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
         const uint32_t t = p - s_nex[wave][q];
         const uint32_t k = done + s_iex[wave][q] + t;
         if (k < wave_cap) {
-          tkeys[base + k] = (rw & 0x3ffffffu) + t;
+          tkeys[base + k] = static_cast<K>((rw & 0x3ffffffu) + t);
           vals[base + k] = s_gid[wave][rw >> 26];
         }
       }
@@ -952,7 +954,8 @@ __global__ __launch_bounds__(kBoThreads) void bucket_offsets_kernel(uint32_t* __
 
 // Full 64-bit keys of the sorted instances (tile << 32 | depth key), for callers that want them.
 // (tile << 32 | depth order key); dkey0 is added back to keys stored relative to it.
-__global__ void full_keys_kernel(const uint32_t* __restrict__ tkeys, const uint32_t* __restrict__ vals,
+template <typename K>
+__global__ void full_keys_kernel(const K* __restrict__ tkeys, const uint32_t* __restrict__ vals,
                                  const uint32_t* __restrict__ dkey_of, uint32_t dkey0, int64_t m,
                                  uint64_t* __restrict__ out) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1105,41 +1108,57 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
 
 // Emission of the instances in depth order, stable sort by tile, tile ranges and bucket
 // offsets. dkey_of [n]: the depth key of every Gaussian (only read for sorted_keys).
+// Emission and the stable tile sort with keys of type K (the ranges preset by the emission
+// and taken by the last pass when there is one), and the full 64-bit keys if asked for.
+template <typename K>
+static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
+                          const uint32_t* order, const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles,
+                          int64_t m, int tile_bits, uint64_t* sorted_keys, uint32_t* point_list, uint32_t* preset,
+                          const EmitLayout& L, char* ws, hipStream_t st) {
+  K* tkeys = reinterpret_cast<K*>(ws + L.tkeys);
+  uint32_t* tvals = reinterpret_cast<uint32_t*>(ws + L.tvals);
+  K* tsorted = reinterpret_cast<K*>(ws + L.tsorted);
+  const uint32_t* wstart = reinterpret_cast<const uint32_t*>(ws + L.wstart);
+  const int64_t n_windows = (m + kEmitSpan - 1) / kEmitSpan;
+  if (rects) {
+    hipLaunchKernelGGL((emit_kernel<true, K>), dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
+                       offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
+  } else {
+    hipLaunchKernelGGL((emit_kernel<false, K>), dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
+                       offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
+  }
+  radix_sort(tkeys, tvals, tsorted, point_list, m, tile_bits, ws + L.sort, st, nullptr, nullptr, preset,
+             preset != nullptr && !sorted_keys);
+  if (sorted_keys)
+    hipLaunchKernelGGL((full_keys_kernel<K>), dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list, dkey_of,
+                       dkey0, m, sorted_keys);
+}
+
 static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
                      const uint32_t* order,
                      const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
                      uint32_t* bucket_offsets, uint32_t* list_header, char* ws, hipStream_t st) {
   const EmitLayout L = emit_layout(m, n_tiles);
-  uint32_t* tkeys = reinterpret_cast<uint32_t*>(ws + L.tkeys);
-  uint32_t* tvals = reinterpret_cast<uint32_t*>(ws + L.tvals);
-  uint32_t* tsorted = reinterpret_cast<uint32_t*>(ws + L.tsorted);
   const int tile_bits = L.tile_bits;
-  char* sort_scratch = ws + L.sort;
-  uint32_t* wstart = reinterpret_cast<uint32_t*>(ws + L.wstart);
   if (m > 0) {
     const int64_t n_windows = (m + kEmitSpan - 1) / kEmitSpan;
     hipLaunchKernelGGL(emit_windows_kernel, dim3(grid_for(n + 1, 256)), dim3(256), 0, st, offsets, n, n_windows,
-                       wstart);
+                       reinterpret_cast<uint32_t*>(ws + L.wstart));
     // with at least one sort pass, the last pass takes the tile ranges (preset by the emission)
-    // and the sorted keys are written only if the caller wants them
+    // and the sorted keys are written only if the caller wants them; tile ids below 2^16 are
+    // emitted and sorted as 16-bit keys
     const bool sort_ranges = tile_bits > 0;
     uint32_t* preset = sort_ranges ? ranges : nullptr;
-    if (rects) {
-      hipLaunchKernelGGL(emit_kernel<true>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
-                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
-    } else {
-      hipLaunchKernelGGL(emit_kernel<false>, dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
-                         offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
-    }
-    radix_sort(tkeys, tvals, tsorted, point_list, m, tile_bits, sort_scratch, st, nullptr, nullptr, preset,
-               sort_ranges && !sorted_keys);
-    if (sorted_keys)
-      hipLaunchKernelGGL(full_keys_kernel, dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list,
-                         dkey_of, dkey0, m, sorted_keys);
+    if (sort_ranges && n_tiles <= 65536)
+      emit_and_sort<uint16_t>(rec, rects, dkey_of, dkey0, order, offsets, n, tiles_x, n_tiles, m, tile_bits,
+                              sorted_keys, point_list, preset, L, ws, st);
+    else
+      emit_and_sort<uint32_t>(rec, rects, dkey_of, dkey0, order, offsets, n, tiles_x, n_tiles, m, tile_bits,
+                              sorted_keys, point_list, preset, L, ws, st);
     if (!sort_ranges)
       hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for((m + kBoundsPer - 1) / kBoundsPer, 256)), dim3(256), 0,
-                         st, tsorted, m, n_tiles, ranges);
+                         st, reinterpret_cast<const uint32_t*>(ws + L.tsorted), m, n_tiles, ranges);
     hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
                        tile_offsets, list_header, sort_ranges);
     return;
