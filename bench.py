@@ -175,23 +175,30 @@ def bucket_stats(fs):
     return int(active.sum()), int(tmax.sum()), int(staged.sum()), int(((staged + 31) // 32).sum())
 
 
-def _profile_value(name: str, key: str):
+def _profile_value(name: str, key: str, workload: str):
+    """A figure from a committed profile summary, if that summary was measured on `workload`
+    (its heading ends with the workload's name); None otherwise."""
     f = ROOT / "profiles" / name
     if not f.exists():
         return None
-    m = re.search(rf"{key}:\s*([0-9.eE+]+)", f.read_text())
+    text = f.read_text()
+    head = text.splitlines()[0] if text else ""
+    if not head.rstrip().endswith(workload):
+        return None
+    m = re.search(rf"{key}:\s*([0-9.eE+]+)", text)
     return float(m.group(1)) if m else None
 
 
-def measured_traffic(kernel: str):
+def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE and
-    WRITE_SIZE, calibrated with a plain copy), or None."""
-    return _profile_value(f"{kernel}_hbm_traffic.md", "traffic_bytes_per_launch")
+    WRITE_SIZE, calibrated with a plain copy) of the same workload, or None."""
+    return _profile_value(f"{kernel}_hbm_traffic.md", "traffic_bytes_per_launch", workload)
 
 
-def measured_valu_instr(kernel: str):
-    """VALU instructions per launch of `kernel` from the committed rocprofv3 SQ summary, or None."""
-    return _profile_value(f"{kernel}_sq.md", "valu_instr_per_launch")
+def measured_valu_instr(kernel: str, workload: str):
+    """VALU instructions per launch of `kernel` from the committed rocprofv3 SQ summary of the same
+    workload, or None."""
+    return _profile_value(f"{kernel}_sq.md", "valu_instr_per_launch", workload)
 
 
 def cpu_model() -> str:
@@ -483,7 +490,7 @@ def bench_3d(args, ceilings) -> dict:
         tops = ops / (t_dom * 1e-3) / 1e12
         roof = {"kernel": kernel, "bound": "valu", "achieved": round(tops, 3), "peak": VALU_PEAK_TOPS,
                 "unit": "T FP32 lane-op/s (157.3 TFLOP/s with an FMA as 2)", "frac": round(tops / VALU_PEAK_TOPS, 4),
-                "traffic": measured_traffic(kernel), "algorithmic_ops": ops,
+                "traffic": measured_traffic(kernel, args.workload), "algorithmic_ops": ops,
                 "ops_model": f"{OPS_PER_PAIR} per evaluated pair + {OPS_PER_STEP_LANE} per lane and bucket-splat "
                              f"step + {OPS_PER_REDUCTION} per reduced bucket-splat",
                 "avg_launch_ms": round(t_dom, 4), "hbm": hbm}
@@ -492,15 +499,15 @@ def bench_3d(args, ceilings) -> dict:
             roof["frac_of_achievable"] = round(tops / ceilings["fma_tops"], 4)
     else:
         roof = {"kernel": kernel, "bound": "hbm", **{k: v for k, v in hbm.items() if k != "algorithmic_bytes"},
-                "traffic": measured_traffic(kernel), "algorithmic_bytes": hbm["algorithmic_bytes"],
+                "traffic": measured_traffic(kernel, args.workload), "algorithmic_bytes": hbm["algorithmic_bytes"],
                 "avg_launch_ms": round(t_dom, 4)}
-    valu_instr = measured_valu_instr(kernel)
+    valu_instr = measured_valu_instr(kernel, args.workload)
     if valu_instr:
         rate = valu_instr / (t_dom * 1e-3)
         roof["issue"] = {"valu_instr_per_launch": valu_instr, "achieved": round(rate / 1e12, 4),
                          "peak": round(VALU_PEAK_INSTR / 1e12, 4), "unit": "T wave64 VALU instr/s",
                          "frac": round(rate / VALU_PEAK_INSTR, 4)}
-    atomics = _profile_value(f"{kernel}_atomics.md", "atomic_requests_per_launch")
+    atomics = _profile_value(f"{kernel}_atomics.md", "atomic_requests_per_launch", args.workload)
     if atomics:
         roof["atomic_requests_per_launch"] = atomics
 
