@@ -70,10 +70,16 @@ class RectBins:
     num_buckets: int
 
 
+# Tile binning of the 2D surfaces: "auto" (the library's choice by size), "spans" or "radix".
+BINNING = "auto"
+
+
 def bin_rects(rects: torch.Tensor, counts: torch.Tensor, depth: torch.Tensor | None, width: int, height: int,
-              want_order: bool = False) -> RectBins:
+              want_order: bool = False, binning: str | None = None) -> RectBins:
     """Per-tile lists of the Gaussians whose tile rectangle covers the tile, in stable depth
-    order (depth given) or index order. Two host reads: the instance and bucket counts."""
+    order (depth given) or index order. Two host reads: the instance and bucket counts.
+    binning: "auto", "spans" or "radix" (default: the module's BINNING); the lists are the same."""
+    flags = _lib.BIN_FLAGS[binning or BINNING]
     dev = rects.device
     n = rects.shape[0]
     tx, ty = tiles_of(width, height)
@@ -98,9 +104,9 @@ def bin_rects(rects: torch.Tensor, counts: torch.Tensor, depth: torch.Tensor | N
         if d.dtype not in (torch.float32, torch.float64):
             d = d.float()
         dcode = dtype_code(d)
-    ws = _u8(_lib.size_call("gs_bin_workspace_size", n, m, T), dev)
+    ws = _u8(_lib.size_call("gs_bin_workspace_size", n, m, tx, ty, flags), dev)
     call("gs_bin_fill_rect", ptr(rects), ptr(d), dcode, ptr(counts), n, tx, ty, m, None, ptr(point_list), ptr(ranges),
-         ptr(tile_offsets), ptr(boff), ptr(order), ptr(ws), ws.numel(), st)
+         ptr(tile_offsets), ptr(boff), ptr(order), flags, ptr(ws), ws.numel(), st)
     nb = int(boff[T].item())
     b2t = torch.empty(max(nb, 1), dtype=torch.int32, device=dev)
     call("gs_bucket_fill", ptr(boff), T, ptr(b2t), nb, st)

@@ -57,14 +57,15 @@ class Camera:
     near: float = 0.01
     far: float = 100.0
     proper_antialiasing: bool = False
+    binning: str = "auto"  # "auto", "spans" or "radix": which tile binning the forward takes
 
     @staticmethod
     def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0,
-               proper_antialiasing: bool = False) -> "Camera":
+               proper_antialiasing: bool = False, binning: str = "auto") -> "Camera":
         K = torch.as_tensor(K, dtype=torch.float64).cpu()
         vm = torch.as_tensor(viewmat, dtype=torch.float32).detach().cpu().reshape(4, 4)
         return Camera(vm, float(K[0, 0]), float(K[1, 1]), float(K[0, 2]), float(K[1, 2]), int(width),
-                      int(height), float(near), float(far), bool(proper_antialiasing))
+                      int(height), float(near), float(far), bool(proper_antialiasing), binning)
 
     @property
     def tiles_x(self) -> int:
@@ -79,9 +80,9 @@ class Camera:
         return self.tiles_x * self.tiles_y
 
     def c_struct(self) -> _lib.GsCamera:
+        flags = (_lib.GS_CAM_PROPER_ANTIALIASING if self.proper_antialiasing else 0) | _lib.BIN_FLAGS[self.binning]
         return _lib.make_camera(self.viewmat.detach().cpu().float(), self.fx, self.fy, self.cx, self.cy,
-                                self.width, self.height, self.near, self.far,
-                                _lib.GS_CAM_PROPER_ANTIALIASING if self.proper_antialiasing else 0)
+                                self.width, self.height, self.near, self.far, flags)
 
 
 @dataclass
@@ -95,7 +96,8 @@ class ForwardState:
     rec: torch.Tensor            # [n, 16] splat records
     touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
     order: torch.Tensor          # [n] int32 Gaussians by depth (culled last)
-    offsets: torch.Tensor        # [n + 1] int32 instance offsets in that order; [n] = m
+    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets in that order ([n] = m), or None
+    #                               where the fill does not need them (gs_bin_needs_offsets)
     m: int                       # instances
     keys: torch.Tensor           # [m] int64 sorted keys (empty unless keep_keys)
     point_list: torch.Tensor     # [m] int32
@@ -234,7 +236,11 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         pre_done.record()
         side.wait_event(pre_done)
     order = torch.empty(n, dtype=torch.int32, device=dev)
-    offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    # the instance offsets in depth order are needed only where the fill emits and sorts the
+    # instances (canvases beyond the span binning's limit)
+    offsets = None
+    if _lib.lib().gs_bin_needs_offsets(n, ccam):
+        offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
     call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
          ws.numel(), st)
@@ -275,7 +281,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         if m >= 1 << 32:
             raise _lib.AmdSplatError(f"{m} tile instances exceed the 32-bit instance index")
     nb_max = (m + (BUCKET - 1) * T) // BUCKET if backward_state else 0  # >= sum over tiles of ceil(len / 32)
-    ws_bytes = max(_lib.size_call("gs_bin_workspace_size", n, m, T), 1)
+    ws_bytes = max(_lib.size_call("gs_bin_workspace_size", n, m, cam.tiles_x, cam.tiles_y, ccam.flags), 1)
     parts = {"point_list": 4 * m, "keys": 8 * m if keep_keys else 0, "ws": ws_bytes}
     if backward_state:
         parts.update(bucket_to_tile=4 * max(nb_max, 1), blist=4 * (4 + nb_max), ckpt=4096 * max(nb_max, 1))

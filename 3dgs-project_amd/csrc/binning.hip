@@ -989,6 +989,689 @@ __global__ void rect_counts_kernel(const int4* __restrict__ rects, int64_t n, in
   counts[i] = (w > 0 && h > 0) ? static_cast<uint32_t>(w * h) : 0u;
 }
 
+// ---------------------------------------------------------------------------------------
+// Span binning (canvases of at most kSpanMaxDim tiles per side).
+//
+// The tile lists in (tile, depth) order without sorting the M instances. A Gaussian's tiles
+// in one tile row form a run of columns, its row span (tx0, nt); two counting passes over the
+// spans place every instance once:
+//   rows     the Gaussians in depth order, kRowChunk per wavefront: each chunk counts its
+//            non-empty (Gaussian, tile row) items per row (span_rows_kernel<count>), a scan of
+//            each row over the chunks gives every chunk its offsets (rs_rowscan_kernel), and
+//            each chunk writes its spans there (span_rows_kernel<write>): the spans of one row
+//            are contiguous and in depth order. Each row's spans start at a multiple of
+//            kSpanChunk.
+//   columns  kSpanChunk spans per wavefront, all of one row: each chunk counts its instances
+//            per column with a difference array over the columns (span_col_count_kernel); a
+//            scan of every (row, column) over the row's chunks gives every chunk its offsets
+//            and the tile counts, and the last workgroup to finish scans the tile counts into
+//            ranges and bucket offsets (span_col_scan_kernel); each chunk expands its spans into
+//            instances and writes the Gaussian of each at its tile's start + the chunk's offset
+//            + its rank among the chunk's instances in that column (span_col_write_kernel).
+// Ranks inside a wavefront come from ballots over the row or column bits in item order, and
+// chunks keep their order through the scans, so both passes are stable and a tile's list
+// holds its Gaussians in depth order: the order of a stable sort by tile of the instances
+// emitted in depth order. No kernel waits on another workgroup.
+// ---------------------------------------------------------------------------------------
+constexpr int kSpanMaxDim = 512;   // tiles per side (the LDS of the placement kernels)
+constexpr int kRowChunk = 256;     // depth positions per wavefront in the row pass
+constexpr int kSpanChunk = 1024;   // spans per workgroup in the column pass
+constexpr int kSpanWaves = 4;      // wavefronts per workgroup (256 threads)
+constexpr int kColScanThreads = kBoThreads;  // the last workgroup runs tile_scan_block
+
+__device__ __forceinline__ int align4i(int v) { return (v + 3) & ~3; }
+
+__device__ __forceinline__ uint32_t span_pad(uint32_t v) {
+  return (v + kSpanChunk - 1) & ~static_cast<uint32_t>(kSpanChunk - 1);
+}
+
+// s_rbase[r], r = 0 .. tiles_y: the start of row r's spans, every row's span count rounded up
+// to a multiple of kSpanChunk (s_rbase[tiles_y] = all of them). Called by every thread of the
+// workgroup; ends with a barrier. s_wsum: one word per wavefront.
+template <int kThreads>
+__device__ void span_row_bases(const uint32_t* __restrict__ rowtot, int tiles_y, uint32_t* s_rbase,
+                               uint32_t* s_wsum) {
+  constexpr int kPer = (kSpanMaxDim + 1 + kThreads - 1) / kThreads;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t v[kPer], sum = 0;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int r = static_cast<int>(threadIdx.x) * kPer + e;
+    v[e] = r < tiles_y ? span_pad(rowtot[r]) : 0u;
+    sum += v[e];
+  }
+  uint32_t incl = sum;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == kWave - 1) s_wsum[wave] = incl;
+  __syncthreads();
+  uint32_t run = incl - sum;
+  for (int w = 0; w < wave; ++w) run += s_wsum[w];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int r = static_cast<int>(threadIdx.x) * kPer + e;
+    if (r <= tiles_y) s_rbase[r] = run;
+    run += v[e];
+  }
+  __syncthreads();
+}
+
+// The row whose spans hold position p: the largest r < tiles_y with s_rbase[r] <= p.
+__device__ __forceinline__ int span_row_of(const uint32_t* s_rbase, int tiles_y, uint32_t p) {
+  int lo = 0, hi = tiles_y - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_rbase[mid] <= p) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// The span of item `item` of a wavefront's 64 Gaussians (their band setups or rectangles in
+// s_set, the exclusive prefix of their row counts in s_rex): the owning Gaussian (lane index),
+// the tile row and first column; returns the number of tiles (0: the row is missed).
+template <bool kRect>
+__device__ __forceinline__ uint32_t row_item(const float4* s_set, const uint32_t* s_rex, uint32_t item, int& own,
+                                             int& row, uint32_t& tx0) {
+  own = 0;  // last Gaussian whose first item is <= item
+#pragma unroll
+  for (int step = 32; step > 0; step >>= 1)
+    if (s_rex[own + step] <= item) own += step;
+  const float4 uu = s_set[3 * own];
+  const int r = static_cast<int>(item - s_rex[own]);
+  if constexpr (kRect) {
+    row = __float_as_int(uu.y) + r;
+    tx0 = static_cast<uint32_t>(__float_as_int(uu.x));
+    return static_cast<uint32_t>(__float_as_int(uu.z));
+  } else {
+    const float4 vv = s_set[3 * own + 1], ww = s_set[3 * own + 2];
+    BandSetup bs;
+    bs.mx = uu.x; bs.my = uu.y; bs.A = 0.0f; bs.B = uu.z; bs.det = uu.w;
+    bs.tA = vv.x; bs.vmax = vv.y; bs.vr = vv.z; bs.invA = vv.w;
+    bs.ok = bs.det > 0.0f;
+    const int4 dd = make_int4(__float_as_int(ww.x), __float_as_int(ww.y), __float_as_int(ww.z), __float_as_int(ww.w));
+    row = dd.z / kTile + r;
+    int t0;
+    const uint32_t nt = row_tiles(bs, dd, row, t0);
+    tx0 = static_cast<uint32_t>(t0);
+    return nt;
+  }
+}
+
+// Spans as the row pass gathers them (depth order, one chunk's spans contiguous):
+// x = Gaussian, y = tx0 | nt << 10 | row << 21 (tx0, row < 1024, nt <= 1024).
+__device__ __forceinline__ uint32_t pack_row_span(uint32_t tx0, uint32_t nt, int row) {
+  return tx0 | (nt << 10) | (static_cast<uint32_t>(row) << 21);
+}
+
+// Row pass, gather: one workgroup per chunk of kRowChunk Gaussians in depth order (wavefront w
+// takes the w-th 64). Reads each Gaussian's record once, counts the chunk's non-empty spans per
+// row into rowhist[r][c], reserves room for them in `gathered` (one atomic add per chunk:
+// chunk_info[c] = (first slot, number of spans)) and writes them there in (Gaussian, row)
+// order. The band arithmetic runs twice (count, then write): it is cheap next to the gather.
+template <bool kRect>
+__global__ __launch_bounds__(256) void span_gather_kernel(const SplatRec* __restrict__ rec,
+                                                          const int4* __restrict__ rects,
+                                                          const uint32_t* __restrict__ order, int64_t n,
+                                                          int n_chunks, int tiles_x, int tiles_y,
+                                                          uint32_t* __restrict__ rowhist,
+                                                          uint2* __restrict__ chunk_info,
+                                                          uint2* __restrict__ gathered, int64_t gathered_cap,
+                                                          uint32_t* __restrict__ counter) {
+  extern __shared__ __align__(16) uint32_t s_dyn[];
+  __shared__ uint32_t s_wcnt[kSpanWaves];
+  __shared__ uint32_t s_base;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // LDS: row counts [tiles_y]; per wavefront the band setups (3 float4), row prefix and ids of
+  // its 64 Gaussians
+  const int ty4 = align4i(tiles_y);
+  uint32_t* s_cnt = s_dyn;
+  uint32_t* s_wbase = s_dyn + ty4 + wave * (64 * 12 + 128);
+  float4* s_set = reinterpret_cast<float4*>(s_wbase);
+  uint32_t* s_rex = s_wbase + 64 * 12;
+  uint32_t* s_gid = s_rex + 64;
+  const int c = xcd_tile(blockIdx.x, gridDim.x);  // the grid has n_chunks workgroups
+  for (int q = threadIdx.x; q < ty4; q += 256) s_cnt[q] = 0u;
+  const int64_t j = static_cast<int64_t>(c) * kRowChunk + wave * kWave + lane;
+  uint32_t rows = 0, g = 0;
+  float4 u = make_float4(0.0f, 0.0f, 0.0f, 0.0f), v = u, w = u;
+  if (j < n) {
+    g = order[j];
+    if constexpr (kRect) {
+      const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
+      if (r.z > r.x && r.w > r.y) {
+        rows = static_cast<uint32_t>(r.w - r.y);
+        u = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z - r.x), 0.0f);
+      }
+    } else {
+      const float4 a = rec[g].a, b = rec[g].b;
+      const int4 d = rec[g].d;
+      if (d.w >= d.z && d.y >= d.x) {  // a culled record holds the empty bounds (0, -1, 0, -1)
+        const BandSetup bs = band_setup(a, b);
+        rows = static_cast<uint32_t>(d.w / kTile - d.z / kTile + 1);
+        u = make_float4(bs.mx, bs.my, bs.B, bs.det);
+        v = make_float4(bs.tA, bs.vmax, bs.vr, bs.invA);
+        w = make_float4(__int_as_float(d.x), __int_as_float(d.y), __int_as_float(d.z), __int_as_float(d.w));
+      }
+    }
+  }
+  s_set[3 * lane] = u;
+  s_set[3 * lane + 1] = v;
+  s_set[3 * lane + 2] = w;
+  s_gid[lane] = g;
+  uint32_t total;
+  s_rex[lane] = wave_excl_scan(rows, lane, total);
+  __syncthreads();  // counts cleared, setups visible
+  uint32_t live_total = 0;
+  for (uint32_t base = 0; base < total; base += kWave) {
+    const uint32_t item = base + static_cast<uint32_t>(lane);
+    bool live = false;
+    if (item < total) {
+      int own, row;
+      uint32_t tx0;
+      live = row_item<kRect>(s_set, s_rex, item, own, row, tx0) > 0u;
+      if (live) atomicAdd(&s_cnt[row], 1u);
+    }
+    live_total += static_cast<uint32_t>(__popcll(__ballot(live ? 1 : 0)));
+  }
+  if (lane == 0) s_wcnt[wave] = live_total;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t all = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+    const uint32_t first = all ? atomicAdd(counter, all) : 0u;
+    s_base = first;
+    chunk_info[c] = make_uint2(first, all);
+  }
+  for (int r = threadIdx.x; r < tiles_y; r += 256) rowhist[static_cast<int64_t>(r) * n_chunks + c] = s_cnt[r];
+  __syncthreads();
+  uint32_t slot = s_base;
+  for (int q = 0; q < wave; ++q) slot += s_wcnt[q];
+  const uint64_t lt = lanemask_lt(lane);
+  for (uint32_t base = 0; base < total; base += kWave) {
+    const uint32_t item = base + static_cast<uint32_t>(lane);
+    int own = 0, row = 0;
+    uint32_t tx0 = 0, nt = 0;
+    if (item < total) nt = row_item<kRect>(s_set, s_rex, item, own, row, tx0);
+    const uint64_t lv = __ballot(nt > 0u ? 1 : 0);
+    if (nt > 0u) {
+      const int64_t p = static_cast<int64_t>(slot) + __popcll(lv & lt);
+      if (p < gathered_cap) gathered[p] = make_uint2(s_gid[own], pack_row_span(tx0, nt, row));
+    }
+    slot += static_cast<uint32_t>(__popcll(lv));
+  }
+}
+
+// Row pass, placement: one workgroup per chunk; its gathered spans, split into four contiguous
+// quarters (one per wavefront), go to their rows: row start + the chunk's offset in the row
+// (rowhist, scanned) + the earlier wavefronts' spans of that row + the span's rank among the
+// wavefront's earlier spans of that row. Ranks inside a window of 64 spans come from a
+// coverage mask per row (each span ORs its lane bit in; the rank is the number of lower bits).
+// Writes (Gaussian, tx0 | nt << 16).
+__global__ __launch_bounds__(256) void span_place_kernel(const uint2* __restrict__ gathered,
+                                                         const uint2* __restrict__ chunk_info,
+                                                         const uint32_t* __restrict__ rowhist,
+                                                         const uint32_t* __restrict__ rowtot, int n_chunks,
+                                                         int tiles_y, uint2* __restrict__ spans,
+                                                         int64_t gathered_cap, int64_t span_cap) {
+  extern __shared__ __align__(16) uint32_t s_dyn[];
+  __shared__ uint32_t s_wsum[kSpanWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // LDS: row bases [tiles_y + 1]; per wavefront: row positions [tiles_y], row coverage masks
+  // [tiles_y] (uint64)
+  const int ty4 = align4i(tiles_y);
+  uint32_t* s_rbase = s_dyn;
+  uint32_t* s_pos = s_dyn + align4i(tiles_y + 1);  // [kSpanWaves][ty4]
+  unsigned long long* s_cov =
+      reinterpret_cast<unsigned long long*>(s_pos + kSpanWaves * ty4) + static_cast<int64_t>(wave) * ty4;
+  span_row_bases<256>(rowtot, tiles_y, s_rbase, s_wsum);
+  const int c = xcd_tile(blockIdx.x, gridDim.x);
+  const uint2 info = chunk_info[c];
+  if (info.y == 0u) return;  // the whole workgroup: no spans
+  uint32_t* my_pos = s_pos + wave * ty4;
+  for (int q = threadIdx.x; q < kSpanWaves * ty4; q += 256) s_pos[q] = 0u;
+  for (int q = lane; q < ty4; q += kWave) s_cov[q] = 0ull;
+  __syncthreads();
+  const uint32_t q0 = static_cast<uint32_t>((static_cast<uint64_t>(info.y) * wave) / kSpanWaves);
+  const uint32_t q1 = static_cast<uint32_t>((static_cast<uint64_t>(info.y) * (wave + 1)) / kSpanWaves);
+  // count this quarter's spans per row
+  for (uint32_t i = q0 + lane; i < q1; i += kWave) {
+    const int64_t p = static_cast<int64_t>(info.x) + i;
+    if (p < gathered_cap) atomicAdd(&my_pos[gathered[p].y >> 21], 1u);
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < tiles_y; r += 256) {
+    uint32_t run = s_rbase[r] + rowhist[static_cast<int64_t>(r) * n_chunks + c];
+#pragma unroll
+    for (int q = 0; q < kSpanWaves; ++q) {
+      const uint32_t cnt = s_pos[q * ty4 + r];
+      s_pos[q * ty4 + r] = run;
+      run += cnt;
+    }
+  }
+  __syncthreads();
+  const uint64_t below = lanemask_lt(lane);
+  for (uint32_t i0 = q0; i0 < q1; i0 += kWave) {
+    const uint32_t i = i0 + static_cast<uint32_t>(lane);
+    const int64_t p = static_cast<int64_t>(info.x) + i;
+    const bool live = i < q1 && p < gathered_cap;
+    uint2 e = make_uint2(0u, 0u);
+    int row = 0;
+    if (live) {
+      e = gathered[p];
+      row = static_cast<int>(e.y >> 21);
+      atomicOr(&s_cov[row], 1ull << lane);
+    }
+    wave_sync();
+    unsigned long long cov = 0ull;
+    if (live) {
+      cov = s_cov[row];
+      const int64_t pos = static_cast<int64_t>(my_pos[row]) + __popcll(cov & below);
+      if (pos < span_cap) spans[pos] = make_uint2(e.x, (e.y & 0x3ffu) | (((e.y >> 10) & 0x7ffu) << 16));
+    }
+    wave_sync();  // every lane has read its row's position and mask
+    if (live && (cov & below) == 0ull) {  // the row's lowest lane advances it and clears the mask
+      my_pos[row] += static_cast<uint32_t>(__popcll(cov));
+      s_cov[row] = 0ull;
+    }
+    wave_sync();
+  }
+}
+
+// Scan of the tile counts of a canvas (one workgroup of kBoThreads threads): ranges [start,
+// end), bucket offsets (32 entries per bucket), optionally CSR tile offsets, and the bucket
+// list header cleared.
+
+__device__ void tile_scan_block(const uint32_t* __restrict__ cnt, int n_tiles, uint32_t* __restrict__ ranges,
+                                uint32_t* __restrict__ boff, uint32_t* __restrict__ tile_offsets,
+                                uint32_t* __restrict__ list_header) {
+  __shared__ uint32_t s_wave[kBoThreads / kWave];
+  __shared__ uint32_t s_wave_inst[kBoThreads / kWave];
+  if (list_header && threadIdx.x < kListHeader) list_header[threadIdx.x] = 0u;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t run = 0, run_inst = 0;
+  for (int c0 = 0; c0 < n_tiles; c0 += kBoThreads * kBoItems) {
+    uint32_t len[kBoItems], sum = 0, sum_inst = 0;
+#pragma unroll
+    for (int e = 0; e < kBoItems; ++e) {
+      const int t = c0 + static_cast<int>(threadIdx.x) * kBoItems + e;
+      len[e] = t < n_tiles ? cnt[t] : 0u;
+      sum += (len[e] + kBucket - 1) / kBucket;
+      sum_inst += len[e];
+    }
+    uint32_t incl = sum, incl_inst = sum_inst;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t u = __shfl_up(incl, o, 64);
+      const uint32_t ui = __shfl_up(incl_inst, o, 64);
+      if (lane >= o) {
+        incl += u;
+        incl_inst += ui;
+      }
+    }
+    if (lane == kWave - 1) {
+      s_wave[wave] = incl;
+      s_wave_inst[wave] = incl_inst;
+    }
+    __syncthreads();
+    uint32_t before = 0, total = 0, before_inst = 0, total_inst = 0;
+    for (int w = 0; w < kBoThreads / kWave; ++w) {
+      const uint32_t v = s_wave[w];
+      const uint32_t vi = s_wave_inst[w];
+      before += w < wave ? v : 0u;
+      before_inst += w < wave ? vi : 0u;
+      total += v;
+      total_inst += vi;
+    }
+    __syncthreads();
+    uint32_t pos = run + before + incl - sum;
+    uint32_t pos_inst = run_inst + before_inst + incl_inst - sum_inst;
+#pragma unroll
+    for (int e = 0; e < kBoItems; ++e) {
+      const int t = c0 + static_cast<int>(threadIdx.x) * kBoItems + e;
+      if (t < n_tiles) {
+        boff[t] = pos;
+        ranges[2 * t] = pos_inst;
+        ranges[2 * t + 1] = pos_inst + len[e];
+        if (tile_offsets) tile_offsets[t] = pos_inst;
+      }
+      pos += (len[e] + kBucket - 1) / kBucket;
+      pos_inst += len[e];
+    }
+    run += total;
+    run_inst += total_inst;
+  }
+  if (threadIdx.x == 0) {
+    boff[n_tiles] = run;
+    if (tile_offsets) tile_offsets[n_tiles] = run_inst;
+  }
+}
+
+// Chunks of the column pass: chunk k (a workgroup) holds span positions [k kSpanChunk,
+// (k + 1) kSpanChunk), all in one row (wavefront w takes the w-th kWaveSpans of them); row r's
+// chunks are [cb, cb + nc) (clamped to the capacity). Chunk counts are stored chunk-major:
+// colcnt[k][t] for column t.
+constexpr int kWaveSpans = kSpanChunk / kSpanWaves;  // 256
+
+struct SpanChunk {
+  int row;
+  int64_t cb, nc;  // the row's first chunk and its number of chunks
+};
+
+__device__ __forceinline__ SpanChunk span_chunk(const uint32_t* s_rbase, int tiles_y, int64_t k, int64_t chunk_cap) {
+  SpanChunk sc;
+  sc.row = span_row_of(s_rbase, tiles_y, static_cast<uint32_t>(k * kSpanChunk));
+  sc.cb = min<int64_t>(s_rbase[sc.row] / kSpanChunk, chunk_cap);
+  sc.nc = min<int64_t>(s_rbase[sc.row + 1] / kSpanChunk, chunk_cap) - sc.cb;
+  return sc;
+}
+
+// The chunks of the column pass are dealt to the XCDs in contiguous ranges (a workgroup runs on
+// XCD blockIdx.x % 8), so the chunks that write neighbouring parts of a tile's list share an
+// L2. The grid is a multiple of 8 workgroups; workgroup `wid` of `nw` in its XCD takes chunks
+// lo + wid, lo + wid + nw, ... below hi.
+struct XcdRange {
+  int64_t lo, hi, wid, nw;
+};
+
+__device__ __forceinline__ XcdRange xcd_range(int64_t n_items) {
+  XcdRange x;
+  const int xcd = static_cast<int>(blockIdx.x & 7u);
+  x.lo = n_items * xcd / 8;
+  x.hi = n_items * (xcd + 1) / 8;
+  x.nw = static_cast<int64_t>(gridDim.x >> 3);
+  x.wid = static_cast<int64_t>(blockIdx.x >> 3);
+  return x;
+}
+
+// Instance counts per column of kWaveSpans spans (this wavefront's), from a difference array
+// over the columns: s_cnt[t] for t < tiles_x (s_cnt holds tiles_x + 1 words). sp: the lane's
+// kPerLane spans (empty ones have nt = 0).
+constexpr int kPerLane = kWaveSpans / kWave;  // 4
+
+__device__ __forceinline__ void wave_column_counts(const uint2 (&sp)[kPerLane], int tiles_x, int lane,
+                                                   uint32_t* s_cnt) {
+  for (int t = lane; t <= tiles_x; t += kWave) s_cnt[t] = 0u;
+  wave_sync();
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) {
+    const uint32_t tx0 = sp[e].y & 0xffffu, nt = sp[e].y >> 16;
+    if (nt) {
+      atomicAdd(&s_cnt[tx0], 1u);
+      atomicAdd(&s_cnt[tx0 + nt], 0xffffffffu);
+    }
+  }
+  wave_sync();
+  const int per = (tiles_x + kWave - 1) / kWave;
+  uint32_t sum = 0;
+  for (int e = 0; e < per; ++e) {
+    const int t = lane * per + e;
+    if (t < tiles_x) sum += s_cnt[t];
+  }
+  uint32_t tot;
+  uint32_t run = wave_excl_scan(sum, lane, tot);
+  wave_sync();
+  for (int e = 0; e < per; ++e) {
+    const int t = lane * per + e;
+    if (t < tiles_x) {
+      run += s_cnt[t];
+      s_cnt[t] = run;
+    }
+  }
+  wave_sync();
+}
+
+// The lane's kPerLane consecutive spans of chunk k, wavefront `wave` (positions at or beyond lim
+// are empty; a span reaching past the last column is dropped).
+__device__ __forceinline__ void load_wave_spans(const uint2* __restrict__ spans, int64_t k, int wave, int lane,
+                                                int64_t lim, int tiles_x, uint2 (&sp)[kPerLane]) {
+  const int64_t p0 = k * kSpanChunk + wave * kWaveSpans + kPerLane * lane;
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) {
+    sp[e] = p0 + e < lim ? spans[p0 + e] : make_uint2(0u, 0u);
+    if ((sp[e].y & 0xffffu) + (sp[e].y >> 16) > static_cast<uint32_t>(tiles_x)) sp[e].y = 0u;
+  }
+}
+
+// Column pass, counts: colcnt[k][t] = instances of chunk k in column t of its row.
+__global__ __launch_bounds__(256) void span_col_count_kernel(const uint2* __restrict__ spans,
+                                                             const uint32_t* __restrict__ rowtot, int tiles_x,
+                                                             int tiles_y, int64_t span_cap, int64_t chunk_cap,
+                                                             uint32_t* __restrict__ colcnt) {
+  extern __shared__ __align__(16) uint32_t s_dyn[];
+  __shared__ uint32_t s_wsum[kSpanWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tx4 = align4i(tiles_x + 1);
+  uint32_t* s_rbase = s_dyn;
+  uint32_t* s_cnt = s_dyn + align4i(tiles_y + 1);  // [kSpanWaves][tx4]
+  span_row_bases<256>(rowtot, tiles_y, s_rbase, s_wsum);
+  const int64_t n_chunks = min<int64_t>(s_rbase[tiles_y] / kSpanChunk, chunk_cap);
+  const XcdRange xr = xcd_range(n_chunks);
+  for (int64_t k = xr.lo + xr.wid; k < xr.hi; k += xr.nw) {
+    const SpanChunk sc = span_chunk(s_rbase, tiles_y, k, chunk_cap);
+    const int64_t lim = min<int64_t>(static_cast<int64_t>(s_rbase[sc.row]) + rowtot[sc.row], span_cap);
+    uint2 sp[kPerLane];
+    load_wave_spans(spans, k, wave, lane, lim, tiles_x, sp);
+    wave_column_counts(sp, tiles_x, lane, s_cnt + wave * tx4);
+    __syncthreads();
+    for (int t = threadIdx.x; t < tiles_x; t += 256)
+      colcnt[k * tiles_x + t] = s_cnt[t] + s_cnt[tx4 + t] + s_cnt[2 * tx4 + t] + s_cnt[3 * tx4 + t];
+    __syncthreads();  // the counts are rewritten for the next chunk
+  }
+}
+
+// Column pass, scan: workgroup r scans every column of row r over the row's chunks, in place
+// (each chunk's offset within the tile), and writes the tile counts. The chunks are split into
+// segments, a thread per (segment, column): segment sums, their prefix, then each thread
+// rewrites its segment.
+constexpr int kColScanMaxSegs = 32;
+
+__global__ __launch_bounds__(kColScanThreads) void span_col_scan_kernel(uint32_t* __restrict__ colcnt,
+                                                                        const uint32_t* __restrict__ rowtot,
+                                                                        int tiles_x, int tiles_y, int64_t chunk_cap,
+                                                                        uint32_t* __restrict__ tcnt) {
+  __shared__ uint32_t s_rbase[kSpanMaxDim + 1];
+  __shared__ uint32_t s_seg[kColScanThreads];
+  __shared__ uint32_t s_wsum[kColScanThreads / kWave];
+  span_row_bases<kColScanThreads>(rowtot, tiles_y, s_rbase, s_wsum);
+  const int r = blockIdx.x;
+  const int64_t cb = min<int64_t>(s_rbase[r] / kSpanChunk, chunk_cap);
+  const int64_t ce = min<int64_t>(s_rbase[r + 1] / kSpanChunk, chunk_cap);
+  int cols_p2 = 1;
+  while (cols_p2 < tiles_x) cols_p2 <<= 1;
+  const int segs = min(kColScanThreads / cols_p2, kColScanMaxSegs);
+  const int col = static_cast<int>(threadIdx.x) & (cols_p2 - 1);
+  const int seg = static_cast<int>(threadIdx.x) / cols_p2;
+  const bool mine = col < tiles_x && seg < segs;
+  const int64_t len = (ce - cb + segs - 1) / segs;
+  const int64_t c0 = cb + seg * len;
+  const int64_t c1 = min<int64_t>(c0 + len, ce);
+  constexpr int kU = 8;  // loads in flight per thread
+  uint32_t sum = 0;
+  if (mine) {
+    for (int64_t k = c0; k < c1; k += kU) {
+      uint32_t v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = k + u < c1 ? colcnt[(k + u) * tiles_x + col] : 0u;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) sum += v[u];
+    }
+  }
+  s_seg[threadIdx.x] = mine ? sum : 0u;
+  __syncthreads();
+  if (!mine) return;  // no barrier follows
+  uint32_t run = 0, total = 0;
+  for (int s = 0; s < segs; ++s) {
+    const uint32_t v = s_seg[s * cols_p2 + col];
+    run += s < seg ? v : 0u;
+    total += v;
+  }
+  for (int64_t k = c0; k < c1; k += kU) {
+    uint32_t v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = k + u < c1 ? colcnt[(k + u) * tiles_x + col] : 0u;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (k + u < c1) colcnt[(k + u) * tiles_x + col] = run;
+      run += v[u];
+    }
+  }
+  if (seg == 0) tcnt[static_cast<int64_t>(r) * tiles_x + col] = total;
+}
+
+// Ranges, bucket offsets and the bucket list header from the tile counts (one workgroup).
+__global__ __launch_bounds__(kBoThreads) void tile_scan_kernel(const uint32_t* __restrict__ tcnt, int n_tiles,
+                                                              uint32_t* __restrict__ ranges,
+                                                              uint32_t* __restrict__ boff,
+                                                              uint32_t* __restrict__ tile_offsets,
+                                                              uint32_t* __restrict__ list_header) {
+  tile_scan_block(tcnt, n_tiles, ranges, boff, tile_offsets, list_header);
+}
+
+// Column pass, placement: workgroup per chunk, each wavefront places the instances of its
+// kWaveSpans spans. Instance i of a wavefront's spans (numbered in (span, column) order) goes
+// to its tile's start + the chunk's offset in the tile + the earlier wavefronts' instances in
+// the column + its rank among the wavefront's earlier instances in the column. The instances
+// are taken in batches of R windows of 64: an owner table gives each instance its span; in a
+// window, each span (at most 64, all of distinct columns) ORs its bit (span - the window's first
+// span) into the window's column mask, so the rank inside the window is the number of lower
+// bits; a pass over the columns then turns the windows' counts into running positions.
+constexpr int kOwnerTable = 2048;  // instances per owner-table segment (one byte each)
+
+template <bool kKeys, int R>
+__global__ __launch_bounds__(256) void span_col_write_kernel(
+    const uint2* __restrict__ spans, const uint32_t* __restrict__ rowtot, const uint32_t* __restrict__ colcnt,
+    const uint32_t* __restrict__ ranges, int tiles_x, int tiles_y, int64_t span_cap, int64_t chunk_cap, int64_t m,
+    uint32_t* __restrict__ point_list, uint64_t* __restrict__ keys, const uint32_t* __restrict__ dkey_of,
+    uint32_t dkey0) {
+  extern __shared__ __align__(16) uint32_t s_dyn[];
+  __shared__ uint32_t s_wsum[kSpanWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // LDS: row bases [tiles_y + 1]; column positions [kSpanWaves][tiles_x + 1]; per wavefront:
+  // the windows' column masks [R][tiles_x] (uint64) and offsets [R][tiles_x], the spans
+  // (uint2) and their instance prefix, the owner table (bytes)
+  const int tx4 = align4i(tiles_x + 1);
+  const int wave_words = R * 3 * tx4 + 2 * kWaveSpans + (kWaveSpans + 4) + kOwnerTable / 4;
+  uint32_t* s_rbase = s_dyn;
+  uint32_t* s_cpos = s_dyn + align4i(tiles_y + 1);  // [kSpanWaves][tx4]
+  uint32_t* s_w = s_cpos + kSpanWaves * tx4 + wave * wave_words;
+  unsigned long long* s_cov = reinterpret_cast<unsigned long long*>(s_w);  // [R][tx4]
+  uint32_t* s_off = s_w + 2 * R * tx4;                                       // [R][tx4]
+  uint2* s_span = reinterpret_cast<uint2*>(s_off + R * tx4);                 // [kWaveSpans]
+  uint32_t* s_pre = s_off + R * tx4 + 2 * kWaveSpans;                        // [kWaveSpans + 1]
+  uint8_t* s_tbl = reinterpret_cast<uint8_t*>(s_pre + kWaveSpans + 4);       // [kOwnerTable]
+  uint32_t* s_pos = s_cpos + wave * tx4;
+  span_row_bases<256>(rowtot, tiles_y, s_rbase, s_wsum);
+  for (int q = lane; q < R * tx4; q += kWave) s_cov[q] = 0ull;
+  const int64_t n_chunks = min<int64_t>(s_rbase[tiles_y] / kSpanChunk, chunk_cap);
+  const XcdRange xr = xcd_range(n_chunks);
+  for (int64_t k = xr.lo + xr.wid; k < xr.hi; k += xr.nw) {
+    const SpanChunk sc = span_chunk(s_rbase, tiles_y, k, chunk_cap);
+    const int64_t lim = min<int64_t>(static_cast<int64_t>(s_rbase[sc.row]) + rowtot[sc.row], span_cap);
+    const int64_t t_row = static_cast<int64_t>(sc.row) * tiles_x;
+    uint2 sp[kPerLane];
+    load_wave_spans(spans, k, wave, lane, lim, tiles_x, sp);
+    wave_column_counts(sp, tiles_x, lane, s_pos);
+    __syncthreads();
+    // each wavefront's first position in every column: the tile's start, the chunk's offset in
+    // the tile, then the earlier wavefronts' instances
+    for (int t = threadIdx.x; t < tiles_x; t += 256) {
+      uint32_t run = ranges[2 * (t_row + t)] + colcnt[k * tiles_x + t];
+#pragma unroll
+      for (int q = 0; q < kSpanWaves; ++q) {
+        const uint32_t c = s_cpos[q * tx4 + t];
+        s_cpos[q * tx4 + t] = run;
+        run += c;
+      }
+    }
+    __syncthreads();
+    uint32_t sum = 0;
+#pragma unroll
+    for (int e = 0; e < kPerLane; ++e) sum += sp[e].y >> 16;
+    uint32_t total;
+    uint32_t run = wave_excl_scan(sum, lane, total);
+#pragma unroll
+    for (int e = 0; e < kPerLane; ++e) {
+      s_pre[kPerLane * lane + e] = run;
+      s_span[kPerLane * lane + e] = sp[e];
+      run += sp[e].y >> 16;
+    }
+    for (uint32_t t0 = 0; t0 < total; t0 += kOwnerTable) {
+      const uint32_t t1 = min<uint32_t>(t0 + kOwnerTable, total);
+      wave_sync();  // the previous segment is done with the table
+      // owner table: every instance of the segment gets its span's index
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) {
+        const uint32_t s = static_cast<uint32_t>(kPerLane * lane + e);
+        const uint32_t a = max(s_pre[s], t0), b = min(s_pre[s] + (sp[e].y >> 16), t1);
+        for (uint32_t i = a; i < b; ++i) s_tbl[i - t0] = static_cast<uint8_t>(s);
+      }
+      wave_sync();
+      for (uint32_t b0 = t0; b0 < t1; b0 += R * kWave) {
+        uint32_t col[R], g[R], bit[R], low[R];
+        bool live[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t w0 = b0 + r * kWave;
+          const uint32_t i = w0 + static_cast<uint32_t>(lane);
+          live[r] = i < t1;
+          col[r] = g[r] = bit[r] = 0u;
+          if (live[r]) {
+            const uint32_t own = s_tbl[i - t0];
+            const uint32_t first = s_tbl[w0 - t0];  // the window's first span
+            const uint2 e = s_span[own];
+            col[r] = (e.y & 0xffffu) + (i - s_pre[own]);
+            g[r] = e.x;
+            bit[r] = own - first;  // < 64: a window's 64 instances lie in at most 64 spans
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (live[r]) atomicOr(&s_cov[r * tx4 + col[r]], 1ull << bit[r]);
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          low[r] = live[r] ? static_cast<uint32_t>(__popcll(s_cov[r * tx4 + col[r]] & ((1ull << bit[r]) - 1ull))) : 0u;
+        wave_sync();
+        // the windows' counts per column -> running positions (and the masks cleared)
+        for (int t = lane; t < tiles_x; t += kWave) {
+          uint32_t p = s_pos[t];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            s_off[r * tx4 + t] = p;
+            p += static_cast<uint32_t>(__popcll(s_cov[r * tx4 + t]));
+            s_cov[r * tx4 + t] = 0ull;
+          }
+          s_pos[t] = p;
+        }
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (live[r]) {
+            const uint32_t pos = s_off[r * tx4 + col[r]] + low[r];
+            if (pos < m) {
+              point_list[pos] = g[r];
+              if constexpr (kKeys)
+                keys[pos] = (static_cast<uint64_t>(t_row + col[r]) << 32) |
+                            static_cast<uint32_t>(dkey_of[g[r]] + dkey0);
+            }
+          }
+        }
+        wave_sync();  // the offsets are rewritten by the next batch
+      }
+    }
+    __syncthreads();  // the column positions are rewritten for the next chunk
+  }
+}
+
 static inline unsigned grid_for(int64_t n, int threads) {
   return static_cast<unsigned>((n + threads - 1) / threads);
 }
@@ -1041,24 +1724,78 @@ static EmitLayout emit_layout(int64_t m, int n_tiles) {
   return L;
 }
 
-// Rectangle binning: the depth ordering, the order and offsets, then the emission.
+// Span binning: row counts per depth chunk [tiles_y][n_chunks], row totals, the gathered
+// spans (depth order; at most m non-empty ones) with each chunk's (first slot, count) and the
+// slot counter, the row-sorted spans (plus each row's padding to a multiple of kSpanChunk),
+// column counts per span chunk, tile counts.
+static bool span_binning(int tiles_x, int tiles_y) { return tiles_x <= kSpanMaxDim && tiles_y <= kSpanMaxDim; }
+
+// Which fill a canvas and Gaussian count take: the span binning on canvases of at most
+// kSpanMaxDim tiles per side from kSpanMinGaussians Gaussians on (below that, the radix path was
+// measured faster: 1M Gaussians at 1297x840 bin in 127 us by radix and 152 us by spans, 3M at
+// 1957x1091 in 1.01 ms by radix and 0.81 ms by spans), unless flags force a path. The choice
+// needs no instance count, so the depth ordering knows beforehand whether the fill needs the
+// instance offsets.
+constexpr int64_t kSpanMinGaussians = 2000000;
+
+static bool use_spans(int64_t n, int tiles_x, int tiles_y, int flags) {
+  if (!span_binning(tiles_x, tiles_y) || (flags & GS_BIN_RADIX)) return false;
+  return (flags & GS_BIN_SPANS) || n >= kSpanMinGaussians;
+}
+
+// m instances fit the span path's 32-bit span positions (m plus every row's padding)
+static bool span_fits(int64_t m, int tiles_y) {
+  return m + static_cast<int64_t>(tiles_y) * kSpanChunk < (int64_t(1) << 32);
+}
+
+struct SpanLayout {
+  size_t rowhist, rowtot, gathered, chunk_info, counter, spans, colhist, tcnt, end;
+  int n_chunks;
+  int64_t gathered_cap, span_cap, chunk_cap;
+};
+
+static SpanLayout span_layout(int64_t n, int64_t m, int tiles_x, int tiles_y) {
+  SpanLayout L;
+  L.n_chunks = static_cast<int>((n + kRowChunk - 1) / kRowChunk);
+  L.gathered_cap = m;
+  L.span_cap = m + static_cast<int64_t>(tiles_y) * (kSpanChunk - 1);
+  L.chunk_cap = (L.span_cap + kSpanChunk - 1) / kSpanChunk;
+  size_t o = 0;
+  L.rowhist = o; o += align_up(static_cast<size_t>(tiles_y) * L.n_chunks * 4);
+  L.rowtot = o; o += align_up(static_cast<size_t>(tiles_y) * 4);
+  L.gathered = o; o += align_up(static_cast<size_t>(L.gathered_cap) * 8);
+  L.chunk_info = o; o += align_up(static_cast<size_t>(L.n_chunks) * 8);
+  L.counter = o; o += align_up(4);
+  L.spans = o; o += align_up(static_cast<size_t>(L.span_cap) * 8);
+  L.colhist = o; o += align_up(static_cast<size_t>(L.chunk_cap) * tiles_x * 4);
+  L.tcnt = o; o += align_up(static_cast<size_t>(tiles_x) * tiles_y * 4);
+  L.end = o;
+  return L;
+}
+
+// Workspace of the fill (emission or span binning) for n Gaussians and m instances.
+static size_t fill_ws(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags) {
+  return use_spans(n, tiles_x, tiles_y, flags) ? span_layout(n, m, tiles_x, tiles_y).end
+                                               : emit_layout(m, tiles_x * tiles_y).end;
+}
+
+// Rectangle binning: the depth ordering, the order and offsets, then the fill.
 struct RectLayout {
   size_t prep, order, offs, emit, end;
 };
 
-static RectLayout rect_layout(int64_t n, int64_t m, int n_tiles) {
+static RectLayout rect_layout(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags) {
   RectLayout L;
   size_t o = 0;
   L.prep = o; o += prep_layout(n).end;
   L.order = o; o += align_up(n * 4);
   L.offs = o; o += align_up((n + 1) * 4);
-  L.emit = o; o += emit_layout(m, n_tiles).end;
+  L.emit = o; o += fill_ws(n, m, tiles_x, tiles_y, flags);
   L.end = o;
   return L;
 }
 
 static size_t prep_ws(int64_t n) { return prep_layout(n).end; }
-static size_t emit_ws(int64_t m, int n_tiles) { return emit_layout(m, n_tiles).end; }
 
 // Stable order of the Gaussians by depth key (keys_in: precomputed 32-bit keys, else computed
 // from rec / depth / depth64; none of them: index order) and, if offsets is not NULL, the
@@ -1134,11 +1871,79 @@ static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t
                        dkey0, m, sorted_keys);
 }
 
+// Span binning of m > 0 instances (span_binning(tiles_x, tiles_y) holds): lists, ranges,
+// bucket offsets, optional sorted keys (dkey_of needed then).
+template <bool kRect>
+static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
+                      const uint32_t* order, int64_t n, int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
+                      uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets, uint32_t* bucket_offsets,
+                      uint32_t* list_header, char* ws, hipStream_t st) {
+  const SpanLayout L = span_layout(n, m, tiles_x, tiles_y);
+  uint32_t* rowhist = reinterpret_cast<uint32_t*>(ws + L.rowhist);
+  uint32_t* rowtot = reinterpret_cast<uint32_t*>(ws + L.rowtot);
+  uint2* gathered = reinterpret_cast<uint2*>(ws + L.gathered);
+  uint2* chunk_info = reinterpret_cast<uint2*>(ws + L.chunk_info);
+  uint32_t* counter = reinterpret_cast<uint32_t*>(ws + L.counter);
+  uint2* spans = reinterpret_cast<uint2*>(ws + L.spans);
+  uint32_t* colhist = reinterpret_cast<uint32_t*>(ws + L.colhist);
+  uint32_t* tcnt = reinterpret_cast<uint32_t*>(ws + L.tcnt);
+  const auto a4 = [](int v) { return (v + 3) & ~3; };
+  // LDS of the kernels (the layouts the kernels carve, in words)
+  const size_t lds_gather = static_cast<size_t>(a4(tiles_y) + kSpanWaves * (64 * 12 + 128)) * 4;
+  const size_t lds_place = static_cast<size_t>(a4(tiles_y + 1) + kSpanWaves * a4(tiles_y) * 3) * 4;
+  const int tx4 = a4(tiles_x + 1);
+  const size_t lds_ccount = (static_cast<size_t>(a4(tiles_y + 1)) + kSpanWaves * tx4) * 4;
+  // placement windows per batch: as many as keep the LDS within 64 KB
+  const int R = tiles_x <= 64 ? 8 : tiles_x <= 128 ? 4 : tiles_x <= 256 ? 2 : 1;
+  const size_t lds_cwrite =
+      (static_cast<size_t>(a4(tiles_y + 1)) + kSpanWaves * tx4 +
+       kSpanWaves * (R * 3 * tx4 + 2 * kWaveSpans + (kWaveSpans + 4) + kOwnerTable / 4)) * 4;
+  const unsigned g_rows = static_cast<unsigned>(L.n_chunks);  // a workgroup per chunk
+  // the column kernels deal their chunks to the 8 XCDs in contiguous ranges: a multiple of 8
+  // workgroups
+  const unsigned g_cols = std::min<unsigned>((static_cast<unsigned>(L.chunk_cap) + 7u) & ~7u, 2048u);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, counter, int64_t(1), 0u);
+  hipLaunchKernelGGL(span_gather_kernel<kRect>, dim3(g_rows), dim3(256), lds_gather, st, rec, rects, order, n,
+                     L.n_chunks, tiles_x, tiles_y, rowhist, chunk_info, gathered, L.gathered_cap, counter);
+  hipLaunchKernelGGL(rs_rowscan_kernel, dim3(tiles_y), dim3(kScanThreads), 0, st, rowhist, L.n_chunks, rowtot);
+  hipLaunchKernelGGL(span_place_kernel, dim3(g_rows), dim3(256), lds_place, st, gathered, chunk_info, rowhist, rowtot,
+                     L.n_chunks, tiles_y, spans, L.gathered_cap, L.span_cap);
+  hipLaunchKernelGGL(span_col_count_kernel, dim3(g_cols), dim3(256), lds_ccount, st, spans, rowtot, tiles_x, tiles_y,
+                     L.span_cap, L.chunk_cap, colhist);
+  hipLaunchKernelGGL(span_col_scan_kernel, dim3(tiles_y), dim3(kColScanThreads), 0, st, colhist, rowtot, tiles_x,
+                     tiles_y, L.chunk_cap, tcnt);
+  hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(kBoThreads), 0, st, tcnt, tiles_x * tiles_y, ranges,
+                     bucket_offsets, tile_offsets, list_header);
+#define GS_SPAN_WRITE(KEYS, RR)                                                                                     \
+  hipLaunchKernelGGL((span_col_write_kernel<KEYS, RR>), dim3(g_cols), dim3(256), lds_cwrite, st, spans, rowtot,     \
+                     colhist, ranges, tiles_x, tiles_y, L.span_cap, L.chunk_cap, m, point_list, sorted_keys, dkey_of, \
+                     dkey0)
+  if (sorted_keys) {
+    if (R == 8) GS_SPAN_WRITE(true, 8); else if (R == 4) GS_SPAN_WRITE(true, 4);
+    else if (R == 2) GS_SPAN_WRITE(true, 2); else GS_SPAN_WRITE(true, 1);
+  } else {
+    if (R == 8) GS_SPAN_WRITE(false, 8); else if (R == 4) GS_SPAN_WRITE(false, 4);
+    else if (R == 2) GS_SPAN_WRITE(false, 2); else GS_SPAN_WRITE(false, 1);
+  }
+#undef GS_SPAN_WRITE
+}
+
 static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
                      const uint32_t* order,
-                     const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles, int64_t m,
+                     const uint32_t* offsets, int64_t n, int tiles_x, int tiles_y, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
-                     uint32_t* bucket_offsets, uint32_t* list_header, char* ws, hipStream_t st) {
+                     uint32_t* bucket_offsets, uint32_t* list_header, int flags, char* ws, hipStream_t st) {
+  const int n_tiles = tiles_x * tiles_y;
+  if (m > 0 && use_spans(n, tiles_x, tiles_y, flags)) {
+    // (gs_bin_fill_* reject an m beyond span_fits for this path)
+    if (rects)
+      bin_spans<true>(rec, rects, dkey_of, dkey0, order, n, tiles_x, tiles_y, m, sorted_keys, point_list, ranges,
+                      tile_offsets, bucket_offsets, list_header, ws, st);
+    else
+      bin_spans<false>(rec, rects, dkey_of, dkey0, order, n, tiles_x, tiles_y, m, sorted_keys, point_list, ranges,
+                       tile_offsets, bucket_offsets, list_header, ws, st);
+    return;
+  }
   const EmitLayout L = emit_layout(m, n_tiles);
   const int tile_bits = L.tile_bits;
   if (m > 0) {
@@ -1205,9 +2010,9 @@ extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_t
                                  uint32_t* offsets, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (int e = check_cam(cam)) return e;
-  GS_REQUIRE(n >= 0 && n < (int64_t(1) << 32) && offsets, GS_ERR_ARG, "invalid bin_prepare arguments");
-  GS_REQUIRE(n == 0 || (tiles_touched && order && (depth_keys || splat_rec)), GS_ERR_ARG,
-             "null pointer argument");
+  GS_REQUIRE(n >= 0 && n < (int64_t(1) << 32), GS_ERR_ARG, "invalid bin_prepare arguments");
+  GS_REQUIRE(n == 0 || (order && (depth_keys || splat_rec) && (tiles_touched || (!offsets && depth_keys))),
+             GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
   const size_t need = prep_ws(n);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
@@ -1218,12 +2023,19 @@ extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_t
   return check_launch("bin_prepare_3d");
 }
 
-extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles) {
+extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags) {
   n = n < 0 ? 0 : n;
-  n_tiles = n_tiles < 1 ? 1 : n_tiles;
+  tiles_x = tiles_x < 1 ? 1 : tiles_x;
+  tiles_y = tiles_y < 1 ? 1 : tiles_y;
   m = m < 0 ? 0 : m;
   // the rectangle binning runs the depth ordering itself: its scratch, order and offsets too
-  return rect_layout(n, m, n_tiles).end;
+  return rect_layout(n, m, tiles_x, tiles_y, flags).end;
+}
+
+extern "C" int gs_bin_needs_offsets(int64_t n, const gs_camera* cam) {
+  if (!cam) return 1;
+  const CamK k = make_cam(*cam);
+  return use_spans(n, k.tiles_x, k.tiles_y, cam->flags) ? 0 : 1;
 }
 
 extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
@@ -1238,17 +2050,19 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const CamK k = make_cam(*cam);
   GS_REQUIRE(static_cast<int64_t>(k.tiles_x) * k.tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
-  const int n_tiles = k.tiles_x * k.tiles_y;
-  const size_t need = emit_ws(m, n_tiles);
+  const bool spans = use_spans(n, k.tiles_x, k.tiles_y, cam->flags);
+  GS_REQUIRE(!spans || span_fits(m, k.tiles_y), GS_ERR_ARG, "%lld instances exceed the 32-bit span positions",
+             static_cast<long long>(m));
+  const size_t need = fill_ws(n, m, k.tiles_x, k.tiles_y, cam->flags);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
-  GS_REQUIRE(m == 0 || (splat_rec && order && offsets && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(m == 0 || (splat_rec && order && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(m == 0 || offsets || spans, GS_ERR_ARG, "this fill emits instances: it needs the offsets");
   GS_REQUIRE(!(sorted_keys && m > 0 && !depth_keys), GS_ERR_ARG, "sorted_keys need depth_keys");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
   bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, order, offsets, n, k.tiles_x,
-           n_tiles,
-           m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, bucket_list, static_cast<char*>(workspace),
-           as_stream(stream));
+           k.tiles_y, m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, bucket_list, cam->flags,
+           static_cast<char*>(workspace), as_stream(stream));
   return check_launch("bin_fill_3d");
 }
 
@@ -1267,7 +2081,7 @@ extern "C" int gs_rect_counts(const int32_t* rects, int64_t n, int tiles_x, int 
 extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int depth_dtype,
                                 const uint32_t* counts, int64_t n, int tiles_x, int tiles_y, int64_t m,
                                 uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
-                                uint32_t* tile_offsets, uint32_t* bucket_offsets, uint32_t* order,
+                                uint32_t* tile_offsets, uint32_t* bucket_offsets, uint32_t* order, int flags,
                                 void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   GS_REQUIRE(n >= 0 && m >= 0 && m < (int64_t(1) << 32) && tiles_x > 0 && tiles_y > 0, GS_ERR_ARG,
@@ -1275,8 +2089,10 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   GS_REQUIRE(static_cast<int64_t>(tiles_x) * tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
   GS_REQUIRE(depth_dtype == GS_FLOAT32 || depth_dtype == GS_FLOAT64, GS_ERR_ARG, "invalid depth dtype");
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
-  const int n_tiles = tiles_x * tiles_y;
-  const size_t need = gs_bin_workspace_size(n, m, n_tiles);
+  const bool spans = use_spans(n, tiles_x, tiles_y, flags);
+  GS_REQUIRE(!spans || span_fits(m, tiles_y), GS_ERR_ARG, "%lld instances exceed the 32-bit span positions",
+             static_cast<long long>(m));
+  const size_t need = gs_bin_workspace_size(n, m, tiles_x, tiles_y, flags);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
   GS_REQUIRE(m == 0 || (rects && counts && point_list), GS_ERR_ARG, "null pointer argument");
@@ -1287,18 +2103,20 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
   const double* d64 = depth_dtype == GS_FLOAT64 ? static_cast<const double*>(depth) : nullptr;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
-  const RectLayout L = rect_layout(n, m, n_tiles);
+  const RectLayout L = rect_layout(n, m, tiles_x, tiles_y, flags);
   char* prep = ws + L.prep;
   uint32_t* dkeys = reinterpret_cast<uint32_t*>(prep + prep_layout(n).dkeys);
   uint32_t* ord = order ? order : reinterpret_cast<uint32_t*>(ws + L.order);
   uint32_t* offs = reinterpret_cast<uint32_t*>(ws + L.offs);
   if (n > 0 && (m > 0 || order)) {
-    bin_prepare(nullptr, d32, d64, nullptr, 32, counts, n, ord, m > 0 ? offs : nullptr, prep, st);
+    // the span binning reads the order only; the emission needs the instance offsets too
+    const bool need_offs = m > 0 && !spans;
+    bin_prepare(nullptr, d32, d64, nullptr, 32, counts, n, ord, need_offs ? offs : nullptr, prep, st);
     if (sorted_keys && m > 0 && !d32)  // index order: the depth part of the keys is 0
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
   }
-  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, n_tiles, m, sorted_keys,
-           point_list, ranges, tile_offsets, bucket_offsets, nullptr, ws + L.emit, st);
+  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, tiles_y, m, sorted_keys,
+           point_list, ranges, tile_offsets, bucket_offsets, nullptr, flags, ws + L.emit, st);
   return check_launch("bin_fill_rect");
 }
 

@@ -390,6 +390,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
       r.c = make_float4(col[0], col[1], col[2], __uint_as_float(mask));
       r.d = bnd;
       rec[i] = r;
+    } else {
+      rec[i].d = make_int4(0, -1, 0, -1);  // empty bounds: the binning skips the record
     }
   }
   if (wave_counts) {

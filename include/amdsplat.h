@@ -61,6 +61,15 @@ typedef struct gs_camera {
  * filter), and its gradient flows through the compensation factor into the covariance. */
 #define GS_CAM_PROPER_ANTIALIASING 1
 
+/* Binning path (gs_camera.flags for the 3D entry points, the flags argument of
+ * gs_bin_fill_rect): by default the span binning is taken from GS_BIN_SPAN_MIN_GAUSSIANS
+ * Gaussians on canvases of at most GS_BIN_SPAN_MAX_TILES tiles per side, the radix path
+ * otherwise; these bits force one of them (GS_BIN_SPANS only where the canvas allows it). Both
+ * give the same lists, ranges and bucket offsets. */
+#define GS_BIN_SPANS 2
+#define GS_BIN_RADIX 4
+#define GS_BIN_SPAN_MIN_GAUSSIANS 2000000
+
 /* Thread-local message of the last failed call. */
 const char* gs_last_error(void);
 
@@ -94,7 +103,8 @@ int gs_sum_u32(const uint32_t* in, int64_t n, uint64_t* out, void* stream);
  *   sh_coeffs in {1,4,9,16} and (sh_degree+1)^2 <= sh_coeffs; or, with sh_rest not NULL, the
  *   DC coefficients sh [n, 1, 3] and the rest sh_rest [n, sh_coeffs - 1, 3] as two arrays (the
  *   sh_coefficients_0 / sh_coefficients_rest split of Faster-GS's model).
- *   out: splat_rec [n,16] floats (16-byte aligned), tiles_touched [n] uint32, and (may be
+ *   out: splat_rec [n,16] floats (16-byte aligned; a culled Gaussian's record gets only the
+ *   empty bounds (0, -1, 0, -1) in its last 4 words), tiles_touched [n] uint32, and (may be
  *   NULL) depth_keys [n] uint32: the orderable bits of the view depth of a Gaussian with
  *   tiles, 0xffffffff for a culled one (the keys gs_bin_prepare_3d sorts by).
  *   wave_counts (may be NULL): [ceil(n / 64)] uint32, the tiles touched by each group of 64
@@ -115,18 +125,26 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  * visible in results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:10-31).
  * Produces the stable order of instances by (tile, depth, Gaussian index) -- the order of a
  * stable sort of 64-bit keys (tile << 32 | orderable depth bits) over instances emitted in
- * Gaussian-index order -- in two levels: a stable radix sort of the Gaussians by depth, then a
- * stable radix sort by tile of the instances emitted in that order.
+ * Gaussian-index order. First a stable radix sort of the Gaussians by depth; then either the
+ * instances are emitted in depth order and stably radix-sorted by tile (radix path), or two
+ * counting passes run over the Gaussians' row spans (the run of tiles a Gaussian touches in one
+ * tile row): by tile row over the Gaussians in depth order, then by column within each row,
+ * which writes every instance once (span binning; see GS_BIN_SPANS for which is taken).
  *
  * gs_bin_prepare_3d: depth ordering.
  *   depth_keys [n] from gs_preprocess_fwd with the same camera (order keys of the view depth
  *   relative to the near plane's, culled Gaussians after every visible one, so the sort reads
- *   only as many bits as the near/far range needs), or NULL (then computed from splat_rec).
+ *   only as many bits as the near/far range needs), or NULL (then computed from splat_rec and
+ *   tiles_touched).
  *   out: order [n]        Gaussian indices by depth key, stable (culled Gaussians last)
- *        offsets [n + 1]  exclusive scan of tiles_touched[order[j]]; offsets[n] = m, the
- *                         number of instances (the caller reads it)
+ *        offsets [n + 1]  (may be NULL: gs_bin_fill_3d needs them only on the radix path,
+ *                         gs_bin_needs_offsets(n, cam)) exclusive scan of tiles_touched[order[j]];
+ *                         offsets[n] = m, the number of instances
+ *   tiles_touched may be NULL when offsets is NULL and depth_keys is given.
  *   Workspace from gs_bin_prepare_workspace_size(n).
- * gs_bin_fill_3d: emission, tile sort, ranges, bucket offsets. Writes
+ * gs_bin_fill_3d: tile lists, ranges, bucket offsets. splat_rec as gs_preprocess_fwd wrote it
+ *   (a culled Gaussian's record holds the empty bounds (0, -1, 0, -1)); m = the sum of the
+ *   preprocess's wave_counts. Writes
  *   point_list [m]        Gaussian index per instance, tile-major, front to back
  *   sorted_keys [m]       the 64-bit keys in that order (may be NULL: not needed downstream;
  *                         needs depth_keys)
@@ -134,13 +152,16 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *   bucket_offsets [T+1]  exclusive scan of ceil(len/32); bucket_offsets[T] = number of buckets
  *   bucket_list (may be NULL): the list gs_blend_fwd_3d appends to; its header is cleared
  *                         here, so that call can take GS_BLEND_LIST_CLEARED
- *   Workspace from gs_bin_workspace_size(n, m, T).
+ *   offsets: as gs_bin_prepare_3d wrote them, or NULL when gs_bin_needs_offsets(n, cam) is 0.
+ *   Workspace from gs_bin_workspace_size(n, m, tiles_x, tiles_y, cam->flags).
  * ------------------------------------------------------------------------------------- */
+#define GS_BIN_SPAN_MAX_TILES 512
 size_t gs_bin_prepare_workspace_size(int64_t n);
 int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched, const uint32_t* depth_keys,
                       int64_t n, const gs_camera* cam, uint32_t* order, uint32_t* offsets,
                       void* workspace, size_t workspace_bytes, void* stream);
-size_t gs_bin_workspace_size(int64_t n, int64_t m, int n_tiles);
+size_t gs_bin_workspace_size(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags);
+int gs_bin_needs_offsets(int64_t n, const gs_camera* cam); /* 1 when the fill takes the radix path */
 int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
                    const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
                    uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
@@ -154,13 +175,14 @@ int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uin
  * order); counts from gs2d_rects_toy / gs2d_rects_phase0 / gs_rect_counts. Outputs as
  * gs_bin_fill_3d, plus (each may be NULL) tile_offsets [T+1] (CSR form of ranges) and
  * order [n] = the stable argsort of depth (toy2d Bins.order). sorted_keys needs a float32
- * depth. Ranges of empty tiles are empty ranges at their CSR position. */
+ * depth. Ranges of empty tiles are empty ranges at their CSR position. flags: GS_BIN_* bits.
+ * Workspace from gs_bin_workspace_size(n, m, tiles_x, tiles_y, flags). */
 int gs_rect_counts(const int32_t* rects, int64_t n, int tiles_x, int tiles_y, uint32_t* counts,
                    void* stream);
 int gs_bin_fill_rect(const int32_t* rects, const void* depth, int depth_dtype, const uint32_t* counts,
                      int64_t n, int tiles_x, int tiles_y, int64_t m, uint64_t* sorted_keys,
                      uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
-                     uint32_t* bucket_offsets, uint32_t* order, void* workspace,
+                     uint32_t* bucket_offsets, uint32_t* order, int flags, void* workspace,
                      size_t workspace_bytes, void* stream);
 
 /* bucket_to_tile[b] = tile of bucket b, for b < bucket_offsets[n_tiles] (read on device);

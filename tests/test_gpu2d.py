@@ -19,6 +19,7 @@ import gs2d
 import splat2d
 from gs2d.params import Gaussians2D, radii_from_cov
 from splat2d import ops as P0
+from amdsplat import raster2d as R2
 
 pytestmark = pytest.mark.gpu
 
@@ -120,9 +121,12 @@ def test_gs2d_forward_matches_oracle_bit_for_bit(name):
                     assert np.abs(ck[b, t] - rck[b, t]).max() <= 1e-6
 
 
-def test_gs2d_bench_scene_against_oracle():
+@pytest.mark.parametrize("binning", ["spans", "radix"])
+def test_gs2d_bench_scene_against_oracle(binning, monkeypatch):
     """512x512, 50k Gaussians of the reference benchmark: pair / bucket counts of its results
-    file, bit-exact lists and counts, forward within 1e-5, gradients within 1e-4 (atomic order)."""
+    file, bit-exact lists and counts, forward within 1e-5, gradients within 1e-4 (atomic order);
+    with either tile binning."""
+    monkeypatch.setattr(R2, "BINNING", binning)
     rows = json.loads((GOLD / "toy2d_bench_counts.json").read_text())["rows"]
     row = rows[1]
     S, n = row["size"], row["n"]
@@ -149,11 +153,14 @@ def test_gs2d_bench_scene_against_oracle():
         assert rel(gg.reshape(-1, len(cols)), gr[:, list(cols)]) < 1e-4
 
 
-def test_gs2d_sparse_wide_canvas_ranges():
+@pytest.mark.parametrize("binning", ["spans", "radix"])
+def test_gs2d_sparse_wide_canvas_ranges(binning, monkeypatch):
     """A 2048x1280 canvas (10240 tiles: more than one 8192-tile chunk of the bucket-offset scan)
     with two clusters of small Gaussians, so most tiles (the first and last ones included) hold
-    no instance: the ranges the tile sort's last pass takes by atomic min / max, the empty
-    tiles' positions, the bucket offsets and the lists equal the oracle's bit for bit."""
+    no instance: the ranges (from the tile sort's last pass by atomic min / max, or from the span
+    binning's tile counts), the empty tiles' positions, the bucket offsets and the lists equal the
+    oracle's bit for bit."""
+    monkeypatch.setattr(R2, "BINNING", binning)
     W, H = 2048, 1280
     gen = torch.Generator().manual_seed(7)
     n = 3000
@@ -172,10 +179,12 @@ def test_gs2d_sparse_wide_canvas_ranges():
     assert np.array_equal(bins.offsets_ext().cpu().numpy().astype(np.int64), boff.astype(np.int64))
 
 
+@pytest.mark.parametrize("binning", ["spans", "radix"])
 @pytest.mark.parametrize("size", [(16, 16), (12, 9)])
-def test_gs2d_single_tile_canvas(size):
-    """A canvas of one tile: the tile sort has no pass, so the ranges come from the key-change
-    kernel; lists and ranges equal the oracle's."""
+def test_gs2d_single_tile_canvas(size, binning, monkeypatch):
+    """A canvas of one tile (on the radix path the tile sort has no pass, so the ranges come from
+    the key-change kernel); lists and ranges equal the oracle's."""
+    monkeypatch.setattr(R2, "BINNING", binning)
     W, H = size
     gen = torch.Generator().manual_seed(3)
     n = 40

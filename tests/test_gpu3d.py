@@ -88,6 +88,15 @@ def test_forward_matches_oracle(name):
     check_forward(make(name))
 
 
+@pytest.mark.parametrize("binning", ["spans", "radix"])
+@pytest.mark.parametrize("name", list(SCENES))
+def test_both_binning_paths_match_oracle(name, binning):
+    """The span binning and the radix path (each forced, whatever the scene's size) give the
+    oracle's keys, lists, ranges and bucket offsets bit for bit."""
+    sc = make(name, seed=7)
+    check_forward(sc, dataclasses.replace(sc.cameras[0], binning=binning))
+
+
 @pytest.mark.parametrize("name", ["tiny", "small_splats", "heavy_overlap"])
 def test_proper_antialiasing_forward_matches_oracle(name):
     sc = make(name, seed=4)
@@ -103,7 +112,7 @@ def check_forward(sc, cam=None):
     assert (np_(fs.touched).astype(np.uint32) == ref["touched"]).all(), "tiles touched differ"
     assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref["rec"][vis].view(np.uint32)), "splat records differ"
     assert fs.m == len(ref["keys"])
-    assert int(fs.offsets[-1]) == fs.m, "early instance count differs from the scan's total"
+    assert fs.m == int(fs.touched.long().sum()), "early instance count differs from the tiles touched"
     assert np.array_equal(np_(fs.keys).view(np.uint64), ref["keys"]), "sorted keys differ"
     assert np.array_equal(np_(fs.point_list).view(np.uint32), ref["point_list"]), "point list differs"
     assert np.array_equal(np_(fs.ranges).view(np.uint32), ref["ranges"]), "tile ranges differ"
@@ -470,10 +479,10 @@ def test_backward_over_long_bucket_table_equals_table_walk():
 @pytest.mark.parametrize("n", [1, 63, 64, 4097])
 def test_instance_count_from_wave_counts(n):
     """The host's instance count (the total of the preprocess's per-wavefront counts, copied on a
-    side stream) equals the depth-ordered scan's total and the sum of tiles touched, at ragged n."""
+    side stream) equals the sum of tiles touched and the tile ranges' total, at ragged n."""
     sc = scenes.small_scene(n, 160, 120, seed=n, scale=(0.01, 0.2))
     p, fs = gpu_forward(sc, 3)
-    assert fs.m == int(fs.offsets[-1]) == int(fs.touched.long().sum())
+    assert fs.m == int(fs.touched.long().sum()) == int(fs.ranges[-1, 1])
 
 
 def test_forward_clears_grad2d_and_bucket_table():

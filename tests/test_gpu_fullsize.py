@@ -29,6 +29,8 @@ by det^2 (the reference's own finding, results/phase1/macro_backward.md:52-63). 
 twice that amplification, measured by running the oracle's chain on the GPU's screen-space
 gradients; both numbers are printed.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -97,10 +99,10 @@ def check_binning(fs, ref):
     assert np.array_equal(np_(fs.bucket_offsets).view(np.uint32), ref["bucket_offsets"]), "bucket offsets differ"
 
 
-@pytest.mark.parametrize("pose", [0, 4])
-def test_sh3_1m_full_frame_forward_backward(sh3_1m, pose):
+@pytest.mark.parametrize("pose,binning", [(0, "auto"), (4, "spans")])
+def test_sh3_1m_full_frame_forward_backward(sh3_1m, pose, binning):
     sc = sh3_1m
-    cam = sc.cameras[pose]
+    cam = dataclasses.replace(sc.cameras[pose], binning=binning)
     host = [t.numpy() for t in sc.params()]
     p = [t.cuda().contiguous() for t in sc.params()]
     fs = R.forward_pass(*p, cam, sh_degree=3, keep_keys=True)
@@ -232,6 +234,11 @@ def test_sh3_3m_binning_and_sampled_tile_backward():
     print(f"[3M] visible {int(vis.sum())}, instances {fs.m}, buckets {int(boff[-1])}", flush=True)
     check_binning(fs, dict(keys=keys, point_list=pl, ranges=ranges, bucket_offsets=boff))
     del keys
+    # the radix path (this size takes the span binning by default) gives the same lists
+    fr = R.forward_pass(*p, dataclasses.replace(cam, binning="radix"), sh_degree=3)
+    assert torch.equal(fr.point_list, fs.point_list) and torch.equal(fr.ranges, fs.ranges)
+    assert torch.equal(fr.bucket_offsets, fs.bucket_offsets)
+    del fr
     # 64 tiles: the 16 longest lists and 48 at random; every other tile gets an empty range
     T = cam.n_tiles
     length = (ranges[:, 1] - ranges[:, 0]).astype(np.int64)

@@ -63,6 +63,11 @@ def test_depth_order_is_the_stable_argsort(n, kind):
     scan = np.zeros(n + 1, np.int64)
     np.cumsum(counts[want], out=scan[1:])
     assert np.array_equal(offsets.cpu().numpy().astype(np.int64), scan)
+    if n == 100_003:  # without the offsets (nor the counts): the same order
+        order2 = torch.empty_like(order)
+        call("gs_bin_prepare_3d", None, None, ptr(kd), n, cam, ptr(order2), None, ptr(ws), ws.numel(),
+             _lib.stream_handle(dev))
+        assert torch.equal(order2, order)
 
 
 def numpy_rect_binning(rects, depth, tiles_x, T):
@@ -90,11 +95,19 @@ def numpy_rect_binning(rects, depth, tiles_x, T):
 
 
 @pytest.mark.parametrize("W,H,n,rmax", [
-    (333, 250, 5_000, 5),           # 336 tiles: 9 bits, one pass
-    (1297, 840, 400_000, 5),        # 4346 tiles: 13 bits in two passes of 7
-    (2048, 2048, 200_000, 16),      # 16384 tiles: 14 bits, ~10M instances, 16 rounds per tile
+    (333, 250, 5_000, 5),           # 336 tiles
+    (1297, 840, 400_000, 5),        # 4346 tiles
+    (2048, 2048, 200_000, 16),      # 16384 tiles, ~10M instances
+    (8192, 40, 60_000, 40),         # 512 x 3 tiles: the widest canvas of the span binning
+    (40, 8192, 60_000, 40),         # 3 x 512 tiles: the tallest
+    (8208, 40, 60_000, 40),         # 513 tiles wide: instances emitted and radix-sorted by tile
+    (40, 8208, 60_000, 40),         # 513 tiles tall: the same
+    (2000, 1200, 30_000, 200),      # wide rectangles: spans of up to 125 tiles
+    (17, 17, 3_000, 3),             # 2 x 2 tiles
+    (16, 16, 1_000, 2),             # one tile
 ])
-def test_rect_binning_matches_the_stable_sort(W, H, n, rmax):
+@pytest.mark.parametrize("binning", ["spans", "radix"])
+def test_rect_binning_matches_the_stable_sort(W, H, n, rmax, binning):
     rng = np.random.default_rng(W * H + n)
     tiles_x, tiles_y = (W + 15) // 16, (H + 15) // 16
     T = tiles_x * tiles_y
@@ -108,7 +121,7 @@ def test_rect_binning_matches_the_stable_sort(W, H, n, rmax):
     rd = torch.from_numpy(rects).to(dev).contiguous()
     counts = torch.empty(n, dtype=torch.int32, device=dev)
     call("gs_rect_counts", ptr(rd), n, tiles_x, tiles_y, ptr(counts), _lib.stream_handle(dev))
-    rb = R2.bin_rects(rd, counts, torch.from_numpy(depth).to(dev), W, H)
+    rb = R2.bin_rects(rd, counts, torch.from_numpy(depth).to(dev), W, H, binning=binning)
     pl, ranges, boff = numpy_rect_binning(rects, depth, tiles_x, T)
     assert len(pl) == rb.point_list.numel()
     assert np.array_equal(rb.point_list.cpu().numpy(), pl)
