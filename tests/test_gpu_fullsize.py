@@ -177,17 +177,20 @@ def test_sh3_1m_training_step(sh3_1m):
     got = [params["means"].grad, params["scales"].grad, params["quats"].grad, params["opacity"].grad,
            torch.cat([params["sh_dc"].grad, params["sh_rest"].grad], 1)]
     want = O.preprocess_bwd(*host, cam, 3, ref["rec"], ref["touched"], g2_full)
-    chain = O.preprocess_bwd(*host, cam, 3, ref["rec"], ref["touched"],
-                             np_(R.backward_pass(R.forward_pass(*[t.cuda().contiguous() for t in sc.params()], cam,
-                                                                sh_degree=3),
-                                                 *[t.cuda().contiguous() for t in sc.params()], img.grad,
-                                                 abs_grad=False)[5]))
+    # the oracle's chain on this very backward's screen-space gradients (the autograd node keeps
+    # them): the float32 atomics' order differs from run to run, and so does what the chain
+    # makes of it, so the amplification is measured on the same run
+    got2_full = np_(img.grad_fn.grad2d)
+    for k, name in enumerate(GRAD2D_COLS[:9]):
+        assert D.rel_err(got2_full[:, k], g2_full[:, k]) < GRAD2D_TOL, f"train grad2d (full image gradient) {name}"
+    chain = O.preprocess_bwd(*host, cam, 3, ref["rec"], ref["touched"], got2_full)
     for name, a, w, c in zip(PARAMS, got, want, chain):
         a = np_(a).reshape(w.shape)
-        e, e_amp = D.rel_err(a, w), D.rel_err(c, w)
+        e, e_amp, e_chain = D.rel_err(a, w), D.rel_err(c, w), D.rel_err(a, c)
         bound = max(GRAD_TOL, 2.0 * e_amp)
-        print(f"[train 1M] grad {name}: end to end {e:.2e} (bound {bound:.1e}); the chain's amplification of the "
-              f"grad2d rounding {e_amp:.2e}", flush=True)
+        print(f"[train 1M] grad {name}: end to end {e:.2e} (bound {bound:.1e}); preprocess backward vs the oracle's "
+              f"chain {e_chain:.2e}; the chain's amplification of the grad2d rounding {e_amp:.2e}", flush=True)
+        assert e_chain < GRAD2D_TOL, f"{name}: preprocess backward {e_chain:.2e}"
         assert e < bound, f"{name}: {e:.2e}"
     # (3) fused Adam, dense and masked, from the step's own gradients: bit-exact against optim.c
     vis = aux["visibility"]
