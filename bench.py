@@ -127,25 +127,48 @@ def probes() -> dict:
 # ---------------------------------------------------------------------------------------
 # 3D workloads
 # ---------------------------------------------------------------------------------------
+def span_count(fs) -> int:
+    """Row spans of a forward (distinct (Gaussian, tile row) pairs of its instances): the unit
+    of the span binning's traffic."""
+    import torch
+
+    rg = fs.ranges.long()
+    T, tx, ty = fs.cam.n_tiles, fs.cam.tiles_x, fs.cam.tiles_y
+    tile = torch.repeat_interleave(torch.arange(T, device=rg.device), rg[:, 1] - rg[:, 0])
+    key = fs.point_list.long() * ty + tile // tx
+    return int(torch.unique(key).numel())
+
+
 def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, ckpt_written,
-                atomics_per_pair=9):
+                atomics_per_pair=9, spans=None):
     """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
-    written once (fp32)."""
+    written once (fp32). spans: the row-span count when the forward took the span binning (its
+    instance offsets are None), else None."""
     n, m, K = fs.n, fs.m, fs.sh_coeffs
     T = fs.cam.n_tiles
     P = fs.cam.width * fs.cam.height
     B = int(fs.bucket_offsets[-1].item())
+    if spans is None:
+        # 3 radix passes over N (histogram read 4 B, key+value read and write 16 B), the counts
+        # gathered into depth order (read + write), the scan (counts read, offsets written)
+        depth = 3 * 20 * n + 8 * n + 8 * n
+        # emission (48 B of the record of the visible, order and offset per Gaussian, key+value
+        # per instance), tile sort pass 1 (histogram 4, key+value read and write 16) and pass 2
+        # (histogram 4, key+value read 8, value write 4), ranges and bucket offsets per tile
+        binning = 48 * n_visible + 8 * n + 8 * m + 20 * m + 16 * m + 20 * T + 4 * B
+    else:
+        # 3 radix passes over N
+        depth = 3 * 20 * n
+        # order 4 B and 48 B of the record of the visible per Gaussian; per span: gathered (8 B
+        # written, read), placed by row (8 B written), read by the column count and the placement
+        # (8 B each); the point list 4 B per instance; tile counts, ranges, bucket offsets
+        binning = 4 * n + 48 * n_visible + 40 * spans + 4 * m + 20 * T + 4 * B
     return {
         # params 44 B/Gaussian + tiles_touched and depth key 8 B; SH 12 K B and the 64 B record
         # per visible one
         "preprocess": 44 * n + 8 * n + n_visible * (12 * K + 64),
-        # 3 radix passes over N (histogram read 4 B, key+value read and write 16 B), the counts
-        # gathered into depth order (read + write), the scan (counts read, offsets written)
-        "depth_order": 3 * 20 * n + 8 * n + 8 * n,
-        # emission (48 B of the record of the visible, order and offset per Gaussian, key+value
-        # per instance), tile sort pass 1 (histogram 4, key+value read and write 16) and pass 2
-        # (histogram 4, key+value read 8, value write 4), ranges and bucket offsets per tile
-        "binning": 48 * n_visible + 8 * n + 8 * m + 20 * m + 16 * m + 20 * T + 4 * B,
+        "depth_order": depth,
+        "binning": binning,
         # per staged list entry: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4;
         # the checkpoints written (4 KiB per bucket reached); tile max, bucket_to_tile, and the
         # backward's screen-space gradient buffer the forward zeroes (48 B per Gaussian)
@@ -469,11 +492,13 @@ def bench_3d(args, ceilings) -> dict:
         ab, ss, stg, ckw = bucket_stats(fs)
         up = int(ctr[0].item()) // 9
         ev = int(ctr[2].item())
+        spans = span_count(fs) if fs.offsets is None else None
         per_pose.append({"visible": nv, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
                          "active_buckets": ab, "bucket_splat_steps": ss, "staged_entries": stg,
                          "ckpt_written": ckw, "reduced_bucket_splats": up, "bwd_pair_evals": ev,
                          "bwd_valu_ops": OPS_PER_PAIR * ev + OPS_PER_STEP_LANE * 64 * ss + OPS_PER_REDUCTION * up,
-                         "bytes": stage_bytes(fs, nv, ab, ss, up, stg, ckw)})
+                         **({"row_spans": spans} if spans is not None else {}),
+                         "bytes": stage_bytes(fs, nv, ab, ss, up, stg, ckw, spans=spans)})
     counts = {k2: round(statistics.mean(pp[k2] for pp in per_pose)) for k2 in per_pose[0] if k2 != "bytes"}
     sb = {k2: statistics.mean(pp["bytes"][k2] for pp in per_pose) for k2 in per_pose[0]["bytes"]}
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
@@ -530,6 +555,7 @@ def bench_3d(args, ceilings) -> dict:
                                f"{fs_cam.width}x{fs_cam.height}, fwd+bwd per view through rasterize(...) and "
                                f"autograd, {views}",
                    "gaussians": scene.n, "width": fs_cam.width, "height": fs_cam.height,
+                   "tile_binning": "spans" if "row_spans" in per_pose[0] else "radix",
                    "parallelism": "single GPU"},
         "low_level_ms_per_step": round(low_ms, 4),
         "stage_ms": {k2: round(v, 4) for k2, v in stage_ms.items()},
