@@ -57,7 +57,7 @@ class Camera:
     near: float = 0.01
     far: float = 100.0
     proper_antialiasing: bool = False
-    binning: str = "auto"  # "auto", "spans" or "radix": which tile binning the forward takes
+    binning: str = "auto"  # "auto", "spans", "radix" or "local": which tile binning the forward takes
 
     @staticmethod
     def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0,
@@ -95,9 +95,9 @@ class ForwardState:
     sh_degree: int
     rec: torch.Tensor            # [n, 16] splat records
     touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
-    order: torch.Tensor          # [n] int32 Gaussians by depth (culled last)
-    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets in that order ([n] = m), or None
-    #                               where the fill does not need them (gs_bin_needs_offsets)
+    order: torch.Tensor | None   # [n] int32 Gaussians by depth (culled last); None on the tile-local path
+    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets ([n] = m): in depth order on the
+    #                               radix path, in index order on the tile-local one; None on the span path
     m: int                       # instances
     keys: torch.Tensor           # [m] int64 sorted keys (empty unless keep_keys)
     point_list: torch.Tensor     # [m] int32
@@ -235,15 +235,22 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         pre_done = torch.cuda.Event()
         pre_done.record()
         side.wait_event(pre_done)
-    order = torch.empty(n, dtype=torch.int32, device=dev)
-    # the instance offsets in depth order are needed only where the fill emits and sorts the
-    # instances (canvases beyond the span binning's limit)
-    offsets = None
-    if _lib.lib().gs_bin_needs_offsets(n, ccam):
+    # The tile binning's path: the tile-local depth order needs only the instance offsets in
+    # index order (no sort of the Gaussians); the radix path the depth order and the offsets in
+    # that order; the span binning the depth order alone.
+    path = _lib.lib().gs_bin_path(n, ccam)
+    order = offsets = None
+    if path == _lib.GS_BIN_PATH_LOCAL:
         offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
-    ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
-    call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
-         ws.numel(), st)
+        ws = _u8(_lib.size_call("gs_scan_workspace_size", n), dev)
+        call("gs_scan_u32", ptr(touched), ptr(offsets), n, ptr(ws), ws.numel(), st)
+    else:
+        order = torch.empty(n, dtype=torch.int32, device=dev)
+        if path == _lib.GS_BIN_PATH_RADIX:
+            offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
+        ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
+        call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
+             ws.numel(), st)
     tm.mark("depth_order")
     m_ready = None
     if side is not None:

@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
     EmitSetup es = {};
     uint32_t g = 0;
     if (cap) {
-      g = order[j];
+      g = order ? order[j] : static_cast<uint32_t>(j);
       if constexpr (kRect) {
         const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
         es.d = r;
@@ -1672,6 +1672,231 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Tile-local depth order. With the instances emitted in Gaussian-index order and stably sorted
+// by tile, each tile's list holds its Gaussians in index order; a stable sort of every list by
+// depth key then gives the (tile, depth, index) order of the global path without sorting the N
+// Gaussians by depth first. LSD radix with 9-bit digits on each list: lists of up to kTsCap
+// entries in one workgroup's registers and LDS (tile_sort_small_kernel), longer ones by one
+// workgroup in 4096-entry chunks through global scratch (tile_sort_large_kernel). Keys are
+// ranked stably by wavefront ballots (match_bits), in position order.
+// ---------------------------------------------------------------------------------------
+constexpr int kTsBits = 9;
+constexpr int kTsRadix = 1 << kTsBits;
+constexpr int kTsWaves = 4;
+constexpr int kTsRounds = 16;
+constexpr int kTsCap = kTsWaves * kWave * kTsRounds;  // 4096 entries
+
+// Exclusive offsets of the digit counts s_cnt[W][kTsRadix] in digit-major, wavefront-minor
+// order, written back in place. Each of the workgroup's THREADS threads takes kTsRadix / THREADS
+// consecutive digits; returns with a barrier.
+template <int W, int THREADS>
+__device__ __forceinline__ void digit_offsets(uint32_t (*s_cnt)[kTsRadix], uint32_t* s_wsum) {
+  constexpr int DPT = kTsRadix / THREADS;
+  static_assert(DPT >= 1 && DPT * THREADS == kTsRadix, "digits per thread");
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int d0 = static_cast<int>(threadIdx.x) * DPT;
+  uint32_t sum = 0;
+#pragma unroll
+  for (int e = 0; e < DPT; ++e)
+#pragma unroll
+    for (int w = 0; w < W; ++w) sum += s_cnt[w][d0 + e];
+  uint32_t incl = sum;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == kWave - 1) s_wsum[wave] = incl;
+  __syncthreads();
+  uint32_t run = incl - sum;
+  for (int q = 0; q < wave; ++q) run += s_wsum[q];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const uint32_t c = s_cnt[w][d0 + e];
+      s_cnt[w][d0 + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+}
+
+// Lists of 2 .. kTsCap entries: keys in registers (position p = 1024 w + 64 r + lane for round
+// r of wavefront w), one LDS copy per pass to redistribute them.
+__global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const uint32_t* __restrict__ ranges,
+                                                                           const uint32_t* __restrict__ dkey,
+                                                                           uint32_t* __restrict__ point_list,
+                                                                           int passes) {
+  __shared__ uint32_t s_k[kTsCap];
+  __shared__ uint32_t s_v[kTsCap];
+  __shared__ uint32_t s_cnt[kTsWaves][kTsRadix];
+  __shared__ uint32_t s_wsum[kTsWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const uint32_t r0 = ranges[2 * tile];
+  const int len = static_cast<int>(ranges[2 * tile + 1] - r0);
+  if (len <= 1 || len > kTsCap) return;  // the whole workgroup
+  const uint64_t lt = lanemask_lt(lane);
+  const int base = wave * (kWave * kTsRounds) + lane;
+  uint32_t key[kTsRounds], val[kTsRounds], rank[kTsRounds];
+#pragma unroll
+  for (int r = 0; r < kTsRounds; ++r) {
+    const int p = base + kWave * r;
+    val[r] = p < len ? point_list[r0 + p] : 0u;
+  }
+#pragma unroll
+  for (int r = 0; r < kTsRounds; ++r) key[r] = base + kWave * r < len ? dkey[val[r]] : 0u;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = kTsBits * pass;
+    for (int q = threadIdx.x; q < kTsWaves * kTsRadix; q += kTsWaves * kWave) (&s_cnt[0][0])[q] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kTsRounds; ++r) {
+      const bool valid = base + kWave * r < len;
+      const uint32_t d = (key[r] >> shift) & (kTsRadix - 1);
+      const uint64_t peers = match_bits<kTsBits>(d, valid);
+      rank[r] = valid ? s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt)) : 0u;
+      wave_sync();
+      if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
+      wave_sync();
+    }
+    __syncthreads();
+    digit_offsets<kTsWaves, kTsWaves * kWave>(s_cnt, s_wsum);
+#pragma unroll
+    for (int r = 0; r < kTsRounds; ++r) {
+      if (base + kWave * r < len) {
+        const uint32_t pos = s_cnt[wave][(key[r] >> shift) & (kTsRadix - 1)] + rank[r];
+        s_k[pos] = key[r];
+        s_v[pos] = val[r];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kTsRounds; ++r) {
+      const int p = base + kWave * r;
+      if (p < len) {
+        key[r] = s_k[p];
+        val[r] = s_v[p];
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < kTsRounds; ++r) {
+    const int p = base + kWave * r;
+    if (p < len) point_list[r0 + p] = val[r];
+  }
+}
+
+// Lists longer than kTsCap: one workgroup of kTlWaves wavefronts per list, each pass a digit
+// histogram over the whole list, then the list in chunks of kTlChunk entries, in order, each
+// chunk ranked stably and scattered to running digit positions; passes go point_list -> (k1,
+// v1) -> (k2, v2) -> (k1, v1) ..., the last one's values into point_list (each list in the
+// scratch arrays at its own range [r0, r1)).
+constexpr int kTlWaves = 16;
+constexpr int kTlRounds = 4;
+constexpr int kTlChunk = kTlWaves * kWave * kTlRounds;  // 4096
+
+__global__ __launch_bounds__(kTlWaves * kWave) void tile_sort_large_kernel(
+    const uint32_t* __restrict__ ranges, const uint32_t* __restrict__ dkey, uint32_t* __restrict__ point_list,
+    uint32_t* __restrict__ k1, uint32_t* __restrict__ v1, uint32_t* __restrict__ k2, uint32_t* __restrict__ v2,
+    int passes) {
+  __shared__ uint32_t s_base[kTsRadix];
+  __shared__ uint32_t s_cnt[kTlWaves][kTsRadix];
+  __shared__ uint32_t s_wsum[kTlWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const uint32_t r0 = ranges[2 * tile];
+  const int len = static_cast<int>(ranges[2 * tile + 1] - r0);
+  if (len <= kTsCap) return;  // the whole workgroup: the small kernel's lists
+  const uint64_t lt = lanemask_lt(lane);
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = kTsBits * pass;
+    const bool last = pass == passes - 1;
+    const uint32_t* src_k = pass == 0 ? nullptr : (pass & 1) ? k1 : k2;  // pass 0 gathers its keys
+    const uint32_t* src_v = pass == 0 ? point_list : (pass & 1) ? v1 : v2;
+    uint32_t* dst_k = last ? nullptr : (pass & 1) ? k2 : k1;
+    uint32_t* dst_v = last ? point_list : (pass & 1) ? v2 : v1;
+    // digit histogram of the whole list
+    for (int q = threadIdx.x; q < kTsRadix; q += kTlWaves * kWave) s_base[q] = 0u;
+    __syncthreads();
+    for (int p = threadIdx.x; p < len; p += kTlWaves * kWave) {
+      const uint32_t k = src_k ? src_k[r0 + p] : dkey[src_v[r0 + p]];
+      atomicAdd(&s_base[(k >> shift) & (kTsRadix - 1)], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave) {  // exclusive scan of the 512 digit counts by one wavefront
+      constexpr int PER = kTsRadix / kWave;
+      uint32_t c[PER], sum = 0;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        c[e] = s_base[PER * lane + e];
+        sum += c[e];
+      }
+      uint32_t tot;
+      uint32_t run = wave_excl_scan(sum, lane, tot);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        s_base[PER * lane + e] = run;
+        run += c[e];
+      }
+    }
+    __syncthreads();
+    // the list in chunks, in order
+    for (int c0 = 0; c0 < len; c0 += kTlChunk) {
+      const int cb = c0 + wave * (kWave * kTlRounds) + lane;
+      uint32_t key[kTlRounds], val[kTlRounds], rank[kTlRounds];
+#pragma unroll
+      for (int r = 0; r < kTlRounds; ++r) {
+        const int p = cb + kWave * r;
+        val[r] = p < len ? src_v[r0 + p] : 0u;
+        key[r] = p < len ? (src_k ? src_k[r0 + p] : dkey[val[r]]) : 0u;
+      }
+      for (int q = threadIdx.x; q < kTlWaves * kTsRadix; q += kTlWaves * kWave) (&s_cnt[0][0])[q] = 0u;
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < kTlRounds; ++r) {
+        const bool valid = cb + kWave * r < len;
+        const uint32_t d = (key[r] >> shift) & (kTsRadix - 1);
+        const uint64_t peers = match_bits<kTsBits>(d, valid);
+        rank[r] = valid ? s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt)) : 0u;
+        wave_sync();
+        if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
+        wave_sync();
+      }
+      __syncthreads();
+      // chunk offsets per (wavefront, digit) from the running digit positions, which then advance
+      // by the chunk's counts
+      if (threadIdx.x < kTsRadix) {
+        const int d = threadIdx.x;
+        uint32_t run = s_base[d];
+#pragma unroll
+        for (int w = 0; w < kTlWaves; ++w) {
+          const uint32_t c = s_cnt[w][d];
+          s_cnt[w][d] = run;
+          run += c;
+        }
+        s_base[d] = run;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < kTlRounds; ++r) {
+        if (cb + kWave * r < len) {
+          const uint32_t pos = s_cnt[wave][(key[r] >> shift) & (kTsRadix - 1)] + rank[r];
+          if (dst_k) dst_k[r0 + pos] = key[r];
+          dst_v[r0 + pos] = val[r];
+        }
+      }
+      __syncthreads();  // the chunk offsets are rewritten by the next chunk
+    }
+  }
+}
+
 static inline unsigned grid_for(int64_t n, int threads) {
   return static_cast<unsigned>((n + threads - 1) / threads);
 }
@@ -1739,8 +1964,18 @@ static bool span_binning(int tiles_x, int tiles_y) { return tiles_x <= kSpanMaxD
 constexpr int64_t kSpanMinGaussians = 2000000;
 
 static bool use_spans(int64_t n, int tiles_x, int tiles_y, int flags) {
-  if (!span_binning(tiles_x, tiles_y) || (flags & GS_BIN_RADIX)) return false;
+  if (!span_binning(tiles_x, tiles_y) || (flags & (GS_BIN_RADIX | GS_BIN_LOCAL))) return false;
   return (flags & GS_BIN_SPANS) || n >= kSpanMinGaussians;
+}
+
+// The 3D fill's path: the span binning as above; below it the instances are emitted and sorted
+// by tile, in depth order after the global depth sort (GS_BIN_PATH_RADIX, the default) or in
+// index order with each tile's list then sorted by depth (GS_BIN_PATH_LOCAL: no sort of the N
+// Gaussians).
+static int bin_path(int64_t n, int tiles_x, int tiles_y, int flags) {
+  if (use_spans(n, tiles_x, tiles_y, flags)) return GS_BIN_PATH_SPANS;
+  if (flags & GS_BIN_LOCAL) return GS_BIN_PATH_LOCAL;
+  return GS_BIN_PATH_RADIX;
 }
 
 // m instances fit the span path's 32-bit span positions (m plus every row's padding)
@@ -1773,10 +2008,15 @@ static SpanLayout span_layout(int64_t n, int64_t m, int tiles_x, int tiles_y) {
   return L;
 }
 
-// Workspace of the fill (emission or span binning) for n Gaussians and m instances.
-static size_t fill_ws(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags) {
-  return use_spans(n, tiles_x, tiles_y, flags) ? span_layout(n, m, tiles_x, tiles_y).end
-                                               : emit_layout(m, tiles_x * tiles_y).end;
+// Workspace of the fill for n Gaussians and m instances: the span binning's; the emission's,
+// followed on the tile-local path by the long-list sort's scratch (two key and two value
+// arrays of m).
+static size_t fill_ws(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags, bool rects = false) {
+  const int path = rects ? (use_spans(n, tiles_x, tiles_y, flags) ? GS_BIN_PATH_SPANS : GS_BIN_PATH_RADIX)
+                         : bin_path(n, tiles_x, tiles_y, flags);
+  if (path == GS_BIN_PATH_SPANS) return span_layout(n, m, tiles_x, tiles_y).end;
+  const size_t e = emit_layout(m, tiles_x * tiles_y).end;
+  return path == GS_BIN_PATH_LOCAL ? e + 4 * align_up(static_cast<size_t>(m) * 4) : e;
 }
 
 // Rectangle binning: the depth ordering, the order and offsets, then the fill.
@@ -1790,7 +2030,7 @@ static RectLayout rect_layout(int64_t n, int64_t m, int tiles_x, int tiles_y, in
   L.prep = o; o += prep_layout(n).end;
   L.order = o; o += align_up(n * 4);
   L.offs = o; o += align_up((n + 1) * 4);
-  L.emit = o; o += fill_ws(n, m, tiles_x, tiles_y, flags);
+  L.emit = o; o += fill_ws(n, m, tiles_x, tiles_y, flags, true);
   L.end = o;
   return L;
 }
@@ -1851,7 +2091,7 @@ template <typename K>
 static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
                           const uint32_t* order, const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles,
                           int64_t m, int tile_bits, uint64_t* sorted_keys, uint32_t* point_list, uint32_t* preset,
-                          const EmitLayout& L, char* ws, hipStream_t st) {
+                          const EmitLayout& L, char* ws, hipStream_t st, bool defer_keys) {
   K* tkeys = reinterpret_cast<K*>(ws + L.tkeys);
   uint32_t* tvals = reinterpret_cast<uint32_t*>(ws + L.tvals);
   K* tsorted = reinterpret_cast<K*>(ws + L.tsorted);
@@ -1866,7 +2106,7 @@ static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t
   }
   radix_sort(tkeys, tvals, tsorted, point_list, m, tile_bits, ws + L.sort, st, nullptr, nullptr, preset,
              preset != nullptr && !sorted_keys);
-  if (sorted_keys)
+  if (sorted_keys && !defer_keys)
     hipLaunchKernelGGL((full_keys_kernel<K>), dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list, dkey_of,
                        dkey0, m, sorted_keys);
 }
@@ -1928,12 +2168,15 @@ static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dk
 #undef GS_SPAN_WRITE
 }
 
-static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
+static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0, int dkey_bits,
                      const uint32_t* order,
                      const uint32_t* offsets, int64_t n, int tiles_x, int tiles_y, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
                      uint32_t* bucket_offsets, uint32_t* list_header, int flags, char* ws, hipStream_t st) {
   const int n_tiles = tiles_x * tiles_y;
+  // the tile-local depth order (3D only): instances emitted in index order, each tile's list
+  // sorted by depth after the tile sort
+  const bool local = !rects && bin_path(n, tiles_x, tiles_y, flags) == GS_BIN_PATH_LOCAL;
   if (m > 0 && use_spans(n, tiles_x, tiles_y, flags)) {
     // (gs_bin_fill_* reject an m beyond span_fits for this path)
     if (rects)
@@ -1955,17 +2198,43 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
     // emitted and sorted as 16-bit keys
     const bool sort_ranges = tile_bits > 0;
     uint32_t* preset = sort_ranges ? ranges : nullptr;
-    if (sort_ranges && n_tiles <= 65536)
+    const bool short_keys = sort_ranges && n_tiles <= 65536;
+    if (short_keys)
       emit_and_sort<uint16_t>(rec, rects, dkey_of, dkey0, order, offsets, n, tiles_x, n_tiles, m, tile_bits,
-                              sorted_keys, point_list, preset, L, ws, st);
+                              sorted_keys, point_list, preset, L, ws, st, local);
     else
       emit_and_sort<uint32_t>(rec, rects, dkey_of, dkey0, order, offsets, n, tiles_x, n_tiles, m, tile_bits,
-                              sorted_keys, point_list, preset, L, ws, st);
+                              sorted_keys, point_list, preset, L, ws, st, local);
     if (!sort_ranges)
       hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for((m + kBoundsPer - 1) / kBoundsPer, 256)), dim3(256), 0,
                          st, reinterpret_cast<const uint32_t*>(ws + L.tsorted), m, n_tiles, ranges);
     hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
                        tile_offsets, list_header, sort_ranges);
+    if (local) {
+      // each tile's list (index order) sorted by depth key: short lists in LDS, long ones through
+      // the scratch after the emission's workspace
+      const int passes = (dkey_bits + kTsBits - 1) / kTsBits;
+      if (passes > 0) {
+        uint32_t* scr = reinterpret_cast<uint32_t*>(ws + L.end);
+        const size_t mw = align_up(static_cast<size_t>(m) * 4) / 4;
+        hipLaunchKernelGGL(tile_sort_small_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kTsWaves * kWave), 0,
+                           st, ranges, dkey_of, point_list, passes);
+        // (at least two passes there: a single one would read and write the point list at once)
+        hipLaunchKernelGGL(tile_sort_large_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kTlWaves * kWave), 0,
+                           st, ranges, dkey_of, point_list, scr, scr + mw, scr + 2 * mw, scr + 3 * mw,
+                           passes > 1 ? passes : 2);
+      }
+      if (sorted_keys) {
+        if (short_keys)
+          hipLaunchKernelGGL((full_keys_kernel<uint16_t>), dim3(grid_for(m, 256)), dim3(256), 0, st,
+                             reinterpret_cast<const uint16_t*>(ws + L.tsorted), point_list, dkey_of, dkey0, m,
+                             sorted_keys);
+        else
+          hipLaunchKernelGGL((full_keys_kernel<uint32_t>), dim3(grid_for(m, 256)), dim3(256), 0, st,
+                             reinterpret_cast<const uint32_t*>(ws + L.tsorted), point_list, dkey_of, dkey0, m,
+                             sorted_keys);
+      }
+    }
     return;
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
@@ -2028,14 +2297,15 @@ extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int tiles_x, int t
   tiles_x = tiles_x < 1 ? 1 : tiles_x;
   tiles_y = tiles_y < 1 ? 1 : tiles_y;
   m = m < 0 ? 0 : m;
-  // the rectangle binning runs the depth ordering itself: its scratch, order and offsets too
-  return rect_layout(n, m, tiles_x, tiles_y, flags).end;
+  // the rectangle binning runs the depth ordering itself: its scratch, order and offsets too;
+  // the 3D fill needs its own path's workspace
+  return std::max(rect_layout(n, m, tiles_x, tiles_y, flags).end, fill_ws(n, m, tiles_x, tiles_y, flags));
 }
 
-extern "C" int gs_bin_needs_offsets(int64_t n, const gs_camera* cam) {
-  if (!cam) return 1;
+extern "C" int gs_bin_path(int64_t n, const gs_camera* cam) {
+  if (!cam) return GS_BIN_PATH_RADIX;
   const CamK k = make_cam(*cam);
-  return use_spans(n, k.tiles_x, k.tiles_y, cam->flags) ? 0 : 1;
+  return bin_path(n, k.tiles_x, k.tiles_y, cam->flags);
 }
 
 extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
@@ -2050,17 +2320,21 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   GS_REQUIRE(ranges && bucket_offsets, GS_ERR_ARG, "null output");
   const CamK k = make_cam(*cam);
   GS_REQUIRE(static_cast<int64_t>(k.tiles_x) * k.tiles_y < kMaxTiles, GS_ERR_ARG, "too many tiles");
-  const bool spans = use_spans(n, k.tiles_x, k.tiles_y, cam->flags);
-  GS_REQUIRE(!spans || span_fits(m, k.tiles_y), GS_ERR_ARG, "%lld instances exceed the 32-bit span positions",
-             static_cast<long long>(m));
+  const int path = bin_path(n, k.tiles_x, k.tiles_y, cam->flags);
+  GS_REQUIRE(path != GS_BIN_PATH_SPANS || span_fits(m, k.tiles_y), GS_ERR_ARG,
+             "%lld instances exceed the 32-bit span positions", static_cast<long long>(m));
   const size_t need = fill_ws(n, m, k.tiles_x, k.tiles_y, cam->flags);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
-  GS_REQUIRE(m == 0 || (splat_rec && order && point_list), GS_ERR_ARG, "null pointer argument");
-  GS_REQUIRE(m == 0 || offsets || spans, GS_ERR_ARG, "this fill emits instances: it needs the offsets");
+  GS_REQUIRE(m == 0 || (splat_rec && point_list), GS_ERR_ARG, "null pointer argument");
+  GS_REQUIRE(m == 0 || order || path == GS_BIN_PATH_LOCAL, GS_ERR_ARG, "this fill needs the depth order");
+  GS_REQUIRE(m == 0 || offsets || path == GS_BIN_PATH_SPANS, GS_ERR_ARG, "this fill emits instances: it needs the offsets");
+  GS_REQUIRE(m == 0 || depth_keys || path != GS_BIN_PATH_LOCAL, GS_ERR_ARG,
+             "the tile-local depth order needs the depth keys");
   GS_REQUIRE(!(sorted_keys && m > 0 && !depth_keys), GS_ERR_ARG, "sorted_keys need depth_keys");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
-  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, order, offsets, n, k.tiles_x,
+  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, depth_key_bits(k), order,
+           offsets, n, k.tiles_x,
            k.tiles_y, m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, bucket_list, cam->flags,
            static_cast<char*>(workspace), as_stream(stream));
   return check_launch("bin_fill_3d");
@@ -2115,7 +2389,7 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
     if (sorted_keys && m > 0 && !d32)  // index order: the depth part of the keys is 0
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
   }
-  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, tiles_y, m, sorted_keys,
+  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, 32, ord, offs, n, tiles_x, tiles_y, m, sorted_keys,
            point_list, ranges, tile_offsets, bucket_offsets, nullptr, flags, ws + L.emit, st);
   return check_launch("bin_fill_rect");
 }

@@ -143,12 +143,20 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
                 atomics_per_pair=9, spans=None):
     """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
     written once (fp32). spans: the row-span count when the forward took the span binning (its
-    instance offsets are None), else None."""
+    instance offsets are None), else None. The path is the forward's: no depth order for the
+    tile-local one, no offsets for the span binning."""
     n, m, K = fs.n, fs.m, fs.sh_coeffs
     T = fs.cam.n_tiles
     P = fs.cam.width * fs.cam.height
     B = int(fs.bucket_offsets[-1].item())
-    if spans is None:
+    if fs.order is None:
+        # the scan of the tile counts (counts read, offsets written)
+        depth = 8 * n
+        # emission (48 B of the record of the visible and the offset per Gaussian, key+value per
+        # instance), tile sort passes 1 and 2 as on the radix path, ranges and bucket offsets per
+        # tile; the per-tile depth sort: list entry read, its depth key gathered, entry written
+        binning = 48 * n_visible + 4 * n + 8 * m + 20 * m + 16 * m + 12 * m + 20 * T + 4 * B
+    elif spans is None:
         # 3 radix passes over N (histogram read 4 B, key+value read and write 16 B), the counts
         # gathered into depth order (read + write), the scan (counts read, offsets written)
         depth = 3 * 20 * n + 8 * n + 8 * n
@@ -483,7 +491,7 @@ def bench_3d(args, ceilings) -> dict:
 
     # counts for the byte and operation models: one counting step per pose outside the timed
     # regions, averaged over the poses like the timings
-    per_pose = []
+    per_pose, paths = [], set()
     for pose in range(len(cams)):
         ctr = torch.zeros(3, dtype=torch.int64, device="cuda")
         fs, _ = step(pose, counters=ctr)
@@ -493,6 +501,7 @@ def bench_3d(args, ceilings) -> dict:
         up = int(ctr[0].item()) // 9
         ev = int(ctr[2].item())
         spans = span_count(fs) if fs.offsets is None else None
+        paths.add("local" if fs.order is None else "spans" if spans is not None else "radix")
         per_pose.append({"visible": nv, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
                          "active_buckets": ab, "bucket_splat_steps": ss, "staged_entries": stg,
                          "ckpt_written": ckw, "reduced_bucket_splats": up, "bwd_pair_evals": ev,
@@ -555,7 +564,7 @@ def bench_3d(args, ceilings) -> dict:
                                f"{fs_cam.width}x{fs_cam.height}, fwd+bwd per view through rasterize(...) and "
                                f"autograd, {views}",
                    "gaussians": scene.n, "width": fs_cam.width, "height": fs_cam.height,
-                   "tile_binning": "spans" if "row_spans" in per_pose[0] else "radix",
+                   "tile_binning": "+".join(sorted(paths)),
                    "parallelism": "single GPU"},
         "low_level_ms_per_step": round(low_ms, 4),
         "stage_ms": {k2: round(v, 4) for k2, v in stage_ms.items()},

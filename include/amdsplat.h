@@ -63,12 +63,16 @@ typedef struct gs_camera {
 
 /* Binning path (gs_camera.flags for the 3D entry points, the flags argument of
  * gs_bin_fill_rect): by default the span binning is taken from GS_BIN_SPAN_MIN_GAUSSIANS
- * Gaussians on canvases of at most GS_BIN_SPAN_MAX_TILES tiles per side, the radix path
- * otherwise; these bits force one of them (GS_BIN_SPANS only where the canvas allows it). Both
- * give the same lists, ranges and bucket offsets. */
+ * Gaussians on canvases of at most GS_BIN_SPAN_MAX_TILES tiles per side, otherwise the radix
+ * path; these bits force one of them or the tile-local depth order
+ * (GS_BIN_SPANS only where the canvas allows it; GS_BIN_LOCAL is 3D only). All give the same
+ * lists, ranges and bucket offsets. */
 #define GS_BIN_SPANS 2
 #define GS_BIN_RADIX 4
+#define GS_BIN_LOCAL 8
 #define GS_BIN_SPAN_MIN_GAUSSIANS 2000000
+/* gs_bin_path values: the 3D fill's path for a camera and Gaussian count */
+enum { GS_BIN_PATH_RADIX = 0, GS_BIN_PATH_SPANS = 1, GS_BIN_PATH_LOCAL = 2 };
 
 /* Thread-local message of the last failed call. */
 const char* gs_last_error(void);
@@ -125,11 +129,17 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  * visible in results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:10-31).
  * Produces the stable order of instances by (tile, depth, Gaussian index) -- the order of a
  * stable sort of 64-bit keys (tile << 32 | orderable depth bits) over instances emitted in
- * Gaussian-index order. First a stable radix sort of the Gaussians by depth; then either the
- * instances are emitted in depth order and stably radix-sorted by tile (radix path), or two
- * counting passes run over the Gaussians' row spans (the run of tiles a Gaussian touches in one
- * tile row): by tile row over the Gaussians in depth order, then by column within each row,
- * which writes every instance once (span binning; see GS_BIN_SPANS for which is taken).
+ * Gaussian-index order, by one of three paths (gs_bin_path):
+ *   GS_BIN_PATH_RADIX (default below GS_BIN_SPAN_MIN_GAUSSIANS): a stable radix sort of the
+ *     Gaussians by depth, then the instances emitted in that order and stably radix-sorted by tile;
+ *   GS_BIN_PATH_LOCAL: the instances emitted in index order and stably radix-sorted by tile,
+ *     then each tile's list stably sorted by depth key;
+ *   GS_BIN_PATH_SPANS: the depth sort, then two counting passes over the Gaussians' row spans
+ *     (the run of tiles a Gaussian touches in one tile row): by tile row over the Gaussians in
+ *     depth order, then by column within each row, which writes every instance once.
+ * The caller runs gs_bin_prepare_3d for the radix and span paths (the depth order; the instance
+ * offsets in that order only for the radix path), gs_scan_u32 of tiles_touched (the instance
+ * offsets in index order) for the local path; then gs_bin_fill_3d.
  *
  * gs_bin_prepare_3d: depth ordering.
  *   depth_keys [n] from gs_preprocess_fwd with the same camera (order keys of the view depth
@@ -137,9 +147,9 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *   only as many bits as the near/far range needs), or NULL (then computed from splat_rec and
  *   tiles_touched).
  *   out: order [n]        Gaussian indices by depth key, stable (culled Gaussians last)
- *        offsets [n + 1]  (may be NULL: gs_bin_fill_3d needs them only on the radix path,
- *                         gs_bin_needs_offsets(n, cam)) exclusive scan of tiles_touched[order[j]];
- *                         offsets[n] = m, the number of instances
+ *        offsets [n + 1]  (may be NULL: gs_bin_fill_3d needs them in depth order only on the
+ *                         radix path) exclusive scan of tiles_touched[order[j]]; offsets[n] = m,
+ *                         the number of instances
  *   tiles_touched may be NULL when offsets is NULL and depth_keys is given.
  *   Workspace from gs_bin_prepare_workspace_size(n).
  * gs_bin_fill_3d: tile lists, ranges, bucket offsets. splat_rec as gs_preprocess_fwd wrote it
@@ -152,7 +162,9 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *   bucket_offsets [T+1]  exclusive scan of ceil(len/32); bucket_offsets[T] = number of buckets
  *   bucket_list (may be NULL): the list gs_blend_fwd_3d appends to; its header is cleared
  *                         here, so that call can take GS_BLEND_LIST_CLEARED
- *   offsets: as gs_bin_prepare_3d wrote them, or NULL when gs_bin_needs_offsets(n, cam) is 0.
+ *   order, offsets: radix path: as gs_bin_prepare_3d wrote them; span path: the order, offsets
+ *   NULL; local path: order NULL, offsets the exclusive scan of tiles_touched in index order
+ *   (depth_keys needed).
  *   Workspace from gs_bin_workspace_size(n, m, tiles_x, tiles_y, cam->flags).
  * ------------------------------------------------------------------------------------- */
 #define GS_BIN_SPAN_MAX_TILES 512
@@ -161,7 +173,7 @@ int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched, con
                       int64_t n, const gs_camera* cam, uint32_t* order, uint32_t* offsets,
                       void* workspace, size_t workspace_bytes, void* stream);
 size_t gs_bin_workspace_size(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags);
-int gs_bin_needs_offsets(int64_t n, const gs_camera* cam); /* 1 when the fill takes the radix path */
+int gs_bin_path(int64_t n, const gs_camera* cam); /* GS_BIN_PATH_* the fill takes for n Gaussians */
 int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
                    const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,
                    uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges,
