@@ -28,6 +28,9 @@ TILE = 16
 BUCKET = 32
 REC_FLOATS = 16
 GRAD2D_FLOATS = 12
+# the tile binning of the views rasterize(...), rasterize_inference and pruning_scores build:
+# "auto", "spans", "radix" or "local" (forward_pass takes its Camera's own field)
+BINNING = "auto"
 
 
 def _u8(nbytes: int, device) -> torch.Tensor:
@@ -95,9 +98,11 @@ class ForwardState:
     sh_degree: int
     rec: torch.Tensor            # [n, 16] splat records
     touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
-    order: torch.Tensor | None   # [n] int32 Gaussians by depth (culled last); None on the tile-local path
-    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets ([n] = m): in depth order on the
-    #                               radix path, in index order on the tile-local one; None on the span path
+    order: torch.Tensor  # [n] int32 Gaussians by depth (culled last); on the tile-local path the
+    #                      Gaussians with tiles in index order (entries past their count unused)
+    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets over `order` ([k] = m past the
+    #                               Gaussians with tiles); None on the span path
+    path: int  # the tile binning's path (GS_BIN_PATH_*)
     m: int                       # instances
     keys: torch.Tensor           # [m] int64 sorted keys (empty unless keep_keys)
     point_list: torch.Tensor     # [m] int32
@@ -235,22 +240,15 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         pre_done = torch.cuda.Event()
         pre_done.record()
         side.wait_event(pre_done)
-    # The tile binning's path: the tile-local depth order needs only the instance offsets in
-    # index order (no sort of the Gaussians); the radix path the depth order and the offsets in
-    # that order; the span binning the depth order alone.
+    # The tile binning's path: the radix path takes the depth order and the instance offsets in
+    # that order; the span binning the depth order alone; the tile-local depth order the
+    # Gaussians with tiles in index order and their offsets (no sort of the Gaussians).
     path = _lib.lib().gs_bin_path(n, ccam)
-    order = offsets = None
-    if path == _lib.GS_BIN_PATH_LOCAL:
-        offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
-        ws = _u8(_lib.size_call("gs_scan_workspace_size", n), dev)
-        call("gs_scan_u32", ptr(touched), ptr(offsets), n, ptr(ws), ws.numel(), st)
-    else:
-        order = torch.empty(n, dtype=torch.int32, device=dev)
-        if path == _lib.GS_BIN_PATH_RADIX:
-            offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
-        ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
-        call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
-             ws.numel(), st)
+    order = torch.empty(n, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n + 1, dtype=torch.int32, device=dev) if path != _lib.GS_BIN_PATH_SPANS else None
+    ws = _u8(_lib.size_call("gs_bin_prepare_workspace_size", n), dev)
+    call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
+         ws.numel(), st)
     tm.mark("depth_order")
     m_ready = None
     if side is not None:
@@ -318,7 +316,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     keys = view("keys", torch.int64) if keep_keys else torch.empty(0, dtype=torch.int64, device=dev)
     if _scores is not None:
         tm.mark("scores")
-        return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges,
+        return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, path, m, keys, point_list, ranges,
                             bucket_offsets, 0, None, None, None, None, None, None, None, tuple(bg),
                             {} if isinstance(timing, StageTimer) else tm.result())
     bucket_to_tile = ckpt = blist = None
@@ -327,8 +325,9 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         blist = view("blist", torch.int32)
         ckpt = view("ckpt", torch.float32).view(max(nb_max, 1), 256, 4)
     tm.mark("blend_fwd")
-    return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, m, keys, point_list, ranges, bucket_offsets,
-                        nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist, tuple(bg),
+    return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, path, m, keys, point_list, ranges,
+                        bucket_offsets, nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist,
+                        tuple(bg),
                         {} if isinstance(timing, StageTimer) else tm.result(), grad2d, ccam)
 
 
@@ -487,7 +486,7 @@ def rasterize(means, scales, quats, opacities, sh, viewmat, K, W: int, H: int, b
     low-pass does not add energy (S the projected 2D covariance); gradients include the factor.
     """
     means, scales, quats, opacities, _ = _prepare(means, scales, quats, opacities, sh, activated)
-    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing)
+    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing, BINNING)
     if bg is None:
         bg = (0.0, 0.0, 0.0)
     bg = tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
@@ -518,7 +517,7 @@ def rasterize_inference(means, scales, quats, opacities, sh, viewmat, K, W: int,
     upstream/upstream_main_kernels.patch:131-150): returns (image [3, H, W], alpha [H, W]), the
     same bits as rasterize, without the backward's bucket table, checkpoints or autograd state."""
     means, scales, quats, opacities, sh = _prepare(means, scales, quats, opacities, sh, activated)
-    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing)
+    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing, BINNING)
     bg = (0.0, 0.0, 0.0) if bg is None else tuple(float(x) for x in (bg.tolist() if torch.is_tensor(bg) else bg))
     fs = forward_pass(means.detach(), scales.detach(), quats.detach(), opacities.detach(),
                       tuple(t.detach() for t in sh) if isinstance(sh, tuple) else sh.detach(), cam,
@@ -535,7 +534,7 @@ def pruning_scores(means, scales, quats, opacities, sh, viewmat, K, W: int, H: i
     into of its blending weight alpha * T, under the forward's rules. Pass the same `scores`
     ([N] float32 CUDA) for every view to accumulate over a set of views; returns it."""
     means, scales, quats, opacities, sh = _prepare(means, scales, quats, opacities, sh, activated)
-    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing)
+    cam = Camera.from_K(viewmat, K, W, H, near, far, proper_antialiasing, BINNING)
     n = means.shape[0]
     if scores is None:
         scores = torch.zeros(n, dtype=torch.float32, device=means.device)

@@ -215,6 +215,139 @@ static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hip
 }
 
 // ---------------------------------------------------------------------------------------
+// The Gaussians with tiles (counts[i] > 0) in index order and their instance offsets: for n
+// Gaussians of which v have tiles, order[k] = the k-th of them, offs[k] = the counts before
+// it (offs[k] = m for k in [v, n]). Two launches over 2048-entry blocks: the blocks' count
+// sums and visible counts, then each block takes the prefixes of the blocks before it (every
+// block reads all the block sums) and scans its own entries.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void block_sum2(uint32_t& a, uint32_t& b, uint2* s_wave) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int off = 32; off > 0; off >>= 1) {
+    a += __shfl_xor(a, off, 64);
+    b += __shfl_xor(b, off, 64);
+  }
+  if (lane == 0) s_wave[wave] = make_uint2(a, b);
+  __syncthreads();
+  a = 0u;
+  b = 0u;
+#pragma unroll
+  for (int w = 0; w < kScanThreads / kWave; ++w) {
+    a += s_wave[w].x;
+    b += s_wave[w].y;
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kScanThreads) void vis_sum_kernel(const uint32_t* __restrict__ counts, int64_t n,
+                                                               uint32_t* __restrict__ sums, int64_t nb) {
+  __shared__ uint2 s_wave[kScanThreads / kWave];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  uint32_t c[kScanItems];
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) c[e] = counts[min(base + e * kScanThreads + threadIdx.x, n - 1)];
+  uint32_t sum = 0, vis = 0;
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) {
+    const bool in = base + e * kScanThreads + threadIdx.x < n;
+    sum += in ? c[e] : 0u;
+    vis += (in && c[e] != 0u) ? 1u : 0u;
+  }
+  block_sum2(sum, vis, s_wave);
+  if (threadIdx.x == 0) {
+    sums[blockIdx.x] = sum;
+    sums[nb + blockIdx.x] = vis;
+  }
+}
+
+__global__ __launch_bounds__(kScanThreads) void vis_scan_kernel(const uint32_t* __restrict__ counts, int64_t n,
+                                                                const uint32_t* __restrict__ sums, int64_t nb,
+                                                                uint32_t* __restrict__ order,
+                                                                uint32_t* __restrict__ offs) {
+  __shared__ uint2 s_wave[kScanThreads / kWave];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  // this thread's kScanItems consecutive entries
+  const int64_t i0 = base + static_cast<int64_t>(threadIdx.x) * kScanItems;
+  uint32_t c[kScanItems];
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) c[e] = counts[min(i0 + e, n - 1)];
+  // the blocks before this one, and all of them
+  uint32_t sb = 0, vb = 0, st = 0, vt = 0;
+  for (int64_t b = threadIdx.x; b < nb; b += kScanThreads) {
+    const uint32_t s = sums[b], v = sums[nb + b];
+    st += s;
+    vt += v;
+    if (b < static_cast<int64_t>(blockIdx.x)) {
+      sb += s;
+      vb += v;
+    }
+  }
+  block_sum2(sb, vb, s_wave);
+  block_sum2(st, vt, s_wave);
+  const uint32_t m = st, n_vis = vt;
+  uint32_t sum = 0, vis = 0;
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) {
+    const bool in = i0 + e < n;
+    c[e] = in ? c[e] : 0u;
+    sum += c[e];
+    vis += c[e] != 0u ? 1u : 0u;
+  }
+  // exclusive scans of both over the workgroup
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  uint32_t is = sum, iv = vis;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t us = __shfl_up(is, o, 64), uv = __shfl_up(iv, o, 64);
+    if (lane >= o) {
+      is += us;
+      iv += uv;
+    }
+  }
+  if (lane == kWave - 1) s_wave[wave] = make_uint2(is, iv);
+  __syncthreads();
+  uint32_t spos = sb + is - sum, vpos = vb + iv - vis;
+  for (int w = 0; w < wave; ++w) {
+    spos += s_wave[w].x;
+    vpos += s_wave[w].y;
+  }
+#pragma unroll
+  for (int e = 0; e < kScanItems; ++e) {
+    if (c[e] != 0u) {
+      order[vpos] = static_cast<uint32_t>(i0 + e);
+      offs[vpos] = spos;
+      ++vpos;
+      spos += c[e];
+    }
+  }
+  // the block's positions at or after the visible count (up to n) hold the total
+  for (int64_t p = base + threadIdx.x; p < base + kScanTile && p <= n; p += kScanThreads)
+    if (p >= static_cast<int64_t>(n_vis)) offs[p] = m;
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
+    // n itself lies past the last block's range when n is a multiple of the block size
+    if (n >= base + kScanTile) offs[n] = m;
+  }
+}
+
+// Gaussians up to which the visible list is two launches (every block reads all block sums)
+constexpr int64_t kLocalMaxGaussians = kScanTile * kScanDirectTiles;
+
+static size_t vis_ws(int64_t n) { return align_up(static_cast<size_t>(2 * ((n + kScanTile - 1) / kScanTile)) * 4); }
+
+// order / offsets of the Gaussians with tiles (n >= 1), as above.
+static void bin_visible(const uint32_t* counts, int64_t n, uint32_t* order, uint32_t* offs, char* ws,
+                        hipStream_t st) {
+  const int64_t nb = (n + kScanTile - 1) / kScanTile;
+  uint32_t* sums = reinterpret_cast<uint32_t*>(ws);
+  hipLaunchKernelGGL(vis_sum_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st, counts, n, sums,
+                     nb);
+  hipLaunchKernelGGL(vis_scan_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st, counts, n, sums,
+                     nb, order, offs);
+}
+
+// ---------------------------------------------------------------------------------------
 // Small kernels
 // ---------------------------------------------------------------------------------------
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
@@ -1742,20 +1875,21 @@ __global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const
   if (len <= 1 || len > kTsCap) return;  // the whole workgroup
   const uint64_t lt = lanemask_lt(lane);
   const int base = wave * (kWave * kTsRounds) + lane;
+  // rounds of this wavefront holding entries (wave-uniform)
+  const int rounds = min(kTsRounds, max(0, (len - wave * (kWave * kTsRounds) + kWave - 1) / kWave));
   uint32_t key[kTsRounds], val[kTsRounds], rank[kTsRounds];
+  // loads at clamped positions, without branches: every one in flight at once
 #pragma unroll
-  for (int r = 0; r < kTsRounds; ++r) {
-    const int p = base + kWave * r;
-    val[r] = p < len ? point_list[r0 + p] : 0u;
-  }
+  for (int r = 0; r < kTsRounds; ++r) val[r] = point_list[r0 + min(base + kWave * r, len - 1)];
 #pragma unroll
-  for (int r = 0; r < kTsRounds; ++r) key[r] = base + kWave * r < len ? dkey[val[r]] : 0u;
+  for (int r = 0; r < kTsRounds; ++r) key[r] = dkey[val[r]];
   for (int pass = 0; pass < passes; ++pass) {
     const int shift = kTsBits * pass;
     for (int q = threadIdx.x; q < kTsWaves * kTsRadix; q += kTsWaves * kWave) (&s_cnt[0][0])[q] = 0u;
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < kTsRounds; ++r) {
+      if (r >= rounds) break;  // wave-uniform
       const bool valid = base + kWave * r < len;
       const uint32_t d = (key[r] >> shift) & (kTsRadix - 1);
       const uint64_t peers = match_bits<kTsBits>(d, valid);
@@ -1825,9 +1959,22 @@ __global__ __launch_bounds__(kTlWaves * kWave) void tile_sort_large_kernel(
     // digit histogram of the whole list
     for (int q = threadIdx.x; q < kTsRadix; q += kTlWaves * kWave) s_base[q] = 0u;
     __syncthreads();
-    for (int p = threadIdx.x; p < len; p += kTlWaves * kWave) {
-      const uint32_t k = src_k ? src_k[r0 + p] : dkey[src_v[r0 + p]];
-      atomicAdd(&s_base[(k >> shift) & (kTsRadix - 1)], 1u);
+    // (kTlRounds entries a thread at a time, loaded at clamped positions before any is counted)
+    for (int p0 = threadIdx.x; p0 < len; p0 += kTlRounds * kTlWaves * kWave) {
+      uint32_t k[kTlRounds];
+      if (src_k) {
+#pragma unroll
+        for (int e = 0; e < kTlRounds; ++e) k[e] = src_k[r0 + min(p0 + e * kTlWaves * kWave, len - 1)];
+      } else {
+        uint32_t v[kTlRounds];
+#pragma unroll
+        for (int e = 0; e < kTlRounds; ++e) v[e] = src_v[r0 + min(p0 + e * kTlWaves * kWave, len - 1)];
+#pragma unroll
+        for (int e = 0; e < kTlRounds; ++e) k[e] = dkey[v[e]];
+      }
+#pragma unroll
+      for (int e = 0; e < kTlRounds; ++e)
+        if (p0 + e * kTlWaves * kWave < len) atomicAdd(&s_base[(k[e] >> shift) & (kTsRadix - 1)], 1u);
     }
     __syncthreads();
     if (threadIdx.x < kWave) {  // exclusive scan of the 512 digit counts by one wavefront
@@ -1851,11 +1998,15 @@ __global__ __launch_bounds__(kTlWaves * kWave) void tile_sort_large_kernel(
     for (int c0 = 0; c0 < len; c0 += kTlChunk) {
       const int cb = c0 + wave * (kWave * kTlRounds) + lane;
       uint32_t key[kTlRounds], val[kTlRounds], rank[kTlRounds];
+      // loads at clamped positions, without branches
 #pragma unroll
-      for (int r = 0; r < kTlRounds; ++r) {
-        const int p = cb + kWave * r;
-        val[r] = p < len ? src_v[r0 + p] : 0u;
-        key[r] = p < len ? (src_k ? src_k[r0 + p] : dkey[val[r]]) : 0u;
+      for (int r = 0; r < kTlRounds; ++r) val[r] = src_v[r0 + min(cb + kWave * r, len - 1)];
+      if (src_k) {
+#pragma unroll
+        for (int r = 0; r < kTlRounds; ++r) key[r] = src_k[r0 + min(cb + kWave * r, len - 1)];
+      } else {
+#pragma unroll
+        for (int r = 0; r < kTlRounds; ++r) key[r] = dkey[val[r]];
       }
       for (int q = threadIdx.x; q < kTlWaves * kTsRadix; q += kTlWaves * kWave) (&s_cnt[0][0])[q] = 0u;
       __syncthreads();
@@ -1974,7 +2125,7 @@ static bool use_spans(int64_t n, int tiles_x, int tiles_y, int flags) {
 // Gaussians).
 static int bin_path(int64_t n, int tiles_x, int tiles_y, int flags) {
   if (use_spans(n, tiles_x, tiles_y, flags)) return GS_BIN_PATH_SPANS;
-  if (flags & GS_BIN_LOCAL) return GS_BIN_PATH_LOCAL;
+  if ((flags & GS_BIN_LOCAL) && n <= kLocalMaxGaussians) return GS_BIN_PATH_LOCAL;
   return GS_BIN_PATH_RADIX;
 }
 
@@ -2035,7 +2186,7 @@ static RectLayout rect_layout(int64_t n, int64_t m, int tiles_x, int tiles_y, in
   return L;
 }
 
-static size_t prep_ws(int64_t n) { return prep_layout(n).end; }
+static size_t prep_ws(int64_t n) { return std::max(prep_layout(n).end, vis_ws(n)); }
 
 // Stable order of the Gaussians by depth key (keys_in: precomputed 32-bit keys, else computed
 // from rec / depth / depth64; none of them: index order) and, if offsets is not NULL, the
@@ -2280,12 +2431,27 @@ extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_t
   clear_error();
   if (int e = check_cam(cam)) return e;
   GS_REQUIRE(n >= 0 && n < (int64_t(1) << 32), GS_ERR_ARG, "invalid bin_prepare arguments");
-  GS_REQUIRE(n == 0 || (order && (depth_keys || splat_rec) && (tiles_touched || (!offsets && depth_keys))),
-             GS_ERR_ARG, "null pointer argument");
+  const CamK k = make_cam(*cam);
+  const bool local = bin_path(n, k.tiles_x, k.tiles_y, cam->flags) == GS_BIN_PATH_LOCAL;
+  if (local) {
+    GS_REQUIRE(offsets && (n == 0 || (order && tiles_touched)), GS_ERR_ARG,
+               "the tile-local path needs the counts, the order and the offsets");
+  } else {
+    GS_REQUIRE(n == 0 || (order && (depth_keys || splat_rec) && (tiles_touched || (!offsets && depth_keys))),
+               GS_ERR_ARG, "null pointer argument");
+  }
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
   const size_t need = prep_ws(n);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "bin_prepare workspace too small: need %zu bytes", need);
+  if (local) {
+    // the Gaussians with tiles in index order and their instance offsets
+    if (n == 0)
+      hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, as_stream(stream), offsets, int64_t(1), 0u);
+    else
+      bin_visible(tiles_touched, n, order, offsets, static_cast<char*>(workspace), as_stream(stream));
+    return check_launch("bin_prepare_3d");
+  }
   bin_prepare(depth_keys ? nullptr : reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, depth_keys,
               depth_key_bits(make_cam(*cam)), tiles_touched, n, order, offsets, static_cast<char*>(workspace),
               as_stream(stream));
@@ -2327,7 +2493,7 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "binning workspace too small: need %zu bytes", need);
   GS_REQUIRE(m == 0 || (splat_rec && point_list), GS_ERR_ARG, "null pointer argument");
-  GS_REQUIRE(m == 0 || order || path == GS_BIN_PATH_LOCAL, GS_ERR_ARG, "this fill needs the depth order");
+  GS_REQUIRE(m == 0 || order, GS_ERR_ARG, "the fill needs the order of gs_bin_prepare_3d");
   GS_REQUIRE(m == 0 || offsets || path == GS_BIN_PATH_SPANS, GS_ERR_ARG, "this fill emits instances: it needs the offsets");
   GS_REQUIRE(m == 0 || depth_keys || path != GS_BIN_PATH_LOCAL, GS_ERR_ARG,
              "the tile-local depth order needs the depth keys");

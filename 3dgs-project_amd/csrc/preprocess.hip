@@ -156,6 +156,46 @@ __device__ __forceinline__ void stage_sh(ShPtr src, int64_t first, int rows, int
   }
 }
 
+// Register copy of one pass of a full wavefront's SH rows (single-array layout, rows whose
+// float count is a multiple of 4: degrees 1 and 3), so that a pass's loads can be issued long
+// before its rows go to LDS. load() and store() take the same `need` (bit r: the pass's row r).
+template <int K>
+struct ShPrefetch {
+  using St = ShStage<K>;
+  static constexpr int R = St::R, RH = St::RH, CP = St::CP;
+  static constexpr bool kOk = R % 4 == 0;
+  static constexpr int N4 = RH * R / 4;  // float4 per pass
+  static constexpr int IT = (N4 + 63) / 64;
+  float4 v[kOk ? IT : 1];
+
+  __device__ __forceinline__ static bool row_needed(int f4, uint64_t need) {
+    return (N4 % 64 == 0 || f4 < N4) && ((need >> (f4 / (R / 4))) & 1u);
+  }
+  // blk: the pass's first row
+  __device__ __forceinline__ void load(const float* __restrict__ blk, uint64_t need, int lane) {
+    if constexpr (kOk) {
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int f4 = lane + 64 * it;
+        if (row_needed(f4, need)) v[it] = reinterpret_cast<const float4*>(blk)[f4];
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float* srow, uint64_t need, int lane) const {
+    if constexpr (kOk) {
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int f4 = lane + 64 * it;
+        if (row_needed(f4, need)) {  // a float4 never crosses a row
+          const int row = f4 / (R / 4), q = f4 - row * (R / 4);
+          float* d = srow + row * CP + 4 * q;
+          d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+        }
+      }
+    }
+  }
+};
+
 // Writes the staged rows of pass h back to the wavefront's rows.
 template <int K>
 __device__ __forceinline__ void unstage_sh(ShOut dst, int64_t first, int rows, int h, const float* srow, int lane) {
@@ -335,6 +375,16 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     ra = make_float4(g.mx, g.my, g.A, g.B);
     rb = make_float4(g.C, g.o, g.vz, thr);
   }
+  // A full wavefront of the single SH array (degrees 1 and 3) issues its first pass's row loads
+  // now, for the Gaussians visible so far (a superset of those with tiles), so that they are in
+  // flight during the tile count and the SH basis; each later pass's loads go out as soon as
+  // the previous pass is in LDS.
+  const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
+  const float* sh_blk = sh.a + wave_first * St::R;
+  const bool prefetch = ShPrefetch<K>::kOk && sh.b == nullptr && rows == 64 && aligned16(sh_blk);
+  const uint64_t pre_mask = __ballot(g.vis ? 1 : 0);
+  ShPrefetch<K> pf;
+  if (prefetch && pre_mask != 0) pf.load(sh_blk, pre_mask, lane);
   // tile rows of the wavefront's splats shared out over its lanes
   const uint32_t count = wave_count_rows(g.vis, ra, rb, bnd, lane, reinterpret_cast<uint32_t*>(s_sh[wave]));
   if (g.vis) g.vis = count > 0;
@@ -345,7 +395,6 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
   uint32_t mask = 0;
   if (vmask != 0) {
     float* srow = s_sh[wave];
-    const int rows = static_cast<int>(min<int64_t>(64, n - wave_first));
     float basis[16];
     float acc[3] = {0.0f, 0.0f, 0.0f};
     if (g.vis) {
@@ -359,7 +408,13 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
 #pragma unroll
     for (int h = 0; h < St::NH; ++h) {
       if (h) wave_sync();  // every lane is done with the previous rows
-      stage_sh<K>(sh, wave_first, rows, h, srow, lane, vmask);
+      if (prefetch) {
+        const uint64_t need = pre_mask >> (St::RH * h);
+        pf.store(srow, need, lane);
+        if (h + 1 < St::NH) pf.load(sh_blk + St::RH * (h + 1) * St::R, pre_mask >> (St::RH * (h + 1)), lane);
+      } else {
+        stage_sh<K>(sh, wave_first, rows, h, srow, lane, vmask);
+      }
       wave_sync();
       if (g.vis && lane / St::RH == h) {
         const float* row = srow + (lane - St::RH * h) * St::CP;

@@ -26,43 +26,92 @@ def host_order_key(v: float) -> int:
 DKEY_CULL = host_order_key(FAR) - host_order_key(NEAR)  # 27 bits for near/far = 0.01 / 100
 
 
-def camera(W=640, H=480):
-    return _lib.make_camera(np.eye(4, dtype=np.float32), 500.0, 500.0, W / 2, H / 2, W, H, NEAR, FAR)
+def camera(W=640, H=480, near=NEAR, far=FAR):
+    return _lib.make_camera(np.eye(4, dtype=np.float32), 500.0, 500.0, W / 2, H / 2, W, H, near, far)
 
 
-def depth_keys(n, kind, rng):
+def depth_keys(n, kind, rng, cull=DKEY_CULL):
     if kind == "distinct":
-        k = rng.integers(1, DKEY_CULL, n, dtype=np.int64)
+        k = rng.integers(1, cull, n, dtype=np.int64)
     elif kind == "few_values":
-        k = rng.choice(rng.integers(1, DKEY_CULL, 37, dtype=np.int64), n)
+        k = rng.choice(rng.integers(1, cull, 37, dtype=np.int64), n)
     elif kind == "culled_mix":  # a third culled (the largest key), the rest spread
-        k = rng.integers(1, DKEY_CULL, n, dtype=np.int64)
-        k[rng.random(n) < 0.33] = DKEY_CULL
+        k = rng.integers(1, cull, n, dtype=np.int64)
+        k[rng.random(n) < 0.33] = cull
     else:  # "equal"
-        k = np.full(n, 12345, np.int64)
+        k = np.full(n, min(12345, cull - 1), np.int64)
     return k.astype(np.uint32)
 
 
-@pytest.mark.parametrize("n", [1, 63, 4097, 100_003, 1_000_000, 9_000_001])
+# tiles of 1024, 2048 and 4096 keys (by size): one partial tile, exact multiples, one key more
+@pytest.mark.parametrize("n", [1, 63, 1024, 1025, 4097, 100_003, 524_288, 524_289, 1_000_000, 8_388_608,
+                               9_000_001])
 @pytest.mark.parametrize("kind", ["distinct", "few_values", "culled_mix", "equal"])
 def test_depth_order_is_the_stable_argsort(n, kind):
+    check_depth_order(n, kind, 9)
+
+
+@pytest.mark.parametrize("n", [100_003, 1_000_000])
+def test_depth_order_offsets_beyond_31_bits(n):
+    """Instance counts whose total passes 2^31 (the offsets are unsigned 32-bit)."""
+    check_depth_order(n, "distinct", (1 << 32) // n - 1)
+
+
+# the visible list of the tile-local path: blocks of 2048 entries (one partial, exact multiples,
+# one entry more), none visible, all visible, and the largest size the path takes
+@pytest.mark.parametrize("n,frac", [(1, 0.0), (1, 1.0), (2047, 0.7), (2048, 0.7), (2049, 0.7), (100_003, 0.0),
+                                    (100_003, 1.0), (1_000_000, 0.66), (8_388_608, 0.5)])
+def test_visible_list_and_offsets(n, frac):
+    """gs_bin_prepare_3d on the tile-local path: the Gaussians with tiles in index order and the
+    exclusive scan of their counts, every offset from the visible count up to n holding m."""
+    rng = np.random.default_rng(n + int(100 * frac))
+    counts = (rng.integers(1, 60, n) * (rng.random(n) < frac)).astype(np.uint32)
+    dev = torch.device("cuda")
+    cd = torch.from_numpy(counts.view(np.int32)).to(dev)
+    order = torch.full((n,), -1, dtype=torch.int32, device=dev)
+    offsets = torch.full((n + 1,), -1, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(_lib.size_call("gs_bin_prepare_workspace_size", n), 1), dtype=torch.uint8, device=dev)
+    cam = _lib.make_camera(np.eye(4, dtype=np.float32), 500.0, 500.0, 320, 240, 640, 480, NEAR, FAR,
+                           flags=_lib.GS_BIN_LOCAL)
+    assert _lib.lib().gs_bin_path(n, cam) == _lib.GS_BIN_PATH_LOCAL
+    call("gs_bin_prepare_3d", None, ptr(cd), None, n, cam, ptr(order), ptr(offsets), ptr(ws), ws.numel(),
+         _lib.stream_handle(dev))
+    vis = np.nonzero(counts)[0]
+    v = len(vis)
+    assert np.array_equal(order.cpu().numpy()[:v], vis)
+    want = np.zeros(n + 1, np.int64)
+    want[1:v + 1] = np.cumsum(counts[vis].astype(np.int64))
+    want[v + 1:] = want[v]
+    assert np.array_equal(offsets.cpu().numpy().view(np.uint32).astype(np.int64), want)
+
+
+# near / far planes whose depth keys take 1 and 2 passes of 9 bits (and 3 for the default)
+@pytest.mark.parametrize("far", [1.0 + 400 * 2.0 ** -23, 1.03, 60.0])
+@pytest.mark.parametrize("n", [1025, 1_000_000])
+def test_depth_order_few_key_bits(n, far):
+    check_depth_order(n, "culled_mix", 9, near=1.0, far=far)
+
+
+def check_depth_order(n, kind, max_count, near=NEAR, far=FAR):
     rng = np.random.default_rng(n + len(kind))
-    keys = depth_keys(n, kind, rng)
-    counts = rng.integers(0, 9, n).astype(np.uint32)
+    cull = host_order_key(far) - host_order_key(near)
+    keys = depth_keys(n, kind, rng, cull)
+    counts = rng.integers(0, max_count, n).astype(np.uint32)
     dev = torch.device("cuda")
     kd = torch.from_numpy(keys.view(np.int32)).to(dev)
     cd = torch.from_numpy(counts.view(np.int32)).to(dev)
     order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev)
     ws = torch.empty(max(_lib.size_call("gs_bin_prepare_workspace_size", n), 1), dtype=torch.uint8, device=dev)
-    cam = camera()
+    cam = camera(near=near, far=far)
     call("gs_bin_prepare_3d", None, ptr(cd), ptr(kd), n, cam, ptr(order), ptr(offsets), ptr(ws), ws.numel(),
          _lib.stream_handle(dev))
     want = np.argsort(keys, kind="stable")
     assert np.array_equal(order.cpu().numpy(), want)
     scan = np.zeros(n + 1, np.int64)
     np.cumsum(counts[want], out=scan[1:])
-    assert np.array_equal(offsets.cpu().numpy().astype(np.int64), scan)
+    assert scan[-1] < 1 << 32
+    assert np.array_equal(offsets.cpu().numpy().view(np.uint32).astype(np.int64), scan)
     if n == 100_003:  # without the offsets (nor the counts): the same order
         order2 = torch.empty_like(order)
         call("gs_bin_prepare_3d", None, None, ptr(kd), n, cam, ptr(order2), None, ptr(ws), ws.numel(),
