@@ -1816,8 +1816,8 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
 // ---------------------------------------------------------------------------------------
 constexpr int kTsBits = 9;
 constexpr int kTsRadix = 1 << kTsBits;
-constexpr int kTsWaves = 4;
-constexpr int kTsRounds = 16;
+constexpr int kTsWaves = 8;
+constexpr int kTsRounds = 8;
 constexpr int kTsCap = kTsWaves * kWave * kTsRounds;  // 4096 entries
 
 // Exclusive offsets of the digit counts s_cnt[W][kTsRadix] in digit-major, wavefront-minor
@@ -1857,8 +1857,11 @@ __device__ __forceinline__ void digit_offsets(uint32_t (*s_cnt)[kTsRadix], uint3
   __syncthreads();
 }
 
-// Lists of 2 .. kTsCap entries: keys in registers (position p = 1024 w + 64 r + lane for round
-// r of wavefront w), one LDS copy per pass to redistribute them.
+// Lists of 2 .. kTsCap entries: keys in registers, one LDS copy per pass to redistribute them.
+// The list is cut into kTsWaves contiguous spans of c = 64 ceil(len / (64 kTsWaves)) positions,
+// one per wavefront (position p = c w + 64 r + lane for round r of wavefront w), so that every
+// wavefront ranks about len / kTsWaves entries: the ranking rounds are a serial chain per
+// wavefront.
 __global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const uint32_t* __restrict__ ranges,
                                                                            const uint32_t* __restrict__ dkey,
                                                                            uint32_t* __restrict__ point_list,
@@ -1874,9 +1877,12 @@ __global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const
   const int len = static_cast<int>(ranges[2 * tile + 1] - r0);
   if (len <= 1 || len > kTsCap) return;  // the whole workgroup
   const uint64_t lt = lanemask_lt(lane);
-  const int base = wave * (kWave * kTsRounds) + lane;
+  const int span = kWave * ((len + kWave * kTsWaves - 1) / (kWave * kTsWaves));
+  const int base = wave * span + lane;
   // rounds of this wavefront holding entries (wave-uniform)
-  const int rounds = min(kTsRounds, max(0, (len - wave * (kWave * kTsRounds) + kWave - 1) / kWave));
+  const int rounds = min(span / kWave, max(0, (len - wave * span + kWave - 1) / kWave));
+  // entry of round r of this lane (a position of this wavefront's span inside the list)
+  auto mine = [&](int r) { return r < rounds && base + kWave * r < len; };
   uint32_t key[kTsRounds], val[kTsRounds], rank[kTsRounds];
   // loads at clamped positions, without branches: every one in flight at once
 #pragma unroll
@@ -1890,7 +1896,7 @@ __global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const
 #pragma unroll
     for (int r = 0; r < kTsRounds; ++r) {
       if (r >= rounds) break;  // wave-uniform
-      const bool valid = base + kWave * r < len;
+      const bool valid = mine(r);
       const uint32_t d = (key[r] >> shift) & (kTsRadix - 1);
       const uint64_t peers = match_bits<kTsBits>(d, valid);
       rank[r] = valid ? s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt)) : 0u;
@@ -1902,7 +1908,7 @@ __global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const
     digit_offsets<kTsWaves, kTsWaves * kWave>(s_cnt, s_wsum);
 #pragma unroll
     for (int r = 0; r < kTsRounds; ++r) {
-      if (base + kWave * r < len) {
+      if (mine(r)) {
         const uint32_t pos = s_cnt[wave][(key[r] >> shift) & (kTsRadix - 1)] + rank[r];
         s_k[pos] = key[r];
         s_v[pos] = val[r];
@@ -1911,19 +1917,16 @@ __global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < kTsRounds; ++r) {
-      const int p = base + kWave * r;
-      if (p < len) {
-        key[r] = s_k[p];
-        val[r] = s_v[p];
+      if (mine(r)) {
+        key[r] = s_k[base + kWave * r];
+        val[r] = s_v[base + kWave * r];
       }
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int r = 0; r < kTsRounds; ++r) {
-    const int p = base + kWave * r;
-    if (p < len) point_list[r0 + p] = val[r];
-  }
+  for (int r = 0; r < kTsRounds; ++r)
+    if (mine(r)) point_list[r0 + base + kWave * r] = val[r];
 }
 
 // Lists longer than kTsCap: one workgroup of kTlWaves wavefronts per list, each pass a digit
