@@ -1737,17 +1737,57 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
       s_span[kPerLane * lane + e] = sp[e];
       run += sp[e].y >> 16;
     }
+    uint32_t carry = 0u;  // the span holding the last instance of the previous segment
     for (uint32_t t0 = 0; t0 < total; t0 += kOwnerTable) {
       const uint32_t t1 = min<uint32_t>(t0 + kOwnerTable, total);
       wave_sync();  // the previous segment is done with the table
-      // owner table: every instance of the segment gets its span's index
+      // owner table: every instance of the segment gets its span's index. The spans' instances
+      // are consecutive in span order, so the owner of instance i is the largest span index
+      // whose first instance is at or before i: each non-empty span starting in the segment
+      // marks its first entry, and a prefix maximum over the entries (seeded with the span
+      // holding the segment's first instance) fills the rest, in the same few instructions
+      // whatever the spans' widths.
+      uint32_t* s_tw = reinterpret_cast<uint32_t*>(s_tbl);
+      for (int q = lane; q < kOwnerTable / 4; q += kWave) s_tw[q] = 0u;
+      wave_sync();
 #pragma unroll
       for (int e = 0; e < kPerLane; ++e) {
-        const uint32_t s = static_cast<uint32_t>(kPerLane * lane + e);
-        const uint32_t a = max(s_pre[s], t0), b = min(s_pre[s] + (sp[e].y >> 16), t1);
-        for (uint32_t i = a; i < b; ++i) s_tbl[i - t0] = static_cast<uint8_t>(s);
+        const uint32_t st = s_pre[kPerLane * lane + e];
+        if ((sp[e].y >> 16) != 0u && st >= t0 && st < t1) s_tbl[st - t0] = static_cast<uint8_t>(kPerLane * lane + e);
       }
       wave_sync();
+      {
+        constexpr int kBytes = kOwnerTable / kWave;  // 32 consecutive entries per lane
+        uint32_t w[kBytes / 4];
+#pragma unroll
+        for (int q = 0; q < kBytes / 4; ++q) w[q] = s_tw[lane * (kBytes / 4) + q];
+        uint32_t run = 0u;
+#pragma unroll
+        for (int q = 0; q < kBytes / 4; ++q)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) run = max(run, (w[q] >> (8 * b)) & 0xffu);
+        // the largest marker of the lanes before this one (a wavefront max-scan), and the seed
+        uint32_t incl = run;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t u = __shfl_up(incl, o, 64);
+          if (lane >= o) incl = max(incl, u);
+        }
+        uint32_t m = max(carry, __shfl_up(incl, 1, 64));
+        if (lane == 0) m = carry;
+#pragma unroll
+        for (int q = 0; q < kBytes / 4; ++q) {
+          uint32_t out = 0u;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            m = max(m, (w[q] >> (8 * b)) & 0xffu);
+            out |= m << (8 * b);
+          }
+          s_tw[lane * (kBytes / 4) + q] = out;
+        }
+      }
+      wave_sync();
+      carry = s_tbl[t1 - 1 - t0];
       for (uint32_t b0 = t0; b0 < t1; b0 += R * kWave) {
         uint32_t col[R], g[R], bit[R], low[R];
         bool live[R];
