@@ -132,16 +132,16 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  * Gaussian-index order, by one of three paths (gs_bin_path):
  *   GS_BIN_PATH_RADIX (default below GS_BIN_SPAN_MIN_GAUSSIANS): a stable radix sort of the
  *     Gaussians by depth, then the instances emitted in that order and stably radix-sorted by tile;
- *   GS_BIN_PATH_LOCAL: the instances emitted in index order and stably radix-sorted by tile,
- *     then each tile's list stably sorted by depth key;
+ *   GS_BIN_PATH_LOCAL (opt-in, at most 2048 * 4096 Gaussians): the Gaussians with tiles listed
+ *     in index order, their instances emitted in that order and stably radix-sorted by tile, then
+ *     each tile's list stably sorted by depth key;
  *   GS_BIN_PATH_SPANS: the depth sort, then two counting passes over the Gaussians' row spans
  *     (the run of tiles a Gaussian touches in one tile row): by tile row over the Gaussians in
  *     depth order, then by column within each row, which writes every instance once.
- * The caller runs gs_bin_prepare_3d for the radix and span paths (the depth order; the instance
- * offsets in that order only for the radix path), gs_scan_u32 of tiles_touched (the instance
- * offsets in index order) for the local path; then gs_bin_fill_3d.
+ * The caller runs gs_bin_prepare_3d (the order and, except on the span path, the instance
+ * offsets), then gs_bin_fill_3d.
  *
- * gs_bin_prepare_3d: depth ordering.
+ * gs_bin_prepare_3d: depth ordering (radix and span paths).
  *   depth_keys [n] from gs_preprocess_fwd with the same camera (order keys of the view depth
  *   relative to the near plane's, culled Gaussians after every visible one, so the sort reads
  *   only as many bits as the near/far range needs), or NULL (then computed from splat_rec and
@@ -151,6 +151,10 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *                         radix path) exclusive scan of tiles_touched[order[j]]; offsets[n] = m,
  *                         the number of instances
  *   tiles_touched may be NULL when offsets is NULL and depth_keys is given.
+ *   On the tile-local path (gs_bin_path): order [n] = the Gaussians with tiles_touched > 0 in
+ *   index order (entries past their count v unspecified), offsets [n + 1] = the exclusive scan of
+ *   their counts, offsets[k] = m for k in [v, n]; tiles_touched, order and offsets are required,
+ *   depth_keys and splat_rec are not read.
  *   Workspace from gs_bin_prepare_workspace_size(n).
  * gs_bin_fill_3d: tile lists, ranges, bucket offsets. splat_rec as gs_preprocess_fwd wrote it
  *   (a culled Gaussian's record holds the empty bounds (0, -1, 0, -1)); m = the sum of the
@@ -162,9 +166,8 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *   bucket_offsets [T+1]  exclusive scan of ceil(len/32); bucket_offsets[T] = number of buckets
  *   bucket_list (may be NULL): the list gs_blend_fwd_3d appends to; its header is cleared
  *                         here, so that call can take GS_BLEND_LIST_CLEARED
- *   order, offsets: radix path: as gs_bin_prepare_3d wrote them; span path: the order, offsets
- *   NULL; local path: order NULL, offsets the exclusive scan of tiles_touched in index order
- *   (depth_keys needed).
+ *   order, offsets: as gs_bin_prepare_3d wrote them for the same path (offsets NULL on the span
+ *   path); the local path also needs depth_keys.
  *   Workspace from gs_bin_workspace_size(n, m, tiles_x, tiles_y, cam->flags).
  * ------------------------------------------------------------------------------------- */
 #define GS_BIN_SPAN_MAX_TILES 512
