@@ -3,8 +3,9 @@ parametrised 2D splat renderer with two custom backward passes, on the MI355X.
 
 Mode "pixel" is the per-pixel atomic backward (A); mode "splat" is the bucketed backward (B)
 that replays from forward checkpoints. float32 and float64 are supported, on CUDA (ROCm)
-tensors only; there is no CPU build.
+tensors only; there is no CPU build. ref_render (and ref_state in splat2d.ops) is the dense
+PyTorch reference model, for checking and small scenes only.
 """
-from splat2d.ops import MODES, Mode, TileBins, bin_tiles, load_extension, render
+from splat2d.ops import MODES, Mode, TileBins, bin_tiles, load_extension, ref_render, render
 
-__all__ = ["MODES", "Mode", "TileBins", "bin_tiles", "load_extension", "render"]
+__all__ = ["MODES", "Mode", "TileBins", "bin_tiles", "load_extension", "ref_render", "render"]

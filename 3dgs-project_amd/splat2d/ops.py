@@ -24,6 +24,7 @@ from torch import Tensor
 
 from amdsplat import raster2d as R2
 from amdsplat._lib import call, ptr
+from splat2d.reference import RefState, ref_render, ref_state  # noqa: F401  (the dense reference model)
 
 Mode = Literal["pixel", "splat"]
 MODES: tuple = ("pixel", "splat")

@@ -298,6 +298,28 @@ def test_splat2d_gradcheck_float64(name, mode):
     assert torch.autograd.gradcheck(fn, tuple(ph0_params(f, torch.float64)), eps=1e-6, atol=1e-8, rtol=1e-6)
 
 
+@pytest.mark.parametrize("mode", ["splat", "pixel"])
+@pytest.mark.parametrize("name", ["seed1_n32", "dense_n96", "sparse_n150"])
+def test_splat2d_render_against_ref_render(name, mode):
+    """phase0/tests/gradcheck/test_gradcheck.py:62-81 and :95-100 with the package's own
+    ref_render (float64 autograd, on the GPU) as the reference: float32 grads within 1e-5,
+    float64 grads within 1e-10, the float64 image within 1e-12."""
+    f = load(f"phase0_{name}")
+    H, W = int(f["H"]), int(f["W"])
+    gi = cuda(f["grad_image"], torch.float64)
+    ref = ph0_params(f, torch.float64)
+    want_img = splat2d.ref_render(*ref, H, W)
+    want = torch.autograd.grad(want_img, ref, gi)
+    for dtype, gtol in ((torch.float32, 1e-5), (torch.float64, 1e-10)):
+        params = ph0_params(f, dtype)
+        image = splat2d.render(*params, H, W, mode=mode)
+        if dtype == torch.float64:
+            assert rel(image, want_img) < 1e-12
+        got = torch.autograd.grad(image, params, gi.to(dtype))
+        for key, g, w in zip(("means", "chol", "opacity_logit", "colors"), got, want):
+            assert rel(g, w) < gtol, f"{name}/{mode}/{dtype}/{key}: {rel(g, w):.2e}"
+
+
 def test_splat2d_extension_surface_and_limitless_backward():
     """The extension functions of phase0/csrc/macrotile/bindings.cpp:156-239 with their return
     values; backward_splat without a per-pixel limit (the reference's signature) equals the

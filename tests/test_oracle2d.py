@@ -227,3 +227,57 @@ def test_render_reference_matches_reference_renderer(name):
     assert rel(img2.numpy(), f["image"]) < 1e-12
     img3 = gs2d.render_reference(*[t.detach() for t in x], fixture_bins(f), torch.tensor(f["bg"]), pixels_per_block=7)
     assert rel(img3.numpy(), f["image"]) < 1e-12
+
+
+# ---------------------------------------------------------------------------------------
+# splat2d.ref_state / ref_render (the dense phase0 model) against the reference's own
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", PH0)
+def test_splat2d_ref_render_matches_reference_model(name):
+    """Image, T, composited-splat counts and autograd gradients (upstream grad_image) of
+    splat2d.ref_state / ref_render in float64 against what the reference's ref_state /
+    ref_render gave for the same scene (the golden fixture): 1e-12, counts exact
+    (phase0/tests/gradcheck/test_gradcheck.py:96-100, test_opcount.py:89-92)."""
+    from splat2d.ops import ref_render, ref_state
+
+    f = load(f"phase0_{name}")
+    H, W = int(f["H"]), int(f["W"])
+    x = [torch.tensor(f[k], dtype=torch.float64, requires_grad=True)
+         for k in ("means", "chol", "opacity_logit", "colors")]
+    st = ref_state(*x, H, W)
+    assert rel(st.image.detach().numpy(), f["image"]) < 1e-12
+    assert rel(st.t_final.detach().numpy(), f["t_final"]) < 1e-12
+    assert np.array_equal(st.contributes.sum(-1).numpy(), f["n_contrib"])
+    # a composited splat passed the alpha test (raw alpha, clamped at 0.99, >= 1/255)
+    assert bool((torch.clamp(st.raw_alpha, max=0.99)[st.contributes] >= 1.0 / 255.0).all())
+    grads = torch.autograd.grad(ref_render(*x, H, W), x, torch.tensor(f["grad_image"]))
+    for g, key in zip(grads, ("g_means", "g_chol", "g_opacity_logit", "g_colors")):
+        assert rel(g.numpy(), f[key]) < 1e-12, key
+    # blocks of another size (31 pixels) give the same image
+    small = ref_state(*[t.detach() for t in x], H, W, max_block_elems=31 * x[0].shape[0])
+    assert rel(small.image.numpy(), f["image"]) < 1e-12
+    assert torch.equal(small.contributes, st.contributes)
+
+
+def test_splat2d_ref_state_empty_and_opaque_stop():
+    """No splats: a black image with T = 1. A stack of opaque splats (alpha 0.99 each): T falls
+    by 100x per splat, so the third splat is the last composited one (T before it 1e-4, T
+    before the fourth 1e-6 < 1e-4)."""
+    from splat2d.ops import ref_state
+
+    z = torch.zeros(0, 2, dtype=torch.float64)
+    st = ref_state(z, torch.zeros(0, 3, dtype=torch.float64), torch.zeros(0, dtype=torch.float64),
+                   torch.zeros(0, 3, dtype=torch.float64), 5, 7)
+    assert st.image.shape == (5, 7, 3) and float(st.image.abs().max()) == 0.0
+    assert float((st.t_final - 1).abs().max()) == 0.0 and st.contributes.shape == (5, 7, 0)
+    k = 5
+    means = torch.tensor([[2.5, 2.5]], dtype=torch.float64).repeat(k, 1)
+    chol = torch.tensor([[1e-3, 0.0, 1e-3]], dtype=torch.float64).repeat(k, 1)  # flat over the image
+    logit = torch.full((k,), 50.0, dtype=torch.float64)  # sigmoid -> 1, clamped to 0.99
+    colors = torch.eye(3, dtype=torch.float64).repeat(2, 1)[:k]
+    st = ref_state(means, chol, logit, colors, 4, 4)
+    assert st.contributes.sum(-1).unique().tolist() == [3]
+    a = 0.99
+    want = torch.tensor([a, a * (1 - a), a * (1 - a) ** 2], dtype=torch.float64)  # weights of splats 0, 1, 2
+    assert torch.allclose(st.image[0, 0], want, rtol=1e-9, atol=0)
+    assert abs(float(st.t_final[0, 0]) - (1 - a) ** 3) < 1e-15
