@@ -23,7 +23,11 @@ struct ShStage {
   static constexpr int R = 3 * K;            // floats per Gaussian row
   static constexpr int RH = K > 9 ? 32 : 64;  // rows per pass
   static constexpr int NH = 64 / RH;         // passes
-  static constexpr int CP = R | 1;           // padded LDS row (odd: conflict-free)
+  // Padded LDS row. Rows of whole float4s (degrees 1 and 3) take an odd number of float4s and
+  // are moved with 16-byte LDS accesses (lanes reading their own rows hit distinct banks);
+  // other rows take an odd number of floats (4-byte accesses, conflict-free the same way).
+  static constexpr bool kVec = R % 4 == 0;
+  static constexpr int CP = kVec ? 4 * ((R / 4) | 1) : (R | 1);
 };
 
 // SH coefficients of the Gaussians: one [n, K, 3] array, or (split) the DC [n, 1, 3] and the
@@ -64,7 +68,11 @@ __device__ __forceinline__ void rows_to_lds(const float* __restrict__ blk, int n
             // a float4 never crosses a row
             const int row = f4 / (RW / 4), q = f4 - row * (RW / 4);
             float* d = srow + row * CP + c0 + 4 * q;
-            d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+            if (CP % 4 == 0 && c0 == 0) {
+              *reinterpret_cast<float4*>(d) = make_float4(v[it].x, v[it].y, v[it].z, v[it].w);
+            } else {
+              d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+            }
           }
         }
         return;
@@ -110,7 +118,12 @@ __device__ __forceinline__ void lds_to_rows(float* __restrict__ blk, int nr, con
         if constexpr (RW % 4 == 0) {  // a float4 never crosses a row
           const int row = f4 / (RW / 4), q = f4 - row * (RW / 4);
           const float* d = srow + row * CP + c0 + 4 * q;
-          vv[0] = d[0]; vv[1] = d[1]; vv[2] = d[2]; vv[3] = d[3];
+          if (CP % 4 == 0 && c0 == 0) {
+            const float4 v = *reinterpret_cast<const float4*>(d);
+            vv[0] = v.x; vv[1] = v.y; vv[2] = v.z; vv[3] = v.w;
+          } else {
+            vv[0] = d[0]; vv[1] = d[1]; vv[2] = d[2]; vv[3] = d[3];
+          }
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -188,8 +201,8 @@ struct ShPrefetch {
         const int f4 = lane + 64 * it;
         if (row_needed(f4, need)) {  // a float4 never crosses a row
           const int row = f4 / (R / 4), q = f4 - row * (R / 4);
-          float* d = srow + row * CP + 4 * q;
-          d[0] = v[it].x; d[1] = v[it].y; d[2] = v[it].z; d[3] = v[it].w;
+          // (CP % 4 == 0 for these rows; the float4 rebuilt from its parts keeps v in registers)
+          *reinterpret_cast<float4*>(srow + row * CP + 4 * q) = make_float4(v[it].x, v[it].y, v[it].z, v[it].w);
         }
       }
     }
@@ -327,6 +340,78 @@ __device__ __forceinline__ void compute_geom(const float* __restrict__ means,
   g.vis = vis;
 }
 
+// acc[ch] = basis[0] row[ch] + sum over 0 < k < active of basis[k] row[3 k + ch] (fmaf, each
+// channel's terms in k order) from the lane's LDS row; rows of whole float4s are read 16 bytes
+// at a time (the same operations in the same order: the same bits).
+template <int K>
+__device__ __forceinline__ void sh_dot_row(const float* row, const float* basis, int active, float acc[3]) {
+  using St = ShStage<K>;
+  if constexpr (St::kVec) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+    for (int c4 = 0; c4 < K / 4; ++c4) {  // 4 coefficients = 12 floats = 3 float4
+      const float4 v0 = r4[3 * c4], v1 = r4[3 * c4 + 1], v2 = r4[3 * c4 + 2];
+      const float c[4][3] = {{v0.x, v0.y, v0.z}, {v0.w, v1.x, v1.y}, {v1.z, v1.w, v2.x}, {v2.y, v2.z, v2.w}};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = 4 * c4 + j;
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+          if (k == 0) {
+            acc[ch] = basis[0] * c[j][ch];
+          } else {
+            const float t = fmaf(basis[k], c[j][ch], acc[ch]);
+            acc[ch] = k < active ? t : acc[ch];  // a select: no branches in the unrolled body
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) {
+      acc[ch] = basis[0] * row[ch];
+      for (int k = 1; k < active; ++k) acc[ch] = fmaf(basis[k], row[3 * k + ch], acc[ch]);
+    }
+  }
+}
+
+// Backward of the SH dot: gb[k] = row_k . gcol (the basis gradient) and the row overwritten
+// with the coefficient gradients basis[k] gcol (zero for k >= active), read and written 16
+// bytes at a time for rows of whole float4s.
+template <int K>
+__device__ __forceinline__ void sh_row_grads(float* row, const float* basis, int active, const float gcol[3],
+                                             float* gb) {
+  using St = ShStage<K>;
+  if constexpr (St::kVec) {
+    float4* r4 = reinterpret_cast<float4*>(row);
+#pragma unroll
+    for (int c4 = 0; c4 < K / 4; ++c4) {  // 4 coefficients = 12 floats = 3 float4
+      const float4 v0 = r4[3 * c4], v1 = r4[3 * c4 + 1], v2 = r4[3 * c4 + 2];
+      const int k = 4 * c4;
+      const bool on0 = k < active, on1 = k + 1 < active, on2 = k + 2 < active, on3 = k + 3 < active;
+      gb[k] = on0 ? v0.x * gcol[0] + v0.y * gcol[1] + v0.z * gcol[2] : 0.0f;
+      gb[k + 1] = on1 ? v0.w * gcol[0] + v1.x * gcol[1] + v1.y * gcol[2] : 0.0f;
+      gb[k + 2] = on2 ? v1.z * gcol[0] + v1.w * gcol[1] + v2.x * gcol[2] : 0.0f;
+      gb[k + 3] = on3 ? v2.y * gcol[0] + v2.z * gcol[1] + v2.w * gcol[2] : 0.0f;
+      const float b0 = on0 ? basis[k] : 0.0f, b1 = on1 ? basis[k + 1] : 0.0f;
+      const float b2 = on2 ? basis[k + 2] : 0.0f, b3 = on3 ? basis[k + 3] : 0.0f;
+      r4[3 * c4] = make_float4(b0 * gcol[0], b0 * gcol[1], b0 * gcol[2], b1 * gcol[0]);
+      r4[3 * c4 + 1] = make_float4(b1 * gcol[1], b1 * gcol[2], b2 * gcol[0], b2 * gcol[1]);
+      r4[3 * c4 + 2] = make_float4(b2 * gcol[2], b3 * gcol[0], b3 * gcol[1], b3 * gcol[2]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const bool on = k < active;
+      gb[k] = on ? row[3 * k] * gcol[0] + row[3 * k + 1] * gcol[1] + row[3 * k + 2] * gcol[2] : 0.0f;
+      const float bk = on ? basis[k] : 0.0f;
+      row[3 * k] = bk * gcol[0];
+      row[3 * k + 1] = bk * gcol[1];
+      row[3 * k + 2] = bk * gcol[2];
+    }
+  }
+}
+
 template <int K>
 __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     const float* __restrict__ means, const float* __restrict__ log_scales,
@@ -335,8 +420,8 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
     uint32_t* __restrict__ tiles_touched, uint32_t* __restrict__ depth_keys, uint32_t* __restrict__ wave_counts) {
   using St = ShStage<K>;
   // per wavefront: the tile-count scratch, then the SH rows
-  constexpr int kWords = St::RH * St::CP > kCountScratchWords ? St::RH * St::CP : kCountScratchWords;
-  __shared__ float s_sh[4][kWords];
+  constexpr int kWords = ((St::RH * St::CP > kCountScratchWords ? St::RH * St::CP : kCountScratchWords) + 3) & ~3;
+  __shared__ __align__(16) float s_sh[4][kWords];  // each wavefront's rows 16-byte aligned
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -417,12 +502,7 @@ __global__ __launch_bounds__(256) void preprocess_fwd_kernel(
       }
       wave_sync();
       if (g.vis && lane / St::RH == h) {
-        const float* row = srow + (lane - St::RH * h) * St::CP;
-#pragma unroll
-        for (int ch = 0; ch < 3; ++ch) {
-          acc[ch] = basis[0] * row[ch];
-          for (int k = 1; k < active; ++k) acc[ch] = fmaf(basis[k], row[3 * k + ch], acc[ch]);
-        }
+        sh_dot_row<K>(srow + (lane - St::RH * h) * St::CP, basis, active, acc);
       }
     }
     if (g.vis) {
@@ -488,7 +568,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
     float* __restrict__ g_opacity, ShOut g_sh) {
   using St = ShStage<K>;
-  __shared__ float s_sh[4][St::RH * St::CP];
+  __shared__ __align__(16) float s_sh[4][St::RH * St::CP];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wave_first = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;
@@ -534,24 +614,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
           // the forward's colour clamp (a channel clamped at 0 passes no gradient), recomputed
           // from the same rows and basis in the forward's operation order: the same bits, without
           // reading the 64-byte splat record for its mask
+          float acc[3];
+          sh_dot_row<K>(row, basis, active, acc);
 #pragma unroll
-          for (int ch = 0; ch < 3; ++ch) {
-            float acc = basis[0] * row[ch];
-            for (int k = 1; k < active; ++k) acc = fmaf(basis[k], row[3 * k + ch], acc);
-            gcol[ch] = (acc + 0.5f < 0.0f) ? 0.0f : g2[6 + ch];
-          }
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const bool on = k < active;
-            gb[k] = on ? row[3 * k] * gcol[0] + row[3 * k + 1] * gcol[1] + row[3 * k + 2] * gcol[2] : 0.0f;
-            // overwrite the row with the coefficient gradients (after its values were read)
-            const float bk = on ? basis[k] : 0.0f;
-            row[3 * k] = bk * gcol[0];
-            row[3 * k + 1] = bk * gcol[1];
-            row[3 * k + 2] = bk * gcol[2];
-          }
+          for (int ch = 0; ch < 3; ++ch) gcol[ch] = (acc[ch] + 0.5f < 0.0f) ? 0.0f : g2[6 + ch];
+          // overwrite the row with the coefficient gradients (after its values were read)
+          sh_row_grads<K>(row, basis, active, gcol, gb);
         } else if (valid) {
-          for (int c = 0; c < St::R; ++c) row[c] = 0.0f;
+          if constexpr (St::kVec) {
+            for (int q = 0; q < St::R / 4; ++q) reinterpret_cast<float4*>(row)[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          } else {
+            for (int c = 0; c < St::R; ++c) row[c] = 0.0f;
+          }
         }
       }
       wave_sync();
