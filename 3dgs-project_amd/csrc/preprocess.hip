@@ -386,6 +386,7 @@ __device__ __forceinline__ void sh_row_grads(float* row, const float* basis, int
     float4* r4 = reinterpret_cast<float4*>(row);
 #pragma unroll
     for (int c4 = 0; c4 < K / 4; ++c4) {  // 4 coefficients = 12 floats = 3 float4
+      if (c4) __builtin_amdgcn_sched_barrier(0);  // one chunk of row values live at a time
       const float4 v0 = r4[3 * c4], v1 = r4[3 * c4 + 1], v2 = r4[3 * c4 + 2];
       const int k = 4 * c4;
       const bool on0 = k < active, on1 = k + 1 < active, on2 = k + 2 < active, on3 = k + 3 < active;
