@@ -177,8 +177,8 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
         binning = 4 * n + 48 * n_visible + 40 * spans + 4 * m + 20 * T + 4 * B
     return {
         # params 44 B/Gaussian + tiles_touched and depth key 8 B; SH 12 K B and the 64 B record
-        # per visible one
-        "preprocess": 44 * n + 8 * n + n_visible * (12 * K + 64),
+        # per visible one; the empty bounds (16 B) of each culled one's record
+        "preprocess": 44 * n + 8 * n + n_visible * (12 * K + 64) + 16 * (n - n_visible),
         "depth_order": depth,
         "binning": binning,
         # per staged list entry: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4;
@@ -189,8 +189,9 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
         # per bucket-splat step: id + record; per reduced bucket-splat: 9 fp32 atomics (11 with
         # the |dL/dmean2d| sums)
         "blend_bwd": active_buckets * (4096 + 256 * 28) + splat_steps * (4 + 64) + used_pairs * 4 * atomics_per_pair,
-        # params, SH, record and grad2d of the visible; every output row written
-        "preprocess_bwd": n_visible * (44 + 12 * K + 64 + 48) + n * (44 + 12 * K),
+        # tiles_touched of every Gaussian; params, SH and grad2d of the visible (the colour clamp
+        # is recomputed from the SH rows, the record is not read); every output row written
+        "preprocess_bwd": 4 * n + n_visible * (44 + 12 * K + 48) + n * (44 + 12 * K),
     }
 
 
