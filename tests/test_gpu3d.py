@@ -120,6 +120,46 @@ def test_long_tile_lists_match_oracle(binning, same_depth):
             assert e - s > 4096 and np.all(np.diff(pl[s:e]) > 0)
 
 
+EDGE = {
+    # name: (n, W, H, scale range, opacity range, depth range, x/y spread)
+    "one_pixel": (50, 1, 1, (0.01, 0.1), (0.05, 0.95), (2.0, 8.0), 0.6),
+    "sub_tile": (300, 7, 5, (0.01, 0.1), (0.05, 0.95), (2.0, 8.0), 0.6),
+    "one_tile": (500, 16, 16, (0.01, 0.1), (0.05, 0.95), (2.0, 8.0), 0.6),
+    "row_strip": (3_000, 1297, 9, (0.005, 0.05), (0.05, 0.95), (2.0, 8.0), 0.6),
+    "column_strip": (3_000, 9, 700, (0.005, 0.05), (0.05, 0.95), (2.0, 8.0), 0.6),
+    # (three different scales: an isotropic splat's rotation gradient is zero, which leaves a
+    # relative error nothing to measure against)
+    "single": (1, 64, 48, (0.03, 0.08), (0.9, 0.9), (3.0, 3.0), 0.05),
+    # depths across the near plane (0.2): culled ones, and splats just past it that cover the image
+    "near_plane": (2_000, 160, 120, (0.01, 0.1), (0.05, 0.95), (0.05, 1.0), 0.6),
+    # splats wider than the image
+    "huge": (300, 200, 152, (0.5, 2.0), (0.05, 0.95), (2.0, 8.0), 0.6),
+}
+
+
+def edge_scene(name, seed=21):
+    n, W, H, sc_, op, dp, spread = EDGE[name]
+    return scenes.small_scene(n, W, H, seed=seed, sh_coeffs=16, scale=sc_, opacity=op, depth=dp, spread=spread)
+
+
+@pytest.mark.parametrize("binning", ["radix", "spans", "local"])
+@pytest.mark.parametrize("name", list(EDGE))
+def test_edge_scenes_match_oracle(name, binning):
+    """Canvases of one pixel, under one tile, exactly one tile, one tile high or wide; one
+    Gaussian; depths across the near plane; splats wider than the image: records, keys, lists,
+    ranges, buckets, image, T, n_contrib and checkpoints as the oracle, on every binning path."""
+    sc = edge_scene(name)
+    cam = dataclasses.replace(sc.cameras[0], binning=binning)
+    check_forward(sc, cam, amb_max=max(1e-3, 2.0 / (cam.width * cam.height)))
+
+
+@pytest.mark.parametrize("name", ["one_pixel", "sub_tile", "row_strip", "column_strip", "single", "near_plane",
+                                  "huge"])
+def test_edge_scenes_gradients_match_float64_autograd(name):
+    sc = edge_scene(name, seed=22)
+    check_gradients(sc, sc.cameras[0], name)
+
+
 @pytest.mark.parametrize("name", ["tiny", "small_splats", "heavy_overlap"])
 def test_proper_antialiasing_forward_matches_oracle(name):
     sc = make(name, seed=4)
@@ -164,7 +204,12 @@ def check_forward(sc, cam=None, amb_max=1e-3):
                                      ("tiny", True), ("small_splats", True)])
 def test_gradients_match_float64_autograd(name, aa):
     sc = make(name, seed=1)
-    cam = dataclasses.replace(sc.cameras[0], proper_antialiasing=aa)
+    check_gradients(sc, dataclasses.replace(sc.cameras[0], proper_antialiasing=aa), name)
+
+
+def check_gradients(sc, cam, name):
+    """Every parameter gradient of the GPU backward (seeded upstream image and alpha gradients)
+    against float64 autograd of the dense restatement over the oracle's lists."""
     deg = 3
     p, fs = gpu_forward(sc, deg, cam=cam)
     g = torch.Generator().manual_seed(7)
@@ -178,7 +223,11 @@ def test_gradients_match_float64_autograd(name, aa):
     pre = D.preprocess64(*P, cam, deg)
     img, fT = D.blend64(pre["mean2d"], pre["conic"], pre["opacity"], pre["color"], ref["point_list"],
                         ref["ranges"], mask, cam.width, cam.height, BG)
-    assert np.abs(img.detach().numpy() - np_(fs.image))[:, ~ref["amb"]].max(initial=0.0) <= FWD_TOL
+    # float32 blending against the float64 restatement: the rounding grows with the splats a
+    # pixel blends (a few units of 2^-24 each); the oracle, in the kernels' float32 operation
+    # order, is held to FWD_TOL alone by check_forward
+    tol64 = FWD_TOL + 2.0 ** -22 * ref["n_contrib"]
+    assert (np.abs(img.detach().numpy() - np_(fs.image)) <= tol64)[:, ~ref["amb"]].all()
     ((img * gi).sum() + ((1 - fT) * ga).sum()).backward()
     for gname, a, b in zip(("means", "log_scales", "quats", "opacity_logits", "sh"), grads[:5], P):
         e = D.rel_err(np_(a), b.grad)
