@@ -192,9 +192,12 @@ def _check_inputs(means, log_scales, quats, opacity_logits, sh):
 
 
 def _sh_parts(sh):
-    """(coefficients or DC, rest or None, K) of an [N, K, 3] tensor or a (DC, rest) pair."""
+    """(coefficients or DC, rest or None, K) of an [N, K, 3] tensor or a (DC, rest) pair. A pair
+    whose rest holds no coefficients ([N, 0, 3]: Faster-GS's degree-0 model) is the DC alone."""
     if isinstance(sh, (tuple, list)):
         a, b = sh[0].contiguous(), sh[1].contiguous()
+        if b.dim() == 3 and b.shape[1] == 0:
+            return a, None, 1
         return a, b, 1 + b.shape[1]
     sh = sh.contiguous()
     return sh, None, sh.shape[1]
@@ -367,6 +370,8 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
     if sh_b is None:
         g_sh = torch.empty(n, fs.sh_coeffs, 3, dtype=torch.float32, device=dev)
         g_a, g_b = g_sh, None
+        if isinstance(sh, (tuple, list)):  # (DC, empty rest): the pair back, the rest's gradient empty
+            g_sh = (g_sh, torch.empty(n, 0, 3, dtype=torch.float32, device=dev))
     else:
         g_a = torch.empty(n, 1, 3, dtype=torch.float32, device=dev)
         g_b = torch.empty(n, fs.sh_coeffs - 1, 3, dtype=torch.float32, device=dev)

@@ -388,10 +388,11 @@ def test_equal_depths_keep_index_order(binning):
         assert np.all(np.diff(pl[s:e].astype(np.int64)) > 0)
 
 
-@pytest.mark.parametrize("K", [4, 9, 16])
+@pytest.mark.parametrize("K", [1, 4, 9, 16])
 def test_split_sh_layout_equals_single_tensor(K):
     """The (DC, rest) pair of Faster-GS's model gives the records and gradients of the single
-    [N, K, 3] tensor bit for bit."""
+    [N, K, 3] tensor bit for bit (K = 1: the degree-0 model's empty rest, whose gradient is an
+    empty [N, 0, 3])."""
     sc = make("partial_tiles", seed=5, sh_coeffs=K)
     cam = sc.cameras[0]
     p = [t.cuda().contiguous() for t in sc.params()]
@@ -410,7 +411,17 @@ def test_split_sh_layout_equals_single_tensor(K):
     # two backward runs: the blend's atomics may add in another order, hence 1e-5 relative
     for a, b in zip(ga[:4], gb[:4]):
         assert rel(a, b) < 1e-5
-    assert rel(gb[4][0], ga[4][:, :1]) < 1e-5 and rel(gb[4][1], ga[4][:, 1:]) < 1e-5
+    assert rel(gb[4][0], ga[4][:, :1]) < 1e-5 and tuple(gb[4][1].shape) == (sc.n, K - 1, 3)
+    if K > 1:
+        assert rel(gb[4][1], ga[4][:, 1:]) < 1e-5
+    # the same through the autograd operator, the rest a leaf of its own
+    leaves = [t.clone().requires_grad_(True) for t in (*p[:4], *split)]
+    Kmat = torch.tensor([[cam.fx, 0.0, cam.cx], [0.0, cam.fy, cam.cy], [0.0, 0.0, 1.0]])
+    img, _, _ = R.rasterize(leaves[0], leaves[1], leaves[2], leaves[3], (leaves[4], leaves[5]), cam.viewmat, Kmat,
+                            cam.width, cam.height, bg=BG, near=cam.near, far=cam.far, sh_degree=deg)
+    (img * gi).sum().backward()
+    assert leaves[5].grad is not None and tuple(leaves[5].grad.shape) == (sc.n, K - 1, 3)
+    assert rel(leaves[4].grad, ga[4][:, :1]) < 1e-5
 
 
 @pytest.mark.parametrize("rows", [2, 3])
