@@ -187,6 +187,34 @@ def test_C_forward_backward_call_shape_and_determinism():
 
 
 @gpu
+def test_C_degree_zero_model():
+    """A DC-only model as Faster-GS keeps it (SH rest [N, 0, 3], active_sh_bases 1): _C.forward /
+    _C.backward and diff_rasterize render the DC alone, the same image and DC gradient as the
+    single [N, 1, 3] tensor, and hand back an empty rest gradient."""
+    sc = scenes.small_scene(20_000, 333, 250, seed=12, sh_coeffs=1)
+    cam = sc.cameras[0]
+    params = faster_gs_params(sc)
+    assert tuple(params[5].shape) == (sc.n, 0, 3)
+    settings = settings_of(cam, active_sh_bases=1).as_tuple()
+    image, pb, tb, ib, bb, n_inst, n_buckets, sel = _C.forward(*params, *settings)
+    gi = torch.randn(image.shape, generator=torch.Generator().manual_seed(4)).cuda()
+    means, scales, rotations, opacities, sh0, sh_rest = params
+    g = _C.backward(None, gi, image, means, scales, rotations, opacities, sh_rest, pb, tb, ib, bb, *settings,
+                    n_inst, n_buckets, sel, 0)
+    fs = R.forward_pass(*[t.cuda() for t in sc.params()], cam, bg=(0.2, 0.5, 0.8))
+    ref = R.backward_pass(fs, *[t.cuda() for t in sc.params()], gi, abs_grad=False)
+    torch.cuda.synchronize()
+    assert torch.equal(fs.image, image)
+    assert tuple(g[5].shape) == (sc.n, 0, 3)
+    assert D.rel_err(g[4].cpu(), ref[4].cpu()) < 1e-5 and D.rel_err(g[0].cpu(), ref[0].cpu()) < 1e-5
+    leaves = [t.clone().requires_grad_(True) for t in params]
+    img2 = diff_rasterize(*leaves, None, RasterizerSettings(*settings))
+    (img2 * gi).sum().backward()
+    assert torch.equal(img2.detach(), image) and tuple(leaves[5].grad.shape) == (sc.n, 0, 3)
+    assert D.rel_err(leaves[4].grad.cpu(), ref[4].cpu()) < 1e-5
+
+
+@gpu
 def test_C_empty_scene():
     """All splats behind the camera: no instances, no buckets, zero gradients
     (phase1/tests/test_parity.py:143-153)."""
