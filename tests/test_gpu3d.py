@@ -293,6 +293,24 @@ def test_empty_scene_behind_camera():
         assert float(g.abs().sum()) == 0.0
 
 
+def test_model_without_gaussians():
+    """N = 0 through the autograd operator: the background, alpha 0, no instances, and empty
+    gradients of the parameters' shapes."""
+    sc = make("tiny", seed=3)
+    cam = sc.cameras[0]
+    leaves = [t[:0].cuda().contiguous().requires_grad_(True) for t in sc.params()]
+    Kmat = torch.tensor([[cam.fx, 0.0, cam.cx], [0.0, cam.fy, cam.cy], [0.0, 0.0, 1.0]])
+    img, alpha, aux = R.rasterize(*leaves, cam.viewmat, Kmat, cam.width, cam.height, bg=BG, near=cam.near,
+                                  far=cam.far)
+    torch.cuda.synchronize()
+    assert aux["n_instances"] == 0 and int(aux["n_buckets"]) == 0
+    assert torch.equal(img, torch.tensor(BG, device="cuda")[:, None, None].expand_as(img).contiguous())
+    assert float(alpha.detach().abs().max()) == 0.0
+    (img.sum() + alpha.sum()).backward()
+    for t in leaves:
+        assert t.grad is not None and t.grad.shape == t.shape and t.grad.numel() == 0
+
+
 def test_deterministic_and_back_to_back():
     """Integer outputs identical across 10 unsynchronised calls; gradients within the noise of
     float atomics arriving in a different order (phase1/tests/test_parity.py:131-140)."""
