@@ -444,7 +444,7 @@ def bench_3d(args, ceilings) -> dict:
     leaves = [t.clone().requires_grad_(True) for t in params]
 
     def autograd_step(k):
-        """The operator north_star names: rasterize(...) -> image, then image.backward(grad)."""
+        """The headline operator: rasterize(...) -> image, then image.backward(grad)."""
         pose = k % len(cams)
         c = cams[pose]
         for t in leaves:
