@@ -38,9 +38,9 @@ GS_ABS_GRAD = 2  # gs_blend_bwd_3d flag: also accumulate |dL/dmean2d| into grad2
 GS_BLEND_LIST_CLEARED = 1  # gs_blend_fwd_3d flag: gs_bin_fill_3d cleared the bucket list's header
 GS_FLOAT32, GS_FLOAT64, GS_BFLOAT16 = 0, 1, 2
 GS_CAM_PROPER_ANTIALIASING = 1  # gs_camera.flags bit
-GS_BIN_SPANS, GS_BIN_RADIX, GS_BIN_LOCAL = 2, 4, 8  # binning path forced (gs_camera.flags, rect flags)
-BIN_FLAGS = {"auto": 0, "spans": GS_BIN_SPANS, "radix": GS_BIN_RADIX, "local": GS_BIN_LOCAL}
-GS_BIN_PATH_RADIX, GS_BIN_PATH_SPANS, GS_BIN_PATH_LOCAL = 0, 1, 2  # gs_bin_path
+GS_BIN_SPANS, GS_BIN_RADIX = 2, 4  # binning path forced (gs_camera.flags, rect flags)
+BIN_FLAGS = {"auto": 0, "spans": GS_BIN_SPANS, "radix": GS_BIN_RADIX}
+GS_BIN_PATH_RADIX, GS_BIN_PATH_SPANS = 0, 1  # gs_bin_path
 GS_ADAM_MAX_GROUPS = 8
 
 
@@ -77,6 +77,7 @@ _SIGS = {
     "gs_bin_prepare_workspace_size": (_sz, [_i64]),
     "gs_bin_prepare_3d": (_i32, [_vp, _vp, _vp, _i64, C.POINTER(GsCamera), _vp, _vp, _vp, _sz, _vp]),
     "gs_bin_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32]),
+    "gs_bin_fill_3d_workspace_size": (_sz, [_i64, _i64, C.POINTER(GsCamera)]),
     "gs_bin_path": (_i32, [_i64, C.POINTER(GsCamera)]),
     "gs_bin_fill_3d": (_i32, [_vp, _vp, _vp, _vp, _i64, C.POINTER(GsCamera), _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                               _sz, _vp]),

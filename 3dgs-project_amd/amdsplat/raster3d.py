@@ -29,7 +29,7 @@ BUCKET = 32
 REC_FLOATS = 16
 GRAD2D_FLOATS = 12
 # the tile binning of the views rasterize(...), rasterize_inference and pruning_scores build:
-# "auto", "spans", "radix" or "local" (forward_pass takes its Camera's own field)
+# "auto", "spans" or "radix" (forward_pass takes its Camera's own field)
 BINNING = "auto"
 
 
@@ -60,7 +60,7 @@ class Camera:
     near: float = 0.01
     far: float = 100.0
     proper_antialiasing: bool = False
-    binning: str = "auto"  # "auto", "spans", "radix" or "local": which tile binning the forward takes
+    binning: str = "auto"  # "auto", "spans" or "radix": which tile binning the forward takes
 
     @staticmethod
     def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0,
@@ -98,10 +98,8 @@ class ForwardState:
     sh_degree: int
     rec: torch.Tensor            # [n, 16] splat records
     touched: torch.Tensor        # [n] int32 tiles touched (0 = culled)
-    order: torch.Tensor  # [n] int32 Gaussians by depth (culled last); on the tile-local path the
-    #                      Gaussians with tiles in index order (entries past their count unused)
-    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets over `order` ([k] = m past the
-    #                               Gaussians with tiles); None on the span path
+    order: torch.Tensor          # [n] int32 Gaussians by depth (culled last)
+    offsets: torch.Tensor | None  # [n + 1] int32 instance offsets over `order`; None on the span path
     path: int  # the tile binning's path (GS_BIN_PATH_*)
     m: int                       # instances
     keys: torch.Tensor           # [m] int64 sorted keys (empty unless keep_keys)
@@ -244,8 +242,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         pre_done.record()
         side.wait_event(pre_done)
     # The tile binning's path: the radix path takes the depth order and the instance offsets in
-    # that order; the span binning the depth order alone; the tile-local depth order the
-    # Gaussians with tiles in index order and their offsets (no sort of the Gaussians).
+    # that order; the span binning the depth order alone.
     path = _lib.lib().gs_bin_path(n, ccam)
     order = torch.empty(n, dtype=torch.int32, device=dev)
     offsets = torch.empty(n + 1, dtype=torch.int32, device=dev) if path != _lib.GS_BIN_PATH_SPANS else None
@@ -289,8 +286,10 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
         if m >= 1 << 32:
             raise _lib.AmdSplatError(f"{m} tile instances exceed the 32-bit instance index")
     nb_max = (m + (BUCKET - 1) * T) // BUCKET if backward_state else 0  # >= sum over tiles of ceil(len / 32)
-    ws_bytes = max(_lib.size_call("gs_bin_workspace_size", n, m, cam.tiles_x, cam.tiles_y, ccam.flags), 1)
-    parts = {"point_list": 4 * m, "keys": 8 * m if keep_keys else 0, "ws": ws_bytes}
+    # the fill's scratch is its own allocation, released when this function returns: nothing the
+    # blends or the backward read lives in it (the caching allocator reuses it in stream order)
+    ws_fill = _u8(_lib.lib().gs_bin_fill_3d_workspace_size(n, m, ccam), dev)
+    parts = {"point_list": 4 * m, "keys": 8 * m if keep_keys else 0}
     if backward_state:
         parts.update(bucket_to_tile=4 * max(nb_max, 1), blist=4 * (4 + nb_max), ckpt=4096 * max(nb_max, 1))
     offs, total = _layout(parts)
@@ -301,7 +300,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     adr = {k: (base + o if parts[k] > 0 else None) for k, o in offs.items()}
     # the fill also clears the bucket list's header for the forward blend
     call("gs_bin_fill_3d", p_rec, p_dkeys, p_order, p_offsets, n, ccam, m, adr["keys"], adr["point_list"], p_ranges,
-         p_boff, adr.get("blist"), adr["ws"], ws_bytes, st)
+         p_boff, adr.get("blist"), ptr(ws_fill), ws_fill.numel(), st)
     tm.mark("binning")
     if _scores is None:
         call("gs_blend_fwd_3d", p_rec, p_ranges, adr["point_list"], p_boff, W, H, bg3, ptr(image), ptr(final_T),

@@ -215,139 +215,6 @@ static void scan_rec(const uint32_t* in, uint32_t* out, int64_t n, char* ws, hip
 }
 
 // ---------------------------------------------------------------------------------------
-// The Gaussians with tiles (counts[i] > 0) in index order and their instance offsets: for n
-// Gaussians of which v have tiles, order[k] = the k-th of them, offs[k] = the counts before
-// it (offs[k] = m for k in [v, n]). Two launches over 2048-entry blocks: the blocks' count
-// sums and visible counts, then each block takes the prefixes of the blocks before it (every
-// block reads all the block sums) and scans its own entries.
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void block_sum2(uint32_t& a, uint32_t& b, uint2* s_wave) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int off = 32; off > 0; off >>= 1) {
-    a += __shfl_xor(a, off, 64);
-    b += __shfl_xor(b, off, 64);
-  }
-  if (lane == 0) s_wave[wave] = make_uint2(a, b);
-  __syncthreads();
-  a = 0u;
-  b = 0u;
-#pragma unroll
-  for (int w = 0; w < kScanThreads / kWave; ++w) {
-    a += s_wave[w].x;
-    b += s_wave[w].y;
-  }
-  __syncthreads();
-}
-
-__global__ __launch_bounds__(kScanThreads) void vis_sum_kernel(const uint32_t* __restrict__ counts, int64_t n,
-                                                               uint32_t* __restrict__ sums, int64_t nb) {
-  __shared__ uint2 s_wave[kScanThreads / kWave];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-  uint32_t c[kScanItems];
-#pragma unroll
-  for (int e = 0; e < kScanItems; ++e) c[e] = counts[min(base + e * kScanThreads + threadIdx.x, n - 1)];
-  uint32_t sum = 0, vis = 0;
-#pragma unroll
-  for (int e = 0; e < kScanItems; ++e) {
-    const bool in = base + e * kScanThreads + threadIdx.x < n;
-    sum += in ? c[e] : 0u;
-    vis += (in && c[e] != 0u) ? 1u : 0u;
-  }
-  block_sum2(sum, vis, s_wave);
-  if (threadIdx.x == 0) {
-    sums[blockIdx.x] = sum;
-    sums[nb + blockIdx.x] = vis;
-  }
-}
-
-__global__ __launch_bounds__(kScanThreads) void vis_scan_kernel(const uint32_t* __restrict__ counts, int64_t n,
-                                                                const uint32_t* __restrict__ sums, int64_t nb,
-                                                                uint32_t* __restrict__ order,
-                                                                uint32_t* __restrict__ offs) {
-  __shared__ uint2 s_wave[kScanThreads / kWave];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-  // this thread's kScanItems consecutive entries
-  const int64_t i0 = base + static_cast<int64_t>(threadIdx.x) * kScanItems;
-  uint32_t c[kScanItems];
-#pragma unroll
-  for (int e = 0; e < kScanItems; ++e) c[e] = counts[min(i0 + e, n - 1)];
-  // the blocks before this one, and all of them
-  uint32_t sb = 0, vb = 0, st = 0, vt = 0;
-  for (int64_t b = threadIdx.x; b < nb; b += kScanThreads) {
-    const uint32_t s = sums[b], v = sums[nb + b];
-    st += s;
-    vt += v;
-    if (b < static_cast<int64_t>(blockIdx.x)) {
-      sb += s;
-      vb += v;
-    }
-  }
-  block_sum2(sb, vb, s_wave);
-  block_sum2(st, vt, s_wave);
-  const uint32_t m = st, n_vis = vt;
-  uint32_t sum = 0, vis = 0;
-#pragma unroll
-  for (int e = 0; e < kScanItems; ++e) {
-    const bool in = i0 + e < n;
-    c[e] = in ? c[e] : 0u;
-    sum += c[e];
-    vis += c[e] != 0u ? 1u : 0u;
-  }
-  // exclusive scans of both over the workgroup
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  uint32_t is = sum, iv = vis;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t us = __shfl_up(is, o, 64), uv = __shfl_up(iv, o, 64);
-    if (lane >= o) {
-      is += us;
-      iv += uv;
-    }
-  }
-  if (lane == kWave - 1) s_wave[wave] = make_uint2(is, iv);
-  __syncthreads();
-  uint32_t spos = sb + is - sum, vpos = vb + iv - vis;
-  for (int w = 0; w < wave; ++w) {
-    spos += s_wave[w].x;
-    vpos += s_wave[w].y;
-  }
-#pragma unroll
-  for (int e = 0; e < kScanItems; ++e) {
-    if (c[e] != 0u) {
-      order[vpos] = static_cast<uint32_t>(i0 + e);
-      offs[vpos] = spos;
-      ++vpos;
-      spos += c[e];
-    }
-  }
-  // the block's positions at or after the visible count (up to n) hold the total
-  for (int64_t p = base + threadIdx.x; p < base + kScanTile && p <= n; p += kScanThreads)
-    if (p >= static_cast<int64_t>(n_vis)) offs[p] = m;
-  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
-    // n itself lies past the last block's range when n is a multiple of the block size
-    if (n >= base + kScanTile) offs[n] = m;
-  }
-}
-
-// Gaussians up to which the visible list is two launches (every block reads all block sums)
-constexpr int64_t kLocalMaxGaussians = kScanTile * kScanDirectTiles;
-
-static size_t vis_ws(int64_t n) { return align_up(static_cast<size_t>(2 * ((n + kScanTile - 1) / kScanTile)) * 4); }
-
-// order / offsets of the Gaussians with tiles (n >= 1), as above.
-static void bin_visible(const uint32_t* counts, int64_t n, uint32_t* order, uint32_t* offs, char* ws,
-                        hipStream_t st) {
-  const int64_t nb = (n + kScanTile - 1) / kScanTile;
-  uint32_t* sums = reinterpret_cast<uint32_t*>(ws);
-  hipLaunchKernelGGL(vis_sum_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st, counts, n, sums,
-                     nb);
-  hipLaunchKernelGGL(vis_scan_kernel, dim3(static_cast<unsigned>(nb)), dim3(kScanThreads), 0, st, counts, n, sums,
-                     nb, order, offs);
-}
-
-// ---------------------------------------------------------------------------------------
 // Small kernels
 // ---------------------------------------------------------------------------------------
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
@@ -1726,15 +1593,27 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
       }
     }
     __syncthreads();
-    uint32_t sum = 0;
-#pragma unroll
-    for (int e = 0; e < kPerLane; ++e) sum += sp[e].y >> 16;
-    uint32_t total;
-    uint32_t run = wave_excl_scan(sum, lane, total);
+    // the wavefront's non-empty spans, compacted in order: span index c of s_span / s_pre is the
+    // c-th non-empty one, so the 64 consecutive instances of a window always lie in at most 64
+    // consecutive span indices (the rank bits below), whatever spans were empty
+    uint32_t sum = 0, nz = 0;
 #pragma unroll
     for (int e = 0; e < kPerLane; ++e) {
-      s_pre[kPerLane * lane + e] = run;
-      s_span[kPerLane * lane + e] = sp[e];
+      sum += sp[e].y >> 16;
+      nz += (sp[e].y >> 16) != 0u ? 1u : 0u;
+    }
+    uint32_t total, n_nz;
+    uint32_t run = wave_excl_scan(sum, lane, total);
+    uint32_t ci = wave_excl_scan(nz, lane, n_nz);
+    uint32_t cidx[kPerLane];
+#pragma unroll
+    for (int e = 0; e < kPerLane; ++e) {
+      cidx[e] = ci;
+      if ((sp[e].y >> 16) != 0u) {
+        s_pre[ci] = run;
+        s_span[ci] = sp[e];
+        ++ci;
+      }
       run += sp[e].y >> 16;
     }
     uint32_t carry = 0u;  // the span holding the last instance of the previous segment
@@ -1752,8 +1631,9 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
       wave_sync();
 #pragma unroll
       for (int e = 0; e < kPerLane; ++e) {
-        const uint32_t st = s_pre[kPerLane * lane + e];
-        if ((sp[e].y >> 16) != 0u && st >= t0 && st < t1) s_tbl[st - t0] = static_cast<uint8_t>(kPerLane * lane + e);
+        if ((sp[e].y >> 16) == 0u) continue;
+        const uint32_t st = s_pre[cidx[e]];
+        if (st >= t0 && st < t1) s_tbl[st - t0] = static_cast<uint8_t>(cidx[e]);
       }
       wave_sync();
       {
@@ -1803,7 +1683,7 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
             const uint2 e = s_span[own];
             col[r] = (e.y & 0xffffu) + (i - s_pre[own]);
             g[r] = e.x;
-            bit[r] = own - first;  // < 64: a window's 64 instances lie in at most 64 spans
+            bit[r] = own - first;  // < 64: 64 instances lie in at most 64 compacted spans
           }
         }
 #pragma unroll
@@ -1842,252 +1722,6 @@ __global__ __launch_bounds__(256) void span_col_write_kernel(
       }
     }
     __syncthreads();  // the column positions are rewritten for the next chunk
-  }
-}
-
-// ---------------------------------------------------------------------------------------
-// Tile-local depth order. With the instances emitted in Gaussian-index order and stably sorted
-// by tile, each tile's list holds its Gaussians in index order; a stable sort of every list by
-// depth key then gives the (tile, depth, index) order of the global path without sorting the N
-// Gaussians by depth first. LSD radix with 9-bit digits on each list: lists of up to kTsCap
-// entries in one workgroup's registers and LDS (tile_sort_small_kernel), longer ones by one
-// workgroup in 4096-entry chunks through global scratch (tile_sort_large_kernel). Keys are
-// ranked stably by wavefront ballots (match_bits), in position order.
-// ---------------------------------------------------------------------------------------
-constexpr int kTsBits = 9;
-constexpr int kTsRadix = 1 << kTsBits;
-constexpr int kTsWaves = 8;
-constexpr int kTsRounds = 8;
-constexpr int kTsCap = kTsWaves * kWave * kTsRounds;  // 4096 entries
-
-// Exclusive offsets of the digit counts s_cnt[W][kTsRadix] in digit-major, wavefront-minor
-// order, written back in place. Each of the workgroup's THREADS threads takes kTsRadix / THREADS
-// consecutive digits; returns with a barrier.
-template <int W, int THREADS>
-__device__ __forceinline__ void digit_offsets(uint32_t (*s_cnt)[kTsRadix], uint32_t* s_wsum) {
-  constexpr int DPT = kTsRadix / THREADS;
-  static_assert(DPT >= 1 && DPT * THREADS == kTsRadix, "digits per thread");
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int d0 = static_cast<int>(threadIdx.x) * DPT;
-  uint32_t sum = 0;
-#pragma unroll
-  for (int e = 0; e < DPT; ++e)
-#pragma unroll
-    for (int w = 0; w < W; ++w) sum += s_cnt[w][d0 + e];
-  uint32_t incl = sum;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t u = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += u;
-  }
-  if (lane == kWave - 1) s_wsum[wave] = incl;
-  __syncthreads();
-  uint32_t run = incl - sum;
-  for (int q = 0; q < wave; ++q) run += s_wsum[q];
-#pragma unroll
-  for (int e = 0; e < DPT; ++e) {
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const uint32_t c = s_cnt[w][d0 + e];
-      s_cnt[w][d0 + e] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-}
-
-// Lists of 2 .. kTsCap entries: keys in registers, one LDS copy per pass to redistribute them.
-// The list is cut into kTsWaves contiguous spans of c = 64 ceil(len / (64 kTsWaves)) positions,
-// one per wavefront (position p = c w + 64 r + lane for round r of wavefront w), so that every
-// wavefront ranks about len / kTsWaves entries: the ranking rounds are a serial chain per
-// wavefront.
-__global__ __launch_bounds__(kTsWaves * kWave) void tile_sort_small_kernel(const uint32_t* __restrict__ ranges,
-                                                                           const uint32_t* __restrict__ dkey,
-                                                                           uint32_t* __restrict__ point_list,
-                                                                           int passes) {
-  __shared__ uint32_t s_k[kTsCap];
-  __shared__ uint32_t s_v[kTsCap];
-  __shared__ uint32_t s_cnt[kTsWaves][kTsRadix];
-  __shared__ uint32_t s_wsum[kTsWaves];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const uint32_t r0 = ranges[2 * tile];
-  const int len = static_cast<int>(ranges[2 * tile + 1] - r0);
-  if (len <= 1 || len > kTsCap) return;  // the whole workgroup
-  const uint64_t lt = lanemask_lt(lane);
-  const int span = kWave * ((len + kWave * kTsWaves - 1) / (kWave * kTsWaves));
-  const int base = wave * span + lane;
-  // rounds of this wavefront holding entries (wave-uniform)
-  const int rounds = min(span / kWave, max(0, (len - wave * span + kWave - 1) / kWave));
-  // entry of round r of this lane (a position of this wavefront's span inside the list)
-  auto mine = [&](int r) { return r < rounds && base + kWave * r < len; };
-  uint32_t key[kTsRounds], val[kTsRounds], rank[kTsRounds];
-  // loads at clamped positions, without branches: every one in flight at once
-#pragma unroll
-  for (int r = 0; r < kTsRounds; ++r) val[r] = point_list[r0 + min(base + kWave * r, len - 1)];
-#pragma unroll
-  for (int r = 0; r < kTsRounds; ++r) key[r] = dkey[val[r]];
-  for (int pass = 0; pass < passes; ++pass) {
-    const int shift = kTsBits * pass;
-    for (int q = threadIdx.x; q < kTsWaves * kTsRadix; q += kTsWaves * kWave) (&s_cnt[0][0])[q] = 0u;
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kTsRounds; ++r) {
-      if (r >= rounds) break;  // wave-uniform
-      const bool valid = mine(r);
-      const uint32_t d = (key[r] >> shift) & (kTsRadix - 1);
-      const uint64_t peers = match_bits<kTsBits>(d, valid);
-      rank[r] = valid ? s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt)) : 0u;
-      wave_sync();
-      if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
-      wave_sync();
-    }
-    __syncthreads();
-    digit_offsets<kTsWaves, kTsWaves * kWave>(s_cnt, s_wsum);
-#pragma unroll
-    for (int r = 0; r < kTsRounds; ++r) {
-      if (mine(r)) {
-        const uint32_t pos = s_cnt[wave][(key[r] >> shift) & (kTsRadix - 1)] + rank[r];
-        s_k[pos] = key[r];
-        s_v[pos] = val[r];
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kTsRounds; ++r) {
-      if (mine(r)) {
-        key[r] = s_k[base + kWave * r];
-        val[r] = s_v[base + kWave * r];
-      }
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int r = 0; r < kTsRounds; ++r)
-    if (mine(r)) point_list[r0 + base + kWave * r] = val[r];
-}
-
-// Lists longer than kTsCap: one workgroup of kTlWaves wavefronts per list, each pass a digit
-// histogram over the whole list, then the list in chunks of kTlChunk entries, in order, each
-// chunk ranked stably and scattered to running digit positions; passes go point_list -> (k1,
-// v1) -> (k2, v2) -> (k1, v1) ..., the last one's values into point_list (each list in the
-// scratch arrays at its own range [r0, r1)).
-constexpr int kTlWaves = 16;
-constexpr int kTlRounds = 4;
-constexpr int kTlChunk = kTlWaves * kWave * kTlRounds;  // 4096
-
-__global__ __launch_bounds__(kTlWaves * kWave) void tile_sort_large_kernel(
-    const uint32_t* __restrict__ ranges, const uint32_t* __restrict__ dkey, uint32_t* __restrict__ point_list,
-    uint32_t* __restrict__ k1, uint32_t* __restrict__ v1, uint32_t* __restrict__ k2, uint32_t* __restrict__ v2,
-    int passes) {
-  __shared__ uint32_t s_base[kTsRadix];
-  __shared__ uint32_t s_cnt[kTlWaves][kTsRadix];
-  __shared__ uint32_t s_wsum[kTlWaves];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const uint32_t r0 = ranges[2 * tile];
-  const int len = static_cast<int>(ranges[2 * tile + 1] - r0);
-  if (len <= kTsCap) return;  // the whole workgroup: the small kernel's lists
-  const uint64_t lt = lanemask_lt(lane);
-  for (int pass = 0; pass < passes; ++pass) {
-    const int shift = kTsBits * pass;
-    const bool last = pass == passes - 1;
-    const uint32_t* src_k = pass == 0 ? nullptr : (pass & 1) ? k1 : k2;  // pass 0 gathers its keys
-    const uint32_t* src_v = pass == 0 ? point_list : (pass & 1) ? v1 : v2;
-    uint32_t* dst_k = last ? nullptr : (pass & 1) ? k2 : k1;
-    uint32_t* dst_v = last ? point_list : (pass & 1) ? v2 : v1;
-    // digit histogram of the whole list
-    for (int q = threadIdx.x; q < kTsRadix; q += kTlWaves * kWave) s_base[q] = 0u;
-    __syncthreads();
-    // (kTlRounds entries a thread at a time, loaded at clamped positions before any is counted)
-    for (int p0 = threadIdx.x; p0 < len; p0 += kTlRounds * kTlWaves * kWave) {
-      uint32_t k[kTlRounds];
-      if (src_k) {
-#pragma unroll
-        for (int e = 0; e < kTlRounds; ++e) k[e] = src_k[r0 + min(p0 + e * kTlWaves * kWave, len - 1)];
-      } else {
-        uint32_t v[kTlRounds];
-#pragma unroll
-        for (int e = 0; e < kTlRounds; ++e) v[e] = src_v[r0 + min(p0 + e * kTlWaves * kWave, len - 1)];
-#pragma unroll
-        for (int e = 0; e < kTlRounds; ++e) k[e] = dkey[v[e]];
-      }
-#pragma unroll
-      for (int e = 0; e < kTlRounds; ++e)
-        if (p0 + e * kTlWaves * kWave < len) atomicAdd(&s_base[(k[e] >> shift) & (kTsRadix - 1)], 1u);
-    }
-    __syncthreads();
-    if (threadIdx.x < kWave) {  // exclusive scan of the 512 digit counts by one wavefront
-      constexpr int PER = kTsRadix / kWave;
-      uint32_t c[PER], sum = 0;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        c[e] = s_base[PER * lane + e];
-        sum += c[e];
-      }
-      uint32_t tot;
-      uint32_t run = wave_excl_scan(sum, lane, tot);
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        s_base[PER * lane + e] = run;
-        run += c[e];
-      }
-    }
-    __syncthreads();
-    // the list in chunks, in order
-    for (int c0 = 0; c0 < len; c0 += kTlChunk) {
-      const int cb = c0 + wave * (kWave * kTlRounds) + lane;
-      uint32_t key[kTlRounds], val[kTlRounds], rank[kTlRounds];
-      // loads at clamped positions, without branches
-#pragma unroll
-      for (int r = 0; r < kTlRounds; ++r) val[r] = src_v[r0 + min(cb + kWave * r, len - 1)];
-      if (src_k) {
-#pragma unroll
-        for (int r = 0; r < kTlRounds; ++r) key[r] = src_k[r0 + min(cb + kWave * r, len - 1)];
-      } else {
-#pragma unroll
-        for (int r = 0; r < kTlRounds; ++r) key[r] = dkey[val[r]];
-      }
-      for (int q = threadIdx.x; q < kTlWaves * kTsRadix; q += kTlWaves * kWave) (&s_cnt[0][0])[q] = 0u;
-      __syncthreads();
-#pragma unroll
-      for (int r = 0; r < kTlRounds; ++r) {
-        const bool valid = cb + kWave * r < len;
-        const uint32_t d = (key[r] >> shift) & (kTsRadix - 1);
-        const uint64_t peers = match_bits<kTsBits>(d, valid);
-        rank[r] = valid ? s_cnt[wave][d] + static_cast<uint32_t>(__popcll(peers & lt)) : 0u;
-        wave_sync();
-        if (valid && (peers & lt) == 0ull) s_cnt[wave][d] += static_cast<uint32_t>(__popcll(peers));
-        wave_sync();
-      }
-      __syncthreads();
-      // chunk offsets per (wavefront, digit) from the running digit positions, which then advance
-      // by the chunk's counts
-      if (threadIdx.x < kTsRadix) {
-        const int d = threadIdx.x;
-        uint32_t run = s_base[d];
-#pragma unroll
-        for (int w = 0; w < kTlWaves; ++w) {
-          const uint32_t c = s_cnt[w][d];
-          s_cnt[w][d] = run;
-          run += c;
-        }
-        s_base[d] = run;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int r = 0; r < kTlRounds; ++r) {
-        if (cb + kWave * r < len) {
-          const uint32_t pos = s_cnt[wave][(key[r] >> shift) & (kTsRadix - 1)] + rank[r];
-          if (dst_k) dst_k[r0 + pos] = key[r];
-          dst_v[r0 + pos] = val[r];
-        }
-      }
-      __syncthreads();  // the chunk offsets are rewritten by the next chunk
-    }
   }
 }
 
@@ -2158,18 +1792,14 @@ static bool span_binning(int tiles_x, int tiles_y) { return tiles_x <= kSpanMaxD
 constexpr int64_t kSpanMinGaussians = 2000000;
 
 static bool use_spans(int64_t n, int tiles_x, int tiles_y, int flags) {
-  if (!span_binning(tiles_x, tiles_y) || (flags & (GS_BIN_RADIX | GS_BIN_LOCAL))) return false;
+  if (!span_binning(tiles_x, tiles_y) || (flags & GS_BIN_RADIX)) return false;
   return (flags & GS_BIN_SPANS) || n >= kSpanMinGaussians;
 }
 
-// The 3D fill's path: the span binning as above; below it the instances are emitted and sorted
-// by tile, in depth order after the global depth sort (GS_BIN_PATH_RADIX, the default) or in
-// index order with each tile's list then sorted by depth (GS_BIN_PATH_LOCAL: no sort of the N
-// Gaussians).
+// The 3D fill's path: the span binning as above; below it the instances are emitted in depth
+// order and stably sorted by tile (GS_BIN_PATH_RADIX).
 static int bin_path(int64_t n, int tiles_x, int tiles_y, int flags) {
-  if (use_spans(n, tiles_x, tiles_y, flags)) return GS_BIN_PATH_SPANS;
-  if ((flags & GS_BIN_LOCAL) && n <= kLocalMaxGaussians) return GS_BIN_PATH_LOCAL;
-  return GS_BIN_PATH_RADIX;
+  return use_spans(n, tiles_x, tiles_y, flags) ? GS_BIN_PATH_SPANS : GS_BIN_PATH_RADIX;
 }
 
 // m instances fit the span path's 32-bit span positions (m plus every row's padding)
@@ -2202,15 +1832,10 @@ static SpanLayout span_layout(int64_t n, int64_t m, int tiles_x, int tiles_y) {
   return L;
 }
 
-// Workspace of the fill for n Gaussians and m instances: the span binning's; the emission's,
-// followed on the tile-local path by the long-list sort's scratch (two key and two value
-// arrays of m).
-static size_t fill_ws(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags, bool rects = false) {
-  const int path = rects ? (use_spans(n, tiles_x, tiles_y, flags) ? GS_BIN_PATH_SPANS : GS_BIN_PATH_RADIX)
-                         : bin_path(n, tiles_x, tiles_y, flags);
-  if (path == GS_BIN_PATH_SPANS) return span_layout(n, m, tiles_x, tiles_y).end;
-  const size_t e = emit_layout(m, tiles_x * tiles_y).end;
-  return path == GS_BIN_PATH_LOCAL ? e + 4 * align_up(static_cast<size_t>(m) * 4) : e;
+// Workspace of the fill for n Gaussians and m instances: the span binning's or the emission's.
+static size_t fill_ws(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags) {
+  if (bin_path(n, tiles_x, tiles_y, flags) == GS_BIN_PATH_SPANS) return span_layout(n, m, tiles_x, tiles_y).end;
+  return emit_layout(m, tiles_x * tiles_y).end;
 }
 
 // Rectangle binning: the depth ordering, the order and offsets, then the fill.
@@ -2224,12 +1849,12 @@ static RectLayout rect_layout(int64_t n, int64_t m, int tiles_x, int tiles_y, in
   L.prep = o; o += prep_layout(n).end;
   L.order = o; o += align_up(n * 4);
   L.offs = o; o += align_up((n + 1) * 4);
-  L.emit = o; o += fill_ws(n, m, tiles_x, tiles_y, flags, true);
+  L.emit = o; o += fill_ws(n, m, tiles_x, tiles_y, flags);
   L.end = o;
   return L;
 }
 
-static size_t prep_ws(int64_t n) { return std::max(prep_layout(n).end, vis_ws(n)); }
+static size_t prep_ws(int64_t n) { return prep_layout(n).end; }
 
 // Stable order of the Gaussians by depth key (keys_in: precomputed 32-bit keys, else computed
 // from rec / depth / depth64; none of them: index order) and, if offsets is not NULL, the
@@ -2285,7 +1910,7 @@ template <typename K>
 static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
                           const uint32_t* order, const uint32_t* offsets, int64_t n, int tiles_x, int n_tiles,
                           int64_t m, int tile_bits, uint64_t* sorted_keys, uint32_t* point_list, uint32_t* preset,
-                          const EmitLayout& L, char* ws, hipStream_t st, bool defer_keys) {
+                          const EmitLayout& L, char* ws, hipStream_t st) {
   K* tkeys = reinterpret_cast<K*>(ws + L.tkeys);
   uint32_t* tvals = reinterpret_cast<uint32_t*>(ws + L.tvals);
   K* tsorted = reinterpret_cast<K*>(ws + L.tsorted);
@@ -2300,7 +1925,7 @@ static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t
   }
   radix_sort(tkeys, tvals, tsorted, point_list, m, tile_bits, ws + L.sort, st, nullptr, nullptr, preset,
              preset != nullptr && !sorted_keys);
-  if (sorted_keys && !defer_keys)
+  if (sorted_keys)
     hipLaunchKernelGGL((full_keys_kernel<K>), dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list, dkey_of,
                        dkey0, m, sorted_keys);
 }
@@ -2362,15 +1987,12 @@ static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dk
 #undef GS_SPAN_WRITE
 }
 
-static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0, int dkey_bits,
+static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
                      const uint32_t* order,
                      const uint32_t* offsets, int64_t n, int tiles_x, int tiles_y, int64_t m,
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
                      uint32_t* bucket_offsets, uint32_t* list_header, int flags, char* ws, hipStream_t st) {
   const int n_tiles = tiles_x * tiles_y;
-  // the tile-local depth order (3D only): instances emitted in index order, each tile's list
-  // sorted by depth after the tile sort
-  const bool local = !rects && bin_path(n, tiles_x, tiles_y, flags) == GS_BIN_PATH_LOCAL;
   if (m > 0 && use_spans(n, tiles_x, tiles_y, flags)) {
     // (gs_bin_fill_* reject an m beyond span_fits for this path)
     if (rects)
@@ -2395,40 +2017,15 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
     const bool short_keys = sort_ranges && n_tiles <= 65536;
     if (short_keys)
       emit_and_sort<uint16_t>(rec, rects, dkey_of, dkey0, order, offsets, n, tiles_x, n_tiles, m, tile_bits,
-                              sorted_keys, point_list, preset, L, ws, st, local);
+                              sorted_keys, point_list, preset, L, ws, st);
     else
       emit_and_sort<uint32_t>(rec, rects, dkey_of, dkey0, order, offsets, n, tiles_x, n_tiles, m, tile_bits,
-                              sorted_keys, point_list, preset, L, ws, st, local);
+                              sorted_keys, point_list, preset, L, ws, st);
     if (!sort_ranges)
       hipLaunchKernelGGL(tile_bounds_kernel, dim3(grid_for((m + kBoundsPer - 1) / kBoundsPer, 256)), dim3(256), 0,
                          st, reinterpret_cast<const uint32_t*>(ws + L.tsorted), m, n_tiles, ranges);
     hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
                        tile_offsets, list_header, sort_ranges);
-    if (local) {
-      // each tile's list (index order) sorted by depth key: short lists in LDS, long ones through
-      // the scratch after the emission's workspace
-      const int passes = (dkey_bits + kTsBits - 1) / kTsBits;
-      if (passes > 0) {
-        uint32_t* scr = reinterpret_cast<uint32_t*>(ws + L.end);
-        const size_t mw = align_up(static_cast<size_t>(m) * 4) / 4;
-        hipLaunchKernelGGL(tile_sort_small_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kTsWaves * kWave), 0,
-                           st, ranges, dkey_of, point_list, passes);
-        // (at least two passes there: a single one would read and write the point list at once)
-        hipLaunchKernelGGL(tile_sort_large_kernel, dim3(static_cast<unsigned>(n_tiles)), dim3(kTlWaves * kWave), 0,
-                           st, ranges, dkey_of, point_list, scr, scr + mw, scr + 2 * mw, scr + 3 * mw,
-                           passes > 1 ? passes : 2);
-      }
-      if (sorted_keys) {
-        if (short_keys)
-          hipLaunchKernelGGL((full_keys_kernel<uint16_t>), dim3(grid_for(m, 256)), dim3(256), 0, st,
-                             reinterpret_cast<const uint16_t*>(ws + L.tsorted), point_list, dkey_of, dkey0, m,
-                             sorted_keys);
-        else
-          hipLaunchKernelGGL((full_keys_kernel<uint32_t>), dim3(grid_for(m, 256)), dim3(256), 0, st,
-                             reinterpret_cast<const uint32_t*>(ws + L.tsorted), point_list, dkey_of, dkey0, m,
-                             sorted_keys);
-      }
-    }
     return;
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
@@ -2474,27 +2071,12 @@ extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_t
   clear_error();
   if (int e = check_cam(cam)) return e;
   GS_REQUIRE(n >= 0 && n < (int64_t(1) << 32), GS_ERR_ARG, "invalid bin_prepare arguments");
-  const CamK k = make_cam(*cam);
-  const bool local = bin_path(n, k.tiles_x, k.tiles_y, cam->flags) == GS_BIN_PATH_LOCAL;
-  if (local) {
-    GS_REQUIRE(offsets && (n == 0 || (order && tiles_touched)), GS_ERR_ARG,
-               "the tile-local path needs the counts, the order and the offsets");
-  } else {
-    GS_REQUIRE(n == 0 || (order && (depth_keys || splat_rec) && (tiles_touched || (!offsets && depth_keys))),
-               GS_ERR_ARG, "null pointer argument");
-  }
+  GS_REQUIRE(n == 0 || (order && (depth_keys || splat_rec) && (tiles_touched || (!offsets && depth_keys))),
+             GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
   const size_t need = prep_ws(n);
   GS_REQUIRE(workspace_bytes >= need && workspace, GS_ERR_WORKSPACE,
              "bin_prepare workspace too small: need %zu bytes", need);
-  if (local) {
-    // the Gaussians with tiles in index order and their instance offsets
-    if (n == 0)
-      hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, as_stream(stream), offsets, int64_t(1), 0u);
-    else
-      bin_visible(tiles_touched, n, order, offsets, static_cast<char*>(workspace), as_stream(stream));
-    return check_launch("bin_prepare_3d");
-  }
   bin_prepare(depth_keys ? nullptr : reinterpret_cast<const SplatRec*>(splat_rec), nullptr, nullptr, depth_keys,
               depth_key_bits(make_cam(*cam)), tiles_touched, n, order, offsets, static_cast<char*>(workspace),
               as_stream(stream));
@@ -2509,6 +2091,12 @@ extern "C" size_t gs_bin_workspace_size(int64_t n, int64_t m, int tiles_x, int t
   // the rectangle binning runs the depth ordering itself: its scratch, order and offsets too;
   // the 3D fill needs its own path's workspace
   return std::max(rect_layout(n, m, tiles_x, tiles_y, flags).end, fill_ws(n, m, tiles_x, tiles_y, flags));
+}
+
+extern "C" size_t gs_bin_fill_3d_workspace_size(int64_t n, int64_t m, const gs_camera* cam) {
+  if (!cam || cam->width <= 0 || cam->height <= 0) return 0;
+  const CamK k = make_cam(*cam);
+  return fill_ws(n < 0 ? 0 : n, m < 0 ? 0 : m, k.tiles_x, k.tiles_y, cam->flags);
 }
 
 extern "C" int gs_bin_path(int64_t n, const gs_camera* cam) {
@@ -2538,11 +2126,9 @@ extern "C" int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys
   GS_REQUIRE(m == 0 || (splat_rec && point_list), GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(m == 0 || order, GS_ERR_ARG, "the fill needs the order of gs_bin_prepare_3d");
   GS_REQUIRE(m == 0 || offsets || path == GS_BIN_PATH_SPANS, GS_ERR_ARG, "this fill emits instances: it needs the offsets");
-  GS_REQUIRE(m == 0 || depth_keys || path != GS_BIN_PATH_LOCAL, GS_ERR_ARG,
-             "the tile-local depth order needs the depth keys");
   GS_REQUIRE(!(sorted_keys && m > 0 && !depth_keys), GS_ERR_ARG, "sorted_keys need depth_keys");
   GS_REQUIRE(aligned(splat_rec, 16), GS_ERR_ALIGN, "splat_rec must be 16-byte aligned");
-  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, depth_key_bits(k), order,
+  bin_emit(reinterpret_cast<const SplatRec*>(splat_rec), nullptr, depth_keys, k.dkey0, order,
            offsets, n, k.tiles_x,
            k.tiles_y, m, sorted_keys, point_list, ranges, nullptr, bucket_offsets, bucket_list, cam->flags,
            static_cast<char*>(workspace), as_stream(stream));
@@ -2598,7 +2184,7 @@ extern "C" int gs_bin_fill_rect(const int32_t* rects, const void* depth, int dep
     if (sorted_keys && m > 0 && !d32)  // index order: the depth part of the keys is 0
       hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, dkeys, n, 0u);
   }
-  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, 32, ord, offs, n, tiles_x, tiles_y, m, sorted_keys,
+  bin_emit(nullptr, reinterpret_cast<const int4*>(rects), dkeys, 0u, ord, offs, n, tiles_x, tiles_y, m, sorted_keys,
            point_list, ranges, tile_offsets, bucket_offsets, nullptr, flags, ws + L.emit, st);
   return check_launch("bin_fill_rect");
 }

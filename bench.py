@@ -75,7 +75,7 @@ def parse():
     ap.add_argument("--no-train-step", action="store_true", help="skip the training-step measurement")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the inference / pruning-score / antialiasing variants (profiling runs)")
-    ap.add_argument("--binning", default="auto", choices=["auto", "radix", "spans", "local"],
+    ap.add_argument("--binning", default="auto", choices=["auto", "radix", "spans"],
                     help="the tile binning of the 3D workloads (auto: the library's choice for the size)")
     ap.add_argument("--json-out", default=None)
     return ap.parse_args()
@@ -145,22 +145,13 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
                 atomics_per_pair=9, spans=None):
     """Algorithmic (compulsory) HBM bytes per stage for the measured counts: each datum read or
     written once (fp32). spans: the row-span count when the forward took the span binning (its
-    instance offsets are None), else None. The path is the forward's: no depth order for the
-    tile-local one, no offsets for the span binning."""
-    from amdsplat import _lib
-
+    instance offsets are None), else None. The path is the forward's: no offsets for the span
+    binning."""
     n, m, K = fs.n, fs.m, fs.sh_coeffs
     T = fs.cam.n_tiles
     P = fs.cam.width * fs.cam.height
     B = int(fs.bucket_offsets[-1].item())
-    if fs.path == _lib.GS_BIN_PATH_LOCAL:
-        # the Gaussians with tiles and their offsets: counts read (twice), list and offsets written
-        depth = 8 * n + 8 * n_visible
-        # emission (order, offset and 48 B of the record per Gaussian with tiles, key+value per
-        # instance), tile sort passes 1 and 2 as on the radix path, ranges and bucket offsets per
-        # tile; the per-tile depth sort: list entry read, its depth key gathered, entry written
-        binning = 56 * n_visible + 8 * m + 20 * m + 16 * m + 12 * m + 20 * T + 4 * B
-    elif spans is None:
+    if spans is None:
         # 3 radix passes over N (histogram read 4 B, key+value read and write 16 B), the counts
         # gathered into depth order (read + write), the scan (counts read, offsets written)
         depth = 3 * 20 * n + 8 * n + 8 * n
@@ -510,7 +501,7 @@ def bench_3d(args, ceilings) -> dict:
         up = int(ctr[0].item()) // 9
         ev = int(ctr[2].item())
         spans = span_count(fs) if fs.path == _lib.GS_BIN_PATH_SPANS else None
-        paths.add({_lib.GS_BIN_PATH_LOCAL: "local", _lib.GS_BIN_PATH_SPANS: "spans"}.get(fs.path, "radix"))
+        paths.add("spans" if fs.path == _lib.GS_BIN_PATH_SPANS else "radix")
         per_pose.append({"visible": nv, "instances": fs.m, "buckets": int(fs.bucket_offsets[-1].item()),
                          "active_buckets": ab, "bucket_splat_steps": ss, "staged_entries": stg,
                          "ckpt_written": ckw, "reduced_bucket_splats": up, "bwd_pair_evals": ev,

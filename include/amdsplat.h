@@ -64,15 +64,13 @@ typedef struct gs_camera {
 /* Binning path (gs_camera.flags for the 3D entry points, the flags argument of
  * gs_bin_fill_rect): by default the span binning is taken from GS_BIN_SPAN_MIN_GAUSSIANS
  * Gaussians on canvases of at most GS_BIN_SPAN_MAX_TILES tiles per side, otherwise the radix
- * path; these bits force one of them or the tile-local depth order
- * (GS_BIN_SPANS only where the canvas allows it; GS_BIN_LOCAL is 3D only). All give the same
- * lists, ranges and bucket offsets. */
+ * path; these bits force one of them (GS_BIN_SPANS only where the canvas allows it). Both give
+ * the same lists, ranges and bucket offsets. */
 #define GS_BIN_SPANS 2
 #define GS_BIN_RADIX 4
-#define GS_BIN_LOCAL 8
 #define GS_BIN_SPAN_MIN_GAUSSIANS 2000000
 /* gs_bin_path values: the 3D fill's path for a camera and Gaussian count */
-enum { GS_BIN_PATH_RADIX = 0, GS_BIN_PATH_SPANS = 1, GS_BIN_PATH_LOCAL = 2 };
+enum { GS_BIN_PATH_RADIX = 0, GS_BIN_PATH_SPANS = 1 };
 
 /* Thread-local message of the last failed call. */
 const char* gs_last_error(void);
@@ -129,12 +127,9 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  * visible in results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:10-31).
  * Produces the stable order of instances by (tile, depth, Gaussian index) -- the order of a
  * stable sort of 64-bit keys (tile << 32 | orderable depth bits) over instances emitted in
- * Gaussian-index order, by one of three paths (gs_bin_path):
+ * Gaussian-index order, by one of two paths (gs_bin_path):
  *   GS_BIN_PATH_RADIX (default below GS_BIN_SPAN_MIN_GAUSSIANS): a stable radix sort of the
  *     Gaussians by depth, then the instances emitted in that order and stably radix-sorted by tile;
- *   GS_BIN_PATH_LOCAL (opt-in, at most 2048 * 4096 Gaussians): the Gaussians with tiles listed
- *     in index order, their instances emitted in that order and stably radix-sorted by tile, then
- *     each tile's list stably sorted by depth key;
  *   GS_BIN_PATH_SPANS: the depth sort, then two counting passes over the Gaussians' row spans
  *     (the run of tiles a Gaussian touches in one tile row): by tile row over the Gaussians in
  *     depth order, then by column within each row, which writes every instance once.
@@ -151,10 +146,6 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *                         radix path) exclusive scan of tiles_touched[order[j]]; offsets[n] = m,
  *                         the number of instances
  *   tiles_touched may be NULL when offsets is NULL and depth_keys is given.
- *   On the tile-local path (gs_bin_path): order [n] = the Gaussians with tiles_touched > 0 in
- *   index order (entries past their count v unspecified), offsets [n + 1] = the exclusive scan of
- *   their counts, offsets[k] = m for k in [v, n]; tiles_touched, order and offsets are required,
- *   depth_keys and splat_rec are not read.
  *   Workspace from gs_bin_prepare_workspace_size(n).
  * gs_bin_fill_3d: tile lists, ranges, bucket offsets. splat_rec as gs_preprocess_fwd wrote it
  *   (a culled Gaussian's record holds the empty bounds (0, -1, 0, -1)); m = the sum of the
@@ -167,8 +158,10 @@ int gs_preprocess_fwd(const float* means, const float* log_scales, const float* 
  *   bucket_list (may be NULL): the list gs_blend_fwd_3d appends to; its header is cleared
  *                         here, so that call can take GS_BLEND_LIST_CLEARED
  *   order, offsets: as gs_bin_prepare_3d wrote them for the same path (offsets NULL on the span
- *   path); the local path also needs depth_keys.
- *   Workspace from gs_bin_workspace_size(n, m, tiles_x, tiles_y, cam->flags).
+ *   path).
+ *   Workspace from gs_bin_fill_3d_workspace_size(n, m, cam): this fill's own path only (the
+ *   larger gs_bin_workspace_size(n, m, tiles_x, tiles_y, cam->flags) also covers it). The
+ *   workspace holds nothing the blends read: it can be released once the fill has run.
  * ------------------------------------------------------------------------------------- */
 #define GS_BIN_SPAN_MAX_TILES 512
 size_t gs_bin_prepare_workspace_size(int64_t n);
@@ -176,6 +169,7 @@ int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched, con
                       int64_t n, const gs_camera* cam, uint32_t* order, uint32_t* offsets,
                       void* workspace, size_t workspace_bytes, void* stream);
 size_t gs_bin_workspace_size(int64_t n, int64_t m, int tiles_x, int tiles_y, int flags);
+size_t gs_bin_fill_3d_workspace_size(int64_t n, int64_t m, const gs_camera* cam);
 int gs_bin_path(int64_t n, const gs_camera* cam); /* GS_BIN_PATH_* the fill takes for n Gaussians */
 int gs_bin_fill_3d(const float* splat_rec, const uint32_t* depth_keys, const uint32_t* order,
                    const uint32_t* offsets, int64_t n, const gs_camera* cam, int64_t m,

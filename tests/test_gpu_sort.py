@@ -57,34 +57,6 @@ def test_depth_order_offsets_beyond_31_bits(n):
     check_depth_order(n, "distinct", (1 << 32) // n - 1)
 
 
-# the visible list of the tile-local path: blocks of 2048 entries (one partial, exact multiples,
-# one entry more), none visible, all visible, and the largest size the path takes
-@pytest.mark.parametrize("n,frac", [(1, 0.0), (1, 1.0), (2047, 0.7), (2048, 0.7), (2049, 0.7), (100_003, 0.0),
-                                    (100_003, 1.0), (1_000_000, 0.66), (8_388_608, 0.5)])
-def test_visible_list_and_offsets(n, frac):
-    """gs_bin_prepare_3d on the tile-local path: the Gaussians with tiles in index order and the
-    exclusive scan of their counts, every offset from the visible count up to n holding m."""
-    rng = np.random.default_rng(n + int(100 * frac))
-    counts = (rng.integers(1, 60, n) * (rng.random(n) < frac)).astype(np.uint32)
-    dev = torch.device("cuda")
-    cd = torch.from_numpy(counts.view(np.int32)).to(dev)
-    order = torch.full((n,), -1, dtype=torch.int32, device=dev)
-    offsets = torch.full((n + 1,), -1, dtype=torch.int32, device=dev)
-    ws = torch.empty(max(_lib.size_call("gs_bin_prepare_workspace_size", n), 1), dtype=torch.uint8, device=dev)
-    cam = _lib.make_camera(np.eye(4, dtype=np.float32), 500.0, 500.0, 320, 240, 640, 480, NEAR, FAR,
-                           flags=_lib.GS_BIN_LOCAL)
-    assert _lib.lib().gs_bin_path(n, cam) == _lib.GS_BIN_PATH_LOCAL
-    call("gs_bin_prepare_3d", None, ptr(cd), None, n, cam, ptr(order), ptr(offsets), ptr(ws), ws.numel(),
-         _lib.stream_handle(dev))
-    vis = np.nonzero(counts)[0]
-    v = len(vis)
-    assert np.array_equal(order.cpu().numpy()[:v], vis)
-    want = np.zeros(n + 1, np.int64)
-    want[1:v + 1] = np.cumsum(counts[vis].astype(np.int64))
-    want[v + 1:] = want[v]
-    assert np.array_equal(offsets.cpu().numpy().view(np.uint32).astype(np.int64), want)
-
-
 # near / far planes whose depth keys take 1 and 2 passes of 9 bits (and 3 for the default)
 @pytest.mark.parametrize("far", [1.0 + 400 * 2.0 ** -23, 1.03, 60.0])
 @pytest.mark.parametrize("n", [1025, 1_000_000])

@@ -65,8 +65,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_binning_path_choice():
     """gs_bin_path (host only): the radix path by default, the span binning from 2M Gaussians
-    on canvases of at most 512 tiles a side, each forced by its flag where it applies; the
-    tile-local order up to 2048 * 4096 Gaussians."""
+    on canvases of at most 512 tiles a side, each forced by its flag where it applies."""
     from amdsplat import _lib
 
     def path(n, flags=0, W=640, H=480):
@@ -79,9 +78,6 @@ def test_binning_path_choice():
     assert path(2_000_000, W=16 * 513) == _lib.GS_BIN_PATH_RADIX
     assert path(1000, _lib.GS_BIN_SPANS) == _lib.GS_BIN_PATH_SPANS
     assert path(3_000_000, _lib.GS_BIN_RADIX) == _lib.GS_BIN_PATH_RADIX
-    assert path(3_000_000, _lib.GS_BIN_LOCAL) == _lib.GS_BIN_PATH_LOCAL
-    assert path(8_388_608, _lib.GS_BIN_LOCAL) == _lib.GS_BIN_PATH_LOCAL
-    assert path(8_388_609, _lib.GS_BIN_LOCAL) == _lib.GS_BIN_PATH_RADIX
 
 
 # ---------------------------------------------------------------------------------------

@@ -73,9 +73,16 @@ def test_no_alloc_refuses_images_beyond_its_buffer():
     max_tiles = 131072
     # 3 channels x 256 x 256 tiles of 16 px = 196608 tile-channels: refused on the host
     h = w = 256 * 16
-    small = torch.zeros(16, device="cuda")  # never read: the size check fails before any launch
-    rc = L.gs_l1_ssim_fwd_noalloc(ptr(small), ptr(small), 3, h, w, ctypes.c_float(0.2), None, ptr(small), None)
+    # real buffers of the full size (about 200 MB each): should the size check ever regress, the
+    # call reads and writes inside them and the assertions below fail, instead of a fault
+    img = torch.zeros(3, h, w, device="cuda")
+    tgt = torch.zeros(3, h, w, device="cuda")
+    loss = torch.zeros(3, device="cuda")
+    rc = L.gs_l1_ssim_fwd_noalloc(ptr(img), ptr(tgt), 3, h, w, ctypes.c_float(0.2), None, ptr(loss), None)
+    torch.cuda.synchronize()
+    del img, tgt
     assert rc == 1  # GS_ERR_ARG
+    assert torch.equal(loss, torch.zeros(3, device="cuda"))  # nothing was launched
     assert b"static" in L.gs_last_error()
     assert 3 * (h // 16) * (w // 16) > max_tiles
     # the next call succeeds (no pending error is left behind)
