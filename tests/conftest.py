@@ -33,3 +33,19 @@ def pytest_runtest_setup(item):
     # name the case before it runs, so a GPU failure can be attributed from partial output
     if "gpu" in item.keywords and os.environ.get("AMDSPLAT_TRACE_TESTS", "1") == "1":
         print(f"\n[gpu-test] {item.nodeid}", flush=True)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The numbers parity tests record with record_property("parity", line) (per-parameter
+    end-to-end errors, the chain's amplification, ambiguous-pixel counts), printed after the
+    run even under -q, in the order the tests ran."""
+    lines = []
+    for key in ("passed", "failed"):
+        for rep in terminalreporter.stats.get(key, []):
+            for name, value in getattr(rep, "user_properties", ()):
+                if name == "parity":
+                    lines.append((rep.nodeid, value))
+    if lines:
+        terminalreporter.section("parity numbers")
+        for nodeid, value in lines:
+            terminalreporter.write_line(f"{value}")

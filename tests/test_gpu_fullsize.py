@@ -1,21 +1,19 @@
 """Full-size parity of the 3D path against the CPU oracle, at the benchmark workloads' own sizes.
 
-  - 1M Gaussians, SH degree 3, 1297x840 (poses 0, 4 and 2; the default radix path on two of them,
-    the span binning on pose 4): the whole frame -- every splat record,
-    sorted key, list entry, tile range and bucket offset bit-exact; image and final T within
-    1e-5 and n_contrib exact outside the oracle's near-threshold pixels (counted and printed);
-    then the backward of a seeded N(0,1) upstream gradient: the screen-space gradients within
-    1e-5 and every parameter gradient within 1e-4 relative L2 of the oracle's.
+  - 1M Gaussians, SH degree 3, 1297x840, all 8 poses (the default radix path on six of them, the
+    span binning on poses 4 and 7): the whole frame -- every splat record, sorted key, list entry,
+    tile range and bucket offset bit-exact; image and final T within 1e-5 and n_contrib exact
+    outside the oracle's near-threshold pixels (counted, recorded and bounded); then the backward
+    of a seeded N(0,1) upstream gradient: the screen-space gradients within 1e-5 and the parameter
+    gradients within the fixed bounds below.
   - The training step at that size (forward, L1 + D-SSIM with lambda 0.2 against a seeded
     U(0,1) target, backward, fused Adam over the six parameter groups, dense and masked to the
     view's visible Gaussians): the loss and its image gradient against the float64 restatement,
     the parameter gradients against the oracle driven by that image gradient, and the Adam update
     bit-exact against the C restatement given the step's own gradients (the checks of
     cluster/tests/test_lean_adam.py:37-134 and phase1/tests/test_parity.py:43-153 at config size).
-  - 3M Gaussians, SH degree 3, 1957x1091: the whole frame's binning bit-exact (58M instances;
-    the span binning, with the radix path giving the same lists),
-    and the screen-space gradients of 64 tiles (the 16 longest lists and 48 drawn at random)
-    against the oracle's backward of the same tiles.
+  - 3M Gaussians, SH degree 3, 1957x1091: the same checks on the whole frame (58M instances; the
+    span binning, with the radix path giving the same lists).
 
 Pixels where a forward decision is ambiguous between the kernels' hardware exp2 and the oracle's
 polynomial exp2 (both within about 1 ulp; the oracle's `amb` mask) are excluded from the forward
@@ -25,11 +23,14 @@ differentiate the same blend.
 The parameter gradients are checked stage by stage. The blend backward's screen-space gradients
 (float32 atomics) must be within 1e-5 of the oracle's (float64 sums). The preprocess backward must
 be within 1e-5 of the oracle's chain rule applied to the same screen-space gradients. End to end,
-the bar is 1e-4 relative L2, except where the exact chain itself amplifies the screen-space
-gradients' float32 rounding beyond that: elongated splats, whose conic-to-covariance step divides
-by det^2 (the reference's own finding, results/phase1/macro_backward.md:52-63). There the bound is
-twice that amplification, measured by running the oracle's chain on the GPU's screen-space
-gradients; both numbers are printed.
+the bar is 1e-4 relative L2 for the means, opacities and SH. The log-scale and rotation gradients
+reach the screen only through the conic, whose step back to the 2D covariance divides by det^2:
+for elongated splats it amplifies the float32 rounding of any conic gradient sum, whatever its
+order (the reference measured 3.0e-3 on scales for its own stock kernel against itself on real
+views, results/phase1/macro_backward.md:52-63). Their bound is the constant GRAD_TOL_COV. Every
+test records the end-to-end error, the preprocess backward's error against the oracle's chain on
+the same screen gradients, and that chain's amplification of the screen gradients' rounding
+(conftest prints them after the run).
 """
 import dataclasses
 
@@ -41,7 +42,7 @@ import dense3d as D
 import loss_ref as L
 import optim as PO
 import oracle as O
-from amdsplat import FusedAdam, l1_ssim_loss, rasterize
+from amdsplat import FusedAdam, _lib, l1_ssim_loss, rasterize
 from amdsplat import raster3d as R
 from amdsplat import scenes
 
@@ -49,7 +50,12 @@ pytestmark = pytest.mark.gpu
 
 FWD_TOL = 1e-5
 GRAD_TOL = 1e-4
+# log-scales and rotations (through the conic's 1/det^2 step)
+GRAD_TOL_COV = 3e-4
 GRAD2D_TOL = 1e-5
+# near-threshold (ambiguous) pixels of a whole frame: at most 398 of 1.09M were seen over the 8
+# poses of the 1M workload and 719 of 2.14M on the 3M one
+AMB_MAX = {"1M": 600, "3M": 1100}
 # Faster-GS's learning rates for the training step: means, log-scales, quats, SH DC, SH rest, opacity
 LR = {"means": 1.6e-4, "scales": 5e-3, "quats": 1e-3, "sh_dc": 2.5e-3, "sh_rest": 1.25e-4, "opacity": 5e-2}
 
@@ -68,29 +74,65 @@ def sh3_1m():
 
 
 PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
+GRAD_BOUND = {"means": GRAD_TOL, "log_scales": GRAD_TOL_COV, "quats": GRAD_TOL_COV, "opacity_logits": GRAD_TOL,
+              "sh": GRAD_TOL}
 GRAD2D_COLS = ["mx", "my", "A", "B", "C", "opacity", "r", "g", "b", "|mx|", "|my|"]
 
 
-def check_gradients(tag, host, cam, rec, touched, got2, g2, got):
-    """got2: the GPU's screen-space gradients, g2: the oracle's; got: the GPU's parameter
-    gradients (5 arrays)."""
-    for k, name in enumerate(GRAD2D_COLS):
-        e = D.rel_err(got2[:, k], g2[:, k])
-        assert e < GRAD2D_TOL, f"{tag} grad2d {name}: {e:.2e}"
-    want = O.preprocess_bwd(*host, cam, 3, rec, touched, g2)
-    chain = O.preprocess_bwd(*host, cam, 3, rec, touched, got2)
-    vis = touched > 0
+def report(record, line):
+    print(line, flush=True)
+    record("parity", line)
+
+
+def check_grad2d(record, tag, got2, g2, cols=GRAD2D_COLS):
+    errs = [D.rel_err(got2[:, k], g2[:, k]) for k in range(len(cols))]
+    report(record, f"[{tag}] grad2d rel L2 (bound {GRAD2D_TOL:.0e}): " +
+           " ".join(f"{c}={e:.2e}" for c, e in zip(cols, errs)))
+    for c, e in zip(cols, errs):
+        assert e < GRAD2D_TOL, f"{tag} grad2d {c}: {e:.2e}"
+
+
+def check_params(record, tag, got, want, chain, vis=None):
+    """got: the GPU's parameter gradients; want: the oracle's end to end; chain: the oracle's
+    preprocess backward applied to the GPU's own screen-space gradients."""
     for name, a, w, c in zip(PARAMS, got, want, chain):
         a = np_(a).reshape(w.shape)
         e_chain = D.rel_err(a, c)
         e_amp = D.rel_err(c, w)
         e = D.rel_err(a, w)
-        bound = max(GRAD_TOL, 2.0 * e_amp)
-        print(f"[{tag}] grad {name}: end to end {e:.2e} (bound {bound:.1e}); preprocess backward vs the oracle's "
-              f"chain {e_chain:.2e}; the chain's amplification of the grad2d rounding {e_amp:.2e}", flush=True)
+        report(record, f"[{tag}] grad {name}: end to end {e:.2e} (bound {GRAD_BOUND[name]:.0e}); preprocess "
+                       f"backward vs the oracle's chain {e_chain:.2e}; the chain's amplification of the grad2d "
+                       f"rounding {e_amp:.2e}")
         assert e_chain < GRAD2D_TOL, f"{tag} {name}: preprocess backward {e_chain:.2e}"
-        assert e < bound, f"{tag} {name}: {e:.2e}"
-        assert np.all(a[~vis] == 0)
+        assert e < GRAD_BOUND[name], f"{tag} {name}: {e:.2e}"
+        if vis is not None:
+            assert np.all(a[~vis] == 0)
+
+
+def check_gradients(record, tag, host, cam, rec, touched, got2, g2, got):
+    """got2: the GPU's screen-space gradients, g2: the oracle's; got: the GPU's parameter
+    gradients (5 arrays)."""
+    check_grad2d(record, tag, got2, g2)
+    want = O.preprocess_bwd(*host, cam, 3, rec, touched, g2)
+    chain = O.preprocess_bwd(*host, cam, 3, rec, touched, got2)
+    check_params(record, tag, got, want, chain, touched > 0)
+
+
+def check_forward(record, tag, fs, ref, cam, amb_max):
+    vis = ref["touched"] > 0
+    assert np.array_equal(np_(fs.touched).astype(np.uint32), ref["touched"])
+    assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref["rec"][vis].view(np.uint32)), "records differ"
+    check_binning(fs, ref)
+    amb = ref["amb"]
+    ok = ~amb
+    e_img = float(np.abs(np_(fs.image) - ref["image"])[:, ok].max())
+    e_T = float(np.abs(np_(fs.final_T) - ref["final_T"])[ok].max())
+    report(record, f"[{tag}] visible {int(vis.sum())}, instances {fs.m}, buckets {fs.n_buckets}, ambiguous pixels "
+                   f"{int(amb.sum())} of {cam.width * cam.height} (bound {amb_max}); image max abs {e_img:.2e}, "
+                   f"final T max abs {e_T:.2e} (bound {FWD_TOL:.0e})")
+    assert amb.sum() <= amb_max
+    assert e_img <= FWD_TOL and e_T <= FWD_TOL
+    assert np.array_equal(np_(fs.n_contrib)[ok], ref["n_contrib"][ok])
 
 
 def check_binning(fs, ref):
@@ -101,39 +143,33 @@ def check_binning(fs, ref):
     assert np.array_equal(np_(fs.bucket_offsets).view(np.uint32), ref["bucket_offsets"]), "bucket offsets differ"
 
 
-@pytest.mark.parametrize("pose,binning", [(0, "auto"), (4, "spans"), (2, "auto")])
-def test_sh3_1m_full_frame_forward_backward(sh3_1m, pose, binning):
-    sc = sh3_1m
-    cam = dataclasses.replace(sc.cameras[pose], binning=binning)
+def full_frame(record, tag, sc, cam, amb_max, seed):
+    """Forward and backward of one view on the whole frame against the oracle."""
     host = [t.numpy() for t in sc.params()]
     p = [t.cuda().contiguous() for t in sc.params()]
     fs = R.forward_pass(*p, cam, sh_degree=3, keep_keys=True)
     torch.cuda.synchronize()
     ref = O.render(*host, cam, 3)
-    vis = ref["touched"] > 0
-    assert np.array_equal(np_(fs.touched).astype(np.uint32), ref["touched"])
-    assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), ref["rec"][vis].view(np.uint32)), "records differ"
-    check_binning(fs, ref)
-    amb = ref["amb"]
-    n_px = cam.width * cam.height
-    print(f"[1M pose {pose}] visible {int(vis.sum())}, instances {fs.m}, buckets {fs.n_buckets}, "
-          f"ambiguous pixels {int(amb.sum())} of {n_px}", flush=True)
-    assert amb.sum() <= 1e-3 * n_px
-    ok = ~amb
-    assert np.abs(np_(fs.image) - ref["image"])[:, ok].max() <= FWD_TOL
-    assert np.abs(np_(fs.final_T) - ref["final_T"])[ok].max() <= FWD_TOL
-    assert np.array_equal(np_(fs.n_contrib)[ok], ref["n_contrib"][ok])
+    check_forward(record, tag, fs, ref, cam, amb_max)
     # backward: seeded N(0,1) upstream gradient, zero on the ambiguous pixels
-    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(100 + pose))
-    gi[:, torch.from_numpy(amb)] = 0.0
+    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(seed))
+    gi[:, torch.from_numpy(ref["amb"])] = 0.0
     grads = R.backward_pass(fs, *p, gi.cuda(), abs_grad=True)
     torch.cuda.synchronize()
     g2 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
                      ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"], sc.n)
-    check_gradients(f"1M pose {pose}", host, cam, ref["rec"], ref["touched"], np_(grads[5]), g2, grads[:5])
+    check_gradients(record, tag, host, cam, ref["rec"], ref["touched"], np_(grads[5]), g2, grads[:5])
+    return p, fs
 
 
-def test_sh3_1m_training_step(sh3_1m):
+@pytest.mark.parametrize("pose,binning", [(0, "auto"), (1, "auto"), (2, "auto"), (3, "auto"), (4, "spans"),
+                                          (5, "auto"), (6, "auto"), (7, "spans")])
+def test_sh3_1m_full_frame_forward_backward(sh3_1m, pose, binning, record_property):
+    cam = dataclasses.replace(sh3_1m.cameras[pose], binning=binning)
+    full_frame(record_property, f"1M pose {pose} {binning}", sh3_1m, cam, AMB_MAX["1M"], 100 + pose)
+
+
+def test_sh3_1m_training_step(sh3_1m, record_property):
     """Config 5 at its own size: one step, pose 0, dense and masked Adam from the same gradients."""
     sc = sh3_1m
     cam = sc.cameras[0]
@@ -151,7 +187,8 @@ def test_sh3_1m_training_step(sh3_1m):
     # (1) the loss and its image gradient against the float64 restatement
     (Lr, l1r, sr), gr = L.loss_and_grad(np_(img), target.numpy(), 0.2)
     pp = np_(parts)
-    print(f"[train 1M] loss {float(loss):.6f} (float64 {Lr:.6f}), L1 {pp[1]:.6f}, SSIM {pp[2]:.6f}", flush=True)
+    report(record_property, f"[train 1M] loss {float(loss):.6f} (float64 {Lr:.6f}), L1 {pp[1]:.6f}, "
+                            f"SSIM {pp[2]:.6f}")
     assert abs(float(loss) - Lr) <= 1e-5 * abs(Lr)
     assert abs(pp[1] - l1r) <= 1e-5 * abs(l1r) and abs(pp[2] - sr) <= 1e-5 * max(abs(sr), 1e-3)
     gimg = np_(img.grad)
@@ -170,8 +207,7 @@ def test_sh3_1m_training_step(sh3_1m):
                                abs_grad=True)[5])
     g2 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
                      ref["image"], gimg_ok, ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"], sc.n)
-    for k, name in enumerate(GRAD2D_COLS):
-        assert D.rel_err(got2[:, k], g2[:, k]) < GRAD2D_TOL, f"train grad2d {name}"
+    check_grad2d(record_property, "train 1M (ambiguous pixels zeroed)", got2, g2)
     # end to end through autograd, with the loss's full image gradient
     g2_full = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width,
                           cam.height, ref["image"], gimg, ref["final_T"], ref["n_contrib"], ref["tile_max"],
@@ -183,17 +219,9 @@ def test_sh3_1m_training_step(sh3_1m):
     # them): the float32 atomics' order differs from run to run, and so does what the chain
     # makes of it, so the amplification is measured on the same run
     got2_full = np_(img.grad_fn.grad2d)
-    for k, name in enumerate(GRAD2D_COLS[:9]):
-        assert D.rel_err(got2_full[:, k], g2_full[:, k]) < GRAD2D_TOL, f"train grad2d (full image gradient) {name}"
+    check_grad2d(record_property, "train 1M", got2_full[:, :9], g2_full[:, :9], GRAD2D_COLS[:9])
     chain = O.preprocess_bwd(*host, cam, 3, ref["rec"], ref["touched"], got2_full)
-    for name, a, w, c in zip(PARAMS, got, want, chain):
-        a = np_(a).reshape(w.shape)
-        e, e_amp, e_chain = D.rel_err(a, w), D.rel_err(c, w), D.rel_err(a, c)
-        bound = max(GRAD_TOL, 2.0 * e_amp)
-        print(f"[train 1M] grad {name}: end to end {e:.2e} (bound {bound:.1e}); preprocess backward vs the oracle's "
-              f"chain {e_chain:.2e}; the chain's amplification of the grad2d rounding {e_amp:.2e}", flush=True)
-        assert e_chain < GRAD2D_TOL, f"{name}: preprocess backward {e_chain:.2e}"
-        assert e < bound, f"{name}: {e:.2e}"
+    check_params(record_property, "train 1M", got, want, chain)
     # (3) fused Adam, dense and masked, from the step's own gradients: bit-exact against optim.c
     vis = aux["visibility"]
     vis_np = np_(vis)
@@ -224,52 +252,12 @@ def test_sh3_1m_training_step(sh3_1m):
     R._Rasterize3D.track_visibility = False
 
 
-def test_sh3_3m_binning_and_sampled_tile_backward():
+def test_sh3_3m_full_frame_forward_backward(record_property):
     sc = scenes.sh3_3m()
     cam = sc.cameras[0]
-    host = [t.numpy() for t in sc.params()]
-    p = [t.cuda().contiguous() for t in sc.params()]
-    fs = R.forward_pass(*p, cam, sh_degree=3, keep_keys=True)
-    torch.cuda.synchronize()
-    rec, touched = O.preprocess_fwd(*host, cam, 3)
-    vis = touched > 0
-    assert np.array_equal(np_(fs.touched).astype(np.uint32), touched)
-    assert np.array_equal(np_(fs.rec)[vis].view(np.uint32), rec[vis].view(np.uint32))
-    keys, pl, ranges, boff = O.bin_instances(rec, touched, cam)
-    print(f"[3M] visible {int(vis.sum())}, instances {fs.m}, buckets {int(boff[-1])}", flush=True)
-    check_binning(fs, dict(keys=keys, point_list=pl, ranges=ranges, bucket_offsets=boff))
-    del keys
+    p, fs = full_frame(record_property, "3M pose 0 auto", sc, cam, AMB_MAX["3M"], 31)
     # the radix path (this size takes the span binning by default) gives the same lists
-    for other in ("radix",):
-        fr = R.forward_pass(*p, dataclasses.replace(cam, binning=other), sh_degree=3)
-        assert torch.equal(fr.point_list, fs.point_list) and torch.equal(fr.ranges, fs.ranges), other
-        assert torch.equal(fr.bucket_offsets, fs.bucket_offsets), other
-        del fr
-    # 64 tiles: the 16 longest lists and 48 at random; every other tile gets an empty range
-    T = cam.n_tiles
-    length = (ranges[:, 1] - ranges[:, 0]).astype(np.int64)
-    heavy = np.argsort(length)[-16:]
-    rest = np.setdiff1d(np.arange(T), heavy)
-    sample = np.concatenate([heavy, np.random.default_rng(0).choice(rest, size=48, replace=False)])
-    keep = np.zeros(T, bool)
-    keep[sample] = True
-    sr = ranges.copy()
-    sr[~keep] = sr[~keep, :1]  # empty range at the tile's position
-    sboff = np.concatenate([[0], np.cumsum((sr[:, 1] - sr[:, 0] + 31) // 32)]).astype(np.uint32)
-    img, fT, nc, tmax, ck, amb = O.blend_fwd(rec, pl, sr, sboff, cam.width, cam.height)
-    px_keep = np.zeros((cam.tiles_y * 16, cam.tiles_x * 16), bool)
-    for t in sample:
-        tx, ty = t % cam.tiles_x, t // cam.tiles_x
-        px_keep[ty * 16:ty * 16 + 16, tx * 16:tx * 16 + 16] = True
-    px_keep = px_keep[:cam.height, :cam.width]
-    ok = px_keep & ~amb
-    print(f"[3M] sampled tiles: {int(length[sample].sum())} list entries, ambiguous pixels {int(amb.sum())}",
-          flush=True)
-    assert np.abs(np_(fs.image) - img)[:, ok].max() <= FWD_TOL
-    assert np.array_equal(np_(fs.n_contrib)[ok], nc[ok])
-    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(31))
-    gi[:, torch.from_numpy(~ok)] = 0.0  # only the sampled tiles' unambiguous pixels contribute
-    grads = R.backward_pass(fs, *p, gi.cuda(), abs_grad=True)
-    g2 = O.blend_bwd(rec, pl, sr, sboff, cam.width, cam.height, img, gi.numpy(), fT, nc, tmax, ck, sc.n)
-    assert np.abs(g2[:, :9]).sum() > 0
-    check_gradients("3M sampled tiles", host, cam, rec, touched, np_(grads[5]), g2, grads[:5])
+    fr = R.forward_pass(*p, dataclasses.replace(cam, binning="radix"), sh_degree=3)
+    assert fs.path == _lib.GS_BIN_PATH_SPANS and fr.path == _lib.GS_BIN_PATH_RADIX
+    assert torch.equal(fr.point_list, fs.point_list) and torch.equal(fr.ranges, fs.ranges)
+    assert torch.equal(fr.bucket_offsets, fs.bucket_offsets)
