@@ -98,6 +98,8 @@ _SIGS = {
     "gs_l1_ssim_fwd": (_i32, [_vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp, _sz, _vp]),
     "gs_l1_ssim_bwd": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp]),
     "gs_l1_ssim_fwd_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp]),
+    "gs_stage_marks": (_i32, [_i32]),
+    "gs_stage_marks_read": (_i32, [C.POINTER(C.c_float), C.POINTER(C.c_char_p), _i32]),
     "gs_probe_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "gs_probe_read_sums": (_i64, [_i64]),
     "gs_probe_read": (_i32, [_vp, _i64, _vp, _vp]),

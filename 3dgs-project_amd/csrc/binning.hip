@@ -1873,6 +1873,7 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
     if (offsets) hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, offsets, int64_t(1), 0u);
     return;
   }
+  stage_mark("start", st);
   if (keys_in || rec || depth || depth64) {
     const uint32_t* keys = keys_in;
     int bits = keys_in ? key_bits : 32;
@@ -1895,7 +1896,11 @@ static void bin_prepare(const SplatRec* rec, const float* depth, const double* d
       radix_sort(keys, nullptr, dsorted, order, n, bits, sort_scratch, st, sorted_counts ? counts : nullptr,
                  sorted_counts, nullptr, true);
     }
-    if (offsets) scan_rec(sorted_counts, offsets, n, scan_scratch, st);
+    stage_mark("depth_sort", st);
+    if (offsets) {
+      scan_rec(sorted_counts, offsets, n, scan_scratch, st);
+      stage_mark("instance_offsets", st);
+    }
   } else {
     hipLaunchKernelGGL(iota_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, order, n);
     if (offsets) scan_rec(counts, offsets, n, scan_scratch, st);  // index order
@@ -1923,8 +1928,10 @@ static void emit_and_sort(const SplatRec* rec, const int4* rects, const uint32_t
     hipLaunchKernelGGL((emit_kernel<false, K>), dim3(grid_for(n_windows, 4)), dim3(256), 0, st, rec, rects, order,
                        offsets, n, wstart, n_windows, tiles_x, n_tiles / tiles_x, tkeys, tvals, preset, n_tiles);
   }
+  stage_mark("key_duplication", st);
   radix_sort(tkeys, tvals, tsorted, point_list, m, tile_bits, ws + L.sort, st, nullptr, nullptr, preset,
              preset != nullptr && !sorted_keys);
+  stage_mark("tile_sort", st);
   if (sorted_keys)
     hipLaunchKernelGGL((full_keys_kernel<K>), dim3(grid_for(m, 256)), dim3(256), 0, st, tsorted, point_list, dkey_of,
                        dkey0, m, sorted_keys);
@@ -1967,12 +1974,14 @@ static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dk
   hipLaunchKernelGGL(rs_rowscan_kernel, dim3(tiles_y), dim3(kScanThreads), 0, st, rowhist, L.n_chunks, rowtot);
   hipLaunchKernelGGL(span_place_kernel, dim3(g_rows), dim3(256), lds_place, st, gathered, chunk_info, rowhist, rowtot,
                      L.n_chunks, tiles_y, spans, L.gathered_cap, L.span_cap);
+  stage_mark("span_rows", st);
   hipLaunchKernelGGL(span_col_count_kernel, dim3(g_cols), dim3(256), lds_ccount, st, spans, rowtot, tiles_x, tiles_y,
                      L.span_cap, L.chunk_cap, colhist);
   hipLaunchKernelGGL(span_col_scan_kernel, dim3(tiles_y), dim3(kColScanThreads), 0, st, colhist, rowtot, tiles_x,
                      tiles_y, L.chunk_cap, tcnt);
   hipLaunchKernelGGL(tile_scan_kernel, dim3(1), dim3(kBoThreads), 0, st, tcnt, tiles_x * tiles_y, ranges,
                      bucket_offsets, tile_offsets, list_header);
+  stage_mark("span_columns", st);
 #define GS_SPAN_WRITE(KEYS, RR)                                                                                     \
   hipLaunchKernelGGL((span_col_write_kernel<KEYS, RR>), dim3(g_cols), dim3(256), lds_cwrite, st, spans, rowtot,     \
                      colhist, ranges, tiles_x, tiles_y, L.span_cap, L.chunk_cap, m, point_list, sorted_keys, dkey_of, \
@@ -1985,6 +1994,7 @@ static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dk
     else if (R == 2) GS_SPAN_WRITE(false, 2); else GS_SPAN_WRITE(false, 1);
   }
 #undef GS_SPAN_WRITE
+  stage_mark("span_write", st);
 }
 
 static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dkey_of, uint32_t dkey0,
@@ -1993,6 +2003,7 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
                      uint64_t* sorted_keys, uint32_t* point_list, uint32_t* ranges, uint32_t* tile_offsets,
                      uint32_t* bucket_offsets, uint32_t* list_header, int flags, char* ws, hipStream_t st) {
   const int n_tiles = tiles_x * tiles_y;
+  stage_mark("start", st);
   if (m > 0 && use_spans(n, tiles_x, tiles_y, flags)) {
     // (gs_bin_fill_* reject an m beyond span_fits for this path)
     if (rects)
@@ -2026,6 +2037,7 @@ static void bin_emit(const SplatRec* rec, const int4* rects, const uint32_t* dke
                          st, reinterpret_cast<const uint32_t*>(ws + L.tsorted), m, n_tiles, ranges);
     hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,
                        tile_offsets, list_header, sort_ranges);
+    stage_mark("ranges_buckets", st);
     return;
   }
   hipLaunchKernelGGL(bucket_offsets_kernel, dim3(1), dim3(kBoThreads), 0, st, ranges, n_tiles, m, bucket_offsets,

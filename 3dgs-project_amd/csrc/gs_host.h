@@ -18,6 +18,9 @@ void clear_error();
 // Returns GS_ERR_LAUNCH (and records the message) if the last launch failed.
 int check_launch(const char* what);
 
+// Records a stage mark on `st` if stage marks are enabled on this thread (gs_stage_marks).
+void stage_mark(const char* name, hipStream_t st);
+
 // Enqueues a zero fill of n floats (a kernel, not hipMemsetAsync, so the call can be
 // captured in a HIP graph).
 void fill_zero_f32(float* p, int64_t n, hipStream_t st);

@@ -45,8 +45,10 @@ HBM_PEAK_GBS = 8000.0
 # FP32 VALU lane operations per second: the published 157.3 TFLOP/s FP32 vector peak with an
 # FMA counted as 2 FLOP (one lane operation)
 VALU_PEAK_TOPS = 157.3 / 2
-# the same peak in wave64 instructions per second
-VALU_PEAK_INSTR = VALU_PEAK_TOPS * 1e12 / 64
+# The issue rate this build can reach: the published peak counts packed FP32 (two lanes' worth per
+# v_pk_* instruction), which the build does not use, so plain VALU instructions issue at half of
+# it: one wave64 instruction per 4 cycles per SIMD, 4 SIMDs x 256 CUs at 2.4 GHz
+VALU_ISSUE_PEAK_INSTR = 256 * 4 * 2.4e9 / 4
 METRIC = "fwd+bwd ms/iter @1M Gaussians SH3 1297x840; per-stage HBM GB/s vs roofline"
 # stages that are one kernel each (the others group several kernels)
 SINGLE_KERNEL = {"preprocess": "preprocess_fwd_kernel", "blend_fwd": "blend_fwd_strip_kernel",
@@ -66,7 +68,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=160)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit"])
+    ap.add_argument("--workload", default="sh3_1m",
+                    choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit", "toy2d_bench"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5, help="all-core CPU baseline runs (median)")
     ap.add_argument("--cpu-single-runs", type=int, default=3, help="single-thread CPU baseline runs (0 = skip)")
@@ -151,21 +154,31 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
     T = fs.cam.n_tiles
     P = fs.cam.width * fs.cam.height
     B = int(fs.bucket_offsets[-1].item())
+    # the depth sort: 3 radix passes over N (histogram read 4 B, key+value read and write 16 B),
+    # the last one also gathering the counts into depth order (read + write 8 B)
+    sub = {"depth_sort": 3 * 20 * n + (8 * n if spans is None else 0)}
     if spans is None:
-        # 3 radix passes over N (histogram read 4 B, key+value read and write 16 B), the counts
-        # gathered into depth order (read + write), the scan (counts read, offsets written)
-        depth = 3 * 20 * n + 8 * n + 8 * n
-        # emission (48 B of the record of the visible, order and offset per Gaussian, key+value
-        # per instance), tile sort pass 1 (histogram 4, key+value read and write 16) and pass 2
-        # (histogram 4, key+value read 8, value write 4), ranges and bucket offsets per tile
-        binning = 48 * n_visible + 8 * n + 8 * m + 20 * m + 16 * m + 20 * T + 4 * B
+        # the scan of the counts in depth order (read, offsets written)
+        sub["instance_offsets"] = 8 * n
+        # tile keys of 16 bits below 65536 tiles, else 32
+        kb = 2 if T <= 65536 else 4
+        # emission: order and offset per Gaussian, 48 B of the record of the visible, key + value
+        # per instance; tile sort pass 1 (histogram read kb, key+value read and written) and
+        # pass 2 (histogram kb, key+value read, value written); ranges and bucket offsets
+        sub["key_duplication"] = 8 * n + 48 * n_visible + (kb + 4) * m
+        sub["tile_sort"] = (kb + 2 * (kb + 4)) * m + (kb + (kb + 4) + 4) * m
+        sub["ranges_buckets"] = 20 * T + 4 * B
+        depth = sub["depth_sort"] + sub["instance_offsets"]
     else:
-        # 3 radix passes over N
-        depth = 3 * 20 * n
-        # order 4 B and 48 B of the record of the visible per Gaussian; per span: gathered (8 B
-        # written, read), placed by row (8 B written), read by the column count and the placement
-        # (8 B each); the point list 4 B per instance; tile counts, ranges, bucket offsets
-        binning = 4 * n + 48 * n_visible + 40 * spans + 4 * m + 20 * T + 4 * B
+        # rows: order 4 B and 48 B of the record of the visible per Gaussian, each span gathered
+        # (8 B written, read) and placed by row (8 B written); columns: each span read by the
+        # column count (8 B), tile counts; the write: each span read (8 B), the point list 4 B per
+        # instance, ranges and bucket offsets
+        sub["span_rows"] = 4 * n + 48 * n_visible + 24 * spans
+        sub["span_columns"] = 8 * spans + 4 * T
+        sub["span_write"] = 8 * spans + 4 * m + 16 * T + 4 * B
+        depth = sub["depth_sort"]
+    binning = sum(v for k, v in sub.items() if k not in ("depth_sort", "instance_offsets"))
     return {
         # params 44 B/Gaussian + tiles_touched and depth key 8 B; SH 12 K B and the 64 B record
         # per visible one; the empty bounds (16 B) of each culled one's record
@@ -183,7 +196,35 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
         # tiles_touched of every Gaussian; params, SH and grad2d of the visible (the colour clamp
         # is recomputed from the SH rows, the record is not read); every output row written
         "preprocess_bwd": 4 * n + n_visible * (44 + 12 * K + 48) + n * (44 + 12 * K),
+        "substages": sub,
     }
+
+
+def substage_times(step, k_steps: int) -> dict:
+    """Mean ms of each stage the library marks inside its calls (gs_stage_marks), over k_steps
+    steps; each step is waited for before the next."""
+    import torch
+
+    from amdsplat import _lib
+
+    L = _lib.lib()
+    cap = 64
+    ms = (ctypes.c_float * cap)()
+    names = (ctypes.c_char_p * cap)()
+    acc = {}
+    torch.cuda.synchronize()
+    for k in range(k_steps):
+        L.gs_stage_marks(1)
+        step(k)
+        n = L.gs_stage_marks_read(ms, names, cap)
+        L.gs_stage_marks(0)
+        if n < 0:
+            raise RuntimeError(L.gs_last_error().decode())
+        for i in range(n):
+            name = names[i].decode()
+            if name != "start":
+                acc.setdefault(name, []).append(ms[i])
+    return {k2: statistics.mean(v) for k2, v in acc.items()}
 
 
 def bucket_stats(fs):
@@ -253,9 +294,10 @@ def _median_runs(fn, runs: int) -> tuple[float, list]:
 
 
 def cpu_baseline_3d(scene, pose: int, runs: int, single_runs: int) -> dict:
-    """The C oracle (the CPU restatement of the same rules: preprocess, binning and forward blend
-    on OpenMP threads, the backward blend single-threaded) timed on the host: one full fwd+bwd of
-    one view of the workload, all cores (median of `runs` after a warm-up) and one thread."""
+    """The C oracle (the CPU restatement of the same rules) timed on the host: one full fwd+bwd of
+    one view of the workload, all cores (median of `runs` after a warm-up) and one thread. The
+    preprocess, the forward and backward blends (tile-parallel) and the preprocess backward run on
+    OpenMP threads; the binning is serial (instances emitted, then one qsort)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -279,8 +321,9 @@ def cpu_baseline_3d(scene, pose: int, runs: int, single_runs: int) -> dict:
     out = {"value": round(med * 1000.0, 1), "unit": "ms/iter", "cores": cores, "kind": "port",
            "runs_s": [round(t, 2) for t in times], "nproc": os.cpu_count(), "cpu_model": cpu_model(),
            "sample": f"the C oracle's fwd+bwd of pose {pose} of this workload, all {scene.n} Gaussians: median of "
-                     f"{runs} runs after a warm-up, {cores} OpenMP threads (preprocess, binning and forward "
-                     f"blend parallel; the backward blend single-threaded)"}
+                     f"{runs} runs after a warm-up, {cores} OpenMP threads (preprocess, forward blend, "
+                     f"backward blend and preprocess backward parallel; the binning serial: instance "
+                     f"emission and one qsort)"}
     if single_runs > 0:
         _omp_threads(1)
         smed, stimes = _median_runs(once, single_runs)
@@ -363,7 +406,36 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
 
         _Rasterize3D.track_visibility = False
         _Rasterize.track_visibility = False
+    out["loss_kernels"] = loss_kernel_times(targets[0], max(steps, 20))
     return out
+
+
+def loss_kernel_times(target, reps: int) -> dict:
+    """Event-timed gs_l1_ssim_fwd (with the backward's per-pixel map) and gs_l1_ssim_bwd on an
+    image of the target's size, each launched `reps` times back to back. Algorithmic bytes: the
+    forward reads both images and writes the map (3 floats per pixel and channel), the backward
+    reads the images and the map and writes the image gradient."""
+    import torch
+
+    from amdsplat import _lib
+    from amdsplat._lib import call, ptr
+
+    C, H, W = target.shape
+    x = torch.rand(C, H, W, generator=torch.Generator().manual_seed(5)).cuda()
+    dmap = torch.empty(C, 3, H, W, device="cuda")
+    loss = torch.empty(3, device="cuda")
+    g = torch.empty_like(x)
+    ws = torch.empty(max(_lib.size_call("gs_l1_ssim_workspace_size", C, H, W), 1), dtype=torch.uint8, device="cuda")
+    st = _lib.stream_handle()
+    fwd = _event_ms(lambda: call("gs_l1_ssim_fwd", ptr(x), ptr(target), C, H, W, 0.2, ptr(dmap), ptr(loss), ptr(ws),
+                                 ws.numel(), st), reps)
+    bwd = _event_ms(lambda: call("gs_l1_ssim_bwd", ptr(x), ptr(target), ptr(dmap), C, H, W, 0.2, None, ptr(g), st),
+                    reps)
+    px = C * H * W
+    fb, bb = 4 * px * (2 + 3), 4 * px * (2 + 3 + 1)
+    return {"image": [C, H, W],
+            "fwd_ms": round(fwd, 4), "fwd_hbm_gbs": round(fb / (fwd * 1e6), 1), "fwd_algorithmic_bytes": fb,
+            "bwd_ms": round(bwd, 4), "bwd_hbm_gbs": round(bb / (bwd * 1e6), 1), "bwd_algorithmic_bytes": bb}
 
 
 def variants_bench(sc, grads, steps: int, warmup: int) -> dict:
@@ -476,6 +548,11 @@ def bench_3d(args, ceilings) -> dict:
     torch.cuda.synchronize()
     staged_wall_ms = (time.perf_counter() - t1) * 1000.0 / args.steps
 
+    # the binning chain's sub-stages, from the library's stage marks (HIP events between its
+    # kernels), over one more pass of the same steps, each step waited for before the next
+    mark_steps = max(len(cams), min(args.steps, 4 * len(cams)))
+    sub_ms = substage_times(lambda k: step(k), mark_steps)
+
     per_stage = {}
     step_ms = []
     pose_ms = [[] for _ in cams]
@@ -509,7 +586,14 @@ def bench_3d(args, ceilings) -> dict:
                          **({"row_spans": spans} if spans is not None else {}),
                          "bytes": stage_bytes(fs, nv, ab, ss, up, stg, ckw, spans=spans)})
     counts = {k2: round(statistics.mean(pp[k2] for pp in per_pose)) for k2 in per_pose[0] if k2 != "bytes"}
-    sb = {k2: statistics.mean(pp["bytes"][k2] for pp in per_pose) for k2 in per_pose[0]["bytes"]}
+    sb = {k2: statistics.mean(pp["bytes"][k2] for pp in per_pose) for k2 in per_pose[0]["bytes"]
+          if k2 != "substages"}
+    sub_bytes = {k2: statistics.mean(pp["bytes"]["substages"].get(k2, 0) for pp in per_pose)
+                 for k2 in per_pose[0]["bytes"]["substages"]}
+    substages = {k2: {"ms": round(v, 4), "algorithmic_bytes": round(sub_bytes[k2]),
+                      "hbm_gbs": round(sub_bytes[k2] / (v * 1e6), 1) if v > 0 else None,
+                      "hbm_frac": round(sub_bytes[k2] / (v * 1e6) / HBM_PEAK_GBS, 4) if v > 0 else None}
+                 for k2, v in sub_ms.items() if k2 in sub_bytes}
     stage_gbs = {k2: sb[k2] / (stage_ms[k2] * 1e6) for k2 in stage_ms if k2 in sb and stage_ms[k2] > 0}
     dominant = max((k2 for k2 in stage_ms if k2 in SINGLE_KERNEL), key=lambda k2: stage_ms[k2])
     kernel = SINGLE_KERNEL[dominant]
@@ -539,8 +623,9 @@ def bench_3d(args, ceilings) -> dict:
     if valu_instr:
         rate = valu_instr / (t_dom * 1e-3)
         roof["issue"] = {"valu_instr_per_launch": valu_instr, "achieved": round(rate / 1e12, 4),
-                         "peak": round(VALU_PEAK_INSTR / 1e12, 4), "unit": "T wave64 VALU instr/s",
-                         "frac": round(rate / VALU_PEAK_INSTR, 4)}
+                         "peak": round(VALU_ISSUE_PEAK_INSTR / 1e12, 4),
+                         "unit": "T wave64 VALU instr/s (plain FP32 issue: 1 per 4 cycles per SIMD at 2.4 GHz)",
+                         "frac": round(rate / VALU_ISSUE_PEAK_INSTR, 4)}
     atomics = _profile_value(f"{kernel}_atomics.md", "atomic_requests_per_launch", args.workload)
     if atomics:
         roof["atomic_requests_per_launch"] = atomics
@@ -568,6 +653,7 @@ def bench_3d(args, ceilings) -> dict:
                    "parallelism": "single GPU"},
         "low_level_ms_per_step": round(low_ms, 4),
         "stage_ms": {k2: round(v, 4) for k2, v in stage_ms.items()},
+        "binning_substages": substages,
         "stage_hbm_gbs": {k2: round(v, 1) for k2, v in stage_gbs.items()},
         "stage_hbm_frac": {k2: round(v / HBM_PEAK_GBS, 4) for k2, v in stage_gbs.items()},
         "event_sum_ms": round(statistics.mean(step_ms), 4),
@@ -747,6 +833,94 @@ def bench_toy2d(args, ceilings) -> dict:
     return out
 
 
+# The reference's own timings of the toy2d kernels (NVIDIA H100, CUDA events, median of 20 calls
+# after 5 warm-ups): forward, forward saving the bucket checkpoints, per-pixel backward, bucketed
+# backward, in ms, per (image size, Gaussians); toy2d/results/bench-cfda5b4-4473561.json:11-76.
+TOY2D_REF_H100 = {
+    (512, 10000): (0.07605, 0.08138, 0.30386, 0.16710),
+    (512, 50000): (0.08946, 0.09562, 0.24104, 0.25720),
+    (512, 200000): (0.19120, 0.22274, 0.28445, 0.49690),
+    (1024, 10000): (0.08664, 0.10072, 1.10880, 0.36314),
+    (1024, 50000): (0.12594, 0.14626, 0.86635, 0.49179),
+    (1024, 200000): (0.22525, 0.26998, 0.79949, 0.82573),
+}
+
+
+def bench_toy2d_kernels(args) -> dict:
+    """The reference's toy2d kernel benchmark (toy2d/bench.py:34-73) on the same scenes:
+    Gaussians2D(n, size, size, seed=0), binned with the float32 depth, a N(0,1) upstream gradient;
+    each of the extension's calls (forward, forward saving the bucket checkpoints, per-pixel
+    backward, bucketed backward) timed alone with HIP events, median of --steps calls after
+    --warmup. The pair and bucket counts must equal the reference's."""
+    import torch
+
+    from gs2d import Gaussians2D, bin_gaussians
+    from gs2d.params import radii_from_cov
+    from gs2d.raster import ext
+
+    golden = json.loads((ROOT / "tests" / "golden" / "toy2d_bench_counts.json").read_text())["rows"]
+    want = {(r["size"], r["n"]): (r["pairs"], r["buckets"]) for r in golden}
+
+    def timed(fn, warmup, iters):
+        for _ in range(warmup):
+            fn()
+        times = []
+        for _ in range(iters):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b))
+        return statistics.median(times)
+
+    rows = []
+    e = ext()
+    for (size, n), ref in TOY2D_REF_H100.items():
+        H = W = size
+        g = Gaussians2D(n, H, W, seed=0).cuda()
+        with torch.no_grad():
+            means, conic, color, opacity, cov = (t.contiguous() for t in g.activated())
+            bins = bin_gaussians(means, radii_from_cov(cov), g.depth, H, W)
+        bg = torch.zeros(3, device="cuda")
+        dout = torch.randn(3, H, W, generator=torch.Generator().manual_seed(0)).cuda()
+        common = (means, conic, color, opacity, bg, bins.ranges, bins.point_list)
+
+        def fwd(save):
+            return e.forward(*common, bins.bucket_offsets, bins.num_buckets, H, W, save)
+
+        out, final_T, n_contrib, _ = fwd(False)
+        out_s, final_T_s, n_contrib_s, bstate = fwd(True)
+        pairs, buckets = int(bins.point_list.numel()), int(bins.num_buckets)
+        if (pairs, buckets) != want[(size, n)]:
+            raise RuntimeError(f"toy2d {size}^2 n={n}: {pairs} pairs, {buckets} buckets; the reference binned "
+                               f"{want[(size, n)]}")
+        r = {"size": size, "n": n, "pairs": pairs, "buckets": buckets,
+             "forward_ms": timed(lambda: fwd(False), args.warmup, args.steps),
+             "forward_save_buckets_ms": timed(lambda: fwd(True), args.warmup, args.steps),
+             "backward_pixel_ms": timed(lambda: e.backward_pixel(*common, final_T, n_contrib, dout), args.warmup,
+                                        args.steps),
+             "backward_splat_ms": timed(lambda: e.backward_splat(*common, bins.bucket_offsets, bins.bucket_to_tile,
+                                                                 out_s, final_T_s, n_contrib_s, bstate, dout),
+                                        args.warmup, args.steps)}
+        r = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        r["reference_h100_ms"] = dict(zip(("forward", "forward_save_buckets", "backward_pixel", "backward_splat"),
+                                          ref))
+        rows.append(r)
+    value = statistics.mean(r["forward_ms"] + r["backward_splat_ms"] for r in rows)
+    ref_value = statistics.mean(v[0] + v[3] for v in TOY2D_REF_H100.values())
+    return {
+        "metric": "toy2d kernels: forward + bucketed backward ms, mean over the reference's 6 bench scenes",
+        "value": round(value, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(value, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (Gaussians2D(n, size, size, seed=0), the reference's bench scenes)",
+        "config": {"workload": "toy2d_bench: 512^2 and 1024^2 x 10k, 50k, 200k 2D Gaussians; each extension call "
+                               "timed alone (median of HIP-event-timed calls)", "parallelism": "single GPU"},
+        "reference_h100_value": round(ref_value, 4),
+        "rows": rows,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -757,7 +931,12 @@ def main():
         print(json.dumps(probes()))
         return
     ceilings = None if args.no_probes else probes()
-    out = bench_toy2d(args, ceilings) if args.workload == "toy2d_fit" else bench_3d(args, ceilings)
+    if args.workload == "toy2d_fit":
+        out = bench_toy2d(args, ceilings)
+    elif args.workload == "toy2d_bench":
+        out = bench_toy2d_kernels(args)
+    else:
+        out = bench_3d(args, ceilings)
     line = json.dumps(out)
     print(line, flush=True)
     if args.json_out:

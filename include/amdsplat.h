@@ -409,6 +409,18 @@ int gs_probe_read(const float* in, int64_t n, float* sums, void* stream);
 int gs_probe_fma(float* out, int64_t threads, int iters, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Stage marks (measurement only; bench.py's per-stage split of the binning chain). After
+ * gs_stage_marks(1), the calls made on this thread record a HIP event on their stream at each
+ * internal stage boundary (the event is named after the stage that ends there; the first mark of
+ * a call is its start). gs_stage_marks_read waits for the last mark and writes, for up to `max`
+ * marks in order, names[i] and ms[i] = the time from mark i - 1 to mark i (ms[0] = 0); it returns
+ * the number written, or -GS_ERR_* on failure. gs_stage_marks(0) stops recording (and both calls forget earlier marks).
+ * The events are created on first use and kept; with marks off (the default) nothing is recorded.
+ * ------------------------------------------------------------------------------------- */
+int gs_stage_marks(int enable);
+int gs_stage_marks_read(float* ms, const char** names, int max);
+
+/* ---------------------------------------------------------------------------------------
  * Allocation-free gs_l1_ssim_fwd. It has no counterpart in the reference. It is for callers
  * that cannot allocate device memory: code under HIP graph capture, tight serving loops, and
  * harnesses that forbid hipMalloc.
