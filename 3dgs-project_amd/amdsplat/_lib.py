@@ -89,9 +89,9 @@ _SIGS = {
                                _vp, _vp, _i64, _i32, _vp]),
     "gs_blend_scores_3d": (_i32, [_vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-                               _vp, _vp, _i32, _vp, _vp]),
+                               _vp, _vp, _vp, _i32, _vp, _vp]),
     "gs_preprocess_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
-                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs_adam_step": (_i32, [C.POINTER(GsAdamGroup), _i32, _i64, _vp, _vp]),
     "gs_densification_stats": (_i32, [_vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp]),
     "gs_l1_ssim_workspace_size": (_sz, [_i32, _i32, _i32]),

@@ -117,7 +117,10 @@ class ForwardState:
     bg: tuple = (0.0, 0.0, 0.0)
     timings: dict = field(default_factory=dict)
     grad2d: torch.Tensor | None = None  # [n, 12] zeroed by the forward blend, for the first backward
+    # [n, 4] float64, zeroed with grad2d: the elongated splats' conic-gradient sums (gs_blend_bwd_3d)
+    grad_conic64: torch.Tensor | None = None
     ccam: "_lib.GsCamera | None" = None  # the camera as the C calls take it (built once per forward)
+    last_conic64: torch.Tensor | None = None  # the float64 conic sums of the last backward
 
     @property
     def n_buckets(self) -> int:
@@ -267,12 +270,15 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
     bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
     backward_state = for_backward and _scores is None
-    n_contrib = tile_max = grad2d = image = final_T = None
+    n_contrib = tile_max = grad2d = conic64 = gbuf = image = final_T = None
     if backward_state:
         n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
         tile_max = torch.empty(T, dtype=torch.int32, device=dev)
-        # the backward's screen gradients, zeroed by the forward blend's workgroups
-        grad2d = torch.empty(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+        # the backward's screen gradients [n, 12] float32 and the elongated splats' float64 conic
+        # sums [n, 4], one buffer that the forward blend's workgroups zero
+        gbuf = torch.empty(n * (GRAD2D_FLOATS + 8), dtype=torch.float32, device=dev)
+        grad2d = gbuf[:n * GRAD2D_FLOATS].view(n, GRAD2D_FLOATS)
+        conic64 = gbuf[n * GRAD2D_FLOATS:].view(torch.float64).view(n, 4)
     if _scores is None:
         image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
         final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
@@ -305,7 +311,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     if _scores is None:
         call("gs_blend_fwd_3d", p_rec, p_ranges, adr["point_list"], p_boff, W, H, bg3, ptr(image), ptr(final_T),
              ptr(n_contrib), ptr(tile_max), adr.get("ckpt"), adr.get("blist"), adr.get("bucket_to_tile"),
-             ptr(grad2d), grad2d.numel() if grad2d is not None else 0,
+             ptr(gbuf), gbuf.numel() if gbuf is not None else 0,
              _lib.GS_BLEND_LIST_CLEARED if backward_state else 0, st)
     else:  # pruning scores: the blend's weights, no image
         call("gs_blend_scores_3d", p_rec, p_ranges, adr["point_list"], W, H, n, ptr(_scores), st)
@@ -330,7 +336,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, path, m, keys, point_list, ranges,
                         bucket_offsets, nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist,
                         tuple(bg),
-                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d, ccam)
+                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d, conic64, ccam)
 
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
@@ -338,7 +344,10 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
                   abs_grad: bool = True):
     """Returns (grad_means, grad_log_scales, grad_quats, grad_opacity_logits, grad_sh, grad2d, timings);
     grad_sh is a (DC, rest) pair when sh is. abs_grad: also sum |dL/dmean2d| into grad2d[:, 9:11]
-    (densification by absolute gradient); otherwise those columns stay zero.
+    (densification by absolute gradient); otherwise those columns stay zero. The conic columns
+    (2-4) of the elongated splats (2D condition number >= 256) are summed in float64 into
+    fs.last_conic64 [n, 4] instead, their rows marked in column 11; combined_grad2d(grad2d,
+    fs.last_conic64) gives all screen-space gradients.
     counters: optional int64 [3] CUDA tensor that the blend backward adds its atomic count and
     pair-evaluation count to (slots 0 and 2)."""
     dev = means.device
@@ -353,12 +362,15 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
     if fs.grad2d is not None:
         # zeroed by the forward blend; a second backward of the same forward starts from zeros
         grad2d, fs.grad2d = fs.grad2d, None
+        conic64, fs.grad_conic64 = fs.grad_conic64, None
     else:
         grad2d = torch.zeros(n, GRAD2D_FLOATS, dtype=torch.float32, device=dev)
+        conic64 = torch.zeros(n, 4, dtype=torch.float64, device=dev)
+    fs.last_conic64 = conic64
     call("gs_blend_bwd_3d", ptr(fs.rec), ptr(fs.ranges), ptr(fs.point_list), ptr(fs.bucket_offsets),
          ptr(fs.bucket_to_tile), fs.n_buckets_max, n, cam.width, cam.height, ptr(fs.image), ptr(grad_image),
          ptr(fs.final_T), ptr(grad_alpha), ptr(fs.n_contrib), ptr(fs.tile_max), ptr(fs.ckpt), ptr(fs.bucket_list),
-         ptr(grad2d),
+         ptr(grad2d), ptr(conic64),
          _lib.GS_ACCUMULATE | (_lib.GS_ABS_GRAD if abs_grad else 0), ptr(counters), st)
     tm.mark("blend_bwd")
     g_means = torch.empty(n, 3, dtype=torch.float32, device=dev)
@@ -377,10 +389,20 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
         g_sh = (g_a, g_b)
     call("gs_preprocess_bwd", ptr(means), ptr(log_scales), ptr(quats), ptr(opacity_logits), ptr(sh_a), ptr(sh_b),
          n, fs.sh_coeffs, fs.sh_degree, fs.ccam if fs.ccam is not None else cam.c_struct(), ptr(fs.touched),
-         ptr(grad2d), ptr(g_means),
+         ptr(grad2d), ptr(conic64), ptr(g_means),
          ptr(g_ls), ptr(g_q), ptr(g_op), ptr(g_a), ptr(g_b), st)
     tm.mark("preprocess_bwd")
     return g_means, g_ls, g_q, g_op, g_sh, grad2d, {} if isinstance(timing, StageTimer) else tm.result()
+
+
+def combined_grad2d(grad2d: torch.Tensor, conic64: torch.Tensor | None) -> torch.Tensor:
+    """The screen-space gradients of a backward as float64 [n, 12]: grad2d with the elongated
+    splats' float64 conic sums added to columns 2-4 (and their mark in column 11 cleared)."""
+    g = grad2d.double()
+    if conic64 is not None:
+        g[:, 2:5] += conic64[:, :3]
+    g[:, 11] = 0.0
+    return g
 
 
 def densification_stats(grad2d: torch.Tensor, touched: torch.Tensor, width: int, height: int,

@@ -20,6 +20,24 @@
 
 namespace gs {
 
+// Elongated splats (3D backward). The conic-gradient sums of a splat whose 2D covariance has a
+// condition number lambda_max / lambda_min >= kElongKappa are reduced over the wavefront and
+// added over the buckets in float64: the preprocess backward's step from the conic to the
+// covariance divides by det^2 and amplifies the rounding of float32 sums for such splats by
+// about that condition number (a few hundred float32 roundings of partial sums with
+// cancellation would move their scale and rotation gradients by 1e-4 of the whole gradient's
+// norm). With t = A + C and d = A C - B^2 of the conic (whose condition number is the
+// covariance's), lambda_max / lambda_min >= k  <=>  t^2 >= d (1 + k)^2 / k.
+constexpr float kElongKappa = 256.0f;
+constexpr float kElongC = (1.0f + kElongKappa) * (1.0f + kElongKappa) / kElongKappa;
+constexpr uint32_t kElongBit = 1u << 4;  // in a staged splat's strip mask word
+
+__device__ __forceinline__ bool elongated(const float* rp) {
+  const float A = rp[2], B = rp[3], C = rp[4];
+  const float t = A + C, d = fmaf(A, C, -(B * B));
+  return t * t >= kElongC * d;
+}
+
 __device__ __forceinline__ uint32_t strip_mask(const int4 d, int tile_y0) {
   uint32_t m = 0;
 #pragma unroll
@@ -54,6 +72,9 @@ struct BlendArgs {
   const S* grad_image;
   const S* grad_alpha;  // 3D: gradient of alpha = 1 - final_T (may be null)
   S* grad_rec;          // [n, 12]
+  // 3D: float64 sums of the conic gradient (A, B, C) of the elongated splats, [n, 4] (may be
+  // null: then every splat takes the float32 sums)
+  double* conic64;
   // pruning scores (3D): scores[g] += sum over pixels of the blending weight alpha T of g
   float* scores;
   // 3D: buckets the backward reads (appended by the forward, consumed by the backward)
@@ -497,6 +518,83 @@ __device__ __forceinline__ void wave_reduce12(const float* v, float& u0, float& 
   u1 += dpp<0x4E>(u1);
 }
 
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double v) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u & 0xffffffffu), CTRL,
+                                                                          0xf, 0xf, false));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, 0xf,
+                                                                          0xf, false));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+__device__ __forceinline__ uint32_t lo32(double v) {
+  return static_cast<uint32_t>(static_cast<uint64_t>(__double_as_longlong(v)) & 0xffffffffu);
+}
+__device__ __forceinline__ uint32_t hi32(double v) {
+  return static_cast<uint32_t>(static_cast<uint64_t>(__double_as_longlong(v)) >> 32);
+}
+__device__ __forceinline__ double f64_of(uint32_t lo, uint32_t hi) {
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// Transposing reduction of 9 per-lane values v[0..7], w over the wavefront (the 3D backward
+// without the |dL/dmean2d| sums): xor 32 with v_permlane32_swap over the pairs (v[i], v[i + 4]),
+// xor 16 with v_permlane16_swap over (s[i], s[i + 2]), xor 8 with DPP row_ror:8 over the last
+// pair, then the 8-lane group sums (half-row mirror, quad xor 1, quad xor 2); w is summed along
+// with each step. On return every lane of group g = lane / 8 holds the total of v[g] in u and
+// the total of w in uw. 26 instructions.
+__device__ __forceinline__ void wave_reduce9(const float* v, float w, float& u, float& uw) {
+  const int lane = threadIdx.x & 63;
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false, false);
+    s[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    w = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float t[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[i]), __float_as_uint(s[i + 2]), false, false);
+    t[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    w = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool b3 = (lane & 8) != 0;
+  u = (b3 ? t[1] : t[0]) + dpp<0x128>(b3 ? t[0] : t[1]);  // row_ror:8 = partner lane ^ 8
+  w += dpp<0x128>(w);
+  u += dpp<0x141>(u);  // row_half_mirror
+  w += dpp<0x141>(w);
+  u += dpp<0xB1>(u);  // quad_perm [1,0,3,2]
+  w += dpp<0xB1>(w);
+  u += dpp<0x4E>(u);  // quad_perm [2,3,0,1]
+  w += dpp<0x4E>(w);
+  uw = w;
+}
+
+// Float64 sum of a per-lane value over the wavefront, in every lane: xor 32 and xor 16 by
+// exchanging each half with itself (v_permlane32_swap / v_permlane16_swap on the two words),
+// then each 16-lane row (row_ror:8, row_half_mirror, quad xor 1, quad xor 2).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  const auto l32 = __builtin_amdgcn_permlane32_swap(lo32(v), lo32(v), false, false);
+  const auto h32 = __builtin_amdgcn_permlane32_swap(hi32(v), hi32(v), false, false);
+  v = f64_of(l32[0], h32[0]) + f64_of(l32[1], h32[1]);
+  const auto l16 = __builtin_amdgcn_permlane16_swap(lo32(v), lo32(v), false, false);
+  const auto h16 = __builtin_amdgcn_permlane16_swap(hi32(v), hi32(v), false, false);
+  v = f64_of(l16[0], h16[0]) + f64_of(l16[1], h16[1]);
+  v += dpp64<0x128>(v);  // row_ror:8
+  v += dpp64<0x141>(v);  // row_half_mirror
+  v += dpp64<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp64<0x4E>(v);   // quad_perm [2,3,0,1]
+  return v;
+}
+
 __device__ __forceinline__ void wave_reduce12(const double* v, double& u0, double& u1) {
   // float64 (2D surfaces): full butterflies, then the float path's placement of the totals
   const int g = (threadIdx.x & 63) >> 3;
@@ -583,7 +681,7 @@ constexpr int kBwdWaves = 4;
 // One bucket b, by one wavefront (whose LDS slots are s_sp, s_m, s_id).
 template <int R, typename S, bool kCount, bool kAbs>
 __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Staged<S>* s_sp, uint32_t* s_m,
-                                           uint32_t* s_id, uint32_t& evals, uint32_t& atomics) {
+                                           uint32_t* s_id, float* s_c, uint32_t& evals, uint32_t& atomics) {
   using Ru = Rule<R, S>;
   constexpr int NV = Ru::kGradVals;
   const int lane = threadIdx.x & 63;
@@ -601,7 +699,13 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     const uint32_t g = a.point_list[r0 + bstart + lane];
     const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
     s_sp[lane] = Ru::stage(rp);
-    if constexpr (Ru::kStrips) s_m[lane] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
+    if constexpr (Ru::kStrips) {
+      uint32_t mk = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
+      if constexpr (R == kRules3D) {
+        if (a.conic64 && elongated(rp)) mk |= kElongBit;
+      }
+      s_m[lane] = mk;
+    }
     s_id[lane] = g;
   }
 
@@ -680,13 +784,21 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     int lim_row[kPixPerLane];
 #pragma unroll
     for (int r = 0; r < kPixPerLane; ++r) lim_row[r] = __builtin_amdgcn_readfirstlane(wave_max(lim[r]));
-    // the final gradient of the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total):
-    // k 0, 1 (mean2d): -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity):
-    // u / o; colour and |dL/dmean2d|: u. The lane-constant parts are chosen once here.
-    const bool k0 = kidx == 0, k1 = kidx == 1, k5 = kidx == 5;
-    const float kc = (kidx == 2 || kidx == 4) ? -0.5f : kidx == 3 ? -1.0f : kidx >= 6 ? 1.0f : 0.0f;
-    const bool live_owner = owner && (kAbs || kidx < 9);
-    const int64_t kofs = kidx;
+    // With |dL/dmean2d| (kAbs) the 12 sums are reduced by wave_reduce12 and the final gradient of
+    // the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total): k 0, 1 (mean2d):
+    // -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity): u / o; colour and
+    // |dL/dmean2d|: u. Without, wave_reduce9 reduces v = (sum h dx, the three conic sums, sum h,
+    // colour) and w = sum h dy, and group g of 8 lanes owns v[g]: group 0 both mean2d values
+    // (lanes 0 and 1: -(A u + B w), -(B u + C w)), groups 1-3 the conic (-u/2, -u, -u/2), group
+    // 4 the opacity (u / o), groups 5-7 the colour (u). The lane-constant parts are chosen here.
+    const bool k0 = kAbs ? kidx == 0 : (grp == 0 && lo == 0);
+    const bool k1 = kAbs ? kidx == 1 : (grp == 0 && lo == 1);
+    const bool k5 = kAbs ? kidx == 5 : grp == 4;
+    const int kslot = kAbs ? kidx : (grp == 0 ? lo : grp + 1);  // the grad2d column
+    const float kc = (kslot == 2 || kslot == 4) ? -0.5f : kslot == 3 ? -1.0f : kslot >= 6 ? 1.0f : 0.0f;
+    const bool live_owner = kAbs ? owner : (grp == 0 ? lo < 2 : lo == 0);
+    const bool conic_owner = kslot >= 2 && kslot <= 4;
+    const int64_t kofs = kslot;
     for (int j = 0; j < jmax; ++j) {
       const Staged<S> sp = s_sp[j];
       const uint32_t m = __builtin_amdgcn_readfirstlane(s_m[j]);  // wave-uniform: scalar tests
@@ -730,14 +842,44 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       }
       if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
       const float dxsh = cl.dx * sh;
-      S acc[12] = {dxsh, shy, cl.dx * dxsh, cl.dx * shy, shyy, sh, cr, cg, cb, ab0, ab1, 0.0f};
-      S u0, u1;
-      wave_reduce12(acc, u0, u1);
+      const float cxx = cl.dx * dxsh, cxy = cl.dx * shy;  // the conic sums of the lane's column
+      const bool wide = (m & kElongBit) != 0u;  // wave-uniform
+      if (wide) {
+        // each lane reads its own three values back after the float32 reduction
+        s_c[lane] = cxx;
+        s_c[kWave + lane] = cxy;
+        s_c[2 * kWave + lane] = shyy;
+      }
       const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : 0.0f;
       const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : 0.0f;
       const float c = k5 ? __builtin_amdgcn_rcpf(sp.o) : kc;
-      const float g = fmaf(c0, u0, fmaf(c1, u1, c * (lo == 0 ? u0 : u1)));
-      if (live_owner) atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kofs, g);
+      float g;
+      if constexpr (kAbs) {
+        S acc[12] = {dxsh, shy, cxx, cxy, shyy, sh, cr, cg, cb, ab0, ab1, 0.0f};
+        S u0, u1;
+        wave_reduce12(acc, u0, u1);
+        g = fmaf(c0, u0, fmaf(c1, u1, c * (lo == 0 ? u0 : u1)));
+      } else {
+        const float v[8] = {dxsh, cxx, cxy, shyy, sh, cr, cg, cb};
+        float u, uw;
+        wave_reduce9(v, shy, u, uw);
+        g = fmaf(c0, u, fmaf(c1, uw, c * u));
+      }
+      // (an elongated splat's conic sums go to the float64 buffer below instead)
+      if (live_owner && !(wide && conic_owner))
+        atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kofs, g);
+      if (wide) {  // the conic sums in float64
+        const int64_t id = __builtin_amdgcn_readfirstlane(s_id[j]);  // wave-uniform
+        // one value at a time (few registers beside the loop's state): A, B, C = -1/2, -1, -1/2
+        // times the sums of dx^2 h, dx dy h, dy^2 h
+#pragma unroll 1
+        for (int k = 0; k < 3; ++k) {
+          const double t = wave_sum_f64(static_cast<double>(s_c[k * kWave + lane]));
+          if (lane == 0) atomic_add_grad(a.conic64 + 4 * id + k, (k == 1 ? -1.0 : -0.5) * t);
+        }
+        // marks the splat's row for the preprocess backward, which then adds the float64 sums
+        if (lane == 0) a.grad_rec[id * kGrad2D + 11] = 1.0f;
+      }
       if constexpr (kCount) atomics += kAbs ? NV : 9;
     }
   } else
@@ -793,30 +935,34 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
 // list's length only reads that length); kList 2, a bounded grid strides over the list (the
 // loop keeps more registers live, so it is used only when the table is much longer).
 template <int R, typename S, bool kCount, bool kAbs = true, int kList = 0>
-__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(BlendArgs<S> a) {
+__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(
+    BlendArgs<S> a) {
   __shared__ Staged<S> s_sp[kBwdWaves][kBucket];
   __shared__ uint32_t s_m[kBwdWaves][kBucket];
   __shared__ uint32_t s_id[kBwdWaves][kBucket];
+  // 3D: an elongated splat's three per-lane conic sums, parked over the float32 reduction
+  __shared__ float s_c[R == kRules3D ? kBwdWaves : 1][3 * kWave];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  float* s_cw = s_c[R == kRules3D ? wave : 0];
   uint32_t evals = 0, atomics = 0;
   if constexpr (kList == 1) {
     // one wavefront per list entry; wavefronts past the list's length leave at once
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
     if (i < static_cast<int64_t>(a.bucket_list[0]))
-      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], evals,
+      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], s_cw, evals,
                                      atomics);
   } else if constexpr (kList == 2) {
     // a bounded grid strides over the list (for bucket tables far longer than the list)
     const int64_t cnt = a.bucket_list[0];
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBwdWaves;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave; i < cnt; i += stride)
-      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], evals,
+      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], s_cw, evals,
                                      atomics);
   } else {
     const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
     if (b < a.n_buckets && !(a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)))
-      bwd_bucket<R, S, kCount, kAbs>(a, b, s_sp[wave], s_m[wave], s_id[wave], evals, atomics);
+      bwd_bucket<R, S, kCount, kAbs>(a, b, s_sp[wave], s_m[wave], s_id[wave], s_cw, evals, atomics);
   }
   if constexpr (kCount) {
     if (lane == 0 && atomics) atomicAdd(a.counters, static_cast<unsigned long long>(atomics));
@@ -1072,15 +1218,18 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
                                int width, int height, const float* image, const float* grad_image,
                                const float* final_T, const float* grad_alpha,
                                const int32_t* n_contrib, const uint32_t* tile_max,
-                               const float* ckpt, uint32_t* bucket_list, float* grad2d, int flags,
-                               unsigned long long* counters, void* stream) {
+                               const float* ckpt, uint32_t* bucket_list, float* grad2d,
+                               double* grad_conic64, int flags, unsigned long long* counters,
+                               void* stream) {
   clear_error();
   GS_REQUIRE(width > 0 && height > 0 && n >= 0 && n_buckets_max >= 0, GS_ERR_ARG,
              "invalid sizes");
   GS_REQUIRE(grad2d || n == 0, GS_ERR_ARG, "null grad2d");
+  GS_REQUIRE(aligned(grad_conic64, 8), GS_ERR_ALIGN, "grad_conic64 must be 8-byte aligned");
   hipStream_t st = as_stream(stream);
   if (!(flags & GS_ACCUMULATE)) {
     fill_zero_f32(grad2d, n * kGrad2D, st);
+    if (grad_conic64) fill_zero_f32(reinterpret_cast<float*>(grad_conic64), n * 8, st);
     if (int e = check_launch("blend_bwd_3d (zero fill)")) return e;
   }
   if (n_buckets_max == 0 || n == 0) return GS_OK;
@@ -1102,6 +1251,7 @@ extern "C" int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges,
   a.grad_image = grad_image;
   a.grad_alpha = grad_alpha;
   a.grad_rec = grad2d;
+  a.conic64 = grad_conic64;
   a.counters = counters;
   GS_REQUIRE(aligned(bucket_list, 16), GS_ERR_ALIGN, "bucket_list must be 16-byte aligned");
   a.bucket_list = bucket_list;

@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     const float* __restrict__ means, const float* __restrict__ log_scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity_logits,
     ShPtr sh, int64_t n, int active, CamK cam, const uint32_t* __restrict__ tiles_touched,
-    const float* __restrict__ grad2d, float* __restrict__ g_means,
+    const float* __restrict__ grad2d, const double* __restrict__ conic64, float* __restrict__ g_means,
     float* __restrict__ g_log_scales, float4* __restrict__ g_quats,
     float* __restrict__ g_opacity, ShOut g_sh) {
   using St = ShStage<K>;
@@ -671,8 +671,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     double gvy = g2[1] * fy * iz;
     double gvz = -(g2[0] * fx * g.vx + g2[1] * fy * g.vy) * iz2;
 
-    // conic (A, B, C) = (c, -b, a) / det  ->  2D covariance (a, b, c)
-    const double gA = g2[2], gB = g2[3], gC = g2[4];
+    // conic (A, B, C) = (c, -b, a) / det  ->  2D covariance (a, b, c); a row marked by the blend
+    // backward (slot 11) also has float64 conic sums (its elongated-splat buckets)
+    double gA = g2[2], gB = g2[3], gC = g2[4];
+    if (conic64 && g2[11] != 0.0f) {
+      gA += conic64[4 * i];
+      gB += conic64[4 * i + 1];
+      gC += conic64[4 * i + 2];
+    }
     const double a = g.a, b = g.b, c = g.c;
     const double det = a * c - b * b;
     const double id2 = 1.0 / (det * det);
@@ -795,11 +801,11 @@ template <int K>
 static void launch_pre_bwd(int64_t blocks, hipStream_t st, const float* means, const float* ls,
                            const float* quats, const float* op, ShPtr sh, int64_t n,
                            int active, const CamK& cam, const uint32_t* touched,
-                           const float* g2, float* gm, float* gls, float* gq, float* gop,
+                           const float* g2, const double* c64, float* gm, float* gls, float* gq, float* gop,
                            ShOut gsh) {
   hipLaunchKernelGGL(preprocess_bwd_kernel<K>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      st, means, ls, reinterpret_cast<const float4*>(quats), op, sh, n, active, cam,
-                     touched, g2, gm, gls,
+                     touched, g2, c64, gm, gls,
                      reinterpret_cast<float4*>(gq), gop, gsh);
 }
 
@@ -844,7 +850,8 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
                                  const float* opacity_logits, const float* sh, const float* sh_rest,
                                  int64_t n, int sh_coeffs, int sh_degree, const gs_camera* cam,
                                  const uint32_t* tiles_touched,
-                                 const float* grad2d, float* grad_means, float* grad_log_scales,
+                                 const float* grad2d, const double* grad_conic64, float* grad_means,
+                                 float* grad_log_scales,
                                  float* grad_quats, float* grad_opacity_logits, float* grad_sh,
                                  float* grad_sh_rest, void* stream) {
   clear_error();
@@ -857,6 +864,7 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
                  grad_sh,
              GS_ERR_ARG, "null pointer argument");
   GS_REQUIRE(!sh_rest == !grad_sh_rest, GS_ERR_ARG, "sh_rest and grad_sh_rest go together");
+  GS_REQUIRE(aligned(grad_conic64, 8), GS_ERR_ALIGN, "grad_conic64 must be 8-byte aligned");
   GS_REQUIRE(!(sh_rest && sh_coeffs == 1), GS_ERR_ARG, "sh_rest given for a DC-only model");
   GS_REQUIRE(aligned(quats, 16) && aligned(grad_quats, 16), GS_ERR_ALIGN,
              "quats and grad_quats must be 16-byte aligned");
@@ -867,10 +875,10 @@ extern "C" int gs_preprocess_bwd(const float* means, const float* log_scales, co
   const ShPtr shp{sh, sh_rest};
   const ShOut gsh{grad_sh, grad_sh_rest};
   switch (sh_coeffs) {
-    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
-    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
-    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
-    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 1: launch_pre_bwd<1>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_conic64, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 4: launch_pre_bwd<4>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_conic64, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    case 9: launch_pre_bwd<9>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_conic64, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
+    default: launch_pre_bwd<16>(blocks, st, means, log_scales, quats, opacity_logits, shp, n, active, k, tiles_touched, grad2d, grad_conic64, grad_means, grad_log_scales, grad_quats, grad_opacity_logits, gsh); break;
   }
   return check_launch("preprocess_bwd");
 }

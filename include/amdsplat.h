@@ -250,6 +250,12 @@ int gs_blend_scores_3d(const float* splat_rec, const uint32_t* ranges, const uin
  * have no blended entry); NULL: every bucket of the table is examined.
  * counters: NULL or 3 device uint64 that receive the atomic adds issued (9 per reduced
  * bucket-splat, 11 with GS_ABS_GRAD) and, in [2], the (pixel, splat) pairs evaluated.
+ * grad_conic64 (may be NULL; 8-byte aligned [n, 4] double, zeroed or accumulated like grad2d):
+ * the conic-gradient sums of the elongated splats in float64. A splat whose 2D covariance has a
+ * condition number of at least 256 (from its record's conic) has its three conic sums reduced and
+ * added over the buckets in float64 into grad_conic64[g, 0..2] instead of grad2d[g, 2..4], and
+ * grad2d[g, 11] set to 1: gs_preprocess_bwd, whose conic -> covariance step divides by det^2,
+ * then takes them unrounded. With NULL every splat takes the float32 sums of grad2d.
  * ------------------------------------------------------------------------------------- */
 enum { GS_ACCUMULATE = 1, GS_ABS_GRAD = 2 };
 int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
@@ -257,8 +263,8 @@ int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32
                     int64_t n_buckets_max, int64_t n, int width, int height, const float* image,
                     const float* grad_image, const float* final_T, const float* grad_alpha,
                     const int32_t* n_contrib, const uint32_t* tile_max, const float* ckpt,
-                    uint32_t* bucket_list, float* grad2d, int flags, unsigned long long* counters,
-                    void* stream);
+                    uint32_t* bucket_list, float* grad2d, double* grad_conic64, int flags,
+                    unsigned long long* counters, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 3D preprocess backward (replaces Faster-GS preprocess_backward_cu, csv:4): chains grad2d
@@ -268,11 +274,14 @@ int gs_blend_bwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32
  *   layout (sh_rest not NULL) grad_sh [n, 1, 3] and grad_sh_rest [n, sh_coeffs - 1, 3].
  *   The colour clamp of the forward is recomputed from the SH rows it reads anyway (the same
  *   operations, so the same bits), so the splat records are not needed.
+ *   grad_conic64 (may be NULL): gs_blend_bwd_3d's float64 conic sums; for a row with grad2d[g, 11]
+ *   set, the conic gradient is grad2d[g, 2..4] + grad_conic64[g, 0..2] (in float64).
  * ------------------------------------------------------------------------------------- */
 int gs_preprocess_bwd(const float* means, const float* log_scales, const float* quats,
                       const float* opacity_logits, const float* sh, const float* sh_rest, int64_t n,
                       int sh_coeffs, int sh_degree, const gs_camera* cam,
-                      const uint32_t* tiles_touched, const float* grad2d, float* grad_means,
+                      const uint32_t* tiles_touched, const float* grad2d, const double* grad_conic64,
+                      float* grad_means,
                       float* grad_log_scales, float* grad_quats, float* grad_opacity_logits,
                       float* grad_sh, float* grad_sh_rest, void* stream);
 

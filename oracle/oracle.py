@@ -108,18 +108,22 @@ def blend_fwd(rec, point_list, ranges, boff, width, height, bg=(0.0, 0.0, 0.0), 
 
 
 def blend_bwd(rec, point_list, ranges, boff, width, height, image, grad_image, final_T, n_contrib, tile_max,
-              ckpt, n, grad_alpha=None):
+              ckpt, n, grad_alpha=None, conic64=False):
+    """grad2d [n, 12] float32; with conic64=True also the conic-gradient sums (columns 2-4)
+    unrounded, float64 [n, 4]: returns (grad2d, conic64)."""
     grad2d = np.zeros((n, 12), np.float32)
+    c64 = np.zeros((n, 4), np.float64) if conic64 else None
     lib().or_blend_bwd(_p(f32(rec)), _p(np.ascontiguousarray(ranges, np.uint32)),
                        _p(np.ascontiguousarray(point_list, np.uint32)), _p(np.ascontiguousarray(boff, np.uint32)),
                        C.c_int(width), C.c_int(height), _p(f32(image)), _p(f32(grad_image)), _p(f32(final_T)),
                        _p(None if grad_alpha is None else f32(grad_alpha)),
                        _p(np.ascontiguousarray(n_contrib, np.int32)), _p(np.ascontiguousarray(tile_max, np.uint32)),
-                       _p(f32(ckpt)), C.c_int64(n), _p(grad2d))
-    return grad2d
+                       _p(f32(ckpt)), C.c_int64(n), _p(grad2d), _p(c64))
+    return (grad2d, c64) if conic64 else grad2d
 
 
-def preprocess_bwd(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, rec, touched, grad2d):
+def preprocess_bwd(means, log_scales, quats, opacity_logits, sh, cam, sh_degree, rec, touched, grad2d, conic64=None):
+    """conic64: None, or float64 [n, 4] conic-gradient sums that replace grad2d's columns 2-4."""
     means, log_scales, quats, opacity_logits, sh = map(f32, (means, log_scales, quats, opacity_logits, sh))
     n, K = means.shape[0], sh.shape[1]
     gm = np.zeros((n, 3), np.float32)
@@ -129,7 +133,8 @@ def preprocess_bwd(means, log_scales, quats, opacity_logits, sh, cam, sh_degree,
     gsh = np.zeros((n, K, 3), np.float32)
     lib().or_preprocess_bwd(_p(means), _p(log_scales), _p(quats), _p(opacity_logits), _p(sh), C.c_int64(n),
                             C.c_int(K), C.c_int(sh_degree), C.byref(camera(cam)), _p(f32(rec)),
-                            _p(np.ascontiguousarray(touched, np.uint32)), _p(f32(grad2d)), _p(gm), _p(gls),
+                            _p(np.ascontiguousarray(touched, np.uint32)), _p(f32(grad2d)),
+                            _p(None if conic64 is None else np.ascontiguousarray(conic64, np.float64)), _p(gm), _p(gls),
                             _p(gq), _p(gop), _p(gsh))
     return gm, gls, gq, gop, gsh
 

@@ -625,12 +625,13 @@ int or_contrib_mask(const float* rec, const uint32_t* ranges, const uint32_t* po
 }
 
 /* Bucketed backward in double, replaying each bucket from its checkpoint.
- * grad2d [n,12] is overwritten. */
+ * grad2d [n,12] is overwritten (the double sums rounded to float); conic64 [n,4] (may be NULL)
+ * receives the conic-gradient sums (columns 2-4) unrounded. */
 int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point_list,
                  const uint32_t* bucket_offsets, int W, int H, const float* image,
                  const float* grad_image, const float* final_T, const float* grad_alpha,
                  const int32_t* n_contrib, const uint32_t* tile_max, const float* ckpt, int64_t n,
-                 float* grad2d) {
+                 float* grad2d, double* conic64) {
   int tiles_x = (W + TILE - 1) / TILE, tiles_y = (H + TILE - 1) / TILE;
   int64_t HW = (int64_t)W * H;
   double* acc = (double*)calloc((size_t)n * 12, sizeof(double));
@@ -700,6 +701,11 @@ int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point
     }
   }
   for (int64_t i = 0; i < n * 12; ++i) grad2d[i] = (float)acc[i];
+  if (conic64)
+    for (int64_t i = 0; i < n; ++i) {
+      for (int k = 0; k < 3; ++k) conic64[4 * i + k] = acc[12 * i + 2 + k];
+      conic64[4 * i + 3] = 0.0;
+    }
   free(acc);
   return 0;
 }
@@ -707,8 +713,9 @@ int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point
 /* ---- preprocess backward (double arithmetic on the float32 forward quantities) ---- */
 int or_preprocess_bwd(const float* means, const float* ls, const float* quats, const float* op,
                       const float* sh, int64_t n, int K, int sh_degree, const or_camera* camera,
-                      const float* rec, const uint32_t* touched, const float* grad2d, float* g_means,
-                      float* g_ls, float* g_quats, float* g_op, float* g_sh) {
+                      const float* rec, const uint32_t* touched, const float* grad2d,
+                      const double* conic64, float* g_means, float* g_ls, float* g_quats, float* g_op,
+                      float* g_sh) {
   Cam cam = make_cam(camera);
   int active = (sh_degree + 1) * (sh_degree + 1);
 #pragma omp parallel for schedule(static)
@@ -752,7 +759,13 @@ int or_preprocess_bwd(const float* means, const float* ls, const float* quats, c
     double gvx = g2[0] * (double)cam.fx * iz, gvy = g2[1] * (double)cam.fy * iz;
     double gvz = -((double)g2[0] * cam.fx * g.vx + (double)g2[1] * cam.fy * g.vy) * iz * iz;
     double a = g.a, b = g.b, c = g.c, det = a * c - b * b;
+    /* the conic gradient: grad2d's float columns, or conic64's unrounded sums when given */
     double gA = g2[2], gB = g2[3], gC = g2[4], id2 = 1.0 / (det * det);
+    if (conic64) {
+      gA = conic64[4 * i];
+      gB = conic64[4 * i + 1];
+      gC = conic64[4 * i + 2];
+    }
     double ga = (-c * c * gA + b * c * gB - b * b * gC) * id2;
     double gbb = (2 * b * c * gA - (a * c + b * b) * gB + 2 * a * b * gC) * id2;
     double gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;

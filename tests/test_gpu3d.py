@@ -241,10 +241,14 @@ def test_grad2d_matches_oracle_replay():
     gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(3))
     g2 = R.backward_pass(fs, *p, gi.cuda())[5]
     ref = O.render(*[t.numpy() for t in sc.params()], cam, 3, bg=BG)
-    o2 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
-                     ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"],
-                     sc.n)
-    g2 = np_(g2)
+    o2, oc = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
+                         ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"],
+                         sc.n, conic64=True)
+    # the conic columns as both sides sum them: the GPU's float32 and float64 (elongated splats)
+    # sums, the oracle's float64 sums
+    o2 = o2.astype(np.float64)
+    o2[:, 2:5] = oc[:, :3]
+    g2 = np_(R.combined_grad2d(g2, fs.last_conic64))
     for k, name in enumerate(["mx", "my", "A", "B", "C", "opacity", "r", "g", "b", "|mx|", "|my|"]):
         e = D.rel_err(g2[:, k], o2[:, k])
         assert e < 1e-5, f"grad2d {name}: {e:.2e}"
@@ -569,8 +573,9 @@ def test_backward_over_long_bucket_table_equals_table_walk():
     fs = R.forward_pass(*p, cam, sh_degree=3)
     assert fs.n_buckets_max > 4 * 65536 * 4  # the striding launch
     gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(6)).cuda()
-    listed = R.backward_pass(fs, *p, gi)[5]
-    table = R.backward_pass(dataclasses.replace(fs, bucket_list=None), *p, gi)[5]
+    listed = R.combined_grad2d(R.backward_pass(fs, *p, gi)[5], fs.last_conic64)
+    fs_table = dataclasses.replace(fs, bucket_list=None)
+    table = R.combined_grad2d(R.backward_pass(fs_table, *p, gi)[5], fs_table.last_conic64)
     torch.cuda.synchronize()
     # the screen-space gradients (what the bucket walk produces); the preprocess backward maps
     # them deterministically, amplifying atomic-order rounding where its terms cancel
@@ -625,9 +630,10 @@ def test_full_size_100k_sh0_matches_oracle():
     img, alpha, _ = R.rasterize(*p, cam.viewmat, K, cam.width, cam.height, near=cam.near, far=cam.far)
     gi = torch.randn(img.shape, generator=torch.Generator().manual_seed(2))
     (img * gi.cuda()).sum().backward()
-    g2 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
-                     ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"], sc.n)
-    want = O.preprocess_bwd(*host, cam, 0, ref["rec"], ref["touched"], g2)
+    g2, c64 = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
+                          ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"],
+                          sc.n, conic64=True)
+    want = O.preprocess_bwd(*host, cam, 0, ref["rec"], ref["touched"], g2, conic64=c64)
     for k, (got, w) in enumerate(zip(p, want)):
         assert D.rel_err(np_(got.grad).reshape(w.shape), w) < GRAD_TOL, k
 
