@@ -578,23 +578,6 @@ __device__ __forceinline__ void wave_reduce9(const float* v, float w, float& u, 
   uw = w;
 }
 
-// Float64 sum of a per-lane value over the wavefront, in every lane: xor 32 and xor 16 by
-// exchanging each half with itself (v_permlane32_swap / v_permlane16_swap on the two words),
-// then each 16-lane row (row_ror:8, row_half_mirror, quad xor 1, quad xor 2).
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  const auto l32 = __builtin_amdgcn_permlane32_swap(lo32(v), lo32(v), false, false);
-  const auto h32 = __builtin_amdgcn_permlane32_swap(hi32(v), hi32(v), false, false);
-  v = f64_of(l32[0], h32[0]) + f64_of(l32[1], h32[1]);
-  const auto l16 = __builtin_amdgcn_permlane16_swap(lo32(v), lo32(v), false, false);
-  const auto h16 = __builtin_amdgcn_permlane16_swap(hi32(v), hi32(v), false, false);
-  v = f64_of(l16[0], h16[0]) + f64_of(l16[1], h16[1]);
-  v += dpp64<0x128>(v);  // row_ror:8
-  v += dpp64<0x141>(v);  // row_half_mirror
-  v += dpp64<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp64<0x4E>(v);   // quad_perm [2,3,0,1]
-  return v;
-}
-
 __device__ __forceinline__ void wave_reduce12(const double* v, double& u0, double& u1) {
   // float64 (2D surfaces): full butterflies, then the float path's placement of the totals
   const int g = (threadIdx.x & 63) >> 3;
@@ -870,15 +853,27 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
         atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kofs, g);
       if (wide) {  // the conic sums in float64
         const int64_t id = __builtin_amdgcn_readfirstlane(s_id[j]);  // wave-uniform
-        // one value at a time (few registers beside the loop's state): A, B, C = -1/2, -1, -1/2
-        // times the sums of dx^2 h, dx dy h, dy^2 h
-#pragma unroll 1
-        for (int k = 0; k < 3; ++k) {
-          const double t = wave_sum_f64(static_cast<double>(s_c[k * kWave + lane]));
-          if (lane == 0) atomic_add_grad(a.conic64 + 4 * id + k, (k == 1 ? -1.0 : -0.5) * t);
+        wave_sync();  // every lane's parked values
+        // row k of 16 lanes (k < 3) sums value k of the 64 lanes: 4 values per lane in float64
+        // (exactly), then the row's 16 partial sums; A, B, C = -1/2, -1, -1/2 times the sums of
+        // dx^2 h, dx dy h, dy^2 h
+        int ln = lane;
+        asm volatile("" : "+v"(ln));  // formed here, not kept in registers over the whole loop
+        const int k = ln >> 4, r16 = ln & 15;
+        double t = 0.0;
+        if (k < 3) {
+          const float* v = s_c + k * kWave + r16;
+          t = (static_cast<double>(v[0]) + static_cast<double>(v[16])) +
+              (static_cast<double>(v[32]) + static_cast<double>(v[48]));
         }
+        t += dpp64<0x128>(t);  // row_ror:8
+        t += dpp64<0x141>(t);  // row_half_mirror
+        t += dpp64<0xB1>(t);   // quad_perm [1,0,3,2]
+        t += dpp64<0x4E>(t);   // quad_perm [2,3,0,1]
+        if (r16 == 0 && k < 3) atomic_add_grad(a.conic64 + 4 * id + k, (k == 1 ? -1.0 : -0.5) * t);
         // marks the splat's row for the preprocess backward, which then adds the float64 sums
-        if (lane == 0) a.grad_rec[id * kGrad2D + 11] = 1.0f;
+        if (lane == 48) a.grad_rec[id * kGrad2D + 11] = 1.0f;
+        wave_sync();  // the parked values are read before the next splat parks its own
       }
       if constexpr (kCount) atomics += kAbs ? NV : 9;
     }
