@@ -575,6 +575,9 @@ __device__ __forceinline__ void wave_reduce9(const float* v, float w, float& u, 
   w += dpp<0xB1>(w);
   u += dpp<0x4E>(u);  // quad_perm [2,3,0,1]
   w += dpp<0x4E>(w);
+  // (the totals are formed here, with every lane active, so that the DPP moves fold into the
+  // adds rather than the adds sinking into the owners' branch)
+  asm volatile("" : "+v"(u), "+v"(w));
   uw = w;
 }
 
@@ -749,7 +752,8 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       }
     }
   }
-  const int jmax = min(bsize, wave_max(lim_max));
+  // (scalar: the splat loop is uniform over the wavefront)
+  const int jmax = __builtin_amdgcn_readfirstlane(min(bsize, wave_max(lim_max)));
   wave_sync();
 
   // value index k owned by this lane after wave_reduce12 (lo = 0 or 1 within the 8-lane group)
@@ -791,7 +795,11 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       // zero to its last update, instead of being re-zeroed on every path that skips a pixel
       float sh = opaque_zero(), shy = opaque_zero(), shyy = opaque_zero();
       float cr = opaque_zero(), cg = opaque_zero(), cb = opaque_zero();
-      float ab0 = opaque_zero(), ab1 = opaque_zero();
+      float ab0 = 0.0f, ab1 = 0.0f;
+      if constexpr (kAbs) {
+        ab0 = opaque_zero();
+        ab1 = opaque_zero();
+      }
       bool used = false;
 #pragma unroll
       for (int r = 0; r < kPixPerLane; ++r) {
