@@ -773,16 +773,18 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     for (int r = 0; r < kPixPerLane; ++r) lim_row[r] = __builtin_amdgcn_readfirstlane(wave_max(lim[r]));
     // With |dL/dmean2d| (kAbs) the 12 sums are reduced by wave_reduce12 and the final gradient of
     // the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total): k 0, 1 (mean2d):
-    // -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity): u / o; colour and
+    // -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity): u; colour and
     // |dL/dmean2d|: u. Without, wave_reduce9 reduces v = (sum h dx, the three conic sums, sum h,
     // colour) and w = sum h dy, and group g of 8 lanes owns v[g]: group 0 both mean2d values
     // (lanes 0 and 1: -(A u + B w), -(B u + C w)), groups 1-3 the conic (-u/2, -u, -u/2), group
-    // 4 the opacity (u / o), groups 5-7 the colour (u). The lane-constant parts are chosen here.
+    // 4 the opacity and groups 5-7 the colour (u). The opacity column holds sum h = sum alpha
+    // dL/dalpha = opacity dL/dopacity: the preprocess backward divides by the opacity once per
+    // Gaussian (in float64) instead of every bucket-splat step here. The lane-constant parts are
+    // chosen here.
     const bool k0 = kAbs ? kidx == 0 : (grp == 0 && lo == 0);
     const bool k1 = kAbs ? kidx == 1 : (grp == 0 && lo == 1);
-    const bool k5 = kAbs ? kidx == 5 : grp == 4;
     const int kslot = kAbs ? kidx : (grp == 0 ? lo : grp + 1);  // the grad2d column
-    const float kc = (kslot == 2 || kslot == 4) ? -0.5f : kslot == 3 ? -1.0f : kslot >= 6 ? 1.0f : 0.0f;
+    const float kc = (kslot == 2 || kslot == 4) ? -0.5f : kslot == 3 ? -1.0f : kslot >= 5 ? 1.0f : 0.0f;
     const bool live_owner = kAbs ? owner : (grp == 0 ? lo < 2 : lo == 0);
     const bool conic_owner = kslot >= 2 && kslot <= 4;
     const int64_t kofs = kslot;
@@ -843,7 +845,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       }
       const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : 0.0f;
       const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : 0.0f;
-      const float c = k5 ? __builtin_amdgcn_rcpf(sp.o) : kc;
+      const float c = kc;
       float g;
       if constexpr (kAbs) {
         S acc[12] = {dxsh, shy, cxx, cxy, shyy, sh, cr, cg, cb, ab0, ab1, 0.0f};

@@ -661,8 +661,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     Geom g;
     compute_geom(means, log_scales, quats, opacity_logits, i, cam, g);
     const bool aa = cam.flags & GS_CAM_PROPER_ANTIALIASING;
-    gop = aa ? static_cast<float>(static_cast<double>(g2[5]) * g.rho * g.os * (1.0 - g.os))
-             : static_cast<float>(static_cast<double>(g2[5]) * g.o * (1.0 - g.o));
+    // grad2d[5] = sum alpha dL/dalpha = o dL/do for the blended opacity o (= os rho under proper
+    // antialiasing); with o = sigmoid(logit) rho: dL/dlogit = dL/do rho os (1 - os) = g2[5] (1 - os)
+    gop = static_cast<float>(static_cast<double>(g2[5]) * (1.0 - (aa ? g.os : g.o)));
 
     // mean2d = (fx vx/vz + cx, fy vy/vz + cy)
     const double fx = cam.fx, fy = cam.fy;
@@ -691,7 +692,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       // d(rho^2)/dc = (ar - rho^2 a) / det, d(rho^2)/db = -2 b (1 - rho^2) / det
       const double ar = g.ar, cr = g.cr;
       const double ratio = (ar * cr - b * b) / det;
-      const double k = static_cast<double>(g2[5]) * g.os / (2.0 * sqrt(ratio) * det);
+      // dL/drho = dL/do os = g2[5] / rho, d rho = d ratio / (2 rho)
+      const double k = static_cast<double>(g2[5]) / (2.0 * static_cast<double>(g.rho) * sqrt(ratio) * det);
       ga += k * (cr - ratio * c);
       gc += k * (ar - ratio * a);
       gbb += -2.0 * k * b * (1.0 - ratio);

@@ -240,7 +240,8 @@ int gs_blend_scores_3d(const float* splat_rec, const uint32_t* ranges, const uin
 /* ---------------------------------------------------------------------------------------
  * 3D bucketed blend backward (replaces blend_backward_cu / blend_backward_macro_cu,
  * phase1/fastergs_macro.patch:40-314). One wavefront per bucket; grad2d [n,12] receives
- * dL/d(mean2d, conic A B C, opacity, colour) and, with GS_ABS_GRAD in flags, |dL/dmean2d|
+ * dL/d(mean2d, conic A B C), opacity x dL/dopacity (sum over pixels of alpha dL/dalpha; the
+ * preprocess backward divides by the opacity), dL/dcolour and, with GS_ABS_GRAD in flags, |dL/dmean2d|
  * (slots 9-10; Faster-GS's compute_abs_grad instantiation, phase1/fastergs_macro.patch:206-209).
  * It is zeroed by the call unless flags has GS_ACCUMULATE (then the call adds to it, e.g. over
  * views).

@@ -678,7 +678,7 @@ int or_blend_bwd(const float* rec, const uint32_t* ranges, const uint32_t* point
           rho -= w * dot;
           float oma = 1.0f - alpha;
           double dLda = (double)T * dot - rho / (double)fmaxf(oma, OMA_EPS);
-          a[5] += (double)Gs * dLda;
+          a[5] += (double)alpha * dLda; /* opacity times dL/dopacity (sum alpha dL/dalpha) */
           double hp = (double)alpha * dLda;
           a[2] += -0.5 * hp * dx * dx;
           a[3] += -hp * dx * dy;
@@ -753,8 +753,8 @@ int or_preprocess_bwd(const float* means, const float* ls, const float* quats, c
     Geom g;
     geom(means, ls, quats, op, i, &cam, &g);
     int aa = cam.flags & CAM_PROPER_ANTIALIASING;
-    g_op[i] = aa ? (float)((double)g2[5] * g.rho * g.os * (1.0 - g.os))
-                 : (float)((double)g2[5] * g.o * (1.0 - g.o));
+    /* g2[5] = o dL/do for the blended opacity o = os rho: dL/dlogit = g2[5] (1 - os) */
+    g_op[i] = (float)((double)g2[5] * (1.0 - (aa ? g.os : g.o)));
     double iz = 1.0 / g.vz;
     double gvx = g2[0] * (double)cam.fx * iz, gvy = g2[1] * (double)cam.fy * iz;
     double gvz = -((double)g2[0] * cam.fx * g.vx + (double)g2[1] * cam.fy * g.vy) * iz * iz;
@@ -771,7 +771,7 @@ int or_preprocess_bwd(const float* means, const float* ls, const float* quats, c
     double gc = (-b * b * gA + a * b * gB - a * a * gC) * id2;
     if (aa) { /* d/d(a, b, c) of rho = sqrt((ar cr - b^2) / (a c - b^2)), ar = a - 0.3, cr = c - 0.3 */
       double ar = g.ar, cr = g.cr, ratio = (ar * cr - b * b) / det, rho = sqrt(ratio);
-      double k = (double)g2[5] * g.os / (2.0 * rho * det);
+      double k = (double)g2[5] / (2.0 * (double)g.rho * rho * det);
       ga += k * (cr - ratio * c);
       gc += k * (ar - ratio * a);
       gbb += -2.0 * k * b * (1.0 - ratio);

@@ -598,7 +598,9 @@ def test_blend_backward_replay_matches_autograd():
                      ref["image"], gi.float().numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"],
                      ref["ckpt"], sc.n, grad_alpha=ga.float().numpy())
     vis = ref["touched"] > 0
-    for cols, t in (((0, 1), m2.grad), ((2, 3, 4), con.grad), ((5,), op.grad[:, None]), ((6, 7, 8), col.grad)):
+    # (the opacity column holds opacity times dL/dopacity)
+    for cols, t in (((0, 1), m2.grad), ((2, 3, 4), con.grad), ((5,), (op.grad * op.detach())[:, None]),
+                    ((6, 7, 8), col.grad)):
         a = g2[vis][:, list(cols)]
         b = t.numpy()[vis]
         assert D.rel_err(a, b) < 2e-5, (cols, D.rel_err(a, b))
@@ -618,8 +620,11 @@ def test_preprocess_backward_matches_autograd(aa):
     pre = D.preprocess64(*P, cam, 3)
     g2t = torch.tensor(g2, dtype=torch.float64) * torch.tensor(vis, dtype=torch.float64)[:, None]
     # clamped colour channels carry no gradient: preprocess64 clamps with torch.clamp as well
+    # (g2's opacity column is opacity times dL/dopacity)
+    o_det = pre["opacity"].detach()
     loss = ((pre["mean2d"] * g2t[:, 0:2]).sum() + (pre["conic"] * g2t[:, 2:5]).sum()
-            + (pre["opacity"] * g2t[:, 5]).sum() + (pre["color"] * g2t[:, 6:9]).sum())
+            + (pre["opacity"] * g2t[:, 5] / torch.where(o_det > 0, o_det, 1.0)).sum()
+            + (pre["color"] * g2t[:, 6:9]).sum())
     loss.backward()
     for name, a, t in (("means", gm, P[0]), ("log_scales", gls, P[1]), ("quats", gq, P[2]),
                        ("opacity", gop, P[3]), ("sh", gsh, P[4])):
