@@ -187,8 +187,9 @@ def stage_bytes(fs, n_visible, active_buckets, splat_steps, used_pairs, staged, 
         "binning": binning,
         # per staged list entry: id + 64 B record; per pixel: image 12 + final T 4 + n_contrib 4;
         # the checkpoints written (4 KiB per bucket reached); tile max, bucket_to_tile, and the
-        # backward's screen-space gradient buffer the forward zeroes (48 B per Gaussian)
-        "blend_fwd": staged * (4 + 64) + P * 20 + ckpt_written * 4096 + 4 * T + 4 * B + 48 * n,
+        # backward's screen-space gradient buffer the forward zeroes (48 B of float32 sums and
+        # 32 B of float64 conic sums per Gaussian)
+        "blend_fwd": staged * (4 + 64) + P * 20 + ckpt_written * 4096 + 4 * T + 4 * B + 80 * n,
         # per active bucket: checkpoints 4 KiB + grad image 12, image 12, n_contrib 4 per pixel;
         # per bucket-splat step: id + record; per reduced bucket-splat: 9 fp32 atomics (11 with
         # the |dL/dmean2d| sums)
