@@ -48,6 +48,51 @@ __device__ __forceinline__ uint32_t strip_mask(const int4 d, int tile_y0) {
   return m;
 }
 
+// The strips of ymask (bits s0 ..: strips inside a 3D splat's pixel y-bounds) whose pixels the
+// splat's alpha >= 1/255 ellipse can reach, for the tile whose first pixel column is tile_x0.
+// With u = row - mean y, the ellipse A v^2 + 2 B u v + C u^2 <= 2 thr (v = column - mean x,
+// thr = ln(255 o) from the record) spans columns v in [(-B u - sqrt(q - det u^2)) / A,
+// (-B u + sqrt(q - det u^2)) / A], q = 2 thr A, det = A C - B^2, for |u| <= sqrt(q / det). Over a
+// strip's pixel-centre rows the right edge is concave in u, largest at u* = -B sqrt(2 thr /
+// (C det)) clamped to the strip, the left edge convex, smallest at -u*; a strip is kept when that
+// extent reaches the tile's pixel-centre columns. The extent is widened by 0.05 px + 1e-3 of its
+// half-width, far above the error of the approximate reciprocals and square roots here and of
+// the blends' own float32 evaluation of the boundary (the hardware exp2 included), so a strip is
+// dropped only where every pixel has alpha < 1/255: the blends' results do not change. Splats
+// with a condition number above about 4096 keep ymask (det then loses too many bits).
+// Evaluated for the strips in `want` only (a forward wavefront needs its own strip).
+__device__ __forceinline__ uint32_t strip_mask_band(const float* rp, int tile_x0, int tile_y0, uint32_t ymask,
+                                                    uint32_t want = 0xfu) {
+  ymask &= want;
+  const float mx = rp[0], my = rp[1], A = rp[2], B = rp[3], C = rp[4], thr = rp[7];
+  const float det = fmaf(A, C, -(B * B));
+  const float t = A + C;
+  if (ymask == 0u || !(det > 0.0f) || !(A > 0.0f) || !(C > 0.0f) || !(thr > 0.0f) || t * t >= 4096.0f * det)
+    return ymask;
+  const float q = (thr + thr) * A;
+  const float idet = __builtin_amdgcn_rcpf(det);
+  const float umax = fmaf(__builtin_amdgcn_sqrtf(q * idet), 1.001f, 0.05f);
+  const float us = -B * __builtin_amdgcn_sqrtf((thr + thr) * __builtin_amdgcn_rcpf(C) * idet);
+  const float iA = __builtin_amdgcn_rcpf(A);
+  const float c0 = (static_cast<float>(tile_x0) + 0.5f) - mx;  // the tile's columns, from the mean
+  const float c1 = c0 + static_cast<float>(kTile - 1);
+  uint32_t m = 0;
+#pragma unroll
+  for (int s = 0; s < kStrips; ++s) {
+    if (((ymask >> s) & 1u) == 0u) continue;
+    const float ya = (static_cast<float>(tile_y0 + kStripRows * s) + 0.5f) - my;
+    const float ua = fmaxf(ya, -umax), ub = fminf(ya + static_cast<float>(kStripRows - 1), umax);
+    if (ua > ub) continue;
+    const float ur = fminf(fmaxf(us, ua), ub), ul = fminf(fmaxf(-us, ua), ub);
+    const float sr = __builtin_amdgcn_sqrtf(fmaxf(fmaf(-det * ur, ur, q), 0.0f));
+    const float sl = __builtin_amdgcn_sqrtf(fmaxf(fmaf(-det * ul, ul, q), 0.0f));
+    const float fr = fmaf(-B, ur, sr) * iA, fl = fmaf(-B, ul, -sl) * iA;
+    const float mg = fmaf(1e-3f, fmaxf(fabsf(fr), fabsf(fl)), 0.05f);
+    if (fr + mg >= c0 && fl - mg <= c1) m |= 1u << s;
+  }
+  return m;
+}
+
 template <typename S>
 struct BlendArgs {
   const S* rec;                    // [n, 16]
@@ -209,7 +254,8 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
       const uint32_t g = a.point_list[r0 + j];
       const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
       s_sp[t] = Ru::stage(rp);
-      if constexpr (Ru::kStrips) s_mask[t] = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
+      if constexpr (Ru::kStrips)
+        s_mask[t] = strip_mask_band(rp, tx * kTile, ty * kTile, strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile));
       if constexpr (kScore) {
         s_gid[t] = g;
         s_score[t] = 0.0f;
@@ -390,7 +436,8 @@ __global__ __launch_bounds__(4 * kWave) void blend_fwd_strip_kernel(BlendArgs<fl
     if (j < len) {
       const float* rp = a.rec + static_cast<int64_t>(a.point_list[r0 + j]) * kRecFloats;
       sw[lane] = Ru::stage(rp);
-      sm = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile) >> (sub * P);
+      sm = strip_mask_band(rp, tx * kTile, ty * kTile, strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile),
+                           ((1u << P) - 1u) << (sub * P)) >> (sub * P);
     }
     // staged entries reaching pixel r of every lane, as 64-bit masks
     uint64_t wm[P];
@@ -688,6 +735,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     if constexpr (Ru::kStrips) {
       uint32_t mk = strip_mask(reinterpret_cast<const int4*>(rp)[3], ty * kTile);
       if constexpr (R == kRules3D) {
+        mk = strip_mask_band(rp, tx * kTile, ty * kTile, mk);
         if (a.conic64 && elongated(rp)) mk |= kElongBit;
       }
       s_m[lane] = mk;
