@@ -166,15 +166,33 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+// Maximum over the wavefront of a non-negative int, every lane active: DPP within the rows of 16
+// (quad swaps, half-row and row mirrors), then the rows exchanged with v_permlane16_swap and
+// v_permlane32_swap (8 instructions instead of 6 LDS-routed shuffle rounds).
 __device__ __forceinline__ int wave_max(int v) {
-  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-  return v;
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xf, 0xf, false));  // row_mirror
+  const auto a = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+  v = max(static_cast<int>(a[0]), static_cast<int>(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+  return max(static_cast<int>(b[0]), static_cast<int>(b[1]));
 }
 
 __device__ __forceinline__ float opaque_zero() {
   float z;
   asm volatile("v_mov_b32 %0, 0" : "=v"(z));
   return z;
+}
+
+// Two such zeros from one 64-bit move (in a register pair).
+__device__ __forceinline__ void opaque_zero2(float& a, float& b) {
+  double z;
+  asm volatile("v_mov_b64 %0, 0" : "=v"(z));
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(z));
+  a = __uint_as_float(static_cast<uint32_t>(u));
+  b = __uint_as_float(static_cast<uint32_t>(u >> 32));
 }
 
 // An integer zero in a vector register: an LDS address offset by it is computed once into a
@@ -728,6 +746,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
   if (bsize <= 0) return;
   const int tx = static_cast<int>(tile) % a.tiles_x, ty = static_cast<int>(tile) / a.tiles_x;
 
+  uint32_t mk_lane = 0;  // the strip mask of this lane's staged splat (3D)
   if (lane < bsize) {
     const uint32_t g = a.point_list[r0 + bstart + lane];
     const S* rp = a.rec + static_cast<int64_t>(g) * kRecFloats;
@@ -737,8 +756,10 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       if constexpr (R == kRules3D) {
         mk = strip_mask_band(rp, tx * kTile, ty * kTile, mk);
         if (a.conic64 && elongated(rp)) mk |= kElongBit;
+        mk_lane = mk;
+      } else {
+        s_m[lane] = mk;
       }
-      s_m[lane] = mk;
     }
     s_id[lane] = g;
   }
@@ -819,6 +840,12 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     int lim_row[kPixPerLane];
 #pragma unroll
     for (int r = 0; r < kPixPerLane; ++r) lim_row[r] = __builtin_amdgcn_readfirstlane(wave_max(lim[r]));
+    // the staged splats' strip bits and elongation bit as scalar bit planes (bit j: splat j), so
+    // the per-splat tests below are scalar bit tests with no LDS read
+    uint64_t plane[kPixPerLane + 1];
+#pragma unroll
+    for (int r = 0; r < kPixPerLane; ++r) plane[r] = __ballot(((mk_lane >> r) & 1u) ? 1 : 0);
+    plane[kPixPerLane] = __ballot((mk_lane & kElongBit) ? 1 : 0);
     // With |dL/dmean2d| (kAbs) the 12 sums are reduced by wave_reduce12 and the final gradient of
     // the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total): k 0, 1 (mean2d):
     // -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity): u; colour and
@@ -838,13 +865,14 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     const int64_t kofs = kslot;
     for (int j = 0; j < jmax; ++j) {
       const Staged<S> sp = s_sp[j];
-      const uint32_t m = __builtin_amdgcn_readfirstlane(s_m[j]);  // wave-uniform: scalar tests
       const typename Ru::Col cl = Ru::col(sp, pxf);
       const float n0dx = sp.n0 * cl.dx, n1dx = sp.n1 * cl.dx;
       // zeros the compiler cannot see through: each sum then lives in one register from its
       // zero to its last update, instead of being re-zeroed on every path that skips a pixel
-      float sh = opaque_zero(), shy = opaque_zero(), shyy = opaque_zero();
-      float cr = opaque_zero(), cg = opaque_zero(), cb = opaque_zero();
+      float sh, shy, shyy, cr, cg, cb;
+      opaque_zero2(sh, shy);
+      opaque_zero2(shyy, cr);
+      opaque_zero2(cg, cb);
       float ab0 = 0.0f, ab1 = 0.0f;
       if constexpr (kAbs) {
         ab0 = opaque_zero();
@@ -853,7 +881,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       bool used = false;
 #pragma unroll
       for (int r = 0; r < kPixPerLane; ++r) {
-        if (((m >> r) & 1u) == 0u || j >= lim_row[r]) continue;  // wave-uniform
+        if (((plane[r] >> j) & 1u) == 0u || j >= lim_row[r]) continue;  // wave-uniform
         const bool live = j < lim[r];
         if constexpr (kCount) evals += live ? 1u : 0u;
         const float dy = sp.my - pyf[r];
@@ -884,7 +912,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
       const float dxsh = cl.dx * sh;
       const float cxx = cl.dx * dxsh, cxy = cl.dx * shy;  // the conic sums of the lane's column
-      const bool wide = (m & kElongBit) != 0u;  // wave-uniform
+      const bool wide = ((plane[kPixPerLane] >> j) & 1u) != 0u;  // wave-uniform
       if (wide) {
         // each lane reads its own three values back after the float32 reduction
         s_c[lane] = cxx;
