@@ -72,6 +72,8 @@ _SIGS = {
     "gs_scan_workspace_size": (_sz, [_i64]),
     "gs_scan_u32": (_i32, [_vp, _vp, _i64, _vp, _sz, _vp]),
     "gs_sum_u32": (_i32, [_vp, _i64, _vp, _vp]),
+    "gs_count_begin": (_i32, [_vp, _i64, _i32, _vp]),
+    "gs_count_end": (_i32, [C.POINTER(C.c_uint64)]),
     "gs_preprocess_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, C.POINTER(GsCamera), _vp, _vp,
                                  _vp, _vp, _vp]),
     "gs_bin_prepare_workspace_size": (_sz, [_i64]),
@@ -85,7 +87,7 @@ _SIGS = {
     "gs_bin_fill_rect": (_i32, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
                                 _sz, _vp]),
     "gs_bucket_fill": (_i32, [_vp, _i32, _vp, _i64, _vp]),
-    "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp,
+    "gs_blend_fwd_3d": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(C.c_float), _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                _vp, _vp, _i64, _i32, _vp]),
     "gs_blend_scores_3d": (_i32, [_vp, _vp, _vp, _i32, _i32, _i64, _vp, _vp]),
     "gs_blend_bwd_3d": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -191,12 +193,13 @@ def float3(v) -> C.Array:
 def make_camera(viewmat, fx: float, fy: float, cx: float, cy: float, width: int, height: int,
                 near: float, far: float, flags: int = 0) -> GsCamera:
     cam = GsCamera()
-    flat = [float(x) for x in viewmat.reshape(-1).tolist()] if hasattr(viewmat, "reshape") else \
-        [float(x) for row in viewmat for x in row]
+    if hasattr(viewmat, "reshape"):
+        flat = viewmat.reshape(-1).tolist()
+    else:
+        flat = [x for row in viewmat for x in row] if viewmat and isinstance(viewmat[0], (list, tuple)) else viewmat
     if len(flat) != 16:
         raise ValueError("viewmat must be 4x4")
-    for i, v in enumerate(flat):
-        cam.viewmat[i] = v
+    cam.viewmat[:] = [float(x) for x in flat]
     cam.fx, cam.fy, cam.cx, cam.cy = float(fx), float(fy), float(cx), float(cy)
     cam.width, cam.height = int(width), int(height)
     cam.near_plane, cam.far_plane = float(near), float(far)

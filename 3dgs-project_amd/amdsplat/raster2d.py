@@ -86,10 +86,11 @@ def bin_rects(rects: torch.Tensor, counts: torch.Tensor, depth: torch.Tensor | N
     T = tx * ty
     st = stream(dev)
     if n > 0:
-        offs = torch.empty(n + 1, dtype=torch.int32, device=dev)
-        ws = _u8(_lib.size_call("gs_scan_workspace_size", n), dev)
-        call("gs_scan_u32", ptr(counts), ptr(offs), n, ptr(ws), ws.numel(), st)
-        m = int(offs[n].item())
+        # the instance count, summed on the library's side stream and read without draining st
+        call("gs_count_begin", ptr(counts), n, 0, st)
+        mv = C.c_uint64()
+        call("gs_count_end", C.byref(mv))
+        m = int(mv.value)
     else:
         m = 0
     point_list = torch.empty(m, dtype=torch.int32, device=dev)

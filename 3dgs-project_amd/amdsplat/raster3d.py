@@ -16,6 +16,7 @@ quaternions, opacity logits, SH coefficients).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, field
 
@@ -28,6 +29,9 @@ TILE = 16
 BUCKET = 32
 REC_FLOATS = 16
 GRAD2D_FLOATS = 12
+# gs_count_begin on the library's side stream (True) or on the forward's own stream (False: the
+# depth sort then waits for the 3-5 us sum, but the host saves an event record and a stream wait)
+COUNT_ON_SIDE_STREAM = True
 # the tile binning of the views rasterize(...), rasterize_inference and pruning_scores build:
 # "auto", "spans" or "radix" (forward_pass takes its Camera's own field)
 BINNING = "auto"
@@ -65,9 +69,9 @@ class Camera:
     @staticmethod
     def from_K(viewmat, K, width: int, height: int, near: float = 0.01, far: float = 100.0,
                proper_antialiasing: bool = False, binning: str = "auto") -> "Camera":
-        K = torch.as_tensor(K, dtype=torch.float64).cpu()
+        k = (K.detach().cpu().double() if torch.is_tensor(K) else torch.as_tensor(K, dtype=torch.float64)).tolist()
         vm = torch.as_tensor(viewmat, dtype=torch.float32).detach().cpu().reshape(4, 4)
-        return Camera(vm, float(K[0, 0]), float(K[1, 1]), float(K[0, 2]), float(K[1, 2]), int(width),
+        return Camera(vm, float(k[0][0]), float(k[1][1]), float(k[0][2]), float(k[1][2]), int(width),
                       int(height), float(near), float(far), bool(proper_antialiasing), binning)
 
     @property
@@ -84,8 +88,8 @@ class Camera:
 
     def c_struct(self) -> _lib.GsCamera:
         flags = (_lib.GS_CAM_PROPER_ANTIALIASING if self.proper_antialiasing else 0) | _lib.BIN_FLAGS[self.binning]
-        return _lib.make_camera(self.viewmat.detach().cpu().float(), self.fx, self.fy, self.cx, self.cy,
-                                self.width, self.height, self.near, self.far, flags)
+        return _lib.make_camera(self.viewmat.detach().cpu().float().reshape(-1).tolist(), self.fx, self.fy, self.cx,
+                                self.cy, self.width, self.height, self.near, self.far, flags)
 
 
 @dataclass
@@ -121,6 +125,7 @@ class ForwardState:
     grad_conic64: torch.Tensor | None = None
     ccam: "_lib.GsCamera | None" = None  # the camera as the C calls take it (built once per forward)
     last_conic64: torch.Tensor | None = None  # the float64 conic sums of the last backward
+    alpha: torch.Tensor | None = None  # [H, W] 1 - final_T, written by the forward blend
 
     @property
     def n_buckets(self) -> int:
@@ -155,16 +160,11 @@ class StageTimer:
         return out
 
 
-_SIDE_STREAMS: dict = {}
-
-
-def _side_stream(dev) -> torch.cuda.Stream:
-    """A second stream per device (default priority) for the instance-count copy."""
-    key = torch.device(dev).index if torch.device(dev).index is not None else torch.cuda.current_device()
-    s = _SIDE_STREAMS.get(key)
-    if s is None:
-        s = _SIDE_STREAMS[key] = torch.cuda.Stream(device=key)
-    return s
+def _count_end() -> int:
+    """The instance count of the pending gs_count_begin on this thread and device."""
+    m = ctypes.c_uint64()
+    call("gs_count_end", ctypes.byref(m))
+    return int(m.value)
 
 
 def _check_inputs(means, log_scales, quats, opacity_logits, sh):
@@ -218,8 +218,6 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     dev = means.device
     if sh_degree is None:
         sh_degree = int(round(math.sqrt(K))) - 1
-    T = cam.n_tiles
-    H, W = cam.height, cam.width
     ccam = cam.c_struct()
     st = _lib.stream_handle(dev)
     tm = timing if isinstance(timing, StageTimer) else StageTimer(bool(timing))
@@ -234,16 +232,29 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
          n, K, sh_degree, ccam, ptr(rec), ptr(touched), ptr(dkeys), ptr(wave_counts), st)
     tm.mark("preprocess")
     # The instance count m (the total of the per-wavefront tile counts) needs only the
-    # preprocess: a side stream sums the counts and copies the total to host memory while the
-    # depth sort runs on this stream, so the host sizes the fill's buffers without the stream
-    # draining first.
-    # (The host enqueues the depth sort before it sets up the copy, so the sort follows the
-    # preprocess without a gap.)
-    side = _side_stream(dev) if n > 0 else None
-    if side is not None:
-        pre_done = torch.cuda.Event()
-        pre_done.record()
-        side.wait_event(pre_done)
+    # preprocess: the library's side stream sums the counts and copies the total to host memory
+    # while the depth sort runs on this stream, so the host sizes the fill's buffers without the
+    # stream draining first.
+    counting = n > 0
+    if counting:
+        call("gs_count_begin", ptr(wave_counts), n_waves, int(COUNT_ON_SIDE_STREAM), st)
+    try:
+        return _forward_rest(means, sh_a, sh_b, K, n, dev, sh_degree, cam, ccam, st, tm, rec, touched, dkeys, bg,
+                             timing, keep_keys, for_backward, _scores, counting)
+    except BaseException:
+        if counting:
+            try:
+                _count_end()  # the side stream's copy is done before any buffer it reads is freed
+            except _lib.AmdSplatError:
+                pass
+        raise
+
+
+def _forward_rest(means, sh_a, sh_b, K, n, dev, sh_degree, cam, ccam, st, tm, rec, touched, dkeys, bg, timing,
+                  keep_keys, for_backward, _scores, counting):
+    """forward_pass after the preprocess: the depth ordering, the count, the fill and the blend."""
+    T = cam.n_tiles
+    H, W = cam.height, cam.width
     # The tile binning's path: the radix path takes the depth order and the instance offsets in
     # that order; the span binning the depth order alone.
     path = _lib.lib().gs_bin_path(n, ccam)
@@ -253,24 +264,13 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     call("gs_bin_prepare_3d", ptr(rec), ptr(touched), ptr(dkeys), n, ccam, ptr(order), ptr(offsets), ptr(ws),
          ws.numel(), st)
     tm.mark("depth_order")
-    m_ready = None
-    if side is not None:
-        total_dev = torch.empty(1, dtype=torch.int64, device=dev)
-        wave_counts.record_stream(side)
-        total_dev.record_stream(side)
-        total_host = torch.empty(1, dtype=torch.int64, pin_memory=True)
-        with torch.cuda.stream(side):
-            call("gs_sum_u32", ptr(wave_counts), n_waves, ptr(total_dev), side.cuda_stream)
-            total_host.copy_(total_dev, non_blocking=True)
-            m_ready = torch.cuda.Event()
-            m_ready.record()
     # Everything whose size does not depend on the instance count is allocated while the copy
     # and the depth sort run; after the count arrives the host only carves the count-sized
     # buffers out of one allocation and launches the fill, before the depth sort ends.
     ranges = torch.empty(T, 2, dtype=torch.int32, device=dev)
     bucket_offsets = torch.empty(T + 1, dtype=torch.int32, device=dev)
     backward_state = for_backward and _scores is None
-    n_contrib = tile_max = grad2d = conic64 = gbuf = image = final_T = None
+    n_contrib = tile_max = grad2d = conic64 = gbuf = image = final_T = alpha = None
     if backward_state:
         n_contrib = torch.empty(H, W, dtype=torch.int32, device=dev)
         tile_max = torch.empty(T, dtype=torch.int32, device=dev)
@@ -282,13 +282,13 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     if _scores is None:
         image = torch.empty(3, H, W, dtype=torch.float32, device=dev)
         final_T = torch.empty(H, W, dtype=torch.float32, device=dev)
+        alpha = torch.empty(H, W, dtype=torch.float32, device=dev)
     # addresses the calls after the readback take (ctypes conversions done before the wait)
     p_rec, p_dkeys, p_order, p_offsets = ptr(rec), ptr(dkeys), ptr(order), ptr(offsets)
     p_ranges, p_boff, bg3 = ptr(ranges), ptr(bucket_offsets), _lib.float3(bg)
     m = 0
-    if m_ready is not None:
-        m_ready.synchronize()
-        m = int(total_host.numpy()[0])
+    if counting:
+        m = _count_end()
         if m >= 1 << 32:
             raise _lib.AmdSplatError(f"{m} tile instances exceed the 32-bit instance index")
     nb_max = (m + (BUCKET - 1) * T) // BUCKET if backward_state else 0  # >= sum over tiles of ceil(len / 32)
@@ -310,7 +310,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     tm.mark("binning")
     if _scores is None:
         call("gs_blend_fwd_3d", p_rec, p_ranges, adr["point_list"], p_boff, W, H, bg3, ptr(image), ptr(final_T),
-             ptr(n_contrib), ptr(tile_max), adr.get("ckpt"), adr.get("blist"), adr.get("bucket_to_tile"),
+             ptr(alpha), ptr(n_contrib), ptr(tile_max), adr.get("ckpt"), adr.get("blist"), adr.get("bucket_to_tile"),
              ptr(gbuf), gbuf.numel() if gbuf is not None else 0,
              _lib.GS_BLEND_LIST_CLEARED if backward_state else 0, st)
     else:  # pruning scores: the blend's weights, no image
@@ -336,7 +336,7 @@ def forward_pass(means, log_scales, quats, opacity_logits, sh, cam: Camera, sh_d
     return ForwardState(cam, n, K, sh_degree, rec, touched, order, offsets, path, m, keys, point_list, ranges,
                         bucket_offsets, nb_max, bucket_to_tile, image, final_T, n_contrib, tile_max, ckpt, blist,
                         tuple(bg),
-                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d, conic64, ccam)
+                        {} if isinstance(timing, StageTimer) else tm.result(), grad2d, conic64, ccam, None, alpha)
 
 
 def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh, grad_image,
@@ -441,7 +441,7 @@ class _Rasterize3D(torch.autograd.Function):
         ctx.dinfo = dinfo
         ctx.split = sh_rest is not None
         ctx.save_for_backward(means, log_scales, quats, opacity_logits, sh, sh_rest)
-        alpha = 1.0 - fs.final_T
+        alpha = fs.alpha.detach()  # 1 - final_T, written by the blend
         n_buckets = fs.bucket_offsets[-1]
         m = torch.tensor(fs.m, dtype=torch.int64)  # host tensor: the count is already on the host
         # The outputs are new tensor objects over the forward state's storage: were they the
@@ -548,7 +548,7 @@ def rasterize_inference(means, scales, quats, opacities, sh, viewmat, K, W: int,
     fs = forward_pass(means.detach(), scales.detach(), quats.detach(), opacities.detach(),
                       tuple(t.detach() for t in sh) if isinstance(sh, tuple) else sh.detach(), cam,
                       sh_degree=sh_degree, bg=bg, for_backward=False)
-    return fs.image, 1.0 - fs.final_T
+    return fs.image, fs.alpha
 
 
 @torch.no_grad()

@@ -2075,6 +2075,67 @@ extern "C" int gs_sum_u32(const uint32_t* in, int64_t n, uint64_t* out, void* st
   return check_launch("sum_u32");
 }
 
+namespace gs {
+// The asynchronous count readback's per-thread, per-device resources (created on first use).
+struct CountSide {
+  hipStream_t side = nullptr;
+  hipEvent_t after = nullptr, done = nullptr;
+  unsigned long long* host_word = nullptr;  // pinned, coherent: the sum kernel stores to it directly
+  bool pending = false;
+};
+constexpr int kCountMaxDevices = 64;
+static thread_local CountSide g_count[kCountMaxDevices];
+}  // namespace gs
+
+extern "C" int gs_count_begin(const uint32_t* wave_counts, int64_t n_waves, int on_side_stream, void* stream) {
+  clear_error();
+  GS_REQUIRE(n_waves >= 0 && (n_waves == 0 || wave_counts), GS_ERR_ARG, "invalid count arguments");
+  GS_REQUIRE(aligned(wave_counts, 4), GS_ERR_ALIGN, "wave_counts must be 4-byte aligned");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return check_launch("count_begin (device)");
+  GS_REQUIRE(dev >= 0 && dev < kCountMaxDevices, GS_ERR_ARG, "device index %d out of range", dev);
+  CountSide& c = g_count[dev];
+  GS_REQUIRE(!c.pending, GS_ERR_ARG, "gs_count_begin: the previous count on this thread and device was not ended");
+  if (!c.side) {
+    if (hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c.after, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c.done, hipEventDisableTiming) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&c.host_word), sizeof(unsigned long long), hipHostMallocCoherent) !=
+            hipSuccess) {
+      const int e = check_launch("count_begin (set-up)");
+      c = CountSide{};  // (a partial set-up is retried on the next call; its pieces leak)
+      return e ? e : GS_ERR_LAUNCH;
+    }
+  }
+  hipStream_t st = as_stream(stream);
+  hipStream_t run = st;
+  if (on_side_stream) {
+    if (hipEventRecord(c.after, st) != hipSuccess || hipStreamWaitEvent(c.side, c.after, 0) != hipSuccess)
+      return check_launch("count_begin (event)");
+    run = c.side;
+  }
+  // one thread stores the total straight into the pinned word: no copy to enqueue
+  hipLaunchKernelGGL(sum_u32_kernel, dim3(1), dim3(kSumThreads), 0, run, wave_counts, n_waves, c.host_word);
+  if (int e = check_launch("count_begin (sum)")) return e;
+  if (hipEventRecord(c.done, run) != hipSuccess) return check_launch("count_begin (event)");
+  c.pending = true;
+  return GS_OK;
+}
+
+extern "C" int gs_count_end(uint64_t* m) {
+  clear_error();
+  GS_REQUIRE(m, GS_ERR_ARG, "null pointer argument");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return check_launch("count_end (device)");
+  GS_REQUIRE(dev >= 0 && dev < kCountMaxDevices && g_count[dev].pending, GS_ERR_ARG,
+             "gs_count_end without gs_count_begin on this thread and device");
+  CountSide& c = g_count[dev];
+  c.pending = false;
+  if (hipEventSynchronize(c.done) != hipSuccess) return check_launch("count_end");
+  *m = *c.host_word;
+  return GS_OK;
+}
+
 extern "C" size_t gs_bin_prepare_workspace_size(int64_t n) { return prep_ws(n < 0 ? 0 : n); }
 
 extern "C" int gs_bin_prepare_3d(const float* splat_rec, const uint32_t* tiles_touched,

@@ -105,6 +105,7 @@ struct BlendArgs {
   // forward outputs / backward inputs
   S* image;
   S* final_T;
+  S* alpha_out;  // 3D forward (may be null): 1 - final_T
   int32_t* n_contrib;     // 3D, toy2d: last position + 1; phase0: number of splats
   int32_t* last_contrib;  // phase0: last position + 1 (may be null)
   uint32_t* tile_max;     // [T] max over pixels of last position + 1 (may be null in backward)
@@ -520,6 +521,7 @@ __global__ __launch_bounds__(4 * kWave) void blend_fwd_strip_kernel(BlendArgs<fl
       a.image[HW + pix] = fmaf(T[r], a.bg1, Cg[r]);
       a.image[2 * HW + pix] = fmaf(T[r], a.bg2, Cb[r]);
       a.final_T[pix] = T[r];
+      if (a.alpha_out) a.alpha_out[pix] = 1.0f - T[r];
       if (a.n_contrib) a.n_contrib[pix] = last[r];
       lmax = max(lmax, last[r]);
     }
@@ -1244,7 +1246,7 @@ void dispatch2d(int rules, int dtype, F&& f) {
 extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
                                const uint32_t* point_list, const uint32_t* bucket_offsets,
                                int width, int height, const float* bg, float* image,
-                               float* final_T, int32_t* n_contrib, uint32_t* tile_max,
+                               float* final_T, float* alpha, int32_t* n_contrib, uint32_t* tile_max,
                                float* ckpt, uint32_t* bucket_list, uint32_t* bucket_to_tile,
                                float* clear, int64_t clear_floats, int flags, void* stream) {
   clear_error();
@@ -1263,6 +1265,7 @@ extern "C" int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges,
   BlendArgs<float> a = make_args<float>(splat_rec, ranges, 2, point_list, bucket_offsets, width, height, bgd);
   a.image = image;
   a.final_T = final_T;
+  a.alpha_out = alpha;
   a.n_contrib = n_contrib;
   a.tile_max = tile_max;
   a.ckpt = ckpt;

@@ -94,6 +94,20 @@ int gs_scan_u32(const uint32_t* in, uint32_t* out, int64_t n, void* workspace,
  * (Faster-GS reads the count back after its scan, phase2/fastergs_readback.patch:46-85). */
 int gs_sum_u32(const uint32_t* in, int64_t n, uint64_t* out, void* stream);
 
+/* The instance count read back to the host without draining `stream`: gs_count_begin enqueues
+ * the sum of wave_counts[0 .. n_waves), stored by its kernel straight into pinned host memory,
+ * on `stream` itself (on_side_stream 0: the work enqueued after it waits for the 3-5 us sum, and
+ * the call costs the host one launch) or on a side stream of the library's (default priority)
+ * that waits for the work enqueued so far on `stream` (on_side_stream 1: nothing on `stream`
+ * waits, at the cost of an event record and a stream wait on the host); gs_count_end (same
+ * thread, same current device) waits for that kernel only and returns the sum in *m. The two are the exceptions to "nothing synchronises or copies": per
+ * host thread and device, the side stream, two events and an 8-byte pinned, coherent host word
+ * are created on first use and kept until the process ends. A second gs_count_begin before gs_count_end on the same thread and device is an
+ * error. (Faster-GS reads the count after its tiles_touched scan, with the stream drained,
+ * phase2/fastergs_readback.patch:46-85.) */
+int gs_count_begin(const uint32_t* wave_counts, int64_t n_waves, int on_side_stream, void* stream);
+int gs_count_end(uint64_t* m);
+
 /* ---------------------------------------------------------------------------------------
  * 3D preprocess forward (replaces Faster-GS preprocess_cu; signature evidence
  * results/phase1/garden_main_4475452_5k_cuda_gpu_kern_sum.csv:7). Per Gaussian: view
@@ -205,7 +219,8 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
  *   the last splat blended into the pixel (0 if none); tile_max [T] = max n_contrib of the
  *   tile; ckpt [n_buckets, 256, 4] = (C.r, C.g, C.b, T) at the start of every 32-entry
  *   bucket. bg is host memory (3 floats) or NULL for black. splat_rec, point_list and ckpt
- *   may be NULL when there are no instances (every tile range empty).
+ *   may be NULL when there are no instances (every tile range empty). alpha [H,W] (may be
+ *   NULL) = 1 - final_T, the rasterizer's alpha output.
  *   bucket_list (NULL, or 16-byte aligned uint32 [4 + n_buckets_max] with the bound of
  *   gs_bucket_fill; needs ckpt): receives the buckets the backward reads (those starting before
  *   their tile's tile_max) for gs_blend_bwd_3d: [0] their number, [4 ...] their indices in any
@@ -222,7 +237,7 @@ int gs_bucket_fill(const uint32_t* bucket_offsets, int n_tiles, uint32_t* bucket
  * ------------------------------------------------------------------------------------- */
 int gs_blend_fwd_3d(const float* splat_rec, const uint32_t* ranges, const uint32_t* point_list,
                     const uint32_t* bucket_offsets, int width, int height, const float* bg,
-                    float* image, float* final_T, int32_t* n_contrib, uint32_t* tile_max,
+                    float* image, float* final_T, float* alpha, int32_t* n_contrib, uint32_t* tile_max,
                     float* ckpt, uint32_t* bucket_list, uint32_t* bucket_to_tile, float* clear,
                     int64_t clear_floats, int flags, void* stream);
 enum { GS_BLEND_LIST_CLEARED = 1 };

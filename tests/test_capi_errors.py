@@ -46,6 +46,8 @@ def test_negative_sizes_and_nulls_are_refused():
            GS_ERR_ARG, "null")
     expect(L.gs_preprocess_fwd(None, None, None, None, None, None, -1, 16, 3, cam(), None, None, None, None, None),
            GS_ERR_ARG, "n must be >= 0")
+    expect(L.gs_count_begin(None, -1, 0, None), GS_ERR_ARG, "invalid count arguments")
+    expect(L.gs_count_end(None), GS_ERR_ARG, "null pointer")
     expect(L.gs_bin_fill_3d(None, None, None, None, -5, cam(), 0, None, None, None, None, None, None, 0, None),
            GS_ERR_ARG, "invalid sizes")
     expect(L.gs_bin_fill_3d(None, None, None, None, 10, cam(), 5, None, None, None, None, None, None, 0, None),
@@ -170,6 +172,24 @@ def test_fill_workspace_short_then_a_good_call():
                             ptr(boff), None, ptr(ws), need, None) == 0
     torch.cuda.synchronize()
     assert torch.equal(pl, fs.point_list) and torch.equal(ranges, fs.ranges) and torch.equal(boff, fs.bucket_offsets)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("side", [0, 1])
+def test_count_readback_pairs_and_sums(side):
+    """gs_count_begin / gs_count_end: the sum of the counts on either stream; an end without a
+    begin and a second begin before the end are refused, and the next pair works."""
+    L = _lib.lib()
+    m = ctypes.c_uint64()
+    expect(L.gs_count_end(ctypes.byref(m)), GS_ERR_ARG, "without gs_count_begin")
+    for n in (0, 1, 63, 64, 1000, 300_001):
+        c = torch.randint(0, 1 << 20, (n,), dtype=torch.int32, device="cuda")
+        assert L.gs_count_begin(ptr(c), n, side, None) == 0
+        if n == 1000:
+            expect(L.gs_count_begin(ptr(c), n, side, None), GS_ERR_ARG, "was not ended")
+        assert L.gs_count_end(ctypes.byref(m)) == 0
+        assert m.value == int(c.long().sum()), n
+    expect(L.gs_count_end(ctypes.byref(m)), GS_ERR_ARG, "without gs_count_begin")
 
 
 @pytest.mark.gpu
