@@ -107,6 +107,8 @@ _SIGS = {
     "gs_probe_read": (_i32, [_vp, _i64, _vp, _vp]),
     "gs_probe_fma": (_i32, [_vp, _i64, _i32, _vp]),
     # 2D rule sets
+    "gs2d_activate_fwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "gs2d_activate_bwd": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "gs2d_rects_toy": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "gs2d_rects_phase0": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "gs2d_pack": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),

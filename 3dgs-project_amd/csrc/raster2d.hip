@@ -97,11 +97,128 @@ __global__ void pack_kernel(const S* __restrict__ means, const S* __restrict__ s
   for (int k = 0; k < kRecFloats; ++k) dst[k] = v[k];
 }
 
+// The toy2d activation (toy2d/gs2d/params.py:36-46) of Gaussian i, in the reference's operation
+// order (each product and sum rounded on its own, as separate tensor operations round them):
+// var = exp(2 log_scale), cxx = c c vx + s s vy, cxy = c s (vx - vy), cyy = s s vx + c c vy with
+// (c, s) = (cos, sin)(theta), det = cxx cyy - cxy cxy, conic = (cyy, -cxy, cxx) / det; and the
+// integer 3-sigma radius of toy2d/gs2d/params.py:49-56 (0 where det <= 0).
+struct Act2D {
+  float vx, vy, c, s, cxx, cxy, cyy, det;
+};
+
+__device__ __forceinline__ Act2D activate2d(const float* __restrict__ log_scale, const float* __restrict__ theta,
+                                            int64_t i) {
+  Act2D a;
+  a.vx = expf(2.0f * log_scale[2 * i]);
+  a.vy = expf(2.0f * log_scale[2 * i + 1]);
+  a.c = cosf(theta[i]);
+  a.s = sinf(theta[i]);
+  const float cc = a.c * a.c, ss = a.s * a.s;
+  a.cxx = cc * a.vx + ss * a.vy;
+  a.cxy = (a.c * a.s) * (a.vx - a.vy);
+  a.cyy = ss * a.vx + cc * a.vy;
+  a.det = a.cxx * a.cyy - a.cxy * a.cxy;
+  return a;
+}
+
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__global__ void activate2d_fwd_kernel(const float* __restrict__ log_scale, const float* __restrict__ theta,
+                                      const float* __restrict__ rgb_logit, const float* __restrict__ opacity_logit,
+                                      int64_t n, float* __restrict__ conic, float* __restrict__ color,
+                                      float* __restrict__ opacity, float* __restrict__ cov,
+                                      int32_t* __restrict__ radii) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const Act2D a = activate2d(log_scale, theta, i);
+  conic[3 * i] = a.cyy / a.det;
+  conic[3 * i + 1] = -a.cxy / a.det;
+  conic[3 * i + 2] = a.cxx / a.det;
+  for (int k = 0; k < 3; ++k) color[3 * i + k] = sigmoid_ref(rgb_logit[3 * i + k]);
+  opacity[i] = sigmoid_ref(opacity_logit[i]);
+  if (cov) {
+    cov[3 * i] = a.cxx;
+    cov[3 * i + 1] = a.cxy;
+    cov[3 * i + 2] = a.cyy;
+  }
+  if (radii) {
+    const float mid = 0.5f * (a.cxx + a.cyy);
+    const float lam = mid + sqrtf(fmaxf(mid * mid - a.det, 0.1f));
+    radii[i] = a.det > 0.0f ? static_cast<int32_t>(ceilf(3.0f * sqrtf(lam))) : 0;
+  }
+}
+
+// Gradients of the activation from those of conic, colour and opacity (means pass through): the
+// chain rule through conic = (cyy, -cxy, cxx) / det, the covariance and exp / cos / sin, with the
+// forward's values recomputed; colour and opacity through the sigmoid, s (1 - s).
+__global__ void activate2d_bwd_kernel(const float* __restrict__ log_scale, const float* __restrict__ theta,
+                                      const float* __restrict__ rgb_logit, const float* __restrict__ opacity_logit,
+                                      int64_t n, const float* __restrict__ g_conic, const float* __restrict__ g_color,
+                                      const float* __restrict__ g_opacity, float* __restrict__ g_log_scale,
+                                      float* __restrict__ g_theta, float* __restrict__ g_rgb_logit,
+                                      float* __restrict__ g_opacity_logit) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const Act2D a = activate2d(log_scale, theta, i);
+  const float gA = g_conic ? g_conic[3 * i] : 0.0f, gB = g_conic ? g_conic[3 * i + 1] : 0.0f;
+  const float gC = g_conic ? g_conic[3 * i + 2] : 0.0f;
+  const float id = 1.0f / a.det;
+  // K = (gA cyy - gB cxy + gC cxx) / det^2 = d L / d(1 / det) / ... : the det term of every entry
+  const float K = (gA * a.cyy - gB * a.cxy + gC * a.cxx) * id * id;
+  const float g_cxx = gC * id - K * a.cyy;
+  const float g_cyy = gA * id - K * a.cxx;
+  const float g_cxy = -gB * id + 2.0f * K * a.cxy;
+  const float cc = a.c * a.c, ss = a.s * a.s, cs = a.c * a.s, dv = a.vx - a.vy;
+  const float g_vx = g_cxx * cc + g_cxy * cs + g_cyy * ss;
+  const float g_vy = g_cxx * ss - g_cxy * cs + g_cyy * cc;
+  const float g_c = 2.0f * a.c * (g_cxx * a.vx + g_cyy * a.vy) + g_cxy * a.s * dv;
+  const float g_s = 2.0f * a.s * (g_cxx * a.vy + g_cyy * a.vx) + g_cxy * a.c * dv;
+  g_log_scale[2 * i] = 2.0f * a.vx * g_vx;
+  g_log_scale[2 * i + 1] = 2.0f * a.vy * g_vy;
+  g_theta[i] = a.c * g_s - a.s * g_c;
+  for (int k = 0; k < 3; ++k) {
+    const float sg = sigmoid_ref(rgb_logit[3 * i + k]);
+    g_rgb_logit[3 * i + k] = g_color ? g_color[3 * i + k] * sg * (1.0f - sg) : 0.0f;
+  }
+  const float so = sigmoid_ref(opacity_logit[i]);
+  g_opacity_logit[i] = g_opacity ? g_opacity[i] * so * (1.0f - so) : 0.0f;
+}
+
 }  // namespace gs
 
 using namespace gs;
 
 static inline unsigned grid256(int64_t n) { return static_cast<unsigned>((n + 255) / 256); }
+
+extern "C" int gs2d_activate_fwd(const float* log_scale, const float* theta, const float* rgb_logit,
+                                 const float* opacity_logit, int64_t n, float* conic, float* color, float* opacity,
+                                 float* cov, int32_t* radii, void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(log_scale && theta && rgb_logit && opacity_logit && conic && color && opacity, GS_ERR_ARG,
+             "null pointer argument");
+  hipLaunchKernelGGL(activate2d_fwd_kernel, dim3(grid256(n)), dim3(256), 0, as_stream(stream), log_scale, theta,
+                     rgb_logit, opacity_logit, n, conic, color, opacity, cov, radii);
+  return check_launch("gs2d_activate_fwd");
+}
+
+extern "C" int gs2d_activate_bwd(const float* log_scale, const float* theta, const float* rgb_logit,
+                                 const float* opacity_logit, int64_t n, const float* grad_conic,
+                                 const float* grad_color, const float* grad_opacity, float* grad_log_scale,
+                                 float* grad_theta, float* grad_rgb_logit, float* grad_opacity_logit,
+                                 void* stream) {
+  clear_error();
+  GS_REQUIRE(n >= 0, GS_ERR_ARG, "n must be >= 0");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(log_scale && theta && rgb_logit && opacity_logit && grad_log_scale && grad_theta && grad_rgb_logit &&
+                 grad_opacity_logit,
+             GS_ERR_ARG, "null pointer argument");
+  hipLaunchKernelGGL(activate2d_bwd_kernel, dim3(grid256(n)), dim3(256), 0, as_stream(stream), log_scale, theta,
+                     rgb_logit, opacity_logit, n, grad_conic, grad_color, grad_opacity, grad_log_scale, grad_theta,
+                     grad_rgb_logit, grad_opacity_logit);
+  return check_launch("gs2d_activate_bwd");
+}
 
 extern "C" int gs2d_rects_toy(const float* means, const int32_t* radii, int64_t n, int width, int height,
                               int32_t* rects, uint32_t* counts, void* stream) {

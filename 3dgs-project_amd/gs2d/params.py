@@ -27,6 +27,11 @@ class Gaussians2D(torch.nn.Module):
     def activated(self):
         return activate(self.xy, self.log_scale, self.theta, self.rgb_logit, self.opacity_logit)
 
+    def activated_fused(self):
+        """(means, conic, color, opacity, cov, radii) of activate_fused: the activation and the
+        3-sigma radii in one launch (CUDA parameters)."""
+        return activate_fused(self.xy, self.log_scale, self.theta, self.rgb_logit, self.opacity_logit)
+
 
 def activate(xy, log_scale, theta, rgb_logit, opacity_logit):
     """(means, conic, color, opacity, cov): cov = (xx, xy, yy) of R diag(s^2) R^T."""
@@ -39,6 +44,48 @@ def activate(xy, log_scale, theta, rgb_logit, opacity_logit):
     det = cxx * cyy - cxy * cxy
     conic = torch.stack([cyy / det, -cxy / det, cxx / det], dim=-1)
     return xy, conic, torch.sigmoid(rgb_logit), torch.sigmoid(opacity_logit), torch.stack([cxx, cxy, cyy], dim=-1)
+
+
+class _ActivateFused(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, xy, log_scale, theta, rgb_logit, opacity_logit):
+        from amdsplat._lib import call, ptr, stream_handle
+
+        ls, th, rl, ol = (t.detach().contiguous() for t in (log_scale, theta, rgb_logit, opacity_logit))
+        n = xy.shape[0]
+        dev = xy.device
+        radii = torch.empty(n, dtype=torch.int32, device=dev)
+        conic, color, cov = (torch.empty(n, 3, dtype=torch.float32, device=dev) for _ in range(3))
+        opacity = torch.empty(n, dtype=torch.float32, device=dev)
+        call("gs2d_activate_fwd", ptr(ls), ptr(th), ptr(rl), ptr(ol), n, ptr(conic), ptr(color), ptr(opacity),
+             ptr(cov), ptr(radii), stream_handle(dev))
+        ctx.save_for_backward(ls, th, rl, ol)
+        ctx.mark_non_differentiable(cov, radii)
+        return xy.view_as(xy), conic, color, opacity, cov, radii
+
+    @staticmethod
+    def backward(ctx, g_means, g_conic, g_color, g_opacity, _g_cov, _g_radii):
+        from amdsplat._lib import call, ptr, stream_handle
+
+        ls, th, rl, ol = ctx.saved_tensors
+        n = ls.shape[0]
+        dev = ls.device
+        g_ls, g_rl = torch.empty_like(ls), torch.empty_like(rl)
+        g_th, g_ol = torch.empty_like(th), torch.empty_like(ol)
+        gc, gcol, gop = (None if g is None else g.contiguous().float() for g in (g_conic, g_color, g_opacity))
+        call("gs2d_activate_bwd", ptr(ls), ptr(th), ptr(rl), ptr(ol), n, ptr(gc), ptr(gcol), ptr(gop), ptr(g_ls),
+             ptr(g_th), ptr(g_rl), ptr(g_ol), stream_handle(dev))
+        return g_means, g_ls, g_th, g_rl, g_ol
+
+
+def activate_fused(xy, log_scale, theta, rgb_logit, opacity_logit):
+    """activate and radii_from_cov in one HIP launch (and one for the backward), for fit loops on
+    the GPU: (means, conic, color, opacity, cov, radii). The same operations in the same order on
+    float32 CUDA tensors, with exp / cos / sin from the device math library (which may round
+    differently from the tensor library's in the last place); cov and radii take no gradient."""
+    if not xy.is_cuda or any(t.dtype != torch.float32 for t in (xy, log_scale, theta, rgb_logit, opacity_logit)):
+        raise ValueError("activate_fused takes float32 CUDA tensors")
+    return _ActivateFused.apply(xy, log_scale, theta, rgb_logit, opacity_logit)
 
 
 @torch.no_grad()

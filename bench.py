@@ -756,8 +756,9 @@ def bench_toy2d(args, ceilings) -> dict:
     def step(k, timer=None):
         tm = timer if timer is not None else R.StageTimer(False)
         tm.mark("start")
-        means, conic, color, opacity, cov = model.activated()
-        bins = bin_gaussians(means, radii_from_cov(cov.detach()), model.depth, H, W)
+        # activate + radii_from_cov (toy2d/fit.py:77-78) in one launch, its backward in one more
+        means, conic, color, opacity, cov, radii = model.activated_fused()
+        bins = bin_gaussians(means, radii, model.depth, H, W)
         tm.mark("binning")
         img = rasterize(means, conic, color, opacity, bins, backend="splat")
         tm.mark("forward")
@@ -826,8 +827,9 @@ def bench_toy2d(args, ceilings) -> dict:
         "dtype": "f32", "data": "synthetic (seeded: means U(0,256)^2, log-scales N(ln 2, 0.3), angle U(0, pi), "
                                 "opacity sigmoid(N(0,1)), colour U(0,1), target U(0,1))",
         "config": {"workload": "toy2d_fit: 4096 2D Gaussians, 256x256, one fit step (activate, GPU binning, "
-                               "forward, L1, bucketed backward, Adam: torch.optim.Adam's update for the five "
-                               "groups in one FusedAdam launch)", "parallelism": "single GPU"},
+                               "forward, L1, bucketed backward, Adam: the activation and radii in one launch "
+                               "(activate_fused), torch.optim.Adam's update for the five groups in one "
+                               "FusedAdam launch)", "parallelism": "single GPU"},
         "stage_ms": {k2: round(v, 4) for k2, v in stage_ms.items()},
         "kernel_ms": {"forward_with_checkpoints": round(fwd_ms, 4), "backward_splat": round(bwd_ms, 4)},
         "counts": {"pairs": m, "buckets": nb},

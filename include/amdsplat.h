@@ -314,6 +314,23 @@ int gs_densification_stats(const float* grad2d, const uint32_t* tiles_touched, i
  * 2D surfaces (rules GS_RULES_TOY2D / GS_RULES_PHASE0; dtype GS_FLOAT32 / GS_FLOAT64)
  * ===================================================================================== */
 
+/* The toy2d activation in one launch (the caller-side toy2d/gs2d/params.py:36-56, activate and
+ * radii_from_cov, for fit loops that would otherwise run a dozen small tensor operations and their
+ * backwards per step; no kernel of the reference): log_scale [n,2], theta [n], rgb_logit [n,3],
+ * opacity_logit [n] -> conic [n,3] = (cyy, -cxy, cxx) / det of cov = R diag(exp(2 log_scale))
+ * R^T, color [n,3] and opacity [n] (sigmoids), cov [n,3] = (cxx, cxy, cyy) and radii [n] (the
+ * integer 3-sigma radius, 0 where det <= 0; cov and radii may be NULL). The reference's operation
+ * order, float32; exp, cos and sin from the device math library. gs2d_activate_bwd: the
+ * gradients of log_scale, theta, rgb_logit and opacity_logit from those of conic, color and
+ * opacity (each may be NULL: zero); the means pass through. */
+int gs2d_activate_fwd(const float* log_scale, const float* theta, const float* rgb_logit,
+                      const float* opacity_logit, int64_t n, float* conic, float* color, float* opacity,
+                      float* cov, int32_t* radii, void* stream);
+int gs2d_activate_bwd(const float* log_scale, const float* theta, const float* rgb_logit,
+                      const float* opacity_logit, int64_t n, const float* grad_conic, const float* grad_color,
+                      const float* grad_opacity, float* grad_log_scale, float* grad_theta,
+                      float* grad_rgb_logit, float* grad_opacity_logit, void* stream);
+
 /* toy2d tile rectangles from the 3-sigma radius (replaces the getRect part of
  * toy2d/gs2d/binning.py:44-57): means [n,2] float32 (8-byte aligned), radii [n] int32 ->
  * rects [n,4] (xmin, ymin, xmax, ymax in tiles, max exclusive, empty = collapsed to

@@ -393,3 +393,51 @@ def test_gs2d_fit_workload_4k_256(backend):
                                ref["ckpt"])
     for cols, gg in (((0, 1), grads[0]), ((2, 3, 4), grads[1]), ((6, 7, 8), grads[2]), ((5,), grads[3])):
         assert rel(gg.reshape(-1, len(cols)), gr[:, list(cols)]) < 1e-4
+
+
+@pytest.mark.parametrize("spread", [False, True])
+def test_fused_activation_matches_the_reference_activation(spread):
+    """gs2d.params.activate_fused against activate / radii_from_cov (the reference's operations as
+    tensor ops on the same GPU): outputs within a few float32 ulps (exp, cos and sin may round
+    differently in the last place), radii equal except where 3 sqrt(lambda) lies within 1e-5 of an
+    integer. Gradients: on the fit's own initial Gaussians (anisotropy <= 3) within 1e-5 relative
+    L2 of float64 autograd of activate; with scales spread over e^(+-3) (condition numbers up to
+    ~1e5, where float32 cancels in the conic's det terms) no further from float64 than 1.5x the
+    float32 autograd of activate itself."""
+    from gs2d.params import Gaussians2D, activate, activate_fused, radii_from_cov
+
+    g = Gaussians2D(20_000, 512, 512, seed=3).cuda()
+    if spread:
+        with torch.no_grad():
+            g.log_scale.add_(torch.randn(g.log_scale.shape, generator=torch.Generator().manual_seed(1)).cuda())
+            g.theta.mul_(3.0)
+    ref = activate(g.xy, g.log_scale, g.theta, g.rgb_logit, g.opacity_logit)
+    out = activate_fused(g.xy, g.log_scale, g.theta, g.rgb_logit, g.opacity_logit)
+    for k, name in enumerate(["means", "conic", "color", "opacity", "cov"]):
+        a, b = out[k].detach(), ref[k].detach()
+        err = ((a - b).abs() / b.abs().clamp_min(1e-30)).max().item()
+        assert err < 4e-6, f"{name}: {err:.2e}"
+    r_ref = radii_from_cov(ref[4].detach())
+    c64 = ref[4].detach().double()
+    mid = 0.5 * (c64[:, 0] + c64[:, 2])
+    det = c64[:, 0] * c64[:, 2] - c64[:, 1] ** 2
+    t = 3.0 * torch.sqrt(mid + torch.sqrt((mid * mid - det).clamp_min(0.1)))
+    near_int = (t - t.round()).abs() < 1e-5
+    assert int(((out[5] != r_ref) & ~near_int).sum()) == 0
+    # gradients: a random linear loss of means, conic, colour and opacity
+    gen = torch.Generator().manual_seed(5)
+    w = [torch.randn(t.shape, generator=gen).cuda() for t in out[:4]]
+    params = (g.xy, g.log_scale, g.theta, g.rgb_logit, g.opacity_logit)
+
+    def grads(fn, dtype):
+        leaves = [p.detach().to(dtype).clone().requires_grad_(True) for p in params]
+        o = fn(*leaves)
+        sum(((r * wi.to(dtype)).sum() for r, wi in zip(o[:4], w))).backward()
+        return [x.grad.double() for x in leaves]
+
+    g64, g32, gf = grads(activate, torch.float64), grads(activate, torch.float32), grads(activate_fused, torch.float32)
+    for a, t32, b, name in zip(gf, g32, g64, ["xy", "log_scale", "theta", "rgb_logit", "opacity_logit"]):
+        e = ((a - b).norm() / b.norm()).item()
+        e32 = ((t32 - b).norm() / b.norm()).item()
+        bound = 1.5 * e32 + 1e-7 if spread else 1e-5
+        assert e < bound, f"grad {name}: {e:.2e} (float32 autograd of activate: {e32:.2e})"
