@@ -76,8 +76,14 @@ class _Extension:
     def __init__(self):
         self._counters = None
         self._ckpt_bytes = 0
+        # the GPU kernels count their atomic adds and splat-pixel evaluations (get_counters)
+        # unless this is off; the reference's CUDA kernels count nothing, so timings of them
+        # compare with this off
+        self.counting = True
 
-    def _ctr(self, device) -> Tensor:
+    def _ctr(self, device) -> Tensor | None:
+        if not self.counting:
+            return None
         if self._counters is None or self._counters.device != device:
             self._counters = torch.zeros(3, dtype=torch.int64, device=device)
         return self._counters

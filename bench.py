@@ -5,7 +5,8 @@ poses (radius U(3,5)); one step = forward + backward of one view (poses cycled) 
 N(0,1) upstream image gradient, through the autograd operator rasterize(...) -> image.backward.
 Inputs are resident in HBM before the timed region.
 
-    python bench.py [--steps K] [--warmup W] [--workload sh3_1m|sh3_3m|sh_rgb_100k|toy2d_fit]
+    python bench.py [--steps K] [--warmup W]
+                    [--workload sh3_1m|sh3_3m|sh_rgb_100k|toy2d_fit|toy2d_bench|phase0_bench]
                     [--no-cpu-baseline] [--no-train-step] [--no-variants] [--no-probes]
     python bench.py --probes          # only the achievable-ceiling probes (copy, read, FMA)
 
@@ -25,6 +26,8 @@ fwd+bwd, all cores (median of 5 after a warm-up) and one thread (median of 3).
 
 toy2d_fit is the 2D image fit (4096 Gaussians, 256x256, L1, Adam): the GPU step through the HIP
 kernels, beside the dense PyTorch reference path (render_reference) on the host cores.
+toy2d_bench and phase0_bench time the 2D extensions' kernels alone on the reference's own bench
+scenes (toy2d/bench.py, bench/phase0/backward_bench.py), beside the reference's published figures.
 """
 from __future__ import annotations
 
@@ -69,7 +72,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=160)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--workload", default="sh3_1m",
-                    choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit", "toy2d_bench"])
+                    choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit", "toy2d_bench", "phase0_bench"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5, help="all-core CPU baseline runs (median)")
     ap.add_argument("--cpu-single-runs", type=int, default=3, help="single-thread CPU baseline runs (0 = skip)")
@@ -933,6 +936,110 @@ def bench_toy2d_kernels(args) -> dict:
     }
 
 
+# The reference's phase0 result on its bench scenes (bench/phase0/backward_bench.py defaults,
+# 1920x1080, sigma 2-10 px, opacity 0.05-0.6): the bucketed backward (B) 8.3x faster than the
+# per-pixel atomic backward (A) at 50k splats and 9.1x at 200k, on an A100 (phase1/PLAN.md:16;
+# its raw logs are not in the tree).
+PHASE0_REF_SPEEDUP = {50_000: 8.3, 200_000: 9.1}
+
+
+def phase0_scene(n: int, h: int, w: int, seed: int = 0, sigma=(2.0, 10.0), opacity=(0.05, 0.6)):
+    """The phase0 bench scene (bench/phase0/backward_bench.py:34-49): float64 draws from one seeded
+    generator in the reference's order -- means x and y U(-2%, 102%) of the image, the two
+    Cholesky diagonals 1 / U(sigma), the off-diagonal U(-0.5, 0.5) times the smaller diagonal,
+    opacity U(opacity), colours U(0, 1) -- as (means, chol, opacity logit, colours); index order is
+    depth order."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+
+    def u(lo, hi, *shape):
+        return lo + (hi - lo) * torch.rand(*shape, generator=g, dtype=torch.float64)
+
+    means = torch.stack([u(-0.02 * w, 1.02 * w, n), u(-0.02 * h, 1.02 * h, n)], dim=-1)
+    l0 = 1.0 / u(sigma[0], sigma[1], n)
+    l2 = 1.0 / u(sigma[0], sigma[1], n)
+    l1 = u(-0.5, 0.5, n) * torch.minimum(l0, l2)
+    o = u(opacity[0], opacity[1], n)
+    colors = u(0.0, 1.0, n, 3)
+    return means, torch.stack([l0, l1, l2], dim=-1), torch.log(o / (1.0 - o)), colors
+
+
+def bench_phase0_kernels(args) -> dict:
+    """The reference's phase0 kernel benchmark (bench/phase0/backward_bench.py:81-175) on its
+    scenes at 50k and 200k splats: forward, per-pixel backward (A) and bucketed backward (B) of
+    the extension, each call timed alone with HIP events (median of --steps calls after --warmup,
+    output allocation included, as the reference times them), without the GPU op counters the
+    reference's CUDA kernels do not have; plus A-versus-B agreement per parameter group."""
+    import torch
+
+    from splat2d import bin_tiles, load_extension
+
+    def timed(fn, warmup, iters):
+        for _ in range(warmup):
+            fn()
+        times = []
+        for _ in range(iters):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b))
+        return statistics.median(times)
+
+    def rel(a, b):
+        return float((a.double() - b.double()).norm() / max(float(b.double().norm()), 1e-12))
+
+    h, w = 1080, 1920
+    ext = load_extension(with_cuda=True)
+    ext.counting = False
+    rows = []
+    try:
+        for n, ref_speedup in PHASE0_REF_SPEEDUP.items():
+            p64 = [t.cuda() for t in phase0_scene(n, h, w)]
+            bins = bin_tiles(*p64[:3], h, w)
+            tb = (bins.tile_offsets, bins.tile_ids, bins.bucket_offsets, bins.bucket_tile)
+            p32 = [t.float().contiguous() for t in p64]
+            g_img = torch.randn(h, w, 3, generator=torch.Generator().manual_seed(1)).cuda()
+            image, t_final, n_contrib, last_contrib, ckpt = ext.forward(*p32, *tb, h, w)
+
+            def fwd():
+                return ext.forward(*p32, *tb, h, w)
+
+            def bwd_a():
+                return ext.backward_pixel(g_img, *p32, *tb, t_final, last_contrib, h, w)
+
+            def bwd_b():
+                return ext.backward_splat(g_img, *p32, *tb, image, ckpt, h, w)
+
+            ga, gb = bwd_a(), bwd_b()
+            counts = (bins.tile_offsets[1:] - bins.tile_offsets[:-1]).double()
+            t_f, t_a, t_b = (timed(f, args.warmup, args.steps) for f in (fwd, bwd_a, bwd_b))
+            rows.append({"width": w, "height": h, "n": n, "list_entries": int(counts.sum()),
+                         "per_tile_mean": round(float(counts.mean()), 1), "per_tile_max": int(counts.max()),
+                         "buckets": bins.num_buckets,
+                         "contributors_per_pixel": round(float(n_contrib.double().mean()), 1),
+                         "forward_ms": round(t_f, 4), "backward_pixel_ms": round(t_a, 4),
+                         "backward_splat_ms": round(t_b, 4), "splat_speedup": round(t_a / t_b, 2),
+                         "reference_a100_splat_speedup": ref_speedup,
+                         "a_vs_b_rel": {k: float(f"{rel(b, a):.2e}") for k, a, b in
+                                        zip(("means", "chol", "opacity_logit", "colors"), ga, gb)}})
+    finally:
+        ext.counting = True
+    value = statistics.mean(r["backward_splat_ms"] for r in rows)
+    return {
+        "metric": "phase0 kernels: bucketed backward ms at 1920x1080, mean over the reference's 50k and 200k scenes",
+        "value": round(value, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(value, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (the reference's seeded phase0 bench scene, seed 0)",
+        "config": {"workload": "phase0_bench: 1920x1080, 50k and 200k 2D splats (sigma 2-10 px, opacity 0.05-0.6); "
+                               "forward, per-pixel backward (A), bucketed backward (B), each call timed alone",
+                   "parallelism": "single GPU"},
+        "rows": rows,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -947,6 +1054,8 @@ def main():
         out = bench_toy2d(args, ceilings)
     elif args.workload == "toy2d_bench":
         out = bench_toy2d_kernels(args)
+    elif args.workload == "phase0_bench":
+        out = bench_phase0_kernels(args)
     else:
         out = bench_3d(args, ceilings)
     line = json.dumps(out)
