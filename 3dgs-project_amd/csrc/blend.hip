@@ -737,7 +737,10 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
                                            uint32_t* s_id, float* s_c, uint32_t& evals, uint32_t& atomics) {
   using Ru = Rule<R, S>;
   constexpr int NV = Ru::kGradVals;
-  const int lane = threadIdx.x & 63;
+  // (opaque: in the striding kernel the lane's constants are then formed per bucket instead of
+  // being hoisted out of its loop and held in registers across it)
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
   const uint32_t tile = a.bucket_to_tile[b];
   const int bstart = static_cast<int>(b - a.bucket_offsets[tile]) * kBucket;
   const int tmax = a.tile_max ? static_cast<int>(a.tile_max[tile]) : INT_MAX;
@@ -1039,9 +1042,13 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(
     // a bounded grid strides over the list (for bucket tables far longer than the list)
     const int64_t cnt = a.bucket_list[0];
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBwdWaves;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave; i < cnt; i += stride)
-      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], s_cw, evals,
-                                     atomics);
+    // the wavefront's index made scalar: the loop state and the LDS slots' addresses then live in
+    // scalar registers (64 VGPRs, 8 wavefronts per SIMD, against 77 and 6)
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+    float* s_cws = s_c[R == kRules3D ? wave_s : 0];
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave_s; i < cnt; i += stride)
+      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave_s], s_m[wave_s], s_id[wave_s], s_cws,
+                                     evals, atomics);
   } else {
     const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
     if (b < a.n_buckets && !(a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)))
