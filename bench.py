@@ -6,7 +6,7 @@ N(0,1) upstream image gradient, through the autograd operator rasterize(...) -> 
 Inputs are resident in HBM before the timed region.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload sh3_1m|sh3_3m|sh_rgb_100k|toy2d_fit|toy2d_bench|phase0_bench]
+                    [--workload sh3_1m|sh3_3m|sh_rgb_100k|toy2d_fit|toy2d_bench|phase0_bench|l1_ssim]
                     [--no-cpu-baseline] [--no-train-step] [--no-variants] [--no-probes]
     python bench.py --probes          # only the achievable-ceiling probes (copy, read, FMA)
 
@@ -28,6 +28,7 @@ toy2d_fit is the 2D image fit (4096 Gaussians, 256x256, L1, Adam): the GPU step 
 kernels, beside the dense PyTorch reference path (render_reference) on the host cores.
 toy2d_bench and phase0_bench time the 2D extensions' kernels alone on the reference's own bench
 scenes (toy2d/bench.py, bench/phase0/backward_bench.py), beside the reference's published figures.
+l1_ssim times the fused L1 + D-SSIM loss kernels alone on the 1M workload's frame size.
 """
 from __future__ import annotations
 
@@ -72,7 +73,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=160)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--workload", default="sh3_1m",
-                    choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit", "toy2d_bench", "phase0_bench"])
+                    choices=["sh3_1m", "sh3_3m", "sh_rgb_100k", "toy2d_fit", "toy2d_bench", "phase0_bench", "l1_ssim"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5, help="all-core CPU baseline runs (median)")
     ap.add_argument("--cpu-single-runs", type=int, default=3, help="single-thread CPU baseline runs (0 = skip)")
@@ -1040,6 +1041,30 @@ def bench_phase0_kernels(args) -> dict:
     }
 
 
+def bench_l1_ssim(args) -> dict:
+    """The fused L1 + D-SSIM loss alone on a 3 x 840 x 1297 frame (the 1M workload's): the forward
+    (with the backward's per-pixel map and the partial-sum reduction) and the backward, each
+    launched --steps times back to back after --warmup and event-timed. The reference's
+    fused-ssim kernels take 0.064 ms (fusedssimCUDA) + 0.093 ms (fusedssim_backwardCUDA) per
+    training step on its H100 (results/phase1/README.md:46-47)."""
+    import torch
+
+    g = torch.Generator().manual_seed(4321)
+    target = torch.rand(3, 840, 1297, generator=g).cuda()
+    loss_kernel_times(target, max(args.warmup, 1))  # warm-up
+    t = loss_kernel_times(target, args.steps)
+    value = t["fwd_ms"] + t["bwd_ms"]
+    return {
+        "metric": "L1 + D-SSIM loss forward + backward ms on a 3x840x1297 frame",
+        "value": round(value, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(value, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded U(0,1) image and target)",
+        "config": {"workload": "l1_ssim: 11x11 Gaussian window (sigma 1.5), lambda 0.2, 3x840x1297",
+                   "parallelism": "single GPU"},
+        "kernels": t, "reference_h100_ms": {"fusedssimCUDA": 0.064, "fusedssim_backwardCUDA": 0.093},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1056,6 +1081,8 @@ def main():
         out = bench_toy2d_kernels(args)
     elif args.workload == "phase0_bench":
         out = bench_phase0_kernels(args)
+    elif args.workload == "l1_ssim":
+        out = bench_l1_ssim(args)
     else:
         out = bench_3d(args, ceilings)
     line = json.dumps(out)
