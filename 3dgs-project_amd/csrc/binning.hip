@@ -1108,11 +1108,14 @@ __device__ __forceinline__ uint32_t pack_row_span(uint32_t tx0, uint32_t nt, int
   return tx0 | (nt << 10) | (static_cast<uint32_t>(row) << 21);
 }
 
+constexpr int kGatherHeld = 8;  // windows of (Gaussian, tile row) items a lane keeps between the passes
+
 // Row pass, gather: one workgroup per chunk of kRowChunk Gaussians in depth order (wavefront w
 // takes the w-th 64). Reads each Gaussian's record once, counts the chunk's non-empty spans per
 // row into rowhist[r][c], reserves room for them in `gathered` (one atomic add per chunk:
 // chunk_info[c] = (first slot, number of spans)) and writes them there in (Gaussian, row)
-// order. The band arithmetic runs twice (count, then write): it is cheap next to the gather.
+// order. The band arithmetic of the first kGatherHeld windows of items runs once (its spans are
+// kept in registers between the passes), that of later windows twice (count, then write).
 template <bool kRect>
 __global__ __launch_bounds__(256) void span_gather_kernel(const SplatRec* __restrict__ rec,
                                                           const int4* __restrict__ rects,
@@ -1167,8 +1170,32 @@ __global__ __launch_bounds__(256) void span_gather_kernel(const SplatRec* __rest
   uint32_t total;
   s_rex[lane] = wave_excl_scan(rows, lane, total);
   __syncthreads();  // counts cleared, setups visible
+  // the first kGatherHeld windows' spans are kept (packed, with their Gaussian's slot) for the
+  // write pass; later windows are evaluated again there
+  uint32_t held_pk[kGatherHeld], held_own[kGatherHeld];
   uint32_t live_total = 0;
-  for (uint32_t base = 0; base < total; base += kWave) {
+#pragma unroll
+  for (int u = 0; u < kGatherHeld; ++u) {
+    held_pk[u] = 0u;
+    held_own[u] = 0u;
+    const uint32_t base = static_cast<uint32_t>(u * kWave);
+    if (base >= total) continue;  // wave-uniform
+    const uint32_t item = base + static_cast<uint32_t>(lane);
+    bool live = false;
+    if (item < total) {
+      int own, row;
+      uint32_t tx0;
+      const uint32_t nt = row_item<kRect>(s_set, s_rex, item, own, row, tx0);
+      live = nt > 0u;
+      if (live) {
+        atomicAdd(&s_cnt[row], 1u);
+        held_pk[u] = pack_row_span(tx0, nt, row);  // nonzero: nt >= 1
+        held_own[u] = static_cast<uint32_t>(own);
+      }
+    }
+    live_total += static_cast<uint32_t>(__popcll(__ballot(live ? 1 : 0)));
+  }
+  for (uint32_t base = kGatherHeld * kWave; base < total; base += kWave) {
     const uint32_t item = base + static_cast<uint32_t>(lane);
     bool live = false;
     if (item < total) {
@@ -1192,7 +1219,18 @@ __global__ __launch_bounds__(256) void span_gather_kernel(const SplatRec* __rest
   uint32_t slot = s_base;
   for (int q = 0; q < wave; ++q) slot += s_wcnt[q];
   const uint64_t lt = lanemask_lt(lane);
-  for (uint32_t base = 0; base < total; base += kWave) {
+#pragma unroll
+  for (int u = 0; u < kGatherHeld; ++u) {
+    if (static_cast<uint32_t>(u * kWave) >= total) continue;  // wave-uniform
+    const bool live = held_pk[u] != 0u;
+    const uint64_t lv = __ballot(live ? 1 : 0);
+    if (live) {
+      const int64_t p = static_cast<int64_t>(slot) + __popcll(lv & lt);
+      if (p < gathered_cap) gathered[p] = make_uint2(s_gid[held_own[u]], held_pk[u]);
+    }
+    slot += static_cast<uint32_t>(__popcll(lv));
+  }
+  for (uint32_t base = kGatherHeld * kWave; base < total; base += kWave) {
     const uint32_t item = base + static_cast<uint32_t>(lane);
     int own = 0, row = 0;
     uint32_t tx0 = 0, nt = 0;
@@ -1211,7 +1249,35 @@ __global__ __launch_bounds__(256) void span_gather_kernel(const SplatRec* __rest
 // (rowhist, scanned) + the earlier wavefronts' spans of that row + the span's rank among the
 // wavefront's earlier spans of that row. Ranks inside a window of 64 spans come from a
 // coverage mask per row (each span ORs its lane bit in; the rank is the number of lower bits).
-// Writes (Gaussian, tx0 | nt << 16).
+// Writes (Gaussian, tx0 | nt << 16). A wavefront's first kPlaceHeld windows are loaded once,
+// all loads issued together, and serve both the counting and the placement; longer quarters
+// read the rest as they go.
+constexpr int kPlaceHeld = 8;
+
+// One window of up to 64 spans of a wavefront, in lane order (lane holds e when live).
+__device__ __forceinline__ void place_window(bool live, uint2 e, int lane, uint64_t below, uint32_t* my_pos,
+                                             unsigned long long* s_cov, uint2* __restrict__ spans,
+                                             int64_t span_cap) {
+  int row = 0;
+  if (live) {
+    row = static_cast<int>(e.y >> 21);
+    atomicOr(&s_cov[row], 1ull << lane);
+  }
+  wave_sync();
+  unsigned long long cov = 0ull;
+  if (live) {
+    cov = s_cov[row];
+    const int64_t pos = static_cast<int64_t>(my_pos[row]) + __popcll(cov & below);
+    if (pos < span_cap) spans[pos] = make_uint2(e.x, (e.y & 0x3ffu) | (((e.y >> 10) & 0x7ffu) << 16));
+  }
+  wave_sync();  // every lane has read its row's position and mask
+  if (live && (cov & below) == 0ull) {  // the row's lowest lane advances it and clears the mask
+    my_pos[row] += static_cast<uint32_t>(__popcll(cov));
+    s_cov[row] = 0ull;
+  }
+  wave_sync();
+}
+
 __global__ __launch_bounds__(256) void span_place_kernel(const uint2* __restrict__ gathered,
                                                          const uint2* __restrict__ chunk_info,
                                                          const uint32_t* __restrict__ rowhist,
@@ -1229,18 +1295,30 @@ __global__ __launch_bounds__(256) void span_place_kernel(const uint2* __restrict
   uint32_t* s_pos = s_dyn + align4i(tiles_y + 1);  // [kSpanWaves][ty4]
   unsigned long long* s_cov =
       reinterpret_cast<unsigned long long*>(s_pos + kSpanWaves * ty4) + static_cast<int64_t>(wave) * ty4;
-  span_row_bases<256>(rowtot, tiles_y, s_rbase, s_wsum);
   const int c = xcd_tile(blockIdx.x, gridDim.x);
   const uint2 info = chunk_info[c];
+  const uint32_t q0 = static_cast<uint32_t>((static_cast<uint64_t>(info.y) * wave) / kSpanWaves);
+  const uint32_t q1 = static_cast<uint32_t>((static_cast<uint64_t>(info.y) * (wave + 1)) / kSpanWaves);
+  uint2 held[kPlaceHeld];
+#pragma unroll
+  for (int u = 0; u < kPlaceHeld; ++u) {
+    const uint32_t i = q0 + static_cast<uint32_t>(u * kWave + lane);
+    const int64_t p = static_cast<int64_t>(info.x) + i;
+    held[u] = (i < q1 && p < gathered_cap) ? gathered[p] : make_uint2(0u, 0u);
+  }
+  span_row_bases<256>(rowtot, tiles_y, s_rbase, s_wsum);
   if (info.y == 0u) return;  // the whole workgroup: no spans
   uint32_t* my_pos = s_pos + wave * ty4;
   for (int q = threadIdx.x; q < kSpanWaves * ty4; q += 256) s_pos[q] = 0u;
   for (int q = lane; q < ty4; q += kWave) s_cov[q] = 0ull;
   __syncthreads();
-  const uint32_t q0 = static_cast<uint32_t>((static_cast<uint64_t>(info.y) * wave) / kSpanWaves);
-  const uint32_t q1 = static_cast<uint32_t>((static_cast<uint64_t>(info.y) * (wave + 1)) / kSpanWaves);
   // count this quarter's spans per row
-  for (uint32_t i = q0 + lane; i < q1; i += kWave) {
+#pragma unroll
+  for (int u = 0; u < kPlaceHeld; ++u) {
+    const uint32_t i = q0 + static_cast<uint32_t>(u * kWave + lane);
+    if (i < q1 && static_cast<int64_t>(info.x) + i < gathered_cap) atomicAdd(&my_pos[held[u].y >> 21], 1u);
+  }
+  for (uint32_t i = q0 + kPlaceHeld * kWave + lane; i < q1; i += kWave) {
     const int64_t p = static_cast<int64_t>(info.x) + i;
     if (p < gathered_cap) atomicAdd(&my_pos[gathered[p].y >> 21], 1u);
   }
@@ -1256,30 +1334,19 @@ __global__ __launch_bounds__(256) void span_place_kernel(const uint2* __restrict
   }
   __syncthreads();
   const uint64_t below = lanemask_lt(lane);
-  for (uint32_t i0 = q0; i0 < q1; i0 += kWave) {
+#pragma unroll
+  for (int u = 0; u < kPlaceHeld; ++u) {
+    const uint32_t i0 = q0 + static_cast<uint32_t>(u * kWave);
+    if (i0 >= q1) break;  // wave-uniform
+    const uint32_t i = i0 + static_cast<uint32_t>(lane);
+    place_window(i < q1 && static_cast<int64_t>(info.x) + i < gathered_cap, held[u], lane, below, my_pos, s_cov,
+                 spans, span_cap);
+  }
+  for (uint32_t i0 = q0 + kPlaceHeld * kWave; i0 < q1; i0 += kWave) {
     const uint32_t i = i0 + static_cast<uint32_t>(lane);
     const int64_t p = static_cast<int64_t>(info.x) + i;
     const bool live = i < q1 && p < gathered_cap;
-    uint2 e = make_uint2(0u, 0u);
-    int row = 0;
-    if (live) {
-      e = gathered[p];
-      row = static_cast<int>(e.y >> 21);
-      atomicOr(&s_cov[row], 1ull << lane);
-    }
-    wave_sync();
-    unsigned long long cov = 0ull;
-    if (live) {
-      cov = s_cov[row];
-      const int64_t pos = static_cast<int64_t>(my_pos[row]) + __popcll(cov & below);
-      if (pos < span_cap) spans[pos] = make_uint2(e.x, (e.y & 0x3ffu) | (((e.y >> 10) & 0x7ffu) << 16));
-    }
-    wave_sync();  // every lane has read its row's position and mask
-    if (live && (cov & below) == 0ull) {  // the row's lowest lane advances it and clears the mask
-      my_pos[row] += static_cast<uint32_t>(__popcll(cov));
-      s_cov[row] = 0ull;
-    }
-    wave_sync();
+    place_window(live, live ? gathered[p] : make_uint2(0u, 0u), lane, below, my_pos, s_cov, spans, span_cap);
   }
 }
 
