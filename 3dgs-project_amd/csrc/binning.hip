@@ -681,15 +681,17 @@ __global__ __launch_bounds__(256) void emit_kernel(const SplatRec* __restrict__ 
 
   for (int64_t j0 = ja; j0 < jb; j0 += kWave) {
     const int64_t j = j0 + lane;
-    uint32_t off = 0, cap = 0, rows = 0;
+    uint32_t off = 0, cap = 0, rows = 0, gj = 0;
     if (j < jb) {
+      // (the Gaussian's id is loaded beside its offsets, not after them)
+      gj = order ? order[j] : static_cast<uint32_t>(j);
       off = offs[j];
       cap = offs[j + 1] - off;
     }
     EmitSetup es = {};
     uint32_t g = 0;
     if (cap) {
-      g = order ? order[j] : static_cast<uint32_t>(j);
+      g = gj;
       if constexpr (kRect) {
         const int4 r = clamp_rect(rects[g], tiles_x, tiles_y);
         es.d = r;
