@@ -2028,8 +2028,10 @@ static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dk
   const size_t lds_place = static_cast<size_t>(a4(tiles_y + 1) + kSpanWaves * a4(tiles_y) * 3) * 4;
   const int tx4 = a4(tiles_x + 1);
   const size_t lds_ccount = (static_cast<size_t>(a4(tiles_y + 1)) + kSpanWaves * tx4) * 4;
-  // placement windows per batch: as many as keep the LDS within 64 KB
-  const int R = tiles_x <= 64 ? 8 : tiles_x <= 128 ? 4 : tiles_x <= 256 ? 2 : 1;
+  // placement windows per batch: fewer windows cost more wavefront syncs per window, more cost LDS
+  // and so occupancy; up to 128 tile columns the LDS stays near 36 KB (4 workgroups per CU)
+  // (3M SH3, 123 columns: 351 us with 2 windows, 363 with 4, 379 with 1)
+  const int R = tiles_x <= 64 ? 4 : tiles_x <= 256 ? 2 : 1;
   const size_t lds_cwrite =
       (static_cast<size_t>(a4(tiles_y + 1)) + kSpanWaves * tx4 +
        kSpanWaves * (R * 3 * tx4 + 2 * kWaveSpans + (kWaveSpans + 4) + kOwnerTable / 4)) * 4;
@@ -2056,11 +2058,9 @@ static void bin_spans(const SplatRec* rec, const int4* rects, const uint32_t* dk
                      colhist, ranges, tiles_x, tiles_y, L.span_cap, L.chunk_cap, m, point_list, sorted_keys, dkey_of, \
                      dkey0)
   if (sorted_keys) {
-    if (R == 8) GS_SPAN_WRITE(true, 8); else if (R == 4) GS_SPAN_WRITE(true, 4);
-    else if (R == 2) GS_SPAN_WRITE(true, 2); else GS_SPAN_WRITE(true, 1);
+    if (R == 4) GS_SPAN_WRITE(true, 4); else if (R == 2) GS_SPAN_WRITE(true, 2); else GS_SPAN_WRITE(true, 1);
   } else {
-    if (R == 8) GS_SPAN_WRITE(false, 8); else if (R == 4) GS_SPAN_WRITE(false, 4);
-    else if (R == 2) GS_SPAN_WRITE(false, 2); else GS_SPAN_WRITE(false, 1);
+    if (R == 4) GS_SPAN_WRITE(false, 4); else if (R == 2) GS_SPAN_WRITE(false, 2); else GS_SPAN_WRITE(false, 1);
   }
 #undef GS_SPAN_WRITE
   stage_mark("span_write", st);
