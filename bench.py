@@ -366,8 +366,13 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
     targets = [torch.rand(3, c.height, c.width, generator=g).cuda() for c in cams]
     Ks = [_K(c) for c in cams]
     n = m.shape[0]
-    out = {"workload": f"{n} Gaussians SH3 {cams[0].width}x{cams[0].height}: fwd, L1+D-SSIM (11x11, lambda 0.2), "
-                       f"bwd, fused Adam over 59 fp32 parameters per Gaussian",
+    n_par = sum(t[0].numel() for t in P.values())  # fp32 parameters per Gaussian
+    deg = int(round(sh.shape[1] ** 0.5)) - 1
+    # Adam moves 28 bytes per element: reads parameter, gradient and both moments, writes
+    # parameter and both moments
+    row_bytes = 28 * n_par
+    out = {"workload": f"{n} Gaussians SH{deg} {cams[0].width}x{cams[0].height}: fwd, L1+D-SSIM (11x11, lambda 0.2), "
+                       f"bwd, fused Adam over {n_par} fp32 parameters per Gaussian",
            "lr": TRAIN_LR}
     for mode in ("dense", "masked"):
         params = {k: torch.nn.Parameter(v.clone()) for k, v in P.items()}
@@ -401,7 +406,7 @@ def train_step_bench(scene, steps: int, warmup: int) -> dict:
         step_ms = (time.perf_counter() - t0) * 1000.0 / steps
         adam_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
         vis_sum = sum(int((t > 0).sum().item()) for t in touched) / steps
-        nbytes = 1652 * n if mode == "dense" else int(1652 * vis_sum) + 4 * n
+        nbytes = row_bytes * n if mode == "dense" else int(row_bytes * vis_sum) + 4 * n
         out[mode] = {"step_ms": round(step_ms, 4), "adam_ms": round(adam_ms, 4),
                      "adam_hbm_gbs": round(nbytes / (adam_ms * 1e6), 1),
                      "adam_hbm_frac": round(nbytes / (adam_ms * 1e6) / HBM_PEAK_GBS, 4),
