@@ -112,6 +112,7 @@ _SIGS = {
     "gs2d_rects_toy": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "gs2d_rects_phase0": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp]),
     "gs2d_pack": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "gs2d_unpack_grads": (_i32, [_i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "gs2d_blend_fwd": (_i32, [_i32, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _i32, C.POINTER(C.c_double), _vp, _vp, _vp,
                               _vp, _vp, _vp, _vp, _vp]),
     "gs2d_blend_bwd_bucket": (_i32, [_i32, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp,

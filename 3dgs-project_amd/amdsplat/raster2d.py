@@ -131,14 +131,14 @@ def blend_fwd(rules: int, rec: torch.Tensor, ranges: torch.Tensor, range_stride:
     dt = rec.dtype
     tx, ty = tiles_of(width, height)
     shape = (3, height, width) if rules == TOY2D else (height, width, 3)
+    # every output is written whole by the kernel (each pixel, each tile, each bucket slot)
     image = torch.empty(shape, dtype=dt, device=dev)
-    final_T = torch.ones(height, width, dtype=dt, device=dev)
-    n_contrib = torch.zeros(height, width, dtype=torch.int32, device=dev)
-    last_contrib = torch.zeros(height, width, dtype=torch.int32, device=dev)
+    final_T = torch.empty(height, width, dtype=dt, device=dev)
+    n_contrib = torch.empty(height, width, dtype=torch.int32, device=dev)
+    last_contrib = torch.empty(height, width, dtype=torch.int32, device=dev)
     tile_max = torch.empty(tx * ty, dtype=torch.int32, device=dev)
     if save_ckpt:
-        alloc = torch.zeros if rules == TOY2D else torch.empty
-        ckpt = alloc(num_buckets, TILE_PIXELS, 4, dtype=dt, device=dev)
+        ckpt = torch.empty(num_buckets, TILE_PIXELS, 4, dtype=dt, device=dev)
     else:
         ckpt = torch.empty(0, dtype=dt, device=dev)
     call("gs2d_blend_fwd", rules, dtype_code(rec), ptr(rec), ptr(ranges), range_stride, ptr(point_list),
@@ -172,5 +172,13 @@ def blend_bwd_pixel(rules: int, rec, ranges, range_stride, point_list, width: in
 
 
 def split_grads(g: torch.Tensor):
-    """(dmeans [n,2], dshape [n,3], dopacity [n], dcolor [n,3]) from a grad record."""
-    return (g[:, 0:2].contiguous(), g[:, 2:5].contiguous(), g[:, 5].contiguous(), g[:, 6:9].contiguous())
+    """(dmeans [n,2], dshape [n,3], dopacity [n], dcolor [n,3]) from a grad record [n,12]
+    (one launch)."""
+    n = g.shape[0]
+    dm = torch.empty(n, 2, dtype=g.dtype, device=g.device)
+    ds = torch.empty(n, 3, dtype=g.dtype, device=g.device)
+    dop = torch.empty(n, dtype=g.dtype, device=g.device)
+    dc = torch.empty(n, 3, dtype=g.dtype, device=g.device)
+    if n:
+        call("gs2d_unpack_grads", dtype_code(g), ptr(g), n, ptr(dm), ptr(ds), ptr(dop), ptr(dc), stream(g.device))
+    return dm, ds, dop, dc

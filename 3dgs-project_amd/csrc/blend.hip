@@ -362,6 +362,16 @@ __global__ __launch_bounds__(kTilePixels) void blend_fwd_kernel(BlendArgs<S> a) 
         c[0] = Cr; c[1] = Cg; c[2] = Cb; c[3] = T;
       }
     }
+  } else if constexpr (R == kRulesToy2D) {
+    // toy2d leaves the buckets after the workgroup stopped zero (toy2d/csrc/rasterize.cu:131-133,
+    // 383, where the state buffer starts zeroed); here they are zeroed by the workgroup itself,
+    // so the buffer needs no clearing beforehand
+    if (ck) {
+      for (int q = (covered + kBucket - 1) / kBucket; q < (len + kBucket - 1) / kBucket; ++q) {
+        S* c = ck + static_cast<int64_t>(q) * kTilePixels * 4;
+        c[0] = S(0); c[1] = S(0); c[2] = S(0); c[3] = S(0);
+      }
+    }
   }
   if (inside) {
     const int64_t pix = static_cast<int64_t>(py) * a.W + px;

@@ -259,6 +259,44 @@ extern "C" int gs2d_rects_phase0(int dtype, const void* means, const void* chol,
   return check_launch("gs2d_rects_phase0");
 }
 
+// Gradient record [n, 12] -> dmeans [n, 2], dshape [n, 3], dopacity [n], dcolor [n, 3] (slots 0-1,
+// 2-4, 5, 6-8), a thread per splat.
+template <typename S>
+__global__ void unpack_grads_kernel(const S* __restrict__ g, int64_t n, S* __restrict__ dm, S* __restrict__ ds,
+                                    S* __restrict__ dop, S* __restrict__ dc) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const S* r = g + i * kGrad2D;
+  dm[2 * i] = r[0];
+  dm[2 * i + 1] = r[1];
+  ds[3 * i] = r[2];
+  ds[3 * i + 1] = r[3];
+  ds[3 * i + 2] = r[4];
+  dop[i] = r[5];
+  dc[3 * i] = r[6];
+  dc[3 * i + 1] = r[7];
+  dc[3 * i + 2] = r[8];
+}
+
+extern "C" int gs2d_unpack_grads(int dtype, const void* grad_rec, int64_t n, void* dmeans, void* dshape,
+                                 void* dopacity, void* dcolor, void* stream) {
+  clear_error();
+  GS_REQUIRE(dtype == GS_FLOAT32 || dtype == GS_FLOAT64, GS_ERR_ARG, "invalid dtype %d", dtype);
+  GS_REQUIRE(n >= 0, GS_ERR_ARG, "invalid size");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(grad_rec && dmeans && dshape && dopacity && dcolor, GS_ERR_ARG, "null pointer argument");
+  hipStream_t st = as_stream(stream);
+  if (dtype == GS_FLOAT32)
+    hipLaunchKernelGGL(unpack_grads_kernel<float>, dim3(grid256(n)), dim3(256), 0, st,
+                       static_cast<const float*>(grad_rec), n, static_cast<float*>(dmeans),
+                       static_cast<float*>(dshape), static_cast<float*>(dopacity), static_cast<float*>(dcolor));
+  else
+    hipLaunchKernelGGL(unpack_grads_kernel<double>, dim3(grid256(n)), dim3(256), 0, st,
+                       static_cast<const double*>(grad_rec), n, static_cast<double*>(dmeans),
+                       static_cast<double*>(dshape), static_cast<double*>(dopacity), static_cast<double*>(dcolor));
+  return check_launch("gs2d_unpack_grads");
+}
+
 extern "C" int gs2d_pack(int rules, int dtype, const void* means, const void* shape, const void* color,
                          const void* opacity, int64_t n, void* rec, void* stream) {
   clear_error();

@@ -18,11 +18,6 @@ from .binning import Bins
 from .reference import render_reference
 
 
-def _offsets_ext(bucket_offsets: torch.Tensor, num_buckets: int) -> torch.Tensor:
-    tail = torch.tensor([int(num_buckets)], dtype=torch.int32, device=bucket_offsets.device)
-    return torch.cat([bucket_offsets.to(torch.int32).reshape(-1), tail]).contiguous()
-
-
 def _check(means, conic, color, opacity):
     R2.require_cuda(means, conic, color, opacity, names=("means", "conic", "color", "opacity"))
     n = means.shape[0]
@@ -47,7 +42,8 @@ class _Ext:
     def forward(means, conic, color, opacity, bg, ranges, point_list, bucket_offsets, num_buckets, H, W,
                 save_buckets):
         rec = _pack(means, conic, color, opacity)
-        boff = _offsets_ext(bucket_offsets, num_buckets) if save_buckets else None
+        # (the kernels read each tile's first bucket only: no appended total is needed)
+        boff = bucket_offsets.to(torch.int32).contiguous() if save_buckets else None
         out, final_T, n_contrib, _, _, ckpt = R2.blend_fwd(
             R2.TOY2D, rec, ranges.contiguous(), 2, point_list.contiguous(), boff, int(num_buckets), int(W), int(H),
             bg=bg, save_ckpt=bool(save_buckets))
@@ -68,7 +64,7 @@ class _Ext:
         rec = _pack(means, conic, color, opacity)
         H, W = final_T.shape
         nb = int(bucket_to_tile.shape[0])
-        boff = offsets_ext if offsets_ext is not None else _offsets_ext(bucket_offsets, nb)
+        boff = offsets_ext if offsets_ext is not None else bucket_offsets.to(torch.int32).contiguous()
         g = R2.blend_bwd_bucket(R2.TOY2D, rec, ranges.contiguous(), 2, point_list.contiguous(), boff,
                                 bucket_to_tile.contiguous(), nb, W, H, out.contiguous(),
                                 dL_dout.contiguous().to(rec.dtype), n_contrib.contiguous(), tile_max,

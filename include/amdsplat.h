@@ -350,13 +350,22 @@ int gs2d_rects_phase0(int dtype, const void* means, const void* chol, const void
 int gs2d_pack(int rules, int dtype, const void* means, const void* shape, const void* color,
               const void* opacity, int64_t n, void* rec, void* stream);
 
+/* Splits a 2D gradient record grad_rec [n,12] of dtype into dmeans [n,2], dshape [n,3],
+ * dopacity [n] and dcolor [n,3] (slots 0-1, 2-4, 5, 6-8), the four tensors the reference's
+ * backward functions return (toy2d/csrc/rasterize.cu:405-406, phase0/csrc/macrotile/
+ * bindings.cpp:111-114), in one launch. */
+int gs2d_unpack_grads(int dtype, const void* grad_rec, int64_t n, void* dmeans, void* dshape, void* dopacity,
+                      void* dcolor, void* stream);
+
 /* 2D forward blend (replaces toy2d rasterize_forward, toy2d/csrc/rasterize.cu:366-394, and
  * phase0 forward, phase0/csrc/macrotile/bindings.cpp:156-178). Tile t's list is
  * point_list[ranges[t*range_stride] .. ranges[t*range_stride+1]) (range_stride 2 for (T,2)
  * ranges, 1 for (T+1) CSR offsets). Outputs: image ([3,H,W] toy2d, [H,W,3] phase0) of dtype,
  * final_T [H,W], n_contrib [H,W] (toy2d: last list position + 1; phase0: number of splats),
  * last_contrib [H,W] (phase0, may be NULL), tile_max [T] (may be NULL), ckpt [B,256,4]
- * (toy2d (T, C); phase0 (C, T); NULL = not saved; bucket_offsets [T+1] needed with it).
+ * (toy2d (T, C); phase0 (C, T); NULL = not saved; bucket_offsets [T], each tile's first bucket,
+ * needed with it). Every output is written whole: ckpt slots of buckets after a tile stopped hold
+ * zeros (toy2d) or the tile's final state (phase0).
  * bg: 3 host doubles (toy2d) or NULL. counters: NULL or 3 device uint64 (atomic adds,
  * checkpoint bytes, splat-pixel evaluations) that the kernels add to
  * (phase0/csrc/macrotile/splat2d_common.h:260-266). */
