@@ -1053,7 +1053,8 @@ __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(
     const int64_t cnt = a.bucket_list[0];
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBwdWaves;
     // the wavefront's index made scalar: the loop state and the LDS slots' addresses then live in
-    // scalar registers (64 VGPRs, 8 wavefronts per SIMD, against 77 and 6)
+    // scalar registers (64 VGPRs and 105 SGPRs, 7 wavefronts per SIMD by the SGPRs, against 77
+    // VGPRs and 6)
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     float* s_cws = s_c[R == kRules3D ? wave_s : 0];
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave_s; i < cnt; i += stride)
