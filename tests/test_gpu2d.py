@@ -121,6 +121,36 @@ def test_gs2d_forward_matches_oracle_bit_for_bit(name):
                     assert np.abs(ck[b, t] - rck[b, t]).max() <= 1e-6
 
 
+def test_gs2d_bucket_states_after_a_tile_stops_are_zero():
+    """600 nearly opaque splats over one 16x16 tile: every pixel stops within the first bucket, so the
+    workgroup stops at its second 256-entry round. The reference leaves the states of the buckets
+    it did not reach zero (toy2d/csrc/rasterize.cu:131-133, 383); here the output is allocated
+    without clearing (poisoned first with NaN through the caching allocator) and the kernel zeroes
+    those slots itself."""
+    n, H, W = 600, 16, 16
+    means = torch.full((n, 2), 8.0, device="cuda")
+    conic = torch.tensor([[0.01, 0.0, 0.01]], device="cuda").repeat(n, 1)
+    color = torch.rand(n, 3, generator=torch.Generator().manual_seed(3)).cuda()
+    opacity = torch.full((n,), 0.99, device="cuda")
+    radii = torch.full((n,), 30, dtype=torch.int32, device="cuda")
+    depth = torch.arange(n, dtype=torch.float32, device="cuda")
+    bins = gs2d.bin_gaussians(means, radii, depth, H, W)
+    assert bins.num_buckets == 19
+    poison = torch.full((bins.num_buckets, 256, 4), float("nan"), device="cuda")
+    del poison
+    e = gs2d.raster.ext()
+    bg = torch.zeros(3, device="cuda")
+    out, fT, nc, bstate = e.forward(means, conic, color, opacity, bg, bins.ranges, bins.point_list,
+                                    bins.bucket_offsets, bins.num_buckets, H, W, True)
+    torch.cuda.synchronize()
+    # every pixel stopped within the first bucket (all 600 splats cover every pixel with alpha > 1/255)
+    assert int(nc.max()) < 32
+    b = bstate.cpu()
+    assert torch.equal(b[8:], torch.zeros_like(b[8:]))  # rounds the workgroup never started
+    assert torch.equal(b[0, :, 0], torch.ones(256))  # the first state: T = 1 (toy2d: T first)
+    assert not torch.isnan(b).any()
+
+
 @pytest.mark.parametrize("binning", ["spans", "radix"])
 def test_gs2d_bench_scene_against_oracle(binning, monkeypatch):
     """512x512, 50k Gaussians of the reference benchmark: pair / bucket counts of its results
