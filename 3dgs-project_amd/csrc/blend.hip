@@ -615,47 +615,58 @@ __device__ __forceinline__ double f64_of(uint32_t lo, uint32_t hi) {
   return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
 }
 
-// Transposing reduction of 9 per-lane values v[0..7], w over the wavefront (the 3D backward
-// without the |dL/dmean2d| sums): xor 32 with v_permlane32_swap over the pairs (v[i], v[i + 4]),
-// xor 16 with v_permlane16_swap over (s[i], s[i + 2]), xor 8 with DPP row_ror:8 over the last
-// pair, then the 8-lane group sums (half-row mirror, quad xor 1, quad xor 2); w is summed along
-// with each step. On return every lane of group g = lane / 8 holds the total of v[g] in u and
-// the total of w in uw. 26 instructions.
-__device__ __forceinline__ void wave_reduce9(const float* v, float w, float& u, float& uw) {
+// Reduction of one bucket-splat step of the 3D backward without the |dL/dmean2d| sums. In: the
+// lane's sums over its 4 pixels (one column) of h, h dy, h dy^2 and the three colour sums, and
+// the column's dx. The 4 lanes of a column (lane ^ 16, ^ 32) are summed first, transposing: xor
+// 32 with v_permlane32_swap over the pairs (h, red), (h dy, green), (h dy^2, blue), leaving the
+// h sums in lanes 0-31 and the colour sums in lanes 32-63; xor 16 with v_permlane16_swap, the
+// first sum in all 4 rows of 16 lanes and the other two split between even and odd rows. Only
+// then are the dx factors applied, once per column instead of once per lane, in row 0 alone
+// (f = dx there, 1 elsewhere). The four values of every lane are then summed over the 16 columns
+// of its row: xor 8 with DPP row_ror:8 over the pairs, then the 8-lane group sums (half-row
+// mirror, quad xor 1, quad xor 2). On return group g = lane / 8 holds in (u0, u1):
+//   g 0: (sum h dx, sum h dy)          g 1: (sum h dx^2, sum h dx dy)
+//   g 2: (sum h, sum h dy^2)           g 4: (red, green)       g 6: (red, blue)
+// (g 3, 5, 7 hold repeats). 25 instructions.
+__device__ __forceinline__ void wave_reduce_cols(float sh, float shy, float shyy, float cr, float cg, float cb,
+                                                 float dx, bool row0, float& u0, float& u1) {
   const int lane = threadIdx.x & 63;
-  float s[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false, false);
-    s[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  float s0, s1, s2;
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sh), __float_as_uint(cr), false, false);
+    s0 = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
   {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(w), __float_as_uint(w), false, false);
-    w = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-  float t[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s[i]), __float_as_uint(s[i + 2]), false, false);
-    t[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(shy), __float_as_uint(cg), false, false);
+    s1 = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
   {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
-    w = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(shyy), __float_as_uint(cb), false, false);
+    s2 = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
+  float t0, t1;
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s0), __float_as_uint(s0), false, false);
+    t0 = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // every row: its quarter's first sum
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s1), __float_as_uint(s2), false, false);
+    t1 = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // even rows s1, odd rows s2
+  }
+  const float f = row0 ? dx : 1.0f;
+  const float v0 = t0 * f, v1 = v0 * f, v3 = t1 * f;
   const bool b3 = (lane & 8) != 0;
-  u = (b3 ? t[1] : t[0]) + dpp<0x128>(b3 ? t[0] : t[1]);  // row_ror:8 = partner lane ^ 8
-  w += dpp<0x128>(w);
-  u += dpp<0x141>(u);  // row_half_mirror
-  w += dpp<0x141>(w);
-  u += dpp<0xB1>(u);  // quad_perm [1,0,3,2]
-  w += dpp<0xB1>(w);
-  u += dpp<0x4E>(u);  // quad_perm [2,3,0,1]
-  w += dpp<0x4E>(w);
+  u0 = (b3 ? v1 : v0) + dpp<0x128>(b3 ? v0 : v1);  // row_ror:8 = partner lane ^ 8
+  u1 = (b3 ? v3 : t1) + dpp<0x128>(b3 ? t1 : v3);
+  u0 += dpp<0x141>(u0);  // row_half_mirror
+  u1 += dpp<0x141>(u1);
+  u0 += dpp<0xB1>(u0);  // quad_perm [1,0,3,2]
+  u1 += dpp<0xB1>(u1);
+  u0 += dpp<0x4E>(u0);  // quad_perm [2,3,0,1]
+  u1 += dpp<0x4E>(u1);
   // (the totals are formed here, with every lane active, so that the DPP moves fold into the
   // adds rather than the adds sinking into the owners' branch)
-  asm volatile("" : "+v"(u), "+v"(w));
-  uw = w;
+  asm volatile("" : "+v"(u0), "+v"(u1));
 }
 
 __device__ __forceinline__ void wave_reduce12(const double* v, double& u0, double& u1) {
@@ -864,18 +875,36 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     // With |dL/dmean2d| (kAbs) the 12 sums are reduced by wave_reduce12 and the final gradient of
     // the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total): k 0, 1 (mean2d):
     // -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity): u; colour and
-    // |dL/dmean2d|: u. Without, wave_reduce9 reduces v = (sum h dx, the three conic sums, sum h,
-    // colour) and w = sum h dy, and group g of 8 lanes owns v[g]: group 0 both mean2d values
-    // (lanes 0 and 1: -(A u + B w), -(B u + C w)), groups 1-3 the conic (-u/2, -u, -u/2), group
-    // 4 the opacity and groups 5-7 the colour (u). The opacity column holds sum h = sum alpha
-    // dL/dalpha = opacity dL/dopacity: the preprocess backward divides by the opacity once per
-    // Gaussian (in float64) instead of every bucket-splat step here. The lane-constant parts are
-    // chosen here.
-    const bool k0 = kAbs ? kidx == 0 : (grp == 0 && lo == 0);
-    const bool k1 = kAbs ? kidx == 1 : (grp == 0 && lo == 1);
-    const int kslot = kAbs ? kidx : (grp == 0 ? lo : grp + 1);  // the grad2d column
-    const float kc = (kslot == 2 || kslot == 4) ? -0.5f : kslot == 3 ? -1.0f : kslot >= 5 ? 1.0f : 0.0f;
-    const bool live_owner = kAbs ? owner : (grp == 0 ? lo < 2 : lo == 0);
+    // |dL/dmean2d|: u. Without, wave_reduce_cols leaves two totals (u0, u1) in each 8-lane group
+    // and the gradient of a lane is c0 u0 + c1 u1: lanes 0 and 1 the mean2d values from (sum h dx,
+    // sum h dy): -(A u0 + B u1), -(B u0 + C u1); lanes 8 and 9 the conic A and B (-u0/2, -u1),
+    // lanes 16 and 17 the opacity (u0) and the conic C (-u1/2), lanes 32, 33 and 49 the colour.
+    // The opacity column holds sum h = sum alpha dL/dalpha = opacity dL/dopacity: the preprocess
+    // backward divides by the opacity once per Gaussian (in float64) instead of every
+    // bucket-splat step here. The lane-constant parts are chosen here.
+    const bool k0 = kAbs ? kidx == 0 : lane == 0;
+    const bool k1 = kAbs ? kidx == 1 : lane == 1;
+    int kslot;  // the grad2d column of the lane's gradient (-1: none)
+    float kc = 0.0f, kc0 = 0.0f, kc1 = 0.0f;
+    if constexpr (kAbs) {
+      kslot = owner ? kidx : -1;
+      kc = (kslot == 2 || kslot == 4) ? -0.5f : kslot == 3 ? -1.0f : kslot >= 5 ? 1.0f : 0.0f;
+    } else {
+      kslot = lane == 0    ? 0
+              : lane == 1  ? 1
+              : lane == 8  ? 2
+              : lane == 9  ? 3
+              : lane == 16 ? 5
+              : lane == 17 ? 4
+              : lane == 32 ? 6
+              : lane == 33 ? 7
+              : lane == 49 ? 8
+                           : -1;
+      kc0 = lane == 8 ? -0.5f : (lane == 16 || lane == 32) ? 1.0f : 0.0f;
+      kc1 = lane == 9 ? -1.0f : lane == 17 ? -0.5f : (lane == 33 || lane == 49) ? 1.0f : 0.0f;
+    }
+    const bool row0 = lane < 16;
+    const bool live_owner = kslot >= 0;
     const bool conic_owner = kslot >= 2 && kslot <= 4;
     const int64_t kofs = kslot;
     for (int j = 0; j < jmax; ++j) {
@@ -925,29 +954,30 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
         T[r] = T[r] * oma;
       }
       if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
-      const float dxsh = cl.dx * sh;
-      const float cxx = cl.dx * dxsh, cxy = cl.dx * shy;  // the conic sums of the lane's column
       const bool wide = ((plane[kPixPerLane] >> j) & 1u) != 0u;  // wave-uniform
       if (wide) {
-        // each lane reads its own three values back after the float32 reduction
-        s_c[lane] = cxx;
-        s_c[kWave + lane] = cxy;
+        // each lane parks the conic sums of its pixels, read back after the float32 reduction
+        const float dxsh = cl.dx * sh;
+        s_c[lane] = cl.dx * dxsh;
+        s_c[kWave + lane] = cl.dx * shy;
         s_c[2 * kWave + lane] = shyy;
       }
-      const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : 0.0f;
-      const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : 0.0f;
-      const float c = kc;
       float g;
       if constexpr (kAbs) {
+        const float dxsh = cl.dx * sh;
+        const float cxx = cl.dx * dxsh, cxy = cl.dx * shy;  // the conic sums of the lane's column
+        const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : 0.0f;
+        const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : 0.0f;
         S acc[12] = {dxsh, shy, cxx, cxy, shyy, sh, cr, cg, cb, ab0, ab1, 0.0f};
         S u0, u1;
         wave_reduce12(acc, u0, u1);
-        g = fmaf(c0, u0, fmaf(c1, u1, c * (lo == 0 ? u0 : u1)));
+        g = fmaf(c0, u0, fmaf(c1, u1, kc * (lo == 0 ? u0 : u1)));
       } else {
-        const float v[8] = {dxsh, cxx, cxy, shyy, sh, cr, cg, cb};
-        float u, uw;
-        wave_reduce9(v, shy, u, uw);
-        g = fmaf(c0, u, fmaf(c1, uw, c * u));
+        float u0, u1;
+        wave_reduce_cols(sh, shy, shyy, cr, cg, cb, cl.dx, row0, u0, u1);
+        const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : kc0;
+        const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : kc1;
+        g = fmaf(c0, u0, c1 * u1);
       }
       // (an elongated splat's conic sums go to the float64 buffer below instead)
       if (live_owner && !(wide && conic_owner))
