@@ -748,6 +748,12 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
 // Bucketed backward
 // ---------------------------------------------------------------------------------------
 constexpr int kBwdWaves = 4;
+// Staged entries that hold the 3D backward's per-lane coefficient pairs (64 float2)
+constexpr int kCoefSlots = (2 * kWave * 4 + static_cast<int>(sizeof(Staged<float>)) - 1) /
+                           static_cast<int>(sizeof(Staged<float>));
+static_assert(sizeof(Staged<float>) == 48 && offsetof(Staged<float>, n0) == 36 && offsetof(Staged<float>, n1) == 40 &&
+                  offsetof(Staged<float>, nat2) == 44,
+              "the 3D backward reads (n0, n1) and (n1, nat2) as float pairs of a staged splat");
 
 // kAbs (3D): also accumulate |dL/dmean2d| (grad2d slots 9-10) for densification by absolute
 // gradient, as Faster-GS's compute_abs_grad instantiation does; without it those slots are
@@ -847,6 +853,13 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       }
     }
   }
+  if constexpr (R == kRules3D && !kAbs) {
+    // the coefficient pair of each lane's gradient, g = -(c0 u0 + c1 u1) of the reduction's totals
+    // (u0, u1); lanes 0 and 1 read theirs, the splat's (A, B) and (B, C), from the staged splat
+    float* kc = reinterpret_cast<float*>(s_sp + kBucket) + 2 * lane;
+    kc[0] = lane == 8 ? 0.5f : (lane == 16 || lane == 32) ? -1.0f : 0.0f;
+    kc[1] = lane == 9 ? 1.0f : lane == 17 ? 0.5f : (lane == 33 || lane == 49) ? -1.0f : 0.0f;
+  }
   // (scalar: the splat loop is uniform over the wavefront)
   const int jmax = __builtin_amdgcn_readfirstlane(min(bsize, wave_max(lim_max)));
   wave_sync();
@@ -858,7 +871,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
   if constexpr (R == kRules3D) {
     // The lane's 4 pixels share a column: the column terms of the power and of the mean
     // gradient are computed once per splat, and per pixel only dy-dependent sums are kept;
-    // the dx factors are applied to the lane's sums before the reduction. Pixel r of every
+    // the dx factors are applied in the reduction, once per column. Pixel r of every
     // lane lies in strip r, so the strip test and the wavefront's largest limit of row r are
     // scalar; inside, the pixel body has no branches: a lane past its limit or below the
     // alpha threshold blends alpha = 0, which leaves its T, rho and every sum unchanged.
@@ -876,16 +889,17 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     // the lane's value index k is c0 u0 + c1 u1 + c u (u = its own total): k 0, 1 (mean2d):
     // -(A u0 + B u1), -(B u0 + C u1); k 2, 4: -u/2; k 3: -u; k 5 (opacity): u; colour and
     // |dL/dmean2d|: u. Without, wave_reduce_cols leaves two totals (u0, u1) in each 8-lane group
-    // and the gradient of a lane is c0 u0 + c1 u1: lanes 0 and 1 the mean2d values from (sum h dx,
-    // sum h dy): -(A u0 + B u1), -(B u0 + C u1); lanes 8 and 9 the conic A and B (-u0/2, -u1),
-    // lanes 16 and 17 the opacity (u0) and the conic C (-u1/2), lanes 32, 33 and 49 the colour.
+    // and the gradient of a lane is -(c0 u0 + c1 u1): lanes 0 and 1 the mean2d values from
+    // (sum h dx, sum h dy), with (c0, c1) = (A, B) and (B, C) read from the staged splat; lanes 8
+    // and 9 the conic A and B (-u0/2, -u1), lanes 16 and 17 the opacity (u0) and the conic C
+    // (-u1/2), lanes 32, 33 and 49 the colour, their pairs read from a table of constants.
     // The opacity column holds sum h = sum alpha dL/dalpha = opacity dL/dopacity: the preprocess
     // backward divides by the opacity once per Gaussian (in float64) instead of every
     // bucket-splat step here. The lane-constant parts are chosen here.
     const bool k0 = kAbs ? kidx == 0 : lane == 0;
     const bool k1 = kAbs ? kidx == 1 : lane == 1;
     int kslot;  // the grad2d column of the lane's gradient (-1: none)
-    float kc = 0.0f, kc0 = 0.0f, kc1 = 0.0f;
+    float kc = 0.0f;
     if constexpr (kAbs) {
       kslot = owner ? kidx : -1;
       kc = (kslot == 2 || kslot == 4) ? -0.5f : kslot == 3 ? -1.0f : kslot >= 5 ? 1.0f : 0.0f;
@@ -900,9 +914,11 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
               : lane == 33 ? 7
               : lane == 49 ? 8
                            : -1;
-      kc0 = lane == 8 ? -0.5f : (lane == 16 || lane == 32) ? 1.0f : 0.0f;
-      kc1 = lane == 9 ? -1.0f : lane == 17 ? -0.5f : (lane == 33 || lane == 49) ? 1.0f : 0.0f;
     }
+    // where the lane's coefficient pair lies: lanes 0 and 1 in staged splat j (j * m01 entries
+    // on), the others in the table after the staged splats
+    const int m01 = lane < 2 ? static_cast<int>(sizeof(Staged<S>) / sizeof(S)) : 0;
+    const int cidx = lane < 2 ? 9 + lane : kBucket * static_cast<int>(sizeof(Staged<S>) / sizeof(S)) + 2 * lane;
     const bool row0 = lane < 16;
     const bool live_owner = kslot >= 0;
     const bool conic_owner = kslot >= 2 && kslot <= 4;
@@ -922,7 +938,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
         ab0 = opaque_zero();
         ab1 = opaque_zero();
       }
-      bool used = false;
+      uint64_t used = 0;  // the lanes that blended the splat (a lane mask: scalar)
 #pragma unroll
       for (int r = 0; r < kPixPerLane; ++r) {
         if (((plane[r] >> j) & 1u) == 0u || j >= lim_row[r]) continue;  // wave-uniform
@@ -931,8 +947,11 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
         const float dy = sp.my - pyf[r];
         const float G = Ru::falloff(Ru::power(sp, cl, dy));
         const float a_raw = sp.o * G;
-        const bool take = live && a_raw >= kAlphaMin;
-        used = used || take;
+        const bool above = a_raw >= kAlphaMin;
+        const bool take = live && above;
+        // (the masks of the two compares themselves: a ballot of their conjunction would first
+        // turn it into a per-lane value)
+        used |= __builtin_amdgcn_ballot_w64(live) & __builtin_amdgcn_ballot_w64(above);
         const float alpha = take ? a_raw : 0.0f;
         const float w = T[r] * alpha;
         const float dot = fmaf(Gb[r], sp.cb, fmaf(Gg[r], sp.cg, Gr[r] * sp.cr));
@@ -953,7 +972,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
         }
         T[r] = T[r] * oma;
       }
-      if (__ballot(used ? 1 : 0) == 0) continue;  // wave-uniform
+      if (used == 0) continue;
       const bool wide = ((plane[kPixPerLane] >> j) & 1u) != 0u;  // wave-uniform
       if (wide) {
         // each lane parks the conic sums of its pixels, read back after the float32 reduction
@@ -975,15 +994,14 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
       } else {
         float u0, u1;
         wave_reduce_cols(sh, shy, shyy, cr, cg, cb, cl.dx, row0, u0, u1);
-        const float c0 = k0 ? -sp.n0 : k1 ? -sp.n1 : kc0;
-        const float c1 = k0 ? -sp.n1 : k1 ? -sp.nat2 : kc1;
-        g = fmaf(c0, u0, c1 * u1);
+        const S* cp = reinterpret_cast<const S*>(s_sp) + (j * m01 + cidx);
+        g = fmaf(-cp[0], u0, -(cp[1] * u1));
       }
       // (an elongated splat's conic sums go to the float64 buffer below instead)
       if (live_owner && !(wide && conic_owner))
         atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[j]) * kGrad2D + kofs, g);
       if (wide) {  // the conic sums in float64
-        const int64_t id = __builtin_amdgcn_readfirstlane(s_id[j]);  // wave-uniform
+        const uint32_t id = __builtin_amdgcn_readfirstlane(s_id[j]);  // wave-uniform
         wave_sync();  // every lane's parked values
         // row k of 16 lanes (k < 3) sums value k of the 64 lanes: 4 values per lane in float64
         // (exactly), then the row's 16 partial sums; A, B, C = -1/2, -1, -1/2 times the sums of
@@ -1001,9 +1019,9 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
         t += dpp64<0x141>(t);  // row_half_mirror
         t += dpp64<0xB1>(t);   // quad_perm [1,0,3,2]
         t += dpp64<0x4E>(t);   // quad_perm [2,3,0,1]
-        if (r16 == 0 && k < 3) atomic_add_grad(a.conic64 + 4 * id + k, (k == 1 ? -1.0 : -0.5) * t);
+        if (r16 == 0 && k < 3) atomic_add_grad(a.conic64 + 4 * static_cast<uint64_t>(id) + k, (k == 1 ? -1.0 : -0.5) * t);
         // marks the splat's row for the preprocess backward, which then adds the float64 sums
-        if (lane == 48) a.grad_rec[id * kGrad2D + 11] = 1.0f;
+        if (lane == 48) a.grad_rec[static_cast<uint64_t>(id) * kGrad2D + 11] = 1.0f;
         wave_sync();  // the parked values are read before the next splat parks its own
       }
       if constexpr (kCount) atomics += kAbs ? NV : 9;
@@ -1063,7 +1081,8 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
 template <int R, typename S, bool kCount, bool kAbs = true, int kList = 0>
 __global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(
     BlendArgs<S> a) {
-  __shared__ Staged<S> s_sp[kBwdWaves][kBucket];
+  // (3D: the lanes' coefficient table after the wavefront's staged splats)
+  __shared__ Staged<S> s_sp[kBwdWaves][kBucket + (R == kRules3D ? kCoefSlots : 0)];
   __shared__ uint32_t s_m[kBwdWaves][kBucket];
   __shared__ uint32_t s_id[kBwdWaves][kBucket];
   // 3D: an elongated splat's three per-lane conic sums, parked over the float32 reduction
