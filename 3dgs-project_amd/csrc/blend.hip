@@ -748,8 +748,8 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
 // Bucketed backward
 // ---------------------------------------------------------------------------------------
 constexpr int kBwdWaves = 4;
-// Staged entries that hold the 3D backward's per-lane coefficient pairs (64 float2)
-constexpr int kCoefSlots = (2 * kWave * 4 + static_cast<int>(sizeof(Staged<float>)) - 1) /
+// Staged entries that hold the 3D backward's coefficient table (65 floats)
+constexpr int kCoefSlots = ((kWave + 1) * 4 + static_cast<int>(sizeof(Staged<float>)) - 1) /
                            static_cast<int>(sizeof(Staged<float>));
 static_assert(sizeof(Staged<float>) == 48 && offsetof(Staged<float>, n0) == 36 && offsetof(Staged<float>, n1) == 40 &&
                   offsetof(Staged<float>, nat2) == 44,
@@ -855,10 +855,16 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
   }
   if constexpr (R == kRules3D && !kAbs) {
     // the coefficient pair of each lane's gradient, g = -(c0 u0 + c1 u1) of the reduction's totals
-    // (u0, u1); lanes 0 and 1 read theirs, the splat's (A, B) and (B, C), from the staged splat
-    float* kc = reinterpret_cast<float*>(s_sp + kBucket) + 2 * lane;
-    kc[0] = lane == 8 ? 0.5f : (lane == 16 || lane == 32) ? -1.0f : 0.0f;
-    kc[1] = lane == 9 ? 1.0f : lane == 17 ? 0.5f : (lane == 33 || lane == 49) ? -1.0f : 0.0f;
+    // (u0, u1); lanes 0 and 1 read theirs, the splat's (A, B) and (B, C), from the staged splat,
+    // lane l >= 2 reads (t[l], t[l + 1]) of this table (consecutive words: no bank conflicts): the
+    // owners' pairs are lane 8 (1/2, 0), 9 (0, 1), 16 (-1, 0), 17 (0, 1/2), 32 (-1, 0), 33 (0, -1),
+    // 49 (0, -1), all others (0, 0)
+    float* kt = reinterpret_cast<float*>(s_sp + kBucket);
+    kt[lane] = lane == 8 || lane == 18 ? 0.5f
+               : lane == 10            ? 1.0f
+               : (lane == 16 || lane == 32 || lane == 34 || lane == 50) ? -1.0f
+                                                                       : 0.0f;
+    if (lane == 0) kt[kWave] = 0.0f;
   }
   // (scalar: the splat loop is uniform over the wavefront)
   const int jmax = __builtin_amdgcn_readfirstlane(min(bsize, wave_max(lim_max)));
@@ -918,7 +924,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     // where the lane's coefficient pair lies: lanes 0 and 1 in staged splat j (j * m01 entries
     // on), the others in the table after the staged splats
     const int m01 = lane < 2 ? static_cast<int>(sizeof(Staged<S>) / sizeof(S)) : 0;
-    const int cidx = lane < 2 ? 9 + lane : kBucket * static_cast<int>(sizeof(Staged<S>) / sizeof(S)) + 2 * lane;
+    const int cidx = lane < 2 ? 9 + lane : kBucket * static_cast<int>(sizeof(Staged<S>) / sizeof(S)) + lane;
     const bool row0 = lane < 16;
     const bool live_owner = kslot >= 0;
     const bool conic_owner = kslot >= 2 && kslot <= 4;
