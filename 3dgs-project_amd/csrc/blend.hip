@@ -902,8 +902,7 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
     // The opacity column holds sum h = sum alpha dL/dalpha = opacity dL/dopacity: the preprocess
     // backward divides by the opacity once per Gaussian (in float64) instead of every
     // bucket-splat step here. The lane-constant parts are chosen here.
-    const bool k0 = kAbs ? kidx == 0 : lane == 0;
-    const bool k1 = kAbs ? kidx == 1 : lane == 1;
+    const bool k0 = kidx == 0, k1 = kidx == 1;  // (kAbs) the lanes of the two mean2d values
     int kslot;  // the grad2d column of the lane's gradient (-1: none)
     float kc = 0.0f;
     if constexpr (kAbs) {
@@ -921,10 +920,12 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
               : lane == 49 ? 8
                            : -1;
     }
-    // where the lane's coefficient pair lies: lanes 0 and 1 in staged splat j (j * m01 entries
-    // on), the others in the table after the staged splats
-    const int m01 = lane < 2 ? static_cast<int>(sizeof(Staged<S>) / sizeof(S)) : 0;
-    const int cidx = lane < 2 ? 9 + lane : kBucket * static_cast<int>(sizeof(Staged<S>) / sizeof(S)) + lane;
+    // (without kAbs) the float index of the lane's coefficient pair in s_sp, j * m01 + cidx:
+    // lanes 0 and 1 in staged splat j, the others in the table after the staged splats
+    constexpr int kStagedFloats = static_cast<int>(sizeof(Staged<S>) / sizeof(S));
+    const int m01 = lane < 2 ? kStagedFloats : 0;
+    const int cidx = lane < 2 ? static_cast<int>(offsetof(Staged<S>, n0) / sizeof(S)) + lane
+                              : kBucket * kStagedFloats + lane;
     const bool row0 = lane < 16;
     const bool live_owner = kslot >= 0;
     const bool conic_owner = kslot >= 2 && kslot <= 4;
