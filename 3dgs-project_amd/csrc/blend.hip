@@ -627,7 +627,7 @@ __device__ __forceinline__ double f64_of(uint32_t lo, uint32_t hi) {
 // mirror, quad xor 1, quad xor 2). On return group g = lane / 8 holds in (u0, u1):
 //   g 0: (sum h dx, sum h dy)          g 1: (sum h dx^2, sum h dx dy)
 //   g 2: (sum h, sum h dy^2)           g 4: (red, green)       g 6: (red, blue)
-// (g 3, 5, 7 hold repeats). 25 instructions.
+// (g 3, 5, 7 hold repeats). 27 instructions, the dx products included.
 __device__ __forceinline__ void wave_reduce_cols(float sh, float shy, float shyy, float cr, float cg, float cb,
                                                  float dx, bool row0, float& u0, float& u1) {
   const int lane = threadIdx.x & 63;
