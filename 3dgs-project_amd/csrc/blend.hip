@@ -1169,6 +1169,13 @@ __global__ __launch_bounds__(kTilePixels) void blend_bwd_pixel_kernel(BlendArgs<
   }
   S acc0 = S(0), acc1 = S(0), acc2 = S(0);  // colour behind the current splat, over T
   uint32_t evals = 0, atomics = 0;
+  // toy2d: the wavefront's contributions to a splat reduced before the atomics (the phase0
+  // surface keeps one atomic per pixel and value: its backward A is that method, counted)
+  constexpr bool kPreReduce = R == kRulesToy2D;
+  const int lane = t & 63;
+  const int grp = lane >> 3, lo = lane & 7;
+  const int kidx = 6 * (grp >> 2) + 3 * ((grp >> 1) & 1) + 2 * (grp & 1) + lo;
+  const bool owner = lo < 2 && (2 * (grp & 1) + lo) < 3 && kidx < 9;
   for (int b0 = 0; b0 < len; b0 += kTilePixels) {
     __syncthreads();  // the previous batch is no longer in use
     const int k = len - 1 - (b0 + t);  // position in the tile list, back to front
@@ -1181,33 +1188,48 @@ __global__ __launch_bounds__(kTilePixels) void blend_bwd_pixel_kernel(BlendArgs<
     const int nb = min(kTilePixels, len - b0);
     for (int jj = 0; jj < nb; ++jj) {
       const int pos = len - 1 - (b0 + jj);
-      if (!inside || pos >= lim) continue;
-      const Staged<S> sp = s_sp[jj];
-      Eval<S> e;
-      ++evals;
-      if (!Ru::eval(sp, pxf, pyf, e)) continue;
-      const S oma = S(1) - e.alpha;
-      const S Tb = Tcur / oma;  // T in front of this splat
-      const S dot = G0 * (sp.cr - acc0) + G1 * (sp.cg - acc1) + G2 * (sp.cb - acc2);
-      acc0 = e.alpha * sp.cr + oma * acc0;
-      acc1 = e.alpha * sp.cg + oma * acc1;
-      acc2 = e.alpha * sp.cb + oma * acc2;
-      Tcur = Tb;
-      S dLda = Tb * dot;
-      if constexpr (Ru::kBackground) dLda += (-T_final / oma) * bg_dot;
-      S g[11];
+      S g[12];
 #pragma unroll
-      for (int q = 0; q < 11; ++q) g[q] = S(0);
-      const S w = e.alpha * Tb;
-      g[6] = w * G0;
-      g[7] = w * G1;
-      g[8] = w * G2;
-      shape_grads<R, S>(sp, e, dLda, g);
-      if constexpr (R == kRulesPhase0) g[5] = g[5] * sp.o * (S(1) - sp.o);
-      S* dst = a.grad_rec + static_cast<int64_t>(s_id[jj]) * kGrad2D;
+      for (int q = 0; q < 12; ++q) g[q] = S(0);
+      bool took = false;
+      if (inside && pos < lim) {
+        const Staged<S> sp = s_sp[jj];
+        Eval<S> e;
+        ++evals;
+        if (Ru::eval(sp, pxf, pyf, e)) {
+          const S oma = S(1) - e.alpha;
+          const S Tb = Tcur / oma;  // T in front of this splat
+          const S dot = G0 * (sp.cr - acc0) + G1 * (sp.cg - acc1) + G2 * (sp.cb - acc2);
+          acc0 = e.alpha * sp.cr + oma * acc0;
+          acc1 = e.alpha * sp.cg + oma * acc1;
+          acc2 = e.alpha * sp.cb + oma * acc2;
+          Tcur = Tb;
+          S dLda = Tb * dot;
+          if constexpr (Ru::kBackground) dLda += (-T_final / oma) * bg_dot;
+          const S w = e.alpha * Tb;
+          g[6] = w * G0;
+          g[7] = w * G1;
+          g[8] = w * G2;
+          shape_grads<R, S>(sp, e, dLda, g);
+          if constexpr (R == kRulesPhase0) g[5] = g[5] * sp.o * (S(1) - sp.o);
+          took = true;
+        }
+      }
+      if constexpr (kPreReduce) {
+        // the wavefront's pixels' gradients of the splat summed first (all lanes take the same
+        // list entry), then one atomic per value from its owner lane
+        if (__ballot(took ? 1 : 0) == 0) continue;  // wave-uniform
+        S u0, u1;
+        wave_reduce12(g, u0, u1);
+        if (owner) atomic_add_grad(a.grad_rec + static_cast<int64_t>(s_id[jj]) * kGrad2D + kidx, lo == 0 ? u0 : u1);
+        atomics += 9;
+      } else {
+        if (!took) continue;
+        S* dst = a.grad_rec + static_cast<int64_t>(s_id[jj]) * kGrad2D;
 #pragma unroll
-      for (int q = 0; q < 9; ++q) atomic_add_grad(dst + q, g[q]);
-      atomics += 9;
+        for (int q = 0; q < 9; ++q) atomic_add_grad(dst + q, g[q]);
+        atomics += 9;
+      }
     }
   }
   if (a.counters) {

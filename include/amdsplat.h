@@ -391,7 +391,9 @@ int gs2d_blend_bwd_bucket(int rules, int dtype, const void* rec, const uint32_t*
 
 /* 2D per-pixel backward (replaces toy2d rasterize_backward_pixel, toy2d/csrc/rasterize.cu:
  * 396-417, and phase0 backward_pixel, phase0/csrc/macrotile/bindings.cpp:180-199): back to
- * front, T recovered by division, one atomic per parameter per (pixel, splat) pair. */
+ * front, T recovered by division. phase0 rules: one atomic per parameter per (pixel, splat) pair
+ * (backward A, counted in counters[0]); toy2d rules: a wavefront's pixels' gradients of a splat
+ * summed first, then one atomic per parameter. */
 int gs2d_blend_bwd_pixel(int rules, int dtype, const void* rec, const uint32_t* ranges,
                          int range_stride, const uint32_t* point_list, int64_t n, int width,
                          int height, const double* bg, const void* final_T, const int32_t* limit,
