@@ -151,11 +151,12 @@ def test_gs2d_bucket_states_after_a_tile_stops_are_zero():
     assert not torch.isnan(b).any()
 
 
-@pytest.mark.parametrize("binning", ["spans", "radix"])
-def test_gs2d_bench_scene_against_oracle(binning, monkeypatch):
+@pytest.mark.parametrize("binning,backend", [("spans", "splat"), ("radix", "splat"), ("radix", "pixel")])
+def test_gs2d_bench_scene_against_oracle(binning, backend, monkeypatch):
     """512x512, 50k Gaussians of the reference benchmark: pair / bucket counts of its results
     file, bit-exact lists and counts, forward within 1e-5, gradients within 1e-4 (atomic order);
-    with either tile binning."""
+    with either tile binning, and the per-pixel backward (a wavefront's pixels' gradients of each
+    splat summed before its atomics) as well as the bucketed one."""
     monkeypatch.setattr(R2, "BINNING", binning)
     rows = json.loads((GOLD / "toy2d_bench_counts.json").read_text())["rows"]
     row = rows[1]
@@ -171,7 +172,7 @@ def test_gs2d_bench_scene_against_oracle(binning, monkeypatch):
     assert np.array_equal(bins.point_list.cpu().numpy(), pl)
     x = [t.cuda().requires_grad_(True) for t in (means, conic, color, opacity)]
     bg = torch.tensor([0.2, 0.5, 0.8])
-    out = gs2d.rasterize(*x, bins, bg.cuda())
+    out = gs2d.rasterize(*x, bins, bg.cuda(), backend=backend)
     dout = torch.randn(3, S, S, generator=torch.Generator().manual_seed(1))
     grads = torch.autograd.grad(out, x, dout.cuda())
     p = [t.numpy() for t in (means, conic, color, opacity)]
