@@ -347,8 +347,8 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
     grad_sh is a (DC, rest) pair when sh is. abs_grad: also sum |dL/dmean2d| into grad2d[:, 9:11]
     (densification by absolute gradient); otherwise those columns stay zero. The conic columns
     (2-4) of the elongated splats (2D condition number >= 256) are summed in float64 into
-    fs.last_conic64 [n, 4] instead, their rows marked in column 11; combined_grad2d(grad2d,
-    fs.last_conic64) gives all screen-space gradients.
+    fs.last_conic64 [n, 4] instead, their rows marked in column 11 (only those rows of it hold
+    sums); combined_grad2d(grad2d, fs.last_conic64) gives all screen-space gradients.
     counters: optional int64 [3] CUDA tensor that the blend backward adds its atomic count and
     pair-evaluation count to (slots 0 and 2)."""
     dev = means.device
@@ -398,10 +398,12 @@ def backward_pass(fs: ForwardState, means, log_scales, quats, opacity_logits, sh
 
 def combined_grad2d(grad2d: torch.Tensor, conic64: torch.Tensor | None) -> torch.Tensor:
     """The screen-space gradients of a backward as float64 [n, 12]: grad2d with the elongated
-    splats' float64 conic sums added to columns 2-4 (and their mark in column 11 cleared)."""
+    splats' float64 conic sums (the rows marked in column 11) added to columns 2-4, and the mark
+    cleared."""
     g = grad2d.double()
     if conic64 is not None:
-        g[:, 2:5] += conic64[:, :3]
+        marked = grad2d[:, 11] != 0  # the rows that hold float64 sums
+        g[marked, 2:5] += conic64[marked, :3]
     g[:, 11] = 0.0
     return g
 

@@ -234,13 +234,30 @@ def check_gradients(sc, cam, name):
         assert e < GRAD_TOL, f"{name}/{gname}: rel err {e:.2e}"
 
 
-def test_grad2d_matches_oracle_replay():
-    sc = make("partial_tiles", seed=2)
+@pytest.mark.parametrize("elongated", [False, True])
+def test_grad2d_matches_oracle_replay(elongated):
+    """The backward's screen gradients against the oracle's float64 sums, with the forward's
+    screen-gradient buffer (grad2d and the elongated splats' float64 conic sums) taken from memory
+    that held NaNs: the forward zeroes it while it blends (elongated: 3D scales over two decades,
+    so that splats of 2D axis ratio 16 and more occur and take the float64 path)."""
+    if elongated:
+        sc = scenes.small_scene(20_000, 333, 250, seed=2, sh_coeffs=16, scale=(0.002, 0.2), opacity=(0.05, 0.95),
+                                depth=(2.0, 8.0))
+    else:
+        sc = make("partial_tiles", seed=2)
     cam = sc.cameras[0]
     p, fs = gpu_forward(sc, 3)
-    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(3))
-    g2 = R.backward_pass(fs, *p, gi.cuda())[5]
+    fs.grad2d.fill_(float("nan"))
+    fs.grad_conic64.fill_(float("nan"))
+    del fs  # the same forward again takes the same blocks from the caching allocator
+    p, fs = gpu_forward(sc, 3)
     ref = O.render(*[t.numpy() for t in sc.params()], cam, 3, bg=BG)
+    gi = torch.randn(3, cam.height, cam.width, generator=torch.Generator().manual_seed(3))
+    gi[:, torch.from_numpy(ref["amb"])] = 0.0  # (near-threshold pixels: either branch is right)
+    g2 = R.backward_pass(fs, *p, gi.cuda())[5]
+    marked = np_(g2)[:, 11] != 0
+    assert marked.sum() > 0 or not elongated, "the scene should hold elongated splats"
+    assert np.isfinite(np_(fs.last_conic64)[marked]).all()
     o2, oc = O.blend_bwd(ref["rec"], ref["point_list"], ref["ranges"], ref["bucket_offsets"], cam.width, cam.height,
                          ref["image"], gi.numpy(), ref["final_T"], ref["n_contrib"], ref["tile_max"], ref["ckpt"],
                          sc.n, conic64=True)
@@ -249,6 +266,7 @@ def test_grad2d_matches_oracle_replay():
     o2 = o2.astype(np.float64)
     o2[:, 2:5] = oc[:, :3]
     g2 = np_(R.combined_grad2d(g2, fs.last_conic64))
+    assert np.isfinite(g2).all()
     for k, name in enumerate(["mx", "my", "A", "B", "C", "opacity", "r", "g", "b", "|mx|", "|my|"]):
         e = D.rel_err(g2[:, k], o2[:, k])
         assert e < 1e-5, f"grad2d {name}: {e:.2e}"
