@@ -747,7 +747,15 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
 // ---------------------------------------------------------------------------------------
 // Bucketed backward
 // ---------------------------------------------------------------------------------------
-constexpr int kBwdWaves = 4;
+// Wavefronts per workgroup of the bucketed backward. Each wavefront takes its own bucket and
+// shares nothing with the others, so a workgroup of one lets a CU take the next bucket as soon
+// as any wavefront ends: 3D (1M SH3: 199.3 -> 195.7 us against four per workgroup) and phase0
+// (0.255 -> 0.242 ms at 50k splats); the toy2d surface keeps four (512^2, 50k: 0.087 against
+// 0.098 ms with one).
+template <int R>
+constexpr int bwd_waves() {
+  return R == kRulesToy2D ? 4 : 1;
+}
 // Staged entries that hold the 3D backward's coefficient table (65 floats)
 constexpr int kCoefSlots = ((kWave + 1) * 4 + static_cast<int>(sizeof(Staged<float>)) - 1) /
                            static_cast<int>(sizeof(Staged<float>));
@@ -1086,8 +1094,9 @@ __device__ __forceinline__ void bwd_bucket(const BlendArgs<S>& a, int64_t b, Sta
 // list's length only reads that length); kList 2, a bounded grid strides over the list (the
 // loop keeps more registers live, so it is used only when the table is much longer).
 template <int R, typename S, bool kCount, bool kAbs = true, int kList = 0>
-__global__ __launch_bounds__(kBwdWaves * kWave) void blend_bwd_bucket_kernel(
+__global__ __launch_bounds__(bwd_waves<R>() * kWave) void blend_bwd_bucket_kernel(
     BlendArgs<S> a) {
+  constexpr int kBwdWaves = bwd_waves<R>();
   // (3D: the lanes' coefficient table after the wavefront's staged splats)
   __shared__ Staged<S> s_sp[kBwdWaves][kBucket + (R == kRules3D ? kCoefSlots : 0)];
   __shared__ uint32_t s_m[kBwdWaves][kBucket];
@@ -1265,13 +1274,14 @@ void launch_fwd(const BlendArgs<S>& a, hipStream_t st) {
   }
 }
 
-// Workgroups of the striding list-driven backward: every CU holds its share several times
-// over. Tables longer than kBwdStrideFrom workgroups use it.
-constexpr int64_t kBwdListBlocks = 256 * 16;
+// Workgroups (of one wavefront: 3D) of the striding list-driven backward: every CU holds its
+// share several times over. Bucket tables longer than kBwdStrideFrom use it.
+constexpr int64_t kBwdListBlocks = 256 * 64;
 constexpr int64_t kBwdStrideFrom = 4 * kBwdListBlocks * 4;
 
 template <int R, typename S, bool kCount, bool kAbs>
 void launch_bwd_bucket_k(const BlendArgs<S>& a, hipStream_t st) {
+  constexpr int kBwdWaves = bwd_waves<R>();
   const int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
   const dim3 block(kBwdWaves * kWave);
   if (a.bucket_list && blocks > kBwdStrideFrom)
