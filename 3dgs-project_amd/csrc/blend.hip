@@ -752,6 +752,7 @@ __device__ __forceinline__ S finish_grad(const Staged<S>& s, int k, S u, S u0, S
 // as any wavefront ends: 3D (1M SH3: 199.3 -> 195.7 us against four per workgroup) and phase0
 // (0.255 -> 0.242 ms at 50k splats); the toy2d surface keeps four (512^2, 50k: 0.087 against
 // 0.098 ms with one).
+constexpr int kXcdRun = 4;  // consecutive bucket-list entries per XCD (one-wavefront workgroups)
 template <int R>
 constexpr int bwd_waves() {
   return R == kRulesToy2D ? 4 : 1;
@@ -1108,8 +1109,15 @@ __global__ __launch_bounds__(bwd_waves<R>() * kWave) void blend_bwd_bucket_kerne
   float* s_cw = s_c[R == kRules3D ? wave : 0];
   uint32_t evals = 0, atomics = 0;
   if constexpr (kList == 1) {
-    // one wavefront per list entry; wavefronts past the list's length leave at once
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
+    // one wavefront per list entry; wavefronts past the list's length leave at once. (One
+    // wavefront per workgroup: workgroup b runs on XCD b % 8, and the k-th workgroup of an XCD
+    // takes entry (k / kXcdRun * 8 + b % 8) * kXcdRun + k % kXcdRun, so that runs of kXcdRun
+    // consecutive entries -- a tile's buckets, which read the same pixels -- share an L2.)
+    int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
+    if constexpr (kBwdWaves == 1) {
+      const int64_t k = blockIdx.x / 8;
+      i = (k / kXcdRun * 8 + blockIdx.x % 8) * kXcdRun + k % kXcdRun;
+    }
     if (i < static_cast<int64_t>(a.bucket_list[0]))
       bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave], s_m[wave], s_id[wave], s_cw, evals,
                                      atomics);
@@ -1282,7 +1290,9 @@ constexpr int64_t kBwdStrideFrom = 4 * kBwdListBlocks * 4;
 template <int R, typename S, bool kCount, bool kAbs>
 void launch_bwd_bucket_k(const BlendArgs<S>& a, hipStream_t st) {
   constexpr int kBwdWaves = bwd_waves<R>();
-  const int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
+  int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
+  // (the list walk's XCD runs map workgroups onto entries within whole groups of 8 kXcdRun)
+  if (kBwdWaves == 1 && a.bucket_list) blocks = (blocks + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
   const dim3 block(kBwdWaves * kWave);
   if (a.bucket_list && blocks > kBwdStrideFrom)
     hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, 2>), dim3(static_cast<unsigned>(kBwdListBlocks)),
