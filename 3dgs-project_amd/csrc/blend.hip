@@ -1130,9 +1130,23 @@ __global__ __launch_bounds__(bwd_waves<R>() * kWave) void blend_bwd_bucket_kerne
     // VGPRs and 6)
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     float* s_cws = s_c[R == kRules3D ? wave_s : 0];
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave_s; i < cnt; i += stride)
-      bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave_s], s_m[wave_s], s_id[wave_s], s_cws,
-                                     evals, atomics);
+    if constexpr (kBwdWaves == 1) {
+      // logical entries L = blockIdx.x + t * gridDim.x (gridDim.x a multiple of 8 kXcdRun) taken
+      // through the list walk's XCD runs (a bijection on every aligned group of 8 kXcdRun), so
+      // that a tile's consecutive buckets share an L2 here too
+      const int64_t cnt_r = (cnt + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
+      for (int64_t L = blockIdx.x; L < cnt_r; L += stride) {
+        const int64_t k = L / 8;
+        const int64_t i = (k / kXcdRun * 8 + L % 8) * kXcdRun + k % kXcdRun;
+        if (i < cnt)
+          bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave_s], s_m[wave_s], s_id[wave_s],
+                                         s_cws, evals, atomics);
+      }
+    } else {
+      for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave_s; i < cnt; i += stride)
+        bwd_bucket<R, S, kCount, kAbs>(a, a.bucket_list[kListHeader + i], s_sp[wave_s], s_m[wave_s], s_id[wave_s],
+                                       s_cws, evals, atomics);
+    }
   } else {
     const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
     if (b < a.n_buckets && !(a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)))
