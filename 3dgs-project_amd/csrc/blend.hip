@@ -1148,7 +1148,11 @@ __global__ __launch_bounds__(bwd_waves<R>() * kWave) void blend_bwd_bucket_kerne
                                        s_cws, evals, atomics);
     }
   } else {
-    const int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
+    int64_t b = static_cast<int64_t>(blockIdx.x) * kBwdWaves + wave;
+    if constexpr (kBwdWaves == 1) {  // the table walk takes the same XCD runs as the list walk
+      const int64_t k = blockIdx.x / 8;
+      b = (k / kXcdRun * 8 + blockIdx.x % 8) * kXcdRun + k % kXcdRun;
+    }
     if (b < a.n_buckets && !(a.n_buckets_dev && b >= static_cast<int64_t>(*a.n_buckets_dev)))
       bwd_bucket<R, S, kCount, kAbs>(a, b, s_sp[wave], s_m[wave], s_id[wave], s_cw, evals, atomics);
   }
@@ -1305,8 +1309,8 @@ template <int R, typename S, bool kCount, bool kAbs>
 void launch_bwd_bucket_k(const BlendArgs<S>& a, hipStream_t st) {
   constexpr int kBwdWaves = bwd_waves<R>();
   int64_t blocks = (a.n_buckets + kBwdWaves - 1) / kBwdWaves;
-  // (the list walk's XCD runs map workgroups onto entries within whole groups of 8 kXcdRun)
-  if (kBwdWaves == 1 && a.bucket_list) blocks = (blocks + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
+  // (the walks' XCD runs map workgroups onto entries within whole groups of 8 kXcdRun)
+  if (kBwdWaves == 1) blocks = (blocks + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
   const dim3 block(kBwdWaves * kWave);
   if (a.bucket_list && blocks > kBwdStrideFrom)
     hipLaunchKernelGGL((blend_bwd_bucket_kernel<R, S, kCount, kAbs, 2>), dim3(static_cast<unsigned>(kBwdListBlocks)),
